@@ -1,0 +1,190 @@
+/*
+ * qwmoe.h — C ABI of the MI355X (gfx950) routed-MoE expert-FFN forward path.
+ *
+ * Drop-in boundary for QuantaWeave's MoE layer.  Every entry point is
+ * `extern "C"`, takes plain device pointers, sizes and a HIP stream
+ * (`void* stream`, a hipStream_t; NULL is the null stream), is stream-ordered,
+ * never synchronises the host, and returns an int status (0 = ok, < 0 = error;
+ * the message is in qw_last_error(), which is thread-local).
+ *
+ * Ownership: every pointer is caller-owned device memory.  The library never
+ * allocates device memory; entry points that need scratch take an explicit
+ * `workspace` whose size the caller obtains from the matching
+ * qw_*_workspace_bytes() function.  The library keeps no mutable global state,
+ * so calls on different streams do not interfere (calls that share a workspace
+ * must be ordered on one stream).
+ *
+ * Reference citations are paths inside the QuantaWeave source tree.
+ */
+#ifndef QWMOE_H
+#define QWMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element formats.  QW_F32/QW_BF16 describe activations and plain weights.
+ * QW_I8: int8 weights [out, padded] with fp32 scales [out, padded/group].
+ * QW_U4: int4 weights packed two per byte [out, padded/2] — even input column
+ * in the low nibble, odd column in the high nibble, each stored as q + 8 — with
+ * fp32 scales [out, padded/group].  Layouts are exactly those of
+ * src/quantization.py:36-40, :53-58. */
+enum qw_dtype { QW_F32 = 0, QW_BF16 = 1, QW_I8 = 2, QW_U4 = 3 };
+
+/* Status codes.  INVALID maps to ValueError, the others to RuntimeError. */
+enum qw_status {
+  QW_OK = 0,
+  QW_ERR_INVALID = -1,     /* bad argument: size, dtype, null pointer, range */
+  QW_ERR_UNSUPPORTED = -2, /* valid but not implemented for this shape/format */
+  QW_ERR_HIP = -3,         /* a HIP runtime call or kernel launch failed */
+  QW_ERR_WORKSPACE = -4    /* workspace missing or smaller than required */
+};
+
+/* Thread-local text of the last error raised on this thread ("" if none). */
+const char* qw_last_error(void);
+
+/* ABI revision of this library (bumped on any signature change). */
+int qw_abi_version(void);
+
+/* Route slots per expert.  Replaces TopKMoE.capacity,
+ * src/quantweave_moe_model.py:100-111: when capacity_factor > 0 and
+ * drop_overflow != 0 it is max(min_capacity,
+ * ceil(tokens*top_k/experts*capacity_factor*capacity_scale)) evaluated in
+ * double, left to right; otherwise tokens*top_k.  Returns < 0 on bad input. */
+int64_t qw_moe_capacity(int64_t tokens, int64_t top_k, int64_t experts, double capacity_factor,
+                        double capacity_scale, int64_t min_capacity, int drop_overflow);
+
+/* Router, softmax, top-k and renormalisation.  Replaces
+ * src/quantweave_moe_model.py:124-137:
+ *   logits = (x.float() @ router_w.float().T) / temperature      [T, E] fp32
+ *   probs  = softmax(logits)                                     [T, E] fp32
+ *   top_idx, w = topk(probs, k)            (expert_bias == NULL)
+ *   top_idx = topk(logits + expert_bias, k).indices; w = probs.gather(top_idx)
+ *   top_w  = w / w.sum(-1)                                       [T, k] fp32
+ * x: [tokens, d_model] (QW_F32 or QW_BF16) with row stride x_row_stride
+ * elements; router_w: [experts, d_model] contiguous (QW_F32 or QW_BF16).
+ * Top-k order is descending, ties resolved towards the lower expert index.
+ * 1 <= top_k <= experts <= 1024. */
+int qw_moe_route(const void* x, int x_dtype, int64_t x_row_stride, const void* router_w, int w_dtype,
+                 int64_t tokens, int64_t d_model, int64_t experts, int64_t top_k, float temperature,
+                 const float* expert_bias, float* logits, float* probs, int32_t* top_idx, float* top_w,
+                 void* stream);
+
+/* The softmax/top-k/renormalise half of qw_moe_route on caller-supplied fp32
+ * logits [tokens, experts] (already divided by the temperature).  With
+ * identical logits this is the routing the bit-exact parity contract covers.
+ * src/quantweave_moe_model.py:129-137. */
+int qw_moe_route_from_logits(const float* logits, int64_t tokens, int64_t experts, int64_t top_k,
+                             const float* expert_bias, float* probs, int32_t* top_idx, float* top_w,
+                             void* stream);
+
+/* Capacity plan.  Replaces TopKMoE._plan, src/quantweave_moe_model.py:166-188.
+ * Routes r = token*top_k + j are ordered by (expert ascending, weight
+ * descending, route id ascending); the first `capacity` routes of each expert
+ * are kept.  Outputs (R = tokens*top_k):
+ *   counts[E]        routes per expert before capacity (bincount)
+ *   kept_counts[E]   min(counts, capacity)
+ *   kept_offsets[E+1] exclusive scan of kept_counts (kept_offsets[E] = kept)
+ *   slot_token[R]    token of each kept route, in plan order   ("tokens")
+ *   slot_weight[R]   renormalised weight of each kept route    ("weights")
+ *   route_slot[R]    slot of route r, or -1 when it was dropped
+ *   dropped_token[R], dropped_expert[R]  dropped routes in plan order
+ *   totals[2]        {kept routes, overflow routes}
+ * Entries past totals[0] / totals[1] are left unwritten. */
+size_t qw_moe_plan_workspace_bytes(int64_t tokens, int64_t top_k, int64_t experts);
+int qw_moe_plan(const int32_t* top_idx, const float* top_w, int64_t tokens, int64_t top_k, int64_t experts,
+                int64_t capacity, int32_t* counts, int32_t* kept_counts, int32_t* kept_offsets,
+                int32_t* slot_token, float* slot_weight, int32_t* route_slot, int32_t* dropped_token,
+                int32_t* dropped_expert, int32_t* totals, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Gather kept rows into plan order: out[s] = x[slot_token[s]] for
+ * s < totals[0] (src/quantweave_moe_model.py:195, `flat_hidden[tokens]`).
+ * x and out are contiguous [*, d_model] of `dtype`. */
+int qw_moe_permute(const void* x, int dtype, int64_t d_model, const int32_t* slot_token, const int32_t* totals,
+                   int64_t max_rows, void* out, void* stream);
+
+/* Grouped SwiGLU experts over plan-ordered rows.  Replaces
+ * moe_kernels.grouped_swiglu (src/moe_kernels.py:186-195), the per-expert loop
+ * (src/quantweave_moe_model.py:203-211) and, for quantised experts,
+ * QuantizedLinear.forward (src/quantization.py:61-72):
+ *   y[s] = down_e( silu(gate_e(x_s)) * up_e(x_s) ) * row_weight[s]
+ * for every s in [kept_offsets[e], kept_offsets[e+1]) of expert e, where x_s is
+ * x[row_index[s]] (row_index == NULL: x[s]).  row_weight may be NULL (factor 1).
+ * Weights per expert, nn.Linear [out, in] layout, stacked over experts:
+ *   QW_F32 / QW_BF16 : gate_w, up_w [E, d_ff, d_model]; down_w [E, d_model, d_ff]
+ *   QW_I8 / QW_U4    : qweight and fp32 scales stacked the same way, group sizes
+ *                      group_in (gate/up, over d_model) and group_ff (down)
+ * act_dtype: QW_F32 or QW_BF16 (x and y).  Quantised weights are dequantised
+ * to fp32, rounded to act_dtype, and multiplied with fp32 accumulation.
+ * max_rows bounds kept_offsets[E] (rows of y and of the hidden workspace). */
+size_t qw_moe_experts_workspace_bytes(int64_t max_rows, int64_t experts, int64_t d_model, int64_t d_ff,
+                                      int act_dtype);
+int qw_moe_experts(const void* x, int act_dtype, const int32_t* row_index, const int32_t* kept_offsets,
+                   int64_t experts, int64_t d_model, int64_t d_ff, int64_t max_rows, int w_format,
+                   int64_t group_in, int64_t group_ff, const void* gate_w, const float* gate_scales,
+                   const void* up_w, const float* up_scales, const void* down_w, const float* down_scales,
+                   const float* row_weight, void* y, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Weighted combine.  Replaces `output.index_add_(0, tokens, expert_output)`
+ * (src/quantweave_moe_model.py:192, :200-201, :210-211): out[t] starts at zero
+ * and adds y[route_slot[t*k+j]] of every kept route of token t in ascending
+ * expert order, rounding to `dtype` after each add.  out: [tokens, d_model]. */
+int qw_moe_combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, int64_t tokens,
+                   int64_t top_k, int64_t d_model, void* out, void* stream);
+
+/* Load-balance loss (src/quantweave_moe_model.py:152-154):
+ * importance[e] = mean_t probs[t, e]; balance = E * sum_e importance[e] *
+ * counts[e] / (tokens*top_k).  importance may be NULL. */
+int qw_moe_balance(const float* probs, const int32_t* counts, int64_t tokens, int64_t top_k, int64_t experts,
+                   float* importance, float* balance, void* stream);
+
+/* Whole MoE layer forward (TopKMoE.forward, src/quantweave_moe_model.py:113-164,
+ * dynamic-dispatch branch): route -> plan -> grouped SwiGLU -> combine, no host
+ * synchronisation.  `out` [tokens, d_model] has act_dtype.  Outputs as for the
+ * calls above; probs/top_idx/top_w/counts/kept_counts/totals/dropped_* are
+ * required.  `capacity` comes from qw_moe_capacity. */
+size_t qw_moe_forward_workspace_bytes(int64_t tokens, int64_t d_model, int64_t experts, int64_t top_k,
+                                      int64_t d_ff, int act_dtype);
+int qw_moe_forward(const void* x, int act_dtype, int64_t tokens, int64_t d_model, const void* router_w,
+                   int router_dtype, float temperature, const float* expert_bias, int64_t experts,
+                   int64_t top_k, int64_t capacity, int64_t d_ff, int w_format, int64_t group_in,
+                   int64_t group_ff, const void* gate_w, const float* gate_scales, const void* up_w,
+                   const float* up_scales, const void* down_w, const float* down_scales, void* out,
+                   float* probs, int32_t* top_idx, float* top_w, int32_t* counts, int32_t* kept_counts,
+                   int32_t* totals, int32_t* dropped_token, int32_t* dropped_expert, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* Weight-only quantisation, QuantizedLinear.from_linear
+ * (src/quantization.py:43-59): w [out, in] fp32 or bf16 is zero-padded to
+ * padded = ceil(in/group)*group columns; per group scale =
+ * max(amax/limit, 1e-8) (limit 127 for bits 8, 7 for bits 4);
+ * q = clamp(round_half_even(w/scale), -limit-(bits==4), limit).
+ * bits 8: qweight int8 [out, padded]; bits 4: uint8 [out, padded/2] with
+ * (q+8) of even columns in the low nibble.  scales fp32 [out, padded/group]. */
+int qw_quantize(const void* w, int w_dtype, int64_t out_features, int64_t in_features, int bits,
+                int64_t group_size, void* qweight, float* scales, void* stream);
+
+/* QuantizedLinear.dequantize (src/quantization.py:61-69): out fp32
+ * [out, in] = q * scale per group, padding columns dropped. */
+int qw_dequantize(const void* qweight, const float* scales, int bits, int64_t out_features, int64_t in_features,
+                  int64_t group_size, float* out, void* stream);
+
+/* Grouped matmul forward, moe_kernels.grouped_matmul (src/moe_kernels.py:118-135,
+ * :167-171): out[rows of e] = x[rows of e] @ w[e]^T with rows of e =
+ * [offsets[e], offsets[e+1]); w [E, out_features, in_features] in w_format
+ * (QW_I8 / QW_U4 with fp32 scales and group size `group`, as
+ * QuantizedLinear.forward, src/quantization.py:71-72); x and out have
+ * act_dtype (QW_F32 or QW_BF16); fp32 accumulation, quantised weights rounded
+ * to act_dtype before the multiply. */
+int qw_grouped_matmul(const void* x, int act_dtype, const void* w, int w_format, const float* scales, int64_t group,
+                      int64_t experts, int64_t out_features, int64_t in_features, const int32_t* offsets,
+                      int64_t rows, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWMOE_H */

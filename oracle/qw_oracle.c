@@ -1,0 +1,265 @@
+/*
+ * CPU oracle for the routed MoE expert-FFN forward path — TEST INFRASTRUCTURE.
+ *
+ * A plain-C restatement of the reference algorithm, used only by tests/,
+ * __graft_entry__.smoke() and bench.py's CPU-baseline leg as the checker.  It
+ * is never linked into or called by the product library.
+ *
+ * Built with -ffp-contract=off and no fast-math: every float operation below
+ * is one IEEE-754 single-precision operation in the written order.
+ *
+ * Functions and the reference lines they restate:
+ *   orc_expf, orc_softmax_row  softmax of src/quantweave_moe_model.py:129 with
+ *                              an exactly specified exp and summation order
+ *   orc_route_from_logits      :129-137 (softmax, topk / biased topk, renorm)
+ *   orc_router_logits          :128 (fp32 logits, double accumulation)
+ *   orc_capacity               :100-111
+ *   orc_plan                   :166-188 (two stable argsorts == one stable
+ *                              sort by (expert, -weight, route))
+ *   orc_quantize               src/quantization.py:43-59
+ *   orc_dequantize             src/quantization.py:61-69
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- exp and softmax --------------------------------------------------- */
+
+static float as_float(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+static uint32_t as_uint(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+
+/* e^x for x <= 0: n = rint(x*log2(e)); r = x - n*ln2 (two-part ln2, fma);
+ * e^r by the degree-7 Taylor polynomial 1/i! in Horner form (fma);
+ * times 2^n via the exponent field, in two steps below 2^-126. */
+float orc_expf(float x) {
+  if (!(x >= -104.0f)) return (x != x) ? x : 0.0f;
+  const float n = rintf(x * 1.4426950216293335f);
+  float r = fmaf(-n, 0.693145751953125f, x);
+  r = fmaf(-n, 1.428606765330187e-06f, r);
+  float p = 0.00019841270113829523f;
+  p = fmaf(p, r, 0.0013888889225199819f);
+  p = fmaf(p, r, 0.008333333767950535f);
+  p = fmaf(p, r, 0.0416666679084301f);
+  p = fmaf(p, r, 0.1666666716337204f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  const int ni = (int)n;
+  if (ni >= -126) return p * as_float((uint32_t)(ni + 127) << 23);
+  return (p * as_float((uint32_t)(ni + 127 + 64) << 23)) * 5.421010862427522e-20f;
+}
+
+/* softmax of one row of E logits.  Summation order: the row is dealt to 64
+ * lanes (expert e to lane e % 64); each lane sums its experts in index order;
+ * then 6 butterfly rounds: v[l] = v[l] + v[l ^ o] for o = 32, 16, 8, 4, 2, 1;
+ * the sum is lane 0's value.  p_e = q_e / sum (IEEE division). */
+void orc_softmax_row(const float* logits, int E, float* probs) {
+  float m = -INFINITY;
+  int has_nan = 0;
+  for (int e = 0; e < E; ++e) {
+    if (logits[e] != logits[e]) has_nan = 1;
+    else if (logits[e] > m) m = logits[e];
+  }
+  if (has_nan) m = NAN;
+  float lane[64];
+  for (int l = 0; l < 64; ++l) lane[l] = 0.0f;
+  for (int e = 0; e < E; ++e) {
+    probs[e] = orc_expf(logits[e] - m);
+  }
+  for (int l = 0; l < 64; ++l) {
+    float s = 0.0f;
+    for (int e = l; e < E; e += 64) s = s + probs[e];
+    lane[l] = s;
+  }
+  for (int o = 32; o >= 1; o >>= 1) {
+    float nxt[64];
+    for (int l = 0; l < 64; ++l) nxt[l] = lane[l] + lane[l ^ o];
+    memcpy(lane, nxt, sizeof(lane));
+  }
+  const float s = lane[0];
+  for (int e = 0; e < E; ++e) probs[e] = probs[e] / s;
+}
+
+/* Total order key: -inf < ... < -0 < +0 < ... < +inf < NaN. */
+static uint32_t sort_key(float f) {
+  uint32_t u = as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+/* probs = softmax(logits); indices = topk(probs or logits+bias, k) in
+ * descending order, equal keys by ascending expert index; w = probs[idx];
+ * top_w = w / (((w0 + w1) + w2) + ...). */
+void orc_route_from_logits(const float* logits, int T, int E, int K, const float* bias, float* probs,
+                           int32_t* top_idx, float* top_w) {
+  uint32_t* key = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)E);
+  char* taken = (char*)malloc((size_t)E);
+  for (int t = 0; t < T; ++t) {
+    const float* l = logits + (size_t)t * E;
+    float* p = probs + (size_t)t * E;
+    orc_softmax_row(l, E, p);
+    for (int e = 0; e < E; ++e) {
+      key[e] = sort_key(bias ? l[e] + bias[e] : p[e]);
+      taken[e] = 0;
+    }
+    float sum = 0.0f;
+    for (int j = 0; j < K; ++j) {
+      int best = -1;
+      for (int e = 0; e < E; ++e) {
+        if (taken[e]) continue;
+        if (best < 0 || key[e] > key[best]) best = e;
+      }
+      taken[best] = 1;
+      top_idx[(size_t)t * K + j] = best;
+      top_w[(size_t)t * K + j] = p[best];
+      sum = (j == 0) ? p[best] : sum + p[best];
+    }
+    for (int j = 0; j < K; ++j) top_w[(size_t)t * K + j] = top_w[(size_t)t * K + j] / sum;
+  }
+  free(key);
+  free(taken);
+}
+
+/* logits[t, e] = (sum_k x[t,k] * w[e,k], in double, rounded to float) / temperature */
+void orc_router_logits(const float* x, const float* w, int T, int D, int E, float temperature, float* logits) {
+  for (int t = 0; t < T; ++t)
+    for (int e = 0; e < E; ++e) {
+      double acc = 0.0;
+      for (int k = 0; k < D; ++k) acc += (double)x[(size_t)t * D + k] * (double)w[(size_t)e * D + k];
+      logits[(size_t)t * E + e] = (float)acc / temperature;
+    }
+}
+
+/* ---- capacity and plan ------------------------------------------------- */
+
+int64_t orc_capacity(int64_t tokens, int64_t top_k, int64_t experts, double capacity_factor, double capacity_scale,
+                     int64_t min_capacity, int drop_overflow) {
+  if (capacity_factor > 0 && drop_overflow) {
+    double v = (double)(tokens * top_k) / (double)experts * capacity_factor * capacity_scale;
+    int64_t c = (int64_t)ceil(v);
+    return c > min_capacity ? c : min_capacity;
+  }
+  return tokens * top_k;
+}
+
+typedef struct {
+  int32_t expert;
+  uint32_t wkey; /* sort_key(weight): larger weight -> larger key */
+  int32_t route;
+} plan_item;
+
+static int plan_cmp(const void* a, const void* b) {
+  const plan_item* x = (const plan_item*)a;
+  const plan_item* y = (const plan_item*)b;
+  if (x->expert != y->expert) return x->expert < y->expert ? -1 : 1;
+  if (x->wkey != y->wkey) return x->wkey > y->wkey ? -1 : 1; /* weight descending */
+  return x->route < y->route ? -1 : (x->route > y->route); /* stability: route ascending */
+}
+
+/* Outputs as qw_moe_plan.  Returns the number of kept routes. */
+int orc_plan(const int32_t* top_idx, const float* top_w, int T, int K, int E, int64_t capacity, int32_t* counts,
+             int32_t* kept_counts, int32_t* kept_offsets, int32_t* slot_token, float* slot_weight,
+             int32_t* route_slot, int32_t* dropped_token, int32_t* dropped_expert, int32_t* totals) {
+  const int R = T * K;
+  plan_item* items = (plan_item*)malloc(sizeof(plan_item) * (size_t)(R > 0 ? R : 1));
+  for (int e = 0; e < E; ++e) counts[e] = 0;
+  for (int r = 0; r < R; ++r) {
+    items[r].expert = top_idx[r];
+    items[r].wkey = sort_key(top_w[r]);
+    items[r].route = r;
+    counts[top_idx[r]] += 1;
+  }
+  qsort(items, (size_t)R, sizeof(plan_item), plan_cmp);
+  int off = 0;
+  for (int e = 0; e < E; ++e) {
+    kept_counts[e] = counts[e] < capacity ? counts[e] : (int32_t)capacity;
+    kept_offsets[e] = off;
+    off += kept_counts[e];
+  }
+  kept_offsets[E] = off;
+  /* position of the i-th sorted route inside its expert = i - first index of its expert */
+  int kept = 0, dropped = 0, start = 0;
+  for (int i = 0; i < R; ++i) {
+    if (i > 0 && items[i].expert != items[i - 1].expert) start = i;
+    const int position = i - start;
+    const int r = items[i].route;
+    if (position < capacity) {
+      slot_token[kept] = r / K;
+      slot_weight[kept] = top_w[r];
+      route_slot[r] = kept;
+      ++kept;
+    } else {
+      dropped_token[dropped] = r / K;
+      dropped_expert[dropped] = items[i].expert;
+      route_slot[r] = -1;
+      ++dropped;
+    }
+  }
+  totals[0] = kept;
+  totals[1] = dropped;
+  free(items);
+  return kept;
+}
+
+/* ---- weight-only quantisation ------------------------------------------ */
+
+/* w fp32 [rows, cols] -> qweight (int8 [rows, padded] or uint8 [rows, padded/2])
+ * and scales fp32 [rows, padded/group]. */
+void orc_quantize(const float* w, int64_t rows, int64_t cols, int bits, int64_t group, void* qweight, float* scales) {
+  const int64_t groups = (cols + group - 1) / group;
+  const int64_t padded = groups * group;
+  const float limit = bits == 8 ? 127.0f : 7.0f;
+  const float lo = bits == 8 ? -127.0f : -8.0f;
+  for (int64_t row = 0; row < rows; ++row) {
+    for (int64_t g = 0; g < groups; ++g) {
+      float amax = 0.0f;
+      for (int64_t c = g * group; c < (g + 1) * group; ++c) {
+        const float v = c < cols ? fabsf(w[row * cols + c]) : 0.0f;
+        if (v > amax) amax = v;
+      }
+      float s = amax / limit;
+      if (s < 1e-8f) s = 1e-8f;
+      scales[row * groups + g] = s;
+      for (int64_t c = g * group; c < (g + 1) * group; ++c) {
+        const float v = c < cols ? w[row * cols + c] : 0.0f;
+        float q = rintf(v / s);
+        if (q < lo) q = lo;
+        if (q > limit) q = limit;
+        if (bits == 8) {
+          ((int8_t*)qweight)[row * padded + c] = (int8_t)q;
+        } else {
+          uint8_t* b = (uint8_t*)qweight + row * (padded / 2) + c / 2;
+          const uint8_t u = (uint8_t)((int)q + 8);
+          if (c % 2 == 0) *b = (uint8_t)((*b & 0xF0) | u);
+          else *b = (uint8_t)((*b & 0x0F) | (u << 4));
+        }
+      }
+    }
+  }
+}
+
+void orc_dequantize(const void* qweight, const float* scales, int bits, int64_t rows, int64_t cols, int64_t group,
+                    float* out) {
+  const int64_t groups = (cols + group - 1) / group;
+  const int64_t padded = groups * group;
+  for (int64_t row = 0; row < rows; ++row)
+    for (int64_t c = 0; c < cols; ++c) {
+      float q;
+      if (bits == 8) {
+        q = (float)((const int8_t*)qweight)[row * padded + c];
+      } else {
+        const uint8_t b = ((const uint8_t*)qweight)[row * (padded / 2) + c / 2];
+        q = (float)((c % 2 == 0) ? (b & 0xF) : (b >> 4)) - 8.0f;
+      }
+      out[row * cols + c] = q * scales[row * groups + c / group];
+    }
+}

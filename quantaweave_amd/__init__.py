@@ -1,0 +1,20 @@
+"""MI355X (gfx950) routed-MoE expert-FFN forward for QuantaWeave.
+
+Drop-in Python surface over the C ABI in include/qwmoe.h:
+
+* ``TopKMoE``, ``SparseSwiGLU``, ``QuantaWeaveConfig``, ``set_moe_kernel``
+  (src/quantweave_moe_model.py)
+* ``moe_kernels``: ``kernels_available``, ``experts_support_grouped``,
+  ``GroupedPlan``, ``grouped_matmul``, ``grouped_swiglu``, ``compute_dtype``,
+  ``benchmark`` (src/moe_kernels.py)
+* ``QuantizedLinear``, ``quantize_model`` (src/quantization.py)
+"""
+
+from . import moe_kernels
+from .moe import QuantaWeaveConfig, SparseSwiGLU, TopKMoE, set_moe_kernel
+from .quantization import QuantizedLinear, quantize_model
+
+__all__ = [
+    "QuantaWeaveConfig", "SparseSwiGLU", "TopKMoE", "set_moe_kernel", "QuantizedLinear", "quantize_model",
+    "moe_kernels",
+]

@@ -1,0 +1,35 @@
+"""Tensor plumbing for the C ABI: device checks, pointers, dtype codes, stream."""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_ACT = {torch.float32: _lib.QW_F32, torch.bfloat16: _lib.QW_BF16}
+
+
+def require_device(t: torch.Tensor, what: str) -> None:
+    if t.device.type != "cuda" or not torch.cuda.is_available():
+        raise RuntimeError(f"{what}: the HIP MoE kernels need a ROCm (cuda) device tensor, got {t.device}")
+
+
+def act_code(t: torch.Tensor, what: str) -> int:
+    try:
+        return _ACT[t.dtype]
+    except KeyError:
+        raise ValueError(f"{what}: dtype {t.dtype} is not supported (float32 or bfloat16)") from None
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)

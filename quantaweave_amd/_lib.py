@@ -1,0 +1,85 @@
+"""ctypes binding of ``libqwmoe.so`` (the C ABI declared in include/qwmoe.h).
+
+The library is loaded from this package directory only; there is no other
+implementation to fall back to, so a missing library is an ImportError-like
+RuntimeError at first use.  Status codes map to the reference's exception
+types: QW_ERR_INVALID -> ValueError, everything else -> RuntimeError.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libqwmoe.so"
+
+QW_F32, QW_BF16, QW_I8, QW_U4 = 0, 1, 2, 3
+QW_OK, QW_ERR_INVALID, QW_ERR_UNSUPPORTED, QW_ERR_HIP, QW_ERR_WORKSPACE = 0, -1, -2, -3, -4
+
+P = ctypes.c_void_p
+I32, I64, F32, F64, SZ = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_double, ctypes.c_size_t
+
+# name -> (restype, argtypes); kept in the order of include/qwmoe.h
+SIGNATURES = {
+    "qw_last_error": (ctypes.c_char_p, []),
+    "qw_abi_version": (I32, []),
+    "qw_moe_capacity": (I64, [I64, I64, I64, F64, F64, I64, I32]),
+    "qw_moe_route": (I32, [P, I32, I64, P, I32, I64, I64, I64, I64, F32, P, P, P, P, P, P]),
+    "qw_moe_route_from_logits": (I32, [P, I64, I64, I64, P, P, P, P, P]),
+    "qw_moe_plan_workspace_bytes": (SZ, [I64, I64, I64]),
+    "qw_moe_plan": (I32, [P, P, I64, I64, I64, I64, P, P, P, P, P, P, P, P, P, P, SZ, P]),
+    "qw_moe_permute": (I32, [P, I32, I64, P, P, I64, P, P]),
+    "qw_moe_experts_workspace_bytes": (SZ, [I64, I64, I64, I64, I32]),
+    "qw_moe_experts": (I32, [P, I32, P, P, I64, I64, I64, I64, I32, I64, I64, P, P, P, P, P, P, P, P, P, SZ, P]),
+    "qw_moe_combine": (I32, [P, I32, P, P, I64, I64, I64, P, P]),
+    "qw_moe_balance": (I32, [P, P, I64, I64, I64, P, P, P]),
+    "qw_moe_forward_workspace_bytes": (SZ, [I64, I64, I64, I64, I64, I32]),
+    "qw_moe_forward": (I32, [P, I32, I64, I64, P, I32, F32, P, I64, I64, I64, I64, I32, I64, I64,
+                             P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, SZ, P]),
+    "qw_quantize": (I32, [P, I32, I64, I64, I32, I64, P, P, P]),
+    "qw_dequantize": (I32, [P, P, I32, I64, I64, I64, P, P]),
+    "qw_grouped_matmul": (I32, [P, I32, P, I32, P, I64, I64, I64, I64, P, I64, P, P]),
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+class QWError(RuntimeError):
+    pass
+
+
+def load() -> ctypes.CDLL:
+    """Load libqwmoe.so once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"the HIP MoE library {LIB_PATH} is not built; run `python -m quantaweave_amd.build`")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status == QW_OK:
+        return
+    msg = load().qw_last_error().decode(errors="replace")
+    text = f"{what}: {msg}" if msg else f"{what} failed with status {status}"
+    if status == QW_ERR_INVALID:
+        raise ValueError(text)
+    raise RuntimeError(text)
+
+
+def call(name: str, *args) -> int:
+    """Call an entry point that returns a status; raise on failure."""
+    status = getattr(load(), name)(*args)
+    check(status, name)
+    return status
+
+
+def available() -> bool:
+    return LIB_PATH.exists()

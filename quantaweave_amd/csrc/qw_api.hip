@@ -1,0 +1,314 @@
+// C ABI entry points (include/qwmoe.h): argument checks, workspace carving and
+// kernel selection.  No entry point allocates device memory or synchronises.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+
+#include "qw_ffn.h"
+
+namespace qw {
+
+static thread_local char g_error[512] = "";
+
+int set_error(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+void clear_error() { g_error[0] = '\0'; }
+
+// Implemented in the kernel files.
+int route(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int64_t T, int64_t D, int64_t E,
+          int64_t K, float temperature, const float* bias, float* logits, float* probs, int32_t* top_idx,
+          float* top_w, hipStream_t stream);
+int route_from_logits(const float* logits, int64_t T, int64_t E, int64_t K, const float* bias, float* probs,
+                      int32_t* top_idx, float* top_w, hipStream_t stream);
+size_t plan_workspace_bytes(int64_t T, int64_t K, int64_t E);
+int plan(const int32_t* top_idx, const float* top_w, int64_t T, int64_t K, int64_t E, int64_t capacity,
+         int32_t* counts, int32_t* kept_counts, int32_t* kept_offsets, int32_t* slot_token, float* slot_weight,
+         int32_t* route_slot, int32_t* dropped_token, int32_t* dropped_expert, int32_t* totals, void* ws,
+         size_t ws_bytes, hipStream_t stream);
+int permute(const void* x, int dtype, int64_t D, const int32_t* slot_token, const int32_t* totals, int64_t max_rows,
+            void* out, hipStream_t stream);
+int combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, int64_t T, int64_t K,
+            int64_t D, void* out, hipStream_t stream);
+int balance(const float* probs, const int32_t* counts, int64_t T, int64_t K, int64_t E, float* importance,
+            float* bal, hipStream_t stream, float* scratch_importance);
+int quantize(const void* w, int wdt, int64_t rows, int64_t cols, int bits, int64_t group, void* qweight, float* scales,
+             hipStream_t stream);
+int dequantize(const void* qweight, const float* scales, int bits, int64_t rows, int64_t cols, int64_t group,
+               float* out, hipStream_t stream);
+int grouped_matmul_generic(const void* x, int act, const WView& w, int wfmt, int64_t E, const int32_t* offsets,
+                           void* out, hipStream_t stream);
+
+// Kernel-path override for testing the general kernel on any shape:
+// QW_FFN_PATH=generic.  Read once per process.
+static int ffn_path_override() {
+  static const int v = [] {
+    const char* s = std::getenv("QW_FFN_PATH");
+    return (s && std::strcmp(s, "generic") == 0) ? 1 : 0;
+  }();
+  return v;
+}
+
+static size_t act_size(int dt) { return dt == QW_F32 ? 4 : 2; }
+
+size_t experts_workspace_bytes(int64_t max_rows, int64_t E, int64_t D, int64_t F, int act) {
+  (void)E;
+  Carver c(nullptr);
+  c.take<char>(static_cast<size_t>(max_rows) * F * act_size(act));  // hidden
+  c.take<float>(static_cast<size_t>(max_rows) * D);                  // split-K partials (decode)
+  return c.used + 256;
+}
+
+int experts(const void* x, int act, const int32_t* row_index, const int32_t* offsets, int64_t E, int64_t D, int64_t F,
+            int64_t max_rows, int wfmt, int64_t group_in, int64_t group_ff, const void* gate_w, const float* gate_s,
+            const void* up_w, const float* up_s, const void* down_w, const float* down_s, const float* row_weight,
+            void* y, void* ws, size_t ws_bytes, hipStream_t stream, int64_t avg_rows) {
+  QW_REQUIRE(act == QW_F32 || act == QW_BF16, "activation dtype must be f32 or bf16");
+  QW_REQUIRE(wfmt >= QW_F32 && wfmt <= QW_U4, "unknown weight format %d", wfmt);
+  QW_REQUIRE(E >= 1 && E <= 65535, "experts out of range");
+  QW_REQUIRE(D >= 1 && D <= INT32_MAX / 2 && F >= 1 && F <= INT32_MAX / 2, "d_model/d_ff out of range");
+  QW_REQUIRE(max_rows >= 0 && max_rows <= INT32_MAX, "max_rows out of range");
+  if (wfmt == QW_I8 || wfmt == QW_U4) {
+    QW_REQUIRE(group_in >= 1 && group_ff >= 1, "quantised weights need positive group sizes");
+    QW_REQUIRE(wfmt == QW_I8 || (group_in % 2 == 0 && group_ff % 2 == 0),
+               "group_size must be even for 4-bit weights");
+    QW_REQUIRE(gate_s && up_s && down_s, "quantised weights need scales");
+  }
+  if (max_rows == 0) return QW_OK;
+  QW_REQUIRE(x && offsets && gate_w && up_w && down_w && y, "experts pointers are required");
+  const size_t need = experts_workspace_bytes(max_rows, E, D, F, act);
+  if (ws_bytes < need || !ws)
+    return set_error(QW_ERR_WORKSPACE, "experts workspace needs %zu bytes, got %zu", need, ws_bytes);
+  Carver c(ws);
+  FfnArgs a{};
+  a.x = x;
+  a.row_index = row_index;
+  a.offsets = offsets;
+  a.experts = E;
+  a.d_model = D;
+  a.d_ff = F;
+  a.max_rows = max_rows;
+  a.act = act;
+  a.wfmt = wfmt;
+  a.gate = make_wview(wfmt, gate_w, gate_s, F, D, group_in);
+  a.up = make_wview(wfmt, up_w, up_s, F, D, group_in);
+  a.down = make_wview(wfmt, down_w, down_s, D, F, group_ff);
+  a.row_weight = row_weight;
+  a.hidden = c.take<char>(static_cast<size_t>(max_rows) * F * act_size(act));
+  a.partial = c.take<float>(static_cast<size_t>(max_rows) * D);
+  a.y = y;
+  a.avg_rows = avg_rows;
+  if (!ffn_path_override()) {
+    bool handled = false;
+    int st = launch_ffn_gemv(a, stream, &handled);
+    if (st || handled) return st;
+    st = launch_ffn_mfma(a, stream, &handled);
+    if (st || handled) return st;
+  }
+  return launch_ffn_generic(a, stream);
+}
+
+size_t forward_workspace_bytes(int64_t T, int64_t D, int64_t E, int64_t K, int64_t F, int act) {
+  const int64_t R = T * K;
+  Carver c(nullptr);
+  c.take<float>(static_cast<size_t>(T) * E);  // logits
+  c.take<int32_t>(R);                           // slot_token
+  c.take<float>(R);                             // slot_weight
+  c.take<int32_t>(R);                           // route_slot
+  c.take<int32_t>(E + 1);                       // kept_offsets
+  c.take<char>(static_cast<size_t>(R) * D * act_size(act));  // y
+  c.take<char>(plan_workspace_bytes(T, K, E));
+  c.take<char>(experts_workspace_bytes(R, E, D, F, act));
+  return c.used + 256;
+}
+
+}  // namespace qw
+
+using namespace qw;
+
+extern "C" {
+
+const char* qw_last_error(void) { return g_error; }
+
+int qw_abi_version(void) { return 1; }
+
+int64_t qw_moe_capacity(int64_t tokens, int64_t top_k, int64_t experts, double capacity_factor,
+                        double capacity_scale, int64_t min_capacity, int drop_overflow) {
+  if (tokens < 0 || top_k < 1 || experts < 1 || min_capacity < 1 || capacity_factor < 0) {
+    set_error(QW_ERR_INVALID, "bad capacity arguments");
+    return QW_ERR_INVALID;
+  }
+  if (capacity_factor > 0 && drop_overflow) {
+    // Python: num_tokens * top_k / num_experts * capacity_factor * capacity_scale,
+    // int*int is exact, `/` is true division in double, then left to right.
+    const double v = static_cast<double>(tokens * top_k) / static_cast<double>(experts) * capacity_factor *
+                     capacity_scale;
+    const double c = std::ceil(v);
+    if (!(c < 9.2e18)) {
+      set_error(QW_ERR_INVALID, "capacity overflows int64");
+      return QW_ERR_INVALID;
+    }
+    const int64_t ci = static_cast<int64_t>(c);
+    return ci > min_capacity ? ci : min_capacity;
+  }
+  return tokens * top_k;
+}
+
+int qw_moe_route(const void* x, int x_dtype, int64_t x_row_stride, const void* router_w, int w_dtype, int64_t tokens,
+                 int64_t d_model, int64_t experts, int64_t top_k, float temperature, const float* expert_bias,
+                 float* logits, float* probs, int32_t* top_idx, float* top_w, void* stream) {
+  clear_error();
+  return route(x, x_dtype, x_row_stride, router_w, w_dtype, tokens, d_model, experts, top_k, temperature, expert_bias,
+               logits, probs, top_idx, top_w, as_stream(stream));
+}
+
+int qw_moe_route_from_logits(const float* logits, int64_t tokens, int64_t experts, int64_t top_k,
+                             const float* expert_bias, float* probs, int32_t* top_idx, float* top_w, void* stream) {
+  clear_error();
+  return route_from_logits(logits, tokens, experts, top_k, expert_bias, probs, top_idx, top_w, as_stream(stream));
+}
+
+size_t qw_moe_plan_workspace_bytes(int64_t tokens, int64_t top_k, int64_t experts) {
+  if (tokens < 0 || top_k < 1 || experts < 1) return 0;
+  return plan_workspace_bytes(tokens, top_k, experts);
+}
+
+int qw_moe_plan(const int32_t* top_idx, const float* top_w, int64_t tokens, int64_t top_k, int64_t experts,
+                int64_t capacity, int32_t* counts, int32_t* kept_counts, int32_t* kept_offsets, int32_t* slot_token,
+                float* slot_weight, int32_t* route_slot, int32_t* dropped_token, int32_t* dropped_expert,
+                int32_t* totals, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  return plan(top_idx, top_w, tokens, top_k, experts, capacity, counts, kept_counts, kept_offsets, slot_token,
+              slot_weight, route_slot, dropped_token, dropped_expert, totals, workspace, workspace_bytes,
+              as_stream(stream));
+}
+
+int qw_moe_permute(const void* x, int dtype, int64_t d_model, const int32_t* slot_token, const int32_t* totals,
+                   int64_t max_rows, void* out, void* stream) {
+  clear_error();
+  return permute(x, dtype, d_model, slot_token, totals, max_rows, out, as_stream(stream));
+}
+
+size_t qw_moe_experts_workspace_bytes(int64_t max_rows, int64_t experts, int64_t d_model, int64_t d_ff,
+                                      int act_dtype) {
+  if (max_rows < 0 || experts < 1 || d_model < 1 || d_ff < 1) return 0;
+  return experts_workspace_bytes(max_rows, experts, d_model, d_ff, act_dtype);
+}
+
+int qw_moe_experts(const void* x, int act_dtype, const int32_t* row_index, const int32_t* kept_offsets,
+                   int64_t experts, int64_t d_model, int64_t d_ff, int64_t max_rows, int w_format, int64_t group_in,
+                   int64_t group_ff, const void* gate_w, const float* gate_scales, const void* up_w,
+                   const float* up_scales, const void* down_w, const float* down_scales, const float* row_weight,
+                   void* y, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  const int64_t avg = experts > 0 ? (max_rows + experts - 1) / experts : 0;
+  return qw::experts(x, act_dtype, row_index, kept_offsets, experts, d_model, d_ff, max_rows, w_format, group_in,
+                     group_ff, gate_w, gate_scales, up_w, up_scales, down_w, down_scales, row_weight, y, workspace,
+                     workspace_bytes, as_stream(stream), avg);
+}
+
+int qw_moe_combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, int64_t tokens,
+                   int64_t top_k, int64_t d_model, void* out, void* stream) {
+  clear_error();
+  return combine(y, dtype, route_slot, top_idx, tokens, top_k, d_model, out, as_stream(stream));
+}
+
+int qw_moe_balance(const float* probs, const int32_t* counts, int64_t tokens, int64_t top_k, int64_t experts,
+                   float* importance, float* balance_out, void* stream) {
+  clear_error();
+  QW_REQUIRE(importance != nullptr, "importance buffer [experts] is required");
+  return balance(probs, counts, tokens, top_k, experts, importance, balance_out, as_stream(stream), nullptr);
+}
+
+size_t qw_moe_forward_workspace_bytes(int64_t tokens, int64_t d_model, int64_t experts, int64_t top_k, int64_t d_ff,
+                                      int act_dtype) {
+  if (tokens < 0 || d_model < 1 || experts < 1 || top_k < 1 || d_ff < 1) return 0;
+  return forward_workspace_bytes(tokens, d_model, experts, top_k, d_ff, act_dtype);
+}
+
+int qw_moe_forward(const void* x, int act_dtype, int64_t tokens, int64_t d_model, const void* router_w,
+                   int router_dtype, float temperature, const float* expert_bias, int64_t experts, int64_t top_k,
+                   int64_t capacity, int64_t d_ff, int w_format, int64_t group_in, int64_t group_ff,
+                   const void* gate_w, const float* gate_scales, const void* up_w, const float* up_scales,
+                   const void* down_w, const float* down_scales, void* out, float* probs, int32_t* top_idx,
+                   float* top_w, int32_t* counts, int32_t* kept_counts, int32_t* totals, int32_t* dropped_token,
+                   int32_t* dropped_expert, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  QW_REQUIRE(act_dtype == QW_F32 || act_dtype == QW_BF16, "activation dtype must be f32 or bf16");
+  QW_REQUIRE(tokens >= 0 && top_k >= 1 && experts >= 1 && d_model >= 1 && d_ff >= 1, "bad forward sizes");
+  QW_REQUIRE(capacity >= 0, "capacity must be >= 0");
+  QW_REQUIRE(probs && top_idx && top_w && counts && kept_counts && totals, "forward outputs are required");
+  if (tokens == 0) return QW_OK;
+  QW_REQUIRE(out && dropped_token && dropped_expert, "forward outputs are required");
+  const size_t need = forward_workspace_bytes(tokens, d_model, experts, top_k, d_ff, act_dtype);
+  if (!workspace || workspace_bytes < need)
+    return set_error(QW_ERR_WORKSPACE, "forward workspace needs %zu bytes, got %zu", need, workspace_bytes);
+  hipStream_t s = as_stream(stream);
+  const int64_t R = tokens * top_k;
+  Carver c(workspace);
+  float* logits = c.take<float>(static_cast<size_t>(tokens) * experts);
+  int32_t* slot_token = c.take<int32_t>(R);
+  float* slot_weight = c.take<float>(R);
+  int32_t* route_slot = c.take<int32_t>(R);
+  int32_t* kept_offsets = c.take<int32_t>(experts + 1);
+  char* y = c.take<char>(static_cast<size_t>(R) * d_model * act_size(act_dtype));
+  const size_t plan_ws = plan_workspace_bytes(tokens, top_k, experts);
+  char* pws = c.take<char>(plan_ws);
+  const int64_t max_rows = std::min<int64_t>(R, capacity * experts);
+  const size_t exp_ws = experts_workspace_bytes(R, experts, d_model, d_ff, act_dtype);
+  char* ews = c.take<char>(exp_ws);
+  int st = route(x, act_dtype, d_model, router_w, router_dtype, tokens, d_model, experts, top_k, temperature,
+                 expert_bias, logits, probs, top_idx, top_w, s);
+  if (st) return st;
+  st = plan(top_idx, top_w, tokens, top_k, experts, capacity, counts, kept_counts, kept_offsets, slot_token,
+            slot_weight, route_slot, dropped_token, dropped_expert, totals, pws, plan_ws, s);
+  if (st) return st;
+  if (max_rows > 0) {
+    const int64_t avg = (R + experts - 1) / experts;
+    st = qw::experts(x, act_dtype, slot_token, kept_offsets, experts, d_model, d_ff, max_rows, w_format, group_in,
+                     group_ff, gate_w, gate_scales, up_w, up_scales, down_w, down_scales, slot_weight, y, ews, exp_ws,
+                     s, avg < capacity ? avg : capacity);
+    if (st) return st;
+  }
+  return combine(y, act_dtype, route_slot, top_idx, tokens, top_k, d_model, out, s);
+}
+
+int qw_quantize(const void* w, int w_dtype, int64_t out_features, int64_t in_features, int bits, int64_t group_size,
+                void* qweight, float* scales, void* stream) {
+  clear_error();
+  return quantize(w, w_dtype, out_features, in_features, bits, group_size, qweight, scales, as_stream(stream));
+}
+
+int qw_dequantize(const void* qweight, const float* scales, int bits, int64_t out_features, int64_t in_features,
+                  int64_t group_size, float* out, void* stream) {
+  clear_error();
+  return dequantize(qweight, scales, bits, out_features, in_features, group_size, out, as_stream(stream));
+}
+
+int qw_grouped_matmul(const void* x, int act_dtype, const void* w, int w_format, const float* scales, int64_t group,
+                      int64_t experts, int64_t out_features, int64_t in_features, const int32_t* offsets,
+                      int64_t rows, void* out, void* stream) {
+  clear_error();
+  QW_REQUIRE(act_dtype == QW_F32 || act_dtype == QW_BF16, "grouped_matmul dtype must be f32 or bf16");
+  QW_REQUIRE(w_format >= QW_F32 && w_format <= QW_U4, "unknown weight format %d", w_format);
+  QW_REQUIRE(experts >= 1 && experts <= 65535 && out_features >= 1 && in_features >= 1 && rows >= 0 &&
+                 out_features <= INT32_MAX / 2 && in_features <= INT32_MAX / 2 && rows <= INT32_MAX,
+             "bad grouped_matmul sizes");
+  if (w_format == QW_I8 || w_format == QW_U4) {
+    QW_REQUIRE(group >= 1 && (w_format == QW_I8 || group % 2 == 0), "bad group size for quantised weights");
+    QW_REQUIRE(scales != nullptr, "quantised weights need scales");
+  }
+  if (rows == 0) return QW_OK;
+  QW_REQUIRE(x && w && offsets && out, "grouped_matmul pointers are required");
+  const WView v = make_wview(w_format, w, scales, out_features, in_features, group);
+  return grouped_matmul_generic(x, act_dtype, v, w_format, experts, offsets, out, as_stream(stream));
+}
+
+}  // extern "C"

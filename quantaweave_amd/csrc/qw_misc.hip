@@ -1,0 +1,228 @@
+// Permute, combine, balance loss, weight quantisation and the plain grouped
+// matmul.
+#include "qw_weights.h"
+#include "qw_ffn.h"
+
+namespace qw {
+
+// ---------------------------------------------------------------------------
+// Permute: out[s] = x[slot_token[s]] (src/quantweave_moe_model.py:195).
+// One block per row; 16-byte vectors when the row is 16-byte aligned.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void permute_kernel(const char* __restrict__ x, int64_t row_bytes,
+                                                      const int32_t* __restrict__ slot_token,
+                                                      const int32_t* __restrict__ totals, int max_rows,
+                                                      char* __restrict__ out) {
+  const int s = blockIdx.x;
+  const int n = min(*totals, max_rows);
+  if (s >= n) return;
+  const char* src = x + static_cast<int64_t>(slot_token[s]) * row_bytes;
+  char* dst = out + static_cast<int64_t>(s) * row_bytes;
+  if ((row_bytes & 15) == 0) {
+    const int64_t nv = row_bytes / 16;
+    for (int64_t i = threadIdx.x; i < nv; i += blockDim.x)
+      reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+  } else {
+    for (int64_t i = threadIdx.x; i < row_bytes; i += blockDim.x) dst[i] = src[i];
+  }
+}
+
+int permute(const void* x, int dtype, int64_t D, const int32_t* slot_token, const int32_t* totals, int64_t max_rows,
+            void* out, hipStream_t stream) {
+  QW_REQUIRE(dtype == QW_F32 || dtype == QW_BF16, "permute dtype must be f32 or bf16");
+  QW_REQUIRE(D >= 1 && max_rows >= 0 && max_rows <= INT32_MAX, "bad permute sizes");
+  if (max_rows == 0) return QW_OK;
+  QW_REQUIRE(x && slot_token && totals && out, "permute pointers are required");
+  const int64_t row_bytes = D * (dtype == QW_F32 ? 4 : 2);
+  permute_kernel<<<static_cast<unsigned>(max_rows), 256, 0, stream>>>(
+      static_cast<const char*>(x), row_bytes, slot_token, totals, static_cast<int>(max_rows), static_cast<char*>(out));
+  QW_LAUNCH_CHECK("permute_kernel");
+  return QW_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Combine: out[t] = sum over kept routes of t, in ascending expert order, with
+// a rounding to the output dtype after every add — the arithmetic of
+// `zeros_like(flat).index_add_(0, tokens, y)` on expert-ordered rows
+// (src/quantweave_moe_model.py:192, :201, :211).  One block per token.
+// ---------------------------------------------------------------------------
+template <int ACT, int VEC>
+__global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y, const int32_t* __restrict__ route_slot,
+                                                      const int32_t* __restrict__ top_idx, int K, int D,
+                                                      void* __restrict__ out) {
+  const int t = blockIdx.x;
+  int slot[64], ord[64];
+  int nk = 0;
+  for (int j = 0; j < K; ++j) {
+    const int s = route_slot[static_cast<int64_t>(t) * K + j];
+    if (s < 0) continue;
+    const int e = top_idx[static_cast<int64_t>(t) * K + j];
+    // insertion by expert id (distinct experts per token)
+    int p = nk;
+    while (p > 0 && ord[p - 1] > e) {
+      ord[p] = ord[p - 1];
+      slot[p] = slot[p - 1];
+      --p;
+    }
+    ord[p] = e;
+    slot[p] = s;
+    ++nk;
+  }
+  const int64_t row = static_cast<int64_t>(t) * D;
+  for (int c = threadIdx.x * VEC; c < D; c += blockDim.x * VEC) {
+    float acc[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
+    for (int j = 0; j < nk; ++j) {
+      const int64_t src = static_cast<int64_t>(slot[j]) * D + c;
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[v] = round_act<ACT>(acc[v] + load_act<ACT>(y, src + v));
+    }
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) store_act<ACT>(out, row + c + v, acc[v]);
+  }
+}
+
+int combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, int64_t T, int64_t K,
+            int64_t D, void* out, hipStream_t stream) {
+  QW_REQUIRE(dtype == QW_F32 || dtype == QW_BF16, "combine dtype must be f32 or bf16");
+  QW_REQUIRE(K >= 1 && K <= 64, "combine supports top_k in [1, 64], got %lld", (long long)K);
+  QW_REQUIRE(T >= 0 && T <= INT32_MAX && D >= 1 && D <= INT32_MAX, "bad combine sizes");
+  if (T == 0) return QW_OK;
+  QW_REQUIRE(y && route_slot && top_idx && out, "combine pointers are required");
+  const unsigned g = static_cast<unsigned>(T);
+  const int k = static_cast<int>(K), d = static_cast<int>(D);
+  if (dtype == QW_F32) {
+    if (D % 4 == 0) combine_kernel<QW_F32, 4><<<g, 256, 0, stream>>>(y, route_slot, top_idx, k, d, out);
+    else combine_kernel<QW_F32, 1><<<g, 256, 0, stream>>>(y, route_slot, top_idx, k, d, out);
+  } else {
+    if (D % 8 == 0) combine_kernel<QW_BF16, 8><<<g, 256, 0, stream>>>(y, route_slot, top_idx, k, d, out);
+    else combine_kernel<QW_BF16, 1><<<g, 256, 0, stream>>>(y, route_slot, top_idx, k, d, out);
+  }
+  QW_LAUNCH_CHECK("combine_kernel");
+  return QW_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Balance loss (src/quantweave_moe_model.py:152-154).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void importance_kernel(const float* __restrict__ probs, int T, int E,
+                                                         float* __restrict__ importance) {
+  __shared__ float red[256];
+  const int e = blockIdx.x;
+  float s = 0.0f;
+  for (int t = threadIdx.x; t < T; t += 256) s += probs[static_cast<int64_t>(t) * E + e];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int o = 128; o >= 1; o >>= 1) {
+    if (threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) importance[e] = red[0] / static_cast<float>(T);
+}
+
+__global__ void balance_kernel(const float* __restrict__ importance, const int32_t* __restrict__ counts, int T, int K,
+                               int E, float* __restrict__ balance) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  const float routes = static_cast<float>(static_cast<int64_t>(T) * K);
+  float s = 0.0f;
+  for (int e = 0; e < E; ++e) s += importance[e] * (static_cast<float>(counts[e]) / routes);
+  *balance = static_cast<float>(E) * s;
+}
+
+int balance(const float* probs, const int32_t* counts, int64_t T, int64_t K, int64_t E, float* importance,
+            float* bal, hipStream_t stream, float* scratch_importance) {
+  QW_REQUIRE(T >= 1 && T <= INT32_MAX && E >= 1 && E <= 1024 && K >= 1, "bad balance sizes");
+  QW_REQUIRE(probs && counts && bal, "balance pointers are required");
+  float* imp = importance ? importance : scratch_importance;
+  QW_REQUIRE(imp != nullptr, "balance needs an importance buffer");
+  importance_kernel<<<static_cast<unsigned>(E), 256, 0, stream>>>(probs, static_cast<int>(T), static_cast<int>(E), imp);
+  QW_LAUNCH_CHECK("importance_kernel");
+  balance_kernel<<<1, 64, 0, stream>>>(imp, counts, static_cast<int>(T), static_cast<int>(K), static_cast<int>(E), bal);
+  QW_LAUNCH_CHECK("balance_kernel");
+  return QW_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Quantisation, QuantizedLinear.from_linear (src/quantization.py:43-59).
+// One thread per (row, group).
+// ---------------------------------------------------------------------------
+template <int WDT, int BITS>
+__global__ void quantize_kernel(const void* __restrict__ w, int64_t rows, int64_t cols, int64_t group,
+                                int64_t groups, void* __restrict__ qweight, float* __restrict__ scales) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= rows * groups) return;
+  const int64_t row = i / groups, g = i % groups;
+  const int64_t c0 = g * group;
+  const float limit = BITS == 8 ? 127.0f : 7.0f;
+  const float lo = BITS == 8 ? -127.0f : -8.0f;
+  float amax = 0.0f;
+  for (int64_t c = c0; c < c0 + group; ++c) {
+    const float v = c < cols ? load_act<WDT>(w, row * cols + c) : 0.0f;
+    amax = fmaxf(amax, fabsf(v));
+  }
+  const float s = fmaxf(amax / limit, 1e-8f);
+  scales[row * groups + g] = s;
+  if (BITS == 8) {
+    int8_t* q = static_cast<int8_t*>(qweight) + row * groups * group;
+    for (int64_t c = c0; c < c0 + group; ++c) {
+      const float v = c < cols ? load_act<WDT>(w, row * cols + c) : 0.0f;
+      const float r = fminf(fmaxf(__builtin_rintf(v / s), lo), limit);
+      q[c] = static_cast<int8_t>(r);
+    }
+  } else {
+    uint8_t* q = static_cast<uint8_t*>(qweight) + row * (groups * group / 2);
+    for (int64_t c = c0; c < c0 + group; c += 2) {
+      const float v0 = c < cols ? load_act<WDT>(w, row * cols + c) : 0.0f;
+      const float v1 = c + 1 < cols ? load_act<WDT>(w, row * cols + c + 1) : 0.0f;
+      const int q0 = static_cast<int>(fminf(fmaxf(__builtin_rintf(v0 / s), lo), limit)) + 8;
+      const int q1 = static_cast<int>(fminf(fmaxf(__builtin_rintf(v1 / s), lo), limit)) + 8;
+      q[c / 2] = static_cast<uint8_t>(q0 | (q1 << 4));
+    }
+  }
+}
+
+int quantize(const void* w, int wdt, int64_t rows, int64_t cols, int bits, int64_t group, void* qweight, float* scales,
+             hipStream_t stream) {
+  QW_REQUIRE(bits == 4 || bits == 8, "bits must be 4 or 8");
+  QW_REQUIRE(wdt == QW_F32 || wdt == QW_BF16, "weight dtype must be f32 or bf16");
+  QW_REQUIRE(group >= 1, "group_size must be positive");
+  QW_REQUIRE(!(bits == 4 && (group % 2)), "group_size must be even for 4-bit weights");
+  QW_REQUIRE(rows >= 0 && cols >= 1, "bad quantize sizes");
+  if (rows == 0) return QW_OK;
+  QW_REQUIRE(w && qweight && scales, "quantize pointers are required");
+  const int64_t groups = ceil_div(cols, group);
+  const int64_t n = rows * groups;
+  const unsigned g = static_cast<unsigned>(ceil_div(n, 256));
+  if (wdt == QW_F32 && bits == 8) quantize_kernel<QW_F32, 8><<<g, 256, 0, stream>>>(w, rows, cols, group, groups, qweight, scales);
+  else if (wdt == QW_F32) quantize_kernel<QW_F32, 4><<<g, 256, 0, stream>>>(w, rows, cols, group, groups, qweight, scales);
+  else if (bits == 8) quantize_kernel<QW_BF16, 8><<<g, 256, 0, stream>>>(w, rows, cols, group, groups, qweight, scales);
+  else quantize_kernel<QW_BF16, 4><<<g, 256, 0, stream>>>(w, rows, cols, group, groups, qweight, scales);
+  QW_LAUNCH_CHECK("quantize_kernel");
+  return QW_OK;
+}
+
+template <int WF>
+__global__ void dequantize_kernel(WView v, float* __restrict__ out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= v.rows * v.cols) return;
+  const int64_t row = i / v.cols, col = i % v.cols;
+  out[i] = load_weight<WF>(v, 0, row, col);
+}
+
+int dequantize(const void* qweight, const float* scales, int bits, int64_t rows, int64_t cols, int64_t group,
+               float* out, hipStream_t stream) {
+  QW_REQUIRE(bits == 4 || bits == 8, "bits must be 4 or 8");
+  QW_REQUIRE(group >= 1 && !(bits == 4 && (group % 2)), "bad group_size");
+  QW_REQUIRE(rows >= 0 && cols >= 1, "bad dequantize sizes");
+  if (rows == 0) return QW_OK;
+  QW_REQUIRE(qweight && scales && out, "dequantize pointers are required");
+  const WView v = make_wview(bits == 8 ? QW_I8 : QW_U4, qweight, scales, rows, cols, group);
+  const unsigned g = static_cast<unsigned>(ceil_div(rows * cols, 256));
+  if (bits == 8) dequantize_kernel<QW_I8><<<g, 256, 0, stream>>>(v, out);
+  else dequantize_kernel<QW_U4><<<g, 256, 0, stream>>>(v, out);
+  QW_LAUNCH_CHECK("dequantize_kernel");
+  return QW_OK;
+}
+
+}  // namespace qw

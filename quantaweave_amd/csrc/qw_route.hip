@@ -1,0 +1,249 @@
+// Router logits, softmax, top-k and renormalisation on gfx950.
+//
+// Reference: src/quantweave_moe_model.py:124-137 (TopKMoE.forward, fp32 routing
+// with autocast disabled).  This file is compiled with -ffp-contract=off: the
+// softmax below uses only IEEE-754 single-precision operations (add, mul, fma,
+// div, rint) in a fixed order, so the same sequence evaluated on any IEEE
+// machine gives the same bits.  That is what makes the routing decisions
+// (indices, capacity slots, drops) reproducible bit-for-bit from the logits.
+#include "qw_common.h"
+
+namespace qw {
+
+// ---------------------------------------------------------------------------
+// Deterministic exp for the softmax argument x = logit - max <= 0.
+// Cody-Waite reduction x = n*ln2 + r with ln2 split into a 16-bit head
+// (0x3f317200, so n*head is exact) and a tail, |r| <= ln2/2; e^r by its
+// degree-7 Taylor polynomial (truncation < 0.1 ulp) in Horner form with fma;
+// scaling by 2^n through the exponent field, in two steps below 2^-126 so the
+// only rounding of a subnormal result is the last multiply.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float det_expf(float x) {
+  if (!(x >= -104.0f)) return (x != x) ? x : 0.0f;  // NaN passes through; e^-104 < 2^-150
+  const float n = __builtin_rintf(x * 1.4426950216293335f);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+  r = __builtin_fmaf(-n, 1.428606765330187e-06f, r);
+  float p = 0.00019841270113829523f;
+  p = __builtin_fmaf(p, r, 0.0013888889225199819f);
+  p = __builtin_fmaf(p, r, 0.008333333767950535f);
+  p = __builtin_fmaf(p, r, 0.0416666679084301f);
+  p = __builtin_fmaf(p, r, 0.1666666716337204f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  const int ni = static_cast<int>(n);
+  if (ni >= -126) return p * __int_as_float((ni + 127) << 23);
+  return (p * __int_as_float((ni + 127 + 64) << 23)) * 5.421010862427522e-20f;  // * 2^-64
+}
+
+// Total order on floats as unsigned keys: -inf < ... < -0 < +0 < ... < +inf < NaN.
+__device__ __forceinline__ uint32_t sortable_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// ---------------------------------------------------------------------------
+// logits[t, e] = (x[t, :] . W[e, :]) / temperature, fp32 accumulation.
+// 64x64 output tile per 256-thread block, K staged through LDS in slices of 16.
+// ---------------------------------------------------------------------------
+template <int XDT, int WDT>
+__global__ __launch_bounds__(256) void router_logits_kernel(const void* __restrict__ x, int64_t x_stride,
+                                                            const void* __restrict__ w, int T, int D, int E,
+                                                            float temperature, float* __restrict__ logits) {
+  constexpr int TM = 64, TN = 64, TK = 16;
+  __shared__ float xs[TK][TM + 4];
+  __shared__ float ws[TK][TN + 4];
+  const int tid = threadIdx.x;
+  const int t0 = blockIdx.x * TM, e0 = blockIdx.y * TN;
+  const int ty = tid / 16, tx = tid % 16;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < D; k0 += TK) {
+    for (int i = tid; i < TM * TK; i += 256) {
+      const int m = i / TK, kk = i % TK;
+      const int t = t0 + m, k = k0 + kk;
+      xs[kk][m] = (t < T && k < D) ? load_act<XDT>(x, static_cast<int64_t>(t) * x_stride + k) : 0.0f;
+      const int e = e0 + m;
+      ws[kk][m] = (e < E && k < D) ? load_act<WDT>(w, static_cast<int64_t>(e) * D + k) : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < TK; ++kk) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = xs[kk][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = ws[kk][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = t0 + ty * 4 + i;
+    if (t >= T) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = e0 + tx * 4 + j;
+      if (e < E) logits[static_cast<int64_t>(t) * E + e] = acc[i][j] / temperature;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// One wavefront per token.  Lane l owns experts l, l+64, ..., l+64*(EPL-1).
+//   m = max_e L_e;  q_e = det_expf(L_e - m)
+//   S = (per-lane sequential sum over its experts in index order) reduced by
+//       the xor butterfly with lane offsets 32, 16, 8, 4, 2, 1
+//   p_e = q_e / S
+//   top-k: k rounds of a wave argmax on (key desc, expert asc), key = p_e
+//          (or L_e + bias_e when a bias is given)
+//   w_j = p_{idx_j} / (((p_{idx_0} + p_{idx_1}) + p_{idx_2}) + ...)
+// ---------------------------------------------------------------------------
+template <int EPL>
+__global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits, int T, int E, int K,
+                                                         const float* __restrict__ bias, float* __restrict__ probs,
+                                                         int32_t* __restrict__ top_idx, float* __restrict__ top_w) {
+  const int lane = threadIdx.x % kWave;
+  const int t = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (t >= T) return;
+  const float* row = logits + static_cast<int64_t>(t) * E;
+  float l[EPL], p[EPL];
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int c = 0; c < EPL; ++c) {
+    const int e = lane + c * kWave;
+    l[c] = (e < E) ? row[e] : -__builtin_inff();
+    m = fmaxf(m, l[c]);
+  }
+  // fmaxf drops NaN; a NaN logit must poison the row as it does in torch.
+  bool has_nan = false;
+#pragma unroll
+  for (int c = 0; c < EPL; ++c) has_nan |= (l[c] != l[c]);
+  m = wave_max(m);
+  if (__any(has_nan)) m = __builtin_nanf("");
+  float s = 0.0f;
+#pragma unroll
+  for (int c = 0; c < EPL; ++c) {
+    const int e = lane + c * kWave;
+    p[c] = (e < E) ? det_expf(l[c] - m) : 0.0f;
+    s += p[c];
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, kWave);
+#pragma unroll
+  for (int c = 0; c < EPL; ++c) {
+    const int e = lane + c * kWave;
+    p[c] = p[c] / s;
+    if (probs != nullptr && e < E) probs[static_cast<int64_t>(t) * E + e] = p[c];
+  }
+  // selection keys
+  uint32_t key[EPL];
+#pragma unroll
+  for (int c = 0; c < EPL; ++c) {
+    const int e = lane + c * kWave;
+    const float v = (bias != nullptr && e < E) ? l[c] + bias[e] : p[c];
+    key[c] = (e < E) ? sortable_key(v) : 0u;
+  }
+  uint32_t taken = 0;
+  float sel_sum = 0.0f;
+  // k <= E <= 64*EPL; selected probabilities stay in registers of lane 0 via shuffles
+  for (int j = 0; j < K; ++j) {
+    uint64_t best = 0;
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) {
+      const int e = lane + c * kWave;
+      if (e < E && !((taken >> c) & 1u)) {
+        const uint64_t cand = (static_cast<uint64_t>(key[c]) << 32) | (0xffffffffu - static_cast<uint32_t>(e));
+        best = cand > best ? cand : best;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const uint64_t other = __shfl_xor(best, o, kWave);
+      best = other > best ? other : best;
+    }
+    const int e_sel = static_cast<int>(0xffffffffu - static_cast<uint32_t>(best & 0xffffffffu));
+    const int owner = e_sel % kWave, slot = e_sel / kWave;
+    float p_sel = 0.0f;
+#pragma unroll
+    for (int c = 0; c < EPL; ++c)
+      if (c == slot) p_sel = p[c];
+    p_sel = __shfl(p_sel, owner, kWave);
+    if (lane == owner) taken |= 1u << slot;
+    sel_sum = (j == 0) ? p_sel : sel_sum + p_sel;
+    if (lane == 0) {
+      top_idx[static_cast<int64_t>(t) * K + j] = e_sel;
+      top_w[static_cast<int64_t>(t) * K + j] = p_sel;  // renormalised below
+    }
+  }
+  if (lane == 0) {
+    for (int j = 0; j < K; ++j) {
+      float* w = top_w + static_cast<int64_t>(t) * K + j;
+      *w = *w / sel_sum;
+    }
+  }
+}
+
+static int launch_topk(const float* logits, int T, int E, int K, const float* bias, float* probs, int32_t* top_idx,
+                       float* top_w, hipStream_t stream) {
+  const int waves_per_block = 4;
+  const dim3 grid(static_cast<unsigned>(ceil_div(T, waves_per_block)));
+  const dim3 block(waves_per_block * kWave);
+  const int epl = static_cast<int>(ceil_div(E, kWave));
+  if (epl <= 1) route_topk_kernel<1><<<grid, block, 0, stream>>>(logits, T, E, K, bias, probs, top_idx, top_w);
+  else if (epl <= 2) route_topk_kernel<2><<<grid, block, 0, stream>>>(logits, T, E, K, bias, probs, top_idx, top_w);
+  else if (epl <= 4) route_topk_kernel<4><<<grid, block, 0, stream>>>(logits, T, E, K, bias, probs, top_idx, top_w);
+  else if (epl <= 8) route_topk_kernel<8><<<grid, block, 0, stream>>>(logits, T, E, K, bias, probs, top_idx, top_w);
+  else route_topk_kernel<16><<<grid, block, 0, stream>>>(logits, T, E, K, bias, probs, top_idx, top_w);
+  QW_LAUNCH_CHECK("route_topk_kernel");
+  return QW_OK;
+}
+
+int route_validate(int64_t T, int64_t E, int64_t K) {
+  QW_REQUIRE(T >= 0 && T <= INT32_MAX / 64, "tokens out of range: %lld", (long long)T);
+  QW_REQUIRE(E >= 1 && E <= 1024, "experts must be in [1, 1024], got %lld", (long long)E);
+  QW_REQUIRE(K >= 1 && K <= E, "top_k must be between 1 and num_experts (got %lld, %lld)", (long long)K,
+             (long long)E);
+  QW_REQUIRE(T * K <= INT32_MAX, "tokens*top_k exceeds int32");
+  return QW_OK;
+}
+
+int route_from_logits(const float* logits, int64_t T, int64_t E, int64_t K, const float* bias, float* probs,
+                      int32_t* top_idx, float* top_w, hipStream_t stream) {
+  int st = route_validate(T, E, K);
+  if (st) return st;
+  if (T == 0) return QW_OK;
+  QW_REQUIRE(logits && top_idx && top_w, "logits, top_idx and top_w are required");
+  return launch_topk(logits, static_cast<int>(T), static_cast<int>(E), static_cast<int>(K), bias, probs, top_idx,
+                     top_w, stream);
+}
+
+int route(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int64_t T, int64_t D, int64_t E,
+          int64_t K, float temperature, const float* bias, float* logits, float* probs, int32_t* top_idx,
+          float* top_w, hipStream_t stream) {
+  int st = route_validate(T, E, K);
+  if (st) return st;
+  QW_REQUIRE(xdt == QW_F32 || xdt == QW_BF16, "router input dtype must be f32 or bf16");
+  QW_REQUIRE(wdt == QW_F32 || wdt == QW_BF16, "router weight dtype must be f32 or bf16");
+  QW_REQUIRE(D >= 1 && D <= INT32_MAX, "d_model out of range");
+  QW_REQUIRE(x_stride >= D, "x row stride %lld smaller than d_model %lld", (long long)x_stride, (long long)D);
+  QW_REQUIRE(temperature > 0.0f, "router_temperature must be positive");
+  if (T == 0) return QW_OK;
+  QW_REQUIRE(x && w && logits && top_idx && top_w, "x, router_w, logits, top_idx and top_w are required");
+  const dim3 grid(static_cast<unsigned>(ceil_div(T, 64)), static_cast<unsigned>(ceil_div(E, 64)));
+  const int t = static_cast<int>(T), d = static_cast<int>(D), e = static_cast<int>(E);
+#define QW_RL(XD, WD) \
+  router_logits_kernel<XD, WD><<<grid, 256, 0, stream>>>(x, x_stride, w, t, d, e, temperature, logits)
+  if (xdt == QW_F32 && wdt == QW_F32) QW_RL(QW_F32, QW_F32);
+  else if (xdt == QW_F32) QW_RL(QW_F32, QW_BF16);
+  else if (wdt == QW_F32) QW_RL(QW_BF16, QW_F32);
+  else QW_RL(QW_BF16, QW_BF16);
+#undef QW_RL
+  QW_LAUNCH_CHECK("router_logits_kernel");
+  return launch_topk(logits, t, e, static_cast<int>(K), bias, probs, top_idx, top_w, stream);
+}
+
+}  // namespace qw

@@ -1,0 +1,310 @@
+"""Routed MoE layer — drop-in for QuantaWeave's ``TopKMoE`` on MI355X.
+
+``TopKMoE`` keeps the reference module's constructor, parameters
+(``router``, ``experts[i].{gate,up,down}``), runtime switches and forward
+signature (src/quantweave_moe_model.py:63-272).  Its forward is one call into
+the C ABI (``qw_moe_forward``): router, softmax/top-k, capacity plan, grouped
+SwiGLU experts and the weighted combine all run as HIP kernels on the current
+stream, with no host synchronisation.  It is forward-only (inference); the
+grouped backward is not part of this library.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor, nn
+
+from . import _hip, _lib
+from .quantization import QuantizedLinear
+
+
+@dataclass
+class QuantaWeaveConfig:
+    """Same fields, defaults and validation as src/quantweave_moe_model.py:15-48."""
+
+    vocab_size: int = 7168
+    hidden_size: int = 64
+    layers: int = 2
+    ffn_size: int = 128
+    num_experts: int = 184
+    top_k: int = 1
+    attention_heads: int = 4
+    max_sequence_length: int = 256
+    router_aux_loss_coef: float = 0.01
+    capacity_factor: float = 1.25
+    min_expert_capacity: int = 4
+    drop_overflow_tokens: bool = True
+    overflow_policy: str = "drop"
+    router_temperature: float = 1.0
+
+    def __post_init__(self) -> None:
+        if self.vocab_size < 2 or self.hidden_size < 1 or self.layers < 1:
+            raise ValueError("vocab_size, hidden_size, and layers must be positive")
+        if self.ffn_size < 1 or self.attention_heads < 1:
+            raise ValueError("ffn_size and attention_heads must be positive")
+        if self.hidden_size % self.attention_heads:
+            raise ValueError("hidden_size must be divisible by attention_heads")
+        if self.num_experts < 1 or not 1 <= self.top_k <= self.num_experts:
+            raise ValueError("top_k must be between 1 and num_experts")
+        if self.max_sequence_length < 2:
+            raise ValueError("max_sequence_length must be at least 2")
+        if self.capacity_factor < 0 or self.min_expert_capacity < 1:
+            raise ValueError("capacity_factor must be >= 0 and min_expert_capacity must be positive")
+        if self.overflow_policy not in {"drop", "residual"}:
+            raise ValueError("overflow_policy must be 'drop' or 'residual'")
+        if self.router_temperature <= 0:
+            raise ValueError("router_temperature must be positive")
+
+
+class SparseSwiGLU(nn.Module):
+    """down(silu(gate(x)) * up(x)) with bias-free projections (src/quantweave_moe_model.py:51-60).
+
+    Holds the parameters of one expert; TopKMoE evaluates all experts together
+    in the grouped HIP kernels.  Calling an expert on its own runs the grouped
+    kernel with one expert."""
+
+    def __init__(self, config, ffn_size: Optional[int] = None) -> None:
+        super().__init__()
+        ffn_size = ffn_size or config.ffn_size
+        self.gate = nn.Linear(config.hidden_size, ffn_size, bias=False)
+        self.up = nn.Linear(config.hidden_size, ffn_size, bias=False)
+        self.down = nn.Linear(ffn_size, config.hidden_size, bias=False)
+
+    def forward(self, hidden: Tensor) -> Tensor:
+        from .moe_kernels import grouped_swiglu
+
+        lead = hidden.shape[:-1]
+        flat = hidden.reshape(-1, hidden.size(-1))
+        return grouped_swiglu(flat, nn.ModuleList([self]), [flat.size(0)]).reshape(*lead, -1)
+
+
+def _expert_format(experts: nn.ModuleList) -> tuple[int, int, int]:
+    """(weight format, gate/up group, down group) shared by every projection."""
+    first = experts[0].gate
+    if isinstance(first, QuantizedLinear):
+        fmt = first.w_format
+        g_in, g_ff = first.group_size, experts[0].down.group_size
+        for e in experts:
+            for name, g in (("gate", g_in), ("up", g_in), ("down", g_ff)):
+                p = getattr(e, name)
+                if not isinstance(p, QuantizedLinear) or p.w_format != fmt or p.group_size != g:
+                    raise ValueError("all experts must share one quantisation format and group size")
+        return fmt, g_in, g_ff
+    dt = first.weight.dtype
+    for e in experts:
+        for name in ("gate", "up", "down"):
+            p = getattr(e, name)
+            if not isinstance(p, nn.Linear) or p.bias is not None or p.weight.dtype != dt:
+                raise ValueError("experts must be bias-free nn.Linear (one dtype) or QuantizedLinear projections")
+    if dt not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"expert weight dtype {dt} is not supported (float32 or bfloat16)")
+    return (_lib.QW_F32 if dt == torch.float32 else _lib.QW_BF16), 0, 0
+
+
+class ExpertPack:
+    """Experts' weights stacked once into [E, out, in] device buffers.
+
+    Replaces the per-call ``torch.stack`` of src/moe_kernels.py:191-193; the pack
+    is rebuilt only when a parameter or buffer changes (tracked by its storage
+    pointer and version counter)."""
+
+    def __init__(self, experts: nn.ModuleList) -> None:
+        self.fmt, self.group_in, self.group_ff = _expert_format(experts)
+        self.key = ExpertPack.signature(experts)
+        if self.fmt in (_lib.QW_F32, _lib.QW_BF16):
+            self.gate = torch.stack([e.gate.weight.detach() for e in experts]).contiguous()
+            self.up = torch.stack([e.up.weight.detach() for e in experts]).contiguous()
+            self.down = torch.stack([e.down.weight.detach() for e in experts]).contiguous()
+            self.gate_s = self.up_s = self.down_s = None
+        else:
+            self.gate = torch.stack([e.gate.qweight for e in experts]).contiguous()
+            self.up = torch.stack([e.up.qweight for e in experts]).contiguous()
+            self.down = torch.stack([e.down.qweight for e in experts]).contiguous()
+            self.gate_s = torch.stack([e.gate.scales.float() for e in experts]).contiguous()
+            self.up_s = torch.stack([e.up.scales.float() for e in experts]).contiguous()
+            self.down_s = torch.stack([e.down.scales.float() for e in experts]).contiguous()
+
+    @staticmethod
+    def signature(experts: nn.ModuleList) -> tuple:
+        sig = []
+        for e in experts:
+            for name in ("gate", "up", "down"):
+                p = getattr(e, name)
+                tensors = (p.qweight, p.scales) if isinstance(p, QuantizedLinear) else (p.weight,)
+                sig.extend((t.data_ptr(), t._version, t.dtype, tuple(t.shape)) for t in tensors)
+        return tuple(sig)
+
+    def args(self) -> list:
+        return [self.fmt, self.group_in, self.group_ff, _hip.ptr(self.gate), _hip.ptr(self.gate_s),
+                _hip.ptr(self.up), _hip.ptr(self.up_s), _hip.ptr(self.down), _hip.ptr(self.down_s)]
+
+
+def packed_experts(owner: nn.Module, experts: nn.ModuleList) -> ExpertPack:
+    pack = getattr(owner, "_qw_pack", None)
+    if pack is None or pack.key != ExpertPack.signature(experts):
+        pack = ExpertPack(experts)
+        owner._qw_pack = pack
+    return pack
+
+
+class TopKMoE(nn.Module):
+    """Top-k routed mixture of SwiGLU experts (src/quantweave_moe_model.py:63-272).
+
+    Routing runs in fp32.  Routes are ordered by (expert, -weight, route id) and
+    each expert keeps its first ``capacity`` routes; the others are skipped and
+    reported as overflow (and as dropped under the "drop" policy).
+    """
+
+    def __init__(self, config, num_local_experts: Optional[int] = None, tensor_parallel=None) -> None:
+        super().__init__()
+        if config.top_k < 1 or config.top_k > config.num_experts:
+            raise ValueError("top_k must be between 1 and num_experts")
+        self.tp_size = getattr(tensor_parallel, "tp_size", 1)
+        if self.tp_size > 1:
+            raise ValueError("tensor-parallel MoE is not supported by the single-GPU HIP path")
+        self.tp_group = None
+        self.num_experts = config.num_experts
+        self.top_k = config.top_k
+        self.capacity_factor = config.capacity_factor
+        self.min_expert_capacity = config.min_expert_capacity
+        self.drop_overflow_tokens = config.drop_overflow_tokens
+        self.overflow_policy = config.overflow_policy
+        self.router_temperature = config.router_temperature
+        self.router = nn.Linear(config.hidden_size, config.num_experts, bias=False)
+        self.num_local_experts = num_local_experts or config.num_experts
+        if self.num_local_experts != self.num_experts:
+            raise ValueError("expert-parallel sharding is not supported by the single-GPU HIP path")
+        self.experts = nn.ModuleList(SparseSwiGLU(config, config.ffn_size) for _ in range(self.num_local_experts))
+        # runtime switches (not parameters or saved state), as in the reference
+        self.collect_stats = False
+        self.static_dispatch = False
+        self.profile_experts = False
+        self.use_triton_kernels = True  # grouped kernels are the only executor here
+        self.expert_bias: Optional[Tensor] = None
+        self.capacity_scale: float = 1.0
+        self.expert_seconds = [0.0] * self.num_local_experts
+        self.last_top_indices: Optional[Tensor] = None
+        self.last_stats: dict[str, Tensor] = {}
+        self.last_plan: dict[str, Tensor] = {}
+
+    def capacity(self, num_tokens: int) -> int:
+        """Route slots per expert (src/quantweave_moe_model.py:100-111)."""
+        if self.capacity_factor > 0 and self.drop_overflow_tokens:
+            return max(
+                self.min_expert_capacity,
+                math.ceil(num_tokens * self.top_k / self.num_experts * self.capacity_factor * self.capacity_scale),
+            )
+        return num_tokens * self.top_k
+
+    def forward(self, hidden: Tensor, token_domains: Optional[Tensor] = None,
+                num_domains: int = 0) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+        """Returns (output, balance_loss, dropped_routes, overflow_routes, domain_loss)."""
+        _hip.require_device(hidden, "TopKMoE.forward")
+        if hidden.requires_grad and torch.is_grad_enabled():
+            raise RuntimeError("the HIP TopKMoE is forward-only; run it under torch.no_grad() / inference_mode()")
+        batch, sequence, width = hidden.shape
+        flat = hidden.reshape(-1, width).contiguous()
+        act = _hip.act_code(flat, "TopKMoE.forward")
+        dev = flat.device
+        T, E, K = flat.size(0), self.num_experts, self.top_k
+        router_w = self.router.weight.detach()
+        if router_w.dtype not in (torch.float32, torch.bfloat16):
+            router_w = router_w.float()
+        router_w = router_w.contiguous()
+        bias = None
+        if self.expert_bias is not None:
+            bias = self.expert_bias.detach().to(dev, torch.float32).contiguous()
+        pack = packed_experts(self, self.experts)
+        # static dispatch is the capacity-free evaluation (src/quantweave_moe_model.py:235-245)
+        cap = T * K if self.static_dispatch else self.capacity(T)
+        R = T * K
+        out = torch.empty_like(flat)
+        probs = torch.empty(T, E, dtype=torch.float32, device=dev)
+        top_idx = torch.empty(T, K, dtype=torch.int32, device=dev)
+        top_w = torch.empty(T, K, dtype=torch.float32, device=dev)
+        counts = torch.empty(E, dtype=torch.int32, device=dev)
+        kept_counts = torch.empty(E, dtype=torch.int32, device=dev)
+        totals = torch.zeros(2, dtype=torch.int32, device=dev)
+        dropped_token = torch.empty(max(R, 1), dtype=torch.int32, device=dev)
+        dropped_expert = torch.empty(max(R, 1), dtype=torch.int32, device=dev)
+        importance = torch.empty(E, dtype=torch.float32, device=dev)
+        balance = torch.zeros((), dtype=torch.float32, device=dev)
+        s = _hip.stream(dev)
+        if T:
+            nbytes = _lib.load().qw_moe_forward_workspace_bytes(T, width, E, K, self.experts[0].gate.out_features, act)
+            ws = _hip.workspace(nbytes, dev)
+            _lib.call("qw_moe_forward", _hip.ptr(flat), act, T, width, _hip.ptr(router_w),
+                      _hip.act_code(router_w, "router"), float(self.router_temperature), _hip.ptr(bias), E, K, cap,
+                      self.experts[0].gate.out_features, *pack.args(), _hip.ptr(out), _hip.ptr(probs),
+                      _hip.ptr(top_idx), _hip.ptr(top_w), _hip.ptr(counts), _hip.ptr(kept_counts), _hip.ptr(totals),
+                      _hip.ptr(dropped_token), _hip.ptr(dropped_expert), _hip.ptr(ws), nbytes, s)
+            _lib.call("qw_moe_balance", _hip.ptr(probs), _hip.ptr(counts), T, K, E, _hip.ptr(importance),
+                      _hip.ptr(balance), s)
+        self.last_top_indices = top_idx.long()
+        self.last_plan = dict(counts=counts, kept_counts=kept_counts, totals=totals, top_w=top_w,
+                              dropped_token=dropped_token, dropped_expert=dropped_expert)
+        overflow_routes = totals[1].long()
+        zero = torch.zeros((), device=dev, dtype=torch.long)
+        dropped_routes = overflow_routes if self.overflow_policy == "drop" else zero
+        if self.collect_stats:
+            self._record_stats(probs, top_idx, kept_counts, totals, dropped_token, dropped_expert)
+        domain_loss = probs.new_zeros(())
+        if token_domains is not None and num_domains > 1:
+            domain_loss = self._domain_loss(probs, token_domains, num_domains)
+        return out.reshape(batch, sequence, width), balance, dropped_routes, overflow_routes, domain_loss
+
+    def _domain_loss(self, router_probs: Tensor, token_domains: Tensor, num_domains: int) -> Tensor:
+        """Mean pairwise cosine similarity of the domains' routing profiles
+        (src/quantweave_moe_model.py:247-257); an auxiliary loss off the FFN path."""
+        membership = F.one_hot(token_domains.reshape(-1).long(), num_domains).to(router_probs.dtype)
+        counts = membership.sum(dim=0)
+        profiles = (membership.t() @ router_probs) / counts.clamp(min=1)[:, None]
+        profiles = F.normalize(profiles[counts > 0], dim=-1)
+        present = profiles.size(0)
+        if present < 2:
+            return router_probs.new_zeros(())
+        similarity = profiles @ profiles.t()
+        return (similarity.sum() - similarity.diagonal().sum()) / (present * (present - 1))
+
+    @torch.no_grad()
+    def _record_stats(self, router_probs, top_indices, kept_counts, totals, dropped_token, dropped_expert) -> None:
+        """src/quantweave_moe_model.py:259-272 (reads the dropped count back to size the lists)."""
+        entropy = -(router_probs * router_probs.clamp_min(1e-12).log()).sum(dim=-1)
+        top_probability = router_probs.max(dim=-1).values
+        n_drop = int(totals[1].item())
+        self.last_stats = {
+            "expert_load": kept_counts.long(),
+            "expert_assigned": torch.bincount(top_indices.reshape(-1).long(), minlength=self.num_experts),
+            "importance": router_probs.mean(dim=0),
+            "entropy_mean": entropy.mean(),
+            "confidence_mean": top_probability.mean(),
+            "confidence_hist": torch.histc(top_probability.float(), bins=10, min=0.0, max=1.0),
+            "dropped_tokens": dropped_token[:n_drop].long(),
+            "dropped_experts": dropped_expert[:n_drop].long(),
+        }
+
+
+def set_moe_kernel(model: nn.Module, kernel: str) -> str:
+    """Expert-compute selection (src/quantweave_moe_model.py:381-393).
+
+    "hip" is the grouped HIP path; "triton" and "auto" select it too (the
+    grouped executor of this build).  "loop" — the reference's per-expert
+    PyTorch loop — has no counterpart here and raises."""
+    if kernel not in {"loop", "triton", "auto", "hip"}:
+        raise ValueError("kernel must be loop, triton, hip or auto")
+    from .moe_kernels import kernels_available
+
+    device = next(model.parameters()).device
+    if kernel == "loop":
+        raise RuntimeError("the per-expert loop executor is not part of the HIP build; use 'hip' or 'auto'")
+    if not kernels_available(device):
+        raise RuntimeError("the HIP MoE kernels need a ROCm device and the built libqwmoe.so")
+    for m in model.modules():
+        if isinstance(m, TopKMoE):
+            m.use_triton_kernels = True
+    return "hip"

@@ -1,0 +1,149 @@
+"""Grouped expert kernels — drop-in for QuantaWeave's moe_kernels.py on MI355X.
+
+Same public names and argument meaning as src/moe_kernels.py:
+``kernels_available``, ``experts_support_grouped``, ``GroupedPlan``,
+``grouped_matmul``, ``compute_dtype``, ``grouped_swiglu`` and ``benchmark``.
+The kernels are hand-written HIP for gfx950 behind the C ABI
+(include/qwmoe.h), forward only.  Differences from the reference:
+
+* quantised experts (``QuantizedLinear``) are supported by the grouped path
+  (the reference restricts it to nn.Linear, src/moe_kernels.py:174-176);
+* the tile schedule is built on the device from per-expert row offsets, so
+  ``GroupedPlan`` only carries those offsets (plus the reference's ``tiles`` /
+  ``rows`` bookkeeping);
+* expert weights are stacked once and cached, not re-stacked per call.
+"""
+
+from __future__ import annotations
+
+import time
+from typing import Optional, Sequence
+
+import torch
+from torch import Tensor, nn
+
+from . import _hip, _lib
+from .moe import packed_experts
+from .quantization import QuantizedLinear
+
+BLOCK_M = 32  # row-tile height used for the reference's `tiles` count
+
+
+def kernels_available(device: torch.device) -> bool:
+    """True when the HIP library is built and `device` is a ROCm device (src/moe_kernels.py:34-35)."""
+    device = torch.device(device)
+    return _lib.available() and device.type == "cuda" and torch.cuda.is_available() and torch.version.hip is not None
+
+
+class GroupedPlan:
+    """Row blocks of expert-sorted rows (src/moe_kernels.py:92-111)."""
+
+    def __init__(self, counts: Sequence[int], device: torch.device) -> None:
+        counts = [int(c) for c in counts]
+        if any(c < 0 for c in counts):
+            raise ValueError("counts must be non-negative")
+        offsets, total = [0], 0
+        for c in counts:
+            total += c
+            offsets.append(total)
+        self.tiles = sum(-(-c // BLOCK_M) for c in counts)
+        self.rows = total
+        self.num_experts = len(counts)
+        self.counts = counts
+        self.offsets = torch.tensor(offsets, dtype=torch.int32, device=device)
+
+
+def experts_support_grouped(experts: nn.ModuleList) -> bool:
+    """Bias-free nn.Linear experts (src/moe_kernels.py:174-176) or QuantizedLinear experts of one format."""
+    def ok(p) -> bool:
+        return isinstance(p, QuantizedLinear) or (isinstance(p, nn.Linear) and p.bias is None)
+
+    return all(ok(getattr(e, name, None)) for e in experts for name in ("gate", "up", "down"))
+
+
+def compute_dtype(inputs: Tensor) -> torch.dtype:
+    """The autocast dtype when autocast is on, else the input dtype (src/moe_kernels.py:179-183)."""
+    device_type = inputs.device.type
+    if torch.is_autocast_enabled(device_type):
+        return torch.get_autocast_dtype(device_type)
+    return inputs.dtype
+
+
+def grouped_matmul(x: Tensor, weight: Tensor, plan: GroupedPlan) -> Tensor:
+    """Per-expert x @ W[e]^T over expert-sorted rows; weight is [E, out, in] (src/moe_kernels.py:167-171).
+
+    Forward only: the result carries no autograd history."""
+    _hip.require_device(x, "grouped_matmul")
+    act = _hip.act_code(x, "grouped_matmul")
+    if weight.dim() != 3 or weight.size(0) != plan.num_experts or weight.size(2) != x.size(1):
+        raise ValueError("weight must be [experts, out, in] matching the plan and x")
+    if x.size(0) != plan.rows:
+        raise ValueError(f"x has {x.size(0)} rows but the plan covers {plan.rows}")
+    x = x.contiguous()
+    w = weight.detach().to(x.dtype).contiguous()
+    out = torch.empty(x.size(0), w.size(1), dtype=x.dtype, device=x.device)
+    if plan.rows:
+        _lib.call("qw_grouped_matmul", _hip.ptr(x), act, _hip.ptr(w), act, None, 0, w.size(0), w.size(1), w.size(2),
+                  _hip.ptr(plan.offsets), x.size(0), _hip.ptr(out), _hip.stream(x.device))
+    return out
+
+
+def grouped_swiglu(inputs: Tensor, experts: nn.ModuleList, counts: Sequence[int], plan: Optional[GroupedPlan] = None) -> Tensor:
+    """SwiGLU over expert-sorted rows: down(silu(gate(x)) * up(x)) with each
+    expert's own weights (src/moe_kernels.py:186-195), in one pair of HIP
+    kernels (fused gate/up + SiLU·mul, then down)."""
+    _hip.require_device(inputs, "grouped_swiglu")
+    plan = plan or GroupedPlan(counts, inputs.device)
+    if plan.num_experts != len(experts):
+        raise ValueError("plan and experts disagree on the number of experts")
+    dtype = compute_dtype(inputs)
+    x = inputs.detach().to(dtype).contiguous()
+    act = _hip.act_code(x, "grouped_swiglu")
+    if x.size(0) != plan.rows:
+        raise ValueError(f"inputs have {x.size(0)} rows but the plan covers {plan.rows}")
+    pack = packed_experts(experts, experts)
+    args = pack.args()
+    if pack.fmt in (_lib.QW_F32, _lib.QW_BF16) and pack.fmt != act:
+        # the reference casts the stacked weights to the compute dtype (src/moe_kernels.py:191-193)
+        cast = getattr(pack, "_cast", None)
+        if cast is None or cast[0] != dtype:
+            cast = (dtype, pack.gate.to(dtype), pack.up.to(dtype), pack.down.to(dtype))
+            pack._cast = cast
+        args = [act, 0, 0, _hip.ptr(cast[1]), None, _hip.ptr(cast[2]), None, _hip.ptr(cast[3]), None]
+    d_ff = pack.gate.size(1)
+    d_model = x.size(1)
+    out = torch.empty(plan.rows, d_model, dtype=dtype, device=x.device)
+    if plan.rows:
+        lib = _lib.load()
+        nbytes = lib.qw_moe_experts_workspace_bytes(plan.rows, len(experts), d_model, d_ff, act)
+        ws = _hip.workspace(nbytes, x.device)
+        _lib.call("qw_moe_experts", _hip.ptr(x), act, None, _hip.ptr(plan.offsets), len(experts), d_model, d_ff,
+                  plan.rows, *args, None, _hip.ptr(out), _hip.ptr(ws), nbytes, _hip.stream(x.device))
+    return out
+
+
+def benchmark(experts: int = 32, tokens: int = 8192, hidden: int = 256, ffn: int = 512, top_k: int = 2, repeats: int = 20,
+              bf16: bool = False) -> dict:
+    """Wall-clock the HIP MoE layer forward on the current GPU (src/moe_kernels.py:198-227).
+
+    The reference times forward+backward of its loop and Triton paths; this
+    build is forward-only, so it reports the forward time of the HIP path."""
+    from .moe import QuantaWeaveConfig, TopKMoE
+
+    if not kernels_available(torch.device("cuda")):
+        raise RuntimeError("benchmark needs a ROCm device and the built HIP library")
+    config = QuantaWeaveConfig(vocab_size=8, hidden_size=hidden, layers=1, ffn_size=ffn, num_experts=experts, top_k=top_k,
+                               attention_heads=1, max_sequence_length=tokens, capacity_factor=0)
+    dtype = torch.bfloat16 if bf16 else torch.float32
+    moe = TopKMoE(config).to("cuda", dtype)
+    x = torch.randn(1, tokens, hidden, device="cuda", dtype=dtype)
+    with torch.no_grad():
+        for _ in range(3):
+            moe(x)
+        torch.cuda.synchronize()
+        started = time.perf_counter()
+        for _ in range(repeats):
+            moe(x)
+        torch.cuda.synchronize()
+    ms = (time.perf_counter() - started) / repeats * 1000
+    return dict(hip_ms=ms, experts=experts, tokens=tokens, hidden=hidden, ffn=ffn, top_k=top_k, bf16=bf16)

@@ -1,0 +1,91 @@
+"""Host-side behaviour of the Python drop-in surface (no GPU needed)."""
+
+import pytest
+import torch
+
+import quantaweave_amd as qa
+from quantaweave_amd import moe_kernels as mk
+
+
+def small_config(**overrides):
+    values = dict(vocab_size=32, hidden_size=16, layers=2, ffn_size=32, num_experts=6, top_k=2,
+                  attention_heads=2, max_sequence_length=16, capacity_factor=0, min_expert_capacity=1)
+    values.update(overrides)
+    return qa.QuantaWeaveConfig(**values)
+
+
+@pytest.mark.parametrize("bad", [dict(top_k=0), dict(top_k=7), dict(capacity_factor=-1), dict(min_expert_capacity=0),
+                                 dict(overflow_policy="x"), dict(router_temperature=0), dict(hidden_size=15)])
+def test_config_validation_mirrors_the_reference(bad):
+    with pytest.raises(ValueError):
+        small_config(**bad)
+
+
+def test_capacity_follows_the_reference_formula():
+    moe = qa.TopKMoE(small_config(capacity_factor=0.6, min_expert_capacity=2))
+    assert moe.capacity(24) == 5
+    moe.capacity_scale = 0.5
+    assert moe.capacity(24) == 3
+    moe.drop_overflow_tokens = False
+    assert moe.capacity(24) == 48
+    assert qa.TopKMoE(small_config()).capacity(10) == 20
+
+
+def test_grouped_plan_bookkeeping():
+    plan = mk.GroupedPlan([3, 0, 40], torch.device("cpu"))
+    assert plan.tiles == 1 + 2 and plan.rows == 43
+    assert plan.offsets.tolist() == [0, 3, 3, 43]
+    assert mk.GroupedPlan([0, 0], torch.device("cpu")).tiles == 0
+    with pytest.raises(ValueError):
+        mk.GroupedPlan([1, -1], torch.device("cpu"))
+
+
+def test_experts_support_grouped_accepts_plain_and_quantised_experts():
+    moe = qa.TopKMoE(small_config())
+    assert mk.experts_support_grouped(moe.experts)
+    moe.experts[0].gate = torch.nn.Linear(16, 32, bias=True)
+    assert not mk.experts_support_grouped(moe.experts)
+    q = qa.QuantizedLinear(16, 32, bits=4)
+    moe.experts[0].gate = q
+    assert mk.experts_support_grouped(moe.experts)
+
+
+def test_quantized_linear_geometry_and_errors():
+    q = qa.QuantizedLinear(40, 24, bits=4, group_size=16)
+    assert q.padded == 48 and q.qweight.shape == (24, 24) and q.qweight.dtype == torch.uint8
+    assert q.scales.shape == (24, 3)
+    q8 = qa.QuantizedLinear(40, 24, bits=8)
+    assert q8.qweight.shape == (24, 40) and q8.scales.shape == (24, 1) and q8.qweight.dtype == torch.int8
+    with pytest.raises(ValueError):
+        qa.QuantizedLinear(8, 1, bits=4, group_size=7)
+    with pytest.raises(ValueError):
+        qa.QuantizedLinear(8, 1, bits=3)
+    with pytest.raises(ValueError, match="bias"):
+        qa.QuantizedLinear.from_linear(torch.nn.Linear(8, 4, bias=True))
+
+
+def test_cpu_tensors_are_refused_not_computed():
+    moe = qa.TopKMoE(small_config())
+    with pytest.raises(RuntimeError, match="ROCm"):
+        moe(torch.randn(1, 4, 16))
+    with pytest.raises(RuntimeError):
+        mk.grouped_swiglu(torch.randn(3, 16), moe.experts, [3, 0, 0, 0, 0, 0])
+
+
+def test_kernel_selection_errors():
+    moe = qa.TopKMoE(small_config())
+    with pytest.raises(ValueError):
+        qa.set_moe_kernel(moe, "bogus")
+    with pytest.raises(RuntimeError):
+        qa.set_moe_kernel(moe, "loop")
+    assert not mk.kernels_available(torch.device("cpu"))
+    if not torch.cuda.is_available():
+        with pytest.raises(RuntimeError):
+            qa.set_moe_kernel(moe, "auto")
+
+
+def test_compute_dtype_rule():
+    x = torch.randn(2, 3)
+    assert mk.compute_dtype(x) == torch.float32
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        assert mk.compute_dtype(x) == torch.bfloat16

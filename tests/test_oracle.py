@@ -1,0 +1,355 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the checker.
+
+Each oracle function is checked against something independent of its own
+formula: float64 mathematics, torch's library routines used the way the
+reference composes them, the reference's known-answer tests, brute force.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+
+
+def ulp_diff(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    ai = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    bi = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    return np.abs(ai - bi)
+
+
+# ---------------------------------------------------------------- exp / softmax
+def test_expf_is_within_one_ulp_of_the_true_exponential():
+    rng = np.random.RandomState(0)
+    xs = np.concatenate([
+        -rng.rand(50000).astype(np.float32) * 104.0,
+        -rng.rand(20000).astype(np.float32) * 1e-3,
+        np.float32([0.0, -0.0, -1e-30, -0.34657359, -0.6931472, -87.33654, -87.34, -88.72, -100.0, -103.27, -103.97]),
+    ]).astype(np.float32)
+    ours = np.array([oracle.expf(float(v)) for v in xs], dtype=np.float32)
+    exact = np.exp(xs.astype(np.float64))
+    spacing = np.spacing(exact.astype(np.float32)).astype(np.float64)
+    err = np.abs(ours.astype(np.float64) - exact) / np.maximum(spacing, 2.0 ** -149)
+    assert err.max() <= 1.0
+    assert oracle.expf(0.0) == 1.0
+    assert oracle.expf(-200.0) == 0.0 and oracle.expf(-float("inf")) == 0.0
+    assert math.isnan(oracle.expf(float("nan")))
+
+
+def test_expf_is_monotone_on_a_dense_grid():
+    xs = np.linspace(-30.0, 0.0, 200001, dtype=np.float32)
+    ys = np.array([oracle.expf(float(v)) for v in xs], dtype=np.float32)
+    assert np.all(np.diff(ys.astype(np.float64)) >= 0)
+
+
+def test_softmax_matches_float64_and_torch_closely():
+    torch.manual_seed(0)
+    logits = (torch.randn(512, 64) * 3).numpy()
+    ours = oracle.softmax(logits)
+    # the argument logit - max is one fp32 subtraction in any fp32 softmax; from there on float64
+    shifted = (logits - logits.max(-1, keepdims=True)).astype(np.float64)
+    exact = np.exp(shifted)
+    exact /= exact.sum(-1, keepdims=True)
+    rel = np.abs(ours - exact) / exact
+    assert rel.max() < 4e-7                                    # a few ulp of the correctly rounded value
+    assert np.abs(ours.astype(np.float64).sum(-1) - 1).max() < 1e-5
+    theirs = torch.from_numpy(logits).softmax(-1).numpy()
+    assert ulp_diff(ours, theirs).max() <= 16                   # torch's exp differs by a few ulp
+
+
+def test_softmax_row_with_extreme_logits_underflows_like_float64():
+    row = np.float32([[0.0, -50.0, -87.5, -95.0, -103.5, -120.0]])
+    p = oracle.softmax(row)[0]
+    exact = np.exp(row[0].astype(np.float64))
+    exact /= exact.sum()
+    assert p[0] == 1.0 or abs(p[0] - 1.0) < 1e-7
+    assert p[-1] == 0.0
+    assert 0 < p[4] < 2 ** -126                                 # subnormal probability survives
+    assert abs(p[4] - exact[4]) <= 2 ** -149 * 1.0
+
+
+# ---------------------------------------------------------------- routing
+@pytest.mark.parametrize("E,k", [(8, 2), (64, 2), (64, 1), (100, 3), (184, 4)])
+def test_route_matches_torch_topk_and_renorm_on_the_same_probabilities(E, k):
+    torch.manual_seed(E + k)
+    logits = (torch.randn(300, E) * 2).numpy()
+    probs, idx, w = oracle.route_from_logits(logits, k)
+    pt = torch.from_numpy(probs)
+    tw, ti = pt.topk(k, dim=-1)
+    tw = tw / tw.sum(dim=-1, keepdim=True)                      # src/quantweave_moe_model.py:131, :136
+    assert np.array_equal(ti.numpy(), idx)
+    assert np.array_equal(tw.numpy().view(np.int32), w.view(np.int32))
+
+
+def test_biased_selection_uses_biased_logits_but_unbiased_weights():
+    torch.manual_seed(7)
+    logits = torch.randn(200, 16)
+    bias = torch.linspace(-1, 1, 16)
+    probs, idx, w = oracle.route_from_logits(logits.numpy(), 2, bias.numpy())
+    ti = (logits + bias).topk(2, dim=-1).indices                 # src/quantweave_moe_model.py:134-135
+    gathered = torch.from_numpy(probs).gather(1, ti)
+    assert np.array_equal(ti.numpy(), idx)
+    assert np.array_equal((gathered / gathered.sum(-1, keepdim=True)).numpy(), w)
+    # known answer (tests/test_parallelism.py:345-357): a zero bias changes nothing, -100 excludes an expert
+    _, idx0, w0 = oracle.route_from_logits(logits.numpy(), 2, np.zeros(16, np.float32))
+    _, idxn, wn = oracle.route_from_logits(logits.numpy(), 2)
+    assert np.array_equal(idx0, idxn) and np.array_equal(w0, wn)
+    b = np.zeros(16, np.float32)
+    b[0] = -100.0
+    _, idxb, _ = oracle.route_from_logits(logits.numpy(), 2, b)
+    assert (idxb == 0).sum() == 0
+
+
+def test_exact_ties_pick_the_lower_expert_index():
+    logits = np.float32([[1.0, 2.0, 2.0, 0.5, 2.0]])
+    _, idx, w = oracle.route_from_logits(logits, 3)
+    assert idx.tolist() == [[1, 2, 4]]
+    assert np.allclose(w.sum(), 1.0)
+
+
+def test_top1_weight_is_exactly_one():
+    _, _, w = oracle.route_from_logits(np.random.RandomState(3).randn(50, 8).astype(np.float32), 1)
+    assert np.all(w == 1.0)
+
+
+def test_router_logits_match_float64_matmul():
+    rng = np.random.RandomState(1)
+    x = rng.randn(33, 40).astype(np.float32)
+    w = (rng.randn(7, 40) * 0.02).astype(np.float32)
+    got = oracle.router_logits(x, w, temperature=2.0)
+    exact = (x.astype(np.float64) @ w.astype(np.float64).T) / 2.0
+    assert np.allclose(got, exact, rtol=1e-6, atol=1e-7)
+
+
+# ---------------------------------------------------------------- capacity and plan
+@pytest.mark.parametrize("args,expected", [
+    ((512, 2, 8, 1.25), 160), ((8192, 2, 64, 1.25), 320), ((64, 2, 64, 0.0), 128), ((16, 2, 64, 0.0), 32),
+    ((4096, 2, 64, 1.0), 128), ((24, 2, 6, 0.6), 5), ((4, 2, 2, 0.5), 4), ((3, 1, 8, 0.1), 4),
+])
+def test_capacity_closed_form(args, expected):
+    T, k, E, cf = args
+    assert oracle.capacity(T, k, E, cf) == expected
+    assert oracle.capacity(T, k, E, cf) == (max(4, math.ceil(T * k / E * cf)) if cf > 0 else T * k)
+
+
+def test_capacity_without_drop_or_with_scale():
+    assert oracle.capacity(100, 2, 8, 1.25, drop_overflow=False) == 200
+    assert oracle.capacity(100, 2, 8, 1.25, capacity_scale=0.5) == math.ceil(100 * 2 / 8 * 1.25 * 0.5)
+
+
+def torch_plan(top_idx: np.ndarray, top_w: np.ndarray, experts: int, capacity: int):
+    """The reference's composition of library calls (src/quantweave_moe_model.py:172-188)."""
+    k = top_idx.shape[1]
+    route_experts = torch.from_numpy(top_idx.astype(np.int64)).reshape(-1)
+    route_weights = torch.from_numpy(top_w).reshape(-1)
+    by_weight = torch.argsort(route_weights, descending=True, stable=True)
+    order = by_weight[torch.argsort(route_experts[by_weight], stable=True)]
+    counts = torch.bincount(route_experts, minlength=experts)
+    offsets = torch.cumsum(counts, dim=0) - counts
+    position = torch.arange(order.numel()) - offsets[route_experts[order]]
+    keep = position < capacity
+    kept, dropped = order[keep], order[~keep]
+    return dict(tokens=kept // k, weights=route_weights[kept], kept_counts=counts.clamp(max=capacity),
+                overflow=int((~keep).sum()), dropped_tokens=dropped // k, dropped_experts=route_experts[dropped],
+                counts=counts)
+
+
+@pytest.mark.parametrize("T,E,k,cf,seed", [(512, 8, 2, 1.25, 0), (300, 16, 2, 0.7, 1), (200, 6, 3, 0.5, 2),
+                                           (64, 64, 2, 0.0, 3), (1000, 64, 2, 1.0, 4), (50, 4, 1, 0.3, 5)])
+def test_plan_matches_the_reference_double_argsort(T, E, k, cf, seed):
+    rng = np.random.RandomState(seed)
+    logits = rng.randn(T, E).astype(np.float32) * 2
+    logits[:, 0] += 1.0                                          # make expert 0 hot so it overflows
+    _, idx, w = oracle.route_from_logits(logits, k)
+    cap = oracle.capacity(T, k, E, cf)
+    ours = oracle.plan(idx, w, E, cap)
+    ref = torch_plan(idx, w, E, cap)
+    assert np.array_equal(ours["slot_token"], ref["tokens"].numpy())
+    assert np.array_equal(ours["slot_weight"], ref["weights"].numpy())
+    assert np.array_equal(ours["kept_counts"], ref["kept_counts"].numpy())
+    assert np.array_equal(ours["counts"], ref["counts"].numpy())
+    assert int(ours["totals"][1]) == ref["overflow"]
+    assert np.array_equal(ours["dropped_token"], ref["dropped_tokens"].numpy())
+    assert np.array_equal(ours["dropped_expert"], ref["dropped_experts"].numpy())
+    assert ours["kept_offsets"][-1] == ours["totals"][0] == len(ours["slot_token"])
+    rs = ours["route_slot"]
+    for s, t in enumerate(ours["slot_token"]):
+        assert rs.reshape(T, k)[t].tolist().count(s) == 1
+
+
+def test_plan_orders_equal_weights_by_route_id():
+    idx = np.int32([[0], [0], [0], [0]])
+    w = np.float32([[0.5], [0.7], [0.5], [0.7]])
+    p = oracle.plan(idx, w, 1, 3)
+    assert p["slot_token"].tolist() == [1, 3, 0] and p["dropped_token"].tolist() == [2]
+
+
+def _two_expert_case(hidden_features, router_weight, capacity_factor=0.5, drop=True, k=2, E=2):
+    """Routing of the reference's two-expert known-answer tests (tests/test_quantweave.py:97-163)."""
+    x = np.stack([np.float32(hidden_features), np.zeros(len(hidden_features), np.float32)], axis=-1)
+    logits = oracle.router_logits(x, np.float32(router_weight))
+    _, idx, w = oracle.route_from_logits(logits, k)
+    cap = oracle.capacity(len(hidden_features), k, E, capacity_factor, min_capacity=1, drop_overflow=drop)
+    return x, oracle.plan(idx, w, E, cap)
+
+
+def test_capacity_keeps_highest_weight_routes_not_first_tokens():
+    x, p = _two_expert_case([0.5, 3.0, -2.0, 1.5], [[1.0, 0.0], [0.0, 0.0]])
+    kc = p["kept_counts"]
+    seen0 = sorted(x[p["slot_token"][:kc[0]], 0].tolist())
+    seen1 = sorted(x[p["slot_token"][kc[0]:kc[0] + kc[1]], 0].tolist())
+    assert int(p["totals"][1]) == 4
+    assert seen0 == [1.5, 3.0] and seen1 == [-2.0, 0.5]
+
+
+def test_drop_overflow_false_disables_capacity():
+    _, p = _two_expert_case([0.5, 3.0, -2.0, 1.5], [[1.0, 0.0], [0.0, 0.0]], drop=False)
+    assert int(p["totals"][1]) == 0 and p["kept_counts"].tolist() == [4, 4]
+
+
+def test_skipped_route_contributes_exactly_zero():
+    # tests/test_quantweave.py:149-163: every token routes to expert 0 with room for one
+    hidden = np.float32([[5.0, 1.0], [4.0, 1.0], [3.0, 1.0], [2.0, 1.0]])
+    rw = np.float32([[1.0, 0.0], [-1.0, 0.0]])
+    rng = np.random.RandomState(0)
+    w = dict(format="f32", d_model=2, d_ff=4, gate=rng.randn(2, 4, 2).astype(np.float32),
+             up=rng.randn(2, 4, 2).astype(np.float32), down=rng.randn(2, 2, 4).astype(np.float32))
+    cap = oracle.capacity(4, 1, 2, 0.5, min_capacity=1)
+    res = oracle.moe_forward(hidden, rw, w, top_k=1, cap=cap, dtype="f32")
+    assert int(res["plan"]["totals"][1]) == 3
+    assert int((np.abs(res["out"]).sum(-1) > 0).sum()) == 1
+
+
+# ---------------------------------------------------------------- quantisation
+def torch_from_linear(weight: torch.Tensor, bits: int, group_size=None):
+    """The reference's quantisation ops (src/quantization.py:32-58) in torch."""
+    out_f, in_f = weight.shape
+    group = group_size or (in_f if bits == 8 else 32)
+    padded = -(-in_f // group) * group
+    wp = F.pad(weight.float(), (0, padded - in_f))
+    grouped = wp.reshape(out_f, -1, group)
+    limit = 127 if bits == 8 else 7
+    scales = (grouped.abs().amax(dim=-1) / limit).clamp(min=1e-8)
+    q = torch.round(grouped / scales[..., None]).clamp(-limit - (bits == 4), limit).reshape(out_f, -1)
+    if bits == 8:
+        return q.to(torch.int8), scales
+    u = (q + 8).to(torch.uint8)
+    return u[:, 0::2] | (u[:, 1::2] << 4), scales
+
+
+@pytest.mark.parametrize("bits,group,shape", [(8, None, (24, 40)), (4, 16, (24, 40)), (4, None, (16, 64)),
+                                              (8, 32, (8, 100)), (4, 8, (5, 7))])
+def test_quantize_bytes_match_the_reference_ops(bits, group, shape):
+    torch.manual_seed(bits + shape[1])
+    weight = torch.randn(*shape) * 0.02
+    q, s, g = oracle.quantize(weight.numpy(), bits, group)
+    tq, ts = torch_from_linear(weight, bits, group)
+    assert q.dtype == (np.int8 if bits == 8 else np.uint8)
+    assert np.array_equal(q, tq.numpy()) and np.array_equal(s, ts.numpy())
+
+
+def test_int4_packing_is_lossless_for_representable_weights():
+    # tests/test_deploy_and_distill.py:173-184
+    weight = np.float32([[-7, -1, 0, 1, 7, 3, -4, 2]]) * 0.5
+    q, s, g = oracle.quantize(weight, 4, 8)
+    assert s.item() == 0.5
+    assert q.tolist() == [[(-7 + 8) | ((-1 + 8) << 4), (0 + 8) | ((1 + 8) << 4), (7 + 8) | ((3 + 8) << 4),
+                           (-4 + 8) | ((2 + 8) << 4)]]
+    assert np.array_equal(oracle.dequantize(q, s, 4, 8, g), weight)
+
+
+@pytest.mark.parametrize("bits,group,max_rel", [(8, None, 0.02), (4, 16, 0.2)])
+def test_quantized_linear_approximates_the_original(bits, group, max_rel):
+    # tests/test_deploy_and_distill.py:161-171 (40 columns exercise the padding)
+    torch.manual_seed(0)
+    weight = torch.nn.Linear(40, 24, bias=False).weight.detach()
+    q, s, g = oracle.quantize(weight.numpy(), bits, group)
+    deq = oracle.dequantize(q, s, bits, 40, g)
+    assert deq.shape == (24, 40)
+    x = torch.randn(5, 40)
+    err = (x @ torch.from_numpy(deq).T - x @ weight.T).norm() / (x @ weight.T).norm()
+    assert err < max_rel
+
+
+def test_rounding_is_half_to_even():
+    # 127 * s is the amax; values at exactly half steps round to even
+    weight = np.float32([[127.0, 2.5, 3.5, -2.5, 0.5]])
+    q, s, _ = oracle.quantize(weight, 8)
+    assert s.item() == 1.0 and q.tolist() == [[127, 2, 4, -2, 0]]
+
+
+# ---------------------------------------------------------------- expert FFN
+def test_swiglu_matches_torch_fp32():
+    torch.manual_seed(5)
+    x = torch.randn(9, 24)
+    g, u, d = torch.randn(32, 24) * 0.1, torch.randn(32, 24) * 0.1, torch.randn(24, 32) * 0.1
+    ref = F.linear(F.silu(F.linear(x, g)) * F.linear(x, u), d)
+    got = oracle.swiglu(x.numpy(), g.numpy(), u.numpy(), d.numpy(), "f32")
+    assert np.allclose(got, ref.numpy(), atol=1e-6, rtol=1e-5)
+
+
+def test_swiglu_bf16_matches_torch_bf16_module():
+    torch.manual_seed(6)
+    x = torch.randn(9, 64).bfloat16()
+    g, u, d = (torch.randn(48, 64) * 0.1).bfloat16(), (torch.randn(48, 64) * 0.1).bfloat16(), (torch.randn(64, 48) * 0.1).bfloat16()
+    ref = F.linear(F.silu(F.linear(x, g)) * F.linear(x, u), d).float()
+    got = oracle.swiglu(x.float().numpy(), g.float().numpy(), u.float().numpy(), d.float().numpy(), "bf16")
+    assert np.abs(got - ref.numpy()).max() <= 2e-2 * np.abs(ref.numpy()).max()
+
+
+def test_round_bf16_matches_torch():
+    v = np.random.RandomState(2).randn(10000).astype(np.float32) * 100
+    assert np.array_equal(oracle.round_bf16(v), torch.from_numpy(v).bfloat16().float().numpy())
+
+
+def reference_moe(x, router_w, w, top_k, capacity):
+    """Straightforward per-expert loop (tests/test_model_features.py:21-35), fp32 torch."""
+    flat = torch.from_numpy(x)
+    probs = torch.from_numpy(oracle.softmax(oracle.router_logits(x, router_w)))
+    weights, indices = probs.topk(top_k, dim=-1)
+    weights = weights / weights.sum(-1, keepdim=True)
+    output = torch.zeros_like(flat)
+    for e in range(router_w.shape[0]):
+        token, rank = (indices == e).nonzero(as_tuple=True)
+        if token.numel() == 0:
+            continue
+        ww = weights[token, rank]
+        keep = ww.argsort(descending=True, stable=True)[:capacity]
+        g, u, d = (torch.from_numpy(w[n][e]) for n in ("gate", "up", "down"))
+        xe = flat[token[keep]]
+        output[token[keep]] += F.linear(F.silu(F.linear(xe, g)) * F.linear(xe, u), d) * ww[keep, None]
+    return output.numpy()
+
+
+@pytest.mark.parametrize("cf", [0.0, 0.6])
+def test_moe_forward_matches_the_per_expert_loop(cf):
+    rng = np.random.RandomState(11)
+    T, D, F_, E, k = 24, 16, 32, 6, 2
+    x = rng.randn(T, D).astype(np.float32)
+    rw = (rng.randn(E, D) * 0.3).astype(np.float32)
+    w = dict(format="f32", d_model=D, d_ff=F_, gate=(rng.randn(E, F_, D) * 0.2).astype(np.float32),
+             up=(rng.randn(E, F_, D) * 0.2).astype(np.float32), down=(rng.randn(E, D, F_) * 0.2).astype(np.float32))
+    cap = oracle.capacity(T, k, E, cf, min_capacity=2)
+    res = oracle.moe_forward(x, rw, w, top_k=k, cap=cap, dtype="f32")
+    ref = reference_moe(x, rw, w, k, cap)
+    assert np.allclose(res["out"], ref, atol=1e-6)
+    if cf:
+        assert int(res["plan"]["totals"][1]) > 0
+
+
+def test_quantized_expert_weights_follow_dequantize_then_cast():
+    rng = np.random.RandomState(4)
+    E, D, F_ = 2, 64, 32
+    gate = (rng.randn(E, F_, D) * 0.02).astype(np.float32)
+    qs = [oracle.quantize(gate[e], 4) for e in range(E)]
+    w = dict(format="u4", d_model=D, d_ff=F_, group_in=32, group_ff=32,
+             gate=np.stack([q for q, _, _ in qs]), gate_scales=np.stack([s for _, s, _ in qs]),
+             up=np.stack([q for q, _, _ in qs]), up_scales=np.stack([s for _, s, _ in qs]),
+             down=np.stack([oracle.quantize(gate[e].T.copy(), 4)[0] for e in range(E)]),
+             down_scales=np.stack([oracle.quantize(gate[e].T.copy(), 4)[1] for e in range(E)]))
+    g, u, d = oracle.expert_weights(w, 1, "bf16")
+    assert np.array_equal(g, oracle.round_bf16(oracle.dequantize(qs[1][0], qs[1][1], 4, D, 32)))
+    assert np.abs(g - gate[1]).max() <= np.abs(gate[1]).max() / 7 * 0.5 + 1e-3
