@@ -1,0 +1,251 @@
+"""Benchmark of the MoE expert-FFN layer forward on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
+
+A step is one whole MoE layer forward (router -> top-k -> capacity plan ->
+grouped SwiGLU experts -> weighted combine) over one batch of synthetic input
+already resident in HBM.  Prints ONE JSON line: throughput of the headline
+workload (bf16 prefill, T=8192, d=2048, 64 experts, d_ff=1024, top-2,
+capacity factor 1.25) with a roofline entry for the expert-FFN stage, the
+CPU baseline (the oracle on the host cores, bounded sample), and per-workload
+numbers for the other workloads.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default=None)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only-headline", action="store_true")
+    return ap.parse_args()
+
+
+def event_time(fn, iters, stream):
+    """Average ms per call of fn() measured with HIP events on `stream`."""
+    import torch
+
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def stage_calls(run):
+    """The forward split into its entry points, with the same buffers as qw_moe_forward."""
+    import torch
+    from quantaweave_amd import _hip, _lib
+
+    lay, w = run.layer, run.layer.w
+    lib = _lib.load()
+    T, E, K, D, F = w.tokens, w.experts, w.top_k, w.d_model, w.d_ff
+    R = T * K
+    P = _hip.ptr
+    logits = run.workspace_view("logits")
+    slot_token = run.workspace_view("slot_token")
+    slot_weight = run.workspace_view("slot_weight")
+    route_slot = run.workspace_view("route_slot")
+    kept_offsets = run.workspace_view("kept_offsets")
+    y = run.workspace_view("y")
+    plan_bytes = lib.qw_moe_plan_workspace_bytes(T, K, E)
+    plan_ws = _hip.workspace(plan_bytes, lay.x.device)
+    max_rows = min(R, run.capacity * E)
+    exp_bytes = lib.qw_moe_experts_workspace_bytes(max_rows, E, D, F, run.act)
+    exp_ws = _hip.workspace(exp_bytes, lay.x.device)
+    s = run.stream
+
+    def route():
+        _lib.check(lib.qw_moe_route(P(lay.x), run.act, D, P(lay.router), run.act, T, D, E, K, 1.0, P(lay.bias),
+                                    P(logits), P(run.probs), P(run.top_idx), P(run.top_w), s), "route")
+
+    def plan():
+        _lib.check(lib.qw_moe_plan(P(run.top_idx), P(run.top_w), T, K, E, run.capacity, P(run.counts),
+                                   P(run.kept_counts), P(kept_offsets), P(slot_token), P(slot_weight), P(route_slot),
+                                   P(run.dropped_token), P(run.dropped_expert), P(run.totals), P(plan_ws),
+                                   plan_bytes, s), "plan")
+
+    def experts():
+        _lib.check(lib.qw_moe_experts(P(lay.x), run.act, P(slot_token), P(kept_offsets), E, D, F, max_rows,
+                                      *lay.weight_args(), P(slot_weight), P(y), P(exp_ws), exp_bytes, s), "experts")
+
+    def combine():
+        _lib.check(lib.qw_moe_combine(P(y), run.act, P(route_slot), P(run.top_idx), T, K, D, P(run.out), s),
+                   "combine")
+
+    return dict(route=route, plan=plan, experts=experts, combine=combine)
+
+
+def measure(name, steps, warmup):
+    import torch
+    from quantaweave_amd import workloads as W
+
+    w = W.WORKLOADS[name]
+    layer = W.build_layer(w)
+    run = W.LayerRunner(layer)
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        run()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1000 / steps
+    ev_ms = event_time(run, steps, stream)
+    torch.cuda.synchronize()
+    # routing outcome of this workload (fixed seed): touched experts and kept rows
+    counts = run.kept_counts.cpu().numpy()
+    kept = int(run.totals[0].item())
+    dropped = int(run.totals[1].item())
+    touched = int((counts > 0).sum())
+    stages = {}
+    calls = stage_calls(run)
+    for k_, fn in calls.items():
+        fn()
+    torch.cuda.synchronize()
+    for k_, fn in calls.items():
+        stages[k_] = event_time(fn, max(5, steps // 2), stream)
+    flops = 6.0 * kept * w.d_model * w.d_ff
+    act_bytes = 4 if w.act == "f32" else 2
+    weight_bytes = touched * layer.expert_bytes()
+    # algorithmic bytes of the expert stage: touched experts' weights once, each kept row read once
+    # (gathered x) and written once (y), plus the d_ff-wide hidden row written and read back
+    stage_bytes = weight_bytes + kept * (2 * w.d_model + 2 * w.d_ff) * act_bytes
+    layer_bytes = weight_bytes + 2 * w.tokens * w.d_model * act_bytes + w.experts * w.d_model * act_bytes
+    return dict(
+        workload=w, wall_ms=wall_ms, event_ms=ev_ms, kept=kept, dropped=dropped, touched=touched, stages=stages,
+        flops=flops, stage_bytes=stage_bytes, layer_bytes=layer_bytes, weight_bytes=weight_bytes,
+        tokens_per_s=w.tokens / (wall_ms / 1000.0),
+    )
+
+
+def cpu_baseline(name, budget_s=20.0):
+    """The oracle's whole-layer forward on the host cores over a bounded token sample."""
+    import torch
+    import oracle
+    from quantaweave_amd import workloads as W
+
+    w = W.WORKLOADS[name]
+    layer = W.build_layer(w)
+    sample = 512 if w.tokens >= 512 else w.tokens
+    x = layer.x[:sample].float().cpu().numpy()
+    rw = layer.router.float().cpu().numpy()
+    wts = dict(format=w.weights, d_model=w.d_model, d_ff=w.d_ff, group_in=layer.group_in, group_ff=layer.group_ff)
+    for n in ("gate", "up", "down"):
+        t = getattr(layer, n)
+        wts[n] = t.float().cpu().numpy() if w.weights in ("f32", "bf16") else t.cpu().numpy()
+        sc = getattr(layer, n + "_s")
+        if sc is not None:
+            wts[n + "_scales"] = sc.cpu().numpy()
+    bias = None if layer.bias is None else layer.bias.cpu().numpy()
+    cap = W.Workload(w.name, sample, w.d_model, w.experts, w.d_ff, w.top_k, w.capacity_factor, w.act, w.weights,
+                     w.seed).capacity()
+    del layer
+    torch.cuda.empty_cache()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while True:
+        t0 = time.perf_counter()
+        oracle.moe_forward(x, rw, wts, top_k=w.top_k, cap=cap, dtype=w.act, expert_bias=bias, accum="f32")
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 5 or time.perf_counter() > t_end:
+            break
+    med = float(np.median(times))
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return dict(value=sample / med, unit="tokens/s", cores=threads, kind="port",
+                sample=f"{sample} of {w.tokens} tokens of {w.name}, all {w.experts} experts, capacity {cap}, "
+                       f"oracle (numpy fp32 BLAS + C routing), median of {len(times)} runs")
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU path is not part of this build",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from quantaweave_amd import workloads as W
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm device", file=sys.stderr)
+        sys.exit(1)
+    head = args.workload or W.HEADLINE
+    results = {head: measure(head, args.steps, args.warmup)}
+    if not args.only_headline:
+        for name in W.WORKLOADS:
+            if name not in results:
+                results[name] = measure(name, args.steps, args.warmup)
+    h = results[head]
+    w = h["workload"]
+    t_exp = h["stages"]["experts"]
+    mfma = w.act == "bf16" and w.tokens * w.top_k // w.experts >= 64
+    if mfma:
+        achieved = h["flops"] / (t_exp / 1000) / 1e12
+        roof = dict(bound="mfma", achieved=round(achieved, 2), peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
+                    frac=round(achieved / BF16_PEAK_TFLOPS, 4), traffic=None)
+    else:
+        achieved = h["stage_bytes"] / (t_exp / 1000) / 1e9
+        roof = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None)
+    roof["kernel"] = "qw_moe_experts (grouped SwiGLU: gate/up+SiLU*mul, down+weight)"
+    roof["algorithmic"] = dict(flops=h["flops"], bytes=h["stage_bytes"], launch_ms=round(t_exp, 4))
+    per = {}
+    for name, r in results.items():
+        ww = r["workload"]
+        te = r["stages"]["experts"]
+        per[name] = dict(
+            tokens_per_s=round(r["tokens_per_s"], 1), ms_per_step=round(r["wall_ms"], 4),
+            event_ms=round(r["event_ms"], 4), stages_ms={k: round(v, 4) for k, v in r["stages"].items()},
+            kept_routes=r["kept"], dropped_routes=r["dropped"], experts_touched=r["touched"],
+            expert_stage_tflops=round(r["flops"] / (te / 1000) / 1e12, 2),
+            expert_stage_gbs=round(r["stage_bytes"] / (te / 1000) / 1e9, 1),
+            hbm_frac=round(r["stage_bytes"] / (te / 1000) / 1e9 / HBM_PEAK_GBS, 4),
+            mfma_frac=round(r["flops"] / (te / 1000) / 1e12 / BF16_PEAK_TFLOPS, 4) if ww.act == "bf16" else None,
+        )
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(head)
+    line = {
+        "metric": "MoE FFN tokens/s + % roofline (HBM GB/s decode, MFMA util prefill)",
+        "value": round(h["tokens_per_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(h["wall_ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if w.act == "bf16" else "f32",
+        "data": "synthetic (N(0,1) activations, N(0,0.02) weights, fixed seed)",
+        "config": {"workload": head, "tokens": w.tokens, "d_model": w.d_model, "experts": w.experts, "d_ff": w.d_ff,
+                   "top_k": w.top_k, "capacity_factor": w.capacity_factor, "weights": w.weights, "seed": w.seed},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "workloads": per,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -202,21 +202,26 @@ def _silu(g: np.ndarray) -> np.ndarray:
     return (g64 / (1.0 + np.exp(-g64))).astype(np.float32)
 
 
-def linear(x: np.ndarray, w: np.ndarray, dtype: str) -> np.ndarray:
-    """F.linear(x, w) in `dtype`: float64 products/accumulation, one rounding
-    to float32 and then to the activation dtype."""
-    out = (x.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32)
+def linear(x: np.ndarray, w: np.ndarray, dtype: str, accum: str = "f64") -> np.ndarray:
+    """F.linear(x, w) in `dtype`: products/accumulation in float64 (or float32
+    with accum="f32", the speed mode of the CPU baseline), one rounding to
+    float32 and then to the activation dtype."""
+    if accum == "f32":
+        out = np.asarray(x, np.float32) @ np.asarray(w, np.float32).T
+    else:
+        out = (x.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32)
     return round_act(out, dtype)
 
 
-def swiglu(x: np.ndarray, gate: np.ndarray, up: np.ndarray, down: np.ndarray, dtype: str) -> np.ndarray:
+def swiglu(x: np.ndarray, gate: np.ndarray, up: np.ndarray, down: np.ndarray, dtype: str,
+           accum: str = "f64") -> np.ndarray:
     """SparseSwiGLU.forward, src/quantweave_moe_model.py:59-60, with the
     reference's rounding points: gate/up outputs, silu, the product and the
     down output are each rounded to `dtype`."""
-    g = linear(x, gate, dtype)
-    u = linear(x, up, dtype)
+    g = linear(x, gate, dtype, accum)
+    u = linear(x, up, dtype, accum)
     h = round_act(round_act(_silu(g), dtype) * u, dtype)
-    return linear(h, down, dtype)
+    return linear(h, down, dtype, accum)
 
 
 def expert_weights(w: dict, e: int, dtype: str) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
@@ -233,7 +238,7 @@ def expert_weights(w: dict, e: int, dtype: str) -> tuple[np.ndarray, np.ndarray,
     return round_act(g, dtype), round_act(u, dtype), round_act(dn, dtype)
 
 
-def experts_forward(x_rows: np.ndarray, kept_counts: np.ndarray, w: dict, dtype: str) -> np.ndarray:
+def experts_forward(x_rows: np.ndarray, kept_counts: np.ndarray, w: dict, dtype: str, accum: str = "f64") -> np.ndarray:
     """The per-expert loop, src/quantweave_moe_model.py:203-209: expert e runs on
     its contiguous block of plan-ordered rows."""
     out = np.zeros((x_rows.shape[0], w["d_model"]), dtype=np.float32)
@@ -241,7 +246,7 @@ def experts_forward(x_rows: np.ndarray, kept_counts: np.ndarray, w: dict, dtype:
     for e, c in enumerate(kept_counts.tolist()):
         if c:
             g, u, dn = expert_weights(w, e, dtype)
-            out[start:start + c] = swiglu(x_rows[start:start + c], g, u, dn, dtype)
+            out[start:start + c] = swiglu(x_rows[start:start + c], g, u, dn, dtype, accum)
         start += c
     return out
 
@@ -257,7 +262,8 @@ def combine(y_rows: np.ndarray, slot_token: np.ndarray, slot_weight: np.ndarray,
 
 
 def moe_forward(x: np.ndarray, router_w: np.ndarray, w: dict, *, top_k: int, cap: int, dtype: str,
-                temperature: float = 1.0, expert_bias: np.ndarray | None = None, logits: np.ndarray | None = None):
+                temperature: float = 1.0, expert_bias: np.ndarray | None = None, logits: np.ndarray | None = None,
+                accum: str = "f64"):
     """TopKMoE.forward, src/quantweave_moe_model.py:113-164 (dynamic dispatch).
 
     x [T, d] holds activation values (already rounded to `dtype`).  Returns a
@@ -271,7 +277,7 @@ def moe_forward(x: np.ndarray, router_w: np.ndarray, w: dict, *, top_k: int, cap
     probs, idx, tw = route_from_logits(logits, top_k, expert_bias)
     p = plan(idx, tw, E, cap)
     rows = x[p["slot_token"]]
-    y = experts_forward(rows, p["kept_counts"], w, dtype)
+    y = experts_forward(rows, p["kept_counts"], w, dtype, accum)
     out = combine(y, p["slot_token"], p["slot_weight"], T, dtype)
     importance = probs.astype(np.float64).mean(axis=0)
     assignments = np.bincount(idx.reshape(-1), minlength=E) / float(T * top_k)

@@ -44,7 +44,7 @@ int quantize(const void* w, int wdt, int64_t rows, int64_t cols, int bits, int64
 int dequantize(const void* qweight, const float* scales, int bits, int64_t rows, int64_t cols, int64_t group,
                float* out, hipStream_t stream);
 int grouped_matmul_generic(const void* x, int act, const WView& w, int wfmt, int64_t E, const int32_t* offsets,
-                           void* out, hipStream_t stream);
+                           int64_t rows, void* out, hipStream_t stream);
 
 // Kernel-path override for testing the general kernel on any shape:
 // QW_FFN_PATH=generic.  Read once per process.
@@ -308,7 +308,7 @@ int qw_grouped_matmul(const void* x, int act_dtype, const void* w, int w_format,
   if (rows == 0) return QW_OK;
   QW_REQUIRE(x && w && offsets && out, "grouped_matmul pointers are required");
   const WView v = make_wview(w_format, w, scales, out_features, in_features, group);
-  return grouped_matmul_generic(x, act_dtype, v, w_format, experts, offsets, out, as_stream(stream));
+  return grouped_matmul_generic(x, act_dtype, v, w_format, experts, offsets, rows, out, as_stream(stream));
 }
 
 }  // extern "C"

@@ -28,13 +28,15 @@ template <int ACT, int WF, bool GATEUP>
 __global__ __launch_bounds__(256) void ffn_generic_kernel(const void* __restrict__ x,
                                                           const int32_t* __restrict__ row_index,
                                                           const int32_t* __restrict__ offsets, WView wa, WView wb,
-                                                          int K, int N_out, const float* __restrict__ row_weight,
+                                                          int K, int N_out, int max_rows,
+                                                          const float* __restrict__ row_weight,
                                                           void* __restrict__ out) {
   __shared__ float ws[GB_N][GB_K + 1];
   __shared__ float xs[GB_M][GB_K + 1];
   __shared__ float os[GB_M][GB_N + 1];
   const int e = blockIdx.y;
-  const int r0 = offsets[e], r1 = offsets[e + 1];
+  // rows of expert e, clamped to the caller's buffers
+  const int r0 = max(offsets[e], 0), r1 = min(offsets[e + 1], max_rows);
   if (r1 <= r0) return;
   const int tid = threadIdx.x;
   // GATEUP: tile covers 32 output columns: weight rows 0..31 gate, 32..63 up.
@@ -112,12 +114,12 @@ int launch_generic_t(const FfnArgs& a, hipStream_t stream) {
   const dim3 g1(static_cast<unsigned>(ceil_div(a.d_ff, GB_N / 2)), static_cast<unsigned>(a.experts));
   ffn_generic_kernel<ACT, WF, true><<<g1, blk, 0, stream>>>(a.x, a.row_index, a.offsets, a.gate, a.up,
                                                             static_cast<int>(a.d_model), static_cast<int>(a.d_ff),
-                                                            nullptr, a.hidden);
+                                                            static_cast<int>(a.max_rows), nullptr, a.hidden);
   QW_LAUNCH_CHECK("ffn_generic_kernel<gateup>");
   const dim3 g2(static_cast<unsigned>(ceil_div(a.d_model, GB_N)), static_cast<unsigned>(a.experts));
   ffn_generic_kernel<ACT, WF, false><<<g2, blk, 0, stream>>>(a.hidden, nullptr, a.offsets, a.down, a.down,
                                                              static_cast<int>(a.d_ff), static_cast<int>(a.d_model),
-                                                             a.row_weight, a.y);
+                                                             static_cast<int>(a.max_rows), a.row_weight, a.y);
   QW_LAUNCH_CHECK("ffn_generic_kernel<down>");
   return QW_OK;
 }
@@ -140,12 +142,12 @@ int launch_ffn_generic(const FfnArgs& a, hipStream_t stream) {
 }
 
 int grouped_matmul_generic(const void* x, int act, const WView& w, int wfmt, int64_t E, const int32_t* offsets,
-                           void* out, hipStream_t stream) {
+                           int64_t rows, void* out, hipStream_t stream) {
   const dim3 g(static_cast<unsigned>(ceil_div(w.rows, GB_N)), static_cast<unsigned>(E));
-  const int K = static_cast<int>(w.cols), N = static_cast<int>(w.rows);
+  const int K = static_cast<int>(w.cols), N = static_cast<int>(w.rows), nrows = static_cast<int>(rows);
 #define QW_GM(ACT, WF)                                                                                         \
   if (act == ACT && wfmt == WF) {                                                                              \
-    ffn_generic_kernel<ACT, WF, false><<<g, 256, 0, stream>>>(x, nullptr, offsets, w, w, K, N, nullptr, out); \
+    ffn_generic_kernel<ACT, WF, false><<<g, 256, 0, stream>>>(x, nullptr, offsets, w, w, K, N, nrows, nullptr, out); \
     QW_LAUNCH_CHECK("ffn_generic_kernel<matmul>");                                                            \
     return QW_OK;                                                                                              \
   }

@@ -1,0 +1,203 @@
+"""Grouped SwiGLU experts, grouped matmul and quantised linear on the GPU vs the oracle.
+
+Tolerances (normwise, max|got-ref| / max|ref|): 1e-4 for fp32, 2e-2 for
+bf16 / int8 / int4 weights with fp32 accumulation.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import quantaweave_amd as qa
+from quantaweave_amd import _lib
+from quantaweave_amd import moe_kernels as mk
+from tests import hipcall as H
+
+pytestmark = pytest.mark.gpu
+
+COUNTS = [0, 5, 37, 1, 0, 64, 33, 2]          # empty experts, partial tiles, exact multiples (tests/test_moe_kernels.py:24)
+TOL = {"f32": 1e-4, "bf16": 2e-2}
+
+
+def normwise(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30)
+
+
+def make_weights(E, D, F_, fmt, seed, group=None, scale=0.05):
+    rng = np.random.RandomState(seed)
+    g32 = (rng.randn(E, F_, D) * scale).astype(np.float32)
+    u32 = (rng.randn(E, F_, D) * scale).astype(np.float32)
+    d32 = (rng.randn(E, D, F_) * scale).astype(np.float32)
+    w = dict(format=fmt, d_model=D, d_ff=F_)
+    if fmt in ("f32", "bf16"):
+        cast = oracle.round_bf16 if fmt == "bf16" else (lambda a: a)
+        w.update(gate=cast(g32), up=cast(u32), down=cast(d32))
+        return w
+    bits = 8 if fmt == "i8" else 4
+    for name, arr in (("gate", g32), ("up", u32), ("down", d32)):
+        qs = [oracle.quantize(arr[e], bits, group) for e in range(E)]
+        w[name] = np.stack([q for q, _, _ in qs])
+        w[name + "_scales"] = np.stack([s for _, s, _ in qs])
+        w["group_in" if name != "down" else "group_ff"] = qs[0][2]
+    return w
+
+
+def device_weights(w):
+    fmt = w["format"]
+    code = {"f32": _lib.QW_F32, "bf16": _lib.QW_BF16, "i8": _lib.QW_I8, "u4": _lib.QW_U4}[fmt]
+    out = dict(fmt=code)
+    for name in ("gate", "up", "down"):
+        a = w[name]
+        if fmt == "bf16":
+            out[name] = H.dev(a, torch.bfloat16)
+        else:
+            out[name] = H.dev(a)
+        if fmt in ("i8", "u4"):
+            out[name + "_s"] = H.dev(w[name + "_scales"])
+    if fmt in ("i8", "u4"):
+        out["group_in"], out["group_ff"] = w["group_in"], w["group_ff"]
+    return out
+
+
+def run_experts(x_np, counts, w, act, row_weight=None, row_index=None, x_rows=None):
+    dw = device_weights(w)
+    tdt = torch.float32 if act == "f32" else torch.bfloat16
+    x = H.dev(x_np, tdt)
+    offsets = H.dev(np.concatenate([[0], np.cumsum(counts)]).astype(np.int32))
+    y = H.experts(x, offsets, dw["fmt"], dw["gate"], dw["up"], dw["down"], dw.get("gate_s"), dw.get("up_s"),
+                  dw.get("down_s"), dw.get("group_in", 0), dw.get("group_ff", 0),
+                  row_index=None if row_index is None else H.dev(row_index.astype(np.int32)),
+                  row_weight=None if row_weight is None else H.dev(row_weight.astype(np.float32)),
+                  max_rows=int(sum(counts)))
+    return y.float().cpu().numpy()
+
+
+CASES = [
+    ("f32", "f32", 48, 80, None), ("f32", "f32", 33, 17, None), ("bf16", "bf16", 64, 96, None),
+    ("bf16", "bf16", 256, 512, None), ("bf16", "i8", 64, 96, None), ("bf16", "i8", 40, 24, 16),
+    ("bf16", "u4", 64, 96, None), ("bf16", "u4", 40, 24, 16), ("f32", "i8", 64, 64, None), ("f32", "u4", 64, 64, 32),
+]
+
+
+@pytest.mark.parametrize("path", ["auto", "generic"])
+@pytest.mark.parametrize("act,fmt,D,F_,group", CASES)
+def test_grouped_swiglu_matches_oracle(act, fmt, D, F_, group, path, monkeypatch):
+    print(f"case act={act} fmt={fmt} D={D} F={F_} group={group} path={path}", flush=True)
+    if path == "generic" and os.environ.get("QW_FFN_PATH") != "generic":
+        pytest.skip("the general kernel is exercised in a process started with QW_FFN_PATH=generic")
+    rng = np.random.RandomState(D + F_)
+    rows = sum(COUNTS)
+    x = rng.randn(rows, D).astype(np.float32)
+    if act == "bf16":
+        x = oracle.round_bf16(x)
+    w = make_weights(len(COUNTS), D, F_, fmt, D * F_, group)
+    rw = rng.rand(rows).astype(np.float32)
+    got = run_experts(x, COUNTS, w, act, row_weight=rw)
+    ref = oracle.round_act(oracle.experts_forward(x, np.array(COUNTS), w, act) * rw[:, None], act)
+    assert np.isfinite(got).all()
+    assert normwise(got, ref) <= TOL[act]
+
+
+def test_gathered_rows_through_row_index():
+    rng = np.random.RandomState(0)
+    D, F_ = 64, 128
+    x_all = oracle.round_bf16(rng.randn(50, D).astype(np.float32))
+    counts = [3, 0, 20, 9]
+    row_index = rng.randint(0, 50, size=sum(counts)).astype(np.int32)
+    w = make_weights(4, D, F_, "bf16", 1)
+    got = run_experts(x_all, counts, w, "bf16", row_index=row_index)
+    ref = oracle.experts_forward(x_all[row_index], np.array(counts), w, "bf16")
+    assert normwise(got, ref) <= 2e-2
+
+
+@pytest.mark.parametrize("in_features,out_features", [(48, 80), (64, 64), (33, 17)])
+def test_grouped_matmul_matches_per_expert_matmuls(in_features, out_features):
+    # tests/test_moe_kernels.py:27-36 (forward)
+    torch.manual_seed(0)
+    x = torch.randn(sum(COUNTS), in_features, device="cuda")
+    weight = torch.randn(len(COUNTS), out_features, in_features, device="cuda")
+    plan = mk.GroupedPlan(COUNTS, x.device)
+    y = mk.grouped_matmul(x, weight, plan)
+    parts, start = [], 0
+    for e, c in enumerate(COUNTS):
+        parts.append(x[start:start + c].double() @ weight[e].double().t())
+        start += c
+    expected = torch.cat(parts).float()
+    assert torch.allclose(y, expected, atol=1e-4, rtol=1e-4)
+
+
+def test_grouped_matmul_bf16_is_close_and_all_empty_plan_is_safe():
+    # tests/test_moe_kernels.py:50-59
+    torch.manual_seed(1)
+    x = torch.randn(sum(COUNTS), 64, device="cuda", dtype=torch.bfloat16)
+    weight = torch.randn(len(COUNTS), 96, 64, device="cuda", dtype=torch.bfloat16)
+    y = mk.grouped_matmul(x, weight, mk.GroupedPlan(COUNTS, x.device))
+    parts, start = [], 0
+    for e, c in enumerate(COUNTS):
+        parts.append(x[start:start + c].double() @ weight[e].double().t())
+        start += c
+    expected = torch.cat(parts)
+    assert (y.double() - expected).abs().max() < 0.25 and y.dtype == torch.bfloat16
+    empty = mk.grouped_matmul(torch.empty(0, 64, device="cuda"), weight.float(), mk.GroupedPlan([0] * len(COUNTS), x.device))
+    assert empty.shape == (0, 96)
+
+
+def test_grouped_swiglu_api_matches_oracle_over_real_experts():
+    # tests/test_moe_kernels.py:62-84 (forward)
+    torch.manual_seed(2)
+    config = qa.QuantaWeaveConfig(vocab_size=8, hidden_size=48, layers=1, ffn_size=72, num_experts=len(COUNTS), top_k=1,
+                                  attention_heads=1, max_sequence_length=8)
+    moe = qa.TopKMoE(config).cuda()
+    x = torch.randn(sum(COUNTS), 48, device="cuda")
+    out = mk.grouped_swiglu(x, moe.experts, COUNTS)
+    w = dict(format="f32", d_model=48, d_ff=72,
+             gate=np.stack([e.gate.weight.detach().cpu().numpy() for e in moe.experts]),
+             up=np.stack([e.up.weight.detach().cpu().numpy() for e in moe.experts]),
+             down=np.stack([e.down.weight.detach().cpu().numpy() for e in moe.experts]))
+    ref = oracle.experts_forward(x.cpu().numpy(), np.array(COUNTS), w, "f32")
+    assert np.allclose(out.cpu().numpy(), ref, atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("bits,group,shape", [(8, None, (24, 40)), (4, 16, (24, 40)), (4, None, (1408, 4096)),
+                                              (8, None, (1024, 2048)), (4, 8, (5, 8))])
+def test_quantized_linear_bytes_match_oracle(bits, group, shape):
+    torch.manual_seed(bits)
+    lin = torch.nn.Linear(shape[1], shape[0], bias=False)
+    lin.weight.data.mul_(0.5)
+    q = qa.QuantizedLinear.from_linear(lin.cuda(), bits, group)
+    oq, os_, og = oracle.quantize(lin.weight.detach().cpu().numpy(), bits, group)
+    assert np.array_equal(q.qweight.cpu().numpy(), oq)
+    assert np.array_equal(q.scales.cpu().numpy(), os_)
+    deq = q.dequantize().cpu().numpy()
+    assert np.array_equal(deq, oracle.dequantize(oq, os_, bits, shape[1], og))
+
+
+def test_int4_lossless_known_answer_on_gpu():
+    # tests/test_deploy_and_distill.py:173-184
+    lin = torch.nn.Linear(8, 1, bias=False)
+    lin.weight.data = torch.tensor([[-7, -1, 0, 1, 7, 3, -4, 2]], dtype=torch.float32) * 0.5
+    q = qa.QuantizedLinear.from_linear(lin.cuda(), 4, 8)
+    assert q.scales.item() == 0.5
+    assert torch.equal(q.dequantize(), lin.weight.detach())
+
+
+@pytest.mark.parametrize("bits,group,max_rel", [(8, None, 0.02), (4, 16, 0.2)])
+def test_quantized_linear_forward(bits, group, max_rel):
+    # tests/test_deploy_and_distill.py:161-171 plus oracle parity of the forward itself
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(40, 24, bias=False).cuda()
+    q = qa.QuantizedLinear.from_linear(lin, bits, group)
+    for dtype, tol in ((torch.float32, 1e-5), (torch.bfloat16, 2e-2)):
+        x = torch.randn(5, 40, device="cuda").to(dtype)
+        got = q(x).float().cpu().numpy()
+        deq = oracle.round_act(q.dequantize().cpu().numpy(), "bf16" if dtype == torch.bfloat16 else "f32")
+        ref = oracle.linear(x.float().cpu().numpy(), deq, "bf16" if dtype == torch.bfloat16 else "f32")
+        assert normwise(got, ref) <= tol
+        err = np.linalg.norm(got - (x.float() @ lin.weight.T).detach().cpu().numpy()) / np.linalg.norm(ref)
+        assert err < max_rel + (0.02 if dtype == torch.bfloat16 else 0)
+    assert q.stored_bytes() < lin.weight.numel() * 4 / (3.5 if bits == 8 else 4)

@@ -1,0 +1,224 @@
+"""Whole MoE layer forward on the GPU (qw_moe_forward / TopKMoE) against the oracle.
+
+Routing (indices, weights, capacity slots, drops, overflow) is compared bit
+for bit given the kernel's logits; outputs normwise within 1e-4 (fp32) or
+2e-2 (bf16 / int8 / int4).  Each workload runs at an oracle-friendly scale and
+at its full size.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import quantaweave_amd as qa
+from quantaweave_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"f32": 1e-4, "bf16": 2e-2}
+
+
+def normwise(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30)
+
+
+def host_weights(layer):
+    w = layer.w
+    fmt = w.weights
+    out = dict(format=fmt, d_model=w.d_model, d_ff=w.d_ff, group_in=layer.group_in, group_ff=layer.group_ff)
+    for name in ("gate", "up", "down"):
+        t = getattr(layer, name)
+        out[name] = t.float().cpu().numpy() if fmt in ("f32", "bf16") else t.cpu().numpy()
+        s = getattr(layer, name + "_s")
+        if s is not None:
+            out[name + "_scales"] = s.cpu().numpy()
+    return out
+
+
+def check_layer(workload, tol_scale=1.0):
+    print(f"case {workload.name} T={workload.tokens} d={workload.d_model} E={workload.experts} f={workload.d_ff}",
+          flush=True)
+    layer = W.build_layer(workload)
+    run = W.LayerRunner(layer)
+    run()
+    torch.cuda.synchronize()
+    logits = run.workspace_view("logits").cpu().numpy()
+    x = layer.x.float().cpu().numpy()
+    rw = layer.router.float().cpu().numpy()
+    # router logits within fp32 accumulation error of the double-precision oracle
+    ref_logits = oracle.router_logits(x, rw)
+    assert np.abs(logits - ref_logits).max() <= 1e-5 * max(1.0, np.abs(ref_logits).max())
+    bias = None if layer.bias is None else layer.bias.cpu().numpy()
+    res = oracle.moe_forward(x, rw, host_weights(layer), top_k=workload.top_k, cap=run.capacity, dtype=workload.act,
+                             expert_bias=bias, logits=logits)
+    # bit-exact routing and plan
+    assert np.array_equal(run.probs.cpu().numpy().view(np.int32), res["probs"].view(np.int32))
+    assert np.array_equal(run.top_idx.cpu().numpy(), res["top_idx"])
+    assert np.array_equal(run.top_w.cpu().numpy().view(np.int32), res["top_w"].view(np.int32))
+    p = res["plan"]
+    assert np.array_equal(run.counts.cpu().numpy(), p["counts"])
+    assert np.array_equal(run.kept_counts.cpu().numpy(), p["kept_counts"])
+    assert run.totals.cpu().tolist() == p["totals"].tolist()
+    kept, nd = int(p["totals"][0]), int(p["totals"][1])
+    assert np.array_equal(run.workspace_view("slot_token").cpu().numpy()[:kept], p["slot_token"])
+    assert np.array_equal(run.workspace_view("route_slot").cpu().numpy(), p["route_slot"])
+    assert np.array_equal(run.dropped_token.cpu().numpy()[:nd], p["dropped_token"])
+    assert np.array_equal(run.dropped_expert.cpu().numpy()[:nd], p["dropped_expert"])
+    # expert outputs
+    got = run.out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    assert normwise(got, res["out"]) <= TOL[workload.act] * tol_scale
+    return run, res
+
+
+SMALL = [
+    W.WORKLOADS["fp32-plumbing-T512-d256-E8-f512-k2"],
+    W.scaled(W.WORKLOADS["bf16-prefill-T8192-d2048-E64-f1024-k2"], tokens=1024, d_model=512, d_ff=256),
+    W.scaled(W.WORKLOADS["int8-decode-T64-d2048-E64-f1024-k2"], d_model=512, d_ff=256),
+    W.scaled(W.WORKLOADS["int4-decode-T16-d4096-E64-f1408-k2"], d_model=1024, d_ff=352),
+    W.scaled(W.WORKLOADS["skewed-T4096-d2048-E64-f1024-k2"], tokens=1024, d_model=512, d_ff=256),
+]
+
+
+@pytest.mark.parametrize("workload", SMALL, ids=lambda w: w.name)
+def test_layer_matches_oracle_small(workload):
+    run, res = check_layer(workload)
+    if workload.capacity_factor == 1.0:
+        assert int(res["plan"]["totals"][1]) > 0            # the skewed workload drops routes
+
+
+@pytest.mark.parametrize("name", [n for n in W.WORKLOADS if not n.startswith("fp32")])
+def test_layer_matches_oracle_full_size(name):
+    check_layer(W.WORKLOADS[name])
+
+
+def test_layer_is_deterministic_across_calls():
+    layer = W.build_layer(W.scaled(W.WORKLOADS["skewed-T4096-d2048-E64-f1024-k2"], tokens=2048, d_model=512, d_ff=256))
+    run = W.LayerRunner(layer)
+    run()
+    first = (run.out.clone(), run.top_idx.clone(), run.workspace_view("slot_token").clone())
+    for _ in range(3):
+        run()
+    torch.cuda.synchronize()
+    assert torch.equal(first[0], run.out) and torch.equal(first[1], run.top_idx)
+    assert torch.equal(first[2], run.workspace_view("slot_token"))
+
+
+# ---------------------------------------------------------------- the TopKMoE module surface
+def small_config(**overrides):
+    values = dict(vocab_size=32, hidden_size=16, layers=2, ffn_size=32, num_experts=6, top_k=2,
+                  attention_heads=2, max_sequence_length=16, capacity_factor=0, min_expert_capacity=1)
+    values.update(overrides)
+    return qa.QuantaWeaveConfig(**values)
+
+
+def module_weights(moe):
+    return dict(format="f32", d_model=moe.router.in_features, d_ff=moe.experts[0].gate.out_features,
+                gate=np.stack([e.gate.weight.detach().cpu().numpy() for e in moe.experts]),
+                up=np.stack([e.up.weight.detach().cpu().numpy() for e in moe.experts]),
+                down=np.stack([e.down.weight.detach().cpu().numpy() for e in moe.experts]))
+
+
+@pytest.mark.parametrize("capacity_factor", [0, 0.6])
+def test_topkmoe_matches_oracle_and_reports_overflow(capacity_factor):
+    # tests/test_model_features.py:38-46
+    torch.manual_seed(0)
+    moe = qa.TopKMoE(small_config(capacity_factor=capacity_factor, min_expert_capacity=2)).cuda()
+    hidden = torch.randn(3, 8, 16, device="cuda")
+    out, balance, dropped, overflow, domain = moe(hidden)
+    flat = hidden.reshape(-1, 16).cpu().numpy()
+    cap = moe.capacity(24)
+    ref = oracle.moe_forward(flat, moe.router.weight.detach().cpu().numpy(), module_weights(moe), top_k=2, cap=cap,
+                             dtype="f32")
+    assert np.allclose(out.reshape(-1, 16).cpu().numpy(), ref["out"], atol=1e-5)
+    assert int(overflow) == int(ref["plan"]["totals"][1]) == int(dropped)
+    assert abs(float(balance) - ref["balance"]) < 1e-5
+    assert out.shape == hidden.shape and balance.dtype == torch.float32 and overflow.dtype == torch.int64
+    assert float(domain) == 0.0
+    if capacity_factor:
+        assert int(overflow) > 0
+
+
+def test_capacity_keeps_highest_weight_routes_not_first_tokens():
+    # tests/test_quantweave.py:116-127, observed through the plan instead of recorder experts
+    cfg = qa.QuantaWeaveConfig(vocab_size=8, hidden_size=2, layers=1, ffn_size=2, num_experts=2, top_k=2,
+                               attention_heads=1, max_sequence_length=4, capacity_factor=0.5, min_expert_capacity=1)
+    moe = qa.TopKMoE(cfg).cuda()
+    moe.router.weight.data = torch.tensor([[1.0, 0.0], [0.0, 0.0]], device="cuda")
+    features = torch.tensor([0.5, 3.0, -2.0, 1.5])
+    hidden = torch.stack([features, torch.zeros(4)], dim=-1)[None].cuda()
+    _, _, dropped, overflow, _ = moe(hidden)
+    assert overflow.item() == 4 and dropped.item() == 4
+    kc = moe.last_plan["kept_counts"].tolist()
+    assert kc == [2, 2]
+    # kept tokens per expert: recover through the dropped list
+    dt = moe.last_plan["dropped_token"][:4].tolist()
+    de = moe.last_plan["dropped_expert"][:4].tolist()
+    kept0 = sorted(features[t].item() for t in range(4) if (t, 0) not in zip(dt, de))
+    kept1 = sorted(features[t].item() for t in range(4) if (t, 1) not in zip(dt, de))
+    assert kept0 == [1.5, 3.0] and kept1 == [-2.0, 0.5]
+
+
+def test_residual_policy_and_disabled_capacity():
+    # tests/test_quantweave.py:129-147
+    for overrides, exp_dropped, exp_overflow in ((dict(overflow_policy="residual"), 0, 4),
+                                                 (dict(drop_overflow_tokens=False), 0, 0)):
+        cfg = qa.QuantaWeaveConfig(vocab_size=8, hidden_size=2, layers=1, ffn_size=2, num_experts=2, top_k=2,
+                                   attention_heads=1, max_sequence_length=4, capacity_factor=0.5,
+                                   min_expert_capacity=1, **overrides)
+        moe = qa.TopKMoE(cfg).cuda()
+        moe.router.weight.data = torch.tensor([[1.0, 0.0], [0.0, 0.0]], device="cuda")
+        hidden = torch.stack([torch.tensor([0.5, 3.0, -2.0, 1.5]), torch.zeros(4)], dim=-1)[None].cuda()
+        _, _, dropped, overflow, _ = moe(hidden)
+        assert dropped.item() == exp_dropped and overflow.item() == exp_overflow
+
+
+def test_skipped_route_contributes_exactly_zero():
+    # tests/test_quantweave.py:149-163
+    cfg = qa.QuantaWeaveConfig(vocab_size=8, hidden_size=2, layers=1, ffn_size=4, num_experts=2, top_k=1,
+                               attention_heads=1, max_sequence_length=4, capacity_factor=0.5, min_expert_capacity=1)
+    moe = qa.TopKMoE(cfg).cuda()
+    moe.router.weight.data = torch.tensor([[1.0, 0.0], [-1.0, 0.0]], device="cuda")
+    hidden = torch.tensor([[[5.0, 1.0], [4.0, 1.0], [3.0, 1.0], [2.0, 1.0]]], device="cuda")
+    output, _, _, overflow, _ = moe(hidden)
+    assert overflow.item() == 3
+    assert (output[0].abs().sum(-1) > 0).sum().item() == 1
+
+
+def test_quantized_experts_take_the_grouped_path():
+    torch.manual_seed(3)
+    cfg = small_config(hidden_size=64, ffn_size=96, num_experts=8, attention_heads=1)
+    moe = qa.TopKMoE(cfg).cuda()
+    moe.to(torch.bfloat16)
+    stats = qa.quantize_model(moe, 4)
+    assert stats["replaced_layers"] == 8 * 3
+    hidden = torch.randn(2, 40, 64, device="cuda").bfloat16()
+    out, *_ = moe(hidden)
+    w = dict(format="u4", d_model=64, d_ff=96, group_in=32, group_ff=32)
+    for name in ("gate", "up", "down"):
+        w[name] = np.stack([getattr(e, name).qweight.cpu().numpy() for e in moe.experts])
+        w[name + "_scales"] = np.stack([getattr(e, name).scales.cpu().numpy() for e in moe.experts])
+    flat = hidden.reshape(-1, 64).float().cpu().numpy()
+    ref = oracle.moe_forward(flat, moe.router.weight.float().detach().cpu().numpy(), w, top_k=2, cap=moe.capacity(80),
+                             dtype="bf16")
+    assert normwise(out.reshape(-1, 64).float().cpu().numpy(), ref["out"]) <= 2e-2
+    with pytest.raises(ValueError, match="already quantized"):
+        qa.quantize_model(moe, 4)
+
+
+def test_stats_and_static_dispatch():
+    torch.manual_seed(1)
+    moe = qa.TopKMoE(small_config(capacity_factor=0.5, min_expert_capacity=1)).cuda()
+    moe.collect_stats = True
+    hidden = torch.randn(2, 8, 16, device="cuda")
+    _, _, dropped, overflow, _ = moe(hidden)
+    st = moe.last_stats
+    assert st["expert_load"].sum().item() == 32 - overflow.item()
+    assert st["dropped_tokens"].numel() == overflow.item() == st["dropped_experts"].numel()
+    assert st["expert_assigned"].sum().item() == 32
+    moe.static_dispatch = True
+    _, _, dropped, overflow, _ = moe(hidden)
+    assert overflow.item() == 0
