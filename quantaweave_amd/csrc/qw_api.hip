@@ -69,7 +69,7 @@ size_t experts_workspace_bytes(int64_t max_rows, int64_t E, int64_t D, int64_t F
 int experts(const void* x, int act, const int32_t* row_index, const int32_t* offsets, int64_t E, int64_t D, int64_t F,
             int64_t max_rows, int wfmt, int64_t group_in, int64_t group_ff, const void* gate_w, const float* gate_s,
             const void* up_w, const float* up_s, const void* down_w, const float* down_s, const float* row_weight,
-            void* y, void* ws, size_t ws_bytes, hipStream_t stream, int64_t avg_rows) {
+            void* y, void* ws, size_t ws_bytes, hipStream_t stream, int64_t avg_rows, int64_t row_cap) {
   QW_REQUIRE(act == QW_F32 || act == QW_BF16, "activation dtype must be f32 or bf16");
   QW_REQUIRE(wfmt >= QW_F32 && wfmt <= QW_U4, "unknown weight format %d", wfmt);
   QW_REQUIRE(E >= 1 && E <= 65535, "experts out of range");
@@ -105,6 +105,7 @@ int experts(const void* x, int act, const int32_t* row_index, const int32_t* off
   a.partial = c.take<float>(static_cast<size_t>(max_rows) * D);
   a.y = y;
   a.avg_rows = avg_rows;
+  a.row_cap = row_cap;
   if (!ffn_path_override()) {
     bool handled = false;
     int st = launch_ffn_gemv(a, stream, &handled);
@@ -211,7 +212,7 @@ int qw_moe_experts(const void* x, int act_dtype, const int32_t* row_index, const
   const int64_t avg = experts > 0 ? (max_rows + experts - 1) / experts : 0;
   return qw::experts(x, act_dtype, row_index, kept_offsets, experts, d_model, d_ff, max_rows, w_format, group_in,
                      group_ff, gate_w, gate_scales, up_w, up_scales, down_w, down_scales, row_weight, y, workspace,
-                     workspace_bytes, as_stream(stream), avg);
+                     workspace_bytes, as_stream(stream), avg, max_rows);
 }
 
 int qw_moe_combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, int64_t tokens,
@@ -274,7 +275,7 @@ int qw_moe_forward(const void* x, int act_dtype, int64_t tokens, int64_t d_model
     const int64_t avg = (R + experts - 1) / experts;
     st = qw::experts(x, act_dtype, slot_token, kept_offsets, experts, d_model, d_ff, max_rows, w_format, group_in,
                      group_ff, gate_w, gate_scales, up_w, up_scales, down_w, down_scales, slot_weight, y, ews, exp_ws,
-                     s, avg < capacity ? avg : capacity);
+                     s, avg < capacity ? avg : capacity, std::min<int64_t>(capacity, R));
     if (st) return st;
   }
   return combine(y, act_dtype, route_slot, top_idx, tokens, top_k, d_model, out, s);

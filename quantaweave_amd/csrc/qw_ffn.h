@@ -17,6 +17,7 @@ struct FfnArgs {
   void* y;                   // [max_rows, d_model] act dtype
   float* partial;            // split-K partial sums (workspace), may be NULL
   int64_t avg_rows;          // expected rows per expert (host-side estimate)
+  int64_t row_cap;           // most rows any one expert can hold (capacity bound)
 };
 
 int launch_ffn_generic(const FfnArgs& a, hipStream_t stream);
