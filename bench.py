@@ -72,11 +72,14 @@ def stage_calls(run):
     max_rows = min(R, run.capacity * E)
     exp_bytes = lib.qw_moe_experts_workspace_bytes(max_rows, E, D, F, run.act)
     exp_ws = _hip.workspace(exp_bytes, lay.x.device)
+    route_bytes = lib.qw_moe_route_workspace_bytes(T, D, E)
+    route_ws = _hip.workspace(route_bytes, lay.x.device)
     s = run.stream
 
     def route():
         _lib.check(lib.qw_moe_route(P(lay.x), run.act, D, P(lay.router), run.act, T, D, E, K, 1.0, P(lay.bias),
-                                    P(logits), P(run.probs), P(run.top_idx), P(run.top_w), s), "route")
+                                    P(logits), P(run.probs), P(run.top_idx), P(run.top_w), P(route_ws), route_bytes,
+                                    s), "route")
 
     def plan():
         _lib.check(lib.qw_moe_plan(P(run.top_idx), P(run.top_w), T, K, E, run.capacity, P(run.counts),

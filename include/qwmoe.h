@@ -67,11 +67,13 @@ int64_t qw_moe_capacity(int64_t tokens, int64_t top_k, int64_t experts, double c
  * x: [tokens, d_model] (QW_F32 or QW_BF16) with row stride x_row_stride
  * elements; router_w: [experts, d_model] contiguous (QW_F32 or QW_BF16).
  * Top-k order is descending, ties resolved towards the lower expert index.
- * 1 <= top_k <= experts <= 1024. */
+ * 1 <= top_k <= experts <= 1024.  The router GEMM is split over d_model; its
+ * fp32 partial sums go to `workspace` and are added in a fixed order. */
+size_t qw_moe_route_workspace_bytes(int64_t tokens, int64_t d_model, int64_t experts);
 int qw_moe_route(const void* x, int x_dtype, int64_t x_row_stride, const void* router_w, int w_dtype,
                  int64_t tokens, int64_t d_model, int64_t experts, int64_t top_k, float temperature,
                  const float* expert_bias, float* logits, float* probs, int32_t* top_idx, float* top_w,
-                 void* stream);
+                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* The softmax/top-k/renormalise half of qw_moe_route on caller-supplied fp32
  * logits [tokens, experts] (already divided by the temperature).  With

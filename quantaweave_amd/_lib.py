@@ -24,7 +24,8 @@ SIGNATURES = {
     "qw_last_error": (ctypes.c_char_p, []),
     "qw_abi_version": (I32, []),
     "qw_moe_capacity": (I64, [I64, I64, I64, F64, F64, I64, I32]),
-    "qw_moe_route": (I32, [P, I32, I64, P, I32, I64, I64, I64, I64, F32, P, P, P, P, P, P]),
+    "qw_moe_route_workspace_bytes": (SZ, [I64, I64, I64]),
+    "qw_moe_route": (I32, [P, I32, I64, P, I32, I64, I64, I64, I64, F32, P, P, P, P, P, P, SZ, P]),
     "qw_moe_route_from_logits": (I32, [P, I64, I64, I64, P, P, P, P, P]),
     "qw_moe_plan_workspace_bytes": (SZ, [I64, I64, I64]),
     "qw_moe_plan": (I32, [P, P, I64, I64, I64, I64, P, P, P, P, P, P, P, P, P, P, SZ, P]),

@@ -25,7 +25,8 @@ void clear_error() { g_error[0] = '\0'; }
 // Implemented in the kernel files.
 int route(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int64_t T, int64_t D, int64_t E,
           int64_t K, float temperature, const float* bias, float* logits, float* probs, int32_t* top_idx,
-          float* top_w, hipStream_t stream);
+          float* top_w, float* partial, size_t partial_bytes, hipStream_t stream);
+size_t route_workspace_bytes(int64_t T, int64_t D, int64_t E);
 int route_from_logits(const float* logits, int64_t T, int64_t E, int64_t K, const float* bias, float* probs,
                       int32_t* top_idx, float* top_w, hipStream_t stream);
 size_t plan_workspace_bytes(int64_t T, int64_t K, int64_t E);
@@ -127,6 +128,7 @@ size_t forward_workspace_bytes(int64_t T, int64_t D, int64_t E, int64_t K, int64
   c.take<char>(static_cast<size_t>(R) * D * act_size(act));  // y
   c.take<char>(plan_workspace_bytes(T, K, E));
   c.take<char>(experts_workspace_bytes(R, E, D, F, act));
+  c.take<char>(route_workspace_bytes(T, D, E));
   return c.used + 256;
 }
 
@@ -162,12 +164,18 @@ int64_t qw_moe_capacity(int64_t tokens, int64_t top_k, int64_t experts, double c
   return tokens * top_k;
 }
 
+size_t qw_moe_route_workspace_bytes(int64_t tokens, int64_t d_model, int64_t experts) {
+  if (tokens < 0 || d_model < 1 || experts < 1) return 0;
+  return route_workspace_bytes(tokens, d_model, experts);
+}
+
 int qw_moe_route(const void* x, int x_dtype, int64_t x_row_stride, const void* router_w, int w_dtype, int64_t tokens,
                  int64_t d_model, int64_t experts, int64_t top_k, float temperature, const float* expert_bias,
-                 float* logits, float* probs, int32_t* top_idx, float* top_w, void* stream) {
+                 float* logits, float* probs, int32_t* top_idx, float* top_w, void* workspace,
+                 size_t workspace_bytes, void* stream) {
   clear_error();
   return route(x, x_dtype, x_row_stride, router_w, w_dtype, tokens, d_model, experts, top_k, temperature, expert_bias,
-               logits, probs, top_idx, top_w, as_stream(stream));
+               logits, probs, top_idx, top_w, static_cast<float*>(workspace), workspace_bytes, as_stream(stream));
 }
 
 int qw_moe_route_from_logits(const float* logits, int64_t tokens, int64_t experts, int64_t top_k,
@@ -265,8 +273,10 @@ int qw_moe_forward(const void* x, int act_dtype, int64_t tokens, int64_t d_model
   const int64_t max_rows = std::min<int64_t>(R, capacity * experts);
   const size_t exp_ws = experts_workspace_bytes(R, experts, d_model, d_ff, act_dtype);
   char* ews = c.take<char>(exp_ws);
+  const size_t route_ws = route_workspace_bytes(tokens, d_model, experts);
+  float* rws = reinterpret_cast<float*>(c.take<char>(route_ws));
   int st = route(x, act_dtype, d_model, router_w, router_dtype, tokens, d_model, experts, top_k, temperature,
-                 expert_bias, logits, probs, top_idx, top_w, s);
+                 expert_bias, logits, probs, top_idx, top_w, rws, route_ws, s);
   if (st) return st;
   st = plan(top_idx, top_w, tokens, top_k, experts, capacity, counts, kept_counts, kept_offsets, slot_token,
             slot_weight, route_slot, dropped_token, dropped_expert, totals, pws, plan_ws, s);

@@ -75,11 +75,38 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
     for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
     for (int j = 0; j < nk; ++j) {
       const int64_t src = static_cast<int64_t>(slot[j]) * D + c;
+      if constexpr (VEC == 8 && ACT == QW_BF16) {
+        const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(y) + src);
+        const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) acc[v] = round_act<ACT>(acc[v] + load_act<ACT>(y, src + v));
+        for (int v = 0; v < 4; ++v) {
+          acc[2 * v] = round_act<ACT>(acc[2 * v] + __uint_as_float(w4[v] << 16));
+          acc[2 * v + 1] = round_act<ACT>(acc[2 * v + 1] + __uint_as_float(w4[v] & 0xffff0000u));
+        }
+      } else if constexpr (VEC == 4 && ACT == QW_F32) {
+        const float4 q = *reinterpret_cast<const float4*>(static_cast<const float*>(y) + src);
+        acc[0] += q.x;
+        acc[1] += q.y;
+        acc[2] += q.z;
+        acc[3] += q.w;
+      } else {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[v] = round_act<ACT>(acc[v] + load_act<ACT>(y, src + v));
+      }
     }
+    if constexpr (VEC == 8 && ACT == QW_BF16) {
+      uint4 o;
+      o.x = f32_to_bf16(acc[0]) | (static_cast<uint32_t>(f32_to_bf16(acc[1])) << 16);
+      o.y = f32_to_bf16(acc[2]) | (static_cast<uint32_t>(f32_to_bf16(acc[3])) << 16);
+      o.z = f32_to_bf16(acc[4]) | (static_cast<uint32_t>(f32_to_bf16(acc[5])) << 16);
+      o.w = f32_to_bf16(acc[6]) | (static_cast<uint32_t>(f32_to_bf16(acc[7])) << 16);
+      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + row + c) = o;
+    } else if constexpr (VEC == 4 && ACT == QW_F32) {
+      *reinterpret_cast<float4*>(static_cast<float*>(out) + row + c) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    } else {
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) store_act<ACT>(out, row + c + v, acc[v]);
+      for (int v = 0; v < VEC; ++v) store_act<ACT>(out, row + c + v, acc[v]);
+    }
   }
 }
 

@@ -1,18 +1,25 @@
-// Capacity plan: per-expert histogram, prefix scans, and capacity slots.
+// Capacity plan: per-expert route counts, prefix scans and capacity slots.
 //
 // Reference: TopKMoE._plan, src/quantweave_moe_model.py:166-188.  The reference
 // orders routes with two stable argsorts (weight descending, then expert), i.e.
 // by the key (expert asc, weight desc, route id asc), keeps the first
-// `capacity` routes of each expert and lists the rest as dropped.  Here the
-// position of a route inside its expert is its rank under that key, counted
-// directly: rank(r) = #{r' in expert(r) : key(r') < key(r)}.  Keys are unique
-// (they contain r), so ranks are a permutation and no sort is needed; the
-// result is independent of scheduling.
+// `capacity` routes of each expert and lists the rest as dropped.
+//
+// Here one workgroup owns one expert.  Kernel 1 counts the expert's routes.
+// Kernel 2 derives every offset from the counts (each workgroup scans the E
+// counts itself), gathers the expert's route keys
+//   key = (~order(weight)) << 32 | route id        (unique per route)
+// into LDS, sorts them with a bitonic network and writes kept slots and
+// dropped routes at their plan positions.  Keys are unique, so the order
+// inside the gather does not matter and the result does not depend on
+// scheduling.  An expert with more routes than the LDS holds ranks its keys
+// against each other through global memory instead (same result, slower).
 #include "qw_common.h"
 
 namespace qw {
 
 constexpr int kPlanThreads = 1024;
+constexpr int kSortCap = 8192;  // keys an expert sorts in LDS (64 KiB)
 
 // Order-preserving map of a float onto uint32 (NaN largest, like torch.sort).
 __device__ __forceinline__ uint32_t weight_key(float f) {
@@ -20,7 +27,11 @@ __device__ __forceinline__ uint32_t weight_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Block-wide exclusive scan of one int per thread (1024 threads).
+__device__ __forceinline__ uint64_t route_key(const float* top_w, int r) {
+  return (static_cast<uint64_t>(~weight_key(top_w[r])) << 32) | static_cast<uint32_t>(r);
+}
+
+// Block-wide exclusive scan of one int per thread; *total gets the sum.
 __device__ int block_exclusive_scan(int v, int* warp_tot, int* total) {
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   int incl = v;
@@ -33,14 +44,14 @@ __device__ int block_exclusive_scan(int v, int* warp_tot, int* total) {
   __syncthreads();
   if (wave == 0) {
     const int nw = blockDim.x / kWave;
-    int w = lane < nw ? warp_tot[lane] : 0;
+    const int w = lane < nw ? warp_tot[lane] : 0;
     int wi = w;
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
       const int n = __shfl_up(wi, o, kWave);
       if (lane >= o) wi += n;
     }
-    if (lane < nw) warp_tot[lane] = wi - w;  // exclusive wave offsets
+    if (lane < nw) warp_tot[lane] = wi - w;
     if (lane == nw - 1) *total = wi;
   }
   __syncthreads();
@@ -49,141 +60,150 @@ __device__ int block_exclusive_scan(int v, int* warp_tot, int* total) {
   return r;
 }
 
-// Histogram of routes per expert and the scans derived from it.  One block.
-__global__ __launch_bounds__(kPlanThreads) void plan_count_kernel(
-    const int32_t* __restrict__ top_idx, int R, int E, int capacity, int32_t* __restrict__ counts,
-    int32_t* __restrict__ kept_counts, int32_t* __restrict__ kept_offsets, int32_t* __restrict__ totals,
-    int32_t* __restrict__ route_off, int32_t* __restrict__ cursor, int32_t* __restrict__ drop_off) {
-  __shared__ int hist[1024];
-  __shared__ int warp_tot[kPlanThreads / kWave];
-  __shared__ int tot_kept, tot_drop, tot_routes;
-  for (int e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
+__device__ int block_sum(int v, int* red) {
+  v = wave_sum_i(v);
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  if (lane == 0) red[wave] = v;
   __syncthreads();
-  for (int r = threadIdx.x; r < R; r += blockDim.x) {
-    const int e = top_idx[r];
-    if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
-  }
-  __syncthreads();
-  const int e = threadIdx.x;  // E <= 1024 == blockDim.x
-  const int c = e < E ? hist[e] : 0;
-  const int kc = c < capacity ? c : capacity;
-  const int dc = c - kc;
-  const int ro = block_exclusive_scan(c, warp_tot, &tot_routes);
-  const int ko = block_exclusive_scan(kc, warp_tot, &tot_kept);
-  const int dof = block_exclusive_scan(dc, warp_tot, &tot_drop);
-  if (e < E) {
-    counts[e] = c;
-    kept_counts[e] = kc;
-    kept_offsets[e] = ko;
-    route_off[e] = ro;
-    cursor[e] = ro;
-    drop_off[e] = dof;
-  }
-  if (e == 0) {
-    kept_offsets[E] = tot_kept;
-    totals[0] = tot_kept;
-    totals[1] = tot_drop;
-  }
-}
-
-// Scatter route ids into per-expert buckets (order inside a bucket is
-// irrelevant: the rank kernel orders by key).  Keys: high word ~weight_key(w)
-// so larger weights come first, low word the route id.
-__global__ void plan_bucket_kernel(const int32_t* __restrict__ top_idx, const float* __restrict__ top_w, int R,
-                                   int E, int32_t* __restrict__ cursor, uint64_t* __restrict__ bucket_key,
-                                   int32_t* __restrict__ bucket_expert) {
-  const int r = blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= R) return;
-  const int e = top_idx[r];
-  if (e < 0 || e >= E) return;
-  const int pos = atomicAdd(&cursor[e], 1);
-  bucket_key[pos] = (static_cast<uint64_t>(~weight_key(top_w[r])) << 32) | static_cast<uint32_t>(r);
-  bucket_expert[pos] = e;
-}
-
-// Rank every bucketed route inside its expert and emit slots / drops.
-// Keys of the block's experts are streamed through LDS in tiles.
-__global__ __launch_bounds__(256) void plan_rank_kernel(
-    const uint64_t* __restrict__ bucket_key, const int32_t* __restrict__ bucket_expert,
-    const int32_t* __restrict__ route_off, const int32_t* __restrict__ counts,
-    const int32_t* __restrict__ kept_offsets, const int32_t* __restrict__ drop_off,
-    const int32_t* __restrict__ totals_routes, const float* __restrict__ top_w, int R, int K, int capacity,
-    int32_t* __restrict__ slot_token, float* __restrict__ slot_weight, int32_t* __restrict__ route_slot,
-    int32_t* __restrict__ dropped_token, int32_t* __restrict__ dropped_expert) {
-  (void)totals_routes;
-  __shared__ uint64_t tile[256];
-  const int pos = blockIdx.x * 256 + threadIdx.x;
-  const int nvalid = *totals_routes;  // routes with a valid expert id
-  const bool active = pos < nvalid;
-  uint64_t my_key = 0;
-  int e = -1, lo = 0, hi = 0;
-  if (active) {
-    my_key = bucket_key[pos];
-    e = bucket_expert[pos];
-    lo = route_off[e];
-    hi = lo + counts[e];
-  }
-  // The block covers bucket positions [b0, b0+256): the experts spanned are a
-  // contiguous range, so the union of their key ranges is [first_lo, last_hi).
-  __shared__ int s_lo, s_hi;
-  const int b0 = blockIdx.x * 256;
-  const int last = min(b0 + 255, nvalid - 1);
+  int s = 0;
   if (threadIdx.x == 0) {
-    s_lo = (b0 < nvalid) ? route_off[bucket_expert[b0]] : 0;
-    s_hi = (b0 < nvalid) ? route_off[bucket_expert[last]] + counts[bucket_expert[last]] : 0;
+    for (int w = 0; w < static_cast<int>(blockDim.x / kWave); ++w) s += red[w];
+    red[0] = s;
   }
   __syncthreads();
-  const int span_lo = s_lo, span_hi = s_hi;
-  int rank = 0;
-  for (int base = span_lo; base < span_hi; base += 256) {
-    const int i = base + threadIdx.x;
-    tile[threadIdx.x] = (i < span_hi) ? bucket_key[i] : 0;
-    __syncthreads();
-    if (active) {
-      const int j0 = max(lo - base, 0), j1 = min(hi - base, 256);
-      for (int j = j0; j < j1; ++j) rank += (tile[j] < my_key) ? 1 : 0;
+  s = red[0];
+  __syncthreads();
+  return s;
+}
+
+// Kernel 1: counts[e] = #{r : top_idx[r] == e}; block e == 0 also marks routes
+// with an out-of-range expert id as not kept.
+__global__ __launch_bounds__(kPlanThreads) void plan_count_kernel(const int32_t* __restrict__ top_idx, int R, int E,
+                                                                  int32_t* __restrict__ counts,
+                                                                  int32_t* __restrict__ route_slot) {
+  __shared__ int red[kPlanThreads / kWave];
+  const int e = blockIdx.x;
+  int c = 0;
+  for (int r = threadIdx.x; r < R; r += blockDim.x) {
+    const int v = top_idx[r];
+    c += (v == e) ? 1 : 0;
+    if (e == 0 && (v < 0 || v >= E)) route_slot[r] = -1;
+  }
+  c = block_sum(c, red);
+  if (threadIdx.x == 0) counts[e] = c;
+}
+
+// Kernel 2: offsets, per-expert sort and placement.
+__global__ __launch_bounds__(kPlanThreads) void plan_place_kernel(
+    const int32_t* __restrict__ top_idx, const float* __restrict__ top_w, int R, int E, int K, int capacity,
+    const int32_t* __restrict__ counts, int32_t* __restrict__ kept_counts, int32_t* __restrict__ kept_offsets,
+    int32_t* __restrict__ totals, int32_t* __restrict__ slot_token, float* __restrict__ slot_weight,
+    int32_t* __restrict__ route_slot, int32_t* __restrict__ dropped_token, int32_t* __restrict__ dropped_expert,
+    uint64_t* __restrict__ spill) {
+  __shared__ uint64_t keys[kSortCap];
+  __shared__ int warp_tot[kPlanThreads / kWave];
+  __shared__ int s_tot_kept, s_tot_drop, s_tot_routes;
+  __shared__ int s_kept_off, s_drop_off, s_route_off, s_fill;
+  const int e = blockIdx.x;
+  const int tid = threadIdx.x;
+
+  // ---- offsets from the E counts (E <= 1024 == blockDim) ----
+  const int c = tid < E ? counts[tid] : 0;
+  const int kc = c < capacity ? c : capacity;
+  const int ko = block_exclusive_scan(kc, warp_tot, &s_tot_kept);
+  const int dof = block_exclusive_scan(c - kc, warp_tot, &s_tot_drop);
+  const int ro = block_exclusive_scan(c, warp_tot, &s_tot_routes);
+  if (tid == e) {
+    s_kept_off = ko;
+    s_drop_off = dof;
+    s_route_off = ro;
+  }
+  if (e == 0 && tid < E) {
+    kept_counts[tid] = kc;
+    kept_offsets[tid] = ko;
+  }
+  if (e == 0 && tid == 0) {
+    kept_offsets[E] = s_tot_kept;
+    totals[0] = s_tot_kept;
+    totals[1] = s_tot_drop;
+  }
+  if (tid == 0) s_fill = 0;
+  __syncthreads();
+  const int n = counts[e];
+  if (n == 0) return;
+  const int kept_off = s_kept_off, drop_off = s_drop_off;
+
+  auto place = [&](uint64_t key, int rank) {
+    const int r = static_cast<int>(key & 0xffffffffu);
+    if (rank < capacity) {
+      const int s = kept_off + rank;
+      slot_token[s] = r / K;
+      slot_weight[s] = top_w[r];
+      route_slot[r] = s;
+    } else {
+      const int q = drop_off + (rank - capacity);
+      dropped_token[q] = r / K;
+      dropped_expert[q] = e;
+      route_slot[r] = -1;
     }
+  };
+
+  if (n <= kSortCap) {
+    // ---- gather this expert's keys into LDS ----
+    for (int r = tid; r < R; r += blockDim.x) {
+      if (top_idx[r] == e) {
+        const int p = atomicAdd(&s_fill, 1);
+        keys[p] = route_key(top_w, r);
+      }
+    }
+    int p2 = 1;
+    while (p2 < n) p2 <<= 1;
     __syncthreads();
-  }
-  if (!active) return;
-  const int r = static_cast<int>(my_key & 0xffffffffu);
-  if (rank < capacity) {
-    const int s = kept_offsets[e] + rank;
-    slot_token[s] = r / K;
-    slot_weight[s] = top_w[r];
-    route_slot[r] = s;
+    for (int i = n + tid; i < p2; i += blockDim.x) keys[i] = ~0ull;  // padding sorts last
+    __syncthreads();
+    // ---- bitonic sort, ascending ----
+    for (int size = 2; size <= p2; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int i = tid; i < p2 / 2; i += blockDim.x) {
+          const int lo = 2 * i - (i & (stride - 1));
+          const int hi = lo + stride;
+          const bool up = ((lo & size) == 0);
+          const uint64_t a = keys[lo], b = keys[hi];
+          if ((a > b) == up) {
+            keys[lo] = b;
+            keys[hi] = a;
+          }
+        }
+        __syncthreads();
+      }
+    }
+    for (int i = tid; i < n; i += blockDim.x) place(keys[i], i);
   } else {
-    const int q = drop_off[e] + (rank - capacity);
-    dropped_token[q] = r / K;
-    dropped_expert[q] = e;
-    route_slot[r] = -1;
+    // ---- large expert: keys in global scratch, rank by counting ----
+    uint64_t* mine = spill + s_route_off;
+    for (int r = tid; r < R; r += blockDim.x) {
+      if (top_idx[r] == e) {
+        const int p = atomicAdd(&s_fill, 1);
+        mine[p] = route_key(top_w, r);
+      }
+    }
+    __threadfence();
+    __syncthreads();
+    // coherent (L1-bypassing) loads: the keys were just written by other waves
+    for (int i = tid; i < n; i += blockDim.x) {
+      const uint64_t k = __hip_atomic_load(&mine[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      int rank = 0;
+      for (int j = 0; j < n; ++j)
+        rank += (__hip_atomic_load(&mine[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < k) ? 1 : 0;
+      place(k, rank);
+    }
   }
-}
-
-// Routes whose expert id is out of range are marked as not kept.
-__global__ void plan_mark_invalid_kernel(const int32_t* __restrict__ top_idx, int R, int E,
-                                         int32_t* __restrict__ route_slot) {
-  const int r = blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= R) return;
-  const int e = top_idx[r];
-  if (e < 0 || e >= E) route_slot[r] = -1;
-}
-
-// Number of routes with a valid expert id = route_off[E-1] + counts[E-1].
-__global__ void plan_valid_total_kernel(const int32_t* __restrict__ route_off, const int32_t* __restrict__ counts,
-                                        int E, int32_t* __restrict__ out) {
-  if (threadIdx.x == 0 && blockIdx.x == 0) *out = route_off[E - 1] + counts[E - 1];
 }
 
 size_t plan_workspace_bytes(int64_t T, int64_t K, int64_t E) {
+  (void)E;
   Carver c(nullptr);
-  const size_t R = static_cast<size_t>(T * K);
-  c.take<int32_t>(E);   // route_off
-  c.take<int32_t>(E);   // cursor
-  c.take<int32_t>(E);   // drop_off
-  c.take<int32_t>(4);   // valid total
-  c.take<uint64_t>(R);  // bucket keys
-  c.take<int32_t>(R);   // bucket experts
+  c.take<uint64_t>(static_cast<size_t>(T * K));  // keys of experts too large for LDS
   return c.used + 256;
 }
 
@@ -201,32 +221,18 @@ int plan(const int32_t* top_idx, const float* top_w, int64_t T, int64_t K, int64
                         dropped_expert),
              "route arrays are required");
   const size_t need = plan_workspace_bytes(T, K, E);
-  if (ws_bytes < need || (need && !ws))
+  if (ws_bytes < need || !ws)
     return set_error(QW_ERR_WORKSPACE, "plan workspace needs %zu bytes, got %zu", need, ws_bytes);
   const int cap = capacity > INT32_MAX ? INT32_MAX : static_cast<int>(capacity);
   Carver c(ws);
-  int32_t* route_off = c.take<int32_t>(E);
-  int32_t* cursor = c.take<int32_t>(E);
-  int32_t* drop_off = c.take<int32_t>(E);
-  int32_t* valid = c.take<int32_t>(4);
-  uint64_t* bkey = c.take<uint64_t>(R);
-  int32_t* bexp = c.take<int32_t>(R);
+  uint64_t* spill = c.take<uint64_t>(static_cast<size_t>(R));
   const int e = static_cast<int>(E);
-  plan_count_kernel<<<1, kPlanThreads, 0, stream>>>(top_idx, R, e, cap, counts, kept_counts, kept_offsets, totals,
-                                                    route_off, cursor, drop_off);
+  plan_count_kernel<<<e, kPlanThreads, 0, stream>>>(top_idx, R, e, counts, route_slot);
   QW_LAUNCH_CHECK("plan_count_kernel");
-  if (R == 0) return QW_OK;
-  plan_valid_total_kernel<<<1, 64, 0, stream>>>(route_off, counts, e, valid);
-  QW_LAUNCH_CHECK("plan_valid_total_kernel");
-  const unsigned nb = static_cast<unsigned>(ceil_div(R, 256));
-  plan_bucket_kernel<<<nb, 256, 0, stream>>>(top_idx, top_w, R, e, cursor, bkey, bexp);
-  QW_LAUNCH_CHECK("plan_bucket_kernel");
-  plan_mark_invalid_kernel<<<nb, 256, 0, stream>>>(top_idx, R, e, route_slot);
-  QW_LAUNCH_CHECK("plan_mark_invalid_kernel");
-  plan_rank_kernel<<<nb, 256, 0, stream>>>(bkey, bexp, route_off, counts, kept_offsets, drop_off, valid, top_w, R,
-                                           static_cast<int>(K), cap, slot_token, slot_weight, route_slot,
-                                           dropped_token, dropped_expert);
-  QW_LAUNCH_CHECK("plan_rank_kernel");
+  plan_place_kernel<<<e, kPlanThreads, 0, stream>>>(top_idx, top_w, R, e, static_cast<int>(K), cap, counts,
+                                                    kept_counts, kept_offsets, totals, slot_token, slot_weight,
+                                                    route_slot, dropped_token, dropped_expert, spill);
+  QW_LAUNCH_CHECK("plan_place_kernel");
   return QW_OK;
 }
 

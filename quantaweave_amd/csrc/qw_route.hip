@@ -43,27 +43,33 @@ __device__ __forceinline__ uint32_t sortable_key(float f) {
 }
 
 // ---------------------------------------------------------------------------
-// logits[t, e] = (x[t, :] . W[e, :]) / temperature, fp32 accumulation.
-// 64x64 output tile per 256-thread block, K staged through LDS in slices of 16.
+// Router GEMM, split over K: partial[s, t, e] = sum over the s-th K range of
+// x[t, k] * W[e, k] (fp32 accumulation).  The top-k kernel adds the partials
+// in ascending s, so the logits do not depend on scheduling.
+//
+// General kernel (any dtype pair, any d): 64x64 output tile per 256-thread
+// block, K staged through LDS in slices of 16, fp32 FMA.
 // ---------------------------------------------------------------------------
 template <int XDT, int WDT>
 __global__ __launch_bounds__(256) void router_logits_kernel(const void* __restrict__ x, int64_t x_stride,
                                                             const void* __restrict__ w, int T, int D, int E,
-                                                            float temperature, float* __restrict__ logits) {
+                                                            int k_len, float* __restrict__ partial) {
   constexpr int TM = 64, TN = 64, TK = 16;
   __shared__ float xs[TK][TM + 4];
   __shared__ float ws[TK][TN + 4];
   const int tid = threadIdx.x;
-  const int t0 = blockIdx.x * TM, e0 = blockIdx.y * TN;
+  const int t0 = blockIdx.x * TM, e0 = blockIdx.z * TN;
+  const int k_begin = blockIdx.y * k_len, k_end = min(D, k_begin + k_len);
+  float* out = partial + static_cast<int64_t>(blockIdx.y) * T * E;
   const int ty = tid / 16, tx = tid % 16;
   float acc[4][4] = {};
-  for (int k0 = 0; k0 < D; k0 += TK) {
+  for (int k0 = k_begin; k0 < k_end; k0 += TK) {
     for (int i = tid; i < TM * TK; i += 256) {
       const int m = i / TK, kk = i % TK;
       const int t = t0 + m, k = k0 + kk;
-      xs[kk][m] = (t < T && k < D) ? load_act<XDT>(x, static_cast<int64_t>(t) * x_stride + k) : 0.0f;
+      xs[kk][m] = (t < T && k < k_end) ? load_act<XDT>(x, static_cast<int64_t>(t) * x_stride + k) : 0.0f;
       const int e = e0 + m;
-      ws[kk][m] = (e < E && k < D) ? load_act<WDT>(w, static_cast<int64_t>(e) * D + k) : 0.0f;
+      ws[kk][m] = (e < E && k < k_end) ? load_act<WDT>(w, static_cast<int64_t>(e) * D + k) : 0.0f;
     }
     __syncthreads();
 #pragma unroll
@@ -87,7 +93,89 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const void* __restri
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int e = e0 + tx * 4 + j;
-      if (e < E) logits[static_cast<int64_t>(t) * E + e] = acc[i][j] / temperature;
+      if (e < E) out[static_cast<int64_t>(t) * E + e] = acc[i][j];
+    }
+  }
+}
+
+// bf16 x bf16 router GEMM on MFMA (products of bf16 values are exact in fp32,
+// so this is the same fp32 dot product up to accumulation order).  Tile: 64
+// tokens x 64 experts per 256-thread block; wave w owns tokens w*16..w*16+15.
+typedef __bf16 rbf16x8 __attribute__((ext_vector_type(8)));
+typedef float rf32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void router_mfma_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
+                                                          const uint16_t* __restrict__ w, int T, int D, int E,
+                                                          int k_len, float* __restrict__ partial) {
+  constexpr int BK = 64, LROW = BK + 8;
+  __shared__ __attribute__((aligned(16))) uint16_t As[64 * LROW];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[64 * LROW];
+  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const int t0 = blockIdx.x * 64, e0 = blockIdx.z * 64;
+  const int k_begin = blockIdx.y * k_len, k_end = min(D, k_begin + k_len);
+  float* out = partial + static_cast<int64_t>(blockIdx.y) * T * E;
+  // 64 rows x 8 pieces of 16 bytes per slice and operand: 2 pieces per thread
+  const uint16_t* a_src[2];
+  const uint16_t* b_src[2];
+  int dst[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = tid + i * 256, row = c / 8, ch = c % 8;
+    dst[i] = row * LROW + ch * 8;
+    a_src[i] = (t0 + row < T) ? x + static_cast<int64_t>(t0 + row) * x_stride + ch * 8 : nullptr;
+    b_src[i] = (e0 + row < E) ? w + static_cast<int64_t>(e0 + row) * D + ch * 8 : nullptr;
+  }
+  uint4 ra[2], rb[2];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      ra[i] = a_src[i] ? *reinterpret_cast<const uint4*>(a_src[i] + k0) : make_uint4(0, 0, 0, 0);
+      rb[i] = b_src[i] ? *reinterpret_cast<const uint4*>(b_src[i] + k0) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      *reinterpret_cast<uint4*>(&As[dst[i]]) = ra[i];
+      *reinterpret_cast<uint4*>(&Bs[dst[i]]) = rb[i];
+    }
+  };
+  rf32x4 acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = rf32x4{0.f, 0.f, 0.f, 0.f};
+  const int l16 = lane % 16, kq = (lane / 16) * 8;
+  if (k_begin < k_end) {  // an empty split still writes its (zero) partial
+    load(k_begin);
+    stash();
+  }
+  __syncthreads();
+  for (int k0 = k_begin; k0 < k_end; k0 += BK) {
+    const bool more = k0 + BK < k_end;
+    if (more) load(k0 + BK);
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      const rbf16x8 afr = *reinterpret_cast<const rbf16x8*>(&As[(wave * 16 + l16) * LROW + ks * 32 + kq]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const rbf16x8 bfr = *reinterpret_cast<const rbf16x8*>(&Bs[(t * 16 + l16) * LROW + ks * 32 + kq]);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr, bfr, acc[t], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+    if (more) {
+      stash();
+      __syncthreads();
+    }
+  }
+  const int rq = (lane / 16) * 4;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int e = e0 + t * 16 + l16;
+    if (e >= E) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tok = t0 + wave * 16 + rq + r;
+      if (tok < T) out[static_cast<int64_t>(tok) * E + e] = acc[t][r];
     }
   }
 }
@@ -102,20 +190,38 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const void* __restri
 //          (or L_e + bias_e when a bias is given)
 //   w_j = p_{idx_j} / (((p_{idx_0} + p_{idx_1}) + p_{idx_2}) + ...)
 // ---------------------------------------------------------------------------
+//
+// With `partial` != NULL the logits are first assembled from the router GEMM's
+// split-K partials: L = ((p_0 + p_1) + ... + p_{S-1}) / temperature, and
+// written to `logits`.
 template <int EPL>
-__global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits, int T, int E, int K,
-                                                         const float* __restrict__ bias, float* __restrict__ probs,
-                                                         int32_t* __restrict__ top_idx, float* __restrict__ top_w) {
+__global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ partial, int splits,
+                                                         float temperature, float* __restrict__ logits, int T, int E,
+                                                         int K, const float* __restrict__ bias,
+                                                         float* __restrict__ probs, int32_t* __restrict__ top_idx,
+                                                         float* __restrict__ top_w) {
   const int lane = threadIdx.x % kWave;
   const int t = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
   if (t >= T) return;
-  const float* row = logits + static_cast<int64_t>(t) * E;
   float l[EPL], p[EPL];
   float m = -__builtin_inff();
 #pragma unroll
   for (int c = 0; c < EPL; ++c) {
     const int e = lane + c * kWave;
-    l[c] = (e < E) ? row[e] : -__builtin_inff();
+    if (e < E) {
+      const int64_t i = static_cast<int64_t>(t) * E + e;
+      if (partial != nullptr) {
+        float v = partial[i];
+        for (int sp = 1; sp < splits; ++sp) v += partial[static_cast<int64_t>(sp) * T * E + i];
+        v = v / temperature;
+        logits[i] = v;
+        l[c] = v;
+      } else {
+        l[c] = logits[i];
+      }
+    } else {
+      l[c] = -__builtin_inff();
+    }
     m = fmaxf(m, l[c]);
   }
   // fmaxf drops NaN; a NaN logit must poison the row as it does in torch.
@@ -187,17 +293,21 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
   }
 }
 
-static int launch_topk(const float* logits, int T, int E, int K, const float* bias, float* probs, int32_t* top_idx,
-                       float* top_w, hipStream_t stream) {
+static int launch_topk(const float* partial, int splits, float temperature, float* logits, int T, int E, int K,
+                       const float* bias, float* probs, int32_t* top_idx, float* top_w, hipStream_t stream) {
   const int waves_per_block = 4;
   const dim3 grid(static_cast<unsigned>(ceil_div(T, waves_per_block)));
   const dim3 block(waves_per_block * kWave);
   const int epl = static_cast<int>(ceil_div(E, kWave));
-  if (epl <= 1) route_topk_kernel<1><<<grid, block, 0, stream>>>(logits, T, E, K, bias, probs, top_idx, top_w);
-  else if (epl <= 2) route_topk_kernel<2><<<grid, block, 0, stream>>>(logits, T, E, K, bias, probs, top_idx, top_w);
-  else if (epl <= 4) route_topk_kernel<4><<<grid, block, 0, stream>>>(logits, T, E, K, bias, probs, top_idx, top_w);
-  else if (epl <= 8) route_topk_kernel<8><<<grid, block, 0, stream>>>(logits, T, E, K, bias, probs, top_idx, top_w);
-  else route_topk_kernel<16><<<grid, block, 0, stream>>>(logits, T, E, K, bias, probs, top_idx, top_w);
+#define QW_TK(N)                                                                                               \
+  route_topk_kernel<N><<<grid, block, 0, stream>>>(partial, splits, temperature, logits, T, E, K, bias, probs, \
+                                                   top_idx, top_w)
+  if (epl <= 1) QW_TK(1);
+  else if (epl <= 2) QW_TK(2);
+  else if (epl <= 4) QW_TK(4);
+  else if (epl <= 8) QW_TK(8);
+  else QW_TK(16);
+#undef QW_TK
   QW_LAUNCH_CHECK("route_topk_kernel");
   return QW_OK;
 }
@@ -217,13 +327,26 @@ int route_from_logits(const float* logits, int64_t T, int64_t E, int64_t K, cons
   if (st) return st;
   if (T == 0) return QW_OK;
   QW_REQUIRE(logits && top_idx && top_w, "logits, top_idx and top_w are required");
-  return launch_topk(logits, static_cast<int>(T), static_cast<int>(E), static_cast<int>(K), bias, probs, top_idx,
-                     top_w, stream);
+  return launch_topk(nullptr, 0, 1.0f, const_cast<float*>(logits), static_cast<int>(T), static_cast<int>(E),
+                     static_cast<int>(K), bias, probs, top_idx, top_w, stream);
+}
+
+// Split count for the router GEMM: enough blocks to cover the chip, each
+// split a multiple of 64 long and at least 256 deep.
+int router_splits(int64_t T, int64_t D, int64_t E) {
+  const int64_t tiles = ceil_div(T, 64) * ceil_div(E, 64);
+  int64_t s = 1;
+  while (tiles * s < 512 && D / (s * 2) >= 256) s *= 2;
+  return static_cast<int>(s);
+}
+
+size_t route_workspace_bytes(int64_t T, int64_t D, int64_t E) {
+  return static_cast<size_t>(router_splits(T, D, E)) * T * E * sizeof(float);
 }
 
 int route(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int64_t T, int64_t D, int64_t E,
           int64_t K, float temperature, const float* bias, float* logits, float* probs, int32_t* top_idx,
-          float* top_w, hipStream_t stream) {
+          float* top_w, float* partial, size_t partial_bytes, hipStream_t stream) {
   int st = route_validate(T, E, K);
   if (st) return st;
   QW_REQUIRE(xdt == QW_F32 || xdt == QW_BF16, "router input dtype must be f32 or bf16");
@@ -233,17 +356,30 @@ int route(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int6
   QW_REQUIRE(temperature > 0.0f, "router_temperature must be positive");
   if (T == 0) return QW_OK;
   QW_REQUIRE(x && w && logits && top_idx && top_w, "x, router_w, logits, top_idx and top_w are required");
-  const dim3 grid(static_cast<unsigned>(ceil_div(T, 64)), static_cast<unsigned>(ceil_div(E, 64)));
-  const int t = static_cast<int>(T), d = static_cast<int>(D), e = static_cast<int>(E);
+  const int splits = router_splits(T, D, E);
+  if (partial_bytes < static_cast<size_t>(splits) * T * E * sizeof(float) || !partial)
+    return set_error(QW_ERR_WORKSPACE, "router needs %zu bytes of partial sums", route_workspace_bytes(T, D, E));
+  int64_t k_len = ceil_div(D, splits);
+  k_len = ceil_div(k_len, 64) * 64;
+  const dim3 grid(static_cast<unsigned>(ceil_div(T, 64)), static_cast<unsigned>(splits),
+                  static_cast<unsigned>(ceil_div(E, 64)));
+  const int t = static_cast<int>(T), d = static_cast<int>(D), e = static_cast<int>(E), kl = static_cast<int>(k_len);
+  if (xdt == QW_BF16 && wdt == QW_BF16 && D % 64 == 0) {
+    router_mfma_kernel<<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(x), x_stride,
+                                                 static_cast<const uint16_t*>(w), t, d, e, kl, partial);
+    QW_LAUNCH_CHECK("router_mfma_kernel");
+  } else {
 #define QW_RL(XD, WD) \
-  router_logits_kernel<XD, WD><<<grid, 256, 0, stream>>>(x, x_stride, w, t, d, e, temperature, logits)
-  if (xdt == QW_F32 && wdt == QW_F32) QW_RL(QW_F32, QW_F32);
-  else if (xdt == QW_F32) QW_RL(QW_F32, QW_BF16);
-  else if (wdt == QW_F32) QW_RL(QW_BF16, QW_F32);
-  else QW_RL(QW_BF16, QW_BF16);
+  router_logits_kernel<XD, WD><<<grid, 256, 0, stream>>>(x, x_stride, w, t, d, e, kl, partial)
+    if (xdt == QW_F32 && wdt == QW_F32) QW_RL(QW_F32, QW_F32);
+    else if (xdt == QW_F32) QW_RL(QW_F32, QW_BF16);
+    else if (wdt == QW_F32) QW_RL(QW_BF16, QW_F32);
+    else QW_RL(QW_BF16, QW_BF16);
 #undef QW_RL
-  QW_LAUNCH_CHECK("router_logits_kernel");
-  return launch_topk(logits, t, e, static_cast<int>(K), bias, probs, top_idx, top_w, stream);
+    QW_LAUNCH_CHECK("router_logits_kernel");
+  }
+  return launch_topk(partial, splits, temperature, logits, t, e, static_cast<int>(K), bias, probs, top_idx, top_w,
+                     stream);
 }
 
 }  // namespace qw

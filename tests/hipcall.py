@@ -36,8 +36,10 @@ def route(x: torch.Tensor, router_w: torch.Tensor, k: int, temperature=1.0, bias
     probs = torch.empty(T, E, dtype=torch.float32, device="cuda")
     idx = torch.empty(T, k, dtype=torch.int32, device="cuda")
     w = torch.empty(T, k, dtype=torch.float32, device="cuda")
+    nb = _lib.load().qw_moe_route_workspace_bytes(T, D, E)
+    ws = _hip.workspace(nb, torch.device("cuda"))
     _lib.call("qw_moe_route", P(x), _hip.act_code(x, "x"), x.stride(0), P(router_w), _hip.act_code(router_w, "w"), T,
-              D, E, k, float(temperature), P(bias), P(logits), P(probs), P(idx), P(w), s())
+              D, E, k, float(temperature), P(bias), P(logits), P(probs), P(idx), P(w), P(ws), nb, s())
     torch.cuda.synchronize()
     return logits, probs, idx, w
 
