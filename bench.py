@@ -34,6 +34,8 @@ def parse():
     ap.add_argument("--workload", default=None)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only-headline", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (calibrates HBM byte counters)")
     return ap.parse_args()
 
 
@@ -192,6 +194,16 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm device", file=sys.stderr)
         sys.exit(1)
+    if args.copy_probe_mib:
+        n = args.copy_probe_mib * (1 << 20)
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n, "launches": 3}), flush=True)
+        return
     head = args.workload or W.HEADLINE
     results = {head: measure(head, args.steps, args.warmup)}
     if not args.only_headline:

@@ -112,4 +112,13 @@ __device__ __forceinline__ int wave_sum_i(int v) {
 
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also waits for every
+// outstanding global load of the wave (vmcnt(0)); this one lets global loads
+// stay in flight across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 }  // namespace qw

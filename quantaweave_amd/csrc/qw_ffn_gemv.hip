@@ -61,16 +61,12 @@ __device__ __forceinline__ float dot2_f16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(gf16x2, a), __builtin_bit_cast(gf16x2, b), c, false);
 }
 
-// Position (within a U4 chunk of 32 columns) of the two columns of pair p
-// (0..15) in the order the nibble conversion emits them: for dword i, pairs
-// (8i, 8i+2), (8i+4, 8i+6), (8i+1, 8i+3), (8i+5, 8i+7).
-__device__ __forceinline__ int u4_pair_col(int p, int which) {
-  const int i = p / 4, j = p % 4;
-  const int base = 8 * i + ((j & 2) ? 1 : 0) + ((j & 1) ? 4 : 0);
-  return base + 2 * which;
+// Makes the compiler treat v as produced here: keeps the weight conversion from
+// being hoisted above the activation staging (which would make the staging
+// wait for the whole weight stream).
+__device__ __forceinline__ void opaque(uint4& v) {
+  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
 }
-// I8 chunk of 16 columns: dword i holds cols 4i..4i+3; pairs (4i, 4i+1), (4i+2, 4i+3).
-__device__ __forceinline__ int i8_pair_col(int p, int which) { return 2 * p + which; }
 
 // Converts one 16-byte weight chunk into the operand pairs of the dot products.
 template <int WF>
@@ -118,7 +114,7 @@ __device__ __forceinline__ float chunk_dot(const uint32_t* cw, const uint32_t* x
 }
 
 // GATEUP: unit = hidden column (gate row + up row); DOWN: unit = output row.
-template <int WF, bool GATEUP, int UNITS, int CPL>
+template <int WF, bool GATEUP, int UNITS, int CPL, int XPIECES_MAX>
 __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
     int max_rows, WView wa, WView wb, int K, int n_out, const float* __restrict__ row_weight,
@@ -137,7 +133,8 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
   const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
   const int unit0 = (blockIdx.x * GV_WAVES + wave) * UNITS;
 
-  // weight row pointers of this wave's units (nullptr: past the end)
+  // weight row pointers of this wave's units; rows past the end are clamped to
+  // the last row (loaded, never written) so that every load is unconditional
   const uint8_t* wrow[UNITS][ROWS];
   const float* srow[UNITS][ROWS];
 #pragma unroll
@@ -145,15 +142,39 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
 #pragma unroll
     for (int rr = 0; rr < ROWS; ++rr) {
       const WView& v = rr == 0 ? wa : wb;
-      const int n = unit0 + u;
+      const int n = min(unit0 + u, n_out - 1);
       const int64_t esz = WF == QW_BF16 ? 2 : 1;
-      wrow[u][rr] = n < n_out ? static_cast<const uint8_t*>(v.w) + (e * v.expert_elems + n * v.row_stride) * esz
-                              : nullptr;
-      srow[u][rr] = (WF != QW_BF16 && n < n_out) ? v.scales + e * v.expert_scales + n * v.groups : nullptr;
+      wrow[u][rr] = static_cast<const uint8_t*>(v.w) + (e * v.expert_elems + n * v.row_stride) * esz;
+      srow[u][rr] = WF != QW_BF16 ? v.scales + e * v.expert_scales + n * v.groups : nullptr;
     }
-  const int group = wa.group;
+  const int cpg = wa.group / CW;  // chunks per quantisation group
 
-  // ---- stream this wave's weight rows once (issued before the activations are staged) ----
+  // Activation pieces (8 columns = 16 bytes) of one pass, loaded into
+  // registers before the weight stream is issued so that waiting for them does
+  // not wait for the weights (loads complete in issue order).
+  constexpr int XPT = (GV_MAXM * XPIECES_MAX + GV_WAVES * 64 - 1) / (GV_WAVES * 64);
+  const int KP = K / 8;  // pieces per activation row
+  uint4 xr[XPT];
+  auto load_x = [&](int m0, int M) {
+    // source rows of the pass first (uniform loads, one wait), then the pieces
+    int64_t src[GV_MAXM];
+#pragma unroll
+    for (int m = 0; m < GV_MAXM; ++m) src[m] = m < M ? (row_index ? row_index[m0 + m] : (m0 + m)) : 0;
+    // unconditional loads (indices clamped into the pass): a load under a branch
+    // makes the compiler wait for it inside the branch
+#pragma unroll
+    for (int j = 0; j < XPT; ++j) {
+      const int i = min(tid + j * GV_WAVES * 64, M * KP - 1);
+      const int m = i / KP, q = i % KP;
+      int64_t row = src[0];
+#pragma unroll
+      for (int t = 1; t < GV_MAXM; ++t) row = (m == t) ? src[t] : row;
+      xr[j] = reinterpret_cast<const uint4*>(x + row * K)[q];
+    }
+  };
+  load_x(r_lo, min(GV_MAXM, r_hi - r_lo));
+
+  // ---- this wave's weight rows, streamed once for all passes ----
   uint4 wv[UNITS][ROWS][CPL];
   float sv[UNITS][ROWS][CPL];
 #pragma unroll
@@ -162,49 +183,72 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
     for (int rr = 0; rr < ROWS; ++rr)
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
-        const int c = lane + 64 * j;
-        const bool ok = wrow[u][rr] != nullptr && c < KC;
-        wv[u][rr][j] = ok ? *reinterpret_cast<const uint4*>(wrow[u][rr] + 16 * c) : make_uint4(0, 0, 0, 0);
-        if constexpr (WF != QW_BF16) sv[u][rr][j] = ok ? srow[u][rr][(c * CW) / group] : 0.0f;
+        const int c = min(lane + 64 * j, KC - 1);  // chunks past the row end are skipped in the math
+        wv[u][rr][j] = *reinterpret_cast<const uint4*>(wrow[u][rr] + 16 * c);
+        if constexpr (WF != QW_BF16) sv[u][rr][j] = srow[u][rr][cpg == 1 ? c : c / cpg];
       }
 
   for (int m0 = r_lo; m0 < r_hi; m0 += GV_MAXM) {
     const int M = min(GV_MAXM, r_hi - m0);
-    // ---- stage activations: pairs in conversion order ----
+    if (m0 != r_lo) load_x(m0, M);
     if constexpr (WF == QW_I8) {
       // power-of-two scale per route so the largest |x| lands in [2^14, 2^15)
-      for (int m = wave; m < M; m += GV_WAVES) {
-        const int64_t src = row_index ? row_index[m0 + m] : (m0 + m);
-        float amax = 0.0f;
-        for (int k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(bf16_to_f32(x[src * K + k])));
-        amax = wave_max(amax);
-        if (lane == 0) {
-          int ex = 0;
-          frexpf(amax, &ex);  // amax in [2^(ex-1), 2^ex)
-          xscale[m] = amax > 0.0f ? ldexpf(1.0f, 15 - ex) : 1.0f;
+      uint32_t* amax_bits = reinterpret_cast<uint32_t*>(xscale);
+      if (tid < GV_MAXM) amax_bits[tid] = 0u;
+      lds_barrier();
+#pragma unroll
+      for (int j = 0; j < XPT; ++j) {
+        const int i = tid + j * GV_WAVES * 64;
+        if (i < M * KP) {
+          const uint32_t v[4] = {xr[j].x, xr[j].y, xr[j].z, xr[j].w};
+          float a = 0.0f;
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            a = fmaxf(a, fmaxf(fabsf(__uint_as_float(v[t] << 16)), fabsf(__uint_as_float(v[t] & 0xffff0000u))));
+          atomicMax(&amax_bits[i / KP], __float_as_uint(a));  // non-negative floats order as integers
         }
       }
-      __syncthreads();
+      lds_barrier();
+      if (tid < M) {
+        const float amax = __uint_as_float(amax_bits[tid]);
+        int ex = 0;
+        frexpf(amax, &ex);  // amax in [2^(ex-1), 2^ex)
+        xscale[tid] = amax > 0.0f ? ldexpf(1.0f, 15 - ex) : 1.0f;
+      }
+      lds_barrier();
     }
-    for (int i = tid; i < M * KC * DW; i += blockDim.x) {
-      const int m = i / (KC * DW), rem = i % (KC * DW), c = rem / DW, p = rem % DW;
-      const int64_t src = row_index ? row_index[m0 + m] : (m0 + m);
-      const uint16_t* xr = x + src * K + c * CW;
-      uint32_t v;
+    // ---- stage activations in LDS: pairs in the order the conversion emits them ----
+#pragma unroll
+    for (int j = 0; j < XPT; ++j) {
+      const int i = tid + j * GV_WAVES * 64;
+      if (i >= M * KP) continue;
+      const int m = i / KP;
+      const uint32_t v[4] = {xr[j].x, xr[j].y, xr[j].z, xr[j].w};  // v[t] = cols (2t, 2t+1) of the piece
+      uint4 o;
       if constexpr (WF == QW_U4) {
-        v = static_cast<uint32_t>(xr[u4_pair_col(p, 0)]) | (static_cast<uint32_t>(xr[u4_pair_col(p, 1)]) << 16);
+        // piece i is dword (i % 4) of a 32-column chunk: pairs (0,2), (4,6), (1,3), (5,7)
+        o.x = __builtin_amdgcn_perm(v[1], v[0], 0x05040100u);
+        o.y = __builtin_amdgcn_perm(v[3], v[2], 0x05040100u);
+        o.z = __builtin_amdgcn_perm(v[1], v[0], 0x07060302u);
+        o.w = __builtin_amdgcn_perm(v[3], v[2], 0x07060302u);
       } else if constexpr (WF == QW_I8) {
         const float sc = xscale[m];
-        const _Float16 a = static_cast<_Float16>(bf16_to_f32(xr[i8_pair_col(p, 0)]) * sc);
-        const _Float16 b = static_cast<_Float16>(bf16_to_f32(xr[i8_pair_col(p, 1)]) * sc);
-        v = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
-            (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+        uint32_t h[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const _Float16 a = static_cast<_Float16>(__uint_as_float(v[t] << 16) * sc);
+          const _Float16 b = static_cast<_Float16>(__uint_as_float(v[t] & 0xffff0000u) * sc);
+          h[t] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
+                 (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+        }
+        o = make_uint4(h[0], h[1], h[2], h[3]);
       } else {
-        v = static_cast<uint32_t>(xr[2 * p]) | (static_cast<uint32_t>(xr[2 * p + 1]) << 16);
+        o = xr[j];
       }
-      xs[i] = v;
+      // staged layout [m][chunk][DW dwords]: 8 columns are 4 dwords in every format
+      reinterpret_cast<uint4*>(xs)[i] = o;
     }
-    __syncthreads();
+    lds_barrier();
     if constexpr (WF != QW_BF16) {
       // per-chunk activation sums (of the values as staged) for the bias correction
       for (int i = tid; i < M * KC; i += blockDim.x) {
@@ -217,7 +261,7 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
         }
         xsum[i] = s;
       }
-      __syncthreads();
+      lds_barrier();
     }
 
     float part[UNITS][ROWS][GV_MAXM];
@@ -227,6 +271,12 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
       for (int rr = 0; rr < ROWS; ++rr)
 #pragma unroll
         for (int m = 0; m < GV_MAXM; ++m) part[u][rr][m] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < UNITS; ++u)
+#pragma unroll
+      for (int rr = 0; rr < ROWS; ++rr)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) opaque(wv[u][rr][j]);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       const int c = lane + 64 * j;
@@ -275,7 +325,7 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
 }
 
@@ -287,7 +337,8 @@ int launch_one(const FfnArgs& a, const WView& wa, const WView& wb, const void* x
   const size_t lds = static_cast<size_t>(GV_MAXM) * KC * (CW / 2) * 4 + static_cast<size_t>(GV_MAXM) * KC * 4 +
                      GV_MAXM * 4;
   const dim3 grid(static_cast<unsigned>(ceil_div(n_out, GV_WAVES * UNITS)), static_cast<unsigned>(a.experts));
-  ffn_gemv_kernel<WF, GATEUP, UNITS, CPL><<<grid, GV_WAVES * 64, lds, stream>>>(
+  // largest activation row the register staging covers: K <= 64*CPL chunks
+  ffn_gemv_kernel<WF, GATEUP, UNITS, CPL, 64 * CPL * CW / 8><<<grid, GV_WAVES * 64, lds, stream>>>(
       static_cast<const uint16_t*>(x), row_index, a.offsets, static_cast<int>(a.max_rows), wa, wb, K, n_out,
       row_weight, static_cast<uint16_t*>(out));
   QW_LAUNCH_CHECK(GATEUP ? "ffn_gemv_kernel<gateup>" : "ffn_gemv_kernel<down>");

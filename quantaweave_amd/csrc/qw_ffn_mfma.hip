@@ -10,16 +10,32 @@
 //                 expert rather than once per small row tile;
 //   column tile : 256 weight rows — GATEUP: 128 gate + 128 up rows (128 hidden
 //                 columns), DOWN: 256 output columns.
-// K is staged through LDS in slices of 64 with the next slice prefetched into
-// registers while the MFMAs consume the current one.  Waves form a 2 x 4 grid:
-// wave (wm, wn) computes row sub-tiles wm, wm+2, ... (16 rows each, skipped
-// when past the expert's row count) against its 64 weight rows (GATEUP: 32 gate
-// rows and the matching 32 up rows, so SiLU(g)*u is formed in registers).
+//
+// Operands move HBM/L2 -> LDS with global_load_lds_dwordx4 (no register
+// staging) in K-slices of 32 through two rings: the weight slices (the HBM
+// stream) are requested MF_BST-1 slices ahead, the activation slices (L2
+// resident) MF_AST-1 ahead, so ~80 KiB of weights per CU stay in flight while
+// the MFMAs run.  One LDS barrier per slice.  Loads complete in issue order
+// and every wave issues the same loads per slice (rows past the end are
+// clamped to a valid row, their results never stored), so waiting for the
+// later-issued activation slice with a fixed `s_waitcnt vmcnt(n)` also covers
+// its weight slice.
+//
+// LDS rows are 64 bytes (32 bf16); the four 16-byte pieces of row r are stored
+// XOR-swizzled by ((r >> 1) & 3) so the 16-row fragment reads of the MFMAs
+// hit distinct banks.
+//
+// Waves form a 2 x 4 grid: wave (wm, wn) computes row sub-tiles wm, wm+2, ...
+// (16 rows each, skipped past the expert's row count) against its 64 weight
+// rows (GATEUP: 32 gate rows and the matching 32 up rows, so SiLU(g)*u is
+// formed in registers).  The MFMA takes the weights as its A operand, so a
+// lane ends up holding 4 consecutive output columns of one row and stores them
+// with one 8-byte write.
 //
 // Workgroup -> tile order is XCD-aware: workgroups are dispatched round-robin
 // over the 8 XCDs, so block b runs on XCD b%8; all tiles of one expert are
 // given to one XCD and enumerated column-fastest, which keeps the expert's
-// activation rows resident in that XCD's L2 while its weight tiles stream.
+// activation rows (and a second row chunk's weights) in that XCD's L2.
 #include "qw_ffn.h"
 
 namespace qw {
@@ -28,12 +44,36 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int MF_BK = 64;             // K slice
-constexpr int MF_LDS_ROW = MF_BK + 8;  // bf16 per LDS row (16-byte pad: conflict-free 128-bit reads)
-constexpr int MF_NB = 256;            // weight rows per column tile
+constexpr int MF_BK = 32;       // K slice (one MFMA K step)
+constexpr int MF_ROWB = 64;     // bytes per LDS row (32 bf16, no padding: swizzled)
+constexpr int MF_NB = 256;      // weight rows per column tile
 constexpr int MF_THREADS = 512;
+constexpr int MF_WAVES = 8;
+constexpr int MF_NT = 4;        // 16-column MFMA tiles per wave
+constexpr int MF_AST = 3;       // activation ring stages
+constexpr int MF_BST = 6;       // weight ring stages
 constexpr int kXcds = 8;
+
+// s_waitcnt immediate waiting for vmcnt <= n only (expcnt, lgkmcnt left at max).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
+}
+
+__device__ __forceinline__ int swz(int row, int piece) { return piece ^ ((row >> 1) & 3); }
+
+// Barrier for the LDS ring: the slice's loads were already waited for with an
+// explicit vmcnt, so no fence is needed (a workgroup fence would wait for every
+// load still in flight, including the slices requested ahead).  The empty asm
+// statements keep the compiler from moving LDS accesses across the barrier.
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 template <bool GATEUP, int SUBT>
 __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
@@ -41,13 +81,19 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
     int max_rows, const uint16_t* __restrict__ wa, const uint16_t* __restrict__ wb, int64_t w_expert_stride,
     int n_w, int K, const float* __restrict__ row_weight, uint16_t* __restrict__ out, int n_out, int n_tiles,
     int m_chunks, int experts) {
-  constexpr int MCH = 32 * SUBT;                       // rows per chunk
-  constexpr int A_CHUNKS = MCH * (MF_BK / 8);          // 16-byte pieces of the A slice
-  constexpr int A_PER = (A_CHUNKS + MF_THREADS - 1) / MF_THREADS;
-  constexpr int B_CHUNKS = MF_NB * (MF_BK / 8);
-  constexpr int B_PER = B_CHUNKS / MF_THREADS;
-  __shared__ __attribute__((aligned(16))) uint16_t As[MCH * MF_LDS_ROW];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[MF_NB * MF_LDS_ROW];
+  constexpr int MCH = 32 * SUBT;                 // rows per chunk
+  constexpr int AG = MCH / 16;                   // 16-row load groups of the A slice
+  constexpr int BG = MF_NB / 16;                 // ... of the B slice
+  constexpr int A_BYTES = MCH * MF_ROWB, B_BYTES = MF_NB * MF_ROWB;
+  // activation stage + 1 KiB that receives the padding loads of waves with one
+  // A group fewer (every wave issues the same number of loads per slice)
+  constexpr int A_STAGE = A_BYTES + 1024;
+  constexpr int AL_MAX = (AG + MF_WAVES - 1) / MF_WAVES;  // A groups per wave (upper bound)
+  constexpr int BL = BG / MF_WAVES;
+  static_assert(BG % MF_WAVES == 0, "B groups per wave");
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  char* const a_ring = smem;
+  char* const b_ring = smem + MF_AST * A_STAGE;
 
   // ---- tile of this workgroup (XCD-aware enumeration) ----
   const int b = blockIdx.x;
@@ -65,35 +111,28 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
 
   const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
   const int wm = wave / 4, wn = wave % 4;
-  // weight rows of this column tile
   const int n0 = nt * (GATEUP ? MF_NB / 2 : MF_NB);
   const uint16_t* wa_e = wa + static_cast<int64_t>(e) * w_expert_stride;
   const uint16_t* wb_e = wb + static_cast<int64_t>(e) * w_expert_stride;
 
-  // ---- per-thread global source pointers (constant over K) ----
-  const uint16_t* a_src[A_PER];
-  int a_dst[A_PER];
+  // ---- per-lane global sources of this wave's load groups (constant over K) ----
+  // lane i of a group writes LDS row (16g + i/4), physical piece i%4, which holds
+  // logical piece swz(row, i%4) of that row.
+  const int lrow = lane / 4, lpiece = lane % 4;
+  const uint16_t* a_src[AL_MAX];
 #pragma unroll
-  for (int i = 0; i < A_PER; ++i) {
-    const int c = tid + i * MF_THREADS;
-    const int row = c / (MF_BK / 8), ch = c % (MF_BK / 8);
-    a_src[i] = nullptr;
-    a_dst[i] = -1;
-    if (c < A_CHUNKS) {
-      a_dst[i] = row * MF_LDS_ROW + ch * 8;
-      if (row < count) {
-        const int64_t src = row_index ? row_index[r0 + row] : (r0 + row);
-        a_src[i] = x + src * K + ch * 8;
-      }
-    }
+  for (int q = 0; q < AL_MAX; ++q) {
+    const int g = wave + q * MF_WAVES;
+    const int row = 16 * g + lrow;
+    const int rr = min(row, count - 1);  // clamp: rows past the end load a valid row
+    const int64_t src = row_index ? row_index[r0 + rr] : (r0 + rr);
+    a_src[q] = x + src * K + swz(row, lpiece) * 8;
   }
-  const uint16_t* b_src[B_PER];
-  int b_dst[B_PER];
+  const uint16_t* b_src[BL];
 #pragma unroll
-  for (int i = 0; i < B_PER; ++i) {
-    const int c = tid + i * MF_THREADS;
-    const int row = c / (MF_BK / 8), ch = c % (MF_BK / 8);
-    b_dst[i] = row * MF_LDS_ROW + ch * 8;
+  for (int q = 0; q < BL; ++q) {
+    const int g = wave + q * MF_WAVES;
+    const int row = 16 * g + lrow;
     int wrow;
     const uint16_t* base;
     if (GATEUP) {
@@ -103,105 +142,129 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
       wrow = n0 + row;
       base = wa_e;
     }
-    b_src[i] = wrow < n_w ? base + static_cast<int64_t>(wrow) * K + ch * 8 : nullptr;
+    wrow = min(wrow, n_w - 1);
+    b_src[q] = base + static_cast<int64_t>(wrow) * K + swz(row, lpiece) * 8;
   }
-
-  uint4 ra[A_PER], rb[B_PER];
-  auto load = [&](int k0) {
+  // waves whose last A group is past AG still issue that load (into the stage's
+  // padding area) so that all waves issue AL_MAX loads per activation slice
+  auto issue_a = [&](int kt) {
+    char* st = a_ring + (kt % MF_AST) * A_STAGE;
+    const int k0 = kt * MF_BK;
 #pragma unroll
-    for (int i = 0; i < A_PER; ++i)
-      ra[i] = a_src[i] ? *reinterpret_cast<const uint4*>(a_src[i] + k0) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-    for (int i = 0; i < B_PER; ++i)
-      rb[i] = b_src[i] ? *reinterpret_cast<const uint4*>(b_src[i] + k0) : make_uint4(0, 0, 0, 0);
+    for (int q = 0; q < AL_MAX; ++q) {
+      const int g = wave + q * MF_WAVES;
+      char* dst = g < AG ? st + g * 1024 : st + A_BYTES;
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(a_src[q] + k0), (lds_void*)dst, 16, 0, 0);
+    }
   };
-  auto stash = [&]() {
+  auto issue_b = [&](int kt) {
+    char* st = b_ring + (kt % MF_BST) * B_BYTES;
+    const int k0 = kt * MF_BK;
 #pragma unroll
-    for (int i = 0; i < A_PER; ++i)
-      if (a_dst[i] >= 0) *reinterpret_cast<uint4*>(&As[a_dst[i]]) = ra[i];
-#pragma unroll
-    for (int i = 0; i < B_PER; ++i) *reinterpret_cast<uint4*>(&Bs[b_dst[i]]) = rb[i];
+    for (int q = 0; q < BL; ++q) {
+      const int g = wave + q * MF_WAVES;
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(b_src[q] + k0), (lds_void*)(st + g * 1024), 16, 0,
+                                       0);
+    }
   };
 
-  f32x4 acc[SUBT][4];
+  f32x4 acc[SUBT][MF_NT];
 #pragma unroll
   for (int i = 0; i < SUBT; ++i)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < MF_NT; ++t) acc[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // B rows (in the LDS tile) of this wave's 4 MFMA column tiles
-  int brow[4];
+  // B rows (in the LDS tile) of this wave's MFMA column tiles; GATEUP: tiles
+  // 0..1 gate, 2..3 the matching up rows
+  int brow[MF_NT];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    if (GATEUP) brow[t] = (t < 2 ? 0 : MF_NB / 2) + wn * 32 + (t % 2) * 16;
+  for (int t = 0; t < MF_NT; ++t) {
+    if (GATEUP) brow[t] = (t < MF_NT / 2 ? 0 : MF_NB / 2) + wn * 32 + (t % (MF_NT / 2)) * 16;
     else brow[t] = wn * 64 + t * 16;
   }
-  const int l16 = lane % 16, kq = (lane / 16) * 8;
-  // row sub-tiles active in this chunk (wave-uniform)
-  const int active_sub = (count + 15) / 16;
-
-  load(0);
-  stash();
-  __syncthreads();
+  const int l16 = lane % 16, lq = lane / 16;
+  const int active_sub = (count + 15) / 16;  // row sub-tiles holding valid rows (wave-uniform)
   const int KT = K / MF_BK;
-  for (int kt = 0; kt < KT; ++kt) {
-    if (kt + 1 < KT) load((kt + 1) * MF_BK);
+
+  // Issue order (iteration i issues A(i+2) then B(i+5); the prologue plays
+  // iterations -5..-1): B0 B1 B2 A0 B3 A1 B4 | A2 B5 | A3 B6 | ...
+  // Slice kt is complete once A(kt) is, which was followed by B(kt+3), A(kt+1)
+  // and B(kt+4) (those that exist).
+  static_assert(MF_AST == 3 && MF_BST == 6, "issue schedule below assumes 3 + 6 stages");
 #pragma unroll
-    for (int ks = 0; ks < MF_BK / 32; ++ks) {
-      bf16x8 bfr[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        bfr[t] = *reinterpret_cast<const bf16x8*>(&Bs[(brow[t] + l16) * MF_LDS_ROW + ks * 32 + kq]);
-#pragma unroll
-      for (int i = 0; i < SUBT; ++i) {
-        const int s = wm + 2 * i;
-        if (s < active_sub) {
-          const bf16x8 afr = *reinterpret_cast<const bf16x8*>(&As[(s * 16 + l16) * MF_LDS_ROW + ks * 32 + kq]);
-#pragma unroll
-          for (int t = 0; t < 4; ++t) acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr, bfr[t], acc[i][t], 0, 0, 0);
-        }
-      }
-    }
-    __syncthreads();
-    if (kt + 1 < KT) {
-      stash();
-      __syncthreads();
-    }
+  for (int i = -5; i < 0; ++i) {
+    if (i + 2 >= 0 && i + 2 < KT) issue_a(i + 2);
+    if (i + 5 < KT) issue_b(i + 5);
   }
 
-  // ---- epilogue: lane holds rows 4*(lane/16)+r of column lane%16 of each tile ----
-  const int rq = (lane / 16) * 4;
+  for (int kt = 0; kt < KT; ++kt) {
+    if (kt + 4 < KT) wait_vmcnt<AL_MAX + 2 * BL>();
+    else if (kt + 3 < KT) wait_vmcnt<AL_MAX + BL>();
+    else if (kt + 1 < KT) wait_vmcnt<AL_MAX>();
+    else wait_vmcnt<0>();
+    ring_barrier();  // slice kt visible to all waves; everyone is done with slice kt-1
+    const char* st_a = a_ring + (kt % MF_AST) * A_STAGE;
+    const char* st_b = b_ring + (kt % MF_BST) * B_BYTES;
+    bf16x8 wfr[MF_NT];
+#pragma unroll
+    for (int t = 0; t < MF_NT; ++t) {
+      const int row = brow[t] + l16;
+      wfr[t] = *reinterpret_cast<const bf16x8*>(st_b + row * MF_ROWB + swz(row, lq) * 16);
+    }
+    // All sub-tiles are computed, also those past the row count (their rows are
+    // clamped copies of a valid row and never stored): a per-sub-tile branch
+    // would keep the compiler from issuing the fragment reads ahead of the
+    // MFMAs and expose the LDS latency once per sub-tile.
+#pragma unroll
+    for (int i = 0; i < SUBT; ++i) {
+      const int row = (wm + 2 * i) * 16 + l16;
+      const bf16x8 xfr = *reinterpret_cast<const bf16x8*>(st_a + row * MF_ROWB + swz(row, lq) * 16);
+#pragma unroll
+      for (int t = 0; t < MF_NT; ++t)
+        acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[t], xfr, acc[i][t], 0, 0, 0);
+    }
+    // requests into the stages of slice kt-1 (every wave is past its reads of
+    // them: they all passed this iteration's barrier)
+    if (kt + 2 < KT) issue_a(kt + 2);
+    if (kt + 5 < KT) issue_b(kt + 5);
+  }
+
+  // ---- epilogue: lane holds row l16 of the sub-tile, columns 4*lq .. 4*lq+3 of each tile ----
 #pragma unroll
   for (int i = 0; i < SUBT; ++i) {
     const int s = wm + 2 * i;
     if (s >= active_sub) continue;
+    const int row = s * 16 + l16;
+    if (row >= count) continue;
+    const int64_t orow = static_cast<int64_t>(r0 + row) * n_out;
     if (GATEUP) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int col = n0 + wn * 32 + t * 16 + l16;
+      for (int t = 0; t < MF_NT / 2; ++t) {
+        const int col = n0 + wn * 32 + t * 16 + 4 * lq;
         if (col >= n_out) continue;
+        uint32_t pk[2];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = s * 16 + rq + r;
-          if (row < count) {
-            const float g = acc[i][t][r], u = acc[i][t + 2][r];
-            out[static_cast<int64_t>(r0 + row) * n_out + col] = f32_to_bf16(silu_f32(g) * u);
-          }
+        for (int h = 0; h < 2; ++h) {
+          const float a = silu_f32(acc[i][t][2 * h]) * acc[i][t + MF_NT / 2][2 * h];
+          const float c = silu_f32(acc[i][t][2 * h + 1]) * acc[i][t + MF_NT / 2][2 * h + 1];
+          pk[h] = f32_to_bf16(a) | (static_cast<uint32_t>(f32_to_bf16(c)) << 16);
         }
+        *reinterpret_cast<uint2*>(out + orow + col) = make_uint2(pk[0], pk[1]);
       }
     } else {
+      const float wgt = row_weight ? row_weight[r0 + row] : 1.0f;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int col = n0 + wn * 64 + t * 16 + l16;
+      for (int t = 0; t < MF_NT; ++t) {
+        const int col = n0 + wn * 64 + t * 16 + 4 * lq;
         if (col >= n_out) continue;
+        uint32_t pk[2];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = s * 16 + rq + r;
-          if (row < count) {
-            const float wgt = row_weight ? row_weight[r0 + row] : 1.0f;
-            out[static_cast<int64_t>(r0 + row) * n_out + col] = f32_to_bf16(round_to_bf16(acc[i][t][r]) * wgt);
-          }
+        for (int h = 0; h < 2; ++h) {
+          const float a = round_to_bf16(acc[i][t][2 * h]) * wgt;
+          const float c = round_to_bf16(acc[i][t][2 * h + 1]) * wgt;
+          pk[h] = f32_to_bf16(a) | (static_cast<uint32_t>(f32_to_bf16(c)) << 16);
         }
+        *reinterpret_cast<uint2*>(out + orow + col) = make_uint2(pk[0], pk[1]);
       }
     }
   }
@@ -215,7 +278,14 @@ int launch_t(const void* x, const int32_t* row_index, const int32_t* offsets, in
   const int m_chunks = static_cast<int>(ceil_div(rows_cap, 32 * SUBT));
   const int64_t grid = static_cast<int64_t>(ceil_div(experts, kXcds)) * kXcds * m_chunks * n_tiles;
   if (grid > INT32_MAX) return set_error(QW_ERR_UNSUPPORTED, "MFMA grid too large");
-  ffn_mfma_kernel<GATEUP, SUBT><<<static_cast<unsigned>(grid), MF_THREADS, 0, stream>>>(
+  const size_t lds = static_cast<size_t>(MF_AST) * (32 * SUBT * MF_ROWB + 1024) +
+                     static_cast<size_t>(MF_BST) * MF_NB * MF_ROWB;
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_mfma_kernel<GATEUP, SUBT>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     static_cast<int>(lds));
+  if (attr != hipSuccess)
+    return set_error(QW_ERR_HIP, "cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(attr));
+  ffn_mfma_kernel<GATEUP, SUBT><<<static_cast<unsigned>(grid), MF_THREADS, lds, stream>>>(
       static_cast<const uint16_t*>(x), row_index, offsets, max_rows, static_cast<const uint16_t*>(wa),
       static_cast<const uint16_t*>(wb), w_stride, n_w, K, row_weight, static_cast<uint16_t*>(out), n_out, n_tiles,
       m_chunks, experts);
@@ -253,7 +323,7 @@ int pick_subt(int64_t rows_cap) {
 int launch_ffn_mfma(const FfnArgs& a, hipStream_t stream, bool* handled) {
   *handled = false;
   if (a.act != QW_BF16 || a.wfmt != QW_BF16) return QW_OK;
-  if (a.d_model % MF_BK || a.d_ff % MF_BK) return QW_OK;
+  if (a.d_model % 64 || a.d_ff % 64) return QW_OK;
   if (a.avg_rows < 16) return QW_OK;  // decode-sized: weight streaming kernels
   const int64_t rows_cap = a.row_cap > 0 ? a.row_cap : a.max_rows;
   const int subt = pick_subt(rows_cap);
