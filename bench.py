@@ -91,7 +91,8 @@ def stage_calls(run):
 
     def experts():
         _lib.check(lib.qw_moe_experts(P(lay.x), run.act, P(slot_token), P(kept_offsets), E, D, F, max_rows,
-                                      *lay.weight_args(), P(slot_weight), P(y), P(exp_ws), exp_bytes, s), "experts")
+                                      min(run.capacity, R), *lay.weight_args(), P(slot_weight), P(y), P(exp_ws),
+                                      exp_bytes, s), "experts")
 
     def combine():
         _lib.check(lib.qw_moe_combine(P(y), run.act, P(route_slot), P(run.top_idx), T, K, D, P(run.out), s),

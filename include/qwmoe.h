@@ -121,11 +121,14 @@ int qw_moe_permute(const void* x, int dtype, int64_t d_model, const int32_t* slo
  *                      group_in (gate/up, over d_model) and group_ff (down)
  * act_dtype: QW_F32 or QW_BF16 (x and y).  Quantised weights are dequantised
  * to fp32, rounded to act_dtype, and multiplied with fp32 accumulation.
- * max_rows bounds kept_offsets[E] (rows of y and of the hidden workspace). */
+ * max_rows bounds kept_offsets[E] (rows of y and of the hidden workspace);
+ * max_rows_per_expert bounds every expert's row count (the capacity; 0 when
+ * unknown, then max_rows) and sizes the launch grids. */
 size_t qw_moe_experts_workspace_bytes(int64_t max_rows, int64_t experts, int64_t d_model, int64_t d_ff,
                                       int act_dtype);
 int qw_moe_experts(const void* x, int act_dtype, const int32_t* row_index, const int32_t* kept_offsets,
-                   int64_t experts, int64_t d_model, int64_t d_ff, int64_t max_rows, int w_format,
+                   int64_t experts, int64_t d_model, int64_t d_ff, int64_t max_rows, int64_t max_rows_per_expert,
+                   int w_format,
                    int64_t group_in, int64_t group_ff, const void* gate_w, const float* gate_scales,
                    const void* up_w, const float* up_scales, const void* down_w, const float* down_scales,
                    const float* row_weight, void* y, void* workspace, size_t workspace_bytes, void* stream);

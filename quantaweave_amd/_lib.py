@@ -31,7 +31,7 @@ SIGNATURES = {
     "qw_moe_plan": (I32, [P, P, I64, I64, I64, I64, P, P, P, P, P, P, P, P, P, P, SZ, P]),
     "qw_moe_permute": (I32, [P, I32, I64, P, P, I64, P, P]),
     "qw_moe_experts_workspace_bytes": (SZ, [I64, I64, I64, I64, I32]),
-    "qw_moe_experts": (I32, [P, I32, P, P, I64, I64, I64, I64, I32, I64, I64, P, P, P, P, P, P, P, P, P, SZ, P]),
+    "qw_moe_experts": (I32, [P, I32, P, P, I64, I64, I64, I64, I64, I32, I64, I64, P, P, P, P, P, P, P, P, P, SZ, P]),
     "qw_moe_combine": (I32, [P, I32, P, P, I64, I64, I64, P, P]),
     "qw_moe_balance": (I32, [P, P, I64, I64, I64, P, P, P]),
     "qw_moe_forward_workspace_bytes": (SZ, [I64, I64, I64, I64, I64, I32]),

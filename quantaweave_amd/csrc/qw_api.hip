@@ -212,15 +212,19 @@ size_t qw_moe_experts_workspace_bytes(int64_t max_rows, int64_t experts, int64_t
 }
 
 int qw_moe_experts(const void* x, int act_dtype, const int32_t* row_index, const int32_t* kept_offsets,
-                   int64_t experts, int64_t d_model, int64_t d_ff, int64_t max_rows, int w_format, int64_t group_in,
+                   int64_t experts, int64_t d_model, int64_t d_ff, int64_t max_rows, int64_t max_rows_per_expert,
+                   int w_format, int64_t group_in,
                    int64_t group_ff, const void* gate_w, const float* gate_scales, const void* up_w,
                    const float* up_scales, const void* down_w, const float* down_scales, const float* row_weight,
                    void* y, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
-  const int64_t avg = experts > 0 ? (max_rows + experts - 1) / experts : 0;
+  QW_REQUIRE(max_rows_per_expert >= 0, "max_rows_per_expert must be >= 0");
+  const int64_t cap = (max_rows_per_expert > 0 && max_rows_per_expert < max_rows) ? max_rows_per_expert : max_rows;
+  int64_t avg = experts > 0 ? (max_rows + experts - 1) / experts : 0;
+  if (avg > cap) avg = cap;
   return qw::experts(x, act_dtype, row_index, kept_offsets, experts, d_model, d_ff, max_rows, w_format, group_in,
                      group_ff, gate_w, gate_scales, up_w, up_scales, down_w, down_scales, row_weight, y, workspace,
-                     workspace_bytes, as_stream(stream), avg, max_rows);
+                     workspace_bytes, as_stream(stream), avg, cap);
 }
 
 int qw_moe_combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, int64_t tokens,

@@ -5,10 +5,10 @@
 // (src/quantization.py:36-58) are read here as they are stored.
 //
 // With a handful of routes per expert the FFN is a set of GEMVs whose cost is
-// reading each touched expert's weights once.  A workgroup (4 waves) owns an
-// (expert, column tile); untouched experts exit at once.  Each lane streams
-// 16-byte weight chunks of its rows (all loads issued before any math) and
-// dequantises in registers without materialising a bf16 weight:
+// reading each touched expert's weights once.  A workgroup of 4 independent
+// waves owns an (expert, column tile); untouched experts exit at once.  Each
+// lane streams the 16-byte weight chunks of its wave's rows (all issued before
+// any math) and dequantises in registers without materialising a bf16 weight:
 //
 //  QW_U4 : a chunk is 32 int4 codes u = q + 8, one quantisation group.  Nibbles
 //          become bf16 pairs with one v_perm each: bf16 bits 0x43nn = 128 + n.
@@ -20,10 +20,11 @@
 //          (exact for bf16 values); value = scale * (acc - 1152 * sum x) / 2^s.
 //  QW_BF16: a chunk is 8 bf16 weights, used directly by v_dot2_f32_bf16.
 //
-// Activation rows of the expert (up to 4 per pass) are staged once per pass in
-// LDS in the pair order the conversion produces, with per-chunk sums for the
-// bias correction.  Per-row partial sums are reduced across the wave with
-// butterflies.
+// The activation pieces matching a lane's chunks come straight from L2 (every
+// wave of the expert reads the same few rows), are put in the pair order of
+// the conversion once per chunk and reused for every row of the wave.  There
+// is no LDS and no barrier, so the waves of a CU overlap freely.  Per-row
+// partial sums are reduced across the wave with butterflies.
 #include "qw_ffn.h"
 
 namespace qw {
@@ -34,7 +35,6 @@ typedef __bf16 gbf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 gf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int GV_WAVES = 4;
-constexpr int GV_MAXM = 4;  // routes per pass
 
 template <int WF>
 struct Fmt;
@@ -59,13 +59,6 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 }
 __device__ __forceinline__ float dot2_f16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(gf16x2, a), __builtin_bit_cast(gf16x2, b), c, false);
-}
-
-// Makes the compiler treat v as produced here: keeps the weight conversion from
-// being hoisted above the activation staging (which would make the staging
-// wait for the whole weight stream).
-__device__ __forceinline__ void opaque(uint4& v) {
-  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
 }
 
 // Converts one 16-byte weight chunk into the operand pairs of the dot products.
@@ -96,174 +89,139 @@ __device__ __forceinline__ void chunk_pairs(const uint4 w, uint32_t* cw) {
   }
 }
 
-// Dot product of converted weight pairs with one staged activation chunk.
-template <int WF, int DW>
-__device__ __forceinline__ float chunk_dot(const uint32_t* cw, const uint32_t* xs) {
-  float acc = 0.0f;
+// Activation pieces of one chunk for one route, prepared for the dot products:
+// U4: bf16 pairs in the order the nibble conversion emits them, plus the sum
+//     of the chunk's 32 values (the bias correction);
+// I8: fp16 pairs of x * 2^s (s per route, brings max|x| into [2^14, 2^15));
+// BF16: the bf16 pairs as stored.
+template <int WF>
+__device__ __forceinline__ void prep_chunk(const uint4* raw, float scale, uint32_t* xq, float* xsum) {
+  if constexpr (WF == QW_U4) {
+    float sm = 0.0f;
 #pragma unroll
-  for (int q = 0; q < DW / 4; ++q) {
-    const uint4 t = reinterpret_cast<const uint4*>(xs)[q];
-    const uint32_t xv[4] = {t.x, t.y, t.z, t.w};
+    for (int q = 0; q < 4; ++q) {  // piece q: cols 8q..8q+7; v[t] = cols (2t, 2t+1)
+      const uint32_t v[4] = {raw[q].x, raw[q].y, raw[q].z, raw[q].w};
+      xq[4 * q + 0] = __builtin_amdgcn_perm(v[1], v[0], 0x05040100u);  // (0, 2)
+      xq[4 * q + 1] = __builtin_amdgcn_perm(v[3], v[2], 0x05040100u);  // (4, 6)
+      xq[4 * q + 2] = __builtin_amdgcn_perm(v[1], v[0], 0x07060302u);  // (1, 3)
+      xq[4 * q + 3] = __builtin_amdgcn_perm(v[3], v[2], 0x07060302u);  // (5, 7)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (WF == QW_I8) acc = dot2_f16(cw[4 * q + i], xv[i], acc);
-      else acc = dot2_bf16(cw[4 * q + i], xv[i], acc);
+      for (int t = 0; t < 4; ++t) sm = dot2_bf16(v[t], 0x3f803f80u, sm);  // + x[2t] + x[2t+1]
     }
+    *xsum = sm;
+  } else if constexpr (WF == QW_I8) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t v[4] = {raw[q].x, raw[q].y, raw[q].z, raw[q].w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const _Float16 a = static_cast<_Float16>(__uint_as_float(v[t] << 16) * scale);
+        const _Float16 b = static_cast<_Float16>(__uint_as_float(v[t] & 0xffff0000u) * scale);
+        xq[4 * q + t] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
+                        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+      }
+    }
+    float sm = 0.0f;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) sm = dot2_f16(xq[p], 0x3c003c00u, sm);  // + x'[2p] + x'[2p+1]
+    *xsum = sm;
+  } else {
+    xq[0] = raw[0].x;
+    xq[1] = raw[0].y;
+    xq[2] = raw[0].z;
+    xq[3] = raw[0].w;
+    *xsum = 0.0f;
   }
-  return acc;
 }
 
-// GATEUP: unit = hidden column (gate row + up row); DOWN: unit = output row.
-template <int WF, bool GATEUP, int UNITS, int CPL, int XPIECES_MAX>
+// Waves work independently (no LDS, no barriers): wave w of block (tile, e)
+// owns units [(tile*GV_WAVES + w)*UNITS, +UNITS) of expert e.  GATEUP: a unit
+// is a hidden column (gate row + up row); DOWN: a unit is an output row.  Each
+// lane streams its 16-byte weight chunks c = lane + 64*j once, then for every
+// pass of up to GV_MAXM routes (2 for int4, 4 otherwise) loads the routes' activation pieces of the same
+// chunks from L2, prepares them once and reuses them for all its rows.
+template <int WF, bool GATEUP, int UNITS, int CPL, int GV_MAXM>
 __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
     int max_rows, WView wa, WView wb, int K, int n_out, const float* __restrict__ row_weight,
     uint16_t* __restrict__ out) {
   constexpr int CW = Fmt<WF>::CW;
-  constexpr int DW = CW / 2;  // staged dwords (activation pairs) per chunk
+  constexpr int DW = CW / 2;   // activation pairs per chunk
+  constexpr int XP = CW / 8;   // 16-byte activation pieces per chunk
   constexpr int ROWS = GATEUP ? 2 : 1;
-  extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
   const int e = blockIdx.y;
   const int r_lo = max(offsets[e], 0), r_hi = min(offsets[e + 1], max_rows);
   if (r_hi <= r_lo) return;
-  const int KC = K / CW;                  // chunks per weight row
-  uint32_t* xs = smem;                    // [GV_MAXM][KC][DW]
-  float* xsum = reinterpret_cast<float*>(smem + GV_MAXM * KC * DW);  // [GV_MAXM][KC]
-  float* xscale = xsum + GV_MAXM * KC;    // [GV_MAXM] multiplier applied to x (I8 path)
-  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
   const int unit0 = (blockIdx.x * GV_WAVES + wave) * UNITS;
-
-  // weight row pointers of this wave's units; rows past the end are clamped to
-  // the last row (loaded, never written) so that every load is unconditional
-  const uint8_t* wrow[UNITS][ROWS];
-  const float* srow[UNITS][ROWS];
-#pragma unroll
-  for (int u = 0; u < UNITS; ++u)
-#pragma unroll
-    for (int rr = 0; rr < ROWS; ++rr) {
-      const WView& v = rr == 0 ? wa : wb;
-      const int n = min(unit0 + u, n_out - 1);
-      const int64_t esz = WF == QW_BF16 ? 2 : 1;
-      wrow[u][rr] = static_cast<const uint8_t*>(v.w) + (e * v.expert_elems + n * v.row_stride) * esz;
-      srow[u][rr] = WF != QW_BF16 ? v.scales + e * v.expert_scales + n * v.groups : nullptr;
-    }
+  if (unit0 >= n_out) return;
+  const int KC = K / CW;
   const int cpg = wa.group / CW;  // chunks per quantisation group
 
-  // Activation pieces (8 columns = 16 bytes) of one pass, loaded into
-  // registers before the weight stream is issued so that waiting for them does
-  // not wait for the weights (loads complete in issue order).
-  constexpr int XPT = (GV_MAXM * XPIECES_MAX + GV_WAVES * 64 - 1) / (GV_WAVES * 64);
-  const int KP = K / 8;  // pieces per activation row
-  uint4 xr[XPT];
-  auto load_x = [&](int m0, int M) {
-    // source rows of the pass first (uniform loads, one wait), then the pieces
-    int64_t src[GV_MAXM];
-#pragma unroll
-    for (int m = 0; m < GV_MAXM; ++m) src[m] = m < M ? (row_index ? row_index[m0 + m] : (m0 + m)) : 0;
-    // unconditional loads (indices clamped into the pass): a load under a branch
-    // makes the compiler wait for it inside the branch
-#pragma unroll
-    for (int j = 0; j < XPT; ++j) {
-      const int i = min(tid + j * GV_WAVES * 64, M * KP - 1);
-      const int m = i / KP, q = i % KP;
-      int64_t row = src[0];
-#pragma unroll
-      for (int t = 1; t < GV_MAXM; ++t) row = (m == t) ? src[t] : row;
-      xr[j] = reinterpret_cast<const uint4*>(x + row * K)[q];
-    }
-  };
-  load_x(r_lo, min(GV_MAXM, r_hi - r_lo));
-
-  // ---- this wave's weight rows, streamed once for all passes ----
+  // ---- this wave's weight chunks (unconditional loads, indices clamped) ----
   uint4 wv[UNITS][ROWS][CPL];
   float sv[UNITS][ROWS][CPL];
 #pragma unroll
   for (int u = 0; u < UNITS; ++u)
 #pragma unroll
-    for (int rr = 0; rr < ROWS; ++rr)
+    for (int rr = 0; rr < ROWS; ++rr) {
+      const WView& v = rr == 0 ? wa : wb;
+      const int n = min(unit0 + u, n_out - 1);  // rows past the end: loaded, never written
+      const int64_t esz = WF == QW_BF16 ? 2 : 1;
+      const uint8_t* wrow = static_cast<const uint8_t*>(v.w) + (e * v.expert_elems + n * v.row_stride) * esz;
+      const float* srow = WF != QW_BF16 ? v.scales + e * v.expert_scales + n * v.groups : nullptr;
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const int c = min(lane + 64 * j, KC - 1);  // chunks past the row end are skipped in the math
-        wv[u][rr][j] = *reinterpret_cast<const uint4*>(wrow[u][rr] + 16 * c);
-        if constexpr (WF != QW_BF16) sv[u][rr][j] = srow[u][rr][cpg == 1 ? c : c / cpg];
+        wv[u][rr][j] = *reinterpret_cast<const uint4*>(wrow + 16 * c);
+        if constexpr (WF != QW_BF16) sv[u][rr][j] = srow[cpg == 1 ? c : c / cpg];
       }
+    }
 
   for (int m0 = r_lo; m0 < r_hi; m0 += GV_MAXM) {
     const int M = min(GV_MAXM, r_hi - m0);
-    if (m0 != r_lo) load_x(m0, M);
+    const uint16_t* xrow[GV_MAXM];
+#pragma unroll
+    for (int m = 0; m < GV_MAXM; ++m) {
+      const int s = m0 + min(m, M - 1);
+      xrow[m] = x + static_cast<int64_t>(row_index ? row_index[s] : s) * K;
+    }
+    // activation pieces of this pass (unconditional loads, clamped)
+    uint4 raw[CPL][GV_MAXM][XP];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = min(lane + 64 * j, KC - 1);
+#pragma unroll
+      for (int m = 0; m < GV_MAXM; ++m)
+#pragma unroll
+        for (int q = 0; q < XP; ++q) raw[j][m][q] = reinterpret_cast<const uint4*>(xrow[m] + c * CW)[q];
+    }
+    float scale[GV_MAXM], inv[GV_MAXM];
+#pragma unroll
+    for (int m = 0; m < GV_MAXM; ++m) scale[m] = inv[m] = 1.0f;
     if constexpr (WF == QW_I8) {
-      // power-of-two scale per route so the largest |x| lands in [2^14, 2^15)
-      uint32_t* amax_bits = reinterpret_cast<uint32_t*>(xscale);
-      if (tid < GV_MAXM) amax_bits[tid] = 0u;
-      lds_barrier();
+      // per-route power of two bringing max|x| into [2^14, 2^15): fp16 then holds the bf16 values exactly
 #pragma unroll
-      for (int j = 0; j < XPT; ++j) {
-        const int i = tid + j * GV_WAVES * 64;
-        if (i < M * KP) {
-          const uint32_t v[4] = {xr[j].x, xr[j].y, xr[j].z, xr[j].w};
-          float a = 0.0f;
+      for (int m = 0; m < GV_MAXM; ++m) {
+        float a = 0.0f;
 #pragma unroll
-          for (int t = 0; t < 4; ++t)
-            a = fmaxf(a, fmaxf(fabsf(__uint_as_float(v[t] << 16)), fabsf(__uint_as_float(v[t] & 0xffff0000u))));
-          atomicMax(&amax_bits[i / KP], __float_as_uint(a));  // non-negative floats order as integers
+        for (int j = 0; j < CPL; ++j) {
+          if (lane + 64 * j >= KC) continue;
+#pragma unroll
+          for (int q = 0; q < XP; ++q) {
+            const uint32_t v[4] = {raw[j][m][q].x, raw[j][m][q].y, raw[j][m][q].z, raw[j][m][q].w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              a = fmaxf(a, fmaxf(fabsf(__uint_as_float(v[t] << 16)), fabsf(__uint_as_float(v[t] & 0xffff0000u))));
+          }
         }
-      }
-      lds_barrier();
-      if (tid < M) {
-        const float amax = __uint_as_float(amax_bits[tid]);
+        a = wave_max(a);
         int ex = 0;
-        frexpf(amax, &ex);  // amax in [2^(ex-1), 2^ex)
-        xscale[tid] = amax > 0.0f ? ldexpf(1.0f, 15 - ex) : 1.0f;
+        frexpf(a, &ex);  // a in [2^(ex-1), 2^ex)
+        scale[m] = a > 0.0f ? ldexpf(1.0f, 15 - ex) : 1.0f;
+        inv[m] = 1.0f / scale[m];
       }
-      lds_barrier();
     }
-    // ---- stage activations in LDS: pairs in the order the conversion emits them ----
-#pragma unroll
-    for (int j = 0; j < XPT; ++j) {
-      const int i = tid + j * GV_WAVES * 64;
-      if (i >= M * KP) continue;
-      const int m = i / KP;
-      const uint32_t v[4] = {xr[j].x, xr[j].y, xr[j].z, xr[j].w};  // v[t] = cols (2t, 2t+1) of the piece
-      uint4 o;
-      if constexpr (WF == QW_U4) {
-        // piece i is dword (i % 4) of a 32-column chunk: pairs (0,2), (4,6), (1,3), (5,7)
-        o.x = __builtin_amdgcn_perm(v[1], v[0], 0x05040100u);
-        o.y = __builtin_amdgcn_perm(v[3], v[2], 0x05040100u);
-        o.z = __builtin_amdgcn_perm(v[1], v[0], 0x07060302u);
-        o.w = __builtin_amdgcn_perm(v[3], v[2], 0x07060302u);
-      } else if constexpr (WF == QW_I8) {
-        const float sc = xscale[m];
-        uint32_t h[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const _Float16 a = static_cast<_Float16>(__uint_as_float(v[t] << 16) * sc);
-          const _Float16 b = static_cast<_Float16>(__uint_as_float(v[t] & 0xffff0000u) * sc);
-          h[t] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
-                 (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
-        }
-        o = make_uint4(h[0], h[1], h[2], h[3]);
-      } else {
-        o = xr[j];
-      }
-      // staged layout [m][chunk][DW dwords]: 8 columns are 4 dwords in every format
-      reinterpret_cast<uint4*>(xs)[i] = o;
-    }
-    lds_barrier();
-    if constexpr (WF != QW_BF16) {
-      // per-chunk activation sums (of the values as staged) for the bias correction
-      for (int i = tid; i < M * KC; i += blockDim.x) {
-        const uint32_t* q = xs + i * DW;
-        float s = 0.0f;
-#pragma unroll
-        for (int p = 0; p < DW; ++p) {
-          if constexpr (WF == QW_U4) s = dot2_bf16(q[p], 0x3f803f80u, s);  // bf16 pair (1, 1)
-          else s = dot2_f16(q[p], 0x3c003c00u, s);                        // fp16 pair (1, 1)
-        }
-        xsum[i] = s;
-      }
-      lds_barrier();
-    }
-
     float part[UNITS][ROWS][GV_MAXM];
 #pragma unroll
     for (int u = 0; u < UNITS; ++u)
@@ -272,15 +230,15 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
 #pragma unroll
         for (int m = 0; m < GV_MAXM; ++m) part[u][rr][m] = 0.0f;
 #pragma unroll
-    for (int u = 0; u < UNITS; ++u)
-#pragma unroll
-      for (int rr = 0; rr < ROWS; ++rr)
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) opaque(wv[u][rr][j]);
-#pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      const int c = lane + 64 * j;
-      if (c >= KC) continue;
+      if (lane + 64 * j >= KC) continue;
+      uint32_t xq[GV_MAXM][DW];
+      float xs[GV_MAXM];
+#pragma unroll
+      for (int m = 0; m < GV_MAXM; ++m) {
+        if (m >= M) break;
+        prep_chunk<WF>(raw[j][m], scale[m], xq[m], &xs[m]);
+      }
 #pragma unroll
       for (int u = 0; u < UNITS; ++u)
 #pragma unroll
@@ -290,13 +248,11 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
 #pragma unroll
           for (int m = 0; m < GV_MAXM; ++m) {
             if (m >= M) break;
-            const float d = chunk_dot<WF, DW>(cw, xs + (m * KC + c) * DW);
-            if constexpr (WF == QW_BF16) {
-              part[u][rr][m] += d;
-            } else {
-              const float corr = Fmt<WF>::BIAS * xsum[m * KC + c];
-              part[u][rr][m] = __builtin_fmaf(sv[u][rr][j], d - corr, part[u][rr][m]);
-            }
+            float d = 0.0f;
+#pragma unroll
+            for (int p = 0; p < DW; ++p) d = WF == QW_I8 ? dot2_f16(cw[p], xq[m][p], d) : dot2_bf16(cw[p], xq[m][p], d);
+            if constexpr (WF == QW_BF16) part[u][rr][m] += d;
+            else part[u][rr][m] = __builtin_fmaf(sv[u][rr][j], d - Fmt<WF>::BIAS * xs[m], part[u][rr][m]);
           }
         }
     }
@@ -307,13 +263,8 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
 #pragma unroll
       for (int m = 0; m < GV_MAXM; ++m) {
         if (m >= M) break;
-        float g = wave_sum_f(part[u][0][m]);
-        float up = GATEUP ? wave_sum_f(part[u][ROWS - 1][m]) : 0.0f;
-        if (WF == QW_I8) {
-          const float inv = 1.0f / xscale[m];
-          g *= inv;
-          up *= inv;
-        }
+        const float g = wave_sum_f(part[u][0][m]) * inv[m];
+        const float up = GATEUP ? wave_sum_f(part[u][ROWS - 1][m]) * inv[m] : 0.0f;
         if (lane == 0 && n < n_out) {
           const int s = m0 + m;
           if (GATEUP) {
@@ -325,47 +276,42 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
         }
       }
     }
-    lds_barrier();
   }
 }
 
 template <int WF, bool GATEUP, int UNITS, int CPL>
 int launch_one(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
                int n_out, const float* row_weight, void* out, hipStream_t stream) {
-  constexpr int CW = Fmt<WF>::CW;
-  const int KC = K / CW;
-  const size_t lds = static_cast<size_t>(GV_MAXM) * KC * (CW / 2) * 4 + static_cast<size_t>(GV_MAXM) * KC * 4 +
-                     GV_MAXM * 4;
-  const dim3 grid(static_cast<unsigned>(ceil_div(n_out, GV_WAVES * UNITS)), static_cast<unsigned>(a.experts));
-  // largest activation row the register staging covers: K <= 64*CPL chunks
-  ffn_gemv_kernel<WF, GATEUP, UNITS, CPL, 64 * CPL * CW / 8><<<grid, GV_WAVES * 64, lds, stream>>>(
+  const dim3 grid(static_cast<unsigned>(ceil_div(n_out, UNITS * GV_WAVES)), static_cast<unsigned>(a.experts));
+  // routes per pass: int4 activation pieces are 4x larger per chunk than bf16 ones
+  constexpr int MAXM = WF == QW_U4 ? 2 : 4;
+  ffn_gemv_kernel<WF, GATEUP, UNITS, CPL, MAXM><<<grid, GV_WAVES * 64, 0, stream>>>(
       static_cast<const uint16_t*>(x), row_index, a.offsets, static_cast<int>(a.max_rows), wa, wb, K, n_out,
       row_weight, static_cast<uint16_t*>(out));
   QW_LAUNCH_CHECK(GATEUP ? "ffn_gemv_kernel<gateup>" : "ffn_gemv_kernel<down>");
   return QW_OK;
 }
 
-template <int WF, bool GATEUP, int UNITS>
+// Units per wave for a row of CPL chunks per lane: 8 weight chunks (16-byte
+// loads) in flight per lane, whatever the row length.
+template <int WF, bool GATEUP>
 int launch_cpl(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
                int n_out, const float* row_weight, void* out, hipStream_t stream) {
   const int KC = K / Fmt<WF>::CW;
   const int cpl = static_cast<int>(ceil_div(KC, 64));
-  if (cpl <= 1) return launch_one<WF, GATEUP, UNITS, 1>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
-  if (cpl <= 2) return launch_one<WF, GATEUP, UNITS, 2>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
-  if (cpl <= 4) return launch_one<WF, GATEUP, UNITS, 4>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+  constexpr int U1 = GATEUP ? 4 : 8;
+  if (cpl <= 1) return launch_one<WF, GATEUP, U1, 1>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+  if (cpl <= 2) return launch_one<WF, GATEUP, U1 / 2, 2>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+  if (cpl <= 4) return launch_one<WF, GATEUP, U1 / 4, 4>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
   return set_error(QW_ERR_UNSUPPORTED, "row of %d chunks is too long for the decode kernel", KC);
 }
 
-// Units per wave: enough 16-byte loads in flight per lane while keeping the
-// register count low enough for several resident workgroups per CU.
 template <int WF>
 int launch_fmt(const FfnArgs& a, hipStream_t stream) {
   const int D = static_cast<int>(a.d_model), F = static_cast<int>(a.d_ff);
-  constexpr int GU = WF == QW_U4 ? 2 : 4;
-  constexpr int DN = WF == QW_U4 ? 4 : 8;
-  int st = launch_cpl<WF, true, GU>(a, a.gate, a.up, a.x, a.row_index, D, F, nullptr, a.hidden, stream);
+  int st = launch_cpl<WF, true>(a, a.gate, a.up, a.x, a.row_index, D, F, nullptr, a.hidden, stream);
   if (st) return st;
-  return launch_cpl<WF, false, DN>(a, a.down, a.down, a.hidden, nullptr, F, D, a.row_weight, a.y, stream);
+  return launch_cpl<WF, false>(a, a.down, a.down, a.hidden, nullptr, F, D, a.row_weight, a.y, stream);
 }
 
 }  // namespace

@@ -118,7 +118,7 @@ def grouped_swiglu(inputs: Tensor, experts: nn.ModuleList, counts: Sequence[int]
         nbytes = lib.qw_moe_experts_workspace_bytes(plan.rows, len(experts), d_model, d_ff, act)
         ws = _hip.workspace(nbytes, x.device)
         _lib.call("qw_moe_experts", _hip.ptr(x), act, None, _hip.ptr(plan.offsets), len(experts), d_model, d_ff,
-                  plan.rows, *args, None, _hip.ptr(out), _hip.ptr(ws), nbytes, _hip.stream(x.device))
+                  plan.rows, max(plan.counts), *args, None, _hip.ptr(out), _hip.ptr(ws), nbytes, _hip.stream(x.device))
     return out
 
 

@@ -73,7 +73,7 @@ def run_experts(x_np, counts, w, act, row_weight=None, row_index=None, x_rows=No
                   dw.get("down_s"), dw.get("group_in", 0), dw.get("group_ff", 0),
                   row_index=None if row_index is None else H.dev(row_index.astype(np.int32)),
                   row_weight=None if row_weight is None else H.dev(row_weight.astype(np.float32)),
-                  max_rows=int(sum(counts)))
+                  max_rows=int(sum(counts)), rows_per_expert=int(max(counts)))
     return y.float().cpu().numpy()
 
 
