@@ -53,6 +53,25 @@ def event_time(fn, iters, stream):
     return start.elapsed_time(end) / iters
 
 
+def event_samples(fn, iters, stream, flush=None):
+    """Per-call ms of fn() from HIP event pairs on `stream`; flush() runs between calls, outside the pairs."""
+    import torch
+
+    pairs = []
+    for _ in range(iters):
+        if flush is not None:
+            flush()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        fn()
+        b.record(stream)
+        pairs.append((a, b))
+    torch.cuda.synchronize()
+    t = np.array([a.elapsed_time(b) for a, b in pairs])
+    return dict(median=float(np.median(t)), p10=float(np.percentile(t, 10)), p90=float(np.percentile(t, 90)))
+
+
 def stage_calls(run):
     """The forward split into its entry points, with the same buffers as qw_moe_forward."""
     import torch
@@ -131,6 +150,11 @@ def measure(name, steps, warmup):
     torch.cuda.synchronize()
     for k_, fn in calls.items():
         stages[k_] = event_time(fn, max(5, steps // 2), stream)
+    # the expert stage again with the 256 MB last-level cache (MALL) flushed before every call: reading
+    # 512 MiB between calls evicts the weights (and leaves no dirty lines), so each call streams them from HBM
+    scratch = torch.ones(64 << 20, dtype=torch.int64, device=layer.x.device)
+    cold = event_samples(calls["experts"], max(20, steps), stream, flush=lambda: scratch.max())
+    del scratch
     flops = 6.0 * kept * w.d_model * w.d_ff
     act_bytes = 4 if w.act == "f32" else 2
     weight_bytes = touched * layer.expert_bytes()
@@ -140,6 +164,7 @@ def measure(name, steps, warmup):
     layer_bytes = weight_bytes + 2 * w.tokens * w.d_model * act_bytes + w.experts * w.d_model * act_bytes
     return dict(
         workload=w, wall_ms=wall_ms, event_ms=ev_ms, kept=kept, dropped=dropped, touched=touched, stages=stages,
+        experts_cold=cold,
         flops=flops, stage_bytes=stage_bytes, layer_bytes=layer_bytes, weight_bytes=weight_bytes,
         tokens_per_s=w.tokens / (wall_ms / 1000.0),
     )
@@ -229,6 +254,7 @@ def main():
     for name, r in results.items():
         ww = r["workload"]
         te = r["stages"]["experts"]
+        tc = r["experts_cold"]["median"]
         per[name] = dict(
             tokens_per_s=round(r["tokens_per_s"], 1), ms_per_step=round(r["wall_ms"], 4),
             event_ms=round(r["event_ms"], 4), stages_ms={k: round(v, 4) for k, v in r["stages"].items()},
@@ -237,6 +263,8 @@ def main():
             expert_stage_gbs=round(r["stage_bytes"] / (te / 1000) / 1e9, 1),
             hbm_frac=round(r["stage_bytes"] / (te / 1000) / 1e9 / HBM_PEAK_GBS, 4),
             mfma_frac=round(r["flops"] / (te / 1000) / 1e12 / BF16_PEAK_TFLOPS, 4) if ww.act == "bf16" else None,
+            experts_cold_ms={k: round(v, 4) for k, v in r["experts_cold"].items()},
+            hbm_frac_cold=round(r["stage_bytes"] / (tc / 1000) / 1e9 / HBM_PEAK_GBS, 4),
         )
     cpu = None
     if not args.no_cpu:

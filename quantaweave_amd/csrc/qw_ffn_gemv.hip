@@ -134,75 +134,143 @@ __device__ __forceinline__ void prep_chunk(const uint4* raw, float scale, uint32
   }
 }
 
-// Waves work independently (no LDS, no barriers): wave w of block (tile, e)
-// owns units [(tile*GV_WAVES + w)*UNITS, +UNITS) of expert e.  GATEUP: a unit
-// is a hidden column (gate row + up row); DOWN: a unit is an output row.  Each
-// lane streams its 16-byte weight chunks c = lane + 64*j once, then for every
-// pass of up to GV_MAXM routes (2 for int4, 4 otherwise) loads the routes' activation pieces of the same
-// chunks from L2, prepares them once and reuses them for all its rows.
-template <int WF, bool GATEUP, int UNITS, int CPL, int GV_MAXM>
+// Sums V = 2^L values over the 64 lanes of the wave with 6 - L + (V - 1)
+// shuffles instead of 6 V: at each of the first L steps a lane keeps half of
+// its values, adds the partner's copies of them and hands over the other half.
+// Afterwards every lane holds the full sum of value index lane >> (6 - L).
+template <int V>
+constexpr int log2i() {
+  int l = 0;
+  while ((1 << l) < V) ++l;
+  return l;
+}
+
+// One step of reduce_scatter over the first N of V values (all indices are
+// compile-time constants, so the values stay in registers).
+template <int V, int N>
+__device__ __forceinline__ void rs_step(float (&v)[V], int lane) {
+  if constexpr (N > 1) {
+    constexpr int half = N / 2;
+    constexpr int o = 32 * N / V;  // lane bit that picks the half this lane keeps
+    const bool upper = lane & o;
+#pragma unroll
+    for (int i = 0; i < half; ++i) {
+      const float give = upper ? v[i] : v[i + half];
+      const float keep = upper ? v[i + half] : v[i];
+      v[i] = keep + __shfl_xor(give, o, kWave);
+    }
+    rs_step<V, half>(v, lane);
+  }
+}
+
+template <int V>
+__device__ __forceinline__ float reduce_scatter(float (&v)[V], int lane) {
+  static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "V must be a power of two <= 64");
+  rs_step<V, V>(v, lane);
+  float r = v[0];
+#pragma unroll
+  for (int o = 32 / V; o >= 1; o >>= 1) r += __shfl_xor(r, o, kWave);
+  return r;
+}
+
+// a[i] for a lane-dependent i, as a select chain (no indexed private memory)
+template <int N>
+__device__ __forceinline__ float pick(const float (&a)[N], int i) {
+  float r = a[0];
+#pragma unroll
+  for (int k = 1; k < N; ++k) r = i == k ? a[k] : r;
+  return r;
+}
+
+// Waves work independently (no LDS, no barriers).  A group is UNITS
+// consecutive units of expert e (GATEUP: a unit is a hidden column, i.e. a gate
+// row and an up row; DOWN: an output row).  Wave w of block (b, e) owns groups
+// [(b*GV_WAVES + w)*gpw, +gpw).  Lane l streams the 16-byte chunks
+// c = l + 64*j (j < CPL) of each row.  The activation pieces of the same chunks
+// for up to MAXM routes come from L2 once per pass, are prepared once and kept
+// in registers while the wave walks its groups; the weights of group g+1 are
+// loaded before group g is computed, so a wave always has a group in flight.
+template <int WF, bool GATEUP, int UNITS, int CPL, int MAXM>
 __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
-    int max_rows, WView wa, WView wb, int K, int n_out, const float* __restrict__ row_weight,
+    int max_rows, WView wa, WView wb, int K, int n_out, int gpw, const float* __restrict__ row_weight,
     uint16_t* __restrict__ out) {
   constexpr int CW = Fmt<WF>::CW;
   constexpr int DW = CW / 2;   // activation pairs per chunk
   constexpr int XP = CW / 8;   // 16-byte activation pieces per chunk
   constexpr int ROWS = GATEUP ? 2 : 1;
+  constexpr int V = UNITS * ROWS * MAXM;  // values reduced per group
+  constexpr int L = log2i<V>();
   const int e = blockIdx.y;
   const int r_lo = max(offsets[e], 0), r_hi = min(offsets[e + 1], max_rows);
   if (r_hi <= r_lo) return;
-  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-  const int unit0 = (blockIdx.x * GV_WAVES + wave) * UNITS;
-  if (unit0 >= n_out) return;
+  const int lane = threadIdx.x % 64;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);  // wave-uniform: keeps the group loop scalar
+  const int n_groups = (n_out + UNITS - 1) / UNITS;
+  const int g_first = (blockIdx.x * GV_WAVES + wave) * gpw;
+  if (g_first >= n_groups) return;
+  const int g_end = min(g_first + gpw, n_groups);
   const int KC = K / CW;
   const int cpg = wa.group / CW;  // chunks per quantisation group
+  const int64_t esz = WF == QW_BF16 ? 2 : 1;
+  const uint8_t* wbase[ROWS];
+  const float* sbase[ROWS];
+#pragma unroll
+  for (int rr = 0; rr < ROWS; ++rr) {
+    const WView& v = rr == 0 ? wa : wb;
+    wbase[rr] = static_cast<const uint8_t*>(v.w) + e * v.expert_elems * esz;
+    sbase[rr] = WF != QW_BF16 ? v.scales + e * v.expert_scales : nullptr;
+  }
+  const int64_t wstride = wa.row_stride * esz;
+  const int sstride = wa.groups;
+  int cidx[CPL], sidx[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    cidx[j] = min(lane + 64 * j, KC - 1);  // chunks past the row end are loaded, never used
+    sidx[j] = cpg == 1 ? cidx[j] : cidx[j] / cpg;
+  }
 
-  // ---- this wave's weight chunks (unconditional loads, indices clamped) ----
-  uint4 wv[UNITS][ROWS][CPL];
-  float sv[UNITS][ROWS][CPL];
+  uint4 w0[UNITS][ROWS][CPL], w1[UNITS][ROWS][CPL];
+  float s0[UNITS][ROWS][CPL], s1[UNITS][ROWS][CPL];
+  // loads group g (clamped to the wave's last group, so the loads are unconditional)
+  auto load = [&](int g, uint4 (&wv)[UNITS][ROWS][CPL], float (&sv)[UNITS][ROWS][CPL]) {
+    g = min(g, g_end - 1);
 #pragma unroll
-  for (int u = 0; u < UNITS; ++u)
+    for (int u = 0; u < UNITS; ++u) {
+      const int n = min(g * UNITS + u, n_out - 1);  // rows past the end: loaded, never written
 #pragma unroll
-    for (int rr = 0; rr < ROWS; ++rr) {
-      const WView& v = rr == 0 ? wa : wb;
-      const int n = min(unit0 + u, n_out - 1);  // rows past the end: loaded, never written
-      const int64_t esz = WF == QW_BF16 ? 2 : 1;
-      const uint8_t* wrow = static_cast<const uint8_t*>(v.w) + (e * v.expert_elems + n * v.row_stride) * esz;
-      const float* srow = WF != QW_BF16 ? v.scales + e * v.expert_scales + n * v.groups : nullptr;
+      for (int rr = 0; rr < ROWS; ++rr) {
+        const uint8_t* wrow = wbase[rr] + n * wstride;
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        const int c = min(lane + 64 * j, KC - 1);  // chunks past the row end are skipped in the math
-        wv[u][rr][j] = *reinterpret_cast<const uint4*>(wrow + 16 * c);
-        if constexpr (WF != QW_BF16) sv[u][rr][j] = srow[cpg == 1 ? c : c / cpg];
+        for (int j = 0; j < CPL; ++j) {
+          wv[u][rr][j] = *reinterpret_cast<const uint4*>(wrow + 16 * cidx[j]);
+          if constexpr (WF != QW_BF16) sv[u][rr][j] = sbase[rr][n * sstride + sidx[j]];
+        }
       }
     }
+  };
 
-  for (int m0 = r_lo; m0 < r_hi; m0 += GV_MAXM) {
-    const int M = min(GV_MAXM, r_hi - m0);
-    const uint16_t* xrow[GV_MAXM];
+  for (int m0 = r_lo; m0 < r_hi; m0 += MAXM) {
+    const int M = min(MAXM, r_hi - m0);
+    // ---- activation pieces of this pass: issued first, prepared while the first group streams in ----
+    uint4 raw[CPL][MAXM][XP];
 #pragma unroll
-    for (int m = 0; m < GV_MAXM; ++m) {
+    for (int m = 0; m < MAXM; ++m) {
       const int s = m0 + min(m, M - 1);
-      xrow[m] = x + static_cast<int64_t>(row_index ? row_index[s] : s) * K;
+      const uint16_t* xrow = x + static_cast<int64_t>(row_index ? row_index[s] : s) * K;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+#pragma unroll
+        for (int q = 0; q < XP; ++q) raw[j][m][q] = reinterpret_cast<const uint4*>(xrow + cidx[j] * CW)[q];
     }
-    // activation pieces of this pass (unconditional loads, clamped)
-    uint4 raw[CPL][GV_MAXM][XP];
+    load(g_first, w0, s0);
+    float scale[MAXM], inv[MAXM];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const int c = min(lane + 64 * j, KC - 1);
-#pragma unroll
-      for (int m = 0; m < GV_MAXM; ++m)
-#pragma unroll
-        for (int q = 0; q < XP; ++q) raw[j][m][q] = reinterpret_cast<const uint4*>(xrow[m] + c * CW)[q];
-    }
-    float scale[GV_MAXM], inv[GV_MAXM];
-#pragma unroll
-    for (int m = 0; m < GV_MAXM; ++m) scale[m] = inv[m] = 1.0f;
+    for (int m = 0; m < MAXM; ++m) scale[m] = inv[m] = 1.0f;
     if constexpr (WF == QW_I8) {
       // per-route power of two bringing max|x| into [2^14, 2^15): fp16 then holds the bf16 values exactly
 #pragma unroll
-      for (int m = 0; m < GV_MAXM; ++m) {
+      for (int m = 0; m < MAXM; ++m) {
         float a = 0.0f;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
@@ -222,59 +290,74 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
         inv[m] = 1.0f / scale[m];
       }
     }
-    float part[UNITS][ROWS][GV_MAXM];
-#pragma unroll
-    for (int u = 0; u < UNITS; ++u)
-#pragma unroll
-      for (int rr = 0; rr < ROWS; ++rr)
-#pragma unroll
-        for (int m = 0; m < GV_MAXM; ++m) part[u][rr][m] = 0.0f;
+    uint32_t xq[CPL][MAXM][DW];
+    float xs[CPL][MAXM];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      if (lane + 64 * j >= KC) continue;
-      uint32_t xq[GV_MAXM][DW];
-      float xs[GV_MAXM];
+      // chunks past the row end get zero activations, so every chunk is used unconditionally below
+      const bool valid = lane + 64 * j < KC;
 #pragma unroll
-      for (int m = 0; m < GV_MAXM; ++m) {
-        if (m >= M) break;
-        prep_chunk<WF>(raw[j][m], scale[m], xq[m], &xs[m]);
+      for (int m = 0; m < MAXM; ++m) {
+        prep_chunk<WF>(raw[j][m], scale[m], xq[j][m], &xs[j][m]);
+#pragma unroll
+        for (int p = 0; p < DW; ++p) xq[j][m][p] = valid ? xq[j][m][p] : 0u;
+        xs[j][m] = valid ? xs[j][m] : 0.0f;
       }
-#pragma unroll
-      for (int u = 0; u < UNITS; ++u)
-#pragma unroll
-        for (int rr = 0; rr < ROWS; ++rr) {
-          uint32_t cw[DW];
-          chunk_pairs<WF>(wv[u][rr][j], cw);
-#pragma unroll
-          for (int m = 0; m < GV_MAXM; ++m) {
-            if (m >= M) break;
-            float d = 0.0f;
-#pragma unroll
-            for (int p = 0; p < DW; ++p) d = WF == QW_I8 ? dot2_f16(cw[p], xq[m][p], d) : dot2_bf16(cw[p], xq[m][p], d);
-            if constexpr (WF == QW_BF16) part[u][rr][m] += d;
-            else part[u][rr][m] = __builtin_fmaf(sv[u][rr][j], d - Fmt<WF>::BIAS * xs[m], part[u][rr][m]);
-          }
-        }
     }
-    // ---- reduce over the wave and write ----
+
+    // ---- one group: dot products, wave reduction, outputs ----
+    auto compute = [&](int g, const uint4 (&wv)[UNITS][ROWS][CPL], const float (&sv)[UNITS][ROWS][CPL]) {
+      float part[V];
 #pragma unroll
-    for (int u = 0; u < UNITS; ++u) {
-      const int n = unit0 + u;
+      for (int i = 0; i < V; ++i) part[i] = 0.0f;
 #pragma unroll
-      for (int m = 0; m < GV_MAXM; ++m) {
-        if (m >= M) break;
-        const float g = wave_sum_f(part[u][0][m]) * inv[m];
-        const float up = GATEUP ? wave_sum_f(part[u][ROWS - 1][m]) * inv[m] : 0.0f;
-        if (lane == 0 && n < n_out) {
-          const int s = m0 + m;
-          if (GATEUP) {
-            out[static_cast<int64_t>(s) * n_out + n] = f32_to_bf16(silu_f32(g) * up);
-          } else {
-            const float wgt = row_weight ? row_weight[s] : 1.0f;
-            out[static_cast<int64_t>(s) * n_out + n] = f32_to_bf16(round_to_bf16(g) * wgt);
+      for (int j = 0; j < CPL; ++j) {
+#pragma unroll
+        for (int u = 0; u < UNITS; ++u)
+#pragma unroll
+          for (int rr = 0; rr < ROWS; ++rr) {
+            uint32_t cw[DW];
+            chunk_pairs<WF>(wv[u][rr][j], cw);
+#pragma unroll
+            for (int m = 0; m < MAXM; ++m) {
+              if (m >= M) break;
+              float d = 0.0f;
+#pragma unroll
+              for (int p = 0; p < DW; ++p)
+                d = WF == QW_I8 ? dot2_f16(cw[p], xq[j][m][p], d) : dot2_bf16(cw[p], xq[j][m][p], d);
+              float& acc = part[((u * MAXM + m) << (ROWS - 1)) | rr];
+              if constexpr (WF == QW_BF16) acc += d;
+              else acc = __builtin_fmaf(sv[u][rr][j], d - Fmt<WF>::BIAS * xs[j][m], acc);
+            }
           }
+      }
+      float r = reduce_scatter<V>(part, lane);
+      const int idx = lane >> (6 - L);  // value index this lane now holds
+      const int rr = GATEUP ? (idx & 1) : 0;
+      const int um = GATEUP ? idx >> 1 : idx;
+      const int u = um / MAXM, m = um % MAXM;
+      const int n = g * UNITS + u;
+      const int s = m0 + m;
+      if constexpr (GATEUP) {
+        const float up = __shfl_xor(r, 1 << (6 - L), kWave);  // the up row of the same unit and route
+        if ((lane & ((2 << (6 - L)) - 1)) == 0 && m < M && n < n_out) {
+          const float im = pick(inv, m);
+          out[static_cast<int64_t>(s) * n_out + n] = f32_to_bf16(silu_f32(r * im) * (up * im));
+        }
+      } else {
+        if ((lane & ((1 << (6 - L)) - 1)) == 0 && m < M && n < n_out) {
+          const float wgt = row_weight ? row_weight[s] : 1.0f;
+          out[static_cast<int64_t>(s) * n_out + n] = f32_to_bf16(round_to_bf16(r * pick(inv, m)) * wgt);
         }
       }
+    };
+
+    for (int g = g_first; g < g_end; g += 2) {
+      load(g + 1, w1, s1);
+      compute(g, w0, s0);
+      if (g + 1 >= g_end) break;
+      load(g + 2, w0, s0);
+      compute(g + 1, w1, s1);
     }
   }
 }
@@ -282,18 +365,25 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
 template <int WF, bool GATEUP, int UNITS, int CPL>
 int launch_one(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
                int n_out, const float* row_weight, void* out, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(ceil_div(n_out, UNITS * GV_WAVES)), static_cast<unsigned>(a.experts));
   // routes per pass: int4 activation pieces are 4x larger per chunk than bf16 ones
   constexpr int MAXM = WF == QW_U4 ? 2 : 4;
+  // groups per wave: about 4096 waves over the experts that can be touched (at most one per kept row),
+  // at least one group and at most eight per wave
+  const int64_t n_groups = ceil_div(n_out, UNITS);
+  const int64_t touched = a.max_rows < a.experts ? a.max_rows : a.experts;
+  int64_t gpw = touched * n_groups / 4096;
+  gpw = gpw < 1 ? 1 : (gpw > 8 ? 8 : gpw);
+  const int64_t waves = ceil_div(n_groups, gpw);
+  const dim3 grid(static_cast<unsigned>(ceil_div(waves, GV_WAVES)), static_cast<unsigned>(a.experts));
   ffn_gemv_kernel<WF, GATEUP, UNITS, CPL, MAXM><<<grid, GV_WAVES * 64, 0, stream>>>(
       static_cast<const uint16_t*>(x), row_index, a.offsets, static_cast<int>(a.max_rows), wa, wb, K, n_out,
-      row_weight, static_cast<uint16_t*>(out));
+      static_cast<int>(gpw), row_weight, static_cast<uint16_t*>(out));
   QW_LAUNCH_CHECK(GATEUP ? "ffn_gemv_kernel<gateup>" : "ffn_gemv_kernel<down>");
   return QW_OK;
 }
 
-// Units per wave for a row of CPL chunks per lane: 8 weight chunks (16-byte
-// loads) in flight per lane, whatever the row length.
+// Units per group for a row of CPL chunks per lane: 8 weight chunks (16-byte
+// loads) per lane and group, whatever the row length.
 template <int WF, bool GATEUP>
 int launch_cpl(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
                int n_out, const float* row_weight, void* out, hipStream_t stream) {
