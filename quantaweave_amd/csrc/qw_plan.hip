@@ -5,13 +5,15 @@
 // by the key (expert asc, weight desc, route id asc), keeps the first
 // `capacity` routes of each expert and lists the rest as dropped.
 //
-// Here one workgroup owns one expert.  Kernel 1 counts the expert's routes.
-// Kernel 2 derives every offset from the counts (each workgroup scans the E
-// counts itself), gathers the expert's route keys
+// One kernel, one workgroup per expert.  Every workgroup reads all routes once
+// (16 per thread, loads issued together), builds the histogram of all experts
+// in LDS (per-wave copies, summed afterwards) and gathers its own expert's
+// route keys
 //   key = (~order(weight)) << 32 | route id        (unique per route)
-// into LDS, sorts them with a bitonic network and writes kept slots and
-// dropped routes at their plan positions.  Keys are unique, so the order
-// inside the gather does not matter and the result does not depend on
+// into LDS.  From the histogram it derives every offset itself, ranks its keys
+// (by counting, or with a bitonic network for large experts) and writes kept
+// slots and dropped routes at their plan positions.  Keys are unique, so the
+// order inside the gather does not matter and the result does not depend on
 // scheduling.  An expert with more routes than the LDS holds ranks its keys
 // against each other through global memory instead (same result, slower).
 #include "qw_common.h"
@@ -20,6 +22,9 @@ namespace qw {
 
 constexpr int kPlanThreads = 1024;
 constexpr int kSortCap = 8192;  // keys an expert sorts in LDS (64 KiB)
+constexpr int kRankCap = 2048;  // keys an expert ranks by counting (n^2 compares) instead of sorting
+constexpr int kMaxExperts = 1024;
+constexpr int kRoutesPerThread = 16;
 
 // Order-preserving map of a float onto uint32 (NaN largest, like torch.sort).
 __device__ __forceinline__ uint32_t weight_key(float f) {
@@ -60,55 +65,58 @@ __device__ int block_exclusive_scan(int v, int* warp_tot, int* total) {
   return r;
 }
 
-__device__ int block_sum(int v, int* red) {
-  v = wave_sum_i(v);
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  if (lane == 0) red[wave] = v;
-  __syncthreads();
-  int s = 0;
-  if (threadIdx.x == 0) {
-    for (int w = 0; w < static_cast<int>(blockDim.x / kWave); ++w) s += red[w];
-    red[0] = s;
-  }
-  __syncthreads();
-  s = red[0];
-  __syncthreads();
-  return s;
-}
 
-// Kernel 1: counts[e] = #{r : top_idx[r] == e}; block e == 0 also marks routes
-// with an out-of-range expert id as not kept.
-__global__ __launch_bounds__(kPlanThreads) void plan_count_kernel(const int32_t* __restrict__ top_idx, int R, int E,
-                                                                  int32_t* __restrict__ counts,
-                                                                  int32_t* __restrict__ route_slot) {
-  __shared__ int red[kPlanThreads / kWave];
-  const int e = blockIdx.x;
-  int c = 0;
-  for (int r = threadIdx.x; r < R; r += blockDim.x) {
-    const int v = top_idx[r];
-    c += (v == e) ? 1 : 0;
-    if (e == 0 && (v < 0 || v >= E)) route_slot[r] = -1;
-  }
-  c = block_sum(c, red);
-  if (threadIdx.x == 0) counts[e] = c;
-}
-
-// Kernel 2: offsets, per-expert sort and placement.
-__global__ __launch_bounds__(kPlanThreads) void plan_place_kernel(
+// Offsets, per-expert ranking and placement.
+__global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const int32_t* __restrict__ top_idx, const float* __restrict__ top_w, int R, int E, int K, int capacity,
-    const int32_t* __restrict__ counts, int32_t* __restrict__ kept_counts, int32_t* __restrict__ kept_offsets,
+    int32_t* __restrict__ counts, int32_t* __restrict__ kept_counts, int32_t* __restrict__ kept_offsets,
     int32_t* __restrict__ totals, int32_t* __restrict__ slot_token, float* __restrict__ slot_weight,
     int32_t* __restrict__ route_slot, int32_t* __restrict__ dropped_token, int32_t* __restrict__ dropped_expert,
     uint64_t* __restrict__ spill) {
+  constexpr int kWaves = kPlanThreads / kWave;
   __shared__ uint64_t keys[kSortCap];
-  __shared__ int warp_tot[kPlanThreads / kWave];
+  __shared__ int hist[kWaves][kMaxExperts];
+  __shared__ int warp_tot[kWaves];
   __shared__ int s_tot_kept, s_tot_drop, s_tot_routes;
   __shared__ int s_kept_off, s_drop_off, s_route_off, s_fill;
   const int e = blockIdx.x;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, wave = tid / kWave;
+  for (int i = tid; i < kWaves * E; i += kPlanThreads) hist[i / E][i % E] = 0;
+  if (tid == 0) s_fill = 0;
+  __syncthreads();
 
-  // ---- offsets from the E counts (E <= 1024 == blockDim) ----
-  const int c = tid < E ? counts[tid] : 0;
+  // ---- one pass over the routes: histogram of all experts, keys of expert e ----
+  // (the keys go to LDS when they fit; the count decides afterwards)
+  for (int base = 0; base < R; base += kPlanThreads * kRoutesPerThread) {
+    int v[kRoutesPerThread];
+#pragma unroll
+    for (int i = 0; i < kRoutesPerThread; ++i) {
+      const int r = base + i * kPlanThreads + tid;
+      v[i] = r < R ? top_idx[r] : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < kRoutesPerThread; ++i) {
+      const int r = base + i * kPlanThreads + tid;
+      if (r >= R) continue;
+      if (v[i] >= 0 && v[i] < E) {
+        atomicAdd(&hist[wave][v[i]], 1);
+        if (v[i] == e) {
+          const int p = atomicAdd(&s_fill, 1);
+          if (p < kSortCap) keys[p] = route_key(top_w, r);
+        }
+      } else if (e == 0) {
+        route_slot[r] = -1;  // out-of-range expert id: never kept
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- counts and offsets of every expert (E <= blockDim) ----
+  int c = 0;
+  if (tid < E) {
+#pragma unroll 4
+    for (int w = 0; w < kWaves; ++w) c += hist[w][tid];
+  }
   const int kc = c < capacity ? c : capacity;
   const int ko = block_exclusive_scan(kc, warp_tot, &s_tot_kept);
   const int dof = block_exclusive_scan(c - kc, warp_tot, &s_tot_drop);
@@ -119,6 +127,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_place_kernel(
     s_route_off = ro;
   }
   if (e == 0 && tid < E) {
+    counts[tid] = c;
     kept_counts[tid] = kc;
     kept_offsets[tid] = ko;
   }
@@ -127,9 +136,8 @@ __global__ __launch_bounds__(kPlanThreads) void plan_place_kernel(
     totals[0] = s_tot_kept;
     totals[1] = s_tot_drop;
   }
-  if (tid == 0) s_fill = 0;
   __syncthreads();
-  const int n = counts[e];
+  const int n = s_fill;
   if (n == 0) return;
   const int kept_off = s_kept_off, drop_off = s_drop_off;
 
@@ -148,17 +156,17 @@ __global__ __launch_bounds__(kPlanThreads) void plan_place_kernel(
     }
   };
 
-  if (n <= kSortCap) {
-    // ---- gather this expert's keys into LDS ----
-    for (int r = tid; r < R; r += blockDim.x) {
-      if (top_idx[r] == e) {
-        const int p = atomicAdd(&s_fill, 1);
-        keys[p] = route_key(top_w, r);
-      }
+  if (n <= kRankCap) {
+    // ---- rank by counting: every key against every key (all lanes read the same key: broadcast) ----
+    for (int i = tid; i < n; i += kPlanThreads) {
+      const uint64_t k = keys[i];
+      int rank = 0;
+      for (int j = 0; j < n; ++j) rank += keys[j] < k ? 1 : 0;
+      place(k, rank);
     }
+  } else if (n <= kSortCap) {
     int p2 = 1;
     while (p2 < n) p2 <<= 1;
-    __syncthreads();
     for (int i = n + tid; i < p2; i += blockDim.x) keys[i] = ~0ull;  // padding sorts last
     __syncthreads();
     // ---- bitonic sort, ascending ----
@@ -181,6 +189,8 @@ __global__ __launch_bounds__(kPlanThreads) void plan_place_kernel(
   } else {
     // ---- large expert: keys in global scratch, rank by counting ----
     uint64_t* mine = spill + s_route_off;
+    if (tid == 0) s_fill = 0;
+    __syncthreads();
     for (int r = tid; r < R; r += blockDim.x) {
       if (top_idx[r] == e) {
         const int p = atomicAdd(&s_fill, 1);
@@ -227,12 +237,10 @@ int plan(const int32_t* top_idx, const float* top_w, int64_t T, int64_t K, int64
   Carver c(ws);
   uint64_t* spill = c.take<uint64_t>(static_cast<size_t>(R));
   const int e = static_cast<int>(E);
-  plan_count_kernel<<<e, kPlanThreads, 0, stream>>>(top_idx, R, e, counts, route_slot);
-  QW_LAUNCH_CHECK("plan_count_kernel");
-  plan_place_kernel<<<e, kPlanThreads, 0, stream>>>(top_idx, top_w, R, e, static_cast<int>(K), cap, counts,
-                                                    kept_counts, kept_offsets, totals, slot_token, slot_weight,
-                                                    route_slot, dropped_token, dropped_expert, spill);
-  QW_LAUNCH_CHECK("plan_place_kernel");
+  plan_kernel<<<e, kPlanThreads, 0, stream>>>(top_idx, top_w, R, e, static_cast<int>(K), cap, counts, kept_counts,
+                                              kept_offsets, totals, slot_token, slot_weight, route_slot, dropped_token,
+                                              dropped_expert, spill);
+  QW_LAUNCH_CHECK("plan_kernel");
   return QW_OK;
 }
 
