@@ -173,27 +173,134 @@ __device__ __forceinline__ float reduce_scatter(float (&v)[V], int lane) {
   return r;
 }
 
-// a[i] for a lane-dependent i, as a select chain (no indexed private memory)
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt immediate waiting for vmcnt <= n only (expcnt, lgkmcnt left at max).
 template <int N>
-__device__ __forceinline__ float pick(const float (&a)[N], int i) {
-  float r = a[0];
-#pragma unroll
-  for (int k = 1; k < N; ++k) r = i == k ? a[k] : r;
-  return r;
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
 }
 
-// Waves work independently (no LDS, no barriers).  A group is UNITS
-// consecutive units of expert e (GATEUP: a unit is a hidden column, i.e. a gate
-// row and an up row; DOWN: an output row).  Wave w of block (b, e) owns groups
-// [(b*GV_WAVES + w)*gpw, +gpw).  Lane l streams the 16-byte chunks
-// c = l + 64*j (j < CPL) of each row.  The activation pieces of the same chunks
-// for up to MAXM routes come from L2 once per pass, are prepared once and kept
-// in registers while the wave walks its groups; the weights of group g+1 are
-// loaded before group g is computed, so a wave always has a group in flight.
-template <int WF, bool GATEUP, int UNITS, int CPL, int MAXM>
+// LDS bytes of one wave: a ring of GV_STAGES groups (weight chunks, then the
+// chunks' scales) and the staging area of the outputs of one pass.
+template <int WF, int UNITS, int ROWS, int CPL, int GPW, int MAXM>
+struct GvLds {
+  static constexpr int NCH = UNITS * ROWS * CPL;                 // chunk loads per group
+  static_assert(NCH == 4 || NCH == 8, "the ring reads four or eight chunks per group");
+  static constexpr bool QUANT = WF != QW_BF16;
+  static constexpr int STAGE = NCH * 1024 + (QUANT ? NCH * 256 : 0);
+  static constexpr int STAGES = 3;
+  static constexpr int NDMA = NCH * (QUANT ? 2 : 1);             // DMA instructions per group
+  static constexpr int OUT = GPW * UNITS * MAXM * 4;             // staged outputs (fp32)
+  static constexpr int WAVE = STAGES * STAGE + OUT;
+};
+
+// Reads the 8 weight chunks (and, with SCALES, their 8 scales) of this lane from
+// one ring stage and waits for them.  Written as one assembly block: the
+// compiler cannot tell these reads from the ring's in-flight DMA writes to other
+// stages and would wait for every DMA load before each read; the group's own
+// DMA loads are covered by the explicit vmcnt wait before this call.
+template <bool SCALES>
+__device__ __forceinline__ void ring_read8(uint32_t w_addr, uint32_t s_addr, uint4 (&w)[8], float (&sv)[8]) {
+  if constexpr (SCALES) {
+    asm volatile(
+        "ds_read_b128 %0, %16\n"
+        "ds_read_b128 %1, %16 offset:1024\n"
+        "ds_read_b128 %2, %16 offset:2048\n"
+        "ds_read_b128 %3, %16 offset:3072\n"
+        "ds_read_b128 %4, %16 offset:4096\n"
+        "ds_read_b128 %5, %16 offset:5120\n"
+        "ds_read_b128 %6, %16 offset:6144\n"
+        "ds_read_b128 %7, %16 offset:7168\n"
+        "ds_read_b32 %8, %17\n"
+        "ds_read_b32 %9, %17 offset:256\n"
+        "ds_read_b32 %10, %17 offset:512\n"
+        "ds_read_b32 %11, %17 offset:768\n"
+        "ds_read_b32 %12, %17 offset:1024\n"
+        "ds_read_b32 %13, %17 offset:1280\n"
+        "ds_read_b32 %14, %17 offset:1536\n"
+        "ds_read_b32 %15, %17 offset:1792\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]), "=&v"(w[6]), "=&v"(w[7]),
+          "=&v"(sv[0]), "=&v"(sv[1]), "=&v"(sv[2]), "=&v"(sv[3]), "=&v"(sv[4]), "=&v"(sv[5]), "=&v"(sv[6]),
+          "=&v"(sv[7])
+        : "v"(w_addr), "v"(s_addr)
+        : "memory");
+  } else {
+    (void)s_addr;
+    asm volatile(
+        "ds_read_b128 %0, %8\n"
+        "ds_read_b128 %1, %8 offset:1024\n"
+        "ds_read_b128 %2, %8 offset:2048\n"
+        "ds_read_b128 %3, %8 offset:3072\n"
+        "ds_read_b128 %4, %8 offset:4096\n"
+        "ds_read_b128 %5, %8 offset:5120\n"
+        "ds_read_b128 %6, %8 offset:6144\n"
+        "ds_read_b128 %7, %8 offset:7168\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]), "=&v"(w[6]), "=&v"(w[7])
+        : "v"(w_addr)
+        : "memory");
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sv[i] = 1.0f;
+  }
+}
+
+template <bool SCALES>
+__device__ __forceinline__ void ring_read4(uint32_t w_addr, uint32_t s_addr, uint4 (&w)[4], float (&sv)[4]) {
+  if constexpr (SCALES) {
+    asm volatile(
+        "ds_read_b128 %0, %8\n"
+        "ds_read_b128 %1, %8 offset:1024\n"
+        "ds_read_b128 %2, %8 offset:2048\n"
+        "ds_read_b128 %3, %8 offset:3072\n"
+        "ds_read_b32 %4, %9\n"
+        "ds_read_b32 %5, %9 offset:256\n"
+        "ds_read_b32 %6, %9 offset:512\n"
+        "ds_read_b32 %7, %9 offset:768\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(sv[0]), "=&v"(sv[1]), "=&v"(sv[2]), "=&v"(sv[3])
+        : "v"(w_addr), "v"(s_addr)
+        : "memory");
+  } else {
+    (void)s_addr;
+    asm volatile(
+        "ds_read_b128 %0, %4\n"
+        "ds_read_b128 %1, %4 offset:1024\n"
+        "ds_read_b128 %2, %4 offset:2048\n"
+        "ds_read_b128 %3, %4 offset:3072\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3])
+        : "v"(w_addr)
+        : "memory");
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sv[i] = 1.0f;
+  }
+}
+
+// LDS byte address of a pointer into the kernel's dynamic LDS.
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
+}
+
+// Waves work independently (no barriers).  A group is UNITS consecutive units
+// of expert e (GATEUP: a unit is a hidden column, i.e. a gate row and an up
+// row; DOWN: an output row).  Wave w of block (b, e) owns groups
+// [(b*GV_WAVES + w)*GPW, +GPW).  Lane l streams the 16-byte chunks
+// c = l + 64*j (j < CPL) of each row, and their scales, HBM -> LDS with
+// global_load_lds into a ring of the wave's own, GV_STAGES-1 groups ahead, so
+// the bytes in flight cost no registers; the loads complete in issue order and
+// every group issues the same loads, so a fixed vmcnt wait marks a group as
+// landed.  The activation pieces of the same chunks for up to MAXM routes come
+// from L2 once per pass, are prepared once and kept in registers while the
+// wave walks its groups.  Outputs are staged in the wave's LDS and stored once
+// the pass is done (a store between the ring loads would break the counts).
+template <int WF, bool GATEUP, int UNITS, int CPL, int MAXM, int GPW>
 __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
-    int max_rows, WView wa, WView wb, int K, int n_out, int gpw, const float* __restrict__ row_weight,
+    int max_rows, WView wa, WView wb, int K, int n_out, const float* __restrict__ row_weight,
     uint16_t* __restrict__ out) {
   constexpr int CW = Fmt<WF>::CW;
   constexpr int DW = CW / 2;   // activation pairs per chunk
@@ -201,15 +308,20 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
   constexpr int ROWS = GATEUP ? 2 : 1;
   constexpr int V = UNITS * ROWS * MAXM;  // values reduced per group
   constexpr int L = log2i<V>();
+  constexpr int OUTS = UNITS * MAXM;      // outputs per group
+  using LD = GvLds<WF, UNITS, ROWS, CPL, GPW, MAXM>;
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
   const int e = blockIdx.y;
   const int r_lo = max(offsets[e], 0), r_hi = min(offsets[e + 1], max_rows);
   if (r_hi <= r_lo) return;
   const int lane = threadIdx.x % 64;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);  // wave-uniform: keeps the group loop scalar
   const int n_groups = (n_out + UNITS - 1) / UNITS;
-  const int g_first = (blockIdx.x * GV_WAVES + wave) * gpw;
+  const int g_first = (blockIdx.x * GV_WAVES + wave) * GPW;
   if (g_first >= n_groups) return;
-  const int g_end = min(g_first + gpw, n_groups);
+  const int g_end = min(g_first + GPW, n_groups);
+  char* const ring = smem + wave * LD::WAVE;
+  float* const staged = reinterpret_cast<float*>(ring + LD::STAGES * LD::STAGE);
   const int KC = K / CW;
   const int cpg = wa.group / CW;  // chunks per quantisation group
   const int64_t esz = WF == QW_BF16 ? 2 : 1;
@@ -230,11 +342,10 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
     sidx[j] = cpg == 1 ? cidx[j] : cidx[j] / cpg;
   }
 
-  uint4 w0[UNITS][ROWS][CPL], w1[UNITS][ROWS][CPL];
-  float s0[UNITS][ROWS][CPL], s1[UNITS][ROWS][CPL];
-  // loads group g (clamped to the wave's last group, so the loads are unconditional)
-  auto load = [&](int g, uint4 (&wv)[UNITS][ROWS][CPL], float (&sv)[UNITS][ROWS][CPL]) {
+  // DMA of group g (clamped to the wave's last group, so every group issues the same loads)
+  auto issue = [&](int g) {
     g = min(g, g_end - 1);
+    char* st = ring + ((g - g_first) % LD::STAGES) * LD::STAGE;
 #pragma unroll
     for (int u = 0; u < UNITS; ++u) {
       const int n = min(g * UNITS + u, n_out - 1);  // rows past the end: loaded, never written
@@ -243,8 +354,12 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
         const uint8_t* wrow = wbase[rr] + n * wstride;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-          wv[u][rr][j] = *reinterpret_cast<const uint4*>(wrow + 16 * cidx[j]);
-          if constexpr (WF != QW_BF16) sv[u][rr][j] = sbase[rr][n * sstride + sidx[j]];
+          const int q = (u * ROWS + rr) * CPL + j;
+          __builtin_amdgcn_global_load_lds(static_cast<const void*>(wrow + 16 * cidx[j]), (lds_void*)(st + q * 1024),
+                                           16, 0, 0);
+          if constexpr (LD::QUANT)
+            __builtin_amdgcn_global_load_lds(static_cast<const void*>(sbase[rr] + n * sstride + sidx[j]),
+                                             (lds_void*)(st + LD::NCH * 1024 + q * 256), 4, 0, 0);
         }
       }
     }
@@ -252,7 +367,7 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
 
   for (int m0 = r_lo; m0 < r_hi; m0 += MAXM) {
     const int M = min(MAXM, r_hi - m0);
-    // ---- activation pieces of this pass: issued first, prepared while the first group streams in ----
+    // ---- activation pieces of this pass (plain loads), then the first groups of the ring ----
     uint4 raw[CPL][MAXM][XP];
 #pragma unroll
     for (int m = 0; m < MAXM; ++m) {
@@ -263,7 +378,8 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
 #pragma unroll
         for (int q = 0; q < XP; ++q) raw[j][m][q] = reinterpret_cast<const uint4*>(xrow + cidx[j] * CW)[q];
     }
-    load(g_first, w0, s0);
+#pragma unroll
+    for (int i = 0; i < LD::STAGES - 1; ++i) issue(g_first + i);
     float scale[MAXM], inv[MAXM];
 #pragma unroll
     for (int m = 0; m < MAXM; ++m) scale[m] = inv[m] = 1.0f;
@@ -305,8 +421,17 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
       }
     }
 
-    // ---- one group: dot products, wave reduction, outputs ----
-    auto compute = [&](int g, const uint4 (&wv)[UNITS][ROWS][CPL], const float (&sv)[UNITS][ROWS][CPL]) {
+    // ---- the groups: issue g+STAGES-1, wait for g, compute g from the ring ----
+    for (int g = g_first; g < g_end; ++g) {
+      issue(g + LD::STAGES - 1);
+      wait_vmcnt<(LD::STAGES - 1) * LD::NDMA>();
+      const char* st = ring + ((g - g_first) % LD::STAGES) * LD::STAGE;
+      uint4 wq[LD::NCH];
+      float sq[LD::NCH];
+      if constexpr (LD::NCH == 8)
+        ring_read8<LD::QUANT>(lds_addr(st) + lane * 16, lds_addr(st + LD::NCH * 1024) + lane * 4, wq, sq);
+      else
+        ring_read4<LD::QUANT>(lds_addr(st) + lane * 16, lds_addr(st + LD::NCH * 1024) + lane * 4, wq, sq);
       float part[V];
 #pragma unroll
       for (int i = 0; i < V; ++i) part[i] = 0.0f;
@@ -316,8 +441,11 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
         for (int u = 0; u < UNITS; ++u)
 #pragma unroll
           for (int rr = 0; rr < ROWS; ++rr) {
+            const int q = (u * ROWS + rr) * CPL + j;
+            const uint4 wv = wq[q];
+            const float sv = sq[q];
             uint32_t cw[DW];
-            chunk_pairs<WF>(wv[u][rr][j], cw);
+            chunk_pairs<WF>(wv, cw);
 #pragma unroll
             for (int m = 0; m < MAXM; ++m) {
               if (m >= M) break;
@@ -327,72 +455,94 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
                 d = WF == QW_I8 ? dot2_f16(cw[p], xq[j][m][p], d) : dot2_bf16(cw[p], xq[j][m][p], d);
               float& acc = part[((u * MAXM + m) << (ROWS - 1)) | rr];
               if constexpr (WF == QW_BF16) acc += d;
-              else acc = __builtin_fmaf(sv[u][rr][j], d - Fmt<WF>::BIAS * xs[j][m], acc);
+              else acc = __builtin_fmaf(sv, d - Fmt<WF>::BIAS * xs[j][m], acc);
             }
           }
       }
+      if constexpr (WF == QW_I8) {  // undo the power-of-two activation scaling (exact)
+#pragma unroll
+        for (int u = 0; u < UNITS; ++u)
+#pragma unroll
+          for (int m = 0; m < MAXM; ++m)
+#pragma unroll
+            for (int rr = 0; rr < ROWS; ++rr) part[((u * MAXM + m) << (ROWS - 1)) | rr] *= inv[m];
+      }
       float r = reduce_scatter<V>(part, lane);
       const int idx = lane >> (6 - L);  // value index this lane now holds
-      const int rr = GATEUP ? (idx & 1) : 0;
       const int um = GATEUP ? idx >> 1 : idx;
-      const int u = um / MAXM, m = um % MAXM;
-      const int n = g * UNITS + u;
-      const int s = m0 + m;
+      float* slot = staged + (g - g_first) * OUTS + um;
       if constexpr (GATEUP) {
         const float up = __shfl_xor(r, 1 << (6 - L), kWave);  // the up row of the same unit and route
-        if ((lane & ((2 << (6 - L)) - 1)) == 0 && m < M && n < n_out) {
-          const float im = pick(inv, m);
-          out[static_cast<int64_t>(s) * n_out + n] = f32_to_bf16(silu_f32(r * im) * (up * im));
-        }
+        if ((lane & ((2 << (6 - L)) - 1)) == 0) *slot = silu_f32(r) * up;
       } else {
-        if ((lane & ((1 << (6 - L)) - 1)) == 0 && m < M && n < n_out) {
-          const float wgt = row_weight ? row_weight[s] : 1.0f;
-          out[static_cast<int64_t>(s) * n_out + n] = f32_to_bf16(round_to_bf16(r * pick(inv, m)) * wgt);
-        }
+        if ((lane & ((1 << (6 - L)) - 1)) == 0) *slot = r;
       }
-    };
-
-    for (int g = g_first; g < g_end; g += 2) {
-      load(g + 1, w1, s1);
-      compute(g, w0, s0);
-      if (g + 1 >= g_end) break;
-      load(g + 2, w0, s0);
-      compute(g + 1, w1, s1);
+    }
+    wait_vmcnt<0>();  // the ring's trailing (clamped) loads land before the next pass reuses the ring
+    // ---- outputs of the pass: value v = (group, unit, route) of this wave's staging area ----
+    const int n_vals = (g_end - g_first) * OUTS;
+    for (int v = lane; v < n_vals; v += 64) {
+      const int gi = v / OUTS, um = v % OUTS;
+      const int u = um / MAXM, m = um % MAXM;
+      const int n = (g_first + gi) * UNITS + u;
+      if (m >= M || n >= n_out) continue;
+      const int srow = m0 + m;
+      const float val = staged[v];
+      if constexpr (GATEUP) {
+        out[static_cast<int64_t>(srow) * n_out + n] = f32_to_bf16(val);
+      } else {
+        const float wgt = row_weight ? row_weight[srow] : 1.0f;
+        out[static_cast<int64_t>(srow) * n_out + n] = f32_to_bf16(round_to_bf16(val) * wgt);
+      }
     }
   }
 }
 
-template <int WF, bool GATEUP, int UNITS, int CPL>
-int launch_one(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
+template <int WF, bool GATEUP, int UNITS, int CPL, int GPW>
+int launch_gpw(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
                int n_out, const float* row_weight, void* out, hipStream_t stream) {
   // routes per pass: int4 activation pieces are 4x larger per chunk than bf16 ones
   constexpr int MAXM = WF == QW_U4 ? 2 : 4;
-  // groups per wave: about 4096 waves over the experts that can be touched (at most one per kept row),
-  // at least one group and at most eight per wave
-  const int64_t n_groups = ceil_div(n_out, UNITS);
-  const int64_t touched = a.max_rows < a.experts ? a.max_rows : a.experts;
-  int64_t gpw = touched * n_groups / 4096;
-  gpw = gpw < 1 ? 1 : (gpw > 8 ? 8 : gpw);
-  const int64_t waves = ceil_div(n_groups, gpw);
+  using LD = GvLds<WF, UNITS, GATEUP ? 2 : 1, CPL, GPW, MAXM>;
+  constexpr size_t lds = static_cast<size_t>(GV_WAVES) * LD::WAVE;
+  auto kernel = ffn_gemv_kernel<WF, GATEUP, UNITS, CPL, MAXM, GPW>;
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     static_cast<int>(lds));
+  if (attr != hipSuccess)
+    return set_error(QW_ERR_HIP, "cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(attr));
+  const int64_t waves = ceil_div(ceil_div(n_out, UNITS), GPW);
   const dim3 grid(static_cast<unsigned>(ceil_div(waves, GV_WAVES)), static_cast<unsigned>(a.experts));
-  ffn_gemv_kernel<WF, GATEUP, UNITS, CPL, MAXM><<<grid, GV_WAVES * 64, 0, stream>>>(
-      static_cast<const uint16_t*>(x), row_index, a.offsets, static_cast<int>(a.max_rows), wa, wb, K, n_out,
-      static_cast<int>(gpw), row_weight, static_cast<uint16_t*>(out));
+  kernel<<<grid, GV_WAVES * 64, lds, stream>>>(static_cast<const uint16_t*>(x), row_index, a.offsets,
+                                               static_cast<int>(a.max_rows), wa, wb, K, n_out, row_weight,
+                                               static_cast<uint16_t*>(out));
   QW_LAUNCH_CHECK(GATEUP ? "ffn_gemv_kernel<gateup>" : "ffn_gemv_kernel<down>");
   return QW_OK;
 }
 
-// Units per group for a row of CPL chunks per lane: 8 weight chunks (16-byte
-// loads) per lane and group, whatever the row length.
+// Groups per wave: about 4096 waves over the experts that can be touched (at most
+// one per kept row), as 4 or 8 groups per wave.
+template <int WF, bool GATEUP, int UNITS, int CPL>
+int launch_one(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
+               int n_out, const float* row_weight, void* out, hipStream_t stream) {
+  const int64_t n_groups = ceil_div(n_out, UNITS);
+  const int64_t touched = a.max_rows < a.experts ? a.max_rows : a.experts;
+  if (touched * n_groups / 4096 >= 6)
+    return launch_gpw<WF, GATEUP, UNITS, CPL, 8>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+  return launch_gpw<WF, GATEUP, UNITS, CPL, 4>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+}
+
+// Units per group for a row of CPL chunks per lane: 4 weight chunks (16-byte
+// loads) per lane and group (8 for gate/up rows of more than 128 chunks).
 template <int WF, bool GATEUP>
 int launch_cpl(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
                int n_out, const float* row_weight, void* out, hipStream_t stream) {
   const int KC = K / Fmt<WF>::CW;
   const int cpl = static_cast<int>(ceil_div(KC, 64));
-  constexpr int U1 = GATEUP ? 4 : 8;
+  constexpr int U1 = GATEUP ? 2 : 4;
   if (cpl <= 1) return launch_one<WF, GATEUP, U1, 1>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
   if (cpl <= 2) return launch_one<WF, GATEUP, U1 / 2, 2>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
-  if (cpl <= 4) return launch_one<WF, GATEUP, U1 / 4, 4>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+  if (cpl <= 4) return launch_one<WF, GATEUP, 1, 4>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
   return set_error(QW_ERR_UNSUPPORTED, "row of %d chunks is too long for the decode kernel", KC);
 }
 

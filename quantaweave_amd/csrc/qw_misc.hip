@@ -46,34 +46,47 @@ int permute(const void* x, int dtype, int64_t D, const int32_t* slot_token, cons
 // `zeros_like(flat).index_add_(0, tokens, y)` on expert-ordered rows
 // (src/quantweave_moe_model.py:192, :201, :211).  One block per token.
 // ---------------------------------------------------------------------------
-template <int ACT, int VEC>
+// KMAX >= K bounds the routes per token; the token's kept routes are put in
+// ascending expert order in registers (a static ranking network, no indexed
+// private memory).
+template <int ACT, int VEC, int KMAX>
 __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y, const int32_t* __restrict__ route_slot,
                                                       const int32_t* __restrict__ top_idx, int K, int D,
                                                       void* __restrict__ out) {
   const int t = blockIdx.x;
-  int slot[64], ord[64];
+  int sl[KMAX], ex[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    sl[j] = j < K ? route_slot[static_cast<int64_t>(t) * K + j] : -1;
+    ex[j] = j < K ? top_idx[static_cast<int64_t>(t) * K + j] : 0;
+  }
+  // rank of each kept route among the kept routes by expert id (experts of a token are distinct)
+  int rk[KMAX];
   int nk = 0;
-  for (int j = 0; j < K; ++j) {
-    const int s = route_slot[static_cast<int64_t>(t) * K + j];
-    if (s < 0) continue;
-    const int e = top_idx[static_cast<int64_t>(t) * K + j];
-    // insertion by expert id (distinct experts per token)
-    int p = nk;
-    while (p > 0 && ord[p - 1] > e) {
-      ord[p] = ord[p - 1];
-      slot[p] = slot[p - 1];
-      --p;
-    }
-    ord[p] = e;
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    int r = 0;
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i) r += (sl[i] >= 0 && ex[i] < ex[j]) ? 1 : 0;
+    rk[j] = sl[j] >= 0 ? r : KMAX;
+    nk += sl[j] >= 0 ? 1 : 0;
+  }
+  int slot[KMAX];
+#pragma unroll
+  for (int p = 0; p < KMAX; ++p) {
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) s = rk[j] == p ? sl[j] : s;
     slot[p] = s;
-    ++nk;
   }
   const int64_t row = static_cast<int64_t>(t) * D;
   for (int c = threadIdx.x * VEC; c < D; c += blockDim.x * VEC) {
     float acc[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
-    for (int j = 0; j < nk; ++j) {
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+      if (j >= nk) break;
       const int64_t src = static_cast<int64_t>(slot[j]) * D + c;
       if constexpr (VEC == 8 && ACT == QW_BF16) {
         const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(y) + src);
@@ -110,6 +123,20 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
   }
 }
 
+template <int KMAX>
+int launch_combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, unsigned g, int k,
+                   int d, void* out, hipStream_t stream) {
+  if (dtype == QW_F32) {
+    if (d % 4 == 0) combine_kernel<QW_F32, 4, KMAX><<<g, 256, 0, stream>>>(y, route_slot, top_idx, k, d, out);
+    else combine_kernel<QW_F32, 1, KMAX><<<g, 256, 0, stream>>>(y, route_slot, top_idx, k, d, out);
+  } else {
+    if (d % 8 == 0) combine_kernel<QW_BF16, 8, KMAX><<<g, 256, 0, stream>>>(y, route_slot, top_idx, k, d, out);
+    else combine_kernel<QW_BF16, 1, KMAX><<<g, 256, 0, stream>>>(y, route_slot, top_idx, k, d, out);
+  }
+  QW_LAUNCH_CHECK("combine_kernel");
+  return QW_OK;
+}
+
 int combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, int64_t T, int64_t K,
             int64_t D, void* out, hipStream_t stream) {
   QW_REQUIRE(dtype == QW_F32 || dtype == QW_BF16, "combine dtype must be f32 or bf16");
@@ -119,15 +146,11 @@ int combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* 
   QW_REQUIRE(y && route_slot && top_idx && out, "combine pointers are required");
   const unsigned g = static_cast<unsigned>(T);
   const int k = static_cast<int>(K), d = static_cast<int>(D);
-  if (dtype == QW_F32) {
-    if (D % 4 == 0) combine_kernel<QW_F32, 4><<<g, 256, 0, stream>>>(y, route_slot, top_idx, k, d, out);
-    else combine_kernel<QW_F32, 1><<<g, 256, 0, stream>>>(y, route_slot, top_idx, k, d, out);
-  } else {
-    if (D % 8 == 0) combine_kernel<QW_BF16, 8><<<g, 256, 0, stream>>>(y, route_slot, top_idx, k, d, out);
-    else combine_kernel<QW_BF16, 1><<<g, 256, 0, stream>>>(y, route_slot, top_idx, k, d, out);
-  }
-  QW_LAUNCH_CHECK("combine_kernel");
-  return QW_OK;
+  if (K <= 2) return launch_combine<2>(y, dtype, route_slot, top_idx, g, k, d, out, stream);
+  if (K <= 4) return launch_combine<4>(y, dtype, route_slot, top_idx, g, k, d, out, stream);
+  if (K <= 8) return launch_combine<8>(y, dtype, route_slot, top_idx, g, k, d, out, stream);
+  if (K <= 16) return launch_combine<16>(y, dtype, route_slot, top_idx, g, k, d, out, stream);
+  return launch_combine<64>(y, dtype, route_slot, top_idx, g, k, d, out, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -22,7 +22,7 @@ namespace qw {
 
 constexpr int kPlanThreads = 1024;
 constexpr int kSortCap = 8192;  // keys an expert sorts in LDS (64 KiB)
-constexpr int kRankCap = 2048;  // keys an expert ranks by counting (n^2 compares) instead of sorting
+constexpr int kRankCap = 1024;  // keys an expert ranks by counting (n^2 compares) instead of sorting
 constexpr int kMaxExperts = 1024;
 constexpr int kRoutesPerThread = 16;
 
@@ -97,15 +97,21 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
 #pragma unroll
     for (int i = 0; i < kRoutesPerThread; ++i) {
       const int r = base + i * kPlanThreads + tid;
-      if (r >= R) continue;
-      if (v[i] >= 0 && v[i] < E) {
-        atomicAdd(&hist[wave][v[i]], 1);
-        if (v[i] == e) {
-          const int p = atomicAdd(&s_fill, 1);
+      const bool valid = r < R && v[i] >= 0 && v[i] < E;
+      if (valid) atomicAdd(&hist[wave][v[i]], 1);
+      if (r < R && !valid && e == 0) route_slot[r] = -1;  // out-of-range expert id: never kept
+      // this expert's routes: one LDS atomic per wave, lanes take consecutive positions
+      const bool mine = valid && v[i] == e;
+      const uint64_t m = __ballot(mine);
+      if (m != 0) {
+        const int lane = tid % kWave;
+        int first = 0;
+        if (lane == __builtin_ctzll(m)) first = atomicAdd(&s_fill, __popcll(m));
+        first = __shfl(first, __builtin_ctzll(m), kWave);
+        if (mine) {
+          const int p = first + __popcll(m & ((1ull << lane) - 1ull));
           if (p < kSortCap) keys[p] = route_key(top_w, r);
         }
-      } else if (e == 0) {
-        route_slot[r] = -1;  // out-of-range expert id: never kept
       }
     }
   }
