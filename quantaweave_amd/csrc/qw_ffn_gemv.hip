@@ -183,7 +183,7 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
 }
 
-// LDS bytes of one wave: a ring of GV_STAGES groups (weight chunks, then the
+// LDS bytes of one wave: a ring of STAGES groups (weight chunks, then the
 // chunks' scales) and the staging area of the outputs of one pass.
 template <int WF, int UNITS, int ROWS, int CPL, int GPW, int MAXM>
 struct GvLds {
@@ -191,7 +191,7 @@ struct GvLds {
   static_assert(NCH == 4 || NCH == 8, "the ring reads four or eight chunks per group");
   static constexpr bool QUANT = WF != QW_BF16;
   static constexpr int STAGE = NCH * 1024 + (QUANT ? NCH * 256 : 0);
-  static constexpr int STAGES = 3;
+  static constexpr int STAGES = 2;
   static constexpr int NDMA = NCH * (QUANT ? 2 : 1);             // DMA instructions per group
   static constexpr int OUT = GPW * UNITS * MAXM * 4;             // staged outputs (fp32)
   static constexpr int WAVE = STAGES * STAGE + OUT;
@@ -290,7 +290,8 @@ __device__ __forceinline__ uint32_t lds_addr(const char* p) {
 // row; DOWN: an output row).  Wave w of block (b, e) owns groups
 // [(b*GV_WAVES + w)*GPW, +GPW).  Lane l streams the 16-byte chunks
 // c = l + 64*j (j < CPL) of each row, and their scales, HBM -> LDS with
-// global_load_lds into a ring of the wave's own, GV_STAGES-1 groups ahead, so
+// global_load_lds into a two-stage ring of the wave's own (one group ahead; a
+// deeper ring costs more LDS per wave than the extra waves it displaces), so
 // the bytes in flight cost no registers; the loads complete in issue order and
 // every group issues the same loads, so a fixed vmcnt wait marks a group as
 // landed.  The activation pieces of the same chunks for up to MAXM routes come
