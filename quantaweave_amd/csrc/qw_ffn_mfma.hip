@@ -12,14 +12,14 @@
 //                 columns), DOWN: 256 output columns.
 //
 // Operands move HBM/L2 -> LDS with global_load_lds_dwordx4 (no register
-// staging) in K-slices of 32 through two rings: the weight slices (the HBM
-// stream) are requested MF_BST-1 slices ahead, the activation slices (L2
-// resident) MF_AST-1 ahead, so ~80 KiB of weights per CU stay in flight while
-// the MFMAs run.  One LDS barrier per slice.  Loads complete in issue order
-// and every wave issues the same loads per slice (rows past the end are
-// clamped to a valid row, their results never stored), so waiting for the
-// later-issued activation slice with a fixed `s_waitcnt vmcnt(n)` also covers
-// its weight slice.
+// staging) in K-slices of 32 through two 3-stage rings, the weight slices (the
+// HBM stream) and the activation slices (L2 resident) both requested two
+// slices ahead, right after the slice's barrier, so they are in flight during
+// the MFMAs (deeper weight rings measured slower: they leave no LDS for a
+// deeper activation ring).  One LDS barrier per slice.  Loads complete in
+// issue order and every wave issues the same loads per slice (rows past the
+// end are clamped to a valid row, their results never stored), so a fixed
+// `s_waitcnt vmcnt(n)` marks a slice as landed.
 //
 // LDS rows are 64 bytes (32 bf16); the four 16-byte pieces of row r are stored
 // XOR-swizzled by ((r >> 1) & 3) so the 16-row fragment reads of the MFMAs
@@ -53,7 +53,7 @@ constexpr int MF_THREADS = 512;
 constexpr int MF_WAVES = 8;
 constexpr int MF_NT = 4;        // 16-column MFMA tiles per wave
 constexpr int MF_AST = 3;       // activation ring stages
-constexpr int MF_BST = 6;       // weight ring stages
+constexpr int MF_BST = 3;       // weight ring stages (both rings requested two slices ahead)
 constexpr int kXcds = 8;
 
 // s_waitcnt immediate waiting for vmcnt <= n only (expcnt, lgkmcnt left at max).
@@ -186,23 +186,20 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
   const int active_sub = (count + 15) / 16;  // row sub-tiles holding valid rows (wave-uniform)
   const int KT = K / MF_BK;
 
-  // Issue order (iteration i issues A(i+2) then B(i+5); the prologue plays
-  // iterations -5..-1): B0 B1 B2 A0 B3 A1 B4 | A2 B5 | A3 B6 | ...
-  // Slice kt is complete once A(kt) is, which was followed by B(kt+3), A(kt+1)
-  // and B(kt+4) (those that exist).
-  static_assert(MF_AST == 3 && MF_BST == 6, "issue schedule below assumes 3 + 6 stages");
-#pragma unroll
-  for (int i = -5; i < 0; ++i) {
-    if (i + 2 >= 0 && i + 2 < KT) issue_a(i + 2);
-    if (i + 5 < KT) issue_b(i + 5);
+  // Issue order: A0 B0 A1 B1 | A2 B2 | A3 B3 | ...  (iteration kt issues A(kt+2), B(kt+2)
+  // right after its barrier).  At the top of iteration kt the loads issued after B(kt) are
+  // A(kt+1) and B(kt+1): waiting for all but those completes slice kt.
+  for (int j = 0; j < 2 && j < KT; ++j) {
+    issue_a(j);
+    issue_b(j);
   }
-
   for (int kt = 0; kt < KT; ++kt) {
-    if (kt + 4 < KT) wait_vmcnt<AL_MAX + 2 * BL>();
-    else if (kt + 3 < KT) wait_vmcnt<AL_MAX + BL>();
-    else if (kt + 1 < KT) wait_vmcnt<AL_MAX>();
+    if (kt + 1 < KT) wait_vmcnt<AL_MAX + BL>();
     else wait_vmcnt<0>();
     ring_barrier();  // slice kt visible to all waves; everyone is done with slice kt-1
+    // requests into the stages of slice kt-1 (every wave is past its reads of them)
+    if (kt + 2 < KT) issue_a(kt + 2);
+    if (kt + 2 < KT) issue_b(kt + 2);
     const char* st_a = a_ring + (kt % MF_AST) * A_STAGE;
     const char* st_b = b_ring + (kt % MF_BST) * B_BYTES;
     bf16x8 wfr[MF_NT];
@@ -223,10 +220,6 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
       for (int t = 0; t < MF_NT; ++t)
         acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[t], xfr, acc[i][t], 0, 0, 0);
     }
-    // requests into the stages of slice kt-1 (every wave is past its reads of
-    // them: they all passed this iteration's barrier)
-    if (kt + 2 < KT) issue_a(kt + 2);
-    if (kt + 5 < KT) issue_b(kt + 5);
   }
 
   // ---- epilogue: lane holds row l16 of the sub-tile, columns 4*lq .. 4*lq+3 of each tile ----
