@@ -8,7 +8,10 @@ already resident in HBM.  Prints ONE JSON line: throughput of the headline
 workload (bf16 prefill, T=8192, d=2048, 64 experts, d_ff=1024, top-2,
 capacity factor 1.25) with a roofline entry for the expert-FFN stage, the
 CPU baseline (the oracle on the host cores, bounded sample), and per-workload
-numbers for the other workloads.
+numbers for the other workloads, and the batch-1 decode step
+(qw_moe_decode_step: the routed experts of one token, fp32 routing, no
+capacity) at three of the workloads' layer shapes, eager and replayed from a
+HIP graph.
 """
 
 from __future__ import annotations
@@ -170,6 +173,52 @@ def measure(name, steps, warmup):
     )
 
 
+DECODE_SHAPES = ["int4-decode-T16-d4096-E64-f1408-k2", "int8-decode-T64-d2048-E64-f1024-k2",
+                 "bf16-prefill-T8192-d2048-E64-f1024-k2"]
+
+
+def measure_decode(name, steps, warmup):
+    """One-token decode step on the layer of workload `name`: per-step ms of eager
+    calls and of HIP-graph replays (warm, and with the last-level cache flushed)."""
+    import torch
+    from quantaweave_amd import workloads as W
+
+    w = W.WORKLOADS[name]
+    layer = W.build_layer(W.scaled(w, tokens=1))
+    run = W.DecodeRunner(layer, tokens=1)
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    eager = event_samples(run, max(20, steps), stream)
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            run()
+    stream.wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    replay_ms = event_time(graph.replay, max(50, steps), stream)
+    scratch = torch.ones(64 << 20, dtype=torch.int64, device="cuda")
+    cold = event_samples(graph.replay, max(20, steps), stream, flush=lambda: scratch.max())
+    del scratch
+    touched = int(torch.unique(run.top_idx).numel())
+    # algorithmic bytes: the routed experts' stored weights once, x, residual and out (fp32), the fp32 router
+    nbytes = touched * layer.expert_bytes() + 3 * w.d_model * 4 + w.experts * w.d_model * 4
+    return dict(
+        shape=f"T1-d{w.d_model}-E{w.experts}-f{w.d_ff}-k{w.top_k}-{w.weights}", experts_read=touched,
+        algorithmic_bytes=nbytes, eager_ms={k: round(v, 4) for k, v in eager.items()},
+        graph_replay_ms=round(replay_ms, 4), graph_replay_cold_ms={k: round(v, 4) for k, v in cold.items()},
+        tokens_per_s_graph=round(1000.0 / replay_ms, 1),
+        hbm_frac_cold=round(nbytes / (cold["median"] / 1000) / 1e9 / HBM_PEAK_GBS, 4),
+    )
+
+
 def cpu_baseline(name, budget_s=20.0):
     """The oracle's whole-layer forward on the host cores over a bounded token sample."""
     import torch
@@ -266,6 +315,11 @@ def main():
             experts_cold_ms={k: round(v, 4) for k, v in r["experts_cold"].items()},
             hbm_frac_cold=round(r["stage_bytes"] / (tc / 1000) / 1e9 / HBM_PEAK_GBS, 4),
         )
+    decode = {}
+    if not args.only_headline:
+        for name in DECODE_SHAPES:
+            r = measure_decode(name, args.steps, args.warmup)
+            decode[r.pop("shape")] = r
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(head)
@@ -287,6 +341,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "workloads": per,
+        "decode_step": decode,
     }
     print(json.dumps(line), flush=True)
 

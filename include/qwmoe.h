@@ -162,6 +162,32 @@ int qw_moe_forward(const void* x, int act_dtype, int64_t tokens, int64_t d_model
                    int32_t* totals, int32_t* dropped_token, int32_t* dropped_expert, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/* One decode step of a MoE layer, the routed-expert lines of
+ * FastDecoder._step (src/fast_decode.py:170-177), with the experts kept in
+ * their stored format (the reference stacks dense dequantised copies,
+ * src/fast_decode.py:64-73, :121-123):
+ *   scores = x @ router_w^T / temperature           (fp32, x and router_w fp32)
+ *   probs = softmax(scores)
+ *   idx = topk(scores + expert_bias, top_k)          (scores alone with no bias;
+ *                                                      equal keys: lower expert)
+ *   w = probs[idx] / sum(probs[idx])
+ *   y_j = down(silu(gate(x_c)) * up(x_c)) of expert idx_j, x_c = x in
+ *         compute_dtype (QW_BF16: round to nearest even; QW_F32: x itself)
+ *   out = residual + ((y_0 * w_0 + y_1 * w_1) + ...)  (fp32; no residual when NULL)
+ * No capacity: every route is evaluated.  x, residual, out: fp32 [tokens, d_model];
+ * out may be residual (in place).  probs [tokens, experts] may be NULL; top_idx
+ * and top_w [tokens, top_k] are required.  Nothing is allocated, copied to the
+ * host or cleared with a memset, so the call can be captured in a HIP graph. */
+size_t qw_moe_decode_step_workspace_bytes(int64_t tokens, int64_t d_model, int64_t experts, int64_t top_k,
+                                          int64_t d_ff, int compute_dtype);
+int qw_moe_decode_step(const float* x, const float* residual, int64_t tokens, int64_t d_model,
+                       const float* router_w, float temperature, const float* expert_bias, int64_t experts,
+                       int64_t top_k, int64_t d_ff, int compute_dtype, int w_format, int64_t group_in,
+                       int64_t group_ff, const void* gate_w, const float* gate_scales, const void* up_w,
+                       const float* up_scales, const void* down_w, const float* down_scales, float* out,
+                       float* probs, int32_t* top_idx, float* top_w, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
 /* Weight-only quantisation, QuantizedLinear.from_linear
  * (src/quantization.py:43-59): w [out, in] fp32 or bf16 is zero-padded to
  * padded = ceil(in/group)*group columns; per group scale =

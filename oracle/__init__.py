@@ -51,6 +51,7 @@ def lib() -> ctypes.CDLL:
         L.orc_expf.argtypes, L.orc_expf.restype = [f32], f32
         L.orc_softmax_row.argtypes = [P, i32, P]
         L.orc_route_from_logits.argtypes = [P, i32, i32, i32, P, P, P, P]
+        L.orc_route_select.argtypes = [P, i32, i32, i32, P, i32, P, P, P]
         L.orc_router_logits.argtypes = [P, P, i32, i32, i32, f32, P]
         L.orc_capacity.argtypes, L.orc_capacity.restype = [i64, i64, i64, f64, f64, i64, i32], i64
         L.orc_plan.argtypes = [P, P, i32, i32, i32, i64, P, P, P, P, P, P, P, P, P]
@@ -121,15 +122,23 @@ def router_logits(x: np.ndarray, w: np.ndarray, temperature: float = 1.0) -> np.
     return out
 
 
-def route_from_logits(logits: np.ndarray, top_k: int, expert_bias: np.ndarray | None = None):
-    """src/quantweave_moe_model.py:129-137.  Returns (probs, top_idx int32, top_w)."""
+def route_from_logits(logits: np.ndarray, top_k: int, expert_bias: np.ndarray | None = None,
+                      select: str = "probs"):
+    """src/quantweave_moe_model.py:129-137.  Returns (probs, top_idx int32, top_w).
+
+    select="logits" is the decode step's selection (src/fast_decode.py:172):
+    top-k of the scores (plus the bias, if any) rather than of the
+    probabilities; it differs only where rounded probabilities tie."""
+    if select not in ("probs", "logits"):
+        raise ValueError("select must be 'probs' or 'logits'")
     logits = np.ascontiguousarray(logits, dtype=np.float32)
     T, E = logits.shape
     probs = np.empty((T, E), dtype=np.float32)
     idx = np.empty((T, top_k), dtype=np.int32)
     w = np.empty((T, top_k), dtype=np.float32)
     bias = None if expert_bias is None else np.ascontiguousarray(expert_bias, dtype=np.float32)
-    lib().orc_route_from_logits(_ptr(logits), T, E, top_k, _ptr(bias), _ptr(probs), _ptr(idx), _ptr(w))
+    lib().orc_route_select(_ptr(logits), T, E, top_k, _ptr(bias), int(select == "logits"), _ptr(probs), _ptr(idx),
+                           _ptr(w))
     return probs, idx, w
 
 
@@ -259,6 +268,35 @@ def combine(y_rows: np.ndarray, slot_token: np.ndarray, slot_weight: np.ndarray,
     for s, t in enumerate(slot_token.tolist()):
         out[t] = round_act(out[t] + contrib[s], dtype)
     return out
+
+
+def decode_step(x: np.ndarray, router_w: np.ndarray, w: dict, *, top_k: int, dtype: str, temperature: float = 1.0,
+                expert_bias: np.ndarray | None = None, residual: np.ndarray | None = None,
+                logits: np.ndarray | None = None, accum: str = "f64"):
+    """The routed-expert lines of FastDecoder._step, src/fast_decode.py:170-177.
+
+    x [T, d] fp32 (the normed hidden state), router_w fp32 [E, d].  Routing in
+    fp32 with selection on the scores (:171-174); every route is evaluated (no
+    capacity); expert inputs are x rounded to `dtype` (:174); each expert's
+    SwiGLU in `dtype` (:175-177, the weights as `expert_weights` gives them);
+    then out = residual + sum_j float(y_j) * w_j in fp32, in top-k order.
+    Returns a dict with logits, probs, top_idx, top_w, y [T, k, d] and out."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, d = x.shape
+    if logits is None:
+        logits = router_logits(x, router_w, temperature)
+    probs, idx, tw = route_from_logits(logits, top_k, expert_bias, select="logits")
+    xc = round_act(x, dtype)
+    y = np.zeros((T, top_k, d), dtype=np.float32)
+    for e in np.unique(idx).tolist():
+        tok, j = np.nonzero(idx == e)
+        g, u, dn = expert_weights(w, e, dtype)
+        y[tok, j] = swiglu(xc[tok], g, u, dn, dtype, accum)
+    acc = np.zeros((T, d), dtype=np.float32)
+    for j in range(top_k):
+        acc = (acc + y[:, j] * tw[:, j:j + 1]).astype(np.float32)
+    out = acc if residual is None else (np.asarray(residual, np.float32) + acc).astype(np.float32)
+    return dict(logits=logits, probs=probs, top_idx=idx, top_w=tw, y=y, out=out)
 
 
 def moe_forward(x: np.ndarray, router_w: np.ndarray, w: dict, *, top_k: int, cap: int, dtype: str,

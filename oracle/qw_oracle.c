@@ -12,6 +12,9 @@
  *   orc_expf, orc_softmax_row  softmax of src/quantweave_moe_model.py:129 with
  *                              an exactly specified exp and summation order
  *   orc_route_from_logits      :129-137 (softmax, topk / biased topk, renorm)
+ *   orc_route_select           the same with the decode step's selection,
+ *                              src/fast_decode.py:170-174 (topk of the
+ *                              scores, biased or not)
  *   orc_router_logits          :128 (fp32 logits, double accumulation)
  *   orc_capacity               :100-111
  *   orc_plan                   :166-188 (two stable argsorts == one stable
@@ -96,11 +99,12 @@ static uint32_t sort_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-/* probs = softmax(logits); indices = topk(probs or logits+bias, k) in
- * descending order, equal keys by ascending expert index; w = probs[idx];
+/* probs = softmax(logits); indices = topk(key, k) in descending order, equal
+ * keys by ascending expert index, with key = logits + bias when a bias is
+ * given, else logits when select_logits, else probs; w = probs[idx];
  * top_w = w / (((w0 + w1) + w2) + ...). */
-void orc_route_from_logits(const float* logits, int T, int E, int K, const float* bias, float* probs,
-                           int32_t* top_idx, float* top_w) {
+void orc_route_select(const float* logits, int T, int E, int K, const float* bias, int select_logits,
+                      float* probs, int32_t* top_idx, float* top_w) {
   uint32_t* key = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)E);
   char* taken = (char*)malloc((size_t)E);
   for (int t = 0; t < T; ++t) {
@@ -108,7 +112,7 @@ void orc_route_from_logits(const float* logits, int T, int E, int K, const float
     float* p = probs + (size_t)t * E;
     orc_softmax_row(l, E, p);
     for (int e = 0; e < E; ++e) {
-      key[e] = sort_key(bias ? l[e] + bias[e] : p[e]);
+      key[e] = sort_key(bias ? l[e] + bias[e] : (select_logits ? l[e] : p[e]));
       taken[e] = 0;
     }
     float sum = 0.0f;
@@ -127,6 +131,11 @@ void orc_route_from_logits(const float* logits, int T, int E, int K, const float
   }
   free(key);
   free(taken);
+}
+
+void orc_route_from_logits(const float* logits, int T, int E, int K, const float* bias, float* probs,
+                           int32_t* top_idx, float* top_w) {
+  orc_route_select(logits, T, E, K, bias, 0, probs, top_idx, top_w);
 }
 
 /* logits[t, e] = (sum_k x[t,k] * w[e,k], in double, rounded to float) / temperature */

@@ -8,13 +8,16 @@ Drop-in Python surface over the C ABI in include/qwmoe.h:
   ``GroupedPlan``, ``grouped_matmul``, ``grouped_swiglu``, ``compute_dtype``,
   ``benchmark`` (src/moe_kernels.py)
 * ``QuantizedLinear``, ``quantize_model`` (src/quantization.py)
+* ``MoEDecodeStep``: the routed experts of FastDecoder's one-token step
+  (src/fast_decode.py:170-177), capturable in a HIP graph
 """
 
 from . import moe_kernels
+from .decode import MoEDecodeStep
 from .moe import QuantaWeaveConfig, SparseSwiGLU, TopKMoE, set_moe_kernel
 from .quantization import QuantizedLinear, quantize_model
 
 __all__ = [
     "QuantaWeaveConfig", "SparseSwiGLU", "TopKMoE", "set_moe_kernel", "QuantizedLinear", "quantize_model",
-    "moe_kernels",
+    "moe_kernels", "MoEDecodeStep",
 ]

@@ -25,7 +25,7 @@ void clear_error() { g_error[0] = '\0'; }
 // Implemented in the kernel files.
 int route(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int64_t T, int64_t D, int64_t E,
           int64_t K, float temperature, const float* bias, float* logits, float* probs, int32_t* top_idx,
-          float* top_w, float* partial, size_t partial_bytes, hipStream_t stream);
+          float* top_w, float* partial, size_t partial_bytes, hipStream_t stream, bool select_logits = false);
 size_t route_workspace_bytes(int64_t T, int64_t D, int64_t E);
 int route_from_logits(const float* logits, int64_t T, int64_t E, int64_t K, const float* bias, float* probs,
                       int32_t* top_idx, float* top_w, hipStream_t stream);
@@ -38,6 +38,9 @@ int permute(const void* x, int dtype, int64_t D, const int32_t* slot_token, cons
             void* out, hipStream_t stream);
 int combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, int64_t T, int64_t K,
             int64_t D, void* out, hipStream_t stream);
+int decode_combine(const void* y, int dtype, const int32_t* route_slot, const float* top_w, const float* residual,
+                   int64_t T, int64_t K, int64_t D, float* out, hipStream_t stream);
+int cast_bf16(const float* x, int64_t n, uint16_t* out, hipStream_t stream);
 int balance(const float* probs, const int32_t* counts, int64_t T, int64_t K, int64_t E, float* importance,
             float* bal, hipStream_t stream, float* scratch_importance);
 int quantize(const void* w, int wdt, int64_t rows, int64_t cols, int bits, int64_t group, void* qweight, float* scales,
@@ -130,6 +133,50 @@ size_t forward_workspace_bytes(int64_t T, int64_t D, int64_t E, int64_t K, int64
   c.take<char>(experts_workspace_bytes(R, E, D, F, act));
   c.take<char>(route_workspace_bytes(T, D, E));
   return c.used + 256;
+}
+
+// The decode step keeps its plan in the workspace: one carve serves both the
+// size query and the call.
+struct DecodeWs {
+  float* logits;
+  int32_t *counts, *kept_counts, *kept_offsets, *totals;
+  int32_t *slot_token, *route_slot, *dropped_token, *dropped_expert;
+  float* slot_weight;
+  uint16_t* xc;
+  char* y;
+  char* plan_ws;
+  size_t plan_bytes;
+  char* exp_ws;
+  size_t exp_bytes;
+  float* route_ws;
+  size_t route_bytes;
+  size_t used;
+};
+
+static DecodeWs carve_decode(void* base, int64_t T, int64_t D, int64_t E, int64_t K, int64_t F, int act) {
+  const int64_t R = T * K;
+  Carver c(base);
+  DecodeWs w{};
+  w.logits = c.take<float>(static_cast<size_t>(T) * E);
+  w.counts = c.take<int32_t>(E);
+  w.kept_counts = c.take<int32_t>(E);
+  w.kept_offsets = c.take<int32_t>(E + 1);
+  w.totals = c.take<int32_t>(2);
+  w.slot_token = c.take<int32_t>(R);
+  w.route_slot = c.take<int32_t>(R);
+  w.dropped_token = c.take<int32_t>(R);
+  w.dropped_expert = c.take<int32_t>(R);
+  w.slot_weight = c.take<float>(R);
+  w.xc = act == QW_BF16 ? c.take<uint16_t>(static_cast<size_t>(T) * D) : nullptr;
+  w.y = c.take<char>(static_cast<size_t>(R) * D * act_size(act));
+  w.plan_bytes = plan_workspace_bytes(T, K, E);
+  w.plan_ws = c.take<char>(w.plan_bytes);
+  w.exp_bytes = experts_workspace_bytes(R, E, D, F, act);
+  w.exp_ws = c.take<char>(w.exp_bytes);
+  w.route_bytes = route_workspace_bytes(T, D, E);
+  w.route_ws = reinterpret_cast<float*>(c.take<char>(w.route_bytes));
+  w.used = c.used + 256;
+  return w;
 }
 
 }  // namespace qw
@@ -293,6 +340,54 @@ int qw_moe_forward(const void* x, int act_dtype, int64_t tokens, int64_t d_model
     if (st) return st;
   }
   return combine(y, act_dtype, route_slot, top_idx, tokens, top_k, d_model, out, s);
+}
+
+size_t qw_moe_decode_step_workspace_bytes(int64_t tokens, int64_t d_model, int64_t experts, int64_t top_k,
+                                          int64_t d_ff, int compute_dtype) {
+  if (tokens < 0 || d_model < 1 || experts < 1 || top_k < 1 || d_ff < 1) return 0;
+  if (compute_dtype != QW_F32 && compute_dtype != QW_BF16) return 0;
+  return carve_decode(nullptr, tokens, d_model, experts, top_k, d_ff, compute_dtype).used;
+}
+
+int qw_moe_decode_step(const float* x, const float* residual, int64_t tokens, int64_t d_model,
+                       const float* router_w, float temperature, const float* expert_bias, int64_t experts,
+                       int64_t top_k, int64_t d_ff, int compute_dtype, int w_format, int64_t group_in,
+                       int64_t group_ff, const void* gate_w, const float* gate_scales, const void* up_w,
+                       const float* up_scales, const void* down_w, const float* down_scales, float* out,
+                       float* probs, int32_t* top_idx, float* top_w, void* workspace, size_t workspace_bytes,
+                       void* stream) {
+  clear_error();
+  QW_REQUIRE(compute_dtype == QW_F32 || compute_dtype == QW_BF16, "compute dtype must be f32 or bf16");
+  QW_REQUIRE(tokens >= 0 && top_k >= 1 && experts >= 1 && d_model >= 1 && d_ff >= 1, "bad decode step sizes");
+  QW_REQUIRE(top_k <= experts, "top_k must be between 1 and num_experts (got %lld, %lld)", (long long)top_k,
+             (long long)experts);
+  if (tokens == 0) return QW_OK;
+  QW_REQUIRE(x && router_w && out && top_idx && top_w, "x, router_w, out, top_idx and top_w are required");
+  const DecodeWs need = carve_decode(nullptr, tokens, d_model, experts, top_k, d_ff, compute_dtype);
+  if (!workspace || workspace_bytes < need.used)
+    return set_error(QW_ERR_WORKSPACE, "decode step workspace needs %zu bytes, got %zu", need.used, workspace_bytes);
+  hipStream_t s = as_stream(stream);
+  const int64_t R = tokens * top_k;
+  const DecodeWs w = carve_decode(workspace, tokens, d_model, experts, top_k, d_ff, compute_dtype);
+  int st = route(x, QW_F32, d_model, router_w, QW_F32, tokens, d_model, experts, top_k, temperature, expert_bias,
+                 w.logits, probs, top_idx, top_w, w.route_ws, w.route_bytes, s, /*select_logits=*/true);
+  if (st) return st;
+  // capacity R: every route keeps its slot
+  st = plan(top_idx, top_w, tokens, top_k, experts, R, w.counts, w.kept_counts, w.kept_offsets, w.slot_token,
+            w.slot_weight, w.route_slot, w.dropped_token, w.dropped_expert, w.totals, w.plan_ws, w.plan_bytes, s);
+  if (st) return st;
+  const void* xc = x;
+  if (compute_dtype == QW_BF16) {
+    st = cast_bf16(x, tokens * d_model, w.xc, s);
+    if (st) return st;
+    xc = w.xc;
+  }
+  const int64_t avg = (R + experts - 1) / experts;
+  st = qw::experts(xc, compute_dtype, w.slot_token, w.kept_offsets, experts, d_model, d_ff, R, w_format, group_in,
+                   group_ff, gate_w, gate_scales, up_w, up_scales, down_w, down_scales, nullptr, w.y, w.exp_ws,
+                   w.exp_bytes, s, avg, std::min<int64_t>(tokens, R));
+  if (st) return st;
+  return decode_combine(w.y, compute_dtype, w.route_slot, top_w, residual, tokens, top_k, d_model, out, s);
 }
 
 int qw_quantize(const void* w, int w_dtype, int64_t out_features, int64_t in_features, int bits, int64_t group_size,

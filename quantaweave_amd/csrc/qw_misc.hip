@@ -154,6 +154,109 @@ int combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* 
 }
 
 // ---------------------------------------------------------------------------
+// Decode-step combine, the last line of the one-token MoE step
+// (src/fast_decode.py:177):
+//   out[t] = residual[t] + ((y_0 * w_0 + y_1 * w_1) + ...)
+// with y_j the expert output row of route j of token t (activation dtype,
+// widened to fp32), w_j its renormalised router weight, products and sums
+// rounded in fp32 in top-k order, and no rounding to the activation dtype.
+// Routes without a slot (route_slot < 0) add nothing.  One block per token;
+// `out` may be `residual` (each element is read, then written, by one thread).
+// ---------------------------------------------------------------------------
+template <int ACT, int VEC>
+__global__ __launch_bounds__(256) void decode_combine_kernel(const void* __restrict__ y,
+                                                             const int32_t* __restrict__ route_slot,
+                                                             const float* __restrict__ top_w, const float* residual,
+                                                             int K, int D, float* out) {
+  const int t = blockIdx.x;
+  const int64_t row = static_cast<int64_t>(t) * D;
+  for (int c = threadIdx.x * VEC; c < D; c += blockDim.x * VEC) {
+    float acc[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
+    for (int j = 0; j < K; ++j) {
+      const int s = route_slot[static_cast<int64_t>(t) * K + j];
+      if (s < 0) continue;
+      const float w = top_w[static_cast<int64_t>(t) * K + j];
+      const int64_t src = static_cast<int64_t>(s) * D + c;
+      float yv[VEC];
+      if constexpr (VEC == 8 && ACT == QW_BF16) {
+        const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(y) + src);
+        const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          yv[2 * v] = __uint_as_float(w4[v] << 16);
+          yv[2 * v + 1] = __uint_as_float(w4[v] & 0xffff0000u);
+        }
+      } else if constexpr (VEC == 4 && ACT == QW_F32) {
+        const float4 q = *reinterpret_cast<const float4*>(static_cast<const float*>(y) + src);
+        yv[0] = q.x;
+        yv[1] = q.y;
+        yv[2] = q.z;
+        yv[3] = q.w;
+      } else {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) yv[v] = load_act<ACT>(y, src + v);
+      }
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[v] = __fadd_rn(acc[v], __fmul_rn(yv[v], w));
+    }
+    if (residual != nullptr) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[v] = __fadd_rn(residual[row + c + v], acc[v]);
+    }
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) out[row + c + v] = acc[v];
+  }
+}
+
+int decode_combine(const void* y, int dtype, const int32_t* route_slot, const float* top_w, const float* residual,
+                   int64_t T, int64_t K, int64_t D, float* out, hipStream_t stream) {
+  QW_REQUIRE(dtype == QW_F32 || dtype == QW_BF16, "decode combine dtype must be f32 or bf16");
+  QW_REQUIRE(T >= 0 && T <= INT32_MAX && K >= 1 && D >= 1 && D <= INT32_MAX, "bad decode combine sizes");
+  if (T == 0) return QW_OK;
+  QW_REQUIRE(y && route_slot && top_w && out, "decode combine pointers are required");
+  const unsigned g = static_cast<unsigned>(T);
+  const int k = static_cast<int>(K), d = static_cast<int>(D);
+  if (dtype == QW_BF16 && d % 8 == 0)
+    decode_combine_kernel<QW_BF16, 8><<<g, 256, 0, stream>>>(y, route_slot, top_w, residual, k, d, out);
+  else if (dtype == QW_BF16)
+    decode_combine_kernel<QW_BF16, 1><<<g, 256, 0, stream>>>(y, route_slot, top_w, residual, k, d, out);
+  else if (d % 4 == 0)
+    decode_combine_kernel<QW_F32, 4><<<g, 256, 0, stream>>>(y, route_slot, top_w, residual, k, d, out);
+  else
+    decode_combine_kernel<QW_F32, 1><<<g, 256, 0, stream>>>(y, route_slot, top_w, residual, k, d, out);
+  QW_LAUNCH_CHECK("decode_combine_kernel");
+  return QW_OK;
+}
+
+// fp32 -> bf16, round to nearest even (`normed.to(torch.bfloat16)`,
+// src/fast_decode.py:174).  Four elements per thread when n % 4 == 0.
+__global__ __launch_bounds__(256) void cast_bf16_kernel(const float* __restrict__ x, int64_t n,
+                                                        uint16_t* __restrict__ out) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  if (i >= n) return;
+  if ((n & 3) == 0) {
+    const float4 v = *reinterpret_cast<const float4*>(x + i);
+    uint2 o;
+    o.x = f32_to_bf16(v.x) | (static_cast<uint32_t>(f32_to_bf16(v.y)) << 16);
+    o.y = f32_to_bf16(v.z) | (static_cast<uint32_t>(f32_to_bf16(v.w)) << 16);
+    *reinterpret_cast<uint2*>(out + i) = o;
+  } else {
+    for (int64_t j = i; j < i + 4 && j < n; ++j) out[j] = f32_to_bf16(x[j]);
+  }
+}
+
+int cast_bf16(const float* x, int64_t n, uint16_t* out, hipStream_t stream) {
+  QW_REQUIRE(n >= 0, "bad cast size");
+  if (n == 0) return QW_OK;
+  QW_REQUIRE(x && out, "cast pointers are required");
+  cast_bf16_kernel<<<static_cast<unsigned>(ceil_div(ceil_div(n, 4), 256)), 256, 0, stream>>>(x, n, out);
+  QW_LAUNCH_CHECK("cast_bf16_kernel");
+  return QW_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Balance loss (src/quantweave_moe_model.py:152-154).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void importance_kernel(const float* __restrict__ probs, int T, int E,

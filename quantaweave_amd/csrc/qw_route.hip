@@ -186,8 +186,9 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const uint16_t* __rest
 //   S = (per-lane sequential sum over its experts in index order) reduced by
 //       the xor butterfly with lane offsets 32, 16, 8, 4, 2, 1
 //   p_e = q_e / S
-//   top-k: k rounds of a wave argmax on (key desc, expert asc), key = p_e
-//          (or L_e + bias_e when a bias is given)
+//   top-k: k rounds of a wave argmax on (key desc, expert asc), key = p_e,
+//          or L_e + bias_e when a bias is given, or L_e when `select_logits`
+//          is set and there is no bias (the decode step's selection)
 //   w_j = p_{idx_j} / (((p_{idx_0} + p_{idx_1}) + p_{idx_2}) + ...)
 // ---------------------------------------------------------------------------
 //
@@ -198,7 +199,8 @@ template <int EPL>
 __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ partial, int splits,
                                                          float temperature, float* __restrict__ logits, int T, int E,
                                                          int K, const float* __restrict__ bias,
-                                                         float* __restrict__ probs, int32_t* __restrict__ top_idx,
+                                                         int select_logits, float* __restrict__ probs,
+                                                         int32_t* __restrict__ top_idx,
                                                          float* __restrict__ top_w) {
   const int lane = threadIdx.x % kWave;
   const int t = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
@@ -250,7 +252,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
 #pragma unroll
   for (int c = 0; c < EPL; ++c) {
     const int e = lane + c * kWave;
-    const float v = (bias != nullptr && e < E) ? l[c] + bias[e] : p[c];
+    const float v = (bias != nullptr && e < E) ? l[c] + bias[e] : (select_logits ? l[c] : p[c]);
     key[c] = (e < E) ? sortable_key(v) : 0u;
   }
   uint32_t taken = 0;
@@ -294,14 +296,15 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
 }
 
 static int launch_topk(const float* partial, int splits, float temperature, float* logits, int T, int E, int K,
-                       const float* bias, float* probs, int32_t* top_idx, float* top_w, hipStream_t stream) {
+                       const float* bias, int select_logits, float* probs, int32_t* top_idx, float* top_w,
+                       hipStream_t stream) {
   const int waves_per_block = 4;
   const dim3 grid(static_cast<unsigned>(ceil_div(T, waves_per_block)));
   const dim3 block(waves_per_block * kWave);
   const int epl = static_cast<int>(ceil_div(E, kWave));
 #define QW_TK(N)                                                                                               \
-  route_topk_kernel<N><<<grid, block, 0, stream>>>(partial, splits, temperature, logits, T, E, K, bias, probs, \
-                                                   top_idx, top_w)
+  route_topk_kernel<N><<<grid, block, 0, stream>>>(partial, splits, temperature, logits, T, E, K, bias, \
+                                                   select_logits, probs, top_idx, top_w)
   if (epl <= 1) QW_TK(1);
   else if (epl <= 2) QW_TK(2);
   else if (epl <= 4) QW_TK(4);
@@ -328,7 +331,7 @@ int route_from_logits(const float* logits, int64_t T, int64_t E, int64_t K, cons
   if (T == 0) return QW_OK;
   QW_REQUIRE(logits && top_idx && top_w, "logits, top_idx and top_w are required");
   return launch_topk(nullptr, 0, 1.0f, const_cast<float*>(logits), static_cast<int>(T), static_cast<int>(E),
-                     static_cast<int>(K), bias, probs, top_idx, top_w, stream);
+                     static_cast<int>(K), bias, 0, probs, top_idx, top_w, stream);
 }
 
 // Split count for the router GEMM: enough blocks to cover the chip, each
@@ -346,7 +349,7 @@ size_t route_workspace_bytes(int64_t T, int64_t D, int64_t E) {
 
 int route(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int64_t T, int64_t D, int64_t E,
           int64_t K, float temperature, const float* bias, float* logits, float* probs, int32_t* top_idx,
-          float* top_w, float* partial, size_t partial_bytes, hipStream_t stream) {
+          float* top_w, float* partial, size_t partial_bytes, hipStream_t stream, bool select_logits) {
   int st = route_validate(T, E, K);
   if (st) return st;
   QW_REQUIRE(xdt == QW_F32 || xdt == QW_BF16, "router input dtype must be f32 or bf16");
@@ -378,8 +381,8 @@ int route(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int6
 #undef QW_RL
     QW_LAUNCH_CHECK("router_logits_kernel");
   }
-  return launch_topk(partial, splits, temperature, logits, t, e, static_cast<int>(K), bias, probs, top_idx, top_w,
-                     stream);
+  return launch_topk(partial, splits, temperature, logits, t, e, static_cast<int>(K), bias, select_logits ? 1 : 0,
+                     probs, top_idx, top_w, stream);
 }
 
 }  // namespace qw

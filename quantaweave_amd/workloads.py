@@ -224,3 +224,37 @@ class LayerRunner:
             n *= s
         nbytes = n * torch.empty((), dtype=dt).element_size()
         return self.ws[start:start + nbytes].view(dt).view(*shape)
+
+
+class DecodeRunner:
+    """Preallocated buffers for repeated qw_moe_decode_step calls on one layer:
+    `tokens` rows of fp32 normed input, the fp32 router (the layer's router
+    widened), the layer's experts in their stored format, bf16 compute."""
+
+    def __init__(self, layer: Layer, tokens: int = 1, seed: int = 0) -> None:
+        w = layer.w
+        dev = layer.x.device
+        self.layer = layer
+        self.tokens = tokens
+        T, E, K = tokens, w.experts, w.top_k
+        g = torch.Generator(device=dev)
+        g.manual_seed(w.seed + 100 + seed)
+        self.x = torch.randn(T, w.d_model, generator=g, device=dev)
+        self.residual = torch.randn(T, w.d_model, generator=g, device=dev)
+        self.router = layer.router.float().contiguous()
+        self.out = torch.empty(T, w.d_model, dtype=torch.float32, device=dev)
+        self.probs = torch.empty(T, E, dtype=torch.float32, device=dev)
+        self.top_idx = torch.empty(T, K, dtype=torch.int32, device=dev)
+        self.top_w = torch.empty(T, K, dtype=torch.float32, device=dev)
+        self.ws_bytes = _lib.load().qw_moe_decode_step_workspace_bytes(T, w.d_model, E, K, w.d_ff, _lib.QW_BF16)
+        self.ws = _hip.workspace(self.ws_bytes, dev)
+        self._fn = _lib.load().qw_moe_decode_step
+        self._head = [_hip.ptr(self.x), _hip.ptr(self.residual), T, w.d_model, _hip.ptr(self.router), 1.0,
+                      _hip.ptr(layer.bias), E, K, w.d_ff, _lib.QW_BF16, *layer.weight_args(), _hip.ptr(self.out),
+                      _hip.ptr(self.probs), _hip.ptr(self.top_idx), _hip.ptr(self.top_w), _hip.ptr(self.ws),
+                      self.ws_bytes]
+
+    def __call__(self) -> None:
+        st = self._fn(*self._head, _hip.stream(self.x.device))
+        if st:
+            _lib.check(st, "qw_moe_decode_step")

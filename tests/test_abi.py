@@ -71,3 +71,24 @@ def test_workspace_sizes_are_positive_and_monotone():
     assert 0 < a < b
     assert lib.qw_moe_plan_workspace_bytes(8192, 2, 64) > 8192 * 2 * 8
     assert lib.qw_moe_experts_workspace_bytes(100, 8, 64, 128, _lib.QW_BF16) >= 100 * 128 * 2
+
+
+def test_decode_step_validation_and_workspace():
+    lib = _lib.load()
+    # fp16 is not a compute dtype; top_k > experts; missing workspace
+    st = lib.qw_moe_decode_step(None, None, 1, 64, None, 1.0, None, 8, 2, 32, 5, _lib.QW_BF16, 0, 0,
+                                None, None, None, None, None, None, None, None, None, None, None, 0, None)
+    assert st == _lib.QW_ERR_INVALID and b"compute dtype" in lib.qw_last_error()
+    st = lib.qw_moe_decode_step(None, None, 1, 64, None, 1.0, None, 8, 9, 32, _lib.QW_BF16, _lib.QW_BF16, 0, 0,
+                                None, None, None, None, None, None, None, None, None, None, None, 0, None)
+    assert st == _lib.QW_ERR_INVALID and b"top_k" in lib.qw_last_error()
+    fake = ctypes.c_void_p(16)    # never dereferenced: the workspace check fails first
+    st = lib.qw_moe_decode_step(fake, None, 1, 64, fake, 1.0, None, 8, 2, 32, _lib.QW_BF16, _lib.QW_BF16, 0, 0,
+                                fake, None, fake, None, fake, None, fake, None, fake, fake, fake, 16, None)
+    assert st == _lib.QW_ERR_WORKSPACE and b"workspace" in lib.qw_last_error()
+    # zero tokens is a no-op that touches nothing
+    assert lib.qw_moe_decode_step(None, None, 0, 64, None, 1.0, None, 8, 2, 32, _lib.QW_BF16, _lib.QW_BF16, 0, 0,
+                                  None, None, None, None, None, None, None, None, None, None, None, 0, None) == 0
+    one = lib.qw_moe_decode_step_workspace_bytes(1, 4096, 64, 2, 1408, _lib.QW_BF16)
+    assert 0 < one < lib.qw_moe_decode_step_workspace_bytes(16, 4096, 64, 2, 1408, _lib.QW_BF16)
+    assert lib.qw_moe_decode_step_workspace_bytes(1, 4096, 64, 2, 1408, 7) == 0

@@ -89,3 +89,14 @@ def test_compute_dtype_rule():
     assert mk.compute_dtype(x) == torch.float32
     with torch.autocast("cpu", dtype=torch.bfloat16):
         assert mk.compute_dtype(x) == torch.bfloat16
+
+
+def test_decode_step_refuses_cpu_and_fp16():
+    moe = qa.TopKMoE(small_config())
+    with pytest.raises(RuntimeError, match="ROCm"):
+        qa.MoEDecodeStep(moe, device=torch.device("cpu"))
+    from quantaweave_amd.decode import precision_dtype
+    assert precision_dtype(torch.device("cuda"), "auto") == torch.bfloat16
+    assert precision_dtype(torch.device("cpu"), "auto") == torch.float32
+    with pytest.raises(ValueError, match="fp16"):
+        precision_dtype(torch.device("cuda"), "fp16")

@@ -353,3 +353,121 @@ def test_quantized_expert_weights_follow_dequantize_then_cast():
     g, u, d = oracle.expert_weights(w, 1, "bf16")
     assert np.array_equal(g, oracle.round_bf16(oracle.dequantize(qs[1][0], qs[1][1], 4, D, 32)))
     assert np.abs(g - gate[1]).max() <= np.abs(gate[1]).max() / 7 * 0.5 + 1e-3
+
+
+# ---------------------------------------------------------------- decode step (src/fast_decode.py:170-177)
+def test_decode_selection_uses_the_scores_where_probabilities_tie():
+    # exp(-201) and exp(-200) both underflow to zero in fp32: the probabilities
+    # of experts 0 and 1 tie (training picks the lower index), the scores do not
+    logits = np.array([[-201.0, -200.0, 0.0]], np.float32)
+    _, idx_train, _ = oracle.route_from_logits(logits, 2)
+    _, idx_dec, w_dec = oracle.route_from_logits(logits, 2, select="logits")
+    assert idx_train.tolist() == [[2, 0]]
+    assert idx_dec.tolist() == [[2, 1]] == torch.from_numpy(logits).topk(2).indices.tolist()
+    assert w_dec.tolist() == [[1.0, 0.0]]
+
+
+def test_decode_selection_is_torch_topk_of_the_scores():
+    rng = np.random.RandomState(21)
+    logits = (rng.randn(300, 16) * 3).astype(np.float32)
+    bias = rng.randn(16).astype(np.float32)
+    for b in (None, bias):
+        scores = torch.from_numpy(logits) + (0 if b is None else torch.from_numpy(b))
+        _, idx, w = oracle.route_from_logits(logits, 3, b, select="logits")
+        assert np.array_equal(idx, scores.topk(3, dim=-1).indices.numpy())
+        # same selection as training on untied inputs; weights always from the probabilities
+        _, idx_t, w_t = oracle.route_from_logits(logits, 3, b)
+        assert np.array_equal(idx, idx_t) and np.array_equal(w, w_t)
+
+
+def _decode_layer(rng, E, D, F_, fmt, group=None):
+    w32 = dict(gate=(rng.randn(E, F_, D) * 0.2).astype(np.float32), up=(rng.randn(E, F_, D) * 0.2).astype(np.float32),
+               down=(rng.randn(E, D, F_) * 0.2).astype(np.float32))
+    if fmt in ("f32", "bf16"):
+        cast = (lambda a: a) if fmt == "f32" else oracle.round_bf16
+        return dict(format=fmt, d_model=D, d_ff=F_, **{k: cast(v) for k, v in w32.items()}), None
+    bits = 8 if fmt == "i8" else 4
+    w = dict(format=fmt, d_model=D, d_ff=F_)
+    for name, a in w32.items():
+        qs = [oracle.quantize(a[e], bits, group) for e in range(E)]
+        w[name] = np.stack([q for q, _, _ in qs])
+        w[name + "_scales"] = np.stack([s for _, s, _ in qs])
+        w["group_in" if name != "down" else "group_ff"] = qs[0][2]
+    dense = {n: np.stack([oracle.dequantize(w[n][e], w[n + "_scales"][e], bits, a.shape[2],
+                                            w["group_in" if n != "down" else "group_ff"]) for e in range(E)])
+             for n, a in w32.items()}
+    return w, dense
+
+
+def torch_decode_step(x, router_w, stacks, top_k, temperature, bias, dtype, residual):
+    """The MoE lines of FastDecoder._step (src/fast_decode.py:170-177) in torch,
+    one token at a time as the reference steps; stacks are [E, out, in]."""
+    normed = torch.from_numpy(x)
+    scores = F.linear(normed, torch.from_numpy(router_w)) / temperature
+    probabilities = scores.softmax(dim=-1)
+    chosen = (scores + torch.from_numpy(bias) if bias is not None else scores).topk(top_k, dim=-1).indices
+    weights = probabilities.gather(1, chosen)
+    weights = weights / weights.sum(dim=-1, keepdim=True)
+    G, U, Dn = (torch.from_numpy(stacks[n]).to(dtype) for n in ("gate", "up", "down"))
+    out = torch.from_numpy(residual).clone()
+    for t in range(normed.size(0)):
+        picked = chosen[t]
+        inputs = normed[t].to(dtype)
+        gate = torch.einsum("kfh,h->kf", G[picked], inputs)
+        up = torch.einsum("kfh,h->kf", U[picked], inputs)
+        expert_out = torch.einsum("khf,kf->kh", Dn[picked], F.silu(gate) * up)
+        out[t] = out[t] + (expert_out.float() * weights[t][:, None]).sum(dim=0)
+    return chosen.numpy(), out.numpy()
+
+
+@pytest.mark.parametrize("fmt,dtype", [("f32", "f32"), ("bf16", "bf16"), ("i8", "bf16"), ("u4", "bf16")])
+def test_decode_step_matches_the_reference_step_in_torch(fmt, dtype):
+    rng = np.random.RandomState(31)
+    T, D, F_, E, k = 5, 64, 96, 8, 2
+    w, dense = _decode_layer(rng, E, D, F_, fmt, group=32 if fmt == "u4" else None)
+    x = rng.randn(T, D).astype(np.float32)
+    rw = (rng.randn(E, D) * 0.3).astype(np.float32)
+    resid = rng.randn(T, D).astype(np.float32)
+    res = oracle.decode_step(x, rw, w, top_k=k, dtype=dtype, temperature=0.8, residual=resid)
+    stacks = dense if dense is not None else {n: w[n] for n in ("gate", "up", "down")}
+    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    chosen, ref = torch_decode_step(x, rw, stacks, k, 0.8, None, tdt, resid)
+    assert np.array_equal(res["top_idx"], chosen)
+    tol = 1e-5 if dtype == "f32" else 2e-2
+    moe_ref, moe_got = ref - resid, res["out"] - resid
+    assert np.abs(moe_got - moe_ref).max() <= tol * np.abs(moe_ref).max()
+
+
+@pytest.mark.parametrize("top_k,temperature,bias", [(1, 1.0, False), (2, 1.0, False), (2, 0.7, True), (3, 2.0, False)])
+def test_decode_step_reproduces_the_layer_forward_without_capacity(top_k, temperature, bias):
+    """tests/test_fast_decode.py:40-56 at the MoE block: the one-token step and
+    the full forward (capacity off) agree to 1e-5."""
+    rng = np.random.RandomState(40 + top_k)
+    T, D, F_, E = 7, 32, 48, 8
+    w, _ = _decode_layer(rng, E, D, F_, "f32")
+    x = rng.randn(T, D).astype(np.float32)
+    rw = (rng.randn(E, D) * 0.5).astype(np.float32)
+    b = rng.randn(E).astype(np.float32) if bias else None
+    resid = rng.randn(T, D).astype(np.float32)
+    dec = oracle.decode_step(x, rw, w, top_k=top_k, dtype="f32", temperature=temperature, expert_bias=b,
+                             residual=resid)
+    full = oracle.moe_forward(x, rw, w, top_k=top_k, cap=T * top_k, dtype="f32", temperature=temperature,
+                              expert_bias=b)
+    assert np.array_equal(dec["top_idx"], full["top_idx"])
+    assert np.allclose(dec["out"], resid + full["out"], atol=1e-5)
+
+
+def test_decode_step_top1_adds_the_expert_output_exactly():
+    rng = np.random.RandomState(50)
+    T, D, F_, E = 4, 16, 24, 5
+    w, _ = _decode_layer(rng, E, D, F_, "bf16")
+    x = rng.randn(T, D).astype(np.float32)
+    rw = rng.randn(E, D).astype(np.float32)
+    resid = rng.randn(T, D).astype(np.float32)
+    res = oracle.decode_step(x, rw, w, top_k=1, dtype="bf16", residual=resid)
+    assert np.all(res["top_w"] == 1.0)
+    assert np.array_equal(res["out"], resid + res["y"][:, 0])
+    # and the expert output is that expert's SwiGLU on x rounded to bf16
+    e = int(res["top_idx"][2, 0])
+    one = oracle.swiglu(oracle.round_bf16(x[2:3]), w["gate"][e], w["up"][e], w["down"][e], "bf16")
+    assert np.array_equal(res["y"][2, 0], one[0])
