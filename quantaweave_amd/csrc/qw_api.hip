@@ -30,6 +30,14 @@ size_t route_workspace_bytes(int64_t T, int64_t D, int64_t E);
 int route_from_logits(const float* logits, int64_t T, int64_t E, int64_t K, const float* bias, float* probs,
                       int32_t* top_idx, float* top_w, hipStream_t stream);
 size_t plan_workspace_bytes(int64_t T, int64_t K, int64_t E);
+bool route_plan_small_fits(int64_t T, int64_t E, int64_t K);
+int route_plan_small(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int64_t T, int64_t D,
+                     int64_t E, int64_t K, float temperature, const float* bias, bool select_logits, float* logits,
+                     float* probs, int32_t* top_idx, float* top_w, int64_t capacity, int32_t* counts,
+                     int32_t* kept_counts, int32_t* kept_offsets, int32_t* totals, int32_t* slot_token,
+                     float* slot_weight, int32_t* route_slot, int32_t* dropped_token, int32_t* dropped_expert,
+                     const float* cast_x, uint16_t* cast_out, float* partial, size_t partial_bytes,
+                     hipStream_t stream);
 int plan(const int32_t* top_idx, const float* top_w, int64_t T, int64_t K, int64_t E, int64_t capacity,
          int32_t* counts, int32_t* kept_counts, int32_t* kept_offsets, int32_t* slot_token, float* slot_weight,
          int32_t* route_slot, int32_t* dropped_token, int32_t* dropped_expert, int32_t* totals, void* ws,
@@ -326,12 +334,21 @@ int qw_moe_forward(const void* x, int act_dtype, int64_t tokens, int64_t d_model
   char* ews = c.take<char>(exp_ws);
   const size_t route_ws = route_workspace_bytes(tokens, d_model, experts);
   float* rws = reinterpret_cast<float*>(c.take<char>(route_ws));
-  int st = route(x, act_dtype, d_model, router_w, router_dtype, tokens, d_model, experts, top_k, temperature,
-                 expert_bias, logits, probs, top_idx, top_w, rws, route_ws, s);
-  if (st) return st;
-  st = plan(top_idx, top_w, tokens, top_k, experts, capacity, counts, kept_counts, kept_offsets, slot_token,
-            slot_weight, route_slot, dropped_token, dropped_expert, totals, pws, plan_ws, s);
-  if (st) return st;
+  int st;
+  if (route_plan_small_fits(tokens, experts, top_k)) {
+    st = route_plan_small(x, act_dtype, d_model, router_w, router_dtype, tokens, d_model, experts, top_k, temperature,
+                          expert_bias, false, logits, probs, top_idx, top_w, capacity, counts, kept_counts,
+                          kept_offsets, totals, slot_token, slot_weight, route_slot, dropped_token, dropped_expert,
+                          nullptr, nullptr, rws, route_ws, s);
+    if (st) return st;
+  } else {
+    st = route(x, act_dtype, d_model, router_w, router_dtype, tokens, d_model, experts, top_k, temperature,
+               expert_bias, logits, probs, top_idx, top_w, rws, route_ws, s);
+    if (st) return st;
+    st = plan(top_idx, top_w, tokens, top_k, experts, capacity, counts, kept_counts, kept_offsets, slot_token,
+              slot_weight, route_slot, dropped_token, dropped_expert, totals, pws, plan_ws, s);
+    if (st) return st;
+  }
   if (max_rows > 0) {
     const int64_t avg = (R + experts - 1) / experts;
     st = qw::experts(x, act_dtype, slot_token, kept_offsets, experts, d_model, d_ff, max_rows, w_format, group_in,
@@ -369,18 +386,27 @@ int qw_moe_decode_step(const float* x, const float* residual, int64_t tokens, in
   hipStream_t s = as_stream(stream);
   const int64_t R = tokens * top_k;
   const DecodeWs w = carve_decode(workspace, tokens, d_model, experts, top_k, d_ff, compute_dtype);
-  int st = route(x, QW_F32, d_model, router_w, QW_F32, tokens, d_model, experts, top_k, temperature, expert_bias,
-                 w.logits, probs, top_idx, top_w, w.route_ws, w.route_bytes, s, /*select_logits=*/true);
-  if (st) return st;
   // capacity R: every route keeps its slot
-  st = plan(top_idx, top_w, tokens, top_k, experts, R, w.counts, w.kept_counts, w.kept_offsets, w.slot_token,
-            w.slot_weight, w.route_slot, w.dropped_token, w.dropped_expert, w.totals, w.plan_ws, w.plan_bytes, s);
-  if (st) return st;
-  const void* xc = x;
-  if (compute_dtype == QW_BF16) {
-    st = cast_bf16(x, tokens * d_model, w.xc, s);
+  const void* xc = compute_dtype == QW_BF16 ? static_cast<const void*>(w.xc) : static_cast<const void*>(x);
+  int st;
+  if (route_plan_small_fits(tokens, experts, top_k)) {
+    st = route_plan_small(x, QW_F32, d_model, router_w, QW_F32, tokens, d_model, experts, top_k, temperature,
+                          expert_bias, /*select_logits=*/true, w.logits, probs, top_idx, top_w, R, w.counts,
+                          w.kept_counts, w.kept_offsets, w.totals, w.slot_token, w.slot_weight, w.route_slot,
+                          w.dropped_token, w.dropped_expert, x, compute_dtype == QW_BF16 ? w.xc : nullptr,
+                          w.route_ws, w.route_bytes, s);
     if (st) return st;
-    xc = w.xc;
+  } else {
+    st = route(x, QW_F32, d_model, router_w, QW_F32, tokens, d_model, experts, top_k, temperature, expert_bias,
+               w.logits, probs, top_idx, top_w, w.route_ws, w.route_bytes, s, /*select_logits=*/true);
+    if (st) return st;
+    st = plan(top_idx, top_w, tokens, top_k, experts, R, w.counts, w.kept_counts, w.kept_offsets, w.slot_token,
+              w.slot_weight, w.route_slot, w.dropped_token, w.dropped_expert, w.totals, w.plan_ws, w.plan_bytes, s);
+    if (st) return st;
+    if (compute_dtype == QW_BF16) {
+      st = cast_bf16(x, tokens * d_model, w.xc, s);
+      if (st) return st;
+    }
   }
   const int64_t avg = (R + experts - 1) / experts;
   st = qw::experts(xc, compute_dtype, w.slot_token, w.kept_offsets, experts, d_model, d_ff, R, w_format, group_in,

@@ -110,6 +110,74 @@ __device__ __forceinline__ int wave_sum_i(int v) {
   return v;
 }
 
+// Sums V = 2^L values over the 64 lanes of the wave with 6 - L + (V - 1)
+// shuffles instead of 6 V: at each of the first L steps a lane keeps half of
+// its values, adds the partner's copies of them and hands over the other half.
+// Afterwards every lane holds the full sum of value index lane >> (6 - L).
+template <int V>
+constexpr int log2i() {
+  int l = 0;
+  while ((1 << l) < V) ++l;
+  return l;
+}
+
+// One step of reduce_scatter over the first N of V values (all indices are
+// compile-time constants, so the values stay in registers).
+template <int V, int N>
+__device__ __forceinline__ void rs_step(float (&v)[V], int lane) {
+  if constexpr (N > 1) {
+    constexpr int half = N / 2;
+    constexpr int o = 32 * N / V;  // lane bit that picks the half this lane keeps
+    const bool upper = lane & o;
+#pragma unroll
+    for (int i = 0; i < half; ++i) {
+      const float give = upper ? v[i] : v[i + half];
+      const float keep = upper ? v[i + half] : v[i];
+      v[i] = keep + __shfl_xor(give, o, kWave);
+    }
+    rs_step<V, half>(v, lane);
+  }
+}
+
+template <int V>
+__device__ __forceinline__ float reduce_scatter(float (&v)[V], int lane) {
+  static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "V must be a power of two <= 64");
+  rs_step<V, V>(v, lane);
+  float r = v[0];
+#pragma unroll
+  for (int o = 32 / V; o >= 1; o >>= 1) r += __shfl_xor(r, o, kWave);
+  return r;
+}
+
+// Block-wide exclusive scan of one int per thread; *total gets the sum.
+__device__ int block_exclusive_scan(int v, int* warp_tot, int* total) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int n = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += n;
+  }
+  if (lane == kWave - 1) warp_tot[wave] = incl;
+  __syncthreads();
+  if (wave == 0) {
+    const int nw = blockDim.x / kWave;
+    const int w = lane < nw ? warp_tot[lane] : 0;
+    int wi = w;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int n = __shfl_up(wi, o, kWave);
+      if (lane >= o) wi += n;
+    }
+    if (lane < nw) warp_tot[lane] = wi - w;
+    if (lane == nw - 1) *total = wi;
+  }
+  __syncthreads();
+  const int r = warp_tot[wave] + incl - v;
+  __syncthreads();
+  return r;
+}
+
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
 
 // Workgroup barrier that orders LDS only.  __syncthreads() also waits for every

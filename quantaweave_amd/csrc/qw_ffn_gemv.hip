@@ -134,46 +134,6 @@ __device__ __forceinline__ void prep_chunk(const uint4* raw, float scale, uint32
   }
 }
 
-// Sums V = 2^L values over the 64 lanes of the wave with 6 - L + (V - 1)
-// shuffles instead of 6 V: at each of the first L steps a lane keeps half of
-// its values, adds the partner's copies of them and hands over the other half.
-// Afterwards every lane holds the full sum of value index lane >> (6 - L).
-template <int V>
-constexpr int log2i() {
-  int l = 0;
-  while ((1 << l) < V) ++l;
-  return l;
-}
-
-// One step of reduce_scatter over the first N of V values (all indices are
-// compile-time constants, so the values stay in registers).
-template <int V, int N>
-__device__ __forceinline__ void rs_step(float (&v)[V], int lane) {
-  if constexpr (N > 1) {
-    constexpr int half = N / 2;
-    constexpr int o = 32 * N / V;  // lane bit that picks the half this lane keeps
-    const bool upper = lane & o;
-#pragma unroll
-    for (int i = 0; i < half; ++i) {
-      const float give = upper ? v[i] : v[i + half];
-      const float keep = upper ? v[i + half] : v[i];
-      v[i] = keep + __shfl_xor(give, o, kWave);
-    }
-    rs_step<V, half>(v, lane);
-  }
-}
-
-template <int V>
-__device__ __forceinline__ float reduce_scatter(float (&v)[V], int lane) {
-  static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "V must be a power of two <= 64");
-  rs_step<V, V>(v, lane);
-  float r = v[0];
-#pragma unroll
-  for (int o = 32 / V; o >= 1; o >>= 1) r += __shfl_xor(r, o, kWave);
-  return r;
-}
-
-
 typedef __attribute__((address_space(3))) void lds_void;
 
 // s_waitcnt immediate waiting for vmcnt <= n only (expcnt, lgkmcnt left at max).
@@ -185,7 +145,9 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 // LDS bytes of one wave: a ring of STAGES groups (weight chunks, then the
 // chunks' scales) and the staging area of the outputs of one pass.
-template <int WF, int UNITS, int ROWS, int CPL, int GPW, int MAXM>
+constexpr int GV_GPW_MAX = 8;  // groups per wave, at most
+
+template <int WF, int UNITS, int ROWS, int CPL, int MAXM>
 struct GvLds {
   static constexpr int NCH = UNITS * ROWS * CPL;                 // chunk loads per group
   static_assert(NCH == 4 || NCH == 8, "the ring reads four or eight chunks per group");
@@ -193,7 +155,7 @@ struct GvLds {
   static constexpr int STAGE = NCH * 1024 + (QUANT ? NCH * 256 : 0);
   static constexpr int STAGES = 2;
   static constexpr int NDMA = NCH * (QUANT ? 2 : 1);             // DMA instructions per group
-  static constexpr int OUT = GPW * UNITS * MAXM * 4;             // staged outputs (fp32)
+  static constexpr int OUT = GV_GPW_MAX * UNITS * MAXM * 4;      // staged outputs (fp32)
   static constexpr int WAVE = STAGES * STAGE + OUT;
 };
 
@@ -285,10 +247,39 @@ __device__ __forceinline__ uint32_t lds_addr(const char* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
 }
 
+// The expert of the j-th non-empty row range, in ascending expert order, and its
+// rows [*lo, *hi); -1 when fewer than j + 1 experts have rows.  The grid's y
+// extent then only needs to cover the experts that can have rows (at most one
+// per row), not all of them.  Wave-uniform result.
+__device__ __forceinline__ int nth_active_expert(const int32_t* __restrict__ offsets, int E, int max_rows, int j,
+                                                 int* lo, int* hi) {
+  const int lane = threadIdx.x % kWave;
+  for (int c = 0; c < E; c += kWave) {
+    const int e = c + lane;
+    int a = 0, b = 0;
+    if (e < E) {
+      a = min(max(offsets[e], 0), max_rows);
+      b = min(offsets[e + 1], max_rows);
+    }
+    const bool act = b > a;
+    const uint64_t m = __ballot(act);
+    const int n = __popcll(m);
+    if (j < n) {
+      const bool hit = act && __popcll(m & ((1ull << lane) - 1ull)) == j;
+      const int src = __builtin_ctzll(__ballot(hit));
+      *lo = __builtin_amdgcn_readfirstlane(__shfl(a, src, kWave));
+      *hi = __builtin_amdgcn_readfirstlane(__shfl(b, src, kWave));
+      return c + src;
+    }
+    j -= n;
+  }
+  return -1;
+}
+
 // Waves work independently (no barriers).  A group is UNITS consecutive units
 // of expert e (GATEUP: a unit is a hidden column, i.e. a gate row and an up
-// row; DOWN: an output row).  Wave w of block (b, e) owns groups
-// [(b*GV_WAVES + w)*GPW, +GPW).  Lane l streams the 16-byte chunks
+// row; DOWN: an output row).  Block (b, j) works on the j-th expert that has
+// rows; its wave w owns groups [(b*GV_WAVES + w)*gpw, +gpw).  Lane l streams the 16-byte chunks
 // c = l + 64*j (j < CPL) of each row, and their scales, HBM -> LDS with
 // global_load_lds into a two-stage ring of the wave's own (one group ahead; a
 // deeper ring costs more LDS per wave than the extra waves it displaces), so
@@ -298,11 +289,11 @@ __device__ __forceinline__ uint32_t lds_addr(const char* p) {
 // from L2 once per pass, are prepared once and kept in registers while the
 // wave walks its groups.  Outputs are staged in the wave's LDS and stored once
 // the pass is done (a store between the ring loads would break the counts).
-template <int WF, bool GATEUP, int UNITS, int CPL, int MAXM, int GPW>
+template <int WF, bool GATEUP, int UNITS, int CPL, int MAXM>
 __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
-    int max_rows, WView wa, WView wb, int K, int n_out, const float* __restrict__ row_weight,
-    uint16_t* __restrict__ out) {
+    int n_experts, int max_rows, WView wa, WView wb, int K, int n_out, int gpw,
+    const float* __restrict__ row_weight, uint16_t* __restrict__ out) {
   constexpr int CW = Fmt<WF>::CW;
   constexpr int DW = CW / 2;   // activation pairs per chunk
   constexpr int XP = CW / 8;   // 16-byte activation pieces per chunk
@@ -310,17 +301,17 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
   constexpr int V = UNITS * ROWS * MAXM;  // values reduced per group
   constexpr int L = log2i<V>();
   constexpr int OUTS = UNITS * MAXM;      // outputs per group
-  using LD = GvLds<WF, UNITS, ROWS, CPL, GPW, MAXM>;
+  using LD = GvLds<WF, UNITS, ROWS, CPL, MAXM>;
   extern __shared__ __attribute__((aligned(1024))) char smem[];
-  const int e = blockIdx.y;
-  const int r_lo = max(offsets[e], 0), r_hi = min(offsets[e + 1], max_rows);
-  if (r_hi <= r_lo) return;
+  int r_lo = 0, r_hi = 0;
+  const int e = nth_active_expert(offsets, n_experts, max_rows, blockIdx.y, &r_lo, &r_hi);
+  if (e < 0) return;
   const int lane = threadIdx.x % 64;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);  // wave-uniform: keeps the group loop scalar
   const int n_groups = (n_out + UNITS - 1) / UNITS;
-  const int g_first = (blockIdx.x * GV_WAVES + wave) * GPW;
+  const int g_first = (blockIdx.x * GV_WAVES + wave) * gpw;
   if (g_first >= n_groups) return;
-  const int g_end = min(g_first + GPW, n_groups);
+  const int g_end = min(g_first + gpw, n_groups);
   char* const ring = smem + wave * LD::WAVE;
   float* const staged = reinterpret_cast<float*>(ring + LD::STAGES * LD::STAGE);
   const int KC = K / CW;
@@ -368,19 +359,26 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
 
   for (int m0 = r_lo; m0 < r_hi; m0 += MAXM) {
     const int M = min(MAXM, r_hi - m0);
-    // ---- activation pieces of this pass (plain loads), then the first groups of the ring ----
-    uint4 raw[CPL][MAXM][XP];
+    // ---- the rows' token indices, the first group of the ring, then the activation
+    //      pieces of this pass (plain loads): the weight DMA does not wait for the
+    //      index loads the activation loads depend on ----
+    int xr[MAXM];
 #pragma unroll
     for (int m = 0; m < MAXM; ++m) {
       const int s = m0 + min(m, M - 1);
-      const uint16_t* xrow = x + static_cast<int64_t>(row_index ? row_index[s] : s) * K;
+      xr[m] = row_index ? row_index[s] : s;
+    }
+#pragma unroll
+    for (int i = 0; i < LD::STAGES - 1; ++i) issue(g_first + i);
+    uint4 raw[CPL][MAXM][XP];
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) {
+      const uint16_t* xrow = x + static_cast<int64_t>(xr[m]) * K;
 #pragma unroll
       for (int j = 0; j < CPL; ++j)
 #pragma unroll
         for (int q = 0; q < XP; ++q) raw[j][m][q] = reinterpret_cast<const uint4*>(xrow + cidx[j] * CW)[q];
     }
-#pragma unroll
-    for (int i = 0; i < LD::STAGES - 1; ++i) issue(g_first + i);
     float scale[MAXM], inv[MAXM];
 #pragma unroll
     for (int m = 0; m < MAXM; ++m) scale[m] = inv[m] = 1.0f;
@@ -422,10 +420,15 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
       }
     }
 
-    // ---- the groups: issue g+STAGES-1, wait for g, compute g from the ring ----
+    // ---- the groups: issue g+1 (if the wave has it), wait for g, compute g from the ring ----
+    static_assert(LD::STAGES == 2, "the wait below assumes one group in flight ahead");
     for (int g = g_first; g < g_end; ++g) {
-      issue(g + LD::STAGES - 1);
-      wait_vmcnt<(LD::STAGES - 1) * LD::NDMA>();
+      if (g + 1 < g_end) {
+        issue(g + 1);
+        wait_vmcnt<LD::NDMA>();
+      } else {
+        wait_vmcnt<0>();
+      }
       const char* st = ring + ((g - g_first) % LD::STAGES) * LD::STAGE;
       uint4 wq[LD::NCH];
       float sq[LD::NCH];
@@ -499,38 +502,40 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
   }
 }
 
-template <int WF, bool GATEUP, int UNITS, int CPL, int GPW>
-int launch_gpw(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
+// Groups per wave: 8 when the touched experts (at most one per row) have 6*4096
+// groups or more; below that fewer, so that about 2048 waves or more (8 per CU)
+// stream the weights, each with its groups in flight at once.
+static int groups_per_wave(int64_t touched, int64_t n_groups) {
+  const int64_t total = touched * n_groups;
+  if (total >= 6 * 4096) return 8;
+  if (total >= 8192) return 4;
+  if (total >= 4096) return 2;
+  return 1;
+}
+
+template <int WF, bool GATEUP, int UNITS, int CPL>
+int launch_one(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
                int n_out, const float* row_weight, void* out, hipStream_t stream) {
   // routes per pass: int4 activation pieces are 4x larger per chunk than bf16 ones
   constexpr int MAXM = WF == QW_U4 ? 2 : 4;
-  using LD = GvLds<WF, UNITS, GATEUP ? 2 : 1, CPL, GPW, MAXM>;
+  using LD = GvLds<WF, UNITS, GATEUP ? 2 : 1, CPL, MAXM>;
   constexpr size_t lds = static_cast<size_t>(GV_WAVES) * LD::WAVE;
-  auto kernel = ffn_gemv_kernel<WF, GATEUP, UNITS, CPL, MAXM, GPW>;
+  auto kernel = ffn_gemv_kernel<WF, GATEUP, UNITS, CPL, MAXM>;
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize,
                                                      static_cast<int>(lds));
   if (attr != hipSuccess)
     return set_error(QW_ERR_HIP, "cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(attr));
-  const int64_t waves = ceil_div(ceil_div(n_out, UNITS), GPW);
-  const dim3 grid(static_cast<unsigned>(ceil_div(waves, GV_WAVES)), static_cast<unsigned>(a.experts));
-  kernel<<<grid, GV_WAVES * 64, lds, stream>>>(static_cast<const uint16_t*>(x), row_index, a.offsets,
-                                               static_cast<int>(a.max_rows), wa, wb, K, n_out, row_weight,
-                                               static_cast<uint16_t*>(out));
-  QW_LAUNCH_CHECK(GATEUP ? "ffn_gemv_kernel<gateup>" : "ffn_gemv_kernel<down>");
-  return QW_OK;
-}
-
-// Groups per wave: about 4096 waves over the experts that can be touched (at most
-// one per kept row), as 4 or 8 groups per wave.
-template <int WF, bool GATEUP, int UNITS, int CPL>
-int launch_one(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
-               int n_out, const float* row_weight, void* out, hipStream_t stream) {
   const int64_t n_groups = ceil_div(n_out, UNITS);
   const int64_t touched = a.max_rows < a.experts ? a.max_rows : a.experts;
-  if (touched * n_groups / 4096 >= 6)
-    return launch_gpw<WF, GATEUP, UNITS, CPL, 8>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
-  return launch_gpw<WF, GATEUP, UNITS, CPL, 4>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+  const int gpw = groups_per_wave(touched, n_groups);
+  const int64_t waves = ceil_div(n_groups, gpw);
+  const dim3 grid(static_cast<unsigned>(ceil_div(waves, GV_WAVES)), static_cast<unsigned>(touched));
+  kernel<<<grid, GV_WAVES * 64, lds, stream>>>(static_cast<const uint16_t*>(x), row_index, a.offsets,
+                                               static_cast<int>(a.experts), static_cast<int>(a.max_rows), wa, wb, K,
+                                               n_out, gpw, row_weight, static_cast<uint16_t*>(out));
+  QW_LAUNCH_CHECK(GATEUP ? "ffn_gemv_kernel<gateup>" : "ffn_gemv_kernel<down>");
+  return QW_OK;
 }
 
 // Units per group for a row of CPL chunks per lane: 4 weight chunks (16-byte

@@ -36,36 +36,6 @@ __device__ __forceinline__ uint64_t route_key(const float* top_w, int r) {
   return (static_cast<uint64_t>(~weight_key(top_w[r])) << 32) | static_cast<uint32_t>(r);
 }
 
-// Block-wide exclusive scan of one int per thread; *total gets the sum.
-__device__ int block_exclusive_scan(int v, int* warp_tot, int* total) {
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  int incl = v;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const int n = __shfl_up(incl, o, kWave);
-    if (lane >= o) incl += n;
-  }
-  if (lane == kWave - 1) warp_tot[wave] = incl;
-  __syncthreads();
-  if (wave == 0) {
-    const int nw = blockDim.x / kWave;
-    const int w = lane < nw ? warp_tot[lane] : 0;
-    int wi = w;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-      const int n = __shfl_up(wi, o, kWave);
-      if (lane >= o) wi += n;
-    }
-    if (lane < nw) warp_tot[lane] = wi - w;
-    if (lane == nw - 1) *total = wi;
-  }
-  __syncthreads();
-  const int r = warp_tot[wave] + incl - v;
-  __syncthreads();
-  return r;
-}
-
-
 // Offsets, per-expert ranking and placement.
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const int32_t* __restrict__ top_idx, const float* __restrict__ top_w, int R, int E, int K, int capacity,

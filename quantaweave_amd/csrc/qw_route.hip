@@ -98,6 +98,73 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const void* __restri
   }
 }
 
+// Router for a few tokens (decode): the GEMM is a GEMV per token, bound by
+// reading the router weight once.  Block (e, b): expert e, tokens
+// [b*TT, b*TT + TT); thread i accumulates x[t, d] * w[e, d] for d = VEC*i + 256*VEC*j (+ 0..VEC-1) with
+// fma (rows past the last token repeat it, so every load is issued at once);
+// the TT per-thread sums are reduced across
+// the wave (reduce_scatter) and then across the 4 waves in wave order, and
+//   logits[t, e] = sum / temperature
+// is written directly (no split-K partials).
+template <int DT, int VEC>
+__device__ __forceinline__ void load_vec(const void* p, int64_t i, float (&v)[VEC]) {
+  if constexpr (VEC == 4 && DT == QW_F32) {
+    const float4 q = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+    v[0] = q.x;
+    v[1] = q.y;
+    v[2] = q.z;
+    v[3] = q.w;
+  } else if constexpr (VEC == 4) {
+    const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+    v[0] = __uint_as_float(q.x << 16);
+    v[1] = __uint_as_float(q.x & 0xffff0000u);
+    v[2] = __uint_as_float(q.y << 16);
+    v[3] = __uint_as_float(q.y & 0xffff0000u);
+  } else {
+#pragma unroll
+    for (int u = 0; u < VEC; ++u) v[u] = load_act<DT>(p, i + u);
+  }
+}
+
+constexpr int kGemvMaxTokens = 64;  // the GEMV router serves up to this many tokens
+
+template <int XDT, int WDT, int VEC, int TT>
+__global__ __launch_bounds__(256) void router_gemv_kernel(const void* __restrict__ x, int64_t x_stride,
+                                                          const void* __restrict__ w, int T, int D, int E,
+                                                          float temperature, float* __restrict__ logits) {
+  constexpr int L = log2i<TT>();
+  __shared__ float red[4][TT];
+  const int e = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int64_t wrow = static_cast<int64_t>(e) * D;
+  const int t0 = blockIdx.y * TT;
+  {
+    const int nt = min(TT, T - t0);
+    float acc[TT];
+#pragma unroll
+    for (int i = 0; i < TT; ++i) acc[i] = 0.0f;
+    for (int d = tid * VEC; d < D; d += 256 * VEC) {
+      float wv[VEC];
+      load_vec<WDT, VEC>(w, wrow + d, wv);
+      float xv[TT][VEC];
+#pragma unroll
+      for (int i = 0; i < TT; ++i)
+        load_vec<XDT, VEC>(x, static_cast<int64_t>(t0 + min(i, nt - 1)) * x_stride + d, xv[i]);
+#pragma unroll
+      for (int i = 0; i < TT; ++i)
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) acc[i] = __builtin_fmaf(xv[i][u], wv[u], acc[i]);
+    }
+    const float r = reduce_scatter<TT>(acc, lane);  // the wave's sum of token lane >> (6 - L)
+    if ((lane & ((1 << (6 - L)) - 1)) == 0) red[wave][lane >> (6 - L)] = r;
+    __syncthreads();
+    if (tid < nt) {
+      const float s = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+      logits[static_cast<int64_t>(t0 + tid) * E + e] = s / temperature;
+    }
+  }
+}
+
 // bf16 x bf16 router GEMM on MFMA (products of bf16 values are exact in fp32,
 // so this is the same fp32 dot product up to accumulation order).  Tile: 64
 // tokens x 64 experts per 256-thread block; wave w owns tokens w*16..w*16+15.
@@ -192,40 +259,22 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const uint16_t* __rest
 //   w_j = p_{idx_j} / (((p_{idx_0} + p_{idx_1}) + p_{idx_2}) + ...)
 // ---------------------------------------------------------------------------
 //
-// With `partial` != NULL the logits are first assembled from the router GEMM's
-// split-K partials: L = ((p_0 + p_1) + ... + p_{S-1}) / temperature, and
-// written to `logits`.
+// The per-token part: softmax and top-k of one token's logits l (lane l owns
+// experts l + 64*c) by one wave.  probs are stored here.  With K <= 64 the
+// choices are returned, lane j holding round j's expert and renormalised weight
+// in *out_e / *out_w (lanes >= K: unspecified), and the caller stores them; with
+// more rounds lane 0 stores each choice to top_idx/top_w and renormalises them
+// in memory.
 template <int EPL>
-__global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ partial, int splits,
-                                                         float temperature, float* __restrict__ logits, int T, int E,
-                                                         int K, const float* __restrict__ bias,
-                                                         int select_logits, float* __restrict__ probs,
-                                                         int32_t* __restrict__ top_idx,
-                                                         float* __restrict__ top_w) {
+__device__ __forceinline__ void select_token(float (&l)[EPL], int t, int E, int K, const float* __restrict__ bias,
+                                             int select_logits, float* __restrict__ probs,
+                                             int32_t* __restrict__ top_idx, float* __restrict__ top_w, int* out_e,
+                                             float* out_w) {
   const int lane = threadIdx.x % kWave;
-  const int t = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
-  if (t >= T) return;
-  float l[EPL], p[EPL];
+  float p[EPL];
   float m = -__builtin_inff();
 #pragma unroll
-  for (int c = 0; c < EPL; ++c) {
-    const int e = lane + c * kWave;
-    if (e < E) {
-      const int64_t i = static_cast<int64_t>(t) * E + e;
-      if (partial != nullptr) {
-        float v = partial[i];
-        for (int sp = 1; sp < splits; ++sp) v += partial[static_cast<int64_t>(sp) * T * E + i];
-        v = v / temperature;
-        logits[i] = v;
-        l[c] = v;
-      } else {
-        l[c] = logits[i];
-      }
-    } else {
-      l[c] = -__builtin_inff();
-    }
-    m = fmaxf(m, l[c]);
-  }
+  for (int c = 0; c < EPL; ++c) m = fmaxf(m, l[c]);
   // fmaxf drops NaN; a NaN logit must poison the row as it does in torch.
   bool has_nan = false;
 #pragma unroll
@@ -257,7 +306,8 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
   }
   uint32_t taken = 0;
   float sel_sum = 0.0f;
-  // k <= E <= 64*EPL; selected probabilities stay in registers of lane 0 via shuffles
+  int my_e = 0;
+  float my_p = 0.0f;
   for (int j = 0; j < K; ++j) {
     uint64_t best = 0;
 #pragma unroll
@@ -282,16 +332,64 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
     p_sel = __shfl(p_sel, owner, kWave);
     if (lane == owner) taken |= 1u << slot;
     sel_sum = (j == 0) ? p_sel : sel_sum + p_sel;
-    if (lane == 0) {
+    if (lane == j) {
+      my_e = e_sel;
+      my_p = p_sel;
+    }
+    if (K > kWave && lane == 0) {
       top_idx[static_cast<int64_t>(t) * K + j] = e_sel;
       top_w[static_cast<int64_t>(t) * K + j] = p_sel;  // renormalised below
     }
   }
-  if (lane == 0) {
+  if (K <= kWave) {
+    *out_e = my_e;
+    *out_w = my_p / sel_sum;
+  } else if (lane == 0) {
     for (int j = 0; j < K; ++j) {
       float* w = top_w + static_cast<int64_t>(t) * K + j;
       *w = *w / sel_sum;
     }
+  }
+}
+
+// With `partial` != NULL the logits are first assembled from the router GEMM's
+// split-K partials: L = ((p_0 + p_1) + ... + p_{S-1}) / temperature, and
+// written to `logits`.
+template <int EPL>
+__global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ partial, int splits,
+                                                         float temperature, float* __restrict__ logits, int T, int E,
+                                                         int K, const float* __restrict__ bias,
+                                                         int select_logits, float* __restrict__ probs,
+                                                         int32_t* __restrict__ top_idx,
+                                                         float* __restrict__ top_w) {
+  const int lane = threadIdx.x % kWave;
+  const int t = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (t >= T) return;
+  float l[EPL];
+#pragma unroll
+  for (int c = 0; c < EPL; ++c) {
+    const int e = lane + c * kWave;
+    if (e < E) {
+      const int64_t i = static_cast<int64_t>(t) * E + e;
+      if (partial != nullptr) {
+        float v = partial[i];
+        for (int sp = 1; sp < splits; ++sp) v += partial[static_cast<int64_t>(sp) * T * E + i];
+        v = v / temperature;
+        logits[i] = v;
+        l[c] = v;
+      } else {
+        l[c] = logits[i];
+      }
+    } else {
+      l[c] = -__builtin_inff();
+    }
+  }
+  int me = 0;
+  float mw = 0.0f;
+  select_token<EPL>(l, t, E, K, bias, select_logits, probs, top_idx, top_w, &me, &mw);
+  if (K <= kWave && lane < K) {
+    top_idx[static_cast<int64_t>(t) * K + lane] = me;
+    top_w[static_cast<int64_t>(t) * K + lane] = mw;
   }
 }
 
@@ -312,6 +410,179 @@ static int launch_topk(const float* partial, int splits, float temperature, floa
   else QW_TK(16);
 #undef QW_TK
   QW_LAUNCH_CHECK("route_topk_kernel");
+  return QW_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Routing and capacity plan of a small batch in one workgroup (decode sizes:
+// R = T*K <= kSmallRoutes, K <= 64), replacing the plan kernel, and for up to
+// 16 tokens (`routed` = 0) the top-k kernel too:
+//   1. wave w routes token w exactly as route_topk_kernel does, the choices
+//      also going to LDS (`routed` = 1: the choices are read from top_idx and
+//      top_w, written by route_topk_kernel);
+//   2. thread r < R counts route r into an LDS histogram; counts, kept counts
+//      min(count, capacity) and their exclusive scans give every expert's
+//      kept and dropped offsets (as plan_kernel does);
+//   3. thread r ranks route r among the routes of its expert by the plan key
+//      (weight descending, then route id: src/quantweave_moe_model.py:174-175)
+//      and writes its slot, or its dropped entry.
+// Optionally the same workgroup writes cast_out = bf16(cast_x) (n values),
+// the decode step's expert input.
+// ---------------------------------------------------------------------------
+constexpr int kSmallThreads = 1024;
+constexpr int kSmallTokens = 64;       // tokens of the one-workgroup plan
+constexpr int kSmallRouteTokens = 16;  // tokens it also routes (one per wave)
+constexpr int kSmallRoutes = 256;
+constexpr int kSmallLogits = 8192;  // T*E logits staged in LDS
+
+template <int EPL>
+__global__ __launch_bounds__(kSmallThreads) void route_plan_small_kernel(
+    int routed, const float* __restrict__ partial, int splits, float temperature, float* __restrict__ logits, int T,
+    int E, int K, const float* __restrict__ bias, int select_logits,
+    float* __restrict__ probs, int32_t* __restrict__ top_idx, float* __restrict__ top_w, int capacity,
+    int32_t* __restrict__ counts, int32_t* __restrict__ kept_counts, int32_t* __restrict__ kept_offsets,
+    int32_t* __restrict__ totals, int32_t* __restrict__ slot_token, float* __restrict__ slot_weight,
+    int32_t* __restrict__ route_slot, int32_t* __restrict__ dropped_token, int32_t* __restrict__ dropped_expert,
+    const float* __restrict__ cast_x, int cast_n, uint16_t* __restrict__ cast_out) {
+  constexpr int kWaves = kSmallThreads / kWave;
+  __shared__ float s_logit[kSmallLogits];
+  __shared__ int s_e[kSmallRoutes];
+  __shared__ float s_w[kSmallRoutes];
+  __shared__ uint64_t s_key[kSmallRoutes];
+  __shared__ int hist[1024], s_ko[1024], s_do[1024];
+  __shared__ int warp_tot[kWaves];
+  __shared__ int s_tot_kept, s_tot_drop;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int R = T * K;
+  for (int i = tid; i < E; i += kSmallThreads) hist[i] = 0;
+  if (cast_out != nullptr) {
+    for (int i = tid * 4; i < cast_n; i += kSmallThreads * 4) {
+      if (i + 4 <= cast_n && (cast_n & 3) == 0) {
+        const float4 v = *reinterpret_cast<const float4*>(cast_x + i);
+        uint2 o;
+        o.x = f32_to_bf16(v.x) | (static_cast<uint32_t>(f32_to_bf16(v.y)) << 16);
+        o.y = f32_to_bf16(v.z) | (static_cast<uint32_t>(f32_to_bf16(v.w)) << 16);
+        *reinterpret_cast<uint2*>(cast_out + i) = o;
+      } else {
+        for (int j = i; j < i + 4 && j < cast_n; ++j) cast_out[j] = f32_to_bf16(cast_x[j]);
+      }
+    }
+  }
+  if (routed) {
+    // ---- the routing was done by route_topk_kernel: its choices into LDS ----
+    for (int r = tid; r < R; r += kSmallThreads) {
+      const int me = top_idx[r];
+      const float mw = top_w[r];
+      s_e[r] = me;
+      s_w[r] = mw;
+      s_key[r] = (static_cast<uint64_t>(~sortable_key(mw)) << 32) | static_cast<uint32_t>(r);
+    }
+  }
+  // ---- 0. all logits into LDS at once (summing split-K partials if given) ----
+  for (int i = tid; i < (routed ? 0 : T * E); i += kSmallThreads) {
+    float v;
+    if (partial != nullptr) {
+      v = partial[i];
+#pragma unroll 4
+      for (int sp = 1; sp < splits; ++sp) v += partial[static_cast<int64_t>(sp) * T * E + i];
+      v = v / temperature;
+      logits[i] = v;
+    } else {
+      v = logits[i];
+    }
+    s_logit[i] = v;
+  }
+  __syncthreads();
+  // ---- 1. routing, one wave per token ----
+  for (int t = wave; t < (routed ? 0 : T); t += kWaves) {
+    float l[EPL];
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) {
+      const int e = lane + c * kWave;
+      l[c] = e < E ? s_logit[t * E + e] : -__builtin_inff();
+    }
+    int me = 0;
+    float mw = 0.0f;
+    select_token<EPL>(l, t, E, K, bias, select_logits, probs, top_idx, top_w, &me, &mw);
+    if (lane < K) {
+      const int r = t * K + lane;
+      top_idx[r] = me;
+      top_w[r] = mw;
+      s_e[r] = me;
+      s_w[r] = mw;
+      s_key[r] = (static_cast<uint64_t>(~sortable_key(mw)) << 32) | static_cast<uint32_t>(r);
+    }
+  }
+  __syncthreads();
+  // ---- 2. counts and offsets ----
+  int my_e = -1;
+  if (tid < R) {
+    my_e = s_e[tid];
+    atomicAdd(&hist[my_e], 1);
+  }
+  __syncthreads();
+  const int c = tid < E ? hist[tid] : 0;
+  const int kc = c < capacity ? c : capacity;
+  const int ko = block_exclusive_scan(kc, warp_tot, &s_tot_kept);
+  const int dof = block_exclusive_scan(c - kc, warp_tot, &s_tot_drop);
+  if (tid < E) {
+    s_ko[tid] = ko;
+    s_do[tid] = dof;
+    counts[tid] = c;
+    kept_counts[tid] = kc;
+    kept_offsets[tid] = ko;
+  }
+  if (tid == 0) {
+    kept_offsets[E] = s_tot_kept;
+    totals[0] = s_tot_kept;
+    totals[1] = s_tot_drop;
+  }
+  __syncthreads();
+  // ---- 3. rank within the expert and place ----
+  if (tid < R) {
+    const uint64_t key = s_key[tid];
+    int pos = 0;
+    for (int j = 0; j < R; ++j) pos += (s_e[j] == my_e && s_key[j] < key) ? 1 : 0;
+    const int token = tid / K;
+    if (pos < capacity) {
+      const int s = s_ko[my_e] + pos;
+      slot_token[s] = token;
+      slot_weight[s] = s_w[tid];
+      route_slot[tid] = s;
+    } else {
+      const int q = s_do[my_e] + (pos - capacity);
+      dropped_token[q] = token;
+      dropped_expert[q] = my_e;
+      route_slot[tid] = -1;
+    }
+  }
+}
+
+template <int XD, int WD, int VEC>
+static void launch_router_gemv_tt(const void* x, int64_t x_stride, const void* w, int t, int d, int e,
+                                  float temperature, float* logits, hipStream_t stream) {
+  const dim3 g16(e, static_cast<unsigned>(ceil_div(t, 16)));
+  if (t <= 1) router_gemv_kernel<XD, WD, VEC, 1><<<e, 256, 0, stream>>>(x, x_stride, w, t, d, e, temperature, logits);
+  else if (t <= 4) router_gemv_kernel<XD, WD, VEC, 4><<<e, 256, 0, stream>>>(x, x_stride, w, t, d, e, temperature, logits);
+  else router_gemv_kernel<XD, WD, VEC, 16><<<g16, 256, 0, stream>>>(x, x_stride, w, t, d, e, temperature, logits);
+}
+
+template <int XD, int WD>
+static void launch_router_gemv_vec(bool vec, const void* x, int64_t x_stride, const void* w, int t, int d, int e,
+                                   float temperature, float* logits, hipStream_t stream) {
+  if (vec) launch_router_gemv_tt<XD, WD, 4>(x, x_stride, w, t, d, e, temperature, logits, stream);
+  else launch_router_gemv_tt<XD, WD, 1>(x, x_stride, w, t, d, e, temperature, logits, stream);
+}
+
+static int launch_router_gemv(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int t, int d,
+                              int e, float temperature, float* logits, hipStream_t stream) {
+  const bool vec = d % 4 == 0 && x_stride % 4 == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0 &&
+                   (reinterpret_cast<uintptr_t>(w) % 16) == 0;
+  if (xdt == QW_F32 && wdt == QW_F32) launch_router_gemv_vec<QW_F32, QW_F32>(vec, x, x_stride, w, t, d, e, temperature, logits, stream);
+  else if (xdt == QW_F32) launch_router_gemv_vec<QW_F32, QW_BF16>(vec, x, x_stride, w, t, d, e, temperature, logits, stream);
+  else if (wdt == QW_F32) launch_router_gemv_vec<QW_BF16, QW_F32>(vec, x, x_stride, w, t, d, e, temperature, logits, stream);
+  else launch_router_gemv_vec<QW_BF16, QW_BF16>(vec, x, x_stride, w, t, d, e, temperature, logits, stream);
+  QW_LAUNCH_CHECK("router_gemv_kernel");
   return QW_OK;
 }
 
@@ -347,26 +618,26 @@ size_t route_workspace_bytes(int64_t T, int64_t D, int64_t E) {
   return static_cast<size_t>(router_splits(T, D, E)) * T * E * sizeof(float);
 }
 
-int route(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int64_t T, int64_t D, int64_t E,
-          int64_t K, float temperature, const float* bias, float* logits, float* probs, int32_t* top_idx,
-          float* top_w, float* partial, size_t partial_bytes, hipStream_t stream, bool select_logits) {
-  int st = route_validate(T, E, K);
-  if (st) return st;
-  QW_REQUIRE(xdt == QW_F32 || xdt == QW_BF16, "router input dtype must be f32 or bf16");
-  QW_REQUIRE(wdt == QW_F32 || wdt == QW_BF16, "router weight dtype must be f32 or bf16");
-  QW_REQUIRE(D >= 1 && D <= INT32_MAX, "d_model out of range");
-  QW_REQUIRE(x_stride >= D, "x row stride %lld smaller than d_model %lld", (long long)x_stride, (long long)D);
-  QW_REQUIRE(temperature > 0.0f, "router_temperature must be positive");
-  if (T == 0) return QW_OK;
-  QW_REQUIRE(x && w && logits && top_idx && top_w, "x, router_w, logits, top_idx and top_w are required");
+// Router logits: up to kGemvMaxTokens tokens by the GEMV kernel straight into
+// `logits` (*splits = 0); more by the tiled GEMM into split-K partials
+// (*splits > 0) that the next kernel sums and divides by the temperature.
+static int launch_router(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int64_t T, int64_t D,
+                         int64_t E, float temperature, float* logits, float* partial, size_t partial_bytes,
+                         int* splits_out, hipStream_t stream) {
+  const int t = static_cast<int>(T), d = static_cast<int>(D), e = static_cast<int>(E);
+  if (T <= kGemvMaxTokens) {
+    *splits_out = 0;
+    return launch_router_gemv(x, xdt, x_stride, w, wdt, t, d, e, temperature, logits, stream);
+  }
   const int splits = router_splits(T, D, E);
   if (partial_bytes < static_cast<size_t>(splits) * T * E * sizeof(float) || !partial)
     return set_error(QW_ERR_WORKSPACE, "router needs %zu bytes of partial sums", route_workspace_bytes(T, D, E));
+  *splits_out = splits;
   int64_t k_len = ceil_div(D, splits);
   k_len = ceil_div(k_len, 64) * 64;
   const dim3 grid(static_cast<unsigned>(ceil_div(T, 64)), static_cast<unsigned>(splits),
                   static_cast<unsigned>(ceil_div(E, 64)));
-  const int t = static_cast<int>(T), d = static_cast<int>(D), e = static_cast<int>(E), kl = static_cast<int>(k_len);
+  const int kl = static_cast<int>(k_len);
   if (xdt == QW_BF16 && wdt == QW_BF16 && D % 64 == 0) {
     router_mfma_kernel<<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(x), x_stride,
                                                  static_cast<const uint16_t*>(w), t, d, e, kl, partial);
@@ -381,8 +652,85 @@ int route(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int6
 #undef QW_RL
     QW_LAUNCH_CHECK("router_logits_kernel");
   }
-  return launch_topk(partial, splits, temperature, logits, t, e, static_cast<int>(K), bias, select_logits ? 1 : 0,
+  return QW_OK;
+}
+
+int route(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int64_t T, int64_t D, int64_t E,
+          int64_t K, float temperature, const float* bias, float* logits, float* probs, int32_t* top_idx,
+          float* top_w, float* partial, size_t partial_bytes, hipStream_t stream, bool select_logits) {
+  int st = route_validate(T, E, K);
+  if (st) return st;
+  QW_REQUIRE(xdt == QW_F32 || xdt == QW_BF16, "router input dtype must be f32 or bf16");
+  QW_REQUIRE(wdt == QW_F32 || wdt == QW_BF16, "router weight dtype must be f32 or bf16");
+  QW_REQUIRE(D >= 1 && D <= INT32_MAX, "d_model out of range");
+  QW_REQUIRE(x_stride >= D, "x row stride %lld smaller than d_model %lld", (long long)x_stride, (long long)D);
+  QW_REQUIRE(temperature > 0.0f, "router_temperature must be positive");
+  if (T == 0) return QW_OK;
+  QW_REQUIRE(x && w && logits && top_idx && top_w, "x, router_w, logits, top_idx and top_w are required");
+  const int t = static_cast<int>(T), e = static_cast<int>(E), k = static_cast<int>(K);
+  int splits = 0;
+  st = launch_router(x, xdt, x_stride, w, wdt, T, D, E, temperature, logits, partial, partial_bytes, &splits, stream);
+  if (st) return st;
+  return launch_topk(splits ? partial : nullptr, splits, temperature, logits, t, e, k, bias, select_logits ? 1 : 0,
                      probs, top_idx, top_w, stream);
+}
+
+// Small batches: router logits, then routing + plan (+ cast) in one workgroup.
+// The caller checks route_plan_small_fits first.
+bool route_plan_small_fits(int64_t T, int64_t E, int64_t K) {
+  return T >= 1 && T <= kSmallTokens && K >= 1 && K <= kWave && K <= E && E <= 1024 && T * K <= kSmallRoutes &&
+         (T > kSmallRouteTokens || T * E <= kSmallLogits);
+}
+
+int route_plan_small(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int64_t T, int64_t D,
+                     int64_t E, int64_t K, float temperature, const float* bias, bool select_logits, float* logits,
+                     float* probs, int32_t* top_idx, float* top_w, int64_t capacity, int32_t* counts,
+                     int32_t* kept_counts, int32_t* kept_offsets, int32_t* totals, int32_t* slot_token,
+                     float* slot_weight, int32_t* route_slot, int32_t* dropped_token, int32_t* dropped_expert,
+                     const float* cast_x, uint16_t* cast_out, float* partial, size_t partial_bytes,
+                     hipStream_t stream) {
+  int st = route_validate(T, E, K);
+  if (st) return st;
+  QW_REQUIRE(route_plan_small_fits(T, E, K), "batch too large for the one-workgroup plan");
+  QW_REQUIRE(xdt == QW_F32 || xdt == QW_BF16, "router input dtype must be f32 or bf16");
+  QW_REQUIRE(wdt == QW_F32 || wdt == QW_BF16, "router weight dtype must be f32 or bf16");
+  QW_REQUIRE(D >= 1 && D <= INT32_MAX / kSmallTokens && x_stride >= D, "bad router sizes");
+  QW_REQUIRE(temperature > 0.0f, "router_temperature must be positive");
+  QW_REQUIRE(capacity >= 0, "capacity must be >= 0");
+  QW_REQUIRE(x && w && logits && top_idx && top_w && counts && kept_counts && kept_offsets && totals && slot_token &&
+                 slot_weight && route_slot && dropped_token && dropped_expert,
+             "routing and plan arrays are required");
+  QW_REQUIRE(cast_out == nullptr || (cast_x != nullptr && x_stride == D), "cast needs contiguous fp32 rows");
+  const int t = static_cast<int>(T), d = static_cast<int>(D), e = static_cast<int>(E), k = static_cast<int>(K);
+  int splits = 0;
+  const int routed = T > kSmallRouteTokens ? 1 : 0;
+  if (routed) {
+    st = route(x, xdt, x_stride, w, wdt, T, D, E, K, temperature, bias, logits, probs, top_idx, top_w, partial,
+               partial_bytes, stream, select_logits);
+  } else {
+    st = launch_router(x, xdt, x_stride, w, wdt, T, D, E, temperature, logits, partial, partial_bytes, &splits,
+                       stream);
+  }
+  if (st) return st;
+  const float* part = splits ? partial : nullptr;
+  const int cap = capacity > INT32_MAX ? INT32_MAX : static_cast<int>(capacity);
+  const int n = cast_out ? t * d : 0;
+  const int epl = static_cast<int>(ceil_div(E, kWave));
+#define QW_RP(N)                                                                                                  \
+  route_plan_small_kernel<N><<<1, kSmallThreads, 0, stream>>>(routed, part, splits, temperature, logits, t, e, k, \
+                                                              bias,                                                   \
+                                                              select_logits ? 1 : 0, probs,                           \
+                                                              top_idx, top_w, cap, counts, kept_counts, kept_offsets, \
+                                                              totals, slot_token, slot_weight, route_slot,          \
+                                                              dropped_token, dropped_expert, cast_x, n, cast_out)
+  if (epl <= 1) QW_RP(1);
+  else if (epl <= 2) QW_RP(2);
+  else if (epl <= 4) QW_RP(4);
+  else if (epl <= 8) QW_RP(8);
+  else QW_RP(16);
+#undef QW_RP
+  QW_LAUNCH_CHECK("route_plan_small_kernel");
+  return QW_OK;
 }
 
 }  // namespace qw

@@ -222,3 +222,37 @@ def test_stats_and_static_dispatch():
     moe.static_dispatch = True
     _, _, dropped, overflow, _ = moe(hidden)
     assert overflow.item() == 0
+
+
+@pytest.mark.parametrize("T,E,k,cap", [(1, 64, 2, 2), (7, 8, 2, 3), (16, 64, 2, 32), (24, 6, 3, 5), (40, 16, 4, 4),
+                                       (64, 64, 2, 128), (64, 8, 4, 20), (33, 1024, 2, 1), (3, 5, 5, 1)])
+def test_small_batch_routing_and_plan_with_duplicate_tokens(T, E, k, cap):
+    """Batches of up to 64 tokens are routed and planned in one workgroup; the
+    result must equal the oracle's plan bit for bit, including equal weights
+    (duplicated tokens: ordered by route id) and capacity drops."""
+    w = W.Workload(f"small-T{T}-E{E}-k{k}", T, 256, E, 128, k, 1.0, "bf16", "bf16", 77 + T)
+    layer = W.build_layer(w)
+    if T > 2:
+        layer.x[1::3] = layer.x[0]                 # every third token repeats token 0
+    run = W.LayerRunner(layer, capacity=cap)
+    run()
+    torch.cuda.synchronize()
+    logits = run.workspace_view("logits").cpu().numpy()
+    res = oracle.moe_forward(layer.x.float().cpu().numpy(), layer.router.float().cpu().numpy(), host_weights(layer),
+                             top_k=k, cap=cap, dtype="bf16", logits=logits)
+    assert np.array_equal(run.top_idx.cpu().numpy(), res["top_idx"])
+    assert np.array_equal(run.top_w.cpu().numpy().view(np.int32), res["top_w"].view(np.int32))
+    assert np.array_equal(run.probs.cpu().numpy().view(np.int32), res["probs"].view(np.int32))
+    p = res["plan"]
+    kept, nd = int(p["totals"][0]), int(p["totals"][1])
+    assert run.totals.cpu().tolist() == p["totals"].tolist()
+    assert np.array_equal(run.counts.cpu().numpy(), p["counts"])
+    assert np.array_equal(run.kept_counts.cpu().numpy(), p["kept_counts"])
+    assert np.array_equal(run.workspace_view("kept_offsets").cpu().numpy(), p["kept_offsets"])
+    assert np.array_equal(run.workspace_view("slot_token").cpu().numpy()[:kept], p["slot_token"])
+    assert np.array_equal(run.workspace_view("slot_weight").cpu().numpy()[:kept].view(np.int32),
+                          p["slot_weight"].view(np.int32))
+    assert np.array_equal(run.workspace_view("route_slot").cpu().numpy(), p["route_slot"])
+    assert np.array_equal(run.dropped_token.cpu().numpy()[:nd], p["dropped_token"])
+    assert np.array_equal(run.dropped_expert.cpu().numpy()[:nd], p["dropped_expert"])
+    assert normwise(run.out.float().cpu().numpy(), res["out"]) <= TOL["bf16"]
