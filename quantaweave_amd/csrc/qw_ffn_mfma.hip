@@ -53,7 +53,8 @@ constexpr int MF_THREADS = 512;
 constexpr int MF_WAVES = 8;
 constexpr int MF_NT = 4;        // 16-column MFMA tiles per wave
 constexpr int MF_AST = 3;       // activation ring stages
-constexpr int MF_BST = 3;       // weight ring stages (both rings requested two slices ahead)
+constexpr int MF_BST = 3;       // weight ring stages
+constexpr int MF_AHEAD = 2;     // slices requested ahead of the one computed (< both stage counts)
 constexpr int kXcds = 8;
 
 // s_waitcnt immediate waiting for vmcnt <= n only (expcnt, lgkmcnt left at max).
@@ -184,41 +185,73 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
   }
   const int l16 = lane % 16, lq = lane / 16;
   const int active_sub = (count + 15) / 16;  // row sub-tiles holding valid rows (wave-uniform)
+  // this wave's sub-tiles are wm, wm+2, ...: pairs of them holding a valid row
+  const int n_pairs = __builtin_amdgcn_readfirstlane((max(0, (active_sub - wm + 1) / 2) + 1) / 2);
   const int KT = K / MF_BK;
 
   // Issue order: A0 B0 A1 B1 | A2 B2 | A3 B3 | ...  (iteration kt issues A(kt+2), B(kt+2)
   // right after its barrier).  At the top of iteration kt the loads issued after B(kt) are
   // A(kt+1) and B(kt+1): waiting for all but those completes slice kt.
-  for (int j = 0; j < 2 && j < KT; ++j) {
+  for (int j = 0; j < MF_AHEAD && j < KT; ++j) {
     issue_a(j);
     issue_b(j);
   }
   for (int kt = 0; kt < KT; ++kt) {
-    if (kt + 1 < KT) wait_vmcnt<AL_MAX + BL>();
+    // slices issued after slice kt: min(MF_AHEAD - 1, KT - 1 - kt), each AL_MAX + BL loads
+    static_assert(MF_AHEAD >= 1 && MF_AHEAD <= 3 && MF_AHEAD < MF_AST && MF_AHEAD < MF_BST, "ring depth");
+    const int after = min(MF_AHEAD - 1, KT - 1 - kt);
+    if (after >= 2) wait_vmcnt<2 * (AL_MAX + BL)>();
+    else if (after == 1) wait_vmcnt<AL_MAX + BL>();
     else wait_vmcnt<0>();
     ring_barrier();  // slice kt visible to all waves; everyone is done with slice kt-1
-    // requests into the stages of slice kt-1 (every wave is past its reads of them)
-    if (kt + 2 < KT) issue_a(kt + 2);
-    if (kt + 2 < KT) issue_b(kt + 2);
     const char* st_a = a_ring + (kt % MF_AST) * A_STAGE;
     const char* st_b = b_ring + (kt % MF_BST) * B_BYTES;
+    auto read_a = [&](int i) {
+      const int row = (wm + 2 * i) * 16 + l16;
+      return *reinterpret_cast<const bf16x8*>(st_a + row * MF_ROWB + swz(row, lq) * 16);
+    };
+    // the slice's weight fragments and the first two activation fragments are
+    // read first, then the requests two slices ahead go out (into the stages of
+    // slice kt-1: every wave is past its reads of them)
     bf16x8 wfr[MF_NT];
 #pragma unroll
     for (int t = 0; t < MF_NT; ++t) {
       const int row = brow[t] + l16;
       wfr[t] = *reinterpret_cast<const bf16x8*>(st_b + row * MF_ROWB + swz(row, lq) * 16);
     }
-    // All sub-tiles are computed, also those past the row count (their rows are
-    // clamped copies of a valid row and never stored): a per-sub-tile branch
-    // would keep the compiler from issuing the fragment reads ahead of the
-    // MFMAs and expose the LDS latency once per sub-tile.
+    // activation fragments in pairs of sub-tiles, two pair buffers: the reads of
+    // pair p+1 are issued right after the first MFMA of pair p (whose wait
+    // covered every earlier read), so seven MFMAs hide them
+    static_assert(SUBT % 2 == 0, "sub-tiles come in pairs");
+    bf16x8 xb[2][2];
+    xb[0][0] = read_a(0);
+    xb[0][1] = read_a(1);
+    __builtin_amdgcn_sched_group_barrier(0x100, MF_NT + 2, 0);  // weight fragments and pair 0 first
+    if (kt + MF_AHEAD < KT) {
+      issue_a(kt + MF_AHEAD);
+      issue_b(kt + MF_AHEAD);
+    }
+    // Pairs of sub-tiles holding no valid row of this wave are skipped (a pair
+    // with one valid sub-tile computes both; the other's rows are clamped copies
+    // of a valid row and never stored).
 #pragma unroll
-    for (int i = 0; i < SUBT; ++i) {
-      const int row = (wm + 2 * i) * 16 + l16;
-      const bf16x8 xfr = *reinterpret_cast<const bf16x8*>(st_a + row * MF_ROWB + swz(row, lq) * 16);
+    for (int p = 0; p < SUBT / 2; ++p) {
+      if (p >= n_pairs) break;
+      const bf16x8 x0 = xb[p & 1][0], x1 = xb[p & 1][1];
+      acc[2 * p][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[0], x0, acc[2 * p][0], 0, 0, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (p + 1 < n_pairs) {
+        xb[(p + 1) & 1][0] = read_a(2 * p + 2);
+        xb[(p + 1) & 1][1] = read_a(2 * p + 3);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+#pragma unroll
+      for (int t = 1; t < MF_NT; ++t)
+        acc[2 * p][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[t], x0, acc[2 * p][t], 0, 0, 0);
 #pragma unroll
       for (int t = 0; t < MF_NT; ++t)
-        acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[t], xfr, acc[i][t], 0, 0, 0);
+        acc[2 * p + 1][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[t], x1, acc[2 * p + 1][t], 0, 0, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * MF_NT - 1, 0);
     }
   }
 
