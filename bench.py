@@ -128,7 +128,7 @@ def measure(name, steps, warmup):
     from quantaweave_amd import workloads as W
 
     w = W.WORKLOADS[name]
-    layer = W.build_layer(w)
+    layer = W.build_layer(w).add_tiles()  # bf16 experts in QW_BF16T tiles, as the TopKMoE module keeps them
     run = W.LayerRunner(layer)
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
@@ -184,7 +184,7 @@ def measure_decode(name, steps, warmup):
     from quantaweave_amd import workloads as W
 
     w = W.WORKLOADS[name]
-    layer = W.build_layer(W.scaled(w, tokens=1))
+    layer = W.build_layer(W.scaled(w, tokens=1)).add_tiles()
     run = W.DecodeRunner(layer, tokens=1)
     stream = torch.cuda.current_stream()
     for _ in range(warmup):

@@ -31,8 +31,14 @@ extern "C" {
  * QW_U4: int4 weights packed two per byte [out, padded/2] — even input column
  * in the low nibble, odd column in the high nibble, each stored as q + 8 — with
  * fp32 scales [out, padded/group].  Layouts are exactly those of
- * src/quantization.py:36-40, :53-58. */
-enum qw_dtype { QW_F32 = 0, QW_BF16 = 1, QW_I8 = 2, QW_U4 = 3 };
+ * src/quantization.py:36-40, :53-58.
+ * QW_BF16T: bf16 weights [out, in] (out % 16 == 0, in % 32 == 0) rearranged
+ * into 1 KiB tiles [out/16][in/32][64][8]: 16-byte piece i of tile (rb, kb)
+ * holds W[16*rb + i/4][32*kb + 8*p .. 8*p + 7], p = (i % 4) ^ ((i / 8) & 3).
+ * One tile is what a 16-row, 32-column operand slice of the MFMA kernels
+ * holds in LDS, so it streams as one contiguous KiB.  No reference
+ * counterpart: it is a cache of QW_BF16 weights made by qw_pack_bf16_tiles. */
+enum qw_dtype { QW_F32 = 0, QW_BF16 = 1, QW_I8 = 2, QW_U4 = 3, QW_BF16T = 4 };
 
 /* Status codes.  INVALID maps to ValueError, the others to RuntimeError. */
 enum qw_status {
@@ -117,6 +123,7 @@ int qw_moe_permute(const void* x, int dtype, int64_t d_model, const int32_t* slo
  * x[row_index[s]] (row_index == NULL: x[s]).  row_weight may be NULL (factor 1).
  * Weights per expert, nn.Linear [out, in] layout, stacked over experts:
  *   QW_F32 / QW_BF16 : gate_w, up_w [E, d_ff, d_model]; down_w [E, d_model, d_ff]
+ *   QW_BF16T         : the same matrices in tiles (d_model and d_ff multiples of 32)
  *   QW_I8 / QW_U4    : qweight and fp32 scales stacked the same way, group sizes
  *                      group_in (gate/up, over d_model) and group_ff (down)
  * act_dtype: QW_F32 or QW_BF16 (x and y).  Quantised weights are dequantised
@@ -202,6 +209,13 @@ int qw_quantize(const void* w, int w_dtype, int64_t out_features, int64_t in_fea
  * [out, in] = q * scale per group, padding columns dropped. */
 int qw_dequantize(const void* qweight, const float* scales, int bits, int64_t out_features, int64_t in_features,
                   int64_t group_size, float* out, void* stream);
+
+/* Rearranges bf16 weights w [experts, out_features, in_features] (nn.Linear
+ * layout, stacked) into the QW_BF16T tiles of the same size.  No reference
+ * counterpart (the reference's Triton kernels read nn.Linear weights as
+ * stored); callers pack once per weight update and pass QW_BF16T. */
+int qw_pack_bf16_tiles(const void* w, int64_t experts, int64_t out_features, int64_t in_features, void* tiled,
+                       void* stream);
 
 /* Grouped matmul forward, moe_kernels.grouped_matmul (src/moe_kernels.py:118-135,
  * :167-171): out[rows of e] = x[rows of e] @ w[e]^T with rows of e =

@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libqwmoe.so"
 
-QW_F32, QW_BF16, QW_I8, QW_U4 = 0, 1, 2, 3
+QW_F32, QW_BF16, QW_I8, QW_U4, QW_BF16T = 0, 1, 2, 3, 4
 QW_OK, QW_ERR_INVALID, QW_ERR_UNSUPPORTED, QW_ERR_HIP, QW_ERR_WORKSPACE = 0, -1, -2, -3, -4
 
 P = ctypes.c_void_p
@@ -42,6 +42,7 @@ SIGNATURES = {
                                  P, P, P, P, P, P, P, P, P, P, P, SZ, P]),
     "qw_quantize": (I32, [P, I32, I64, I64, I32, I64, P, P, P]),
     "qw_dequantize": (I32, [P, P, I32, I64, I64, I64, P, P]),
+    "qw_pack_bf16_tiles": (I32, [P, I64, I64, I64, P, P]),
     "qw_grouped_matmul": (I32, [P, I32, P, I32, P, I64, I64, I64, I64, P, I64, P, P]),
 }
 

@@ -49,6 +49,7 @@ int combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* 
 int decode_combine(const void* y, int dtype, const int32_t* route_slot, const float* top_w, const float* residual,
                    int64_t T, int64_t K, int64_t D, float* out, hipStream_t stream);
 int cast_bf16(const float* x, int64_t n, uint16_t* out, hipStream_t stream);
+int pack_bf16_tiles(const void* w, int64_t E, int64_t rows, int64_t cols, void* out, hipStream_t stream);
 int balance(const float* probs, const int32_t* counts, int64_t T, int64_t K, int64_t E, float* importance,
             float* bal, hipStream_t stream, float* scratch_importance);
 int quantize(const void* w, int wdt, int64_t rows, int64_t cols, int bits, int64_t group, void* qweight, float* scales,
@@ -83,8 +84,10 @@ int experts(const void* x, int act, const int32_t* row_index, const int32_t* off
             const void* up_w, const float* up_s, const void* down_w, const float* down_s, const float* row_weight,
             void* y, void* ws, size_t ws_bytes, hipStream_t stream, int64_t avg_rows, int64_t row_cap) {
   QW_REQUIRE(act == QW_F32 || act == QW_BF16, "activation dtype must be f32 or bf16");
-  QW_REQUIRE(wfmt >= QW_F32 && wfmt <= QW_U4, "unknown weight format %d", wfmt);
+  QW_REQUIRE(wfmt >= QW_F32 && wfmt <= QW_BF16T, "unknown weight format %d", wfmt);
   QW_REQUIRE(E >= 1 && E <= 65535, "experts out of range");
+  QW_REQUIRE(wfmt != QW_BF16T || (D % 32 == 0 && F % 32 == 0),
+             "tiled bf16 weights need d_model and d_ff multiples of 32 (got %lld, %lld)", (long long)D, (long long)F);
   QW_REQUIRE(D >= 1 && D <= INT32_MAX / 2 && F >= 1 && F <= INT32_MAX / 2, "d_model/d_ff out of range");
   QW_REQUIRE(max_rows >= 0 && max_rows <= INT32_MAX, "max_rows out of range");
   if (wfmt == QW_I8 || wfmt == QW_U4) {
@@ -428,12 +431,20 @@ int qw_dequantize(const void* qweight, const float* scales, int bits, int64_t ou
   return dequantize(qweight, scales, bits, out_features, in_features, group_size, out, as_stream(stream));
 }
 
+int qw_pack_bf16_tiles(const void* w, int64_t experts, int64_t out_features, int64_t in_features, void* tiled,
+                       void* stream) {
+  clear_error();
+  return pack_bf16_tiles(w, experts, out_features, in_features, tiled, as_stream(stream));
+}
+
 int qw_grouped_matmul(const void* x, int act_dtype, const void* w, int w_format, const float* scales, int64_t group,
                       int64_t experts, int64_t out_features, int64_t in_features, const int32_t* offsets,
                       int64_t rows, void* out, void* stream) {
   clear_error();
   QW_REQUIRE(act_dtype == QW_F32 || act_dtype == QW_BF16, "grouped_matmul dtype must be f32 or bf16");
-  QW_REQUIRE(w_format >= QW_F32 && w_format <= QW_U4, "unknown weight format %d", w_format);
+  QW_REQUIRE(w_format >= QW_F32 && w_format <= QW_BF16T, "unknown weight format %d", w_format);
+  QW_REQUIRE(w_format != QW_BF16T || (out_features % 16 == 0 && in_features % 32 == 0),
+             "tiled bf16 weights need out_features %% 16 == 0 and in_features %% 32 == 0");
   QW_REQUIRE(experts >= 1 && experts <= 65535 && out_features >= 1 && in_features >= 1 && rows >= 0 &&
                  out_features <= INT32_MAX / 2 && in_features <= INT32_MAX / 2 && rows <= INT32_MAX,
              "bad grouped_matmul sizes");

@@ -18,7 +18,8 @@
 //          1024 + u by the same v_perm trick and v_dot2_f32_f16 accumulates
 //          against activations scaled by a power of two into fp16 range
 //          (exact for bf16 values); value = scale * (acc - 1152 * sum x) / 2^s.
-//  QW_BF16: a chunk is 8 bf16 weights, used directly by v_dot2_f32_bf16.
+//  QW_BF16: a chunk is 8 bf16 weights, used directly by v_dot2_f32_bf16 (also
+//           from QW_BF16T tiles, which only changes where a chunk is read).
 //
 // The activation pieces matching a lane's chunks come straight from L2 (every
 // wave of the expert reads the same few rows), are put in the pair order of
@@ -51,8 +52,13 @@ struct Fmt<QW_I8> {
 template <>
 struct Fmt<QW_BF16> {
   static constexpr int CW = 8;
-  static constexpr float BIAS = 0.0f;
 };
+template <>
+struct Fmt<QW_BF16T> : Fmt<QW_BF16> {};  // the same weights in 1 KiB tiles
+
+// Format of the arithmetic: tiled bf16 weights are bf16 weights once loaded.
+constexpr int math_fmt(int wf) { return wf == QW_BF16T ? QW_BF16 : wf; }
+constexpr bool quantized(int wf) { return wf == QW_I8 || wf == QW_U4; }
 
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(gbf16x2, a), __builtin_bit_cast(gbf16x2, b), c, false);
@@ -151,7 +157,7 @@ template <int WF, int UNITS, int ROWS, int CPL, int MAXM>
 struct GvLds {
   static constexpr int NCH = UNITS * ROWS * CPL;                 // chunk loads per group
   static_assert(NCH == 4 || NCH == 8, "the ring reads four or eight chunks per group");
-  static constexpr bool QUANT = WF != QW_BF16;
+  static constexpr bool QUANT = quantized(WF);
   static constexpr int STAGE = NCH * 1024 + (QUANT ? NCH * 256 : 0);
   static constexpr int STAGES = 2;
   static constexpr int NDMA = NCH * (QUANT ? 2 : 1);             // DMA instructions per group
@@ -294,6 +300,8 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
     int n_experts, int max_rows, WView wa, WView wb, int K, int n_out, int gpw,
     const float* __restrict__ row_weight, uint16_t* __restrict__ out) {
+  constexpr int MW = math_fmt(WF);
+  constexpr bool TILED = WF == QW_BF16T;
   constexpr int CW = Fmt<WF>::CW;
   constexpr int DW = CW / 2;   // activation pairs per chunk
   constexpr int XP = CW / 8;   // 16-byte activation pieces per chunk
@@ -316,14 +324,14 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
   float* const staged = reinterpret_cast<float*>(ring + LD::STAGES * LD::STAGE);
   const int KC = K / CW;
   const int cpg = wa.group / CW;  // chunks per quantisation group
-  const int64_t esz = WF == QW_BF16 ? 2 : 1;
+  const int64_t esz = MW == QW_BF16 ? 2 : 1;
   const uint8_t* wbase[ROWS];
   const float* sbase[ROWS];
 #pragma unroll
   for (int rr = 0; rr < ROWS; ++rr) {
     const WView& v = rr == 0 ? wa : wb;
     wbase[rr] = static_cast<const uint8_t*>(v.w) + e * v.expert_elems * esz;
-    sbase[rr] = WF != QW_BF16 ? v.scales + e * v.expert_scales : nullptr;
+    sbase[rr] = quantized(WF) ? v.scales + e * v.expert_scales : nullptr;
   }
   const int64_t wstride = wa.row_stride * esz;
   const int sstride = wa.groups;
@@ -343,12 +351,18 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
       const int n = min(g * UNITS + u, n_out - 1);  // rows past the end: loaded, never written
 #pragma unroll
       for (int rr = 0; rr < ROWS; ++rr) {
-        const uint8_t* wrow = wbase[rr] + n * wstride;
+        // QW_BF16T: chunk c of row n sits in tile (n/16, c/4) at 16-byte piece
+        // 4*(n%16) + ((c%4) ^ ((n%16)/2 & 3)); the tiles of rows n&~15 start
+        // where those rows start in the plain layout
+        const uint8_t* wrow = wbase[rr] + static_cast<int64_t>(TILED ? (n & ~15) : n) * wstride;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
           const int q = (u * ROWS + rr) * CPL + j;
-          __builtin_amdgcn_global_load_lds(static_cast<const void*>(wrow + 16 * cidx[j]), (lds_void*)(st + q * 1024),
-                                           16, 0, 0);
+          const int64_t off = TILED ? (static_cast<int64_t>(cidx[j] >> 2) << 10) +
+                                          ((4 * (n & 15) + ((cidx[j] & 3) ^ (((n & 15) >> 1) & 3))) << 4)
+                                    : 16 * static_cast<int64_t>(cidx[j]);
+          __builtin_amdgcn_global_load_lds(static_cast<const void*>(wrow + off), (lds_void*)(st + q * 1024), 16, 0,
+                                           0);
           if constexpr (LD::QUANT)
             __builtin_amdgcn_global_load_lds(static_cast<const void*>(sbase[rr] + n * sstride + sidx[j]),
                                              (lds_void*)(st + LD::NCH * 1024 + q * 256), 4, 0, 0);
@@ -413,7 +427,7 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
       const bool valid = lane + 64 * j < KC;
 #pragma unroll
       for (int m = 0; m < MAXM; ++m) {
-        prep_chunk<WF>(raw[j][m], scale[m], xq[j][m], &xs[j][m]);
+        prep_chunk<MW>(raw[j][m], scale[m], xq[j][m], &xs[j][m]);
 #pragma unroll
         for (int p = 0; p < DW; ++p) xq[j][m][p] = valid ? xq[j][m][p] : 0u;
         xs[j][m] = valid ? xs[j][m] : 0.0f;
@@ -449,7 +463,7 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
             const uint4 wv = wq[q];
             const float sv = sq[q];
             uint32_t cw[DW];
-            chunk_pairs<WF>(wv, cw);
+            chunk_pairs<MW>(wv, cw);
 #pragma unroll
             for (int m = 0; m < MAXM; ++m) {
               if (m >= M) break;
@@ -458,8 +472,8 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
               for (int p = 0; p < DW; ++p)
                 d = WF == QW_I8 ? dot2_f16(cw[p], xq[j][m][p], d) : dot2_bf16(cw[p], xq[j][m][p], d);
               float& acc = part[((u * MAXM + m) << (ROWS - 1)) | rr];
-              if constexpr (WF == QW_BF16) acc += d;
-              else acc = __builtin_fmaf(sv, d - Fmt<WF>::BIAS * xs[j][m], acc);
+              if constexpr (MW == QW_BF16) acc += d;
+              else acc = __builtin_fmaf(sv, d - Fmt<MW>::BIAS * xs[j][m], acc);
             }
           }
       }
@@ -572,7 +586,7 @@ int launch_ffn_gemv(const FfnArgs& a, hipStream_t stream, bool* handled) {
   } else if (a.wfmt == QW_I8) {
     if (a.gate.group % 16 || a.down.group % 16) return QW_OK;
     cw = 16;
-  } else if (a.wfmt == QW_BF16) {
+  } else if (a.wfmt == QW_BF16 || a.wfmt == QW_BF16T) {
     cw = 8;
   } else {
     return QW_OK;
@@ -580,12 +594,13 @@ int launch_ffn_gemv(const FfnArgs& a, hipStream_t stream, bool* handled) {
   if (a.d_model % cw || a.d_ff % cw) return QW_OK;
   if (ceil_div(a.d_model / cw, 64) > 4 || ceil_div(a.d_ff / cw, 64) > 4) return QW_OK;
   // the padded int4/int8 row must equal the logical row (true when K is a multiple of the group)
-  if (a.wfmt != QW_BF16 && (a.gate.row_stride * (a.wfmt == QW_U4 ? 2 : 1) != a.d_model ||
+  if (quantized(a.wfmt) && (a.gate.row_stride * (a.wfmt == QW_U4 ? 2 : 1) != a.d_model ||
                             a.down.row_stride * (a.wfmt == QW_U4 ? 2 : 1) != a.d_ff))
     return QW_OK;
   int st;
   if (a.wfmt == QW_U4) st = launch_fmt<QW_U4>(a, stream);
   else if (a.wfmt == QW_I8) st = launch_fmt<QW_I8>(a, stream);
+  else if (a.wfmt == QW_BF16T) st = launch_fmt<QW_BF16T>(a, stream);
   else st = launch_fmt<QW_BF16>(a, stream);
   if (st) return st;
   *handled = true;

@@ -36,6 +36,8 @@
 // over the 8 XCDs, so block b runs on XCD b%8; all tiles of one expert are
 // given to one XCD and enumerated column-fastest, which keeps the expert's
 // activation rows (and a second row chunk's weights) in that XCD's L2.
+#include <type_traits>
+
 #include "qw_ffn.h"
 
 namespace qw {
@@ -76,7 +78,7 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <bool GATEUP, int SUBT>
+template <bool GATEUP, int SUBT, bool TILED>
 __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
     int max_rows, const uint16_t* __restrict__ wa, const uint16_t* __restrict__ wb, int64_t w_expert_stride,
@@ -144,7 +146,10 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
       base = wa_e;
     }
     wrow = min(wrow, n_w - 1);
-    b_src[q] = base + static_cast<int64_t>(wrow) * K + swz(row, lpiece) * 8;
+    if (TILED)  // the group's tile column: tiles [wrow/16][kt], one contiguous KiB each
+      b_src[q] = base + static_cast<int64_t>(wrow & ~15) * K + lane * 8;
+    else
+      b_src[q] = base + static_cast<int64_t>(wrow) * K + swz(row, lpiece) * 8;
   }
   // waves whose last A group is past AG still issue that load (into the stage's
   // padding area) so that all waves issue AL_MAX loads per activation slice
@@ -164,8 +169,8 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
 #pragma unroll
     for (int q = 0; q < BL; ++q) {
       const int g = wave + q * MF_WAVES;
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(b_src[q] + k0), (lds_void*)(st + g * 1024), 16, 0,
-                                       0);
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(b_src[q] + (TILED ? kt * 512 : k0)),
+                                       (lds_void*)(st + g * 1024), 16, 0, 0);
     }
   };
 
@@ -296,7 +301,7 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
   }
 }
 
-template <bool GATEUP, int SUBT>
+template <bool GATEUP, int SUBT, bool TILED>
 int launch_t(const void* x, const int32_t* row_index, const int32_t* offsets, int max_rows, const void* wa,
              const void* wb, int64_t w_stride, int n_w, int K, const float* row_weight, void* out, int n_out,
              int experts, int64_t rows_cap, hipStream_t stream) {
@@ -306,12 +311,12 @@ int launch_t(const void* x, const int32_t* row_index, const int32_t* offsets, in
   if (grid > INT32_MAX) return set_error(QW_ERR_UNSUPPORTED, "MFMA grid too large");
   const size_t lds = static_cast<size_t>(MF_AST) * (32 * SUBT * MF_ROWB + 1024) +
                      static_cast<size_t>(MF_BST) * MF_NB * MF_ROWB;
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_mfma_kernel<GATEUP, SUBT>),
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_mfma_kernel<GATEUP, SUBT, TILED>),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize,
                                                      static_cast<int>(lds));
   if (attr != hipSuccess)
     return set_error(QW_ERR_HIP, "cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(attr));
-  ffn_mfma_kernel<GATEUP, SUBT><<<static_cast<unsigned>(grid), MF_THREADS, lds, stream>>>(
+  ffn_mfma_kernel<GATEUP, SUBT, TILED><<<static_cast<unsigned>(grid), MF_THREADS, lds, stream>>>(
       static_cast<const uint16_t*>(x), row_index, offsets, max_rows, static_cast<const uint16_t*>(wa),
       static_cast<const uint16_t*>(wb), w_stride, n_w, K, row_weight, static_cast<uint16_t*>(out), n_out, n_tiles,
       m_chunks, experts);
@@ -320,13 +325,14 @@ int launch_t(const void* x, const int32_t* row_index, const int32_t* offsets, in
 }
 
 // rows_cap: most rows any expert can hold (the capacity bound).
-template <bool GATEUP>
+template <bool GATEUP, bool TILED>
 int launch_sel(int subt, const void* x, const int32_t* row_index, const int32_t* offsets, int max_rows,
                const void* wa, const void* wb, int64_t w_stride, int n_w, int K, const float* row_weight, void* out,
                int n_out, int experts, int64_t rows_cap, hipStream_t stream) {
 #define QW_MF(S)                                                                                                \
   if (subt == S)                                                                                               \
-    return launch_t<GATEUP, S>(x, row_index, offsets, max_rows, wa, wb, w_stride, n_w, K, row_weight, out, n_out, \
+    return launch_t<GATEUP, S, TILED>(x, row_index, offsets, max_rows, wa, wb, w_stride, n_w, K, row_weight, out,   \
+                                      n_out, \
                                experts, rows_cap, stream);
   QW_MF(2)
   QW_MF(4)
@@ -348,18 +354,22 @@ int pick_subt(int64_t rows_cap) {
 
 int launch_ffn_mfma(const FfnArgs& a, hipStream_t stream, bool* handled) {
   *handled = false;
-  if (a.act != QW_BF16 || a.wfmt != QW_BF16) return QW_OK;
+  if (a.act != QW_BF16 || (a.wfmt != QW_BF16 && a.wfmt != QW_BF16T)) return QW_OK;
   if (a.d_model % 64 || a.d_ff % 64) return QW_OK;
   if (a.avg_rows < 16) return QW_OK;  // decode-sized: weight streaming kernels
   const int64_t rows_cap = a.row_cap > 0 ? a.row_cap : a.max_rows;
   const int subt = pick_subt(rows_cap);
   const int D = static_cast<int>(a.d_model), F = static_cast<int>(a.d_ff), E = static_cast<int>(a.experts);
   const int mr = static_cast<int>(a.max_rows);
-  int st = launch_sel<true>(subt, a.x, a.row_index, a.offsets, mr, a.gate.w, a.up.w, a.gate.expert_elems, F, D,
-                            nullptr, a.hidden, F, E, rows_cap, stream);
-  if (st) return st;
-  st = launch_sel<false>(subt, a.hidden, nullptr, a.offsets, mr, a.down.w, a.down.w, a.down.expert_elems, D, F,
-                         a.row_weight, a.y, D, E, rows_cap, stream);
+  auto both = [&](auto tiled) -> int {
+    constexpr bool T = decltype(tiled)::value;
+    int st = launch_sel<true, T>(subt, a.x, a.row_index, a.offsets, mr, a.gate.w, a.up.w, a.gate.expert_elems, F, D,
+                                 nullptr, a.hidden, F, E, rows_cap, stream);
+    if (st) return st;
+    return launch_sel<false, T>(subt, a.hidden, nullptr, a.offsets, mr, a.down.w, a.down.w, a.down.expert_elems, D,
+                                F, a.row_weight, a.y, D, E, rows_cap, stream);
+  };
+  const int st = a.wfmt == QW_BF16T ? both(std::true_type{}) : both(std::false_type{});
   if (st) return st;
   *handled = true;
   return QW_OK;

@@ -257,6 +257,42 @@ int cast_bf16(const float* x, int64_t n, uint16_t* out, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------
+// QW_BF16T packing: one thread per 16-byte piece of the tiled output, which is
+// written in order (the reads are 16-byte pieces of the plain rows).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void pack_bf16_tiles_kernel(const uint16_t* __restrict__ w, int64_t pieces,
+                                                              int64_t rows, int64_t cols,
+                                                              uint16_t* __restrict__ out) {
+  const int64_t o = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (o >= pieces) return;
+  const int64_t per_expert = rows * cols / 8;
+  const int64_t e = o / per_expert, rem = o % per_expert;
+  const int64_t tile = rem / 64, i = rem % 64;
+  const int64_t kt = cols / 32;
+  const int64_t rb = tile / kt, kb = tile % kt;
+  const int64_t row = 16 * rb + i / 4;
+  const int64_t p = (i % 4) ^ ((i / 8) & 3);
+  const uint4 v = *reinterpret_cast<const uint4*>(w + e * rows * cols + row * cols + kb * 32 + p * 8);
+  *reinterpret_cast<uint4*>(out + o * 8) = v;
+}
+
+int pack_bf16_tiles(const void* w, int64_t E, int64_t rows, int64_t cols, void* out, hipStream_t stream) {
+  QW_REQUIRE(E >= 1 && rows >= 1 && cols >= 1, "bad tile packing sizes");
+  QW_REQUIRE(rows % 16 == 0 && cols % 32 == 0,
+             "tiled bf16 weights need out_features %% 16 == 0 and in_features %% 32 == 0 (got %lld, %lld)",
+             (long long)rows, (long long)cols);
+  QW_REQUIRE(w && out, "packing pointers are required");
+  QW_REQUIRE(w != out, "packing cannot run in place");
+  QW_REQUIRE((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out)) % 16 == 0,
+             "packing needs 16-byte aligned buffers");
+  const int64_t pieces = E * rows * cols / 8;
+  pack_bf16_tiles_kernel<<<static_cast<unsigned>(ceil_div(pieces, 256)), 256, 0, stream>>>(
+      static_cast<const uint16_t*>(w), pieces, rows, cols, static_cast<uint16_t*>(out));
+  QW_LAUNCH_CHECK("pack_bf16_tiles_kernel");
+  return QW_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Balance loss (src/quantweave_moe_model.py:152-154).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void importance_kernel(const float* __restrict__ probs, int T, int E,

@@ -33,7 +33,7 @@ inline WView make_wview(int fmt, const void* w, const float* scales, int64_t row
   v.rows = rows;
   v.cols = cols;
   v.group = group;
-  if (fmt == QW_F32 || fmt == QW_BF16) {
+  if (fmt == QW_F32 || fmt == QW_BF16 || fmt == QW_BF16T) {
     v.row_stride = cols;
     v.groups = 0;
   } else {
@@ -46,6 +46,16 @@ inline WView make_wview(int fmt, const void* w, const float* scales, int64_t row
   return v;
 }
 
+// Element offset of W[row][col] in the QW_BF16T tiles of a [rows, cols] matrix:
+// tile (row/16, col/32) of 512 elements; in it, 16-byte piece i = 4*(row%16) +
+// (p ^ ((row%16 / 2) & 3)) with p = (col%32) / 8, then col%8.
+__host__ __device__ __forceinline__ int64_t bf16t_index(int64_t row, int64_t col, int64_t cols) {
+  const int64_t tile = (row >> 4) * (cols >> 5) + (col >> 5);
+  const int r = static_cast<int>(row & 15);
+  const int piece = 4 * r + ((static_cast<int>((col >> 3) & 3)) ^ ((r >> 1) & 3));
+  return tile * 512 + piece * 8 + (col & 7);
+}
+
 // Dequantised fp32 value of element (row, col) of expert e, before the cast to
 // the activation dtype.
 template <int WF>
@@ -54,6 +64,8 @@ __device__ __forceinline__ float load_weight(const WView& v, int64_t e, int64_t 
     return static_cast<const float*>(v.w)[e * v.expert_elems + row * v.row_stride + col];
   } else if constexpr (WF == QW_BF16) {
     return bf16_to_f32(static_cast<const uint16_t*>(v.w)[e * v.expert_elems + row * v.row_stride + col]);
+  } else if constexpr (WF == QW_BF16T) {
+    return bf16_to_f32(static_cast<const uint16_t*>(v.w)[e * v.expert_elems + bf16t_index(row, col, v.cols)]);
   } else if constexpr (WF == QW_I8) {
     const int8_t q = static_cast<const int8_t*>(v.w)[e * v.expert_elems + row * v.row_stride + col];
     const float s = v.scales[e * v.expert_scales + row * v.groups + col / v.group];

@@ -81,6 +81,7 @@ class MoEDecodeStep:
                 setattr(self.pack, name, t.contiguous())
         if cast:
             self.pack.fmt = _lib.QW_BF16
+            self.pack.maybe_tile()
         self.ffn = int(experts[0].gate.out_features)
         T, E, K = self.tokens, self.experts_count, self.top_k
         lib = _lib.load()

@@ -106,12 +106,30 @@ def _expert_format(experts: nn.ModuleList) -> tuple[int, int, int]:
     return (_lib.QW_F32 if dt == torch.float32 else _lib.QW_BF16), 0, 0
 
 
+def tile_bf16(stack: Tensor) -> Tensor:
+    """bf16 weights [E, out, in] (nn.Linear layout) rearranged into the 1 KiB
+    tiles of QW_BF16T (qw_pack_bf16_tiles); same shape and size."""
+    stack = stack.contiguous()
+    _hip.require_device(stack, "tile_bf16")
+    if stack.dtype != torch.bfloat16 or stack.dim() != 3:
+        raise ValueError("tile_bf16 takes a bf16 [experts, out, in] tensor")
+    out = torch.empty_like(stack)
+    E, rows, cols = stack.shape
+    _lib.call("qw_pack_bf16_tiles", _hip.ptr(stack), E, rows, cols, _hip.ptr(out), _hip.stream(stack.device))
+    return out
+
+
+def can_tile(stack: Tensor) -> bool:
+    return stack.dtype == torch.bfloat16 and stack.size(1) % 16 == 0 and stack.size(2) % 32 == 0
+
+
 class ExpertPack:
     """Experts' weights stacked once into [E, out, in] device buffers.
 
     Replaces the per-call ``torch.stack`` of src/moe_kernels.py:191-193; the pack
     is rebuilt only when a parameter or buffer changes (tracked by its storage
-    pointer and version counter)."""
+    pointer and version counter).  bf16 weights whose shapes allow it are kept
+    in the QW_BF16T tiles the prefill kernels stream contiguously."""
 
     def __init__(self, experts: nn.ModuleList) -> None:
         self.fmt, self.group_in, self.group_ff = _expert_format(experts)
@@ -121,6 +139,7 @@ class ExpertPack:
             self.up = torch.stack([e.up.weight.detach() for e in experts]).contiguous()
             self.down = torch.stack([e.down.weight.detach() for e in experts]).contiguous()
             self.gate_s = self.up_s = self.down_s = None
+            self.maybe_tile()
         else:
             self.gate = torch.stack([e.gate.qweight for e in experts]).contiguous()
             self.up = torch.stack([e.up.qweight for e in experts]).contiguous()
@@ -128,6 +147,14 @@ class ExpertPack:
             self.gate_s = torch.stack([e.gate.scales.float() for e in experts]).contiguous()
             self.up_s = torch.stack([e.up.scales.float() for e in experts]).contiguous()
             self.down_s = torch.stack([e.down.scales.float() for e in experts]).contiguous()
+
+    def maybe_tile(self) -> None:
+        """bf16 stacks on a ROCm device -> QW_BF16T tiles (in place of the plain stacks)."""
+        if self.fmt != _lib.QW_BF16 or self.gate.device.type != "cuda":
+            return
+        if all(can_tile(t) for t in (self.gate, self.up, self.down)):
+            self.gate, self.up, self.down = tile_bf16(self.gate), tile_bf16(self.up), tile_bf16(self.down)
+            self.fmt = _lib.QW_BF16T
 
     @staticmethod
     def signature(experts: nn.ModuleList) -> tuple:

@@ -89,8 +89,19 @@ class Layer:
     extra: dict = field(default_factory=dict)
 
     def weight_args(self) -> list:
+        """Weight arguments of the C ABI; bf16 layers pass their QW_BF16T tiles when they have them."""
+        if "tiles" in self.extra:
+            g, u, d = self.extra["tiles"]
+            return [_lib.QW_BF16T, 0, 0, _hip.ptr(g), None, _hip.ptr(u), None, _hip.ptr(d), None]
         return [self.fmt, self.group_in, self.group_ff, _hip.ptr(self.gate), _hip.ptr(self.gate_s),
                 _hip.ptr(self.up), _hip.ptr(self.up_s), _hip.ptr(self.down), _hip.ptr(self.down_s)]
+
+    def add_tiles(self) -> "Layer":
+        """Pack bf16 weights into QW_BF16T tiles (as the TopKMoE module does) and use them."""
+        from .moe import can_tile, tile_bf16
+        if self.fmt == _lib.QW_BF16 and all(can_tile(t) for t in (self.gate, self.up, self.down)):
+            self.extra["tiles"] = (tile_bf16(self.gate), tile_bf16(self.up), tile_bf16(self.down))
+        return self
 
     def expert_bytes(self) -> int:
         """Stored bytes of one expert's three projections (weights + scales)."""

@@ -51,11 +51,14 @@ def make_moe(E, D, F_, k, fmt, seed, temperature=1.0, bias=False, group=None):
 def oracle_weights(step):
     """The expert weights the step multiplies, as the oracle's weight dict."""
     p = step.pack
-    fmt = {_lib.QW_F32: "f32", _lib.QW_BF16: "bf16", _lib.QW_I8: "i8", _lib.QW_U4: "u4"}[p.fmt]
+    fmt = {_lib.QW_F32: "f32", _lib.QW_BF16: "bf16", _lib.QW_BF16T: "bf16", _lib.QW_I8: "i8",
+           _lib.QW_U4: "u4"}[p.fmt]
     w = dict(format=fmt, d_model=step.hidden, d_ff=step.ffn, group_in=p.group_in, group_ff=p.group_ff)
     for name in ("gate", "up", "down"):
         t = getattr(p, name)
         w[name] = t.float().cpu().numpy() if fmt in ("f32", "bf16") else t.cpu().numpy()
+        if p.fmt == _lib.QW_BF16T:
+            w[name] = oracle.untile_bf16(w[name])
         s = getattr(p, name + "_s")
         if s is not None:
             w[name + "_scales"] = s.cpu().numpy()

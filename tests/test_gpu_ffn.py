@@ -201,3 +201,49 @@ def test_quantized_linear_forward(bits, group, max_rel):
         err = np.linalg.norm(got - (x.float() @ lin.weight.T).detach().cpu().numpy()) / np.linalg.norm(ref)
         assert err < max_rel + (0.02 if dtype == torch.bfloat16 else 0)
     assert q.stored_bytes() < lin.weight.numel() * 4 / (3.5 if bits == 8 else 4)
+
+
+# ---------------------------------------------------------------- QW_BF16T tiled weights
+def test_bf16_tile_packing_matches_the_layout():
+    rng = np.random.RandomState(70)
+    w = oracle.round_bf16(rng.randn(3, 48, 96).astype(np.float32))
+    tiled = qa.moe.tile_bf16(H.dev(w, torch.bfloat16))
+    torch.cuda.synchronize()
+    assert np.array_equal(tiled.float().cpu().numpy(), oracle.tile_bf16(w))
+    with pytest.raises(ValueError, match="16"):
+        bad = H.dev(np.zeros((1, 8, 64), np.float32), torch.bfloat16)
+        _lib.call("qw_pack_bf16_tiles", H.P(bad), 1, 8, 64, H.P(torch.empty_like(bad)), H.s())
+
+
+@pytest.mark.parametrize("counts,D,F_", [
+    ([40, 0, 70, 33, 64, 1], 128, 256),   # prefill-sized rows: MFMA kernels
+    ([1, 0, 3, 2], 256, 512),             # decode-sized rows: weight-streaming kernels
+    (COUNTS, 64, 96),                     # d_ff not a multiple of 64: general kernel
+])
+def test_tiled_bf16_weights_give_identical_outputs(counts, D, F_):
+    """The tiles change where each weight is read, not the arithmetic: the
+    outputs equal those from the plain layout bit for bit, on every path."""
+    print(f"case tiles counts={counts} D={D} F={F_}", flush=True)
+    rng = np.random.RandomState(D + F_ + 1)
+    rows = sum(counts)
+    x = oracle.round_bf16(rng.randn(rows, D).astype(np.float32))
+    w = make_weights(len(counts), D, F_, "bf16", D * F_ + 3)
+    rw = rng.rand(rows).astype(np.float32)
+    plain = run_experts(x, counts, w, "bf16", row_weight=rw)
+    dw = device_weights(w)
+    offsets = H.dev(np.concatenate([[0], np.cumsum(counts)]).astype(np.int32))
+    tiled = H.experts(H.dev(x, torch.bfloat16), offsets, _lib.QW_BF16T, qa.moe.tile_bf16(dw["gate"]),
+                      qa.moe.tile_bf16(dw["up"]), qa.moe.tile_bf16(dw["down"]),
+                      row_weight=H.dev(rw), max_rows=rows, rows_per_expert=max(counts)).float().cpu().numpy()
+    assert np.array_equal(plain, tiled)
+    ref = oracle.round_act(oracle.experts_forward(x, np.array(counts), w, "bf16") * rw[:, None], "bf16")
+    assert normwise(tiled, ref) <= 2e-2
+
+
+def test_tiled_bf16_shape_errors():
+    x = H.dev(np.zeros((4, 48), np.float32), torch.bfloat16)
+    wt = H.dev(np.zeros((1, 64, 48), np.float32), torch.bfloat16)
+    wd = H.dev(np.zeros((1, 48, 64), np.float32), torch.bfloat16)
+    offsets = H.dev(np.array([0, 4], np.int32))
+    with pytest.raises(ValueError, match="multiples of 32"):
+        H.experts(x, offsets, _lib.QW_BF16T, wt, wt, wd, max_rows=4, rows_per_expert=4)

@@ -256,3 +256,17 @@ def test_small_batch_routing_and_plan_with_duplicate_tokens(T, E, k, cap):
     assert np.array_equal(run.dropped_token.cpu().numpy()[:nd], p["dropped_token"])
     assert np.array_equal(run.dropped_expert.cpu().numpy()[:nd], p["dropped_expert"])
     assert normwise(run.out.float().cpu().numpy(), res["out"]) <= TOL["bf16"]
+
+
+def test_layer_with_tiled_bf16_weights_is_identical():
+    """The module packs bf16 experts into QW_BF16T tiles; the layer output is the
+    same bit for bit as with the plain weights."""
+    w = W.scaled(W.WORKLOADS["bf16-prefill-T8192-d2048-E64-f1024-k2"], tokens=1024, d_model=512, d_ff=256)
+    layer = W.build_layer(w)
+    plain = W.LayerRunner(layer)
+    plain()
+    tiled = W.LayerRunner(W.build_layer(w).add_tiles())
+    assert "tiles" in tiled.layer.extra
+    tiled()
+    torch.cuda.synchronize()
+    assert torch.equal(plain.out, tiled.out) and torch.equal(plain.top_idx, tiled.top_idx)
