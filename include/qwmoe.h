@@ -32,12 +32,13 @@ extern "C" {
  * in the low nibble, odd column in the high nibble, each stored as q + 8 — with
  * fp32 scales [out, padded/group].  Layouts are exactly those of
  * src/quantization.py:36-40, :53-58.
- * QW_BF16T: bf16 weights [out, in] (out % 16 == 0, in % 32 == 0) rearranged
- * into 1 KiB tiles [out/16][in/32][64][8]: 16-byte piece i of tile (rb, kb)
- * holds W[16*rb + i/4][32*kb + 8*p .. 8*p + 7], p = (i % 4) ^ ((i / 8) & 3).
- * One tile is what a 16-row, 32-column operand slice of the MFMA kernels
- * holds in LDS, so it streams as one contiguous KiB.  No reference
- * counterpart: it is a cache of QW_BF16 weights made by qw_pack_bf16_tiles. */
+ * QW_BF16T: bf16 weights [out, in] (out % 8 == 0, in % 64 == 0) rearranged
+ * into 1 KiB tiles [out/8][in/64][64][8]: 16-byte piece i of tile (rb, kb)
+ * holds W[r][64*kb + 8*p .. 8*p + 7] with r = 8*rb + i/8 and
+ * p = (i % 8) ^ ((r / 2) % 8).  One tile is what an 8-row, 64-column operand
+ * slice of the MFMA kernels holds in LDS, so it streams as one contiguous KiB.
+ * No reference counterpart: it is a cache of QW_BF16 weights made by
+ * qw_pack_bf16_tiles. */
 enum qw_dtype { QW_F32 = 0, QW_BF16 = 1, QW_I8 = 2, QW_U4 = 3, QW_BF16T = 4 };
 
 /* Status codes.  INVALID maps to ValueError, the others to RuntimeError. */
@@ -123,7 +124,7 @@ int qw_moe_permute(const void* x, int dtype, int64_t d_model, const int32_t* slo
  * x[row_index[s]] (row_index == NULL: x[s]).  row_weight may be NULL (factor 1).
  * Weights per expert, nn.Linear [out, in] layout, stacked over experts:
  *   QW_F32 / QW_BF16 : gate_w, up_w [E, d_ff, d_model]; down_w [E, d_model, d_ff]
- *   QW_BF16T         : the same matrices in tiles (d_model and d_ff multiples of 32)
+ *   QW_BF16T         : the same matrices in tiles (d_model and d_ff multiples of 64)
  *   QW_I8 / QW_U4    : qweight and fp32 scales stacked the same way, group sizes
  *                      group_in (gate/up, over d_model) and group_ff (down)
  * act_dtype: QW_F32 or QW_BF16 (x and y).  Quantised weights are dequantised

@@ -177,31 +177,33 @@ def plan(top_idx: np.ndarray, top_w: np.ndarray, experts: int, cap: int) -> dict
 # ---------------------------------------------------------------------------
 def _tile_perm(shape):
     E, R, K = shape
-    if R % 16 or K % 32:
-        raise ValueError("tiles need out % 16 == 0 and in % 32 == 0")
-    r = np.arange(16)[:, None]
-    phys = np.arange(4)[None, :]
-    return (R, K), r, phys ^ ((r >> 1) & 3)
+    if R % 8 or K % 64:
+        raise ValueError("tiles need out % 8 == 0 and in % 64 == 0")
+    rb = np.arange(R // 8)[:, None, None]
+    r = np.arange(8)[None, :, None]
+    phys = np.arange(8)[None, None, :]
+    return (R, K), rb, r, phys ^ (((8 * rb + r) >> 1) & 7)
 
 
 def tile_bf16(w: np.ndarray) -> np.ndarray:
-    """[E, out, in] -> the same values in QW_BF16T order (tile (rb, kb) =
-    512 consecutive elements; its 16-byte piece 4*r + phys holds row 16*rb + r,
-    columns 32*kb + 8*p .. +7 with p = phys ^ ((r >> 1) & 3))."""
+    """[E, out, in] -> the same values in QW_BF16T order (tile (rb, kb) = 512
+    consecutive elements; its 16-byte piece 8*r + phys holds row 8*rb + r,
+    columns 64*kb + 8*p .. +7 with p = phys ^ (((8*rb + r) >> 1) & 7))."""
     E = w.shape[0]
-    (R, K), r, p = _tile_perm(w.shape)
-    w6 = w.reshape(E, R // 16, 16, K // 32, 4, 8).transpose(0, 1, 3, 2, 4, 5)  # E, rb, kb, r, p, 8
-    return np.ascontiguousarray(w6[:, :, :, r, p, :]).reshape(E, R, K)
+    (R, K), rb, r, p = _tile_perm(w.shape)
+    w6 = w.reshape(E, R // 8, 8, K // 64, 8, 8).transpose(0, 3, 1, 2, 4, 5)  # E, kb, rb, r, p, 8
+    t = w6[:, :, rb, r, p, :]  # E, kb, rb, r, phys, 8
+    return np.ascontiguousarray(t.transpose(0, 2, 1, 3, 4, 5)).reshape(E, R, K)
 
 
 def untile_bf16(t: np.ndarray) -> np.ndarray:
     """Inverse of tile_bf16."""
     E = t.shape[0]
-    (R, K), r, p = _tile_perm(t.shape)
-    t6 = t.reshape(E, R // 16, K // 32, 16, 4, 8)  # E, rb, kb, r, phys, 8
-    w6 = np.empty_like(t6)
-    w6[:, :, :, r, p, :] = t6
-    return np.ascontiguousarray(w6.transpose(0, 1, 3, 2, 4, 5)).reshape(E, R, K)
+    (R, K), rb, r, p = _tile_perm(t.shape)
+    t6 = t.reshape(E, R // 8, K // 64, 8, 8, 8).transpose(0, 2, 1, 3, 4, 5)  # E, kb, rb, r, phys, 8
+    w6 = np.empty_like(t6)  # E, kb, rb, r, p, 8
+    w6[:, :, rb, r, p, :] = t6
+    return np.ascontiguousarray(w6.transpose(0, 2, 3, 1, 4, 5)).reshape(E, R, K)
 
 
 # ---------------------------------------------------------------------------

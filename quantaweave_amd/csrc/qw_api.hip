@@ -86,8 +86,8 @@ int experts(const void* x, int act, const int32_t* row_index, const int32_t* off
   QW_REQUIRE(act == QW_F32 || act == QW_BF16, "activation dtype must be f32 or bf16");
   QW_REQUIRE(wfmt >= QW_F32 && wfmt <= QW_BF16T, "unknown weight format %d", wfmt);
   QW_REQUIRE(E >= 1 && E <= 65535, "experts out of range");
-  QW_REQUIRE(wfmt != QW_BF16T || (D % 32 == 0 && F % 32 == 0),
-             "tiled bf16 weights need d_model and d_ff multiples of 32 (got %lld, %lld)", (long long)D, (long long)F);
+  QW_REQUIRE(wfmt != QW_BF16T || (D % 64 == 0 && F % 64 == 0),
+             "tiled bf16 weights need d_model and d_ff multiples of 64 (got %lld, %lld)", (long long)D, (long long)F);
   QW_REQUIRE(D >= 1 && D <= INT32_MAX / 2 && F >= 1 && F <= INT32_MAX / 2, "d_model/d_ff out of range");
   QW_REQUIRE(max_rows >= 0 && max_rows <= INT32_MAX, "max_rows out of range");
   if (wfmt == QW_I8 || wfmt == QW_U4) {
@@ -443,8 +443,8 @@ int qw_grouped_matmul(const void* x, int act_dtype, const void* w, int w_format,
   clear_error();
   QW_REQUIRE(act_dtype == QW_F32 || act_dtype == QW_BF16, "grouped_matmul dtype must be f32 or bf16");
   QW_REQUIRE(w_format >= QW_F32 && w_format <= QW_BF16T, "unknown weight format %d", w_format);
-  QW_REQUIRE(w_format != QW_BF16T || (out_features % 16 == 0 && in_features % 32 == 0),
-             "tiled bf16 weights need out_features %% 16 == 0 and in_features %% 32 == 0");
+  QW_REQUIRE(w_format != QW_BF16T || (out_features % 8 == 0 && in_features % 64 == 0),
+             "tiled bf16 weights need out_features %% 8 == 0 and in_features %% 64 == 0");
   QW_REQUIRE(experts >= 1 && experts <= 65535 && out_features >= 1 && in_features >= 1 && rows >= 0 &&
                  out_features <= INT32_MAX / 2 && in_features <= INT32_MAX / 2 && rows <= INT32_MAX,
              "bad grouped_matmul sizes");

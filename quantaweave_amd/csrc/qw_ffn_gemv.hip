@@ -351,15 +351,15 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
       const int n = min(g * UNITS + u, n_out - 1);  // rows past the end: loaded, never written
 #pragma unroll
       for (int rr = 0; rr < ROWS; ++rr) {
-        // QW_BF16T: chunk c of row n sits in tile (n/16, c/4) at 16-byte piece
-        // 4*(n%16) + ((c%4) ^ ((n%16)/2 & 3)); the tiles of rows n&~15 start
-        // where those rows start in the plain layout
-        const uint8_t* wrow = wbase[rr] + static_cast<int64_t>(TILED ? (n & ~15) : n) * wstride;
+        // QW_BF16T: chunk c of row n sits in tile (n/8, c/8) at 16-byte piece
+        // 8*(n%8) + ((c%8) ^ ((n/2) % 8)); the tiles of rows n&~7 start where
+        // those rows start in the plain layout
+        const uint8_t* wrow = wbase[rr] + static_cast<int64_t>(TILED ? (n & ~7) : n) * wstride;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
           const int q = (u * ROWS + rr) * CPL + j;
-          const int64_t off = TILED ? (static_cast<int64_t>(cidx[j] >> 2) << 10) +
-                                          ((4 * (n & 15) + ((cidx[j] & 3) ^ (((n & 15) >> 1) & 3))) << 4)
+          const int64_t off = TILED ? (static_cast<int64_t>(cidx[j] >> 3) << 10) +
+                                          ((8 * (n & 7) + ((cidx[j] & 7) ^ ((n >> 1) & 7))) << 4)
                                     : 16 * static_cast<int64_t>(cidx[j]);
           __builtin_amdgcn_global_load_lds(static_cast<const void*>(wrow + off), (lds_void*)(st + q * 1024), 16, 0,
                                            0);

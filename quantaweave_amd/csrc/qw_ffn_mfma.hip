@@ -12,21 +12,25 @@
 //                 columns), DOWN: 256 output columns.
 //
 // Operands move HBM/L2 -> LDS with global_load_lds_dwordx4 (no register
-// staging) in K-slices of 32 through two 3-stage rings, the weight slices (the
-// HBM stream) and the activation slices (L2 resident) both requested two
-// slices ahead, right after the slice's barrier, so they are in flight during
-// the MFMAs (deeper weight rings measured slower: they leave no LDS for a
-// deeper activation ring).  One LDS barrier per slice.  Loads complete in
-// issue order and every wave issues the same loads per slice (rows past the
-// end are clamped to a valid row, their results never stored), so a fixed
-// `s_waitcnt vmcnt(n)` marks a slice as landed.
+// staging) in K-slices of 64 (two MFMA K steps) through rings of two or three
+// stages (three when the row chunk leaves room in the 160 KiB of LDS), the
+// next slices requested right after each slice's barrier so they are in
+// flight during the MFMAs.  One LDS barrier per slice.  A load group is eight
+// whole 128-byte row segments (one KiB), so every request is full cache lines;
+// QW_BF16T weights come pre-arranged in exactly those KiB tiles and stream
+// contiguously.  Loads complete in issue order and every wave issues the same
+// loads per slice (rows past the end are clamped to a valid row, their results
+// never stored), so a fixed `s_waitcnt vmcnt(n)` marks a slice as landed.
 //
-// LDS rows are 64 bytes (32 bf16); the four 16-byte pieces of row r are stored
-// XOR-swizzled by ((r >> 1) & 3) so the 16-row fragment reads of the MFMAs
-// hit distinct banks.
+// LDS rows are 128 bytes (64 bf16); the eight 16-byte pieces of row r are
+// stored XOR-swizzled by ((r >> 1) & 7) so the 16-row fragment reads of the
+// MFMAs hit distinct banks.  Within a slice the fragment reads are pipelined
+// behind the MFMAs (two activation pair buffers, weight fragments per K step),
+// with the order pinned by scheduling barriers.
 //
 // Waves form a 2 x 4 grid: wave (wm, wn) computes row sub-tiles wm, wm+2, ...
-// (16 rows each, skipped past the expert's row count) against its 64 weight
+// (16 rows each; those past the expert's row count run on clamped copies of a
+// valid row and are not stored) against its 64 weight
 // rows (GATEUP: 32 gate rows and the matching 32 up rows, so SiLU(g)*u is
 // formed in registers).  The MFMA takes the weights as its A operand, so a
 // lane ends up holding 4 consecutive output columns of one row and stores them
@@ -48,15 +52,21 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int MF_BK = 32;       // K slice (one MFMA K step)
-constexpr int MF_ROWB = 64;     // bytes per LDS row (32 bf16, no padding: swizzled)
+constexpr int MF_BK = 64;       // K slice: two MFMA K steps
+constexpr int MF_ROWB = 128;    // bytes per LDS row (64 bf16, no padding: swizzled)
+constexpr int MF_GROWS = 8;     // rows per 1 KiB load group (8 lanes per 128-byte row)
 constexpr int MF_NB = 256;      // weight rows per column tile
 constexpr int MF_THREADS = 512;
 constexpr int MF_WAVES = 8;
 constexpr int MF_NT = 4;        // 16-column MFMA tiles per wave
-constexpr int MF_AST = 3;       // activation ring stages
-constexpr int MF_BST = 3;       // weight ring stages
-constexpr int MF_AHEAD = 2;     // slices requested ahead of the one computed (< both stage counts)
+constexpr int MF_LDS = 160 * 1024;  // LDS per workgroup
+
+// Ring stages (activation and weight slices together) that fit the LDS, at most
+// three; the slices requested ahead are one fewer.
+constexpr int mf_stages(int subt) {
+  const int stage = 32 * subt * MF_ROWB + MF_NB * MF_ROWB;
+  return MF_LDS / stage >= 3 ? 3 : 2;
+}
 constexpr int kXcds = 8;
 
 // s_waitcnt immediate waiting for vmcnt <= n only (expcnt, lgkmcnt left at max).
@@ -66,7 +76,10 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
 }
 
-__device__ __forceinline__ int swz(int row, int piece) { return piece ^ ((row >> 1) & 3); }
+// 16-byte piece `piece` (0..7) of LDS row `row` is stored at physical piece
+// piece ^ ((row >> 1) & 7): the 16-row fragment reads of an MFMA (one logical
+// piece, rows 0..15) then touch 16 distinct bank groups.
+__device__ __forceinline__ int swz(int row, int piece) { return piece ^ ((row >> 1) & 7); }
 
 // Barrier for the LDS ring: the slice's loads were already waited for with an
 // explicit vmcnt, so no fence is needed (a workgroup fence would wait for every
@@ -85,18 +98,16 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
     int n_w, int K, const float* __restrict__ row_weight, uint16_t* __restrict__ out, int n_out, int n_tiles,
     int m_chunks, int experts) {
   constexpr int MCH = 32 * SUBT;                 // rows per chunk
-  constexpr int AG = MCH / 16;                   // 16-row load groups of the A slice
-  constexpr int BG = MF_NB / 16;                 // ... of the B slice
-  constexpr int A_BYTES = MCH * MF_ROWB, B_BYTES = MF_NB * MF_ROWB;
-  // activation stage + 1 KiB that receives the padding loads of waves with one
-  // A group fewer (every wave issues the same number of loads per slice)
-  constexpr int A_STAGE = A_BYTES + 1024;
-  constexpr int AL_MAX = (AG + MF_WAVES - 1) / MF_WAVES;  // A groups per wave (upper bound)
+  constexpr int AG = MCH / MF_GROWS;             // 8-row load groups of the A slice
+  constexpr int BG = MF_NB / MF_GROWS;           // ... of the B slice
+  constexpr int A_STAGE = MCH * MF_ROWB, B_STAGE = MF_NB * MF_ROWB;
+  constexpr int AL = AG / MF_WAVES;              // A groups per wave
   constexpr int BL = BG / MF_WAVES;
-  static_assert(BG % MF_WAVES == 0, "B groups per wave");
+  constexpr int ST = mf_stages(SUBT), AHEAD = ST - 1;
+  static_assert(AG % MF_WAVES == 0 && BG % MF_WAVES == 0, "load groups per wave");
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   char* const a_ring = smem;
-  char* const b_ring = smem + MF_AST * A_STAGE;
+  char* const b_ring = smem + ST * A_STAGE;
 
   // ---- tile of this workgroup (XCD-aware enumeration) ----
   const int b = blockIdx.x;
@@ -119,14 +130,15 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
   const uint16_t* wb_e = wb + static_cast<int64_t>(e) * w_expert_stride;
 
   // ---- per-lane global sources of this wave's load groups (constant over K) ----
-  // lane i of a group writes LDS row (16g + i/4), physical piece i%4, which holds
-  // logical piece swz(row, i%4) of that row.
-  const int lrow = lane / 4, lpiece = lane % 4;
-  const uint16_t* a_src[AL_MAX];
+  // lane i of a group writes LDS row (8g + i/8), physical piece i%8, which holds
+  // logical piece swz(row, i%8) of that row: each group is 8 whole 128-byte row
+  // segments.
+  const int lrow = lane / 8, lpiece = lane % 8;
+  const uint16_t* a_src[AL];
 #pragma unroll
-  for (int q = 0; q < AL_MAX; ++q) {
+  for (int q = 0; q < AL; ++q) {
     const int g = wave + q * MF_WAVES;
-    const int row = 16 * g + lrow;
+    const int row = MF_GROWS * g + lrow;
     const int rr = min(row, count - 1);  // clamp: rows past the end load a valid row
     const int64_t src = row_index ? row_index[r0 + rr] : (r0 + rr);
     a_src[q] = x + src * K + swz(row, lpiece) * 8;
@@ -135,7 +147,7 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
 #pragma unroll
   for (int q = 0; q < BL; ++q) {
     const int g = wave + q * MF_WAVES;
-    const int row = 16 * g + lrow;
+    const int row = MF_GROWS * g + lrow;
     int wrow;
     const uint16_t* base;
     if (GATEUP) {
@@ -146,25 +158,24 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
       base = wa_e;
     }
     wrow = min(wrow, n_w - 1);
-    if (TILED)  // the group's tile column: tiles [wrow/16][kt], one contiguous KiB each
-      b_src[q] = base + static_cast<int64_t>(wrow & ~15) * K + lane * 8;
+    // the LDS row's swizzle, (row >> 1) & 7, equals (wrow >> 1) & 7: n0 is a multiple of 128
+    if (TILED)  // the group's tile column: tiles [wrow/8][kt], one contiguous KiB each
+      b_src[q] = base + static_cast<int64_t>(wrow & ~7) * K + lane * 8;
     else
       b_src[q] = base + static_cast<int64_t>(wrow) * K + swz(row, lpiece) * 8;
   }
-  // waves whose last A group is past AG still issue that load (into the stage's
-  // padding area) so that all waves issue AL_MAX loads per activation slice
   auto issue_a = [&](int kt) {
-    char* st = a_ring + (kt % MF_AST) * A_STAGE;
+    char* st = a_ring + (kt % ST) * A_STAGE;
     const int k0 = kt * MF_BK;
 #pragma unroll
-    for (int q = 0; q < AL_MAX; ++q) {
+    for (int q = 0; q < AL; ++q) {
       const int g = wave + q * MF_WAVES;
-      char* dst = g < AG ? st + g * 1024 : st + A_BYTES;
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(a_src[q] + k0), (lds_void*)dst, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(a_src[q] + k0), (lds_void*)(st + g * 1024), 16, 0,
+                                       0);
     }
   };
   auto issue_b = [&](int kt) {
-    char* st = b_ring + (kt % MF_BST) * B_BYTES;
+    char* st = b_ring + (kt % ST) * B_STAGE;
     const int k0 = kt * MF_BK;
 #pragma unroll
     for (int q = 0; q < BL; ++q) {
@@ -190,72 +201,75 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
   }
   const int l16 = lane % 16, lq = lane / 16;
   const int active_sub = (count + 15) / 16;  // row sub-tiles holding valid rows (wave-uniform)
-  // this wave's sub-tiles are wm, wm+2, ...: pairs of them holding a valid row
-  const int n_pairs = __builtin_amdgcn_readfirstlane((max(0, (active_sub - wm + 1) / 2) + 1) / 2);
   const int KT = K / MF_BK;
 
-  // Issue order: A0 B0 A1 B1 | A2 B2 | A3 B3 | ...  (iteration kt issues A(kt+2), B(kt+2)
-  // right after its barrier).  At the top of iteration kt the loads issued after B(kt) are
-  // A(kt+1) and B(kt+1): waiting for all but those completes slice kt.
-  for (int j = 0; j < MF_AHEAD && j < KT; ++j) {
+  // Iteration kt: wait for slice kt (slices kt+1 .. kt+AHEAD-1 may still be in
+  // flight), barrier (slice kt visible; every wave is done with slice kt-1),
+  // read the first fragments, request slice kt+AHEAD into the stage of slice
+  // kt-1, compute slice kt.
+  for (int j = 0; j < AHEAD && j < KT; ++j) {
     issue_a(j);
     issue_b(j);
   }
+  static_assert(SUBT % 2 == 0, "sub-tiles come in pairs");
+  static_assert(AHEAD >= 1 && AHEAD <= 2 && 2 * (AL + BL) < 64, "ring depth");
+  constexpr int NP = SUBT / 2;  // pairs of sub-tiles per K step
   for (int kt = 0; kt < KT; ++kt) {
-    // slices issued after slice kt: min(MF_AHEAD - 1, KT - 1 - kt), each AL_MAX + BL loads
-    static_assert(MF_AHEAD >= 1 && MF_AHEAD <= 3 && MF_AHEAD < MF_AST && MF_AHEAD < MF_BST, "ring depth");
-    const int after = min(MF_AHEAD - 1, KT - 1 - kt);
-    if (after >= 2) wait_vmcnt<2 * (AL_MAX + BL)>();
-    else if (after == 1) wait_vmcnt<AL_MAX + BL>();
+    if (AHEAD == 2 && kt + 1 < KT) wait_vmcnt<AL + BL>();
     else wait_vmcnt<0>();
-    ring_barrier();  // slice kt visible to all waves; everyone is done with slice kt-1
-    const char* st_a = a_ring + (kt % MF_AST) * A_STAGE;
-    const char* st_b = b_ring + (kt % MF_BST) * B_BYTES;
-    auto read_a = [&](int i) {
+    ring_barrier();
+    const char* st_a = a_ring + (kt % ST) * A_STAGE;
+    const char* st_b = b_ring + (kt % ST) * B_STAGE;
+    auto read_a = [&](int i, int ks) {
       const int row = (wm + 2 * i) * 16 + l16;
-      return *reinterpret_cast<const bf16x8*>(st_a + row * MF_ROWB + swz(row, lq) * 16);
+      return *reinterpret_cast<const bf16x8*>(st_a + row * MF_ROWB + swz(row, lq + 4 * ks) * 16);
     };
-    // the slice's weight fragments and the first two activation fragments are
-    // read first, then the requests two slices ahead go out (into the stages of
-    // slice kt-1: every wave is past its reads of them)
-    bf16x8 wfr[MF_NT];
-#pragma unroll
-    for (int t = 0; t < MF_NT; ++t) {
+    auto read_b = [&](int t, int ks) {
       const int row = brow[t] + l16;
-      wfr[t] = *reinterpret_cast<const bf16x8*>(st_b + row * MF_ROWB + swz(row, lq) * 16);
-    }
-    // activation fragments in pairs of sub-tiles, two pair buffers: the reads of
-    // pair p+1 are issued right after the first MFMA of pair p (whose wait
-    // covered every earlier read), so seven MFMAs hide them
-    static_assert(SUBT % 2 == 0, "sub-tiles come in pairs");
+      return *reinterpret_cast<const bf16x8*>(st_b + row * MF_ROWB + swz(row, lq + 4 * ks) * 16);
+    };
+    // Units u = 0 .. 2*NP-1 are (K step ks = u / NP, sub-tile pair p = u % NP),
+    // with activation fragments in two pair buffers (u & 1) and weight fragments
+    // per K step.  The reads of unit u+1 (and, before the second K step, its
+    // weight fragments) go out right after the first MFMA of unit u, whose wait
+    // covered every earlier read, so seven MFMAs hide them.
+    bf16x8 wfr[2][MF_NT];
     bf16x8 xb[2][2];
-    xb[0][0] = read_a(0);
-    xb[0][1] = read_a(1);
-    __builtin_amdgcn_sched_group_barrier(0x100, MF_NT + 2, 0);  // weight fragments and pair 0 first
-    if (kt + MF_AHEAD < KT) {
-      issue_a(kt + MF_AHEAD);
-      issue_b(kt + MF_AHEAD);
-    }
-    // Pairs of sub-tiles holding no valid row of this wave are skipped (a pair
-    // with one valid sub-tile computes both; the other's rows are clamped copies
-    // of a valid row and never stored).
 #pragma unroll
-    for (int p = 0; p < SUBT / 2; ++p) {
-      if (p >= n_pairs) break;
-      const bf16x8 x0 = xb[p & 1][0], x1 = xb[p & 1][1];
-      acc[2 * p][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[0], x0, acc[2 * p][0], 0, 0, 0);
+    for (int t = 0; t < MF_NT; ++t) wfr[0][t] = read_b(t, 0);
+    xb[0][0] = read_a(0, 0);
+    xb[0][1] = read_a(1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, MF_NT + 2, 0);  // first fragments, then the requests
+    if (kt + AHEAD < KT) {
+      issue_a(kt + AHEAD);
+      issue_b(kt + AHEAD);
+    }
+#pragma unroll
+    for (int u = 0; u < 2 * NP; ++u) {
+      const int ks = u / NP, p = u % NP;
+      const bf16x8 x0 = xb[u & 1][0], x1 = xb[u & 1][1];
+      acc[2 * p][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[ks][0], x0, acc[2 * p][0], 0, 0, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (p + 1 < n_pairs) {
-        xb[(p + 1) & 1][0] = read_a(2 * p + 2);
-        xb[(p + 1) & 1][1] = read_a(2 * p + 3);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      if (u + 1 < 2 * NP) {
+        const int ks1 = (u + 1) / NP, p1 = (u + 1) % NP;
+        if (ks1 != ks) {
+#pragma unroll
+          for (int t = 0; t < MF_NT; ++t) wfr[1][t] = read_b(t, 1);
+          xb[(u + 1) & 1][0] = read_a(2 * p1, 1);
+          xb[(u + 1) & 1][1] = read_a(2 * p1 + 1, 1);
+          __builtin_amdgcn_sched_group_barrier(0x100, MF_NT + 2, 0);
+        } else {
+          xb[(u + 1) & 1][0] = read_a(2 * p1, ks1);
+          xb[(u + 1) & 1][1] = read_a(2 * p1 + 1, ks1);
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
       }
 #pragma unroll
       for (int t = 1; t < MF_NT; ++t)
-        acc[2 * p][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[t], x0, acc[2 * p][t], 0, 0, 0);
+        acc[2 * p][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[ks][t], x0, acc[2 * p][t], 0, 0, 0);
 #pragma unroll
       for (int t = 0; t < MF_NT; ++t)
-        acc[2 * p + 1][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[t], x1, acc[2 * p + 1][t], 0, 0, 0);
+        acc[2 * p + 1][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[ks][t], x1, acc[2 * p + 1][t], 0, 0, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 2 * MF_NT - 1, 0);
     }
   }
@@ -309,8 +323,7 @@ int launch_t(const void* x, const int32_t* row_index, const int32_t* offsets, in
   const int m_chunks = static_cast<int>(ceil_div(rows_cap, 32 * SUBT));
   const int64_t grid = static_cast<int64_t>(ceil_div(experts, kXcds)) * kXcds * m_chunks * n_tiles;
   if (grid > INT32_MAX) return set_error(QW_ERR_UNSUPPORTED, "MFMA grid too large");
-  const size_t lds = static_cast<size_t>(MF_AST) * (32 * SUBT * MF_ROWB + 1024) +
-                     static_cast<size_t>(MF_BST) * MF_NB * MF_ROWB;
+  const size_t lds = static_cast<size_t>(mf_stages(SUBT)) * (32 * SUBT * MF_ROWB + MF_NB * MF_ROWB);
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_mfma_kernel<GATEUP, SUBT, TILED>),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize,
                                                      static_cast<int>(lds));

@@ -268,18 +268,18 @@ __global__ __launch_bounds__(256) void pack_bf16_tiles_kernel(const uint16_t* __
   const int64_t per_expert = rows * cols / 8;
   const int64_t e = o / per_expert, rem = o % per_expert;
   const int64_t tile = rem / 64, i = rem % 64;
-  const int64_t kt = cols / 32;
+  const int64_t kt = cols / 64;
   const int64_t rb = tile / kt, kb = tile % kt;
-  const int64_t row = 16 * rb + i / 4;
-  const int64_t p = (i % 4) ^ ((i / 8) & 3);
-  const uint4 v = *reinterpret_cast<const uint4*>(w + e * rows * cols + row * cols + kb * 32 + p * 8);
+  const int64_t row = 8 * rb + i / 8;
+  const int64_t p = (i % 8) ^ ((row >> 1) & 7);
+  const uint4 v = *reinterpret_cast<const uint4*>(w + e * rows * cols + row * cols + kb * 64 + p * 8);
   *reinterpret_cast<uint4*>(out + o * 8) = v;
 }
 
 int pack_bf16_tiles(const void* w, int64_t E, int64_t rows, int64_t cols, void* out, hipStream_t stream) {
   QW_REQUIRE(E >= 1 && rows >= 1 && cols >= 1, "bad tile packing sizes");
-  QW_REQUIRE(rows % 16 == 0 && cols % 32 == 0,
-             "tiled bf16 weights need out_features %% 16 == 0 and in_features %% 32 == 0 (got %lld, %lld)",
+  QW_REQUIRE(rows % 8 == 0 && cols % 64 == 0,
+             "tiled bf16 weights need out_features %% 8 == 0 and in_features %% 64 == 0 (got %lld, %lld)",
              (long long)rows, (long long)cols);
   QW_REQUIRE(w && out, "packing pointers are required");
   QW_REQUIRE(w != out, "packing cannot run in place");

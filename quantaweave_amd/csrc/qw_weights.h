@@ -47,12 +47,11 @@ inline WView make_wview(int fmt, const void* w, const float* scales, int64_t row
 }
 
 // Element offset of W[row][col] in the QW_BF16T tiles of a [rows, cols] matrix:
-// tile (row/16, col/32) of 512 elements; in it, 16-byte piece i = 4*(row%16) +
-// (p ^ ((row%16 / 2) & 3)) with p = (col%32) / 8, then col%8.
+// tile (row/8, col/64) of 512 elements; in it, 16-byte piece
+// 8*(row%8) + (p ^ ((row/2) % 8)) with p = (col%64) / 8, then col%8.
 __host__ __device__ __forceinline__ int64_t bf16t_index(int64_t row, int64_t col, int64_t cols) {
-  const int64_t tile = (row >> 4) * (cols >> 5) + (col >> 5);
-  const int r = static_cast<int>(row & 15);
-  const int piece = 4 * r + ((static_cast<int>((col >> 3) & 3)) ^ ((r >> 1) & 3));
+  const int64_t tile = (row >> 3) * (cols >> 6) + (col >> 6);
+  const int piece = 8 * static_cast<int>(row & 7) + (static_cast<int>((col >> 3) & 7) ^ static_cast<int>((row >> 1) & 7));
   return tile * 512 + piece * 8 + (col & 7);
 }
 

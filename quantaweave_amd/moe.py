@@ -120,7 +120,7 @@ def tile_bf16(stack: Tensor) -> Tensor:
 
 
 def can_tile(stack: Tensor) -> bool:
-    return stack.dtype == torch.bfloat16 and stack.size(1) % 16 == 0 and stack.size(2) % 32 == 0
+    return stack.dtype == torch.bfloat16 and stack.size(1) % 64 == 0 and stack.size(2) % 64 == 0
 
 
 class ExpertPack:

@@ -206,19 +206,19 @@ def test_quantized_linear_forward(bits, group, max_rel):
 # ---------------------------------------------------------------- QW_BF16T tiled weights
 def test_bf16_tile_packing_matches_the_layout():
     rng = np.random.RandomState(70)
-    w = oracle.round_bf16(rng.randn(3, 48, 96).astype(np.float32))
+    w = oracle.round_bf16(rng.randn(3, 48, 128).astype(np.float32))
     tiled = qa.moe.tile_bf16(H.dev(w, torch.bfloat16))
     torch.cuda.synchronize()
     assert np.array_equal(tiled.float().cpu().numpy(), oracle.tile_bf16(w))
-    with pytest.raises(ValueError, match="16"):
-        bad = H.dev(np.zeros((1, 8, 64), np.float32), torch.bfloat16)
-        _lib.call("qw_pack_bf16_tiles", H.P(bad), 1, 8, 64, H.P(torch.empty_like(bad)), H.s())
+    with pytest.raises(ValueError, match="64"):
+        bad = H.dev(np.zeros((1, 8, 32), np.float32), torch.bfloat16)
+        _lib.call("qw_pack_bf16_tiles", H.P(bad), 1, 8, 32, H.P(torch.empty_like(bad)), H.s())
 
 
 @pytest.mark.parametrize("counts,D,F_", [
     ([40, 0, 70, 33, 64, 1], 128, 256),   # prefill-sized rows: MFMA kernels
     ([1, 0, 3, 2], 256, 512),             # decode-sized rows: weight-streaming kernels
-    (COUNTS, 64, 96),                     # d_ff not a multiple of 64: general kernel
+    ([1, 0, 2], 4096, 128),               # decode-sized rows longer than the streaming kernel takes: general kernel
 ])
 def test_tiled_bf16_weights_give_identical_outputs(counts, D, F_):
     """The tiles change where each weight is read, not the arithmetic: the
@@ -245,5 +245,5 @@ def test_tiled_bf16_shape_errors():
     wt = H.dev(np.zeros((1, 64, 48), np.float32), torch.bfloat16)
     wd = H.dev(np.zeros((1, 48, 64), np.float32), torch.bfloat16)
     offsets = H.dev(np.array([0, 4], np.int32))
-    with pytest.raises(ValueError, match="multiples of 32"):
+    with pytest.raises(ValueError, match="multiples of 64"):
         H.experts(x, offsets, _lib.QW_BF16T, wt, wt, wd, max_rows=4, rows_per_expert=4)

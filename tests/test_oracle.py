@@ -477,18 +477,17 @@ def test_decode_step_top1_adds_the_expert_output_exactly():
 def test_tile_layout_matches_the_element_formula():
     """Brute force over every element of a small stack: the vectorised tiling
     puts W[e, row, col] at e*out*in + tile*512 + piece*8 + col%8 with tile =
-    (row//16)*(in//32) + col//32 and piece = 4*(row%16) + (((col//8)%4) ^ ((row%16)//2 % 4))."""
+    (row//8)*(in//64) + col//64 and piece = 8*(row%8) + (((col//8)%8) ^ ((row//2)%8))."""
     rng = np.random.RandomState(60)
-    E, R, K = 2, 32, 64
+    E, R, K = 2, 24, 128
     w = rng.randn(E, R, K).astype(np.float32)
     t = oracle.tile_bf16(w).reshape(-1)
     for e in range(E):
         for row in range(R):
             for col in range(K):
-                r = row % 16
-                tile = (row // 16) * (K // 32) + col // 32
-                piece = 4 * r + (((col // 8) % 4) ^ ((r // 2) % 4))
+                tile = (row // 8) * (K // 64) + col // 64
+                piece = 8 * (row % 8) + (((col // 8) % 8) ^ ((row // 2) % 8))
                 assert t[e * R * K + tile * 512 + piece * 8 + col % 8] == w[e, row, col]
     assert np.array_equal(oracle.untile_bf16(oracle.tile_bf16(w)), w)
     with pytest.raises(ValueError):
-        oracle.tile_bf16(np.zeros((1, 8, 64), np.float32))
+        oracle.tile_bf16(np.zeros((1, 8, 32), np.float32))
