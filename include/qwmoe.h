@@ -150,7 +150,8 @@ int qw_moe_combine(const void* y, int dtype, const int32_t* route_slot, const in
 
 /* Load-balance loss (src/quantweave_moe_model.py:152-154):
  * importance[e] = mean_t probs[t, e]; balance = E * sum_e importance[e] *
- * counts[e] / (tokens*top_k).  importance may be NULL. */
+ * counts[e] / (tokens*top_k).  importance [experts] receives the means
+ * (required). */
 int qw_moe_balance(const float* probs, const int32_t* counts, int64_t tokens, int64_t top_k, int64_t experts,
                    float* importance, float* balance, void* stream);
 
@@ -228,6 +229,63 @@ int qw_pack_bf16_tiles(const void* w, int64_t experts, int64_t out_features, int
 int qw_grouped_matmul(const void* x, int act_dtype, const void* w, int w_format, const float* scales, int64_t group,
                       int64_t experts, int64_t out_features, int64_t in_features, const int32_t* offsets,
                       int64_t rows, void* out, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Training: the backward pass of the grouped expert matmuls and of the MoE
+ * layer's routing and combine.  All gradients are fp32-accumulated; bf16
+ * tensors are rounded where torch's bf16 ops round.
+ * ------------------------------------------------------------------------ */
+
+/* Backward of qw_grouped_matmul with plain weights, _GroupedMatmul.backward
+ * (src/moe_kernels.py:146-164) and _grouped_dw_kernel (:66-89):
+ *   grad_x[r]   = grad_out[r] @ w[e]            (r in [offsets[e], offsets[e+1]))
+ *   grad_w[e]   = grad_out[rows of e]^T @ x[rows of e]   (exactly 0 without rows)
+ * grad_out [rows, out_features], x [rows, in_features], w [E, out, in], all of
+ * `dtype` (QW_F32 or QW_BF16).  grad_x or grad_w may be NULL (not computed).
+ * accumulate_grad_x != 0 adds to grad_x instead of overwriting it.
+ * max_rows_per_expert bounds every expert's row count (0: `rows`). */
+int qw_grouped_matmul_backward(const void* grad_out, const void* x, const void* w, int dtype, int64_t experts,
+                               int64_t out_features, int64_t in_features, const int32_t* offsets, int64_t rows,
+                               int64_t max_rows_per_expert, void* grad_x, int accumulate_grad_x, void* grad_w,
+                               void* stream);
+
+/* hidden = silu(gate) * up over n elements, `F.silu(gate) * up` of
+ * grouped_swiglu (src/moe_kernels.py:194); bf16 rounds silu and the product. */
+int qw_swiglu(const void* gate, const void* up, int dtype, int64_t n, void* hidden, void* stream);
+
+/* Its derivative: grad_up = grad_hidden * silu(gate); grad_gate =
+ * (grad_hidden * up) * silu'(gate). */
+int qw_swiglu_backward(const void* grad_hidden, const void* gate, const void* up, int dtype, int64_t n,
+                       void* grad_gate, void* grad_up, void* stream);
+
+/* Combine with router weights and a separate output dtype,
+ * `output.index_add_(0, tokens, (expert_output * weights[:, None]).to(out))`
+ * (src/quantweave_moe_model.py:201-202): out[t] = sum over the kept routes of
+ * t in ascending expert order of (y[slot] * top_w).to(out_dtype), rounded to
+ * out_dtype after every add.  top_w == NULL: weight 1 (then this is also the
+ * backward of the row gather flat[tokens], :192, with out_dtype fp32). */
+int qw_moe_combine_weighted(const void* y, int y_dtype, const int32_t* route_slot, const int32_t* top_idx,
+                            const float* top_w, int64_t tokens, int64_t top_k, int64_t d_model, void* out,
+                            int out_dtype, void* stream);
+
+/* Backward of qw_moe_combine_weighted: for every kept route (t, j) with slot s,
+ * grad_y[s] = grad_out[t] * top_w[t, j] (y_dtype) and grad_top_w[t, j] =
+ * sum_c grad_out[t, c] * y[s, c]; dropped routes get grad_top_w = 0.
+ * top_k <= 64. */
+int qw_moe_combine_backward(const void* grad_out, int out_dtype, const void* y, int y_dtype,
+                            const int32_t* route_slot, const float* top_w, int64_t tokens, int64_t top_k,
+                            int64_t d_model, void* grad_y, float* grad_top_w, void* stream);
+
+/* Backward of the routing (src/quantweave_moe_model.py:126-135, :152-154):
+ * from the gradients of the renormalised top-k weights (grad_top_w), of the
+ * router probabilities (grad_probs, NULL = 0) and of the balance loss
+ * (grad_balance, a device scalar, NULL = 0; needs `counts`, the per-expert
+ * route counts of the plan), computes grad_scores [tokens, experts] = the
+ * gradient with respect to x @ router_w^T (before the temperature).  The
+ * expert bias only steers selection and gets no gradient.  top_k <= 64. */
+int qw_moe_route_backward(const float* probs, const int32_t* top_idx, const float* top_w, const float* grad_top_w,
+                          const float* grad_probs, const float* grad_balance, const int32_t* counts, int64_t tokens,
+                          int64_t experts, int64_t top_k, float temperature, float* grad_scores, void* stream);
 
 #ifdef __cplusplus
 }

@@ -58,6 +58,20 @@ int dequantize(const void* qweight, const float* scales, int bits, int64_t rows,
                float* out, hipStream_t stream);
 int grouped_matmul_generic(const void* x, int act, const WView& w, int wfmt, int64_t E, const int32_t* offsets,
                            int64_t rows, void* out, hipStream_t stream);
+int combine_weighted(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, const float* top_w,
+                     int64_t T, int64_t K, int64_t D, void* out, int out_dtype, hipStream_t stream);
+int grouped_matmul_backward(const void* gy, const void* x, const void* w, int dtype, int64_t E, int64_t N, int64_t K,
+                            const int32_t* offsets, int64_t rows, int64_t max_rows_per_expert, void* gx, int accumulate,
+                            void* gw, hipStream_t stream);
+int swiglu(const void* g, const void* u, int dtype, int64_t n, void* h, hipStream_t stream);
+int swiglu_backward(const void* dh, const void* g, const void* u, int dtype, int64_t n, void* dg, void* du,
+                    hipStream_t stream);
+int combine_backward(const void* grad_out, int out_dtype, const void* y, int y_dtype, const int32_t* route_slot,
+                     const float* top_w, int64_t T, int64_t K, int64_t D, void* grad_y, float* grad_top_w,
+                     hipStream_t stream);
+int route_backward(const float* probs, const int32_t* top_idx, const float* top_w, const float* grad_top_w,
+                   const float* grad_probs, const float* grad_balance, const int32_t* counts, int64_t T, int64_t E,
+                   int64_t K, float temperature, float* out, hipStream_t stream);
 
 // Kernel-path override for testing the general kernel on any shape:
 // QW_FFN_PATH=generic.  Read once per process.
@@ -456,6 +470,50 @@ int qw_grouped_matmul(const void* x, int act_dtype, const void* w, int w_format,
   QW_REQUIRE(x && w && offsets && out, "grouped_matmul pointers are required");
   const WView v = make_wview(w_format, w, scales, out_features, in_features, group);
   return grouped_matmul_generic(x, act_dtype, v, w_format, experts, offsets, rows, out, as_stream(stream));
+}
+
+int qw_moe_combine_weighted(const void* y, int y_dtype, const int32_t* route_slot, const int32_t* top_idx,
+                            const float* top_w, int64_t tokens, int64_t top_k, int64_t d_model, void* out,
+                            int out_dtype, void* stream) {
+  clear_error();
+  return combine_weighted(y, y_dtype, route_slot, top_idx, top_w, tokens, top_k, d_model, out, out_dtype,
+                          as_stream(stream));
+}
+
+int qw_grouped_matmul_backward(const void* grad_out, const void* x, const void* w, int dtype, int64_t experts,
+                               int64_t out_features, int64_t in_features, const int32_t* offsets, int64_t rows,
+                               int64_t max_rows_per_expert, void* grad_x, int accumulate_grad_x, void* grad_w,
+                               void* stream) {
+  clear_error();
+  return grouped_matmul_backward(grad_out, x, w, dtype, experts, out_features, in_features, offsets, rows,
+                                 max_rows_per_expert, grad_x, accumulate_grad_x, grad_w, as_stream(stream));
+}
+
+int qw_swiglu(const void* gate, const void* up, int dtype, int64_t n, void* hidden, void* stream) {
+  clear_error();
+  return swiglu(gate, up, dtype, n, hidden, as_stream(stream));
+}
+
+int qw_swiglu_backward(const void* grad_hidden, const void* gate, const void* up, int dtype, int64_t n,
+                       void* grad_gate, void* grad_up, void* stream) {
+  clear_error();
+  return swiglu_backward(grad_hidden, gate, up, dtype, n, grad_gate, grad_up, as_stream(stream));
+}
+
+int qw_moe_combine_backward(const void* grad_out, int out_dtype, const void* y, int y_dtype,
+                            const int32_t* route_slot, const float* top_w, int64_t tokens, int64_t top_k,
+                            int64_t d_model, void* grad_y, float* grad_top_w, void* stream) {
+  clear_error();
+  return combine_backward(grad_out, out_dtype, y, y_dtype, route_slot, top_w, tokens, top_k, d_model, grad_y,
+                          grad_top_w, as_stream(stream));
+}
+
+int qw_moe_route_backward(const float* probs, const int32_t* top_idx, const float* top_w, const float* grad_top_w,
+                          const float* grad_probs, const float* grad_balance, const int32_t* counts, int64_t tokens,
+                          int64_t experts, int64_t top_k, float temperature, float* grad_scores, void* stream) {
+  clear_error();
+  return route_backward(probs, top_idx, top_w, grad_top_w, grad_probs, grad_balance, counts, tokens, experts, top_k,
+                        temperature, grad_scores, as_stream(stream));
 }
 
 }  // extern "C"

@@ -92,6 +92,63 @@ __device__ __forceinline__ float round_act(float v) {
   else return round_to_bf16(v);
 }
 
+// VEC consecutive activations from element i, widened to fp32, in one load
+// (VEC 4 or 8 needs i aligned to VEC).
+template <int DT, int VEC>
+__device__ __forceinline__ void load_vec(const void* p, int64_t i, float (&v)[VEC]) {
+  if constexpr (VEC == 8 && DT == QW_BF16) {
+    const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      v[2 * u] = __uint_as_float(w[u] << 16);
+      v[2 * u + 1] = __uint_as_float(w[u] & 0xffff0000u);
+    }
+  } else if constexpr (VEC % 4 == 0 && DT == QW_F32) {
+#pragma unroll
+    for (int u = 0; u < VEC; u += 4) {
+      const float4 q = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i + u);
+      v[u] = q.x;
+      v[u + 1] = q.y;
+      v[u + 2] = q.z;
+      v[u + 3] = q.w;
+    }
+  } else if constexpr (VEC == 4) {
+    const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+    v[0] = __uint_as_float(q.x << 16);
+    v[1] = __uint_as_float(q.x & 0xffff0000u);
+    v[2] = __uint_as_float(q.y << 16);
+    v[3] = __uint_as_float(q.y & 0xffff0000u);
+  } else {
+#pragma unroll
+    for (int u = 0; u < VEC; ++u) v[u] = load_act<DT>(p, i + u);
+  }
+}
+
+// Stores VEC fp32 values as activations of dtype DT (rounded to nearest even
+// for bf16) from element i, in one store where VEC allows.
+template <int DT, int VEC>
+__device__ __forceinline__ void store_vec(void* p, int64_t i, const float (&v)[VEC]) {
+  if constexpr (VEC == 8 && DT == QW_BF16) {
+    uint32_t w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      w[u] = f32_to_bf16(v[2 * u]) | (static_cast<uint32_t>(f32_to_bf16(v[2 * u + 1])) << 16);
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p) + i) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else if constexpr (VEC % 4 == 0 && DT == QW_F32) {
+#pragma unroll
+    for (int u = 0; u < VEC; u += 4)
+      *reinterpret_cast<float4*>(static_cast<float*>(p) + i + u) = make_float4(v[u], v[u + 1], v[u + 2], v[u + 3]);
+  } else if constexpr (VEC == 4) {
+    const uint32_t lo = f32_to_bf16(v[0]) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
+    const uint32_t hi = f32_to_bf16(v[2]) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p) + i) = make_uint2(lo, hi);
+  } else {
+#pragma unroll
+    for (int u = 0; u < VEC; ++u) store_act<DT>(p, i + u, v[u]);
+  }
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));

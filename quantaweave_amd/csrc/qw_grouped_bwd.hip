@@ -1,0 +1,159 @@
+// Backward of the grouped matmul y[rows of e] = x[rows of e] @ W[e]^T.
+//
+// Reference: _GroupedMatmul.backward (src/moe_kernels.py:146-164) with its two
+// kernels: grad_x through the forward kernel with the weight transposed
+// (:118-135, transpose=True), and _grouped_dw_kernel (:66-89):
+//   grad_x[r, k]    = sum_n grad_y[r, n] * W[e][n, k]          (r in rows of e)
+//   grad_W[e][n, k] = sum_{r in rows of e} grad_y[r, n] * x[r, k]
+// An expert without rows gets an exactly zero grad_W.  fp32 accumulation,
+// output in the operands' dtype (fp32 or bf16); with `accumulate` grad_x
+// receives grad_x + result (one rounding), which sums the gate and up
+// projections' input gradients of a SwiGLU expert in place.
+//
+// Both kernels compute a 64x64 output tile per 256-thread block (4x4 per
+// thread) from 16-deep slices of the reduction staged in LDS; the reduction
+// runs in ascending order, so results do not depend on scheduling.
+#include "qw_common.h"
+
+namespace qw {
+
+namespace {
+
+constexpr int BT = 64;  // output tile edge
+constexpr int BR = 16;  // reduction slice
+
+// grad_x: block (k tile, row tile, expert)
+template <int DT>
+__global__ __launch_bounds__(256) void grouped_dx_kernel(const void* __restrict__ gy, const void* __restrict__ w,
+                                                         const int32_t* __restrict__ offsets, int N, int K,
+                                                         int rows, int accumulate, void* __restrict__ gx) {
+  __shared__ float gs[BR][BT + 4];  // [n][row]
+  __shared__ float ws[BR][BT + 4];  // [n][k]
+  const int e = blockIdx.z;
+  const int lo = min(max(offsets[e], 0), rows), hi = min(offsets[e + 1], rows);
+  const int r0 = lo + blockIdx.y * BT;
+  if (r0 >= hi) return;
+  const int k0 = blockIdx.x * BT;
+  const int tid = threadIdx.x, ty = tid / 16, tx = tid % 16;
+  const int64_t wbase = static_cast<int64_t>(e) * N * K;
+  float acc[4][4] = {};
+  for (int n0 = 0; n0 < N; n0 += BR) {
+    for (int i = tid; i < BT * BR; i += 256) {
+      const int m = i / BR, nn = i % BR;
+      const int r = r0 + m, n = n0 + nn;
+      gs[nn][m] = (r < hi && n < N) ? load_act<DT>(gy, static_cast<int64_t>(r) * N + n) : 0.0f;
+      const int wn = i / BT, kk = i % BT;
+      const int n2 = n0 + wn, k = k0 + kk;
+      ws[wn][kk] = (n2 < N && k < K) ? load_act<DT>(w, wbase + static_cast<int64_t>(n2) * K + k) : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int nn = 0; nn < BR; ++nn) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = gs[nn][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = ws[nn][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = r0 + ty * 4 + i;
+    if (r >= hi) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = k0 + tx * 4 + j;
+      if (k >= K) continue;
+      const int64_t o = static_cast<int64_t>(r) * K + k;
+      store_act<DT>(gx, o, accumulate ? load_act<DT>(gx, o) + acc[i][j] : acc[i][j]);
+    }
+  }
+}
+
+// grad_W: block (k tile, n tile, expert)
+template <int DT>
+__global__ __launch_bounds__(256) void grouped_dw_kernel(const void* __restrict__ gy, const void* __restrict__ x,
+                                                         const int32_t* __restrict__ offsets, int N, int K,
+                                                         int rows, void* __restrict__ gw) {
+  __shared__ float gs[BR][BT + 4];  // [row][n]
+  __shared__ float xs[BR][BT + 4];  // [row][k]
+  const int e = blockIdx.z;
+  const int lo = min(max(offsets[e], 0), rows), hi = min(offsets[e + 1], rows);
+  const int n0 = blockIdx.y * BT, k0 = blockIdx.x * BT;
+  const int tid = threadIdx.x, ty = tid / 16, tx = tid % 16;
+  float acc[4][4] = {};
+  for (int m0 = lo; m0 < hi; m0 += BR) {
+    for (int i = tid; i < BR * BT; i += 256) {
+      const int m = i / BT, c = i % BT;
+      const int r = m0 + m;
+      const bool ok = r < hi;
+      gs[m][c] = (ok && n0 + c < N) ? load_act<DT>(gy, static_cast<int64_t>(r) * N + n0 + c) : 0.0f;
+      xs[m][c] = (ok && k0 + c < K) ? load_act<DT>(x, static_cast<int64_t>(r) * K + k0 + c) : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < BR; ++m) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = gs[m][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = xs[m][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+  const int64_t wbase = static_cast<int64_t>(e) * N * K;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int n = n0 + ty * 4 + i;
+    if (n >= N) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = k0 + tx * 4 + j;
+      if (k < K) store_act<DT>(gw, wbase + static_cast<int64_t>(n) * K + k, acc[i][j]);
+    }
+  }
+}
+
+}  // namespace
+
+int grouped_matmul_backward(const void* gy, const void* x, const void* w, int dtype, int64_t E, int64_t N, int64_t K,
+                            const int32_t* offsets, int64_t rows, int64_t max_rows_per_expert, void* gx, int accumulate,
+                            void* gw, hipStream_t stream) {
+  QW_REQUIRE(dtype == QW_F32 || dtype == QW_BF16, "grouped backward dtype must be f32 or bf16");
+  QW_REQUIRE(E >= 1 && E <= 65535 && N >= 1 && K >= 1 && N <= INT32_MAX && K <= INT32_MAX && rows >= 0 &&
+                 rows <= INT32_MAX && max_rows_per_expert >= 0,
+             "bad grouped backward sizes");
+  QW_REQUIRE(offsets != nullptr, "offsets are required");
+  const int n = static_cast<int>(N), k = static_cast<int>(K), r = static_cast<int>(rows);
+  if (gx != nullptr && rows > 0) {
+    QW_REQUIRE(gy && w, "grad_x needs grad_out and w");
+    const int64_t per = max_rows_per_expert > 0 && max_rows_per_expert < rows ? max_rows_per_expert : rows;
+    QW_REQUIRE(ceil_div(per, BT) <= 65535, "too many rows per expert");
+    const dim3 g(static_cast<unsigned>(ceil_div(K, BT)), static_cast<unsigned>(ceil_div(per, BT)),
+                 static_cast<unsigned>(E));
+    if (dtype == QW_F32) grouped_dx_kernel<QW_F32><<<g, 256, 0, stream>>>(gy, w, offsets, n, k, r, accumulate, gx);
+    else grouped_dx_kernel<QW_BF16><<<g, 256, 0, stream>>>(gy, w, offsets, n, k, r, accumulate, gx);
+    QW_LAUNCH_CHECK("grouped_dx_kernel");
+  }
+  if (gw != nullptr) {
+    QW_REQUIRE(rows == 0 || (gy && x), "grad_w needs grad_out and x");
+    QW_REQUIRE(ceil_div(N, BT) <= 65535, "too many output features");
+    const dim3 g(static_cast<unsigned>(ceil_div(K, BT)), static_cast<unsigned>(ceil_div(N, BT)),
+                 static_cast<unsigned>(E));
+    if (dtype == QW_F32) grouped_dw_kernel<QW_F32><<<g, 256, 0, stream>>>(gy, x, offsets, n, k, r, gw);
+    else grouped_dw_kernel<QW_BF16><<<g, 256, 0, stream>>>(gy, x, offsets, n, k, r, gw);
+    QW_LAUNCH_CHECK("grouped_dw_kernel");
+  }
+  return QW_OK;
+}
+
+}  // namespace qw

@@ -45,20 +45,27 @@ int permute(const void* x, int dtype, int64_t D, const int32_t* slot_token, cons
 // a rounding to the output dtype after every add — the arithmetic of
 // `zeros_like(flat).index_add_(0, tokens, y)` on expert-ordered rows
 // (src/quantweave_moe_model.py:192, :201, :211).  One block per token.
+// WEIGHTED: each row enters as (y * w).to(out dtype), w the route's router
+// weight — `expert_output * weights[:, None]` (:201) with unweighted rows.
+// The same kernel with weights off and OUT = fp32 is the backward of the row
+// gather flat[tokens] (:192): index_add of the rows' gradients.
 // ---------------------------------------------------------------------------
 // KMAX >= K bounds the routes per token; the token's kept routes are put in
 // ascending expert order in registers (a static ranking network, no indexed
 // private memory).
-template <int ACT, int VEC, int KMAX>
+template <int ACT, int OUT, int VEC, int KMAX, bool WEIGHTED>
 __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y, const int32_t* __restrict__ route_slot,
-                                                      const int32_t* __restrict__ top_idx, int K, int D,
+                                                      const int32_t* __restrict__ top_idx,
+                                                      const float* __restrict__ top_w, int K, int D,
                                                       void* __restrict__ out) {
   const int t = blockIdx.x;
   int sl[KMAX], ex[KMAX];
+  float wt[KMAX];
 #pragma unroll
   for (int j = 0; j < KMAX; ++j) {
     sl[j] = j < K ? route_slot[static_cast<int64_t>(t) * K + j] : -1;
     ex[j] = j < K ? top_idx[static_cast<int64_t>(t) * K + j] : 0;
+    wt[j] = (WEIGHTED && j < K) ? top_w[static_cast<int64_t>(t) * K + j] : 1.0f;
   }
   // rank of each kept route among the kept routes by expert id (experts of a token are distinct)
   int rk[KMAX];
@@ -72,12 +79,18 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
     nk += sl[j] >= 0 ? 1 : 0;
   }
   int slot[KMAX];
+  float wsl[KMAX];
 #pragma unroll
   for (int p = 0; p < KMAX; ++p) {
     int s = 0;
+    float w = 1.0f;
 #pragma unroll
-    for (int j = 0; j < KMAX; ++j) s = rk[j] == p ? sl[j] : s;
+    for (int j = 0; j < KMAX; ++j) {
+      s = rk[j] == p ? sl[j] : s;
+      w = rk[j] == p ? wt[j] : w;
+    }
     slot[p] = s;
+    wsl[p] = w;
   }
   const int64_t row = static_cast<int64_t>(t) * D;
   for (int c = threadIdx.x * VEC; c < D; c += blockDim.x * VEC) {
@@ -86,71 +99,73 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
     for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
 #pragma unroll
     for (int j = 0; j < KMAX; ++j) {
-      if (j >= nk) break;
-      const int64_t src = static_cast<int64_t>(slot[j]) * D + c;
-      if constexpr (VEC == 8 && ACT == QW_BF16) {
-        const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(y) + src);
-        const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+      if (j < nk) {
+        float yv[VEC];
+        load_vec<ACT, VEC>(y, static_cast<int64_t>(slot[j]) * D + c, yv);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          acc[2 * v] = round_act<ACT>(acc[2 * v] + __uint_as_float(w4[v] << 16));
-          acc[2 * v + 1] = round_act<ACT>(acc[2 * v + 1] + __uint_as_float(w4[v] & 0xffff0000u));
+        for (int v = 0; v < VEC; ++v) {
+          const float term = WEIGHTED ? round_act<OUT>(yv[v] * wsl[j]) : yv[v];
+          acc[v] = round_act<OUT>(acc[v] + term);
         }
-      } else if constexpr (VEC == 4 && ACT == QW_F32) {
-        const float4 q = *reinterpret_cast<const float4*>(static_cast<const float*>(y) + src);
-        acc[0] += q.x;
-        acc[1] += q.y;
-        acc[2] += q.z;
-        acc[3] += q.w;
-      } else {
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) acc[v] = round_act<ACT>(acc[v] + load_act<ACT>(y, src + v));
       }
     }
-    if constexpr (VEC == 8 && ACT == QW_BF16) {
-      uint4 o;
-      o.x = f32_to_bf16(acc[0]) | (static_cast<uint32_t>(f32_to_bf16(acc[1])) << 16);
-      o.y = f32_to_bf16(acc[2]) | (static_cast<uint32_t>(f32_to_bf16(acc[3])) << 16);
-      o.z = f32_to_bf16(acc[4]) | (static_cast<uint32_t>(f32_to_bf16(acc[5])) << 16);
-      o.w = f32_to_bf16(acc[6]) | (static_cast<uint32_t>(f32_to_bf16(acc[7])) << 16);
-      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + row + c) = o;
-    } else if constexpr (VEC == 4 && ACT == QW_F32) {
-      *reinterpret_cast<float4*>(static_cast<float*>(out) + row + c) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-    } else {
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) store_act<ACT>(out, row + c + v, acc[v]);
-    }
+    store_vec<OUT, VEC>(out, row + c, acc);
   }
 }
 
-template <int KMAX>
-int launch_combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, unsigned g, int k,
-                   int d, void* out, hipStream_t stream) {
-  if (dtype == QW_F32) {
-    if (d % 4 == 0) combine_kernel<QW_F32, 4, KMAX><<<g, 256, 0, stream>>>(y, route_slot, top_idx, k, d, out);
-    else combine_kernel<QW_F32, 1, KMAX><<<g, 256, 0, stream>>>(y, route_slot, top_idx, k, d, out);
-  } else {
-    if (d % 8 == 0) combine_kernel<QW_BF16, 8, KMAX><<<g, 256, 0, stream>>>(y, route_slot, top_idx, k, d, out);
-    else combine_kernel<QW_BF16, 1, KMAX><<<g, 256, 0, stream>>>(y, route_slot, top_idx, k, d, out);
-  }
+template <int ACT, int OUT, int KMAX, bool WEIGHTED>
+void launch_combine_vec(const void* y, const int32_t* route_slot, const int32_t* top_idx, const float* top_w,
+                        unsigned g, int k, int d, void* out, hipStream_t stream) {
+  constexpr int V = (ACT == QW_BF16 || OUT == QW_BF16) ? 8 : 4;
+  if (d % V == 0)
+    combine_kernel<ACT, OUT, V, KMAX, WEIGHTED><<<g, 256, 0, stream>>>(y, route_slot, top_idx, top_w, k, d, out);
+  else
+    combine_kernel<ACT, OUT, 1, KMAX, WEIGHTED><<<g, 256, 0, stream>>>(y, route_slot, top_idx, top_w, k, d, out);
+}
+
+template <int KMAX, bool WEIGHTED>
+int launch_combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, const float* top_w,
+                   unsigned g, int k, int d, void* out, int out_dtype, hipStream_t stream) {
+  if (dtype == QW_F32 && out_dtype == QW_F32)
+    launch_combine_vec<QW_F32, QW_F32, KMAX, WEIGHTED>(y, route_slot, top_idx, top_w, g, k, d, out, stream);
+  else if (dtype == QW_F32)
+    launch_combine_vec<QW_F32, QW_BF16, KMAX, WEIGHTED>(y, route_slot, top_idx, top_w, g, k, d, out, stream);
+  else if (out_dtype == QW_F32)
+    launch_combine_vec<QW_BF16, QW_F32, KMAX, WEIGHTED>(y, route_slot, top_idx, top_w, g, k, d, out, stream);
+  else
+    launch_combine_vec<QW_BF16, QW_BF16, KMAX, WEIGHTED>(y, route_slot, top_idx, top_w, g, k, d, out, stream);
   QW_LAUNCH_CHECK("combine_kernel");
   return QW_OK;
 }
 
-int combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, int64_t T, int64_t K,
-            int64_t D, void* out, hipStream_t stream) {
-  QW_REQUIRE(dtype == QW_F32 || dtype == QW_BF16, "combine dtype must be f32 or bf16");
+template <bool WEIGHTED>
+int combine_k(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, const float* top_w,
+              int64_t T, int64_t K, int64_t D, void* out, int out_dtype, hipStream_t stream) {
+  const unsigned g = static_cast<unsigned>(T);
+  const int k = static_cast<int>(K), d = static_cast<int>(D);
+  if (K <= 2) return launch_combine<2, WEIGHTED>(y, dtype, route_slot, top_idx, top_w, g, k, d, out, out_dtype, stream);
+  if (K <= 4) return launch_combine<4, WEIGHTED>(y, dtype, route_slot, top_idx, top_w, g, k, d, out, out_dtype, stream);
+  if (K <= 8) return launch_combine<8, WEIGHTED>(y, dtype, route_slot, top_idx, top_w, g, k, d, out, out_dtype, stream);
+  if (K <= 16)
+    return launch_combine<16, WEIGHTED>(y, dtype, route_slot, top_idx, top_w, g, k, d, out, out_dtype, stream);
+  return launch_combine<64, WEIGHTED>(y, dtype, route_slot, top_idx, top_w, g, k, d, out, out_dtype, stream);
+}
+
+int combine_weighted(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, const float* top_w,
+                     int64_t T, int64_t K, int64_t D, void* out, int out_dtype, hipStream_t stream) {
+  QW_REQUIRE((dtype == QW_F32 || dtype == QW_BF16) && (out_dtype == QW_F32 || out_dtype == QW_BF16),
+             "combine dtypes must be f32 or bf16");
   QW_REQUIRE(K >= 1 && K <= 64, "combine supports top_k in [1, 64], got %lld", (long long)K);
   QW_REQUIRE(T >= 0 && T <= INT32_MAX && D >= 1 && D <= INT32_MAX, "bad combine sizes");
   if (T == 0) return QW_OK;
   QW_REQUIRE(y && route_slot && top_idx && out, "combine pointers are required");
-  const unsigned g = static_cast<unsigned>(T);
-  const int k = static_cast<int>(K), d = static_cast<int>(D);
-  if (K <= 2) return launch_combine<2>(y, dtype, route_slot, top_idx, g, k, d, out, stream);
-  if (K <= 4) return launch_combine<4>(y, dtype, route_slot, top_idx, g, k, d, out, stream);
-  if (K <= 8) return launch_combine<8>(y, dtype, route_slot, top_idx, g, k, d, out, stream);
-  if (K <= 16) return launch_combine<16>(y, dtype, route_slot, top_idx, g, k, d, out, stream);
-  return launch_combine<64>(y, dtype, route_slot, top_idx, g, k, d, out, stream);
+  if (top_w) return combine_k<true>(y, dtype, route_slot, top_idx, top_w, T, K, D, out, out_dtype, stream);
+  return combine_k<false>(y, dtype, route_slot, top_idx, nullptr, T, K, D, out, out_dtype, stream);
+}
+
+int combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, int64_t T, int64_t K,
+            int64_t D, void* out, hipStream_t stream) {
+  return combine_weighted(y, dtype, route_slot, top_idx, nullptr, T, K, D, out, dtype, stream);
 }
 
 // ---------------------------------------------------------------------------

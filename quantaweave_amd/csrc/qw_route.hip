@@ -106,26 +106,6 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const void* __restri
 // the wave (reduce_scatter) and then across the 4 waves in wave order, and
 //   logits[t, e] = sum / temperature
 // is written directly (no split-K partials).
-template <int DT, int VEC>
-__device__ __forceinline__ void load_vec(const void* p, int64_t i, float (&v)[VEC]) {
-  if constexpr (VEC == 4 && DT == QW_F32) {
-    const float4 q = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
-    v[0] = q.x;
-    v[1] = q.y;
-    v[2] = q.z;
-    v[3] = q.w;
-  } else if constexpr (VEC == 4) {
-    const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
-    v[0] = __uint_as_float(q.x << 16);
-    v[1] = __uint_as_float(q.x & 0xffff0000u);
-    v[2] = __uint_as_float(q.y << 16);
-    v[3] = __uint_as_float(q.y & 0xffff0000u);
-  } else {
-#pragma unroll
-    for (int u = 0; u < VEC; ++u) v[u] = load_act<DT>(p, i + u);
-  }
-}
-
 constexpr int kGemvMaxTokens = 64;  // the GEMV router serves up to this many tokens
 
 template <int XDT, int WDT, int VEC, int TT>

@@ -5,8 +5,10 @@
 signature (src/quantweave_moe_model.py:63-272).  Its forward is one call into
 the C ABI (``qw_moe_forward``): router, softmax/top-k, capacity plan, grouped
 SwiGLU experts and the weighted combine all run as HIP kernels on the current
-stream, with no host synchronisation.  It is forward-only (inference); the
-grouped backward is not part of this library.
+stream, with no host synchronisation.  With autograd on and float experts,
+the same kernels run inside ``_MoELayer`` (one C call per stage, outputs
+identical to the inference call), whose backward recomputes the expert
+activations and runs the grouped backward kernels.
 """
 
 from __future__ import annotations
@@ -228,50 +230,46 @@ class TopKMoE(nn.Module):
             )
         return num_tokens * self.top_k
 
+    def _wants_grad(self, hidden: Tensor) -> bool:
+        if not torch.is_grad_enabled():
+            return False
+        return hidden.requires_grad or any(p.requires_grad for p in self.parameters())
+
     def forward(self, hidden: Tensor, token_domains: Optional[Tensor] = None,
                 num_domains: int = 0) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
         """Returns (output, balance_loss, dropped_routes, overflow_routes, domain_loss)."""
         _hip.require_device(hidden, "TopKMoE.forward")
-        if hidden.requires_grad and torch.is_grad_enabled():
-            raise RuntimeError("the HIP TopKMoE is forward-only; run it under torch.no_grad() / inference_mode()")
         batch, sequence, width = hidden.shape
-        flat = hidden.reshape(-1, width).contiguous()
+        flat = hidden.reshape(-1, width)
         act = _hip.act_code(flat, "TopKMoE.forward")
         dev = flat.device
         T, E, K = flat.size(0), self.num_experts, self.top_k
-        router_w = self.router.weight.detach()
-        if router_w.dtype not in (torch.float32, torch.bfloat16):
-            router_w = router_w.float()
-        router_w = router_w.contiguous()
         bias = None
         if self.expert_bias is not None:
             bias = self.expert_bias.detach().to(dev, torch.float32).contiguous()
         pack = packed_experts(self, self.experts)
         # static dispatch is the capacity-free evaluation (src/quantweave_moe_model.py:235-245)
         cap = T * K if self.static_dispatch else self.capacity(T)
-        R = T * K
-        out = torch.empty_like(flat)
-        probs = torch.empty(T, E, dtype=torch.float32, device=dev)
-        top_idx = torch.empty(T, K, dtype=torch.int32, device=dev)
-        top_w = torch.empty(T, K, dtype=torch.float32, device=dev)
-        counts = torch.empty(E, dtype=torch.int32, device=dev)
-        kept_counts = torch.empty(E, dtype=torch.int32, device=dev)
-        totals = torch.zeros(2, dtype=torch.int32, device=dev)
-        dropped_token = torch.empty(max(R, 1), dtype=torch.int32, device=dev)
-        dropped_expert = torch.empty(max(R, 1), dtype=torch.int32, device=dev)
-        importance = torch.empty(E, dtype=torch.float32, device=dev)
-        balance = torch.zeros((), dtype=torch.float32, device=dev)
-        s = _hip.stream(dev)
-        if T:
-            nbytes = _lib.load().qw_moe_forward_workspace_bytes(T, width, E, K, self.experts[0].gate.out_features, act)
-            ws = _hip.workspace(nbytes, dev)
-            _lib.call("qw_moe_forward", _hip.ptr(flat), act, T, width, _hip.ptr(router_w),
-                      _hip.act_code(router_w, "router"), float(self.router_temperature), _hip.ptr(bias), E, K, cap,
-                      self.experts[0].gate.out_features, *pack.args(), _hip.ptr(out), _hip.ptr(probs),
-                      _hip.ptr(top_idx), _hip.ptr(top_w), _hip.ptr(counts), _hip.ptr(kept_counts), _hip.ptr(totals),
-                      _hip.ptr(dropped_token), _hip.ptr(dropped_expert), _hip.ptr(ws), nbytes, s)
-            _lib.call("qw_moe_balance", _hip.ptr(probs), _hip.ptr(counts), T, K, E, _hip.ptr(importance),
-                      _hip.ptr(balance), s)
+        if self._wants_grad(hidden):
+            if pack.fmt not in (_lib.QW_F32, _lib.QW_BF16, _lib.QW_BF16T):
+                if hidden.requires_grad:
+                    raise NotImplementedError("gradients through quantised experts are not supported")
+            else:
+                weights = [getattr(e, n).weight for e in self.experts for n in ("gate", "up", "down")]
+                out, probs, balance, top_idx, top_w, counts, kept_counts, totals, dropped_token, dropped_expert = \
+                    _MoELayer.apply(flat, self.router.weight, self, pack, cap, bias, *weights)
+                return self._finish(out, probs, balance, top_idx, top_w, counts, kept_counts, totals, dropped_token,
+                                    dropped_expert, token_domains, num_domains, (batch, sequence, width))
+        with torch.no_grad():
+            res = _forward_call(flat.detach().contiguous(), act, self.router.weight.detach(), self, pack, cap, bias)
+        out, probs, balance = res["out"], res["probs"], res["balance"]
+        return self._finish(out, probs, balance, res["top_idx"], res["top_w"], res["counts"], res["kept_counts"],
+                            res["totals"], res["dropped_token"], res["dropped_expert"], token_domains, num_domains,
+                            (batch, sequence, width))
+
+    def _finish(self, out, probs, balance, top_idx, top_w, counts, kept_counts, totals, dropped_token, dropped_expert,
+                token_domains, num_domains, shape):
+        dev = out.device
         self.last_top_indices = top_idx.long()
         self.last_plan = dict(counts=counts, kept_counts=kept_counts, totals=totals, top_w=top_w,
                               dropped_token=dropped_token, dropped_expert=dropped_expert)
@@ -279,11 +277,11 @@ class TopKMoE(nn.Module):
         zero = torch.zeros((), device=dev, dtype=torch.long)
         dropped_routes = overflow_routes if self.overflow_policy == "drop" else zero
         if self.collect_stats:
-            self._record_stats(probs, top_idx, kept_counts, totals, dropped_token, dropped_expert)
+            self._record_stats(probs.detach(), top_idx, kept_counts, totals, dropped_token, dropped_expert)
         domain_loss = probs.new_zeros(())
         if token_domains is not None and num_domains > 1:
             domain_loss = self._domain_loss(probs, token_domains, num_domains)
-        return out.reshape(batch, sequence, width), balance, dropped_routes, overflow_routes, domain_loss
+        return out.reshape(*shape), balance, dropped_routes, overflow_routes, domain_loss
 
     def _domain_loss(self, router_probs: Tensor, token_domains: Tensor, num_domains: int) -> Tensor:
         """Mean pairwise cosine similarity of the domains' routing profiles
@@ -314,6 +312,190 @@ class TopKMoE(nn.Module):
             "dropped_tokens": dropped_token[:n_drop].long(),
             "dropped_experts": dropped_expert[:n_drop].long(),
         }
+
+
+def _router_operand(router_w: Tensor) -> Tensor:
+    w = router_w.detach()
+    if w.dtype not in (torch.float32, torch.bfloat16):
+        w = w.float()
+    return w.contiguous()
+
+
+def _forward_call(flat: Tensor, act: int, router_w: Tensor, moe: TopKMoE, pack: ExpertPack, cap: int,
+                  bias: Optional[Tensor]) -> dict:
+    """The whole layer forward as one qw_moe_forward call (inference)."""
+    dev = flat.device
+    T, width = flat.shape
+    E, K = moe.num_experts, moe.top_k
+    R = T * K
+    rw = _router_operand(router_w)
+    r = dict(out=torch.empty_like(flat), probs=torch.empty(T, E, dtype=torch.float32, device=dev),
+             top_idx=torch.empty(T, K, dtype=torch.int32, device=dev),
+             top_w=torch.empty(T, K, dtype=torch.float32, device=dev),
+             counts=torch.empty(E, dtype=torch.int32, device=dev),
+             kept_counts=torch.empty(E, dtype=torch.int32, device=dev),
+             totals=torch.zeros(2, dtype=torch.int32, device=dev),
+             dropped_token=torch.empty(max(R, 1), dtype=torch.int32, device=dev),
+             dropped_expert=torch.empty(max(R, 1), dtype=torch.int32, device=dev),
+             balance=torch.zeros((), dtype=torch.float32, device=dev))
+    if T:
+        s = _hip.stream(dev)
+        d_ff = moe.experts[0].gate.out_features
+        nbytes = _lib.load().qw_moe_forward_workspace_bytes(T, width, E, K, d_ff, act)
+        ws = _hip.workspace(nbytes, dev)
+        _lib.call("qw_moe_forward", _hip.ptr(flat), act, T, width, _hip.ptr(rw), _hip.act_code(rw, "router"),
+                  float(moe.router_temperature), _hip.ptr(bias), E, K, cap, d_ff, *pack.args(), _hip.ptr(r["out"]),
+                  _hip.ptr(r["probs"]), _hip.ptr(r["top_idx"]), _hip.ptr(r["top_w"]), _hip.ptr(r["counts"]),
+                  _hip.ptr(r["kept_counts"]), _hip.ptr(r["totals"]), _hip.ptr(r["dropped_token"]),
+                  _hip.ptr(r["dropped_expert"]), _hip.ptr(ws), nbytes, s)
+        importance = torch.empty(E, dtype=torch.float32, device=dev)
+        _lib.call("qw_moe_balance", _hip.ptr(r["probs"]), _hip.ptr(r["counts"]), T, K, E, _hip.ptr(importance),
+                  _hip.ptr(r["balance"]), s)
+    return r
+
+
+class _MoELayer(torch.autograd.Function):
+    """TopKMoE.forward with gradients for the input, the router and the
+    experts (src/quantweave_moe_model.py:113-164, :190-202 through autograd).
+
+    Forward: the inference kernels as separate C calls — qw_moe_route,
+    qw_moe_plan, qw_moe_experts (fused, weighted rows), qw_moe_combine and
+    qw_moe_balance — so the output equals qw_moe_forward's.  Backward
+    recomputes the routed rows' activations (qw_moe_permute, grouped gate/up/
+    down matmuls, qw_swiglu), then
+      qw_moe_combine_backward   d(expert rows), d(router weights)
+      grouped backward kernels  down, SwiGLU, gate and up
+      qw_moe_combine_weighted   index_add of the row gradients (weights off)
+      qw_moe_route_backward     renormalise + balance + softmax backward
+    and the router's two plain products (library GEMMs)."""
+
+    @staticmethod
+    def forward(ctx, flat, router_w, moe, pack, cap, bias, *weights):
+        ctx.set_materialize_grads(False)
+        flat = flat.detach().contiguous()
+        act = _hip.act_code(flat, "TopKMoE.forward")
+        dev = flat.device
+        T, D = flat.shape
+        E, K = moe.num_experts, moe.top_k
+        R = T * K
+        F_ = moe.experts[0].gate.out_features
+        rw = _router_operand(router_w)
+        i32 = dict(dtype=torch.int32, device=dev)
+        probs = torch.empty(T, E, dtype=torch.float32, device=dev)
+        top_idx = torch.empty(T, K, **i32)
+        top_w = torch.empty(T, K, dtype=torch.float32, device=dev)
+        counts, kept_counts = torch.empty(E, **i32), torch.empty(E, **i32)
+        kept_offsets = torch.zeros(E + 1, **i32)
+        slot_token, route_slot = torch.empty(max(R, 1), **i32), torch.empty(max(R, 1), **i32)
+        slot_weight = torch.empty(max(R, 1), dtype=torch.float32, device=dev)
+        dropped_token, dropped_expert = torch.empty(max(R, 1), **i32), torch.empty(max(R, 1), **i32)
+        totals = torch.zeros(2, **i32)
+        balance = torch.zeros((), dtype=torch.float32, device=dev)
+        out = torch.empty_like(flat)
+        lib = _lib.load()
+        s = _hip.stream(dev)
+        if T:
+            logits = torch.empty(T, E, dtype=torch.float32, device=dev)
+            nb = lib.qw_moe_route_workspace_bytes(T, D, E)
+            ws = _hip.workspace(nb, dev)
+            _lib.call("qw_moe_route", _hip.ptr(flat), act, D, _hip.ptr(rw), _hip.act_code(rw, "router"), T, D, E, K,
+                      float(moe.router_temperature), _hip.ptr(bias), _hip.ptr(logits), _hip.ptr(probs),
+                      _hip.ptr(top_idx), _hip.ptr(top_w), _hip.ptr(ws), nb, s)
+            nb = lib.qw_moe_plan_workspace_bytes(T, K, E)
+            ws = _hip.workspace(nb, dev)
+            _lib.call("qw_moe_plan", _hip.ptr(top_idx), _hip.ptr(top_w), T, K, E, cap, _hip.ptr(counts),
+                      _hip.ptr(kept_counts), _hip.ptr(kept_offsets), _hip.ptr(slot_token), _hip.ptr(slot_weight),
+                      _hip.ptr(route_slot), _hip.ptr(dropped_token), _hip.ptr(dropped_expert), _hip.ptr(totals),
+                      _hip.ptr(ws), nb, s)
+            max_rows = min(R, cap * E)
+            y = torch.empty(R, D, dtype=flat.dtype, device=dev)
+            nb = lib.qw_moe_experts_workspace_bytes(max_rows, E, D, F_, act)
+            ws = _hip.workspace(nb, dev)
+            _lib.call("qw_moe_experts", _hip.ptr(flat), act, _hip.ptr(slot_token), _hip.ptr(kept_offsets), E, D, F_,
+                      max_rows, min(cap, R), *pack.args(), _hip.ptr(slot_weight), _hip.ptr(y), _hip.ptr(ws), nb, s)
+            _lib.call("qw_moe_combine", _hip.ptr(y), act, _hip.ptr(route_slot), _hip.ptr(top_idx), T, K, D,
+                      _hip.ptr(out), s)
+            importance = torch.empty(E, dtype=torch.float32, device=dev)
+            _lib.call("qw_moe_balance", _hip.ptr(probs), _hip.ptr(counts), T, K, E, _hip.ptr(importance),
+                      _hip.ptr(balance), s)
+        ctx.save_for_backward(flat, rw, probs, top_idx, top_w, counts, kept_offsets, slot_token, route_slot, totals)
+        ctx.moe, ctx.cap, ctx.router_dtype = moe, cap, router_w.dtype
+        ctx.mark_non_differentiable(top_idx, top_w, counts, kept_counts, totals, dropped_token, dropped_expert)
+        return out, probs, balance, top_idx, top_w, counts, kept_counts, totals, dropped_token, dropped_expert
+
+    @staticmethod
+    def backward(ctx, d_out, d_probs, d_balance, *unused):
+        flat, rw, probs, top_idx, top_w, counts, kept_offsets, slot_token, route_slot, totals = ctx.saved_tensors
+        moe = ctx.moe
+        n_w = 3 * len(moe.experts)
+        need_x, need_router = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        need_experts = any(ctx.needs_input_grad[6:6 + n_w])
+        T, D = flat.shape
+        E, K = moe.num_experts, moe.top_k
+        R = T * K
+        dev = flat.device
+        s = _hip.stream(dev)
+        act = _hip.act_code(flat, "TopKMoE.backward")
+        d_flat = None
+        expert_grads = [None] * n_w
+        d_top_w = torch.zeros(T, K, dtype=torch.float32, device=dev)
+        if T and d_out is not None and (need_x or need_router or need_experts):
+            from .moe_kernels import _backward, _forward
+
+            stacks = [torch.stack([getattr(e, n).weight.detach() for e in moe.experts]).to(flat.dtype).contiguous()
+                      for n in ("gate", "up", "down")]
+            plan = _RowPlan(kept_offsets, E, min(ctx.cap, R))
+            xp = torch.empty(R, D, dtype=flat.dtype, device=dev)
+            _lib.call("qw_moe_permute", _hip.ptr(flat), act, D, _hip.ptr(slot_token), _hip.ptr(totals), R,
+                      _hip.ptr(xp), s)
+            g = _forward(xp, stacks[0], plan, act)
+            u = _forward(xp, stacks[1], plan, act)
+            h = torch.empty_like(g)
+            _lib.call("qw_swiglu", _hip.ptr(g), _hip.ptr(u), act, g.numel(), _hip.ptr(h), s)
+            y = _forward(h, stacks[2], plan, act)
+            d_out = d_out.contiguous().to(flat.dtype)
+            dy = torch.empty_like(y)
+            _lib.call("qw_moe_combine_backward", _hip.ptr(d_out), act, _hip.ptr(y), act, _hip.ptr(route_slot),
+                      _hip.ptr(top_w), T, K, D, _hip.ptr(dy), _hip.ptr(d_top_w), s)
+            if need_x or need_experts:
+                dh, d_down = _backward(dy, h, stacks[2], plan, act, True, need_experts)
+                dg, du = torch.empty_like(g), torch.empty_like(u)
+                _lib.call("qw_swiglu_backward", _hip.ptr(dh), _hip.ptr(g), _hip.ptr(u), act, g.numel(), _hip.ptr(dg),
+                          _hip.ptr(du), s)
+                dxp, d_gate = _backward(dg, xp, stacks[0], plan, act, need_x, need_experts)
+                dxp, d_up = _backward(du, xp, stacks[1], plan, act, need_x, need_experts, grad_x=dxp)
+                if need_experts:
+                    for i, e in enumerate(moe.experts):
+                        for j, (n, gw) in enumerate((("gate", d_gate), ("up", d_up), ("down", d_down))):
+                            expert_grads[3 * i + j] = gw[i].to(getattr(e, n).weight.dtype)
+                if need_x:
+                    d_flat = torch.empty_like(flat)
+                    _lib.call("qw_moe_combine_weighted", _hip.ptr(dxp), act, _hip.ptr(route_slot), _hip.ptr(top_idx),
+                              None, T, K, D, _hip.ptr(d_flat), act, s)
+        d_router = None
+        if T and (need_x or need_router) and (d_out is not None or d_probs is not None or d_balance is not None):
+            d_scores = torch.empty(T, E, dtype=torch.float32, device=dev)
+            gp = None if d_probs is None else d_probs.contiguous().float()
+            gb = None if d_balance is None else d_balance.reshape(1).contiguous().float()
+            _lib.call("qw_moe_route_backward", _hip.ptr(probs), _hip.ptr(top_idx), _hip.ptr(top_w), _hip.ptr(d_top_w),
+                      _hip.ptr(gp), _hip.ptr(gb), _hip.ptr(counts), T, E, K, float(moe.router_temperature),
+                      _hip.ptr(d_scores), s)
+            if need_router:
+                d_router = (d_scores.t() @ flat.float()).to(ctx.router_dtype)
+            if need_x:
+                dx_router = (d_scores @ rw.float()).to(flat.dtype)
+                d_flat = dx_router if d_flat is None else d_flat + dx_router
+        return (d_flat, d_router, None, None, None, None, *expert_grads)
+
+
+class _RowPlan:
+    """Device row offsets of the plan-ordered rows, in the shape the grouped
+    matmul helpers take (offsets, experts, per-expert row bound)."""
+
+    def __init__(self, offsets: Tensor, experts: int, max_count: int) -> None:
+        self.offsets = offsets
+        self.num_experts = experts
+        self.max_count = max_count
 
 
 def set_moe_kernel(model: nn.Module, kernel: str) -> str:

@@ -4,7 +4,7 @@ Same public names and argument meaning as src/moe_kernels.py:
 ``kernels_available``, ``experts_support_grouped``, ``GroupedPlan``,
 ``grouped_matmul``, ``compute_dtype``, ``grouped_swiglu`` and ``benchmark``.
 The kernels are hand-written HIP for gfx950 behind the C ABI
-(include/qwmoe.h), forward only.  Differences from the reference:
+(include/qwmoe.h), forward and backward.  Differences from the reference:
 
 * quantised experts (``QuantizedLinear``) are supported by the grouped path
   (the reference restricts it to nn.Linear, src/moe_kernels.py:174-176);
@@ -50,6 +50,7 @@ class GroupedPlan:
         self.rows = total
         self.num_experts = len(counts)
         self.counts = counts
+        self.max_count = max(counts, default=0)
         self.offsets = torch.tensor(offsets, dtype=torch.int32, device=device)
 
 
@@ -69,38 +70,140 @@ def compute_dtype(inputs: Tensor) -> torch.dtype:
     return inputs.dtype
 
 
-def grouped_matmul(x: Tensor, weight: Tensor, plan: GroupedPlan) -> Tensor:
-    """Per-expert x @ W[e]^T over expert-sorted rows; weight is [E, out, in] (src/moe_kernels.py:167-171).
-
-    Forward only: the result carries no autograd history."""
-    _hip.require_device(x, "grouped_matmul")
-    act = _hip.act_code(x, "grouped_matmul")
+def _check_operands(x: Tensor, weight: Tensor, plan: GroupedPlan, what: str) -> int:
+    _hip.require_device(x, what)
+    act = _hip.act_code(x, what)
     if weight.dim() != 3 or weight.size(0) != plan.num_experts or weight.size(2) != x.size(1):
         raise ValueError("weight must be [experts, out, in] matching the plan and x")
     if x.size(0) != plan.rows:
         raise ValueError(f"x has {x.size(0)} rows but the plan covers {plan.rows}")
-    x = x.contiguous()
-    w = weight.detach().to(x.dtype).contiguous()
+    return act
+
+
+def _forward(x: Tensor, w: Tensor, plan: GroupedPlan, act: int) -> Tensor:
+    """out[rows of e] = x[rows of e] @ w[e]^T; x, w contiguous of one dtype."""
     out = torch.empty(x.size(0), w.size(1), dtype=x.dtype, device=x.device)
-    if plan.rows:
+    if x.size(0):
         _lib.call("qw_grouped_matmul", _hip.ptr(x), act, _hip.ptr(w), act, None, 0, w.size(0), w.size(1), w.size(2),
                   _hip.ptr(plan.offsets), x.size(0), _hip.ptr(out), _hip.stream(x.device))
     return out
 
 
+def _backward(grad: Tensor, x: Tensor, w: Tensor, plan: GroupedPlan, act: int, need_x: bool, need_w: bool,
+              grad_x: Optional[Tensor] = None) -> tuple[Optional[Tensor], Optional[Tensor]]:
+    """(grad_x, grad_w) of out = grouped x @ w^T.  A given grad_x is added to."""
+    gx = gw = None
+    accumulate = grad_x is not None
+    if need_x:
+        gx = grad_x if accumulate else torch.empty_like(x)
+    if need_w:
+        gw = torch.empty_like(w)
+    if gx is not None or gw is not None:
+        _lib.call("qw_grouped_matmul_backward", _hip.ptr(grad), _hip.ptr(x), _hip.ptr(w), act, w.size(0), w.size(1),
+                  w.size(2), _hip.ptr(plan.offsets), x.size(0), plan.max_count, _hip.ptr(gx), int(accumulate),
+                  _hip.ptr(gw), _hip.stream(x.device))
+    return gx, gw
+
+
+class _GroupedMatmul(torch.autograd.Function):
+    """src/moe_kernels.py:138-164: grad_x = grad_out @ W[e] per expert block,
+    grad_W[e] = grad_out[rows of e]^T @ x[rows of e] (exactly zero for an
+    expert without rows), both through qw_grouped_matmul_backward."""
+
+    @staticmethod
+    def forward(ctx, x: Tensor, weight: Tensor, plan: GroupedPlan) -> Tensor:
+        act = _check_operands(x, weight, plan, "grouped_matmul")
+        x = x.contiguous()
+        w = weight.detach().to(x.dtype).contiguous()
+        ctx.save_for_backward(x, w)
+        ctx.plan, ctx.act, ctx.weight_dtype = plan, act, weight.dtype
+        return _forward(x, w, plan, act)
+
+    @staticmethod
+    def backward(ctx, grad_output: Tensor):
+        x, w = ctx.saved_tensors
+        grad = grad_output.contiguous().to(x.dtype)
+        gx, gw = _backward(grad, x, w, ctx.plan, ctx.act, ctx.needs_input_grad[0], ctx.needs_input_grad[1])
+        if gw is not None:
+            gw = gw.to(ctx.weight_dtype)
+        return gx, gw, None
+
+
+def grouped_matmul(x: Tensor, weight: Tensor, plan: GroupedPlan) -> Tensor:
+    """Per-expert x @ W[e]^T over expert-sorted rows; weight is [E, out, in] (src/moe_kernels.py:167-171).
+
+    Differentiable in x and weight (the backward runs the grouped HIP kernels)."""
+    return _GroupedMatmul.apply(x, weight, plan)
+
+
+class _GroupedSwiGLU(torch.autograd.Function):
+    """down(silu(gate(x)) * up(x)) over expert blocks with its backward, the
+    composition grouped_swiglu builds from _GroupedMatmul and F.silu
+    (src/moe_kernels.py:186-195): three grouped matmuls and qw_swiglu forward;
+    qw_swiglu_backward and five grouped backward products (grad_x of gate and
+    up summed in place) backward.  Weights are stacked [E, out, in] of x's dtype."""
+
+    @staticmethod
+    def forward(ctx, x: Tensor, gate: Tensor, up: Tensor, down: Tensor, plan: GroupedPlan) -> Tensor:
+        act = _hip.act_code(x, "grouped_swiglu")
+        x = x.contiguous()
+        gate, up, down = (t.detach().contiguous() for t in (gate, up, down))
+        g = _forward(x, gate, plan, act)
+        u = _forward(x, up, plan, act)
+        h = torch.empty_like(g)
+        _lib.call("qw_swiglu", _hip.ptr(g), _hip.ptr(u), act, g.numel(), _hip.ptr(h), _hip.stream(x.device))
+        y = _forward(h, down, plan, act)
+        ctx.save_for_backward(x, gate, up, down, g, u, h)
+        ctx.plan, ctx.act = plan, act
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_output: Tensor):
+        x, gate, up, down, g, u, h = ctx.saved_tensors
+        plan, act = ctx.plan, ctx.act
+        need_x, need_g, need_u, need_d = ctx.needs_input_grad[:4]
+        grad = grad_output.contiguous().to(x.dtype)
+        dh, d_down = _backward(grad, h, down, plan, act, True, need_d)
+        dg, du = torch.empty_like(g), torch.empty_like(u)
+        _lib.call("qw_swiglu_backward", _hip.ptr(dh), _hip.ptr(g), _hip.ptr(u), act, g.numel(), _hip.ptr(dg),
+                  _hip.ptr(du), _hip.stream(x.device))
+        dx, d_gate = _backward(dg, x, gate, plan, act, need_x, need_g)
+        dx, d_up = _backward(du, x, up, plan, act, need_x, need_u, grad_x=dx)
+        return dx, d_gate, d_up, d_down, None
+
+
+def _needs_grad(inputs: Tensor, experts: nn.ModuleList) -> bool:
+    if not torch.is_grad_enabled():
+        return False
+    return inputs.requires_grad or any(p.requires_grad for p in experts.parameters())
+
+
 def grouped_swiglu(inputs: Tensor, experts: nn.ModuleList, counts: Sequence[int], plan: Optional[GroupedPlan] = None) -> Tensor:
     """SwiGLU over expert-sorted rows: down(silu(gate(x)) * up(x)) with each
-    expert's own weights (src/moe_kernels.py:186-195), in one pair of HIP
-    kernels (fused gate/up + SiLU·mul, then down)."""
+    expert's own weights (src/moe_kernels.py:186-195).
+
+    Without gradients: one pair of HIP kernels (fused gate/up + SiLU·mul, then
+    down) on the cached expert stacks.  With gradients (autograd on and the
+    inputs or expert weights requiring grad): the differentiable composition
+    over freshly stacked weights, as the reference stacks them per call."""
     _hip.require_device(inputs, "grouped_swiglu")
     plan = plan or GroupedPlan(counts, inputs.device)
     if plan.num_experts != len(experts):
         raise ValueError("plan and experts disagree on the number of experts")
     dtype = compute_dtype(inputs)
+    if inputs.size(0) != plan.rows:
+        raise ValueError(f"inputs have {inputs.size(0)} rows but the plan covers {plan.rows}")
+    if _needs_grad(inputs, experts):
+        if any(isinstance(getattr(e, n), QuantizedLinear) for e in experts for n in ("gate", "up", "down")):
+            raise NotImplementedError("gradients through quantised experts are not supported")
+        x = inputs.to(dtype)
+        _hip.act_code(x, "grouped_swiglu")
+        gate = torch.stack([e.gate.weight for e in experts]).to(dtype)
+        up = torch.stack([e.up.weight for e in experts]).to(dtype)
+        down = torch.stack([e.down.weight for e in experts]).to(dtype)
+        return _GroupedSwiGLU.apply(x, gate, up, down, plan)
     x = inputs.detach().to(dtype).contiguous()
     act = _hip.act_code(x, "grouped_swiglu")
-    if x.size(0) != plan.rows:
-        raise ValueError(f"inputs have {x.size(0)} rows but the plan covers {plan.rows}")
     pack = packed_experts(experts, experts)
     args = pack.args()
     if pack.fmt in (_lib.QW_F32, _lib.QW_BF16) and pack.fmt != act:

@@ -92,3 +92,27 @@ def test_decode_step_validation_and_workspace():
     one = lib.qw_moe_decode_step_workspace_bytes(1, 4096, 64, 2, 1408, _lib.QW_BF16)
     assert 0 < one < lib.qw_moe_decode_step_workspace_bytes(16, 4096, 64, 2, 1408, _lib.QW_BF16)
     assert lib.qw_moe_decode_step_workspace_bytes(1, 4096, 64, 2, 1408, 7) == 0
+
+
+def test_backward_entry_points_validate_before_any_launch():
+    lib = _lib.load()
+    bad = _lib.QW_ERR_INVALID
+    # grouped backward: plain fp32/bf16 only, offsets required
+    assert lib.qw_grouped_matmul_backward(None, None, None, _lib.QW_I8, 8, 16, 16, None, 4, 0, None, 0, None,
+                                          None) == bad
+    assert b"dtype" in lib.qw_last_error()
+    assert lib.qw_grouped_matmul_backward(None, None, None, _lib.QW_F32, 8, 16, 16, None, 4, 0, None, 0, None,
+                                          None) == bad
+    assert b"offsets" in lib.qw_last_error()
+    assert lib.qw_swiglu(None, None, _lib.QW_F32, -1, None, None) == bad
+    assert lib.qw_swiglu_backward(None, None, None, _lib.QW_U4, 8, None, None, None) == bad
+    # combine and route backward: top_k <= 64
+    assert lib.qw_moe_combine_backward(None, _lib.QW_F32, None, _lib.QW_F32, None, None, 4, 65, 8, None, None,
+                                       None) == bad
+    assert lib.qw_moe_route_backward(None, None, None, None, None, None, None, 4, 128, 65, 1.0, None, None) == bad
+    assert b"top_k" in lib.qw_last_error()
+    assert lib.qw_moe_route_backward(None, None, None, None, None, None, None, 4, 8, 2, 0.0, None, None) == bad
+    assert lib.qw_moe_combine_weighted(None, _lib.QW_F32, None, None, None, 4, 2, 8, None, _lib.QW_I8, None) == bad
+    # nothing to do is not an error
+    assert lib.qw_moe_route_backward(None, None, None, None, None, None, None, 0, 8, 2, 1.0, None, None) == 0
+    assert lib.qw_swiglu(None, None, _lib.QW_BF16, 0, None, None) == 0

@@ -154,13 +154,17 @@ def test_grouped_swiglu_api_matches_oracle_over_real_experts():
                                   attention_heads=1, max_sequence_length=8)
     moe = qa.TopKMoE(config).cuda()
     x = torch.randn(sum(COUNTS), 48, device="cuda")
-    out = mk.grouped_swiglu(x, moe.experts, COUNTS)
+    with torch.no_grad():
+        fused = mk.grouped_swiglu(x, moe.experts, COUNTS)  # fused gate/up + down kernels
+    composed = mk.grouped_swiglu(x, moe.experts, COUNTS)  # differentiable composition (weights need grad)
+    assert composed.requires_grad and not fused.requires_grad
     w = dict(format="f32", d_model=48, d_ff=72,
              gate=np.stack([e.gate.weight.detach().cpu().numpy() for e in moe.experts]),
              up=np.stack([e.up.weight.detach().cpu().numpy() for e in moe.experts]),
              down=np.stack([e.down.weight.detach().cpu().numpy() for e in moe.experts]))
     ref = oracle.experts_forward(x.cpu().numpy(), np.array(COUNTS), w, "f32")
-    assert np.allclose(out.cpu().numpy(), ref, atol=1e-4, rtol=1e-4)
+    for out in (fused, composed):
+        assert np.allclose(out.detach().cpu().numpy(), ref, atol=1e-4, rtol=1e-4)
 
 
 @pytest.mark.parametrize("bits,group,shape", [(8, None, (24, 40)), (4, 16, (24, 40)), (4, None, (1408, 4096)),
