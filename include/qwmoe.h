@@ -249,6 +249,21 @@ int qw_grouped_matmul_backward(const void* grad_out, const void* x, const void* 
                                int64_t max_rows_per_expert, void* grad_x, int accumulate_grad_x, void* grad_w,
                                void* stream);
 
+/* qw_moe_experts that also keeps what its backward needs, for training
+ * (the activations autograd saves for SparseSwiGLU.forward,
+ * src/quantweave_moe_model.py:59-60): gate_out / up_out [max_rows, d_ff] the
+ * gate and up projections before the SiLU, hidden_out [max_rows, d_ff] the
+ * SiLU product, y_unweighted [max_rows, d_model] the expert rows before
+ * row_weight; all act_dtype, plan-ordered.  y and the other arguments as for
+ * qw_moe_experts, with identical results. */
+int qw_moe_experts_save(const void* x, int act_dtype, const int32_t* row_index, const int32_t* kept_offsets,
+                        int64_t experts, int64_t d_model, int64_t d_ff, int64_t max_rows,
+                        int64_t max_rows_per_expert, int w_format, int64_t group_in, int64_t group_ff,
+                        const void* gate_w, const float* gate_scales, const void* up_w, const float* up_scales,
+                        const void* down_w, const float* down_scales, const float* row_weight, void* y,
+                        void* gate_out, void* up_out, void* hidden_out, void* y_unweighted, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
 /* hidden = silu(gate) * up over n elements, `F.silu(gate) * up` of
  * grouped_swiglu (src/moe_kernels.py:194); bf16 rounds silu and the product. */
 int qw_swiglu(const void* gate, const void* up, int dtype, int64_t n, void* hidden, void* stream);

@@ -96,7 +96,9 @@ size_t experts_workspace_bytes(int64_t max_rows, int64_t E, int64_t D, int64_t F
 int experts(const void* x, int act, const int32_t* row_index, const int32_t* offsets, int64_t E, int64_t D, int64_t F,
             int64_t max_rows, int wfmt, int64_t group_in, int64_t group_ff, const void* gate_w, const float* gate_s,
             const void* up_w, const float* up_s, const void* down_w, const float* down_s, const float* row_weight,
-            void* y, void* ws, size_t ws_bytes, hipStream_t stream, int64_t avg_rows, int64_t row_cap) {
+            void* y, void* ws, size_t ws_bytes, hipStream_t stream, int64_t avg_rows, int64_t row_cap,
+            void* save_gate = nullptr, void* save_up = nullptr, void* save_y = nullptr,
+            void* hidden_out = nullptr) {
   QW_REQUIRE(act == QW_F32 || act == QW_BF16, "activation dtype must be f32 or bf16");
   QW_REQUIRE(wfmt >= QW_F32 && wfmt <= QW_BF16T, "unknown weight format %d", wfmt);
   QW_REQUIRE(E >= 1 && E <= 65535, "experts out of range");
@@ -131,7 +133,11 @@ int experts(const void* x, int act, const int32_t* row_index, const int32_t* off
   a.down = make_wview(wfmt, down_w, down_s, D, F, group_ff);
   a.row_weight = row_weight;
   a.hidden = c.take<char>(static_cast<size_t>(max_rows) * F * act_size(act));
+  if (hidden_out) a.hidden = hidden_out;
   a.partial = c.take<float>(static_cast<size_t>(max_rows) * D);
+  a.save_gate = save_gate;
+  a.save_up = save_up;
+  a.save_y = save_y;
   a.y = y;
   a.avg_rows = avg_rows;
   a.row_cap = row_cap;
@@ -470,6 +476,24 @@ int qw_grouped_matmul(const void* x, int act_dtype, const void* w, int w_format,
   QW_REQUIRE(x && w && offsets && out, "grouped_matmul pointers are required");
   const WView v = make_wview(w_format, w, scales, out_features, in_features, group);
   return grouped_matmul_generic(x, act_dtype, v, w_format, experts, offsets, rows, out, as_stream(stream));
+}
+
+int qw_moe_experts_save(const void* x, int act_dtype, const int32_t* row_index, const int32_t* kept_offsets,
+                        int64_t experts, int64_t d_model, int64_t d_ff, int64_t max_rows,
+                        int64_t max_rows_per_expert, int w_format, int64_t group_in, int64_t group_ff,
+                        const void* gate_w, const float* gate_scales, const void* up_w, const float* up_scales,
+                        const void* down_w, const float* down_scales, const float* row_weight, void* y,
+                        void* gate_out, void* up_out, void* hidden_out, void* y_unweighted, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  clear_error();
+  QW_REQUIRE(max_rows_per_expert >= 0, "max_rows_per_expert must be >= 0");
+  QW_REQUIRE(gate_out && up_out && hidden_out && y_unweighted, "the saved activation buffers are required");
+  const int64_t cap = (max_rows_per_expert > 0 && max_rows_per_expert < max_rows) ? max_rows_per_expert : max_rows;
+  int64_t avg = experts > 0 ? (max_rows + experts - 1) / experts : 0;
+  if (avg > cap) avg = cap;
+  return qw::experts(x, act_dtype, row_index, kept_offsets, experts, d_model, d_ff, max_rows, w_format, group_in,
+                     group_ff, gate_w, gate_scales, up_w, up_scales, down_w, down_scales, row_weight, y, workspace,
+                     workspace_bytes, as_stream(stream), avg, cap, gate_out, up_out, y_unweighted, hidden_out);
 }
 
 int qw_moe_combine_weighted(const void* y, int y_dtype, const int32_t* route_slot, const int32_t* top_idx,

@@ -18,6 +18,13 @@ struct FfnArgs {
   float* partial;            // split-K partial sums (workspace), may be NULL
   int64_t avg_rows;          // expected rows per expert (host-side estimate)
   int64_t row_cap;           // most rows any one expert can hold (capacity bound)
+  // Optional saved activations for a backward pass (act dtype, plan-ordered
+  // rows): gate and up projections [max_rows, d_ff] before the SiLU, and the
+  // expert output rows [max_rows, d_model] before the row weight.  The GEMV
+  // path does not save; the MFMA and general kernels do.
+  void* save_gate = nullptr;
+  void* save_up = nullptr;
+  void* save_y = nullptr;
 };
 
 int launch_ffn_generic(const FfnArgs& a, hipStream_t stream);

@@ -579,6 +579,7 @@ int launch_fmt(const FfnArgs& a, hipStream_t stream) {
 int launch_ffn_gemv(const FfnArgs& a, hipStream_t stream, bool* handled) {
   *handled = false;
   if (a.act != QW_BF16 || a.avg_rows >= 16) return QW_OK;
+  if (a.save_gate || a.save_y) return QW_OK;  // saving activations: MFMA or general kernels
   int cw = 0;
   if (a.wfmt == QW_U4) {
     if (a.gate.group % 32 || a.down.group % 32) return QW_OK;

@@ -30,7 +30,8 @@ __global__ __launch_bounds__(256) void ffn_generic_kernel(const void* __restrict
                                                           const int32_t* __restrict__ offsets, WView wa, WView wb,
                                                           int K, int N_out, int max_rows,
                                                           const float* __restrict__ row_weight,
-                                                          void* __restrict__ out) {
+                                                          void* __restrict__ out, void* __restrict__ save_a,
+                                                          void* __restrict__ save_b) {
   __shared__ float ws[GB_N][GB_K + 1];
   __shared__ float xs[GB_M][GB_K + 1];
   __shared__ float os[GB_M][GB_N + 1];
@@ -91,7 +92,12 @@ __global__ __launch_bounds__(256) void ffn_generic_kernel(const void* __restrict
         if (s < r1 && c0 + c < N_out) {
           const float g = round_act<ACT>(os[m][c]);
           const float u = round_act<ACT>(os[m][c + COLS]);
-          store_act<ACT>(out, static_cast<int64_t>(s) * N_out + c0 + c, silu_f32(g) * u);
+          const int64_t o = static_cast<int64_t>(s) * N_out + c0 + c;
+          store_act<ACT>(out, o, silu_f32(g) * u);
+          if (save_a) {  // gate and up projections, for the backward pass
+            store_act<ACT>(save_a, o, g);
+            store_act<ACT>(save_b, o, u);
+          }
         }
       }
       __syncthreads();
@@ -101,7 +107,9 @@ __global__ __launch_bounds__(256) void ffn_generic_kernel(const void* __restrict
         const int s = m0 + mg * 4 + i;
         if (s < r1 && c0 + n < N_out) {
           const float wgt = row_weight ? row_weight[s] : 1.0f;
-          store_act<ACT>(out, static_cast<int64_t>(s) * N_out + c0 + n, round_act<ACT>(acc[i]) * wgt);
+          const int64_t o = static_cast<int64_t>(s) * N_out + c0 + n;
+          store_act<ACT>(out, o, round_act<ACT>(acc[i]) * wgt);
+          if (save_a) store_act<ACT>(save_a, o, acc[i]);  // the row before its weight
         }
       }
     }
@@ -114,12 +122,14 @@ int launch_generic_t(const FfnArgs& a, hipStream_t stream) {
   const dim3 g1(static_cast<unsigned>(ceil_div(a.d_ff, GB_N / 2)), static_cast<unsigned>(a.experts));
   ffn_generic_kernel<ACT, WF, true><<<g1, blk, 0, stream>>>(a.x, a.row_index, a.offsets, a.gate, a.up,
                                                             static_cast<int>(a.d_model), static_cast<int>(a.d_ff),
-                                                            static_cast<int>(a.max_rows), nullptr, a.hidden);
+                                                            static_cast<int>(a.max_rows), nullptr, a.hidden,
+                                                            a.save_gate, a.save_up);
   QW_LAUNCH_CHECK("ffn_generic_kernel<gateup>");
   const dim3 g2(static_cast<unsigned>(ceil_div(a.d_model, GB_N)), static_cast<unsigned>(a.experts));
   ffn_generic_kernel<ACT, WF, false><<<g2, blk, 0, stream>>>(a.hidden, nullptr, a.offsets, a.down, a.down,
                                                              static_cast<int>(a.d_ff), static_cast<int>(a.d_model),
-                                                             static_cast<int>(a.max_rows), a.row_weight, a.y);
+                                                             static_cast<int>(a.max_rows), a.row_weight, a.y,
+                                                             a.save_y, nullptr);
   QW_LAUNCH_CHECK("ffn_generic_kernel<down>");
   return QW_OK;
 }
@@ -149,7 +159,8 @@ int grouped_matmul_generic(const void* x, int act, const WView& w, int wfmt, int
   const int K = static_cast<int>(w.cols), N = static_cast<int>(w.rows), nrows = static_cast<int>(rows);
 #define QW_GM(ACT, WF)                                                                                         \
   if (act == ACT && wfmt == WF) {                                                                              \
-    ffn_generic_kernel<ACT, WF, false><<<g, 256, 0, stream>>>(x, nullptr, offsets, w, w, K, N, nrows, nullptr, out); \
+    ffn_generic_kernel<ACT, WF, false><<<g, 256, 0, stream>>>(x, nullptr, offsets, w, w, K, N, nrows, nullptr, out, \
+                                                              nullptr, nullptr);                                \
     QW_LAUNCH_CHECK("ffn_generic_kernel<matmul>");                                                            \
     return QW_OK;                                                                                              \
   }

@@ -96,7 +96,7 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
     int max_rows, const uint16_t* __restrict__ wa, const uint16_t* __restrict__ wb, int64_t w_expert_stride,
     int n_w, int K, const float* __restrict__ row_weight, uint16_t* __restrict__ out, int n_out, int n_tiles,
-    int m_chunks, int experts) {
+    int m_chunks, int experts, uint16_t* __restrict__ save_a, uint16_t* __restrict__ save_b) {
   constexpr int MCH = 32 * SUBT;                 // rows per chunk
   constexpr int AG = MCH / MF_GROWS;             // 8-row load groups of the A slice
   constexpr int BG = MF_NB / MF_GROWS;           // ... of the B slice
@@ -295,6 +295,17 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
           pk[h] = f32_to_bf16(a) | (static_cast<uint32_t>(f32_to_bf16(c)) << 16);
         }
         *reinterpret_cast<uint2*>(out + orow + col) = make_uint2(pk[0], pk[1]);
+        if (save_a) {  // gate and up projections, for the backward pass
+          uint32_t g2[2], u2[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            g2[h] = f32_to_bf16(acc[i][t][2 * h]) | (static_cast<uint32_t>(f32_to_bf16(acc[i][t][2 * h + 1])) << 16);
+            u2[h] = f32_to_bf16(acc[i][t + MF_NT / 2][2 * h]) |
+                    (static_cast<uint32_t>(f32_to_bf16(acc[i][t + MF_NT / 2][2 * h + 1])) << 16);
+          }
+          *reinterpret_cast<uint2*>(save_a + orow + col) = make_uint2(g2[0], g2[1]);
+          *reinterpret_cast<uint2*>(save_b + orow + col) = make_uint2(u2[0], u2[1]);
+        }
       }
     } else {
       const float wgt = row_weight ? row_weight[r0 + row] : 1.0f;
@@ -302,14 +313,16 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
       for (int t = 0; t < MF_NT; ++t) {
         const int col = n0 + wn * 64 + t * 16 + 4 * lq;
         if (col >= n_out) continue;
-        uint32_t pk[2];
+        uint32_t pk[2], un[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const float a = round_to_bf16(acc[i][t][2 * h]) * wgt;
           const float c = round_to_bf16(acc[i][t][2 * h + 1]) * wgt;
           pk[h] = f32_to_bf16(a) | (static_cast<uint32_t>(f32_to_bf16(c)) << 16);
+          un[h] = f32_to_bf16(acc[i][t][2 * h]) | (static_cast<uint32_t>(f32_to_bf16(acc[i][t][2 * h + 1])) << 16);
         }
         *reinterpret_cast<uint2*>(out + orow + col) = make_uint2(pk[0], pk[1]);
+        if (save_a) *reinterpret_cast<uint2*>(save_a + orow + col) = make_uint2(un[0], un[1]);
       }
     }
   }
@@ -318,7 +331,7 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
 template <bool GATEUP, int SUBT, bool TILED>
 int launch_t(const void* x, const int32_t* row_index, const int32_t* offsets, int max_rows, const void* wa,
              const void* wb, int64_t w_stride, int n_w, int K, const float* row_weight, void* out, int n_out,
-             int experts, int64_t rows_cap, hipStream_t stream) {
+             int experts, int64_t rows_cap, void* save_a, void* save_b, hipStream_t stream) {
   const int n_tiles = static_cast<int>(ceil_div(GATEUP ? n_w : n_out, GATEUP ? MF_NB / 2 : MF_NB));
   const int m_chunks = static_cast<int>(ceil_div(rows_cap, 32 * SUBT));
   const int64_t grid = static_cast<int64_t>(ceil_div(experts, kXcds)) * kXcds * m_chunks * n_tiles;
@@ -332,7 +345,7 @@ int launch_t(const void* x, const int32_t* row_index, const int32_t* offsets, in
   ffn_mfma_kernel<GATEUP, SUBT, TILED><<<static_cast<unsigned>(grid), MF_THREADS, lds, stream>>>(
       static_cast<const uint16_t*>(x), row_index, offsets, max_rows, static_cast<const uint16_t*>(wa),
       static_cast<const uint16_t*>(wb), w_stride, n_w, K, row_weight, static_cast<uint16_t*>(out), n_out, n_tiles,
-      m_chunks, experts);
+      m_chunks, experts, static_cast<uint16_t*>(save_a), static_cast<uint16_t*>(save_b));
   QW_LAUNCH_CHECK(GATEUP ? "ffn_mfma_kernel<gateup>" : "ffn_mfma_kernel<down>");
   return QW_OK;
 }
@@ -341,12 +354,11 @@ int launch_t(const void* x, const int32_t* row_index, const int32_t* offsets, in
 template <bool GATEUP, bool TILED>
 int launch_sel(int subt, const void* x, const int32_t* row_index, const int32_t* offsets, int max_rows,
                const void* wa, const void* wb, int64_t w_stride, int n_w, int K, const float* row_weight, void* out,
-               int n_out, int experts, int64_t rows_cap, hipStream_t stream) {
+               int n_out, int experts, int64_t rows_cap, void* save_a, void* save_b, hipStream_t stream) {
 #define QW_MF(S)                                                                                                \
   if (subt == S)                                                                                               \
     return launch_t<GATEUP, S, TILED>(x, row_index, offsets, max_rows, wa, wb, w_stride, n_w, K, row_weight, out,   \
-                                      n_out, \
-                               experts, rows_cap, stream);
+                                      n_out, experts, rows_cap, save_a, save_b, stream);
   QW_MF(2)
   QW_MF(4)
   QW_MF(6)
@@ -377,10 +389,10 @@ int launch_ffn_mfma(const FfnArgs& a, hipStream_t stream, bool* handled) {
   auto both = [&](auto tiled) -> int {
     constexpr bool T = decltype(tiled)::value;
     int st = launch_sel<true, T>(subt, a.x, a.row_index, a.offsets, mr, a.gate.w, a.up.w, a.gate.expert_elems, F, D,
-                                 nullptr, a.hidden, F, E, rows_cap, stream);
+                                 nullptr, a.hidden, F, E, rows_cap, a.save_gate, a.save_up, stream);
     if (st) return st;
     return launch_sel<false, T>(subt, a.hidden, nullptr, a.offsets, mr, a.down.w, a.down.w, a.down.expert_elems, D,
-                                F, a.row_weight, a.y, D, E, rows_cap, stream);
+                                F, a.row_weight, a.y, D, E, rows_cap, a.save_y, nullptr, stream);
   };
   const int st = a.wfmt == QW_BF16T ? both(std::true_type{}) : both(std::false_type{});
   if (st) return st;

@@ -7,8 +7,8 @@ the C ABI (``qw_moe_forward``): router, softmax/top-k, capacity plan, grouped
 SwiGLU experts and the weighted combine all run as HIP kernels on the current
 stream, with no host synchronisation.  With autograd on and float experts,
 the same kernels run inside ``_MoELayer`` (one C call per stage, outputs
-identical to the inference call), whose backward recomputes the expert
-activations and runs the grouped backward kernels.
+identical to the inference call, the experts keeping their activations),
+whose backward runs the grouped backward kernels.
 """
 
 from __future__ import annotations
@@ -172,6 +172,22 @@ class ExpertPack:
         return [self.fmt, self.group_in, self.group_ff, _hip.ptr(self.gate), _hip.ptr(self.gate_s),
                 _hip.ptr(self.up), _hip.ptr(self.up_s), _hip.ptr(self.down), _hip.ptr(self.down_s)]
 
+    def args_for(self, act: int) -> list:
+        """Weight arguments for activations of dtype code `act`: fp32 experts
+        multiplied in bf16 use bf16 copies (tiled where the shapes allow),
+        made once per weight version — the reference's per-call
+        ``stack(...).to(dtype)`` (src/moe_kernels.py:191-193)."""
+        if not (self.fmt == _lib.QW_F32 and act == _lib.QW_BF16):
+            return self.args()
+        if getattr(self, "_bf16", None) is None:
+            cast = ExpertPack.__new__(ExpertPack)
+            cast.fmt, cast.group_in, cast.group_ff, cast.key = _lib.QW_BF16, 0, 0, self.key
+            cast.gate, cast.up, cast.down = (t.to(torch.bfloat16).contiguous() for t in (self.gate, self.up, self.down))
+            cast.gate_s = cast.up_s = cast.down_s = None
+            cast.maybe_tile()
+            self._bf16 = cast
+        return self._bf16.args()
+
 
 def packed_experts(owner: nn.Module, experts: nn.ModuleList) -> ExpertPack:
     pack = getattr(owner, "_qw_pack", None)
@@ -250,6 +266,7 @@ class TopKMoE(nn.Module):
         pack = packed_experts(self, self.experts)
         # static dispatch is the capacity-free evaluation (src/quantweave_moe_model.py:235-245)
         cap = T * K if self.static_dispatch else self.capacity(T)
+        cdt = _compute_dtype(flat)
         if self._wants_grad(hidden):
             if pack.fmt not in (_lib.QW_F32, _lib.QW_BF16, _lib.QW_BF16T):
                 if hidden.requires_grad:
@@ -257,15 +274,18 @@ class TopKMoE(nn.Module):
             else:
                 weights = [getattr(e, n).weight for e in self.experts for n in ("gate", "up", "down")]
                 out, probs, balance, top_idx, top_w, counts, kept_counts, totals, dropped_token, dropped_expert = \
-                    _MoELayer.apply(flat, self.router.weight, self, pack, cap, bias, *weights)
+                    _MoELayer.apply(flat, self.router.weight, self, pack, cap, bias, cdt, *weights)
                 return self._finish(out, probs, balance, top_idx, top_w, counts, kept_counts, totals, dropped_token,
                                     dropped_expert, token_domains, num_domains, (batch, sequence, width))
         with torch.no_grad():
-            res = _forward_call(flat.detach().contiguous(), act, self.router.weight.detach(), self, pack, cap, bias)
-        out, probs, balance = res["out"], res["probs"], res["balance"]
-        return self._finish(out, probs, balance, res["top_idx"], res["top_w"], res["counts"], res["kept_counts"],
-                            res["totals"], res["dropped_token"], res["dropped_expert"], token_domains, num_domains,
-                            (batch, sequence, width))
+            flat = flat.detach().contiguous()
+            if cdt == flat.dtype:
+                res = _forward_call(flat, act, self.router.weight, self, pack, cap, bias)
+            else:
+                res = _layer_chain(flat, cdt, self.router.weight, self, pack, cap, bias)
+        return self._finish(res["out"], res["probs"], res["balance"], res["top_idx"], res["top_w"], res["counts"],
+                            res["kept_counts"], res["totals"], res["dropped_token"], res["dropped_expert"],
+                            token_domains, num_domains, (batch, sequence, width))
 
     def _finish(self, out, probs, balance, top_idx, top_w, counts, kept_counts, totals, dropped_token, dropped_expert,
                 token_domains, num_domains, shape):
@@ -354,15 +374,94 @@ def _forward_call(flat: Tensor, act: int, router_w: Tensor, moe: TopKMoE, pack: 
     return r
 
 
+def _compute_dtype(flat: Tensor) -> torch.dtype:
+    """The experts' arithmetic dtype: the autocast dtype when autocast is on,
+    else the input dtype (src/moe_kernels.py:179-183).  An autocast dtype the
+    kernels do not take (fp16) leaves the input dtype in place."""
+    dt = flat.dtype
+    if torch.is_autocast_enabled(flat.device.type):
+        dt = torch.get_autocast_dtype(flat.device.type)
+    return dt if dt in (torch.float32, torch.bfloat16) else flat.dtype
+
+
+def _layer_chain(flat: Tensor, cdt: torch.dtype, router_w: Tensor, moe: TopKMoE, pack: ExpertPack, cap: int,
+                 bias: Optional[Tensor], save: bool = False) -> dict:
+    """The layer forward as one C call per stage: qw_moe_route (on the input
+    dtype, src/quantweave_moe_model.py:126-127), qw_moe_plan, qw_moe_experts
+    on the rows cast to `cdt` and qw_moe_combine, then qw_moe_balance.
+
+    With cdt == flat.dtype the experts scale their rows by the route weights
+    and the combine adds them in that dtype — the stages and arguments of
+    qw_moe_forward, so the output is identical.  With cdt != flat.dtype (bf16
+    autocast on an fp32 stream) the expert rows stay unweighted in bf16 and
+    qw_moe_combine_weighted adds (y * w) in the input dtype, as
+    `(expert_output * weights[:, None]).to(output.dtype)` does (:201).
+    save: keep the activations a backward pass reads (qw_moe_experts_save):
+    gate, up, hidden [R, d_ff] and the unweighted expert rows [R, d_model]."""
+    dev = flat.device
+    T, D = flat.shape
+    E, K = moe.num_experts, moe.top_k
+    R = T * K
+    F_ = moe.experts[0].gate.out_features
+    act_in = _hip.act_code(flat, "TopKMoE.forward")
+    act = _hip.act_code(torch.empty(0, dtype=cdt), "TopKMoE.forward")
+    mixed = act != act_in
+    rw = _router_operand(router_w)
+    i32 = dict(dtype=torch.int32, device=dev)
+    r = dict(out=torch.empty_like(flat), probs=torch.empty(T, E, dtype=torch.float32, device=dev),
+             top_idx=torch.empty(T, K, **i32), top_w=torch.empty(T, K, dtype=torch.float32, device=dev),
+             counts=torch.empty(E, **i32), kept_counts=torch.empty(E, **i32), kept_offsets=torch.zeros(E + 1, **i32),
+             slot_token=torch.empty(max(R, 1), **i32), route_slot=torch.empty(max(R, 1), **i32),
+             slot_weight=torch.empty(max(R, 1), dtype=torch.float32, device=dev),
+             dropped_token=torch.empty(max(R, 1), **i32), dropped_expert=torch.empty(max(R, 1), **i32),
+             totals=torch.zeros(2, **i32), balance=torch.zeros((), dtype=torch.float32, device=dev))
+    if not T:
+        return r
+    lib = _lib.load()
+    s = _hip.stream(dev)
+    p = {k: _hip.ptr(v) for k, v in r.items()}
+    logits = torch.empty(T, E, dtype=torch.float32, device=dev)
+    nb = lib.qw_moe_route_workspace_bytes(T, D, E)
+    ws = _hip.workspace(nb, dev)
+    _lib.call("qw_moe_route", _hip.ptr(flat), act_in, D, _hip.ptr(rw), _hip.act_code(rw, "router"), T, D, E, K,
+              float(moe.router_temperature), _hip.ptr(bias), _hip.ptr(logits), p["probs"], p["top_idx"], p["top_w"],
+              _hip.ptr(ws), nb, s)
+    nb = lib.qw_moe_plan_workspace_bytes(T, K, E)
+    ws = _hip.workspace(nb, dev)
+    _lib.call("qw_moe_plan", p["top_idx"], p["top_w"], T, K, E, cap, p["counts"], p["kept_counts"],
+              p["kept_offsets"], p["slot_token"], p["slot_weight"], p["route_slot"], p["dropped_token"],
+              p["dropped_expert"], p["totals"], _hip.ptr(ws), nb, s)
+    xc = flat.to(cdt) if mixed else flat
+    max_rows = min(R, cap * E)
+    y = torch.empty(R, D, dtype=cdt, device=dev)
+    nb = lib.qw_moe_experts_workspace_bytes(max_rows, E, D, F_, act)
+    ws = _hip.workspace(nb, dev)
+    args = [_hip.ptr(xc), act, p["slot_token"], p["kept_offsets"], E, D, F_, max_rows, min(cap, R),
+            *pack.args_for(act), None if mixed else p["slot_weight"], _hip.ptr(y)]
+    if save:
+        for name, width in (("gate", F_), ("up", F_), ("hidden", F_), ("y_unweighted", D)):
+            r[name] = torch.empty(R, width, dtype=cdt, device=dev)
+        _lib.call("qw_moe_experts_save", *args, *(_hip.ptr(r[n]) for n in ("gate", "up", "hidden", "y_unweighted")),
+                  _hip.ptr(ws), nb, s)
+    else:
+        _lib.call("qw_moe_experts", *args, _hip.ptr(ws), nb, s)
+    if mixed:
+        _lib.call("qw_moe_combine_weighted", _hip.ptr(y), act, p["route_slot"], p["top_idx"], p["top_w"], T, K, D,
+                  p["out"], act_in, s)
+    else:
+        _lib.call("qw_moe_combine", _hip.ptr(y), act, p["route_slot"], p["top_idx"], T, K, D, p["out"], s)
+    importance = torch.empty(E, dtype=torch.float32, device=dev)
+    _lib.call("qw_moe_balance", p["probs"], p["counts"], T, K, E, _hip.ptr(importance), p["balance"], s)
+    return r
+
+
 class _MoELayer(torch.autograd.Function):
     """TopKMoE.forward with gradients for the input, the router and the
     experts (src/quantweave_moe_model.py:113-164, :190-202 through autograd).
 
-    Forward: the inference kernels as separate C calls — qw_moe_route,
-    qw_moe_plan, qw_moe_experts (fused, weighted rows), qw_moe_combine and
-    qw_moe_balance — so the output equals qw_moe_forward's.  Backward
-    recomputes the routed rows' activations (qw_moe_permute, grouped gate/up/
-    down matmuls, qw_swiglu), then
+    Forward: ``_layer_chain`` (the inference kernels, one C call per stage),
+    its expert call keeping the gate/up projections, the SiLU product and the
+    unweighted expert rows (qw_moe_experts_save).  Backward:
       qw_moe_combine_backward   d(expert rows), d(router weights)
       grouped backward kernels  down, SwiGLU, gate and up
       qw_moe_combine_weighted   index_add of the row gradients (weights off)
@@ -370,94 +469,51 @@ class _MoELayer(torch.autograd.Function):
     and the router's two plain products (library GEMMs)."""
 
     @staticmethod
-    def forward(ctx, flat, router_w, moe, pack, cap, bias, *weights):
+    def forward(ctx, flat, router_w, moe, pack, cap, bias, cdt, *weights):
         ctx.set_materialize_grads(False)
         flat = flat.detach().contiguous()
-        act = _hip.act_code(flat, "TopKMoE.forward")
-        dev = flat.device
-        T, D = flat.shape
-        E, K = moe.num_experts, moe.top_k
-        R = T * K
-        F_ = moe.experts[0].gate.out_features
-        rw = _router_operand(router_w)
-        i32 = dict(dtype=torch.int32, device=dev)
-        probs = torch.empty(T, E, dtype=torch.float32, device=dev)
-        top_idx = torch.empty(T, K, **i32)
-        top_w = torch.empty(T, K, dtype=torch.float32, device=dev)
-        counts, kept_counts = torch.empty(E, **i32), torch.empty(E, **i32)
-        kept_offsets = torch.zeros(E + 1, **i32)
-        slot_token, route_slot = torch.empty(max(R, 1), **i32), torch.empty(max(R, 1), **i32)
-        slot_weight = torch.empty(max(R, 1), dtype=torch.float32, device=dev)
-        dropped_token, dropped_expert = torch.empty(max(R, 1), **i32), torch.empty(max(R, 1), **i32)
-        totals = torch.zeros(2, **i32)
-        balance = torch.zeros((), dtype=torch.float32, device=dev)
-        out = torch.empty_like(flat)
-        lib = _lib.load()
-        s = _hip.stream(dev)
-        if T:
-            logits = torch.empty(T, E, dtype=torch.float32, device=dev)
-            nb = lib.qw_moe_route_workspace_bytes(T, D, E)
-            ws = _hip.workspace(nb, dev)
-            _lib.call("qw_moe_route", _hip.ptr(flat), act, D, _hip.ptr(rw), _hip.act_code(rw, "router"), T, D, E, K,
-                      float(moe.router_temperature), _hip.ptr(bias), _hip.ptr(logits), _hip.ptr(probs),
-                      _hip.ptr(top_idx), _hip.ptr(top_w), _hip.ptr(ws), nb, s)
-            nb = lib.qw_moe_plan_workspace_bytes(T, K, E)
-            ws = _hip.workspace(nb, dev)
-            _lib.call("qw_moe_plan", _hip.ptr(top_idx), _hip.ptr(top_w), T, K, E, cap, _hip.ptr(counts),
-                      _hip.ptr(kept_counts), _hip.ptr(kept_offsets), _hip.ptr(slot_token), _hip.ptr(slot_weight),
-                      _hip.ptr(route_slot), _hip.ptr(dropped_token), _hip.ptr(dropped_expert), _hip.ptr(totals),
-                      _hip.ptr(ws), nb, s)
-            max_rows = min(R, cap * E)
-            y = torch.empty(R, D, dtype=flat.dtype, device=dev)
-            nb = lib.qw_moe_experts_workspace_bytes(max_rows, E, D, F_, act)
-            ws = _hip.workspace(nb, dev)
-            _lib.call("qw_moe_experts", _hip.ptr(flat), act, _hip.ptr(slot_token), _hip.ptr(kept_offsets), E, D, F_,
-                      max_rows, min(cap, R), *pack.args(), _hip.ptr(slot_weight), _hip.ptr(y), _hip.ptr(ws), nb, s)
-            _lib.call("qw_moe_combine", _hip.ptr(y), act, _hip.ptr(route_slot), _hip.ptr(top_idx), T, K, D,
-                      _hip.ptr(out), s)
-            importance = torch.empty(E, dtype=torch.float32, device=dev)
-            _lib.call("qw_moe_balance", _hip.ptr(probs), _hip.ptr(counts), T, K, E, _hip.ptr(importance),
-                      _hip.ptr(balance), s)
-        ctx.save_for_backward(flat, rw, probs, top_idx, top_w, counts, kept_offsets, slot_token, route_slot, totals)
-        ctx.moe, ctx.cap, ctx.router_dtype = moe, cap, router_w.dtype
-        ctx.mark_non_differentiable(top_idx, top_w, counts, kept_counts, totals, dropped_token, dropped_expert)
-        return out, probs, balance, top_idx, top_w, counts, kept_counts, totals, dropped_token, dropped_expert
+        r = _layer_chain(flat, cdt, router_w.detach(), moe, pack, cap, bias, save=flat.size(0) > 0)
+        saved = [r.get(n) for n in ("gate", "up", "hidden", "y_unweighted")]
+        ctx.save_for_backward(flat, _router_operand(router_w), r["probs"], r["top_idx"], r["top_w"], r["counts"],
+                              r["kept_offsets"], r["slot_token"], r["route_slot"], r["totals"], *saved)
+        ctx.moe, ctx.cap, ctx.cdt, ctx.router_dtype = moe, cap, cdt, router_w.dtype
+        ctx.mark_non_differentiable(r["top_idx"], r["top_w"], r["counts"], r["kept_counts"], r["totals"],
+                                    r["dropped_token"], r["dropped_expert"])
+        return (r["out"], r["probs"], r["balance"], r["top_idx"], r["top_w"], r["counts"], r["kept_counts"],
+                r["totals"], r["dropped_token"], r["dropped_expert"])
 
     @staticmethod
     def backward(ctx, d_out, d_probs, d_balance, *unused):
-        flat, rw, probs, top_idx, top_w, counts, kept_offsets, slot_token, route_slot, totals = ctx.saved_tensors
-        moe = ctx.moe
+        (flat, rw, probs, top_idx, top_w, counts, kept_offsets, slot_token, route_slot, totals, g, u, h,
+         y) = ctx.saved_tensors
+        moe, cdt = ctx.moe, ctx.cdt
         n_w = 3 * len(moe.experts)
         need_x, need_router = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        need_experts = any(ctx.needs_input_grad[6:6 + n_w])
+        need_experts = any(ctx.needs_input_grad[7:7 + n_w])
         T, D = flat.shape
         E, K = moe.num_experts, moe.top_k
         R = T * K
         dev = flat.device
         s = _hip.stream(dev)
-        act = _hip.act_code(flat, "TopKMoE.backward")
+        act_in = _hip.act_code(flat, "TopKMoE.backward")
+        act = _hip.act_code(torch.empty(0, dtype=cdt), "TopKMoE.backward")
         d_flat = None
         expert_grads = [None] * n_w
         d_top_w = torch.zeros(T, K, dtype=torch.float32, device=dev)
         if T and d_out is not None and (need_x or need_router or need_experts):
-            from .moe_kernels import _backward, _forward
+            from .moe_kernels import _backward
 
-            stacks = [torch.stack([getattr(e, n).weight.detach() for e in moe.experts]).to(flat.dtype).contiguous()
-                      for n in ("gate", "up", "down")]
-            plan = _RowPlan(kept_offsets, E, min(ctx.cap, R))
-            xp = torch.empty(R, D, dtype=flat.dtype, device=dev)
-            _lib.call("qw_moe_permute", _hip.ptr(flat), act, D, _hip.ptr(slot_token), _hip.ptr(totals), R,
-                      _hip.ptr(xp), s)
-            g = _forward(xp, stacks[0], plan, act)
-            u = _forward(xp, stacks[1], plan, act)
-            h = torch.empty_like(g)
-            _lib.call("qw_swiglu", _hip.ptr(g), _hip.ptr(u), act, g.numel(), _hip.ptr(h), s)
-            y = _forward(h, stacks[2], plan, act)
             d_out = d_out.contiguous().to(flat.dtype)
             dy = torch.empty_like(y)
-            _lib.call("qw_moe_combine_backward", _hip.ptr(d_out), act, _hip.ptr(y), act, _hip.ptr(route_slot),
+            _lib.call("qw_moe_combine_backward", _hip.ptr(d_out), act_in, _hip.ptr(y), act, _hip.ptr(route_slot),
                       _hip.ptr(top_w), T, K, D, _hip.ptr(dy), _hip.ptr(d_top_w), s)
             if need_x or need_experts:
+                stacks = [torch.stack([getattr(e, n).weight.detach() for e in moe.experts]).to(cdt).contiguous()
+                          for n in ("gate", "up", "down")]
+                plan = _RowPlan(kept_offsets, E, min(ctx.cap, R))
+                xp = torch.empty(R, D, dtype=cdt, device=dev)
+                _lib.call("qw_moe_permute", _hip.ptr(flat.to(cdt)), act, D, _hip.ptr(slot_token), _hip.ptr(totals), R,
+                          _hip.ptr(xp), s)
                 dh, d_down = _backward(dy, h, stacks[2], plan, act, True, need_experts)
                 dg, du = torch.empty_like(g), torch.empty_like(u)
                 _lib.call("qw_swiglu_backward", _hip.ptr(dh), _hip.ptr(g), _hip.ptr(u), act, g.numel(), _hip.ptr(dg),
@@ -465,13 +521,14 @@ class _MoELayer(torch.autograd.Function):
                 dxp, d_gate = _backward(dg, xp, stacks[0], plan, act, need_x, need_experts)
                 dxp, d_up = _backward(du, xp, stacks[1], plan, act, need_x, need_experts, grad_x=dxp)
                 if need_experts:
-                    for i, e in enumerate(moe.experts):
-                        for j, (n, gw) in enumerate((("gate", d_gate), ("up", d_up), ("down", d_down))):
-                            expert_grads[3 * i + j] = gw[i].to(getattr(e, n).weight.dtype)
+                    for j, (n, gw) in enumerate((("gate", d_gate), ("up", d_up), ("down", d_down))):
+                        per = gw.to(getattr(moe.experts[0], n).weight.dtype).unbind(0)
+                        for i in range(len(moe.experts)):
+                            expert_grads[3 * i + j] = per[i]
                 if need_x:
                     d_flat = torch.empty_like(flat)
                     _lib.call("qw_moe_combine_weighted", _hip.ptr(dxp), act, _hip.ptr(route_slot), _hip.ptr(top_idx),
-                              None, T, K, D, _hip.ptr(d_flat), act, s)
+                              None, T, K, D, _hip.ptr(d_flat), act_in, s)
         d_router = None
         if T and (need_x or need_router) and (d_out is not None or d_probs is not None or d_balance is not None):
             d_scores = torch.empty(T, E, dtype=torch.float32, device=dev)
@@ -485,7 +542,7 @@ class _MoELayer(torch.autograd.Function):
             if need_x:
                 dx_router = (d_scores @ rw.float()).to(flat.dtype)
                 d_flat = dx_router if d_flat is None else d_flat + dx_router
-        return (d_flat, d_router, None, None, None, None, *expert_grads)
+        return (d_flat, d_router, None, None, None, None, None, *expert_grads)
 
 
 class _RowPlan:

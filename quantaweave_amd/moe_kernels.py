@@ -205,14 +205,9 @@ def grouped_swiglu(inputs: Tensor, experts: nn.ModuleList, counts: Sequence[int]
     x = inputs.detach().to(dtype).contiguous()
     act = _hip.act_code(x, "grouped_swiglu")
     pack = packed_experts(experts, experts)
-    args = pack.args()
-    if pack.fmt in (_lib.QW_F32, _lib.QW_BF16) and pack.fmt != act:
-        # the reference casts the stacked weights to the compute dtype (src/moe_kernels.py:191-193)
-        cast = getattr(pack, "_cast", None)
-        if cast is None or cast[0] != dtype:
-            cast = (dtype, pack.gate.to(dtype), pack.up.to(dtype), pack.down.to(dtype))
-            pack._cast = cast
-        args = [act, 0, 0, _hip.ptr(cast[1]), None, _hip.ptr(cast[2]), None, _hip.ptr(cast[3]), None]
+    # the reference casts the stacked weights to the compute dtype (src/moe_kernels.py:191-193);
+    # bf16 weights under fp32 activations are widened exactly inside the kernels
+    args = pack.args_for(act)
     d_ff = pack.gate.size(1)
     d_model = x.size(1)
     out = torch.empty(plan.rows, d_model, dtype=dtype, device=x.device)
@@ -227,26 +222,43 @@ def grouped_swiglu(inputs: Tensor, experts: nn.ModuleList, counts: Sequence[int]
 
 def benchmark(experts: int = 32, tokens: int = 8192, hidden: int = 256, ffn: int = 512, top_k: int = 2, repeats: int = 20,
               bf16: bool = False) -> dict:
-    """Wall-clock the HIP MoE layer forward on the current GPU (src/moe_kernels.py:198-227).
+    """Wall-clock forward + backward of the HIP MoE layer on the current GPU,
+    optionally under bf16 autocast (src/moe_kernels.py:198-227).
 
-    The reference times forward+backward of its loop and Triton paths; this
-    build is forward-only, so it reports the forward time of the HIP path."""
+    The reference times its per-expert loop and its Triton executor; this
+    build has one executor, reported as ``hip_ms`` (forward + backward, the
+    reference's measurement), with ``forward_ms`` the forward alone under
+    no_grad."""
     from .moe import QuantaWeaveConfig, TopKMoE
 
     if not kernels_available(torch.device("cuda")):
         raise RuntimeError("benchmark needs a ROCm device and the built HIP library")
     config = QuantaWeaveConfig(vocab_size=8, hidden_size=hidden, layers=1, ffn_size=ffn, num_experts=experts, top_k=top_k,
                                attention_heads=1, max_sequence_length=tokens, capacity_factor=0)
-    dtype = torch.bfloat16 if bf16 else torch.float32
-    moe = TopKMoE(config).to("cuda", dtype)
-    x = torch.randn(1, tokens, hidden, device="cuda", dtype=dtype)
-    with torch.no_grad():
-        for _ in range(3):
+    moe = TopKMoE(config).cuda()
+    x = torch.randn(1, tokens, hidden, device="cuda", requires_grad=True)
+
+    def context():
+        return torch.autocast("cuda", dtype=torch.bfloat16) if bf16 else torch.autocast("cuda", enabled=False)
+
+    def train_step():
+        with context():
+            out = moe(x)[0]
+        out.float().sum().backward()
+
+    def forward():
+        with torch.no_grad(), context():
             moe(x)
+
+    result = {}
+    for name, fn in (("hip", train_step), ("forward", forward)):
+        for _ in range(3):
+            fn()
         torch.cuda.synchronize()
         started = time.perf_counter()
         for _ in range(repeats):
-            moe(x)
+            fn()
         torch.cuda.synchronize()
-    ms = (time.perf_counter() - started) / repeats * 1000
-    return dict(hip_ms=ms, experts=experts, tokens=tokens, hidden=hidden, ffn=ffn, top_k=top_k, bf16=bf16)
+        result[name + "_ms"] = (time.perf_counter() - started) / repeats * 1000
+    result.update(experts=experts, tokens=tokens, hidden=hidden, ffn=ffn, top_k=top_k, bf16=bf16)
+    return result

@@ -235,3 +235,34 @@ def test_training_steps_reduce_the_loss():
         opt.step()
         losses.append(loss.item())
     assert losses[-1] < losses[0]
+
+
+def test_layer_under_bf16_autocast():
+    """Experts in bf16 on an fp32 stream: routing on the fp32 input, expert rows
+    in bf16, (y * w) added in fp32 (src/quantweave_moe_model.py:126-127, :201;
+    src/moe_kernels.py:179-195); forward equal with and without autograd."""
+    print("case layer autocast", flush=True)
+    moe = make_moe(16, 128, 256, 2, 1.25, seed=11)
+    x = torch.randn(2, 64, 128, device="cuda", requires_grad=True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out, balance, *_ = moe(x)
+    assert out.dtype == torch.float32
+    (out.square().sum() + balance).backward()
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        infer = moe(x)[0]
+    assert torch.equal(infer, out.detach())
+    ref, probs, bal, xr, rw, ws, _ = layer_reference(moe, x)
+    (ref.square().sum() + bal).backward()
+    assert normwise(out, ref) <= 2e-2
+    assert x.grad.dtype == torch.float32
+    for got, want in ((x.grad, xr.grad), (moe.router.weight.grad, rw.grad),
+                      (torch.stack([e.down.weight.grad for e in moe.experts]), ws[2].grad)):
+        assert normwise(got, want) <= 3e-2
+
+
+def test_kernel_benchmark_reports_forward_and_backward():
+    # tests/test_moe_kernels.py:113-116
+    result = mk.benchmark(experts=16, tokens=2048, hidden=64, ffn=128, repeats=3)
+    assert result["hip_ms"] > 0 and result["forward_ms"] > 0
+    result = mk.benchmark(experts=16, tokens=2048, hidden=64, ffn=128, repeats=2, bf16=True)
+    assert result["hip_ms"] > 0 and result["bf16"]
