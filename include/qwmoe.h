@@ -225,10 +225,12 @@ int qw_pack_bf16_tiles(const void* w, int64_t experts, int64_t out_features, int
  * (QW_I8 / QW_U4 with fp32 scales and group size `group`, as
  * QuantizedLinear.forward, src/quantization.py:71-72); x and out have
  * act_dtype (QW_F32 or QW_BF16); fp32 accumulation, quantised weights rounded
- * to act_dtype before the multiply. */
+ * to act_dtype before the multiply.  max_rows_per_expert bounds every
+ * expert's row count (0: rows); bf16 with plain bf16 weights and
+ * in_features % 64 == 0 runs on the matrix cores. */
 int qw_grouped_matmul(const void* x, int act_dtype, const void* w, int w_format, const float* scales, int64_t group,
                       int64_t experts, int64_t out_features, int64_t in_features, const int32_t* offsets,
-                      int64_t rows, void* out, void* stream);
+                      int64_t rows, int64_t max_rows_per_expert, void* out, void* stream);
 
 /* ------------------------------------------------------------------------
  * Training: the backward pass of the grouped expert matmuls and of the MoE
@@ -243,11 +245,17 @@ int qw_grouped_matmul(const void* x, int act_dtype, const void* w, int w_format,
  * grad_out [rows, out_features], x [rows, in_features], w [E, out, in], all of
  * `dtype` (QW_F32 or QW_BF16).  grad_x or grad_w may be NULL (not computed).
  * accumulate_grad_x != 0 adds to grad_x instead of overwriting it.
- * max_rows_per_expert bounds every expert's row count (0: `rows`). */
+ * max_rows_per_expert bounds every expert's row count (0: `rows`).
+ * bf16 with a workspace of qw_grouped_matmul_backward_workspace_bytes runs on
+ * the matrix cores (grad_x when out_features % 64 == 0; grad_w always): the
+ * weights and the row blocks are transposed into the workspace first.  fp32,
+ * or no workspace, runs the vector-ALU kernels. */
+size_t qw_grouped_matmul_backward_workspace_bytes(int64_t experts, int64_t out_features, int64_t in_features,
+                                                  int64_t rows, int dtype);
 int qw_grouped_matmul_backward(const void* grad_out, const void* x, const void* w, int dtype, int64_t experts,
                                int64_t out_features, int64_t in_features, const int32_t* offsets, int64_t rows,
                                int64_t max_rows_per_expert, void* grad_x, int accumulate_grad_x, void* grad_w,
-                               void* stream);
+                               void* workspace, size_t workspace_bytes, void* stream);
 
 /* qw_moe_experts that also keeps what its backward needs, for training
  * (the activations autograd saves for SparseSwiGLU.forward,

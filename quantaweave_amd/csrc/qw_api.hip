@@ -62,7 +62,11 @@ int combine_weighted(const void* y, int dtype, const int32_t* route_slot, const 
                      int64_t T, int64_t K, int64_t D, void* out, int out_dtype, hipStream_t stream);
 int grouped_matmul_backward(const void* gy, const void* x, const void* w, int dtype, int64_t E, int64_t N, int64_t K,
                             const int32_t* offsets, int64_t rows, int64_t max_rows_per_expert, void* gx, int accumulate,
-                            void* gw, hipStream_t stream);
+                            void* gw, void* ws, size_t ws_bytes, hipStream_t stream);
+size_t grouped_backward_workspace_bytes(int64_t E, int64_t N, int64_t K, int64_t rows, int dtype);
+bool gemm_rows_fits(int64_t K, int64_t rows, int64_t E);
+int gemm_grouped_forward(const void* x, const void* w, int64_t E, int64_t N, int64_t K, const int32_t* offsets,
+                         int64_t rows, int64_t rows_per_expert, void* out, hipStream_t stream);
 int swiglu(const void* g, const void* u, int dtype, int64_t n, void* h, hipStream_t stream);
 int swiglu_backward(const void* dh, const void* g, const void* u, int dtype, int64_t n, void* dg, void* du,
                     hipStream_t stream);
@@ -459,7 +463,7 @@ int qw_pack_bf16_tiles(const void* w, int64_t experts, int64_t out_features, int
 
 int qw_grouped_matmul(const void* x, int act_dtype, const void* w, int w_format, const float* scales, int64_t group,
                       int64_t experts, int64_t out_features, int64_t in_features, const int32_t* offsets,
-                      int64_t rows, void* out, void* stream) {
+                      int64_t rows, int64_t max_rows_per_expert, void* out, void* stream) {
   clear_error();
   QW_REQUIRE(act_dtype == QW_F32 || act_dtype == QW_BF16, "grouped_matmul dtype must be f32 or bf16");
   QW_REQUIRE(w_format >= QW_F32 && w_format <= QW_BF16T, "unknown weight format %d", w_format);
@@ -472,8 +476,13 @@ int qw_grouped_matmul(const void* x, int act_dtype, const void* w, int w_format,
     QW_REQUIRE(group >= 1 && (w_format == QW_I8 || group % 2 == 0), "bad group size for quantised weights");
     QW_REQUIRE(scales != nullptr, "quantised weights need scales");
   }
+  QW_REQUIRE(max_rows_per_expert >= 0, "max_rows_per_expert must be >= 0");
   if (rows == 0) return QW_OK;
   QW_REQUIRE(x && w && offsets && out, "grouped_matmul pointers are required");
+  const int64_t per = max_rows_per_expert > 0 && max_rows_per_expert < rows ? max_rows_per_expert : rows;
+  if (act_dtype == QW_BF16 && w_format == QW_BF16 && gemm_rows_fits(in_features, rows, experts) &&
+      ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out)) & 15) == 0)
+    return gemm_grouped_forward(x, w, experts, out_features, in_features, offsets, rows, per, out, as_stream(stream));
   const WView v = make_wview(w_format, w, scales, out_features, in_features, group);
   return grouped_matmul_generic(x, act_dtype, v, w_format, experts, offsets, rows, out, as_stream(stream));
 }
@@ -504,13 +513,20 @@ int qw_moe_combine_weighted(const void* y, int y_dtype, const int32_t* route_slo
                           as_stream(stream));
 }
 
+size_t qw_grouped_matmul_backward_workspace_bytes(int64_t experts, int64_t out_features, int64_t in_features,
+                                                  int64_t rows, int dtype) {
+  if (experts < 1 || out_features < 1 || in_features < 1 || rows < 0) return 0;
+  return grouped_backward_workspace_bytes(experts, out_features, in_features, rows, dtype);
+}
+
 int qw_grouped_matmul_backward(const void* grad_out, const void* x, const void* w, int dtype, int64_t experts,
                                int64_t out_features, int64_t in_features, const int32_t* offsets, int64_t rows,
                                int64_t max_rows_per_expert, void* grad_x, int accumulate_grad_x, void* grad_w,
-                               void* stream) {
+                               void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   return grouped_matmul_backward(grad_out, x, w, dtype, experts, out_features, in_features, offsets, rows,
-                                 max_rows_per_expert, grad_x, accumulate_grad_x, grad_w, as_stream(stream));
+                                 max_rows_per_expert, grad_x, accumulate_grad_x, grad_w, workspace, workspace_bytes,
+                                 as_stream(stream));
 }
 
 int qw_swiglu(const void* gate, const void* up, int dtype, int64_t n, void* hidden, void* stream) {

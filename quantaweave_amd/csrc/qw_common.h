@@ -149,6 +149,40 @@ __device__ __forceinline__ void store_vec(void* p, int64_t i, const float (&v)[V
   }
 }
 
+// Tile t of a grid laid over the row blocks of E groups, group e holding rows
+// [offsets[e], offsets[e+1]) clamped to [0, rows), in tiles of `gran` rows:
+// returns the group (or -1 when t is past the last tile) and sets *local to the
+// tile's index within it.  Every lane of the wave computes the same answer
+// (wave prefix sums over 64 groups at a time), so a grid of
+// ceil(rows / gran) + E tiles covers any distribution of rows.
+__device__ __forceinline__ int find_tile(const int32_t* __restrict__ offsets, int E, int rows, int gran, int t,
+                                         int* local) {
+  const int lane = threadIdx.x % kWave;
+  int carry = 0;
+  for (int e0 = 0; e0 < E; e0 += kWave) {
+    const int e = e0 + lane;
+    int n = 0;
+    if (e < E) {
+      const int lo = min(max(offsets[e], 0), rows), hi = min(offsets[e + 1], rows);
+      n = hi > lo ? (hi - lo + gran - 1) / gran : 0;
+    }
+    int incl = n;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int v = __shfl_up(incl, o, kWave);
+      if (lane >= o) incl += v;
+    }
+    const unsigned long long hit = __ballot(carry + incl > t);
+    if (hit) {
+      const int l = __ffsll(static_cast<long long>(hit)) - 1;
+      *local = t - carry - __shfl(incl - n, l, kWave);
+      return e0 + l;
+    }
+    carry += __shfl(incl, kWave - 1, kWave);
+  }
+  return -1;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));

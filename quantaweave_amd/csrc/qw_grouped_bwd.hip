@@ -10,9 +10,12 @@
 // receives grad_x + result (one rounding), which sums the gate and up
 // projections' input gradients of a SwiGLU expert in place.
 //
-// Both kernels compute a 64x64 output tile per 256-thread block (4x4 per
-// thread) from 16-deep slices of the reduction staged in LDS; the reduction
-// runs in ascending order, so results do not depend on scheduling.
+// bf16 with a workspace runs on the matrix cores (gemm_grouped_backward,
+// qw_gemm_mfma.hip).  Otherwise (fp32, or shapes the matrix-core path does not
+// take) two vector-ALU kernels compute a 64x64 output tile per 256-thread
+// block (4x4 per thread) from 16-deep slices of the reduction staged in LDS;
+// the reduction runs in ascending order, so results do not depend on
+// scheduling.
 #include "qw_common.h"
 
 namespace qw {
@@ -125,19 +128,44 @@ __global__ __launch_bounds__(256) void grouped_dw_kernel(const void* __restrict_
 
 }  // namespace
 
+size_t gemm_backward_workspace_bytes(int64_t E, int64_t N, int64_t K, int64_t rows);
+bool gemm_backward_fits(int64_t rows, int64_t E);
+int gemm_grouped_backward(const void* gy, const void* x, const void* w, int64_t E, int64_t N, int64_t K,
+                          const int32_t* offsets, int64_t rows, int64_t rows_per_expert, void* gx, int accumulate,
+                          void* gw, void* ws, size_t ws_bytes, hipStream_t stream);
+
+size_t grouped_backward_workspace_bytes(int64_t E, int64_t N, int64_t K, int64_t rows, int dtype) {
+  return dtype == QW_BF16 ? gemm_backward_workspace_bytes(E, N, K, rows) : 256;
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 int grouped_matmul_backward(const void* gy, const void* x, const void* w, int dtype, int64_t E, int64_t N, int64_t K,
                             const int32_t* offsets, int64_t rows, int64_t max_rows_per_expert, void* gx, int accumulate,
-                            void* gw, hipStream_t stream) {
+                            void* gw, void* ws, size_t ws_bytes, hipStream_t stream) {
   QW_REQUIRE(dtype == QW_F32 || dtype == QW_BF16, "grouped backward dtype must be f32 or bf16");
   QW_REQUIRE(E >= 1 && E <= 65535 && N >= 1 && K >= 1 && N <= INT32_MAX && K <= INT32_MAX && rows >= 0 &&
                  rows <= INT32_MAX && max_rows_per_expert >= 0,
              "bad grouped backward sizes");
   QW_REQUIRE(offsets != nullptr, "offsets are required");
+  if (gx != nullptr && rows > 0) QW_REQUIRE(gy && w, "grad_x needs grad_out and w");
+  if (gw != nullptr) QW_REQUIRE(rows == 0 || (gy && x), "grad_w needs grad_out and x");
+  const int64_t per = max_rows_per_expert > 0 && max_rows_per_expert < rows ? max_rows_per_expert : rows;
+  QW_REQUIRE(ceil_div(per, BT) <= 65535 && ceil_div(N, BT) <= 65535, "grouped backward sizes out of range");
+  // matrix-core path (bf16 with a workspace): dX needs out_features % 64 == 0, dW any shape
+  const bool core = dtype == QW_BF16 && ws != nullptr && ws_bytes >= gemm_backward_workspace_bytes(E, N, K, rows) &&
+                    aligned16(gy) && aligned16(x) && aligned16(w) && gemm_backward_fits(rows, E);
+  const bool core_dx = core && gx != nullptr && aligned16(gx) && N % 64 == 0 && K % 4 == 0;
+  const bool core_dw = core && gw != nullptr && aligned16(gw);
+  if (core_dx || core_dw) {
+    const int st = gemm_grouped_backward(gy, x, w, E, N, K, offsets, rows, per, core_dx ? gx : nullptr, accumulate,
+                                         core_dw ? gw : nullptr, ws, ws_bytes, stream);
+    if (st) return st;
+    if (core_dx) gx = nullptr;
+    if (core_dw) gw = nullptr;
+  }
   const int n = static_cast<int>(N), k = static_cast<int>(K), r = static_cast<int>(rows);
   if (gx != nullptr && rows > 0) {
-    QW_REQUIRE(gy && w, "grad_x needs grad_out and w");
-    const int64_t per = max_rows_per_expert > 0 && max_rows_per_expert < rows ? max_rows_per_expert : rows;
-    QW_REQUIRE(ceil_div(per, BT) <= 65535, "too many rows per expert");
     const dim3 g(static_cast<unsigned>(ceil_div(K, BT)), static_cast<unsigned>(ceil_div(per, BT)),
                  static_cast<unsigned>(E));
     if (dtype == QW_F32) grouped_dx_kernel<QW_F32><<<g, 256, 0, stream>>>(gy, w, offsets, n, k, r, accumulate, gx);
@@ -145,8 +173,6 @@ int grouped_matmul_backward(const void* gy, const void* x, const void* w, int dt
     QW_LAUNCH_CHECK("grouped_dx_kernel");
   }
   if (gw != nullptr) {
-    QW_REQUIRE(rows == 0 || (gy && x), "grad_w needs grad_out and x");
-    QW_REQUIRE(ceil_div(N, BT) <= 65535, "too many output features");
     const dim3 g(static_cast<unsigned>(ceil_div(K, BT)), static_cast<unsigned>(ceil_div(N, BT)),
                  static_cast<unsigned>(E));
     if (dtype == QW_F32) grouped_dw_kernel<QW_F32><<<g, 256, 0, stream>>>(gy, x, offsets, n, k, r, gw);

@@ -172,6 +172,17 @@ class ExpertPack:
         return [self.fmt, self.group_in, self.group_ff, _hip.ptr(self.gate), _hip.ptr(self.gate_s),
                 _hip.ptr(self.up), _hip.ptr(self.up_s), _hip.ptr(self.down), _hip.ptr(self.down_s)]
 
+    def plain(self, experts: nn.ModuleList, dtype: torch.dtype) -> list:
+        """[gate, up, down] stacks [E, out, in] in `dtype`, untiled, for the
+        backward kernels; made once per weight version."""
+        cache = getattr(self, "_plain", None)
+        if cache is None or cache[0] != dtype:
+            stacks = [torch.stack([getattr(e, n).weight.detach() for e in experts]).to(dtype).contiguous()
+                      for n in ("gate", "up", "down")]
+            cache = (dtype, stacks)
+            self._plain = cache
+        return cache[1]
+
     def args_for(self, act: int) -> list:
         """Weight arguments for activations of dtype code `act`: fp32 experts
         multiplied in bf16 use bf16 copies (tiled where the shapes allow),
@@ -476,7 +487,7 @@ class _MoELayer(torch.autograd.Function):
         saved = [r.get(n) for n in ("gate", "up", "hidden", "y_unweighted")]
         ctx.save_for_backward(flat, _router_operand(router_w), r["probs"], r["top_idx"], r["top_w"], r["counts"],
                               r["kept_offsets"], r["slot_token"], r["route_slot"], r["totals"], *saved)
-        ctx.moe, ctx.cap, ctx.cdt, ctx.router_dtype = moe, cap, cdt, router_w.dtype
+        ctx.moe, ctx.pack, ctx.cap, ctx.cdt, ctx.router_dtype = moe, pack, cap, cdt, router_w.dtype
         ctx.mark_non_differentiable(r["top_idx"], r["top_w"], r["counts"], r["kept_counts"], r["totals"],
                                     r["dropped_token"], r["dropped_expert"])
         return (r["out"], r["probs"], r["balance"], r["top_idx"], r["top_w"], r["counts"], r["kept_counts"],
@@ -508,8 +519,7 @@ class _MoELayer(torch.autograd.Function):
             _lib.call("qw_moe_combine_backward", _hip.ptr(d_out), act_in, _hip.ptr(y), act, _hip.ptr(route_slot),
                       _hip.ptr(top_w), T, K, D, _hip.ptr(dy), _hip.ptr(d_top_w), s)
             if need_x or need_experts:
-                stacks = [torch.stack([getattr(e, n).weight.detach() for e in moe.experts]).to(cdt).contiguous()
-                          for n in ("gate", "up", "down")]
+                stacks = ctx.pack.plain(moe.experts, cdt)
                 plan = _RowPlan(kept_offsets, E, min(ctx.cap, R))
                 xp = torch.empty(R, D, dtype=cdt, device=dev)
                 _lib.call("qw_moe_permute", _hip.ptr(flat.to(cdt)), act, D, _hip.ptr(slot_token), _hip.ptr(totals), R,

@@ -85,7 +85,7 @@ def _forward(x: Tensor, w: Tensor, plan: GroupedPlan, act: int) -> Tensor:
     out = torch.empty(x.size(0), w.size(1), dtype=x.dtype, device=x.device)
     if x.size(0):
         _lib.call("qw_grouped_matmul", _hip.ptr(x), act, _hip.ptr(w), act, None, 0, w.size(0), w.size(1), w.size(2),
-                  _hip.ptr(plan.offsets), x.size(0), _hip.ptr(out), _hip.stream(x.device))
+                  _hip.ptr(plan.offsets), x.size(0), plan.max_count, _hip.ptr(out), _hip.stream(x.device))
     return out
 
 
@@ -99,9 +99,11 @@ def _backward(grad: Tensor, x: Tensor, w: Tensor, plan: GroupedPlan, act: int, n
     if need_w:
         gw = torch.empty_like(w)
     if gx is not None or gw is not None:
+        nbytes = _lib.load().qw_grouped_matmul_backward_workspace_bytes(w.size(0), w.size(1), w.size(2), x.size(0), act)
+        ws = _hip.workspace(nbytes, x.device)
         _lib.call("qw_grouped_matmul_backward", _hip.ptr(grad), _hip.ptr(x), _hip.ptr(w), act, w.size(0), w.size(1),
                   w.size(2), _hip.ptr(plan.offsets), x.size(0), plan.max_count, _hip.ptr(gx), int(accumulate),
-                  _hip.ptr(gw), _hip.stream(x.device))
+                  _hip.ptr(gw), _hip.ptr(ws), nbytes, _hip.stream(x.device))
     return gx, gw
 
 

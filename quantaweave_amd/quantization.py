@@ -93,7 +93,7 @@ class QuantizedLinear(nn.Module):
             scales = self.scales if self.scales.dtype == torch.float32 else self.scales.float()
             _lib.call("qw_grouped_matmul", _hip.ptr(flat), act, _hip.ptr(self.qweight), self.w_format,
                       _hip.ptr(scales.contiguous()), self.group_size, 1, self.out_features, self.in_features,
-                      _hip.ptr(offsets), rows, _hip.ptr(out), _hip.stream(x.device))
+                      _hip.ptr(offsets), rows, 0, _hip.ptr(out), _hip.stream(x.device))
         return out.reshape(*lead, self.out_features)
 
     def stored_bytes(self) -> int:

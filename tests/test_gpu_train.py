@@ -266,3 +266,30 @@ def test_kernel_benchmark_reports_forward_and_backward():
     assert result["hip_ms"] > 0 and result["forward_ms"] > 0
     result = mk.benchmark(experts=16, tokens=2048, hidden=64, ffn=128, repeats=2, bf16=True)
     assert result["hip_ms"] > 0 and result["bf16"]
+
+
+@pytest.mark.parametrize("counts,in_features,out_features", [
+    ([0, 5, 300, 1, 0, 129, 64, 2], 128, 192),     # matrix cores for dX (192 % 64 == 0) and dW
+    ([7, 0, 200, 33], 320, 96),                    # dX on the vector ALUs (96 % 64 != 0), dW on the matrix cores
+    ([1000, 24], 64, 2048),                        # many row tiles, many column tiles
+])
+def test_grouped_matmul_bf16_matrix_core_paths(counts, in_features, out_features):
+    print(f"case grouped_matmul bf16 {counts} {in_features}x{out_features}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(sum(counts))
+    x = torch.randn(sum(counts), in_features, device="cuda", generator=g).bfloat16().requires_grad_()
+    weight = (torch.randn(len(counts), out_features, in_features, device="cuda", generator=g) * 0.1).bfloat16()
+    weight.requires_grad_()
+    y = mk.grouped_matmul(x, weight, mk.GroupedPlan(counts, x.device))
+    upstream = torch.randn(y.shape, device="cuda", generator=g).bfloat16()
+    y.backward(upstream)
+    xr, wr = cpu64(x).requires_grad_(), cpu64(weight).requires_grad_()
+    ref = tr.grouped_matmul(xr, wr, counts)
+    ref.backward(cpu64(upstream))
+    assert normwise(y, ref) <= 1e-2
+    assert normwise(x.grad, xr.grad) <= 1e-2
+    assert normwise(weight.grad, wr.grad) <= 1e-2
+    for e, c in enumerate(counts):
+        if c == 0:
+            assert (weight.grad[e] == 0).all()
+        else:  # every expert's gradient block is its own (no cross-expert mixing)
+            assert normwise(weight.grad[e], wr.grad[e]) <= 1e-2
