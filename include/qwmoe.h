@@ -244,6 +244,8 @@ int qw_grouped_matmul(const void* x, int act_dtype, const void* w, int w_format,
  *   grad_w[e]   = grad_out[rows of e]^T @ x[rows of e]   (exactly 0 without rows)
  * grad_out [rows, out_features], x [rows, in_features], w [E, out, in], all of
  * `dtype` (QW_F32 or QW_BF16).  grad_x or grad_w may be NULL (not computed).
+ * grad_w has grad_w_dtype: `dtype`, or QW_F32 for fp32 parameters multiplied
+ * in bf16 (the gradient is then not rounded to bf16).
  * accumulate_grad_x != 0 adds to grad_x instead of overwriting it.
  * max_rows_per_expert bounds every expert's row count (0: `rows`).
  * bf16 with a workspace of qw_grouped_matmul_backward_workspace_bytes runs on
@@ -255,7 +257,7 @@ size_t qw_grouped_matmul_backward_workspace_bytes(int64_t experts, int64_t out_f
 int qw_grouped_matmul_backward(const void* grad_out, const void* x, const void* w, int dtype, int64_t experts,
                                int64_t out_features, int64_t in_features, const int32_t* offsets, int64_t rows,
                                int64_t max_rows_per_expert, void* grad_x, int accumulate_grad_x, void* grad_w,
-                               void* workspace, size_t workspace_bytes, void* stream);
+                               int grad_w_dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /* qw_moe_experts that also keeps what its backward needs, for training
  * (the activations autograd saves for SparseSwiGLU.forward,

@@ -45,7 +45,7 @@ SIGNATURES = {
     "qw_pack_bf16_tiles": (I32, [P, I64, I64, I64, P, P]),
     "qw_grouped_matmul": (I32, [P, I32, P, I32, P, I64, I64, I64, I64, P, I64, I64, P, P]),
     "qw_grouped_matmul_backward_workspace_bytes": (SZ, [I64, I64, I64, I64, I32]),
-    "qw_grouped_matmul_backward": (I32, [P, P, P, I32, I64, I64, I64, P, I64, I64, P, I32, P, P, SZ, P]),
+    "qw_grouped_matmul_backward": (I32, [P, P, P, I32, I64, I64, I64, P, I64, I64, P, I32, P, I32, P, SZ, P]),
     "qw_moe_experts_save": (I32, [P, I32, P, P, I64, I64, I64, I64, I64, I32, I64, I64, P, P, P, P, P, P, P, P,
                                   P, P, P, P, P, SZ, P]),
     "qw_swiglu": (I32, [P, P, I32, I64, P, P]),

@@ -62,7 +62,7 @@ int combine_weighted(const void* y, int dtype, const int32_t* route_slot, const 
                      int64_t T, int64_t K, int64_t D, void* out, int out_dtype, hipStream_t stream);
 int grouped_matmul_backward(const void* gy, const void* x, const void* w, int dtype, int64_t E, int64_t N, int64_t K,
                             const int32_t* offsets, int64_t rows, int64_t max_rows_per_expert, void* gx, int accumulate,
-                            void* gw, void* ws, size_t ws_bytes, hipStream_t stream);
+                            void* gw, int gw_dtype, void* ws, size_t ws_bytes, hipStream_t stream);
 size_t grouped_backward_workspace_bytes(int64_t E, int64_t N, int64_t K, int64_t rows, int dtype);
 bool gemm_rows_fits(int64_t K, int64_t rows, int64_t E);
 int gemm_grouped_forward(const void* x, const void* w, int64_t E, int64_t N, int64_t K, const int32_t* offsets,
@@ -522,11 +522,11 @@ size_t qw_grouped_matmul_backward_workspace_bytes(int64_t experts, int64_t out_f
 int qw_grouped_matmul_backward(const void* grad_out, const void* x, const void* w, int dtype, int64_t experts,
                                int64_t out_features, int64_t in_features, const int32_t* offsets, int64_t rows,
                                int64_t max_rows_per_expert, void* grad_x, int accumulate_grad_x, void* grad_w,
-                               void* workspace, size_t workspace_bytes, void* stream) {
+                               int grad_w_dtype, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   return grouped_matmul_backward(grad_out, x, w, dtype, experts, out_features, in_features, offsets, rows,
-                                 max_rows_per_expert, grad_x, accumulate_grad_x, grad_w, workspace, workspace_bytes,
-                                 as_stream(stream));
+                                 max_rows_per_expert, grad_x, accumulate_grad_x, grad_w, grad_w_dtype, workspace,
+                                 workspace_bytes, as_stream(stream));
 }
 
 int qw_swiglu(const void* gate, const void* up, int dtype, int64_t n, void* hidden, void* stream) {

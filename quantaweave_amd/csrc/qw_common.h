@@ -155,12 +155,15 @@ __device__ __forceinline__ void store_vec(void* p, int64_t i, const float (&v)[V
 // tile's index within it.  Every lane of the wave computes the same answer
 // (wave prefix sums over 64 groups at a time), so a grid of
 // ceil(rows / gran) + E tiles covers any distribution of rows.
+// With stride > 1 only the groups start, start + stride, ... take part (the
+// groups one XCD owns); the returned index is the group's own.
 __device__ __forceinline__ int find_tile(const int32_t* __restrict__ offsets, int E, int rows, int gran, int t,
-                                         int* local) {
+                                         int* local, int start = 0, int stride = 1) {
   const int lane = threadIdx.x % kWave;
   int carry = 0;
-  for (int e0 = 0; e0 < E; e0 += kWave) {
-    const int e = e0 + lane;
+  const int groups = start < E ? (E - start + stride - 1) / stride : 0;
+  for (int i0 = 0; i0 < groups; i0 += kWave) {
+    const int e = start + stride * (i0 + lane);
     int n = 0;
     if (e < E) {
       const int lo = min(max(offsets[e], 0), rows), hi = min(offsets[e + 1], rows);
@@ -176,7 +179,7 @@ __device__ __forceinline__ int find_tile(const int32_t* __restrict__ offsets, in
     if (hit) {
       const int l = __ffsll(static_cast<long long>(hit)) - 1;
       *local = t - carry - __shfl(incl - n, l, kWave);
-      return e0 + l;
+      return start + stride * (i0 + l);
     }
     carry += __shfl(incl, kWave - 1, kWave);
   }

@@ -112,11 +112,20 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
   // ---- tile of this workgroup (XCD-aware enumeration) ----
   const int b = blockIdx.x;
   const int xcd = b % kXcds, j = b / kXcds;
-  const int per_expert = m_chunks * n_tiles;
-  const int e = xcd + kXcds * (j / per_expert);
-  if (e >= experts) return;
-  const int rem = j % per_expert;
-  const int mc = rem / n_tiles, nt = rem % n_tiles;
+  // XCD x takes the row chunks of experts x, x + 8, ..., each chunk's column
+  // tiles back to back.  m_chunks > 0: every expert has m_chunks chunk slots
+  // (the capacity bound is tight); m_chunks == 0: the chunks that hold rows
+  // are found on the device, so a loose bound (no capacity) costs no launches.
+  const int nt = j % n_tiles;
+  int mc = 0, e;
+  if (m_chunks > 0) {
+    e = xcd + kXcds * (j / n_tiles / m_chunks);
+    mc = (j / n_tiles) % m_chunks;
+    if (e >= experts) return;
+  } else {
+    e = find_tile(offsets, experts, max_rows, MCH, j / n_tiles, &mc, xcd, kXcds);
+    if (e < 0) return;
+  }
   const int e_lo = max(offsets[e], 0);
   const int r0 = e_lo + mc * MCH;
   const int r1 = min(min(offsets[e + 1], r0 + MCH), max_rows);
@@ -333,8 +342,14 @@ int launch_t(const void* x, const int32_t* row_index, const int32_t* offsets, in
              const void* wb, int64_t w_stride, int n_w, int K, const float* row_weight, void* out, int n_out,
              int experts, int64_t rows_cap, void* save_a, void* save_b, hipStream_t stream) {
   const int n_tiles = static_cast<int>(ceil_div(GATEUP ? n_w : n_out, GATEUP ? MF_NB / 2 : MF_NB));
-  const int m_chunks = static_cast<int>(ceil_div(rows_cap, 32 * SUBT));
-  const int64_t grid = static_cast<int64_t>(ceil_div(experts, kXcds)) * kXcds * m_chunks * n_tiles;
+  // chunks one XCD can own: its experts' chunks at the capacity bound, and at
+  // most all rows in chunks plus one partial chunk per expert
+  const int64_t per_xcd_experts = ceil_div(experts, kXcds);
+  const int64_t slots = per_xcd_experts * ceil_div(rows_cap, 32 * SUBT);
+  const int64_t found = ceil_div(max_rows, 32 * SUBT) + per_xcd_experts;
+  const int64_t chunks = std::min(slots, found);
+  const int m_chunks = slots <= found ? static_cast<int>(ceil_div(rows_cap, 32 * SUBT)) : 0;
+  const int64_t grid = static_cast<int64_t>(kXcds) * chunks * n_tiles;
   if (grid > INT32_MAX) return set_error(QW_ERR_UNSUPPORTED, "MFMA grid too large");
   const size_t lds = static_cast<size_t>(mf_stages(SUBT)) * (32 * SUBT * MF_ROWB + MF_NB * MF_ROWB);
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_mfma_kernel<GATEUP, SUBT, TILED>),

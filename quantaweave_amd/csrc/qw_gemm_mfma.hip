@@ -42,10 +42,10 @@ constexpr int G_XCDS = 8;                    // XCDs of the MI355X, workgroups d
 // quarter-wave reads at one logical piece land on 16 different bank groups.
 __device__ __forceinline__ int gswz(int row, int piece) { return piece ^ ((row >> 1) & 7); }
 
-template <int MODE, bool ACCUM, bool BRED>
+template <int MODE, bool ACCUM, bool BRED, bool C32>
 __global__ __launch_bounds__(256) void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda,
                                                       const uint16_t* __restrict__ B, int64_t ldb,
-                                                      int64_t b_expert_stride, uint16_t* __restrict__ C, int64_t ldc,
+                                                      int64_t b_expert_stride, void* __restrict__ C, int64_t ldc,
                                                       int64_t c_expert_stride, const int32_t* __restrict__ offsets,
                                                       int rows, int M, int N, int K, int E) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
@@ -58,7 +58,7 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(const uint16_t* __restrict
   int e, nt, m0, mcount, k_lo, k_len;
   const uint16_t* a_base;
   const uint16_t* b_base;
-  uint16_t* c_base;
+  int64_t c_off;  // element offset of the block's first output row
   if (MODE == MODE_ROWS) {  // row tiles of all experts, found on the device
     int local = 0;
     nt = j % n_nt;
@@ -72,7 +72,7 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(const uint16_t* __restrict
     k_len = K;
     a_base = A + static_cast<int64_t>(m0) * lda;
     b_base = B + static_cast<int64_t>(e) * b_expert_stride;
-    c_base = C + static_cast<int64_t>(m0) * ldc;
+    c_off = static_cast<int64_t>(m0) * ldc;
   } else {
     const int per_e = ((M + GT - 1) / GT) * n_nt;
     e = (j / per_e) * G_XCDS + xcd;
@@ -85,7 +85,7 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(const uint16_t* __restrict
     k_len = offsets[e + 1] - k_lo;
     a_base = A + static_cast<int64_t>(m0) * lda + k_lo;
     b_base = B + k_lo;
-    c_base = C + static_cast<int64_t>(e) * c_expert_stride + static_cast<int64_t>(m0) * ldc;
+    c_off = static_cast<int64_t>(e) * c_expert_stride + static_cast<int64_t>(m0) * ldc;
   }
   const int n0 = nt * GT;
   const int ncount = min(GT, N - n0);
@@ -215,17 +215,37 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(const uint16_t* __restrict
 #undef QW_LO2
 #undef QW_HI2
 
-  // lane holds C[m = 16 i + l16][n = 16 j + 4 lq + v] of its wave's quarter
+  // lane holds C[m = 16 i + l16][n = 16 j + 4 lq + v] of its wave's quarter;
+  // C32: fp32 output, else bf16
   const bool vec = (ldc & 3) == 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int m = wm * 64 + 16 * i + l16;
     if (m >= mcount) continue;
-    uint16_t* crow = c_base + static_cast<int64_t>(m) * ldc + n0;
+    const int64_t row = c_off + static_cast<int64_t>(m) * ldc + n0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int n = wn * 64 + 16 * j + 4 * lq;
       f32x4 v = acc[i][j];
+      if (C32) {
+        float* c = static_cast<float*>(C) + row;
+        if (vec && n + 3 < ncount) {
+          if (ACCUM) {
+            const float4 old = *reinterpret_cast<const float4*>(c + n);
+            v[0] += old.x;
+            v[1] += old.y;
+            v[2] += old.z;
+            v[3] += old.w;
+          }
+          *reinterpret_cast<float4*>(c + n) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            if (n + u < ncount) c[n + u] = v[u] + (ACCUM ? c[n + u] : 0.0f);
+        }
+        continue;
+      }
+      uint16_t* crow = static_cast<uint16_t*>(C) + row;
       if (vec && n + 3 < ncount) {
         if (ACCUM) {
           const uint2 old = *reinterpret_cast<const uint2*>(crow + n);
@@ -300,11 +320,11 @@ __global__ __launch_bounds__(256) void transpose_pad_kernel(const uint16_t* __re
   }
 }
 
-template <int MODE, bool ACCUM, bool BRED = false>
+template <int MODE, bool ACCUM, bool BRED = false, bool C32 = false>
 int launch_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t b_stride, void* C, int64_t ldc,
                 int64_t c_stride, const int32_t* offsets, int rows, int M, int N, int K, int E, int64_t m_extent,
                 hipStream_t stream) {
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_nt_kernel<MODE, ACCUM, BRED>),
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_nt_kernel<MODE, ACCUM, BRED, C32>),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, G_LDS);
   if (attr != hipSuccess) return set_error(QW_ERR_HIP, "cannot reserve LDS: %s", hipGetErrorString(attr));
   // one grid dimension: MODE_ROWS, the row tiles of all experts (at most
@@ -314,10 +334,9 @@ int launch_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t 
   const int64_t blocks = MODE == MODE_ROWS ? G_XCDS * n_nt * ceil_div(ceil_div(m_extent, GT) + E, G_XCDS)
                                            : G_XCDS * n_nt * ceil_div(m_extent, GT) * ceil_div(E, G_XCDS);
   if (blocks > INT32_MAX) return set_error(QW_ERR_UNSUPPORTED, "grouped GEMM grid too large");
-  gemm_nt_kernel<MODE, ACCUM, BRED><<<static_cast<unsigned>(blocks), 256, G_LDS, stream>>>(static_cast<const uint16_t*>(A), lda,
-                                                         static_cast<const uint16_t*>(B), ldb, b_stride,
-                                                         static_cast<uint16_t*>(C), ldc, c_stride, offsets, rows, M,
-                                                         N, K, E);
+  gemm_nt_kernel<MODE, ACCUM, BRED, C32><<<static_cast<unsigned>(blocks), 256, G_LDS, stream>>>(
+      static_cast<const uint16_t*>(A), lda, static_cast<const uint16_t*>(B), ldb, b_stride, C, ldc, c_stride, offsets,
+      rows, M, N, K, E);
   QW_LAUNCH_CHECK("gemm_nt_kernel");
   return QW_OK;
 }
@@ -352,10 +371,10 @@ int gemm_grouped_forward(const void* x, const void* w, int64_t E, int64_t N, int
 }
 
 // Backward of gemm_grouped_forward on the matrix cores (bf16):
-//   gx = gy . w[e] (+ gx when accumulate), gw[e] = gy_e^T . x_e.
+//   gx = gy . w[e] (+ gx when accumulate), gw[e] = gy_e^T . x_e (fp32 when gw_f32).
 int gemm_grouped_backward(const void* gy, const void* x, const void* w, int64_t E, int64_t N, int64_t K,
                           const int32_t* offsets, int64_t rows, int64_t rows_per_expert, void* gx, int accumulate,
-                          void* gw, void* ws, size_t ws_bytes, hipStream_t stream) {
+                          void* gw, int gw_f32, void* ws, size_t ws_bytes, hipStream_t stream) {
   const size_t need = gemm_backward_workspace_bytes(E, N, K, rows);
   if (!ws || ws_bytes < need)
     return set_error(QW_ERR_WORKSPACE, "grouped backward workspace needs %zu bytes, got %zu", need, ws_bytes);
@@ -385,7 +404,9 @@ int gemm_grouped_backward(const void* gy, const void* x, const void* w, int64_t 
       transpose_pad_kernel<<<g2, 256, 0, stream>>>(static_cast<const uint16_t*>(x), k, offsets, poff, e, r, rp, xt);
       QW_LAUNCH_CHECK("transpose_pad_kernel");
     }
-    return launch_gemm<MODE_RED, false>(gyt, rp, xt, rp, 0, gw, K, N * K, poff, r, n, k, 0, e, N, stream);
+    return gw_f32 ? launch_gemm<MODE_RED, false, false, true>(gyt, rp, xt, rp, 0, gw, K, N * K, poff, r, n, k, 0, e,
+                                                              N, stream)
+                  : launch_gemm<MODE_RED, false>(gyt, rp, xt, rp, 0, gw, K, N * K, poff, r, n, k, 0, e, N, stream);
   }
   return QW_OK;
 }

@@ -78,8 +78,8 @@ __global__ __launch_bounds__(256) void grouped_dx_kernel(const void* __restrict_
   }
 }
 
-// grad_W: block (k tile, n tile, expert)
-template <int DT>
+// grad_W: block (k tile, n tile, expert); ODT the output dtype
+template <int DT, int ODT>
 __global__ __launch_bounds__(256) void grouped_dw_kernel(const void* __restrict__ gy, const void* __restrict__ x,
                                                          const int32_t* __restrict__ offsets, int N, int K,
                                                          int rows, void* __restrict__ gw) {
@@ -121,7 +121,7 @@ __global__ __launch_bounds__(256) void grouped_dw_kernel(const void* __restrict_
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int k = k0 + tx * 4 + j;
-      if (k < K) store_act<DT>(gw, wbase + static_cast<int64_t>(n) * K + k, acc[i][j]);
+      if (k < K) store_act<ODT>(gw, wbase + static_cast<int64_t>(n) * K + k, acc[i][j]);
     }
   }
 }
@@ -132,7 +132,7 @@ size_t gemm_backward_workspace_bytes(int64_t E, int64_t N, int64_t K, int64_t ro
 bool gemm_backward_fits(int64_t rows, int64_t E);
 int gemm_grouped_backward(const void* gy, const void* x, const void* w, int64_t E, int64_t N, int64_t K,
                           const int32_t* offsets, int64_t rows, int64_t rows_per_expert, void* gx, int accumulate,
-                          void* gw, void* ws, size_t ws_bytes, hipStream_t stream);
+                          void* gw, int gw_f32, void* ws, size_t ws_bytes, hipStream_t stream);
 
 size_t grouped_backward_workspace_bytes(int64_t E, int64_t N, int64_t K, int64_t rows, int dtype) {
   return dtype == QW_BF16 ? gemm_backward_workspace_bytes(E, N, K, rows) : 256;
@@ -142,8 +142,9 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 int grouped_matmul_backward(const void* gy, const void* x, const void* w, int dtype, int64_t E, int64_t N, int64_t K,
                             const int32_t* offsets, int64_t rows, int64_t max_rows_per_expert, void* gx, int accumulate,
-                            void* gw, void* ws, size_t ws_bytes, hipStream_t stream) {
+                            void* gw, int gw_dtype, void* ws, size_t ws_bytes, hipStream_t stream) {
   QW_REQUIRE(dtype == QW_F32 || dtype == QW_BF16, "grouped backward dtype must be f32 or bf16");
+  QW_REQUIRE(gw_dtype == dtype || gw_dtype == QW_F32, "grad_w dtype must be the operands' dtype or f32");
   QW_REQUIRE(E >= 1 && E <= 65535 && N >= 1 && K >= 1 && N <= INT32_MAX && K <= INT32_MAX && rows >= 0 &&
                  rows <= INT32_MAX && max_rows_per_expert >= 0,
              "bad grouped backward sizes");
@@ -159,7 +160,7 @@ int grouped_matmul_backward(const void* gy, const void* x, const void* w, int dt
   const bool core_dw = core && gw != nullptr && aligned16(gw);
   if (core_dx || core_dw) {
     const int st = gemm_grouped_backward(gy, x, w, E, N, K, offsets, rows, per, core_dx ? gx : nullptr, accumulate,
-                                         core_dw ? gw : nullptr, ws, ws_bytes, stream);
+                                         core_dw ? gw : nullptr, gw_dtype == QW_F32, ws, ws_bytes, stream);
     if (st) return st;
     if (core_dx) gx = nullptr;
     if (core_dw) gw = nullptr;
@@ -175,8 +176,9 @@ int grouped_matmul_backward(const void* gy, const void* x, const void* w, int dt
   if (gw != nullptr) {
     const dim3 g(static_cast<unsigned>(ceil_div(K, BT)), static_cast<unsigned>(ceil_div(N, BT)),
                  static_cast<unsigned>(E));
-    if (dtype == QW_F32) grouped_dw_kernel<QW_F32><<<g, 256, 0, stream>>>(gy, x, offsets, n, k, r, gw);
-    else grouped_dw_kernel<QW_BF16><<<g, 256, 0, stream>>>(gy, x, offsets, n, k, r, gw);
+    if (dtype == QW_F32) grouped_dw_kernel<QW_F32, QW_F32><<<g, 256, 0, stream>>>(gy, x, offsets, n, k, r, gw);
+    else if (gw_dtype == QW_F32) grouped_dw_kernel<QW_BF16, QW_F32><<<g, 256, 0, stream>>>(gy, x, offsets, n, k, r, gw);
+    else grouped_dw_kernel<QW_BF16, QW_BF16><<<g, 256, 0, stream>>>(gy, x, offsets, n, k, r, gw);
     QW_LAUNCH_CHECK("grouped_dw_kernel");
   }
   return QW_OK;

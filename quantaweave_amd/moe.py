@@ -524,12 +524,15 @@ class _MoELayer(torch.autograd.Function):
                 xp = torch.empty(R, D, dtype=cdt, device=dev)
                 _lib.call("qw_moe_permute", _hip.ptr(flat.to(cdt)), act, D, _hip.ptr(slot_token), _hip.ptr(totals), R,
                           _hip.ptr(xp), s)
-                dh, d_down = _backward(dy, h, stacks[2], plan, act, True, need_experts)
+                wdt = moe.experts[0].gate.weight.dtype  # fp32 parameters: unrounded fp32 gradients
+                gwd = torch.float32 if wdt == torch.float32 else None
+                dh, d_down = _backward(dy, h, stacks[2], plan, act, True, need_experts, grad_w_dtype=gwd)
                 dg, du = torch.empty_like(g), torch.empty_like(u)
                 _lib.call("qw_swiglu_backward", _hip.ptr(dh), _hip.ptr(g), _hip.ptr(u), act, g.numel(), _hip.ptr(dg),
                           _hip.ptr(du), s)
-                dxp, d_gate = _backward(dg, xp, stacks[0], plan, act, need_x, need_experts)
-                dxp, d_up = _backward(du, xp, stacks[1], plan, act, need_x, need_experts, grad_x=dxp)
+                dxp, d_gate = _backward(dg, xp, stacks[0], plan, act, need_x, need_experts, grad_w_dtype=gwd)
+                dxp, d_up = _backward(du, xp, stacks[1], plan, act, need_x, need_experts, grad_x=dxp,
+                                      grad_w_dtype=gwd)
                 if need_experts:
                     for j, (n, gw) in enumerate((("gate", d_gate), ("up", d_up), ("down", d_down))):
                         per = gw.to(getattr(moe.experts[0], n).weight.dtype).unbind(0)

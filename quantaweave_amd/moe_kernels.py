@@ -90,20 +90,25 @@ def _forward(x: Tensor, w: Tensor, plan: GroupedPlan, act: int) -> Tensor:
 
 
 def _backward(grad: Tensor, x: Tensor, w: Tensor, plan: GroupedPlan, act: int, need_x: bool, need_w: bool,
-              grad_x: Optional[Tensor] = None) -> tuple[Optional[Tensor], Optional[Tensor]]:
-    """(grad_x, grad_w) of out = grouped x @ w^T.  A given grad_x is added to."""
+              grad_x: Optional[Tensor] = None, grad_w_dtype: Optional[torch.dtype] = None
+              ) -> tuple[Optional[Tensor], Optional[Tensor]]:
+    """(grad_x, grad_w) of out = grouped x @ w^T.  A given grad_x is added to.
+    grad_w_dtype: float32 to get the weight gradient unrounded (fp32
+    parameters multiplied in bf16); default the operands' dtype."""
     gx = gw = None
     accumulate = grad_x is not None
     if need_x:
         gx = grad_x if accumulate else torch.empty_like(x)
+    gw_dtype = w.dtype if grad_w_dtype is None else grad_w_dtype
     if need_w:
-        gw = torch.empty_like(w)
+        gw = torch.empty(w.shape, dtype=gw_dtype, device=w.device)
     if gx is not None or gw is not None:
         nbytes = _lib.load().qw_grouped_matmul_backward_workspace_bytes(w.size(0), w.size(1), w.size(2), x.size(0), act)
         ws = _hip.workspace(nbytes, x.device)
         _lib.call("qw_grouped_matmul_backward", _hip.ptr(grad), _hip.ptr(x), _hip.ptr(w), act, w.size(0), w.size(1),
                   w.size(2), _hip.ptr(plan.offsets), x.size(0), plan.max_count, _hip.ptr(gx), int(accumulate),
-                  _hip.ptr(gw), _hip.ptr(ws), nbytes, _hip.stream(x.device))
+                  _hip.ptr(gw), _hip.act_code(torch.empty(0, dtype=gw_dtype), "grad_w"), _hip.ptr(ws), nbytes,
+                  _hip.stream(x.device))
     return gx, gw
 
 
@@ -264,3 +269,20 @@ def benchmark(experts: int = 32, tokens: int = 8192, hidden: int = 256, ffn: int
         result[name + "_ms"] = (time.perf_counter() - started) / repeats * 1000
     result.update(experts=experts, tokens=tokens, hidden=hidden, ffn=ffn, top_k=top_k, bf16=bf16)
     return result
+
+
+if __name__ == "__main__":
+    # src/moe_kernels.py:230-235: print the benchmark as JSON
+    import argparse
+    import json
+
+    ap = argparse.ArgumentParser(description="forward + backward wall clock of the HIP MoE layer")
+    ap.add_argument("--experts", type=int, default=32)
+    ap.add_argument("--tokens", type=int, default=8192)
+    ap.add_argument("--hidden", type=int, default=256)
+    ap.add_argument("--ffn", type=int, default=512)
+    ap.add_argument("--top-k", type=int, default=2)
+    ap.add_argument("--repeats", type=int, default=20)
+    ap.add_argument("--bf16", action="store_true", help="under bf16 autocast")
+    a = ap.parse_args()
+    print(json.dumps(benchmark(a.experts, a.tokens, a.hidden, a.ffn, a.top_k, a.repeats, a.bf16)), flush=True)

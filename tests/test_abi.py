@@ -99,10 +99,10 @@ def test_backward_entry_points_validate_before_any_launch():
     bad = _lib.QW_ERR_INVALID
     # grouped backward: plain fp32/bf16 only, offsets required
     assert lib.qw_grouped_matmul_backward(None, None, None, _lib.QW_I8, 8, 16, 16, None, 4, 0, None, 0, None,
-                                          None, 0, None) == bad
+                                          _lib.QW_I8, None, 0, None) == bad
     assert b"dtype" in lib.qw_last_error()
     assert lib.qw_grouped_matmul_backward(None, None, None, _lib.QW_F32, 8, 16, 16, None, 4, 0, None, 0, None,
-                                          None, 0, None) == bad
+                                          _lib.QW_F32, None, 0, None) == bad
     assert lib.qw_grouped_matmul_backward_workspace_bytes(8, 64, 64, 100, _lib.QW_BF16) > 64 * 64 * 8 * 2
     assert lib.qw_grouped_matmul_backward_workspace_bytes(0, 64, 64, 100, _lib.QW_BF16) == 0
     assert b"offsets" in lib.qw_last_error()
