@@ -224,6 +224,7 @@ class TopKMoE(nn.Module):
         if self.tp_size > 1:
             raise ValueError("tensor-parallel MoE is not supported by the single-GPU HIP path")
         self.tp_group = None
+        self.config = config  # kept for save_quantized of a bare layer
         self.num_experts = config.num_experts
         self.top_k = config.top_k
         self.capacity_factor = config.capacity_factor
