@@ -322,16 +322,21 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
       for (int t = 0; t < MF_NT; ++t) {
         const int col = n0 + wn * 64 + t * 16 + 4 * lq;
         if (col >= n_out) continue;
-        uint32_t pk[2], un[2];
+        uint32_t pk[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const float a = round_to_bf16(acc[i][t][2 * h]) * wgt;
           const float c = round_to_bf16(acc[i][t][2 * h + 1]) * wgt;
           pk[h] = f32_to_bf16(a) | (static_cast<uint32_t>(f32_to_bf16(c)) << 16);
-          un[h] = f32_to_bf16(acc[i][t][2 * h]) | (static_cast<uint32_t>(f32_to_bf16(acc[i][t][2 * h + 1])) << 16);
         }
         *reinterpret_cast<uint2*>(out + orow + col) = make_uint2(pk[0], pk[1]);
-        if (save_a) *reinterpret_cast<uint2*>(save_a + orow + col) = make_uint2(un[0], un[1]);
+        if (save_a) {  // the rows before their weight, for the backward pass
+          uint32_t un[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            un[h] = f32_to_bf16(acc[i][t][2 * h]) | (static_cast<uint32_t>(f32_to_bf16(acc[i][t][2 * h + 1])) << 16);
+          *reinterpret_cast<uint2*>(save_a + orow + col) = make_uint2(un[0], un[1]);
+        }
       }
     }
   }
