@@ -13,6 +13,8 @@
 //
 // Stage 1 (GATEUP): h[s, c] = silu(x_s . G_e[c]) * (x_s . U_e[c])
 // Stage 2 (DOWN):   y[s, c] = (h_s . D_e[c]) * row_weight[s]
+#include <algorithm>
+
 #include "qw_weights.h"
 #include "qw_ffn.h"
 
@@ -47,7 +49,8 @@ __global__ __launch_bounds__(256) void ffn_generic_kernel(const void* __restrict
   if (c0 >= N_out) return;
   const int n = tid % GB_N;        // weight row in tile
   const int mg = tid / GB_N;       // 0..3 -> rows mg*4 .. mg*4+3
-  for (int m0 = r0; m0 < r1; m0 += GB_M) {
+  // 16-row chunks of the expert, dealt over the grid's z extent
+  for (int m0 = r0 + static_cast<int>(blockIdx.z) * GB_M; m0 < r1; m0 += static_cast<int>(gridDim.z) * GB_M) {
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     for (int k0 = 0; k0 < K; k0 += GB_K) {
       for (int i = tid; i < GB_N * GB_K; i += 256) {
@@ -116,16 +119,23 @@ __global__ __launch_bounds__(256) void ffn_generic_kernel(const void* __restrict
   }
 }
 
+// Workgroups per (column tile, expert): one per 16-row chunk of an expert of
+// the expected size, at most 32 (each loops over its share of the chunks).
+unsigned row_splits(int64_t avg_rows) {
+  return static_cast<unsigned>(std::min<int64_t>(std::max<int64_t>(ceil_div(avg_rows, GB_M), 1), 32));
+}
+
 template <int ACT, int WF>
 int launch_generic_t(const FfnArgs& a, hipStream_t stream) {
   const dim3 blk(256);
-  const dim3 g1(static_cast<unsigned>(ceil_div(a.d_ff, GB_N / 2)), static_cast<unsigned>(a.experts));
+  const unsigned z = row_splits(a.avg_rows > 0 ? a.avg_rows : ceil_div(a.max_rows, a.experts));
+  const dim3 g1(static_cast<unsigned>(ceil_div(a.d_ff, GB_N / 2)), static_cast<unsigned>(a.experts), z);
   ffn_generic_kernel<ACT, WF, true><<<g1, blk, 0, stream>>>(a.x, a.row_index, a.offsets, a.gate, a.up,
                                                             static_cast<int>(a.d_model), static_cast<int>(a.d_ff),
                                                             static_cast<int>(a.max_rows), nullptr, a.hidden,
                                                             a.save_gate, a.save_up);
   QW_LAUNCH_CHECK("ffn_generic_kernel<gateup>");
-  const dim3 g2(static_cast<unsigned>(ceil_div(a.d_model, GB_N)), static_cast<unsigned>(a.experts));
+  const dim3 g2(static_cast<unsigned>(ceil_div(a.d_model, GB_N)), static_cast<unsigned>(a.experts), z);
   ffn_generic_kernel<ACT, WF, false><<<g2, blk, 0, stream>>>(a.hidden, nullptr, a.offsets, a.down, a.down,
                                                              static_cast<int>(a.d_ff), static_cast<int>(a.d_model),
                                                              static_cast<int>(a.max_rows), a.row_weight, a.y,
@@ -155,7 +165,7 @@ int launch_ffn_generic(const FfnArgs& a, hipStream_t stream) {
 
 int grouped_matmul_generic(const void* x, int act, const WView& w, int wfmt, int64_t E, const int32_t* offsets,
                            int64_t rows, void* out, hipStream_t stream) {
-  const dim3 g(static_cast<unsigned>(ceil_div(w.rows, GB_N)), static_cast<unsigned>(E));
+  const dim3 g(static_cast<unsigned>(ceil_div(w.rows, GB_N)), static_cast<unsigned>(E), row_splits(ceil_div(rows, E)));
   const int K = static_cast<int>(w.cols), N = static_cast<int>(w.rows), nrows = static_cast<int>(rows);
 #define QW_GM(ACT, WF)                                                                                         \
   if (act == ACT && wfmt == WF) {                                                                              \
