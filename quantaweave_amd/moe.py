@@ -13,6 +13,7 @@ whose backward runs the grouped backward kernels.
 
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass
 from typing import Optional
@@ -188,8 +189,12 @@ class ExpertPack:
         multiplied in bf16 use bf16 copies (tiled where the shapes allow),
         made once per weight version — the reference's per-call
         ``stack(...).to(dtype)`` (src/moe_kernels.py:191-193)."""
+        return self.for_act(act).args()
+
+    def for_act(self, act: int) -> "ExpertPack":
+        """This pack, or its bf16 copy for fp32 experts multiplied in bf16."""
         if not (self.fmt == _lib.QW_F32 and act == _lib.QW_BF16):
-            return self.args()
+            return self
         if getattr(self, "_bf16", None) is None:
             cast = ExpertPack.__new__(ExpertPack)
             cast.fmt, cast.group_in, cast.group_ff, cast.key = _lib.QW_BF16, 0, 0, self.key
@@ -197,7 +202,15 @@ class ExpertPack:
             cast.gate_s = cast.up_s = cast.down_s = None
             cast.maybe_tile()
             self._bf16 = cast
-        return self._bf16.args()
+        return self._bf16
+
+    def expert_args(self, e: int) -> list:
+        """Weight arguments of expert e alone (views into the stacks)."""
+        def one(t):
+            return None if t is None else _hip.ptr(t[e])
+
+        return [self.fmt, self.group_in, self.group_ff, one(self.gate), one(self.gate_s), one(self.up),
+                one(self.up_s), one(self.down), one(self.down_s)]
 
 
 def packed_experts(owner: nn.Module, experts: nn.ModuleList) -> ExpertPack:
@@ -279,7 +292,10 @@ class TopKMoE(nn.Module):
         # static dispatch is the capacity-free evaluation (src/quantweave_moe_model.py:235-245)
         cap = T * K if self.static_dispatch else self.capacity(T)
         cdt = _compute_dtype(flat)
-        if self._wants_grad(hidden):
+        # per-expert timing (profile_experts) runs the experts one call at a time and
+        # records no autograd graph; an input that requires grad keeps the graph instead
+        profiling = self.profile_experts and not (hidden.requires_grad and torch.is_grad_enabled())
+        if not profiling and self._wants_grad(hidden):
             if pack.fmt not in (_lib.QW_F32, _lib.QW_BF16, _lib.QW_BF16T):
                 if hidden.requires_grad:
                     raise NotImplementedError("gradients through quantised experts are not supported")
@@ -291,7 +307,9 @@ class TopKMoE(nn.Module):
                                     dropped_expert, token_domains, num_domains, (batch, sequence, width))
         with torch.no_grad():
             flat = flat.detach().contiguous()
-            if cdt == flat.dtype:
+            if profiling:
+                res = _layer_chain(flat, cdt, self.router.weight, self, pack, cap, bias, profile=self.expert_seconds)
+            elif cdt == flat.dtype:
                 res = _forward_call(flat, act, self.router.weight, self, pack, cap, bias)
             else:
                 res = _layer_chain(flat, cdt, self.router.weight, self, pack, cap, bias)
@@ -397,7 +415,7 @@ def _compute_dtype(flat: Tensor) -> torch.dtype:
 
 
 def _layer_chain(flat: Tensor, cdt: torch.dtype, router_w: Tensor, moe: TopKMoE, pack: ExpertPack, cap: int,
-                 bias: Optional[Tensor], save: bool = False) -> dict:
+                 bias: Optional[Tensor], save: bool = False, profile: Optional[list] = None) -> dict:
     """The layer forward as one C call per stage: qw_moe_route (on the input
     dtype, src/quantweave_moe_model.py:126-127), qw_moe_plan, qw_moe_experts
     on the rows cast to `cdt` and qw_moe_combine, then qw_moe_balance.
@@ -409,7 +427,11 @@ def _layer_chain(flat: Tensor, cdt: torch.dtype, router_w: Tensor, moe: TopKMoE,
     qw_moe_combine_weighted adds (y * w) in the input dtype, as
     `(expert_output * weights[:, None]).to(output.dtype)` does (:201).
     save: keep the activations a backward pass reads (qw_moe_experts_save):
-    gate, up, hidden [R, d_ff] and the unweighted expert rows [R, d_model]."""
+    gate, up, hidden [R, d_ff] and the unweighted expert rows [R, d_model].
+    profile: a list of per-expert seconds; the experts then run one call per
+    expert with rows, each bracketed by synchronisations and its wall time
+    added to the list (the reference's profile_experts,
+    src/quantweave_moe_model.py:220-233)."""
     dev = flat.device
     T, D = flat.shape
     E, K = moe.num_experts, moe.top_k
@@ -446,11 +468,26 @@ def _layer_chain(flat: Tensor, cdt: torch.dtype, router_w: Tensor, moe: TopKMoE,
     xc = flat.to(cdt) if mixed else flat
     max_rows = min(R, cap * E)
     y = torch.empty(R, D, dtype=cdt, device=dev)
-    nb = lib.qw_moe_experts_workspace_bytes(max_rows, E, D, F_, act)
+    nb = lib.qw_moe_experts_workspace_bytes(R if profile is not None else max_rows, E, D, F_, act)
     ws = _hip.workspace(nb, dev)
     args = [_hip.ptr(xc), act, p["slot_token"], p["kept_offsets"], E, D, F_, max_rows, min(cap, R),
             *pack.args_for(act), None if mixed else p["slot_weight"], _hip.ptr(y)]
-    if save:
+    if profile is not None:
+        import time
+
+        kept = r["kept_counts"].tolist()  # host sync, as the reference's loop makes
+        weights = pack.for_act(act)
+        for e in range(E):
+            if not kept[e]:
+                continue
+            offs = ctypes.c_void_p(r["kept_offsets"].data_ptr() + 4 * e)
+            torch.cuda.synchronize(dev)
+            started = time.perf_counter()
+            _lib.call("qw_moe_experts", _hip.ptr(xc), act, p["slot_token"], offs, 1, D, F_, R, min(cap, R),
+                      *weights.expert_args(e), None if mixed else p["slot_weight"], _hip.ptr(y), _hip.ptr(ws), nb, s)
+            torch.cuda.synchronize(dev)
+            profile[e] += time.perf_counter() - started
+    elif save:
         for name, width in (("gate", F_), ("up", F_), ("hidden", F_), ("y_unweighted", D)):
             r[name] = torch.empty(R, width, dtype=cdt, device=dev)
         _lib.call("qw_moe_experts_save", *args, *(_hip.ptr(r[n]) for n in ("gate", "up", "hidden", "y_unweighted")),
