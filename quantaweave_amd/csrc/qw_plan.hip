@@ -6,7 +6,7 @@
 // `capacity` routes of each expert and lists the rest as dropped.
 //
 // One kernel, one workgroup per expert.  Every workgroup reads all routes once
-// (16 per thread, loads issued together), builds the histogram of all experts
+// (16 expert ids and weights per thread, loads issued together), builds the histogram of all experts
 // in LDS (per-wave copies, summed afterwards) and gathers its own expert's
 // route keys
 //   key = (~order(weight)) << 32 | route id        (unique per route)
@@ -58,11 +58,14 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   // ---- one pass over the routes: histogram of all experts, keys of expert e ----
   // (the keys go to LDS when they fit; the count decides afterwards)
   for (int base = 0; base < R; base += kPlanThreads * kRoutesPerThread) {
+    // expert ids and weights of 16 routes per thread, all loads issued before any use
     int v[kRoutesPerThread];
+    float wv[kRoutesPerThread];
 #pragma unroll
     for (int i = 0; i < kRoutesPerThread; ++i) {
       const int r = base + i * kPlanThreads + tid;
       v[i] = r < R ? top_idx[r] : -1;
+      wv[i] = r < R ? top_w[r] : 0.0f;
     }
 #pragma unroll
     for (int i = 0; i < kRoutesPerThread; ++i) {
@@ -80,7 +83,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
         first = __shfl(first, __builtin_ctzll(m), kWave);
         if (mine) {
           const int p = first + __popcll(m & ((1ull << lane) - 1ull));
-          if (p < kSortCap) keys[p] = route_key(top_w, r);
+          if (p < kSortCap) keys[p] = (static_cast<uint64_t>(~weight_key(wv[i])) << 32) | static_cast<uint32_t>(r);
         }
       }
     }
@@ -137,7 +140,8 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     for (int i = tid; i < n; i += kPlanThreads) {
       const uint64_t k = keys[i];
       int rank = 0;
-      for (int j = 0; j < n; ++j) rank += keys[j] < k ? 1 : 0;
+#pragma unroll 16
+      for (int j = 0; j < n; ++j) rank += keys[j] < k ? 1 : 0;  // reads in flight together
       place(k, rank);
     }
   } else if (n <= kSortCap) {
