@@ -535,9 +535,7 @@ int launch_one(const FfnArgs& a, const WView& wa, const WView& wb, const void* x
   using LD = GvLds<WF, UNITS, GATEUP ? 2 : 1, CPL, MAXM>;
   constexpr size_t lds = static_cast<size_t>(GV_WAVES) * LD::WAVE;
   auto kernel = ffn_gemv_kernel<WF, GATEUP, UNITS, CPL, MAXM>;
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                     static_cast<int>(lds));
+  const hipError_t attr = reserve_lds<ffn_gemv_kernel<WF, GATEUP, UNITS, CPL, MAXM>>(static_cast<int>(lds));
   if (attr != hipSuccess)
     return set_error(QW_ERR_HIP, "cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(attr));
   const int64_t n_groups = ceil_div(n_out, UNITS);

@@ -357,9 +357,7 @@ int launch_t(const void* x, const int32_t* row_index, const int32_t* offsets, in
   const int64_t grid = static_cast<int64_t>(kXcds) * chunks * n_tiles;
   if (grid > INT32_MAX) return set_error(QW_ERR_UNSUPPORTED, "MFMA grid too large");
   const size_t lds = static_cast<size_t>(mf_stages(SUBT)) * (32 * SUBT * MF_ROWB + MF_NB * MF_ROWB);
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&ffn_mfma_kernel<GATEUP, SUBT, TILED>),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                     static_cast<int>(lds));
+  const hipError_t attr = reserve_lds<ffn_mfma_kernel<GATEUP, SUBT, TILED>>(static_cast<int>(lds));
   if (attr != hipSuccess)
     return set_error(QW_ERR_HIP, "cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(attr));
   ffn_mfma_kernel<GATEUP, SUBT, TILED><<<static_cast<unsigned>(grid), MF_THREADS, lds, stream>>>(

@@ -324,8 +324,7 @@ template <int MODE, bool ACCUM, bool BRED = false, bool C32 = false>
 int launch_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t b_stride, void* C, int64_t ldc,
                 int64_t c_stride, const int32_t* offsets, int rows, int M, int N, int K, int E, int64_t m_extent,
                 hipStream_t stream) {
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_nt_kernel<MODE, ACCUM, BRED, C32>),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, G_LDS);
+  const hipError_t attr = reserve_lds<gemm_nt_kernel<MODE, ACCUM, BRED, C32>>(G_LDS);
   if (attr != hipSuccess) return set_error(QW_ERR_HIP, "cannot reserve LDS: %s", hipGetErrorString(attr));
   // one grid dimension: MODE_ROWS, the row tiles of all experts (at most
   // rows/128 + E) times the column tiles; MODE_RED, experts times output tiles;
