@@ -6,16 +6,18 @@
 // `capacity` routes of each expert and lists the rest as dropped.
 //
 // One kernel, one workgroup per expert.  Every workgroup reads all routes once
-// (16 expert ids and weights per thread, loads issued together), builds the histogram of all experts
-// in LDS (per-wave copies, summed afterwards) and gathers its own expert's
-// route keys
+// (16 expert ids and weights per thread, loads issued together), builds the
+// histogram of all experts in LDS (per-wave copies, summed afterwards) and
+// gathers its own expert's route keys
 //   key = (~order(weight)) << 32 | route id        (unique per route)
-// into LDS.  From the histogram it derives every offset itself, ranks its keys
-// (by counting, or with a bitonic network for large experts) and writes kept
-// slots and dropped routes at their plan positions.  Keys are unique, so the
-// order inside the gather does not matter and the result does not depend on
-// scheduling.  An expert with more routes than the LDS holds ranks its keys
-// against each other through global memory instead (same result, slower).
+// into LDS (a wave finds its matches with one ballot per route column and
+// claims their positions with a single LDS atomic).  From the histogram it
+// derives every offset itself, ranks its keys (by counting, or with a bitonic
+// network for large experts) and writes kept slots and dropped routes at
+// their plan positions.  Keys are unique, so the order inside the gather does
+// not matter and the result does not depend on scheduling.  An expert with
+// more routes than the LDS holds ranks its keys against each other through
+// global memory instead (same result, slower).
 #include "qw_common.h"
 
 namespace qw {
@@ -30,6 +32,12 @@ constexpr int kRoutesPerThread = 16;
 __device__ __forceinline__ uint32_t weight_key(float f) {
   uint32_t u = __float_as_uint(f);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// The weight a key was made from (weight_key inverted, exact for every bit pattern).
+__device__ __forceinline__ float key_weight(uint64_t key) {
+  const uint32_t k = ~static_cast<uint32_t>(key >> 32);
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
 __device__ __forceinline__ uint64_t route_key(const float* top_w, int r) {
@@ -67,24 +75,32 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       v[i] = r < R ? top_idx[r] : -1;
       wv[i] = r < R ? top_w[r] : 0.0f;
     }
+    uint64_t mask[kRoutesPerThread];
+    int wave_n = 0;
 #pragma unroll
     for (int i = 0; i < kRoutesPerThread; ++i) {
       const int r = base + i * kPlanThreads + tid;
       const bool valid = r < R && v[i] >= 0 && v[i] < E;
       if (valid) atomicAdd(&hist[wave][v[i]], 1);
       if (r < R && !valid && e == 0) route_slot[r] = -1;  // out-of-range expert id: never kept
-      // this expert's routes: one LDS atomic per wave, lanes take consecutive positions
-      const bool mine = valid && v[i] == e;
-      const uint64_t m = __ballot(mine);
-      if (m != 0) {
-        const int lane = tid % kWave;
-        int first = 0;
-        if (lane == __builtin_ctzll(m)) first = atomicAdd(&s_fill, __popcll(m));
-        first = __shfl(first, __builtin_ctzll(m), kWave);
-        if (mine) {
-          const int p = first + __popcll(m & ((1ull << lane) - 1ull));
+      mask[i] = __ballot(valid && v[i] == e);
+      wave_n += __popcll(mask[i]);
+    }
+    if (wave_n != 0) {
+      // this expert's routes of the wave: one LDS atomic, then consecutive positions
+      const int lane = tid % kWave;
+      int first = 0;
+      if (lane == 0) first = atomicAdd(&s_fill, wave_n);
+      first = __shfl(first, 0, kWave);
+      const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+      for (int i = 0; i < kRoutesPerThread; ++i) {
+        const int r = base + i * kPlanThreads + tid;
+        if ((mask[i] >> lane) & 1ull) {
+          const int p = first + __popcll(mask[i] & below);
           if (p < kSortCap) keys[p] = (static_cast<uint64_t>(~weight_key(wv[i])) << 32) | static_cast<uint32_t>(r);
         }
+        first += __popcll(mask[i]);
       }
     }
   }
@@ -125,7 +141,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     if (rank < capacity) {
       const int s = kept_off + rank;
       slot_token[s] = r / K;
-      slot_weight[s] = top_w[r];
+      slot_weight[s] = key_weight(key);
       route_slot[r] = s;
     } else {
       const int q = drop_off + (rank - capacity);

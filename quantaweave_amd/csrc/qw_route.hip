@@ -332,6 +332,75 @@ __device__ __forceinline__ void select_token(float (&l)[EPL], int t, int E, int 
   }
 }
 
+// select_token for E <= 64 (lane l owns expert l) on TT tokens of one wave at
+// once: each token goes through exactly the operations select_token applies
+// (same reduction trees, same order), and the TT independent chains of
+// cross-lane exchanges overlap instead of running one after another.  Tokens
+// with valid[i] false are computed on their (finite) inputs and not stored.
+// Lane j < K returns round j's expert and renormalised weight of token i in
+// out_e[i] / out_w[i].
+template <int TT>
+__device__ __forceinline__ void select_tokens(float (&l)[TT], const int (&t)[TT], const bool (&valid)[TT], int E,
+                                              int K, const float* __restrict__ bias, int select_logits,
+                                              float* __restrict__ probs, int (&out_e)[TT], float (&out_w)[TT]) {
+  const int lane = threadIdx.x % kWave;
+  const bool live = lane < E;
+  float m[TT], p[TT], s[TT];
+#pragma unroll
+  for (int i = 0; i < TT; ++i) m[i] = l[i];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1)
+#pragma unroll
+    for (int i = 0; i < TT; ++i) m[i] = fmaxf(m[i], __shfl_xor(m[i], o, kWave));
+#pragma unroll
+  for (int i = 0; i < TT; ++i) {
+    if (__any(l[i] != l[i])) m[i] = __builtin_nanf("");  // fmaxf drops NaN; torch's softmax does not
+    p[i] = live ? det_expf(l[i] - m[i]) : 0.0f;
+    s[i] = 0.0f + p[i];  // select_token's per-lane sum starts at 0 (0 + -0 is +0)
+    out_e[i] = 0;
+    out_w[i] = 0.0f;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1)
+#pragma unroll
+    for (int i = 0; i < TT; ++i) s[i] += __shfl_xor(s[i], o, kWave);
+  uint64_t key[TT];
+  const float b = (bias != nullptr && live) ? bias[lane] : 0.0f;
+#pragma unroll
+  for (int i = 0; i < TT; ++i) {
+    p[i] = p[i] / s[i];
+    if (probs != nullptr && live && valid[i]) probs[static_cast<int64_t>(t[i]) * E + lane] = p[i];
+    const float v = (bias != nullptr && live) ? l[i] + b : (select_logits ? l[i] : p[i]);
+    key[i] = live ? (static_cast<uint64_t>(sortable_key(v)) << 32) | (0xffffffffu - static_cast<uint32_t>(lane)) : 0;
+  }
+  float sel_sum[TT];
+  for (int j = 0; j < K; ++j) {
+    uint64_t best[TT];
+#pragma unroll
+    for (int i = 0; i < TT; ++i) best[i] = key[i];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+#pragma unroll
+      for (int i = 0; i < TT; ++i) {
+        const uint64_t other = __shfl_xor(best[i], o, kWave);
+        best[i] = other > best[i] ? other : best[i];
+      }
+#pragma unroll
+    for (int i = 0; i < TT; ++i) {
+      const int e_sel = static_cast<int>(0xffffffffu - static_cast<uint32_t>(best[i] & 0xffffffffu));
+      const float p_sel = __shfl(p[i], e_sel, kWave);
+      if (lane == e_sel) key[i] = 0;  // taken
+      sel_sum[i] = (j == 0) ? p_sel : sel_sum[i] + p_sel;
+      if (lane == j) {
+        out_e[i] = e_sel;
+        out_w[i] = p_sel;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TT; ++i) out_w[i] = out_w[i] / sel_sum[i];
+}
+
 // With `partial` != NULL the logits are first assembled from the router GEMM's
 // split-K partials: L = ((p_0 + p_1) + ... + p_{S-1}) / temperature, and
 // written to `logits`.
@@ -371,6 +440,131 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
     top_idx[static_cast<int64_t>(t) * K + lane] = me;
     top_w[static_cast<int64_t>(t) * K + lane] = mw;
   }
+}
+
+// ---------------------------------------------------------------------------
+// Router logits and routing in one kernel (bf16 x and weights, E <= 64,
+// D % 64 == 0): 32 tokens per 512-thread block.  Wave w multiplies the
+// block's token rows by the E router rows over the 64-wide k chunks
+// w, w + 8, w + 16, ... with bf16 MFMA (fp32 accumulation; operands go from
+// global memory straight into registers, one chunk in flight while the
+// previous is multiplied), the eight partial sums meet in LDS and are added in
+// wave order, L = (((p_0 + p_1) + ...) + p_7) / temperature, and wave w then
+// routes tokens 4w..4w+3 together (select_tokens), writing logits, probs and
+// choices exactly as route_topk_kernel does from the same logits.
+// ---------------------------------------------------------------------------
+constexpr int kFuseTokens = 32, kFuseWaves = 8, kFuseChunk = 64, kFuseSteps = kFuseChunk / 32;
+constexpr int kFusePitch = 68;  // LDS row pitch in floats: the partial stores of a wave hit 64 distinct banks
+
+__global__ __launch_bounds__(kFuseWaves * kWave) void router_topk_kernel(
+    const uint16_t* __restrict__ x, int64_t x_stride, const uint16_t* __restrict__ w, int T, int D, int E, int K,
+    float temperature, const float* __restrict__ bias, int select_logits, float* __restrict__ logits,
+    float* __restrict__ probs, int32_t* __restrict__ top_idx, float* __restrict__ top_w) {
+  __shared__ float part[kFuseWaves][kFuseTokens][kFusePitch];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int t0 = blockIdx.x * kFuseTokens;
+  const int l16 = lane % 16, kq = (lane / 16) * 8;
+  // a-operand rows: tokens t0 + 16m + l16; b-operand rows: experts 16n + l16.
+  // Rows past T or E read row 0 instead: an output row (column) depends only on
+  // its own a (b) row, and those rows and columns are never read back.
+  const uint16_t* arow0 = x + static_cast<int64_t>(t0 + l16 < T ? t0 + l16 : 0) * x_stride + kq;
+  const uint16_t* arow1 = x + static_cast<int64_t>(t0 + 16 + l16 < T ? t0 + 16 + l16 : 0) * x_stride + kq;
+  const uint16_t* brow[4];
+#pragma unroll
+  for (int n = 0; n < 4; ++n) brow[n] = w + static_cast<int64_t>(16 * n + l16 < E ? 16 * n + l16 : 0) * D + kq;
+  rf32x4 acc[2][4];
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int n = 0; n < 4; ++n) acc[m][n] = rf32x4{0.f, 0.f, 0.f, 0.f};
+  // one chunk: k-steps of 32, lane (l16, kq) holding elements k0 + 32s + kq .. +7 of its rows
+  uint4 a0[2][kFuseSteps], b0[4][kFuseSteps], a1[2][kFuseSteps], b1[4][kFuseSteps];
+#define QW_RT_LOAD(A, B, C)                                                                  \
+  {                                                                                          \
+    const int k0_ = (C) * kFuseChunk;                                                        \
+    _Pragma("unroll") for (int s = 0; s < kFuseSteps; ++s) {                                          \
+      A[0][s] = *reinterpret_cast<const uint4*>(arow0 + k0_ + 32 * s);                       \
+      A[1][s] = *reinterpret_cast<const uint4*>(arow1 + k0_ + 32 * s);                       \
+      _Pragma("unroll") for (int n = 0; n < 4; ++n) B[n][s] =                                \
+          *reinterpret_cast<const uint4*>(brow[n] + k0_ + 32 * s);                           \
+    }                                                                                        \
+  }
+#define QW_RT_MUL(A, B)                                                                      \
+  {                                                                                          \
+    _Pragma("unroll") for (int s = 0; s < kFuseSteps; ++s) {                                          \
+      _Pragma("unroll") for (int m = 0; m < 2; ++m) {                                        \
+        const rbf16x8 af = __builtin_bit_cast(rbf16x8, A[m][s]);                             \
+        _Pragma("unroll") for (int n = 0; n < 4; ++n) acc[m][n] =                            \
+            __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, __builtin_bit_cast(rbf16x8, B[n][s]), \
+                                                    acc[m][n], 0, 0, 0);                     \
+      }                                                                                      \
+    }                                                                                        \
+  }
+  // The next chunk's loads are issued unconditionally (past the wave's last
+  // chunk they re-read it), so each multiply waits for exactly its own loads.
+  const int nc = D / kFuseChunk;
+  const int mine = wave < nc ? (nc - 1 - wave) / kFuseWaves + 1 : 0;  // chunks of this wave
+  int c = wave;
+  if (mine > 0) {
+    QW_RT_LOAD(a0, b0, c);
+    for (int i = 0;; i += 2) {
+      QW_RT_LOAD(a1, b1, i + 1 < mine ? c + kFuseWaves : c);
+      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the multiplies
+      QW_RT_MUL(a0, b0);
+      if (i + 1 >= mine) break;
+      c += kFuseWaves;
+      QW_RT_LOAD(a0, b0, i + 2 < mine ? c + kFuseWaves : c);
+      __builtin_amdgcn_sched_barrier(0);
+      QW_RT_MUL(a1, b1);
+      if (i + 2 >= mine) break;
+      c += kFuseWaves;
+    }
+  }
+#undef QW_RT_LOAD
+#undef QW_RT_MUL
+  // lane holds C[token 16m + 4(lane/16) + r][expert 16n + l16]
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) part[wave][16 * m + 4 * (lane / 16) + r][16 * n + l16] = acc[m][n][r];
+  __syncthreads();
+  constexpr int TPW = kFuseTokens / kFuseWaves;  // tokens each wave routes
+  float l[TPW];
+  int tok[TPW];
+  bool ok[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int tl = wave * TPW + i;
+    tok[i] = t0 + tl;
+    ok[i] = tok[i] < T;
+    if (lane < E) {
+      float v = part[0][tl][lane];
+#pragma unroll
+      for (int p = 1; p < kFuseWaves; ++p) v += part[p][tl][lane];
+      v = v / temperature;
+      if (ok[i]) logits[static_cast<int64_t>(tok[i]) * E + lane] = v;
+      l[i] = v;
+    } else {
+      l[i] = -__builtin_inff();
+    }
+  }
+  int me[TPW];
+  float mw[TPW];
+  select_tokens<TPW>(l, tok, ok, E, K, bias, select_logits, probs, me, mw);
+#pragma unroll
+  for (int i = 0; i < TPW; ++i)
+    if (ok[i] && lane < K) {
+      top_idx[static_cast<int64_t>(tok[i]) * K + lane] = me[i];
+      top_w[static_cast<int64_t>(tok[i]) * K + lane] = mw[i];
+    }
+}
+
+static bool router_topk_fits(int xdt, int wdt, const void* x, int64_t x_stride, const void* w, int64_t T,
+                             int64_t D, int64_t E) {
+  return xdt == QW_BF16 && wdt == QW_BF16 && T > kGemvMaxTokens && E <= kWave && D % kFuseChunk == 0 &&
+         x_stride % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
 }
 
 static int launch_topk(const float* partial, int splits, float temperature, float* logits, int T, int E, int K,
@@ -648,6 +842,13 @@ int route(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int6
   if (T == 0) return QW_OK;
   QW_REQUIRE(x && w && logits && top_idx && top_w, "x, router_w, logits, top_idx and top_w are required");
   const int t = static_cast<int>(T), e = static_cast<int>(E), k = static_cast<int>(K);
+  if (router_topk_fits(xdt, wdt, x, x_stride, w, T, D, E)) {
+    router_topk_kernel<<<static_cast<unsigned>(ceil_div(T, kFuseTokens)), kFuseWaves * kWave, 0, stream>>>(
+        static_cast<const uint16_t*>(x), x_stride, static_cast<const uint16_t*>(w), t, static_cast<int>(D), e, k,
+        temperature, bias, select_logits ? 1 : 0, logits, probs, top_idx, top_w);
+    QW_LAUNCH_CHECK("router_topk_kernel");
+    return QW_OK;
+  }
   int splits = 0;
   st = launch_router(x, xdt, x_stride, w, wdt, T, D, E, temperature, logits, partial, partial_bytes, &splits, stream);
   if (st) return st;

@@ -58,7 +58,8 @@ def test_expert_bias_steers_selection_only():
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("T,D,E", [(512, 256, 8), (100, 2048, 64), (16, 4096, 64), (7, 33, 5)])
+@pytest.mark.parametrize("T,D,E", [(512, 256, 8), (100, 2048, 64), (16, 4096, 64), (7, 33, 5),
+                                   (8192, 2048, 64), (301, 192, 40), (65, 64, 1)])
 def test_router_logits_match_oracle_and_routing_follows(dtype, T, D, E):
     print(f"case T={T} D={D} E={E} {dtype}", flush=True)
     g = torch.Generator().manual_seed(T + D)
@@ -74,6 +75,19 @@ def test_router_logits_match_oracle_and_routing_follows(dtype, T, D, E):
     assert np.array_equal(probs.cpu().numpy().view(np.int32), p_o.view(np.int32))
     assert np.array_equal(idx.cpu().numpy(), i_o) and np.array_equal(tw.cpu().numpy(), w_o)
 
+
+
+@pytest.mark.parametrize("T,D,E", [(300, 256, 64), (40, 512, 16)])
+def test_router_reads_strided_rows(T, D, E):
+    """x given as a view with a row stride larger than d_model gives the same bits as contiguous rows."""
+    print(f"case T={T} D={D} E={E} strided", flush=True)
+    g = torch.Generator().manual_seed(T * D)
+    wide = torch.randn(T, D + 64, generator=g).to(torch.bfloat16).cuda()
+    w = (torch.randn(E, D, generator=g) * 0.02).to(torch.bfloat16).cuda()
+    got = H.route(wide[:, :D], w, 2)
+    ref = H.route(wide[:, :D].contiguous(), w, 2)
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
 
 def _check_plan(idx, w, E, cap):
     ref = oracle.plan(idx, w, E, cap)
