@@ -29,10 +29,12 @@
 // with the order pinned by scheduling barriers.
 //
 // Waves form a 2 x 4 grid: wave (wm, wn) computes row sub-tiles wm, wm+2, ...
-// (16 rows each; those past the expert's row count run on clamped copies of a
-// valid row and are not stored) against its 64 weight
-// rows (GATEUP: 32 gate rows and the matching 32 up rows, so SiLU(g)*u is
-// formed in registers).  The MFMA takes the weights as its A operand, so a
+// (16 rows each) against its 64 weight rows (GATEUP: 32 gate rows and the
+// matching 32 up rows, so SiLU(g)*u is formed in registers).  Sub-tiles go in
+// pairs; a pair wholly past the expert's row count is not multiplied (the K
+// loop is instantiated per number of active pairs), and the rows past the
+// count inside a live pair run on clamped copies of a valid row and are not
+// stored.  The MFMA takes the weights as its A operand, so a
 // lane ends up holding 4 consecutive output columns of one row and stores them
 // with one 8-byte write.
 //
@@ -223,64 +225,83 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
   static_assert(SUBT % 2 == 0, "sub-tiles come in pairs");
   static_assert(AHEAD >= 1 && AHEAD <= 2 && 2 * (AL + BL) < 64, "ring depth");
   constexpr int NP = SUBT / 2;  // pairs of sub-tiles per K step
-  for (int kt = 0; kt < KT; ++kt) {
-    if (AHEAD == 2 && kt + 1 < KT) wait_vmcnt<AL + BL>();
-    else wait_vmcnt<0>();
-    ring_barrier();
-    const char* st_a = a_ring + (kt % ST) * A_STAGE;
-    const char* st_b = b_ring + (kt % ST) * B_STAGE;
-    auto read_a = [&](int i, int ks) {
-      const int row = (wm + 2 * i) * 16 + l16;
-      return *reinterpret_cast<const bf16x8*>(st_a + row * MF_ROWB + swz(row, lq + 4 * ks) * 16);
-    };
-    auto read_b = [&](int t, int ks) {
-      const int row = brow[t] + l16;
-      return *reinterpret_cast<const bf16x8*>(st_b + row * MF_ROWB + swz(row, lq + 4 * ks) * 16);
-    };
-    // Units u = 0 .. 2*NP-1 are (K step ks = u / NP, sub-tile pair p = u % NP),
-    // with activation fragments in two pair buffers (u & 1) and weight fragments
-    // per K step.  The reads of unit u+1 (and, before the second K step, its
-    // weight fragments) go out right after the first MFMA of unit u, whose wait
-    // covered every earlier read, so seven MFMAs hide them.
-    bf16x8 wfr[2][MF_NT];
-    bf16x8 xb[2][2];
-#pragma unroll
-    for (int t = 0; t < MF_NT; ++t) wfr[0][t] = read_b(t, 0);
-    xb[0][0] = read_a(0, 0);
-    xb[0][1] = read_a(1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, MF_NT + 2, 0);  // first fragments, then the requests
-    if (kt + AHEAD < KT) {
-      issue_a(kt + AHEAD);
-      issue_b(kt + AHEAD);
-    }
-#pragma unroll
-    for (int u = 0; u < 2 * NP; ++u) {
-      const int ks = u / NP, p = u % NP;
-      const bf16x8 x0 = xb[u & 1][0], x1 = xb[u & 1][1];
-      acc[2 * p][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[ks][0], x0, acc[2 * p][0], 0, 0, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (u + 1 < 2 * NP) {
-        const int ks1 = (u + 1) / NP, p1 = (u + 1) % NP;
-        if (ks1 != ks) {
-#pragma unroll
-          for (int t = 0; t < MF_NT; ++t) wfr[1][t] = read_b(t, 1);
-          xb[(u + 1) & 1][0] = read_a(2 * p1, 1);
-          xb[(u + 1) & 1][1] = read_a(2 * p1 + 1, 1);
-          __builtin_amdgcn_sched_group_barrier(0x100, MF_NT + 2, 0);
-        } else {
-          xb[(u + 1) & 1][0] = read_a(2 * p1, ks1);
-          xb[(u + 1) & 1][1] = read_a(2 * p1 + 1, ks1);
-          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        }
+  // The K loop, for a wave whose first NPA sub-tile pairs hold rows: pairs
+  // wholly past the expert's rows are not multiplied (their rows are loaded
+  // with the rest and never stored).  Every wave takes part in every load and
+  // barrier whatever its NPA.
+  auto k_loop = [&](auto npa) {
+    constexpr int NPA = decltype(npa)::value;
+    for (int kt = 0; kt < KT; ++kt) {
+      if (AHEAD == 2 && kt + 1 < KT) wait_vmcnt<AL + BL>();
+      else wait_vmcnt<0>();
+      ring_barrier();
+      const char* st_a = a_ring + (kt % ST) * A_STAGE;
+      const char* st_b = b_ring + (kt % ST) * B_STAGE;
+      auto read_a = [&](int i, int ks) {
+        const int row = (wm + 2 * i) * 16 + l16;
+        return *reinterpret_cast<const bf16x8*>(st_a + row * MF_ROWB + swz(row, lq + 4 * ks) * 16);
+      };
+      auto read_b = [&](int t, int ks) {
+        const int row = brow[t] + l16;
+        return *reinterpret_cast<const bf16x8*>(st_b + row * MF_ROWB + swz(row, lq + 4 * ks) * 16);
+      };
+      // Units u = 0 .. 2*NP-1 are (K step ks = u / NP, sub-tile pair p = u % NP),
+      // with activation fragments in two pair buffers (u & 1) and weight fragments
+      // per K step.  The reads of unit u+1 (and, before the second K step, its
+      // weight fragments) go out right after the first MFMA of unit u, whose wait
+      // covered every earlier read, so seven MFMAs hide them.
+      bf16x8 wfr[2][MF_NT];
+      bf16x8 xb[2][2];
+  #pragma unroll
+      for (int t = 0; t < MF_NT; ++t) wfr[0][t] = read_b(t, 0);
+      xb[0][0] = read_a(0, 0);
+      xb[0][1] = read_a(1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, MF_NT + 2, 0);  // first fragments, then the requests
+      if (kt + AHEAD < KT) {
+        issue_a(kt + AHEAD);
+        issue_b(kt + AHEAD);
       }
-#pragma unroll
-      for (int t = 1; t < MF_NT; ++t)
-        acc[2 * p][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[ks][t], x0, acc[2 * p][t], 0, 0, 0);
-#pragma unroll
-      for (int t = 0; t < MF_NT; ++t)
-        acc[2 * p + 1][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[ks][t], x1, acc[2 * p + 1][t], 0, 0, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2 * MF_NT - 1, 0);
+  #pragma unroll
+      for (int u = 0; u < 2 * NPA; ++u) {
+        const int ks = u / NPA, p = u % NPA;
+        const bf16x8 x0 = xb[u & 1][0], x1 = xb[u & 1][1];
+        acc[2 * p][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[ks][0], x0, acc[2 * p][0], 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (u + 1 < 2 * NPA) {
+          const int ks1 = (u + 1) / NPA, p1 = (u + 1) % NPA;
+          if (ks1 != ks) {
+  #pragma unroll
+            for (int t = 0; t < MF_NT; ++t) wfr[1][t] = read_b(t, 1);
+            xb[(u + 1) & 1][0] = read_a(2 * p1, 1);
+            xb[(u + 1) & 1][1] = read_a(2 * p1 + 1, 1);
+            __builtin_amdgcn_sched_group_barrier(0x100, MF_NT + 2, 0);
+          } else {
+            xb[(u + 1) & 1][0] = read_a(2 * p1, ks1);
+            xb[(u + 1) & 1][1] = read_a(2 * p1 + 1, ks1);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+          }
+        }
+  #pragma unroll
+        for (int t = 1; t < MF_NT; ++t)
+          acc[2 * p][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[ks][t], x0, acc[2 * p][t], 0, 0, 0);
+  #pragma unroll
+        for (int t = 0; t < MF_NT; ++t)
+          acc[2 * p + 1][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[ks][t], x1, acc[2 * p + 1][t], 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * MF_NT - 1, 0);
+      }
     }
+  };
+  // this wave's sub-tiles wm, wm + 2, ...: those below active_sub hold rows
+  const int wave_sub = active_sub > wm ? (active_sub - wm + 1) / 2 : 0;
+  const int npa = __builtin_amdgcn_readfirstlane((wave_sub + 1) / 2);
+  if constexpr (NP >= 4) {  // chunks of 256 and 320 rows
+    if (npa >= NP) k_loop(std::integral_constant<int, NP>{});
+    else if (npa >= 4) k_loop(std::integral_constant<int, 4>{});
+    else if (npa == 3) k_loop(std::integral_constant<int, 3>{});
+    else if (npa == 2) k_loop(std::integral_constant<int, 2>{});
+    else k_loop(std::integral_constant<int, 1>{});
+  } else {
+    k_loop(std::integral_constant<int, NP>{});
   }
 
   // ---- epilogue: lane holds row l16 of the sub-tile, columns 4*lq .. 4*lq+3 of each tile ----
