@@ -102,7 +102,7 @@ def _check_plan(idx, w, E, cap):
 @pytest.mark.parametrize("T,E,k,cf,hot,seed", [
     (512, 8, 2, 1.25, 0.0, 0), (8192, 64, 2, 1.25, 0.0, 1), (64, 64, 2, 0.0, 0.0, 2), (16, 64, 2, 0.0, 0.0, 3),
     (4096, 64, 2, 1.0, 3.0, 4), (300, 16, 3, 0.5, 2.0, 5), (1000, 4, 1, 0.3, 0.0, 6), (9000, 1, 1, 0.5, 0.0, 7),
-    (3000, 2, 2, 0.1, 0.0, 8), (5, 64, 2, 1.0, 0.0, 9),
+    (3000, 2, 2, 0.1, 0.0, 8), (5, 64, 2, 1.0, 0.0, 9), (8191, 64, 2, 1.25, 0.0, 10), (4097, 64, 2, 1.0, 3.0, 11),
 ])
 def test_plan_is_bit_exact(T, E, k, cf, hot, seed):
     print(f"case T={T} E={E} k={k} cf={cf}", flush=True)
