@@ -115,12 +115,12 @@ def stage_calls(run):
 
     def experts():
         _lib.check(lib.qw_moe_experts(P(lay.x), run.act, P(slot_token), P(kept_offsets), E, D, F, max_rows,
-                                      min(run.capacity, R), *lay.weight_args(), P(slot_weight), P(y), P(exp_ws),
+                                      min(run.capacity, R), *lay.weight_args(), None, P(y), P(exp_ws),
                                       exp_bytes, s), "experts")
 
     def combine():
-        _lib.check(lib.qw_moe_combine(P(y), run.act, P(route_slot), P(run.top_idx), T, K, D, P(run.out), s),
-                   "combine")
+        _lib.check(lib.qw_moe_combine_weighted(P(y), run.act, P(route_slot), P(run.top_idx), P(run.top_w), T, K, D,
+                                               P(run.out), run.act, s), "combine")
 
     return dict(route=route, plan=plan, experts=experts, combine=combine)
 

@@ -376,14 +376,18 @@ int qw_moe_forward(const void* x, int act_dtype, int64_t tokens, int64_t d_model
               slot_weight, route_slot, dropped_token, dropped_expert, totals, pws, plan_ws, s);
     if (st) return st;
   }
+  // The experts store unweighted rows and the combine applies the route
+  // weights: it computes the same bf16(bf16(y) * w) per route that the
+  // expert kernels would store, and the down projection's epilogue then waits
+  // on no weight loads.
   if (max_rows > 0) {
     const int64_t avg = (R + experts - 1) / experts;
     st = qw::experts(x, act_dtype, slot_token, kept_offsets, experts, d_model, d_ff, max_rows, w_format, group_in,
-                     group_ff, gate_w, gate_scales, up_w, up_scales, down_w, down_scales, slot_weight, y, ews, exp_ws,
-                     s, avg < capacity ? avg : capacity, std::min<int64_t>(capacity, R));
+                     group_ff, gate_w, gate_scales, up_w, up_scales, down_w, down_scales, nullptr, y, ews, exp_ws, s,
+                     avg < capacity ? avg : capacity, std::min<int64_t>(capacity, R));
     if (st) return st;
   }
-  return combine(y, act_dtype, route_slot, top_idx, tokens, top_k, d_model, out, s);
+  return combine_weighted(y, act_dtype, route_slot, top_idx, top_w, tokens, top_k, d_model, out, act_dtype, s);
 }
 
 size_t qw_moe_decode_step_workspace_bytes(int64_t tokens, int64_t d_model, int64_t experts, int64_t top_k,

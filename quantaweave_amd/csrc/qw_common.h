@@ -79,14 +79,14 @@ constexpr int kWave = 64;
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
 
-// Round-to-nearest-even float -> bf16 (NaN stays NaN), the rounding torch uses
-// for `.to(torch.bfloat16)`.
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
-}
+// Round-to-nearest-even float -> bf16, the rounding torch uses for
+// `.to(torch.bfloat16)` on non-NaN values: (bits + 0x7fff + lsb) >> 16; a NaN
+// keeps its sign and top payload with the quiet bit set (torch returns one
+// canonical NaN).  gfx950's conversion
+// instruction (v_cvt_pk_bf16_f32, what the cast compiles to) produces exactly
+// these bits for every input, NaNs and denormals included; the bf16 rounding
+// test pins it against the formula.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f)); }
 
 __device__ __forceinline__ float round_to_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 

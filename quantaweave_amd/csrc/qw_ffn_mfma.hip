@@ -305,6 +305,16 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
   }
 
   // ---- epilogue: lane holds row l16 of the sub-tile, columns 4*lq .. 4*lq+3 of each tile ----
+  // DOWN: the route weights of all of this lane's rows are requested together
+  // (one memory round trip, not one per sub-tile).
+  float row_w[GATEUP ? 1 : SUBT];
+  if constexpr (!GATEUP) {
+#pragma unroll
+    for (int i = 0; i < SUBT; ++i) {
+      const int row = min((wm + 2 * i) * 16 + l16, count - 1);
+      row_w[i] = row_weight ? row_weight[r0 + row] : 1.0f;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < SUBT; ++i) {
     const int s = wm + 2 * i;
@@ -338,7 +348,7 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
         }
       }
     } else {
-      const float wgt = row_weight ? row_weight[r0 + row] : 1.0f;
+      const float wgt = row_w[i];
 #pragma unroll
       for (int t = 0; t < MF_NT; ++t) {
         const int col = n0 + wn * 64 + t * 16 + 4 * lq;

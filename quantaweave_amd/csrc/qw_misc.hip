@@ -58,6 +58,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
                                                       const int32_t* __restrict__ top_idx,
                                                       const float* __restrict__ top_w, int K, int D,
                                                       void* __restrict__ out) {
+  // products and sums rounded one by one (no fused multiply-add): the weighted
+  // term is the reference's y * w, rounded before its index_add
+#pragma clang fp contract(off)
   const int t = blockIdx.x;
   int sl[KMAX], ex[KMAX];
   float wt[KMAX];
