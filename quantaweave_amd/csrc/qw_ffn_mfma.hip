@@ -356,8 +356,9 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
         uint32_t pk[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const float a = round_to_bf16(acc[i][t][2 * h]) * wgt;
-          const float c = round_to_bf16(acc[i][t][2 * h + 1]) * wgt;
+          // without weights bf16(bf16(v) * 1) is bf16(v): one rounding
+          const float a = row_weight ? round_to_bf16(acc[i][t][2 * h]) * wgt : acc[i][t][2 * h];
+          const float c = row_weight ? round_to_bf16(acc[i][t][2 * h + 1]) * wgt : acc[i][t][2 * h + 1];
           pk[h] = f32_to_bf16(a) | (static_cast<uint32_t>(f32_to_bf16(c)) << 16);
         }
         *reinterpret_cast<uint2*>(out + orow + col) = make_uint2(pk[0], pk[1]);
