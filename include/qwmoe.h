@@ -141,10 +141,33 @@ int qw_moe_experts(const void* x, int act_dtype, const int32_t* row_index, const
                    const void* up_w, const float* up_scales, const void* down_w, const float* down_scales,
                    const float* row_weight, void* y, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Kernel families of the grouped SwiGLU (qw_moe_experts_on_path). */
+enum qw_ffn_path {
+  QW_PATH_AUTO = 0,    /* what qw_moe_experts picks for the shape */
+  QW_PATH_GENERAL = 1, /* the general kernel: every format and shape */
+  QW_PATH_MFMA = 2,    /* the matrix-core prefill kernels */
+  QW_PATH_STREAM = 3   /* the weight-streaming decode kernels */
+};
+
+/* qw_moe_experts with the kernel family chosen by the caller instead of by
+ * the row count.  A family that does not take the given formats or shape
+ * returns QW_ERR_UNSUPPORTED and launches nothing.  Every family computes
+ * the same arithmetic (fp32 accumulation, the same rounding points), so
+ * results agree within accumulation order.  No reference counterpart: it
+ * lets a caller or a test pin one kernel (the reference's grouped executor
+ * has a single Triton kernel, src/moe_kernels.py:186-195). */
+int qw_moe_experts_on_path(int path, const void* x, int act_dtype, const int32_t* row_index,
+                           const int32_t* kept_offsets, int64_t experts, int64_t d_model, int64_t d_ff,
+                           int64_t max_rows, int64_t max_rows_per_expert, int w_format, int64_t group_in,
+                           int64_t group_ff, const void* gate_w, const float* gate_scales, const void* up_w,
+                           const float* up_scales, const void* down_w, const float* down_scales,
+                           const float* row_weight, void* y, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Weighted combine.  Replaces `output.index_add_(0, tokens, expert_output)`
  * (src/quantweave_moe_model.py:192, :200-201, :210-211): out[t] starts at zero
  * and adds y[route_slot[t*k+j]] of every kept route of token t in ascending
- * expert order, rounding to `dtype` after each add.  out: [tokens, d_model]. */
+ * expert order (the plan order of `tokens`) in fp32, rounded to `dtype` once,
+ * as torch's index_add_ does for a bf16 output.  out: [tokens, d_model]. */
 int qw_moe_combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, int64_t tokens,
                    int64_t top_k, int64_t d_model, void* out, void* stream);
 
@@ -232,6 +255,17 @@ int qw_grouped_matmul(const void* x, int act_dtype, const void* w, int w_format,
                       int64_t experts, int64_t out_features, int64_t in_features, const int32_t* offsets,
                       int64_t rows, int64_t max_rows_per_expert, void* out, void* stream);
 
+/* The accumulation of the capacity-free static dispatch, replacing the loop
+ * of TopKMoE._static_output (src/quantweave_moe_model.py:235-245):
+ * out[t] = sum over the routes of t in ascending expert order of
+ * y[slot] * top_w.to(out_dtype), each product and each add rounded to
+ * out_dtype (`output = output + expert(x) * dense_weights[:, e].to(dtype)`;
+ * the experts a token does not use add exact zeros).  y holds the unweighted
+ * expert rows of a capacity-free plan. */
+int qw_moe_combine_static(const void* y, int y_dtype, const int32_t* route_slot, const int32_t* top_idx,
+                          const float* top_w, int64_t tokens, int64_t top_k, int64_t d_model, void* out,
+                          int out_dtype, void* stream);
+
 /* ------------------------------------------------------------------------
  * Training: the backward pass of the grouped expert matmuls and of the MoE
  * layer's routing and combine.  All gradients are fp32-accumulated; bf16
@@ -286,8 +320,8 @@ int qw_swiglu_backward(const void* grad_hidden, const void* gate, const void* up
 /* Combine with router weights and a separate output dtype,
  * `output.index_add_(0, tokens, (expert_output * weights[:, None]).to(out))`
  * (src/quantweave_moe_model.py:201-202): out[t] = sum over the kept routes of
- * t in ascending expert order of (y[slot] * top_w).to(out_dtype), rounded to
- * out_dtype after every add.  top_w == NULL: weight 1 (then this is also the
+ * t in ascending expert order of (y[slot] * top_w).to(out_dtype), added in
+ * fp32 and rounded to out_dtype once.  top_w == NULL: weight 1 (then this is also the
  * backward of the row gather flat[tokens], :192, with out_dtype fp32). */
 int qw_moe_combine_weighted(const void* y, int y_dtype, const int32_t* route_slot, const int32_t* top_idx,
                             const float* top_w, int64_t tokens, int64_t top_k, int64_t d_model, void* out,

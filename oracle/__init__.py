@@ -296,8 +296,26 @@ def experts_forward(x_rows: np.ndarray, kept_counts: np.ndarray, w: dict, dtype:
 
 def combine(y_rows: np.ndarray, slot_token: np.ndarray, slot_weight: np.ndarray, tokens: int, dtype: str) -> np.ndarray:
     """src/quantweave_moe_model.py:192, :210-211: `(Y * weights[:, None])` in
-    fp32, `.to(dtype)`, then index_add_ in plan order with one rounding per add."""
+    fp32, `.to(dtype)`, then `zeros.index_add_(0, tokens, ...)`: torch adds
+    the rows into a float32 accumulator in the order of `tokens` (plan order)
+    and rounds to `dtype` once at the end (what its CPU kernel does for a
+    bf16 output; identical to a rounding per add when a token has at most two
+    routes)."""
     contrib = round_act(y_rows.astype(np.float32) * slot_weight[:, None].astype(np.float32), dtype)
+    acc = np.zeros((tokens, y_rows.shape[1]), dtype=np.float32)
+    for s, t in enumerate(slot_token.tolist()):
+        acc[t] = acc[t] + contrib[s]
+    return round_act(acc, dtype)
+
+
+def combine_static(y_rows: np.ndarray, slot_token: np.ndarray, slot_weight: np.ndarray, tokens: int,
+                   dtype: str) -> np.ndarray:
+    """src/quantweave_moe_model.py:235-245 (TopKMoE._static_output): the dense
+    weights cast to `dtype` before the product, `output = output + term`
+    rounded to `dtype` after every add, experts in ascending order (the plan
+    order of a token's routes; experts it does not use add exact zeros)."""
+    w = round_act(np.asarray(slot_weight, np.float32), dtype)
+    contrib = round_act(y_rows.astype(np.float32) * w[:, None], dtype)
     out = np.zeros((tokens, y_rows.shape[1]), dtype=np.float32)
     for s, t in enumerate(slot_token.tolist()):
         out[t] = round_act(out[t] + contrib[s], dtype)

@@ -15,6 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libqwmoe.so"
 
 QW_F32, QW_BF16, QW_I8, QW_U4, QW_BF16T = 0, 1, 2, 3, 4
 QW_OK, QW_ERR_INVALID, QW_ERR_UNSUPPORTED, QW_ERR_HIP, QW_ERR_WORKSPACE = 0, -1, -2, -3, -4
+QW_PATH_AUTO, QW_PATH_GENERAL, QW_PATH_MFMA, QW_PATH_STREAM = 0, 1, 2, 3
 
 P = ctypes.c_void_p
 I32, I64, F32, F64, SZ = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_double, ctypes.c_size_t
@@ -32,6 +33,8 @@ SIGNATURES = {
     "qw_moe_permute": (I32, [P, I32, I64, P, P, I64, P, P]),
     "qw_moe_experts_workspace_bytes": (SZ, [I64, I64, I64, I64, I32]),
     "qw_moe_experts": (I32, [P, I32, P, P, I64, I64, I64, I64, I64, I32, I64, I64, P, P, P, P, P, P, P, P, P, SZ, P]),
+    "qw_moe_experts_on_path": (I32, [I32, P, I32, P, P, I64, I64, I64, I64, I64, I32, I64, I64, P, P, P, P, P, P,
+                                     P, P, P, SZ, P]),
     "qw_moe_combine": (I32, [P, I32, P, P, I64, I64, I64, P, P]),
     "qw_moe_balance": (I32, [P, P, I64, I64, I64, P, P, P]),
     "qw_moe_forward_workspace_bytes": (SZ, [I64, I64, I64, I64, I64, I32]),
@@ -44,6 +47,7 @@ SIGNATURES = {
     "qw_dequantize": (I32, [P, P, I32, I64, I64, I64, P, P]),
     "qw_pack_bf16_tiles": (I32, [P, I64, I64, I64, P, P]),
     "qw_grouped_matmul": (I32, [P, I32, P, I32, P, I64, I64, I64, I64, P, I64, I64, P, P]),
+    "qw_moe_combine_static": (I32, [P, I32, P, P, P, I64, I64, I64, P, I32, P]),
     "qw_grouped_matmul_backward_workspace_bytes": (SZ, [I64, I64, I64, I64, I32]),
     "qw_grouped_matmul_backward": (I32, [P, P, P, I32, I64, I64, I64, P, I64, I64, P, I32, P, I32, P, SZ, P]),
     "qw_moe_experts_save": (I32, [P, I32, P, P, I64, I64, I64, I64, I64, I32, I64, I64, P, P, P, P, P, P, P, P,

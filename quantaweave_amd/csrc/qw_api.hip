@@ -1,5 +1,6 @@
 // C ABI entry points (include/qwmoe.h): argument checks, workspace carving and
 // kernel selection.  No entry point allocates device memory or synchronises.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -60,6 +61,8 @@ int grouped_matmul_generic(const void* x, int act, const WView& w, int wfmt, int
                            int64_t rows, void* out, hipStream_t stream);
 int combine_weighted(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, const float* top_w,
                      int64_t T, int64_t K, int64_t D, void* out, int out_dtype, hipStream_t stream);
+int combine_static(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, const float* top_w,
+                   int64_t T, int64_t K, int64_t D, void* out, int out_dtype, hipStream_t stream);
 int grouped_matmul_backward(const void* gy, const void* x, const void* w, int dtype, int64_t E, int64_t N, int64_t K,
                             const int32_t* offsets, int64_t rows, int64_t max_rows_per_expert, void* gx, int accumulate,
                             void* gw, int gw_dtype, void* ws, size_t ws_bytes, hipStream_t stream);
@@ -77,16 +80,6 @@ int route_backward(const float* probs, const int32_t* top_idx, const float* top_
                    const float* grad_probs, const float* grad_balance, const int32_t* counts, int64_t T, int64_t E,
                    int64_t K, float temperature, float* out, hipStream_t stream);
 
-// Kernel-path override for testing the general kernel on any shape:
-// QW_FFN_PATH=generic.  Read once per process.
-static int ffn_path_override() {
-  static const int v = [] {
-    const char* s = std::getenv("QW_FFN_PATH");
-    return (s && std::strcmp(s, "generic") == 0) ? 1 : 0;
-  }();
-  return v;
-}
-
 static size_t act_size(int dt) { return dt == QW_F32 ? 4 : 2; }
 
 size_t experts_workspace_bytes(int64_t max_rows, int64_t E, int64_t D, int64_t F, int act) {
@@ -102,7 +95,8 @@ int experts(const void* x, int act, const int32_t* row_index, const int32_t* off
             const void* up_w, const float* up_s, const void* down_w, const float* down_s, const float* row_weight,
             void* y, void* ws, size_t ws_bytes, hipStream_t stream, int64_t avg_rows, int64_t row_cap,
             void* save_gate = nullptr, void* save_up = nullptr, void* save_y = nullptr,
-            void* hidden_out = nullptr) {
+            void* hidden_out = nullptr, int path = QW_PATH_AUTO) {
+  QW_REQUIRE(path >= QW_PATH_AUTO && path <= QW_PATH_STREAM, "unknown kernel path %d", path);
   QW_REQUIRE(act == QW_F32 || act == QW_BF16, "activation dtype must be f32 or bf16");
   QW_REQUIRE(wfmt >= QW_F32 && wfmt <= QW_BF16T, "unknown weight format %d", wfmt);
   QW_REQUIRE(E >= 1 && E <= 65535, "experts out of range");
@@ -145,14 +139,28 @@ int experts(const void* x, int act, const int32_t* row_index, const int32_t* off
   a.y = y;
   a.avg_rows = avg_rows;
   a.row_cap = row_cap;
-  if (!ffn_path_override()) {
-    bool handled = false;
-    int st = launch_ffn_gemv(a, stream, &handled);
-    if (st || handled) return st;
-    st = launch_ffn_mfma(a, stream, &handled);
-    if (st || handled) return st;
+  bool handled = false;
+  int st = QW_OK;
+  switch (path) {
+    case QW_PATH_GENERAL:
+      return launch_ffn_generic(a, stream);
+    case QW_PATH_STREAM:
+      a.avg_rows = 0;  // the family is chosen: no row-count threshold
+      st = launch_ffn_gemv(a, stream, &handled);
+      if (st || handled) return st;
+      return set_error(QW_ERR_UNSUPPORTED, "the weight-streaming kernels do not take this shape or format");
+    case QW_PATH_MFMA:
+      a.avg_rows = std::max<int64_t>(a.avg_rows, 16);
+      st = launch_ffn_mfma(a, stream, &handled);
+      if (st || handled) return st;
+      return set_error(QW_ERR_UNSUPPORTED, "the matrix-core kernels do not take this shape or format");
+    default:
+      st = launch_ffn_gemv(a, stream, &handled);
+      if (st || handled) return st;
+      st = launch_ffn_mfma(a, stream, &handled);
+      if (st || handled) return st;
+      return launch_ffn_generic(a, stream);
   }
-  return launch_ffn_generic(a, stream);
 }
 
 size_t forward_workspace_bytes(int64_t T, int64_t D, int64_t E, int64_t K, int64_t F, int act) {
@@ -307,6 +315,22 @@ int qw_moe_experts(const void* x, int act_dtype, const int32_t* row_index, const
   return qw::experts(x, act_dtype, row_index, kept_offsets, experts, d_model, d_ff, max_rows, w_format, group_in,
                      group_ff, gate_w, gate_scales, up_w, up_scales, down_w, down_scales, row_weight, y, workspace,
                      workspace_bytes, as_stream(stream), avg, cap);
+}
+
+int qw_moe_experts_on_path(int path, const void* x, int act_dtype, const int32_t* row_index,
+                           const int32_t* kept_offsets, int64_t experts, int64_t d_model, int64_t d_ff,
+                           int64_t max_rows, int64_t max_rows_per_expert, int w_format, int64_t group_in,
+                           int64_t group_ff, const void* gate_w, const float* gate_scales, const void* up_w,
+                           const float* up_scales, const void* down_w, const float* down_scales,
+                           const float* row_weight, void* y, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  QW_REQUIRE(max_rows_per_expert >= 0, "max_rows_per_expert must be >= 0");
+  const int64_t cap = (max_rows_per_expert > 0 && max_rows_per_expert < max_rows) ? max_rows_per_expert : max_rows;
+  int64_t avg = experts > 0 ? (max_rows + experts - 1) / experts : 0;
+  if (avg > cap) avg = cap;
+  return qw::experts(x, act_dtype, row_index, kept_offsets, experts, d_model, d_ff, max_rows, w_format, group_in,
+                     group_ff, gate_w, gate_scales, up_w, up_scales, down_w, down_scales, row_weight, y, workspace,
+                     workspace_bytes, as_stream(stream), avg, cap, nullptr, nullptr, nullptr, nullptr, path);
 }
 
 int qw_moe_combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, int64_t tokens,
@@ -515,6 +539,14 @@ int qw_moe_combine_weighted(const void* y, int y_dtype, const int32_t* route_slo
   clear_error();
   return combine_weighted(y, y_dtype, route_slot, top_idx, top_w, tokens, top_k, d_model, out, out_dtype,
                           as_stream(stream));
+}
+
+int qw_moe_combine_static(const void* y, int y_dtype, const int32_t* route_slot, const int32_t* top_idx,
+                          const float* top_w, int64_t tokens, int64_t top_k, int64_t d_model, void* out,
+                          int out_dtype, void* stream) {
+  clear_error();
+  return combine_static(y, y_dtype, route_slot, top_idx, top_w, tokens, top_k, d_model, out, out_dtype,
+                        as_stream(stream));
 }
 
 size_t qw_grouped_matmul_backward_workspace_bytes(int64_t experts, int64_t out_features, int64_t in_features,

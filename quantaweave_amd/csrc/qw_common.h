@@ -291,6 +291,16 @@ __device__ int block_exclusive_scan(int v, int* warp_tot, int* total) {
 
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
 
+// silu(gate) * up with the rounding points of tensors held in activation dtype
+// DT: gate and up are rounded (they are stored projections), silu(gate) is
+// rounded, and the caller rounds the product when it stores it.
+template <int DT>
+__device__ __forceinline__ float swiglu_act(float g, float u) {
+  const float gr = round_act<DT>(g);
+  return round_act<DT>(silu_f32(gr)) * round_act<DT>(u);
+}
+__device__ __forceinline__ float swiglu_bf16(float g, float u) { return swiglu_act<QW_BF16>(g, u); }
+
 // Workgroup barrier that orders LDS only.  __syncthreads() also waits for every
 // outstanding global load of the wave (vmcnt(0)); this one lets global loads
 // stay in flight across the barrier.

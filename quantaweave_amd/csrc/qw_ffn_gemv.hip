@@ -153,7 +153,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 // chunks' scales) and the staging area of the outputs of one pass.
 constexpr int GV_GPW_MAX = 8;  // groups per wave, at most
 
-template <int WF, int UNITS, int ROWS, int CPL, int MAXM>
+template <int WF, int UNITS, int ROWS, int CPL, int MAXM, bool SAVE = false>
 struct GvLds {
   static constexpr int NCH = UNITS * ROWS * CPL;                 // chunk loads per group
   static_assert(NCH == 4 || NCH == 8, "the ring reads four or eight chunks per group");
@@ -161,7 +161,9 @@ struct GvLds {
   static constexpr int STAGE = NCH * 1024 + (QUANT ? NCH * 256 : 0);
   static constexpr int STAGES = 2;
   static constexpr int NDMA = NCH * (QUANT ? 2 : 1);             // DMA instructions per group
-  static constexpr int OUT = GV_GPW_MAX * UNITS * MAXM * 4;      // staged outputs (fp32)
+  // staged outputs (fp32): per value one output, or with SAVE on gate/up rows
+  // three (the SiLU product, the gate and the up projection)
+  static constexpr int OUT = GV_GPW_MAX * UNITS * MAXM * 4 * (SAVE && ROWS == 2 ? 3 : 1);
   static constexpr int WAVE = STAGES * STAGE + OUT;
 };
 
@@ -295,11 +297,14 @@ __device__ __forceinline__ int nth_active_expert(const int32_t* __restrict__ off
 // from L2 once per pass, are prepared once and kept in registers while the
 // wave walks its groups.  Outputs are staged in the wave's LDS and stored once
 // the pass is done (a store between the ring loads would break the counts).
-template <int WF, bool GATEUP, int UNITS, int CPL, int MAXM>
+// SAVE (training): gate/up also stores the gate and up projections (save_a,
+// save_b); down also stores the rows before their row weight (save_a).
+template <int WF, bool GATEUP, int UNITS, int CPL, int MAXM, bool SAVE>
 __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
     int n_experts, int max_rows, WView wa, WView wb, int K, int n_out, int gpw,
-    const float* __restrict__ row_weight, uint16_t* __restrict__ out) {
+    const float* __restrict__ row_weight, uint16_t* __restrict__ out, uint16_t* __restrict__ save_a,
+    uint16_t* __restrict__ save_b) {
   constexpr int MW = math_fmt(WF);
   constexpr bool TILED = WF == QW_BF16T;
   constexpr int CW = Fmt<WF>::CW;
@@ -309,7 +314,8 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
   constexpr int V = UNITS * ROWS * MAXM;  // values reduced per group
   constexpr int L = log2i<V>();
   constexpr int OUTS = UNITS * MAXM;      // outputs per group
-  using LD = GvLds<WF, UNITS, ROWS, CPL, MAXM>;
+  using LD = GvLds<WF, UNITS, ROWS, CPL, MAXM, SAVE>;
+  constexpr int SLOTS = GV_GPW_MAX * OUTS;  // staged values of one kind per wave
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   int r_lo = 0, r_hi = 0;
   const int e = nth_active_expert(offsets, n_experts, max_rows, blockIdx.y, &r_lo, &r_hi);
@@ -491,7 +497,13 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
       float* slot = staged + (g - g_first) * OUTS + um;
       if constexpr (GATEUP) {
         const float up = __shfl_xor(r, 1 << (6 - L), kWave);  // the up row of the same unit and route
-        if ((lane & ((2 << (6 - L)) - 1)) == 0) *slot = silu_f32(r) * up;
+        if ((lane & ((2 << (6 - L)) - 1)) == 0) {
+          *slot = swiglu_bf16(r, up);
+          if constexpr (SAVE) {
+            slot[SLOTS] = r;
+            slot[2 * SLOTS] = up;
+          }
+        }
       } else {
         if ((lane & ((1 << (6 - L)) - 1)) == 0) *slot = r;
       }
@@ -506,11 +518,17 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
       if (m >= M || n >= n_out) continue;
       const int srow = m0 + m;
       const float val = staged[v];
+      const int64_t o = static_cast<int64_t>(srow) * n_out + n;
       if constexpr (GATEUP) {
-        out[static_cast<int64_t>(srow) * n_out + n] = f32_to_bf16(val);
+        out[o] = f32_to_bf16(val);
+        if constexpr (SAVE) {
+          save_a[o] = f32_to_bf16(staged[SLOTS + v]);
+          save_b[o] = f32_to_bf16(staged[2 * SLOTS + v]);
+        }
       } else {
         const float wgt = row_weight ? row_weight[srow] : 1.0f;
-        out[static_cast<int64_t>(srow) * n_out + n] = f32_to_bf16(round_to_bf16(val) * wgt);
+        out[o] = f32_to_bf16(round_to_bf16(val) * wgt);
+        if constexpr (SAVE) save_a[o] = f32_to_bf16(val);
       }
     }
   }
@@ -527,15 +545,15 @@ static int groups_per_wave(int64_t touched, int64_t n_groups) {
   return 1;
 }
 
-template <int WF, bool GATEUP, int UNITS, int CPL>
-int launch_one(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
-               int n_out, const float* row_weight, void* out, hipStream_t stream) {
+template <int WF, bool GATEUP, int UNITS, int CPL, bool SAVE>
+int launch_save(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
+                int n_out, const float* row_weight, void* out, void* save_a, void* save_b, hipStream_t stream) {
   // routes per pass: int4 activation pieces are 4x larger per chunk than bf16 ones
   constexpr int MAXM = WF == QW_U4 ? 2 : 4;
-  using LD = GvLds<WF, UNITS, GATEUP ? 2 : 1, CPL, MAXM>;
+  using LD = GvLds<WF, UNITS, GATEUP ? 2 : 1, CPL, MAXM, SAVE>;
   constexpr size_t lds = static_cast<size_t>(GV_WAVES) * LD::WAVE;
-  auto kernel = ffn_gemv_kernel<WF, GATEUP, UNITS, CPL, MAXM>;
-  const hipError_t attr = reserve_lds<ffn_gemv_kernel<WF, GATEUP, UNITS, CPL, MAXM>>(static_cast<int>(lds));
+  auto kernel = ffn_gemv_kernel<WF, GATEUP, UNITS, CPL, MAXM, SAVE>;
+  const hipError_t attr = reserve_lds<ffn_gemv_kernel<WF, GATEUP, UNITS, CPL, MAXM, SAVE>>(static_cast<int>(lds));
   if (attr != hipSuccess)
     return set_error(QW_ERR_HIP, "cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(attr));
   const int64_t n_groups = ceil_div(n_out, UNITS);
@@ -545,31 +563,51 @@ int launch_one(const FfnArgs& a, const WView& wa, const WView& wb, const void* x
   const dim3 grid(static_cast<unsigned>(ceil_div(waves, GV_WAVES)), static_cast<unsigned>(touched));
   kernel<<<grid, GV_WAVES * 64, lds, stream>>>(static_cast<const uint16_t*>(x), row_index, a.offsets,
                                                static_cast<int>(a.experts), static_cast<int>(a.max_rows), wa, wb, K,
-                                               n_out, gpw, row_weight, static_cast<uint16_t*>(out));
+                                               n_out, gpw, row_weight, static_cast<uint16_t*>(out),
+                                               static_cast<uint16_t*>(save_a), static_cast<uint16_t*>(save_b));
   QW_LAUNCH_CHECK(GATEUP ? "ffn_gemv_kernel<gateup>" : "ffn_gemv_kernel<down>");
   return QW_OK;
+}
+
+// The saving variants exist for bf16 weights only (quantised experts do not train).
+template <int WF, bool GATEUP, int UNITS, int CPL>
+int launch_one(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
+               int n_out, const float* row_weight, void* out, void* save_a, void* save_b, hipStream_t stream) {
+  if constexpr (!quantized(WF)) {
+    if (save_a)
+      return launch_save<WF, GATEUP, UNITS, CPL, true>(a, wa, wb, x, row_index, K, n_out, row_weight, out, save_a,
+                                                       save_b, stream);
+  }
+  return launch_save<WF, GATEUP, UNITS, CPL, false>(a, wa, wb, x, row_index, K, n_out, row_weight, out, nullptr,
+                                                    nullptr, stream);
 }
 
 // Units per group for a row of CPL chunks per lane: 4 weight chunks (16-byte
 // loads) per lane and group (8 for gate/up rows of more than 128 chunks).
 template <int WF, bool GATEUP>
 int launch_cpl(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
-               int n_out, const float* row_weight, void* out, hipStream_t stream) {
+               int n_out, const float* row_weight, void* out, void* save_a, void* save_b, hipStream_t stream) {
   const int KC = K / Fmt<WF>::CW;
   const int cpl = static_cast<int>(ceil_div(KC, 64));
   constexpr int U1 = GATEUP ? 2 : 4;
-  if (cpl <= 1) return launch_one<WF, GATEUP, U1, 1>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
-  if (cpl <= 2) return launch_one<WF, GATEUP, U1 / 2, 2>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
-  if (cpl <= 4) return launch_one<WF, GATEUP, 1, 4>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+  if (cpl <= 1)
+    return launch_one<WF, GATEUP, U1, 1>(a, wa, wb, x, row_index, K, n_out, row_weight, out, save_a, save_b, stream);
+  if (cpl <= 2)
+    return launch_one<WF, GATEUP, U1 / 2, 2>(a, wa, wb, x, row_index, K, n_out, row_weight, out, save_a, save_b,
+                                             stream);
+  if (cpl <= 4)
+    return launch_one<WF, GATEUP, 1, 4>(a, wa, wb, x, row_index, K, n_out, row_weight, out, save_a, save_b, stream);
   return set_error(QW_ERR_UNSUPPORTED, "row of %d chunks is too long for the decode kernel", KC);
 }
 
 template <int WF>
 int launch_fmt(const FfnArgs& a, hipStream_t stream) {
   const int D = static_cast<int>(a.d_model), F = static_cast<int>(a.d_ff);
-  int st = launch_cpl<WF, true>(a, a.gate, a.up, a.x, a.row_index, D, F, nullptr, a.hidden, stream);
+  int st = launch_cpl<WF, true>(a, a.gate, a.up, a.x, a.row_index, D, F, nullptr, a.hidden, a.save_gate, a.save_up,
+                                stream);
   if (st) return st;
-  return launch_cpl<WF, false>(a, a.down, a.down, a.hidden, nullptr, F, D, a.row_weight, a.y, stream);
+  return launch_cpl<WF, false>(a, a.down, a.down, a.hidden, nullptr, F, D, a.row_weight, a.y, a.save_y, nullptr,
+                               stream);
 }
 
 }  // namespace
@@ -577,7 +615,7 @@ int launch_fmt(const FfnArgs& a, hipStream_t stream) {
 int launch_ffn_gemv(const FfnArgs& a, hipStream_t stream, bool* handled) {
   *handled = false;
   if (a.act != QW_BF16 || a.avg_rows >= 16) return QW_OK;
-  if (a.save_gate || a.save_y) return QW_OK;  // saving activations: MFMA or general kernels
+  if ((a.save_gate || a.save_y) && quantized(a.wfmt)) return QW_OK;  // quantised experts do not train
   int cw = 0;
   if (a.wfmt == QW_U4) {
     if (a.gate.group % 32 || a.down.group % 32) return QW_OK;

@@ -96,7 +96,7 @@ __global__ __launch_bounds__(256) void ffn_generic_kernel(const void* __restrict
           const float g = round_act<ACT>(os[m][c]);
           const float u = round_act<ACT>(os[m][c + COLS]);
           const int64_t o = static_cast<int64_t>(s) * N_out + c0 + c;
-          store_act<ACT>(out, o, silu_f32(g) * u);
+          store_act<ACT>(out, o, swiglu_act<ACT>(g, u));
           if (save_a) {  // gate and up projections, for the backward pass
             store_act<ACT>(save_a, o, g);
             store_act<ACT>(save_b, o, u);

@@ -330,8 +330,10 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
         uint32_t pk[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const float a = silu_f32(acc[i][t][2 * h]) * acc[i][t + MF_NT / 2][2 * h];
-          const float c = silu_f32(acc[i][t][2 * h + 1]) * acc[i][t + MF_NT / 2][2 * h + 1];
+          // the reference's bf16 tensors: gate, up and silu(gate) are each
+          // rounded to bf16 before the product (src/moe_kernels.py:194)
+          const float a = swiglu_bf16(acc[i][t][2 * h], acc[i][t + MF_NT / 2][2 * h]);
+          const float c = swiglu_bf16(acc[i][t][2 * h + 1], acc[i][t + MF_NT / 2][2 * h + 1]);
           pk[h] = f32_to_bf16(a) | (static_cast<uint32_t>(f32_to_bf16(c)) << 16);
         }
         *reinterpret_cast<uint2*>(out + orow + col) = make_uint2(pk[0], pk[1]);

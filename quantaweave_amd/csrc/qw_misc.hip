@@ -41,25 +41,34 @@ int permute(const void* x, int dtype, int64_t D, const int32_t* slot_token, cons
 }
 
 // ---------------------------------------------------------------------------
-// Combine: out[t] = sum over kept routes of t, in ascending expert order, with
-// a rounding to the output dtype after every add — the arithmetic of
-// `zeros_like(flat).index_add_(0, tokens, y)` on expert-ordered rows
-// (src/quantweave_moe_model.py:192, :201, :211).  One block per token.
+// Combine: out[t] = the kept routes of t added in ascending expert order (the
+// plan order of `tokens`) in fp32, starting from zero, and rounded to the
+// output dtype once — the arithmetic of torch's
+// `zeros_like(flat).index_add_(0, tokens, y)` (src/quantweave_moe_model.py:192,
+// :201, :211), which for a bf16 output accumulates in fp32 in index order and
+// rounds at the end.  One block per token.
 // WEIGHTED: each row enters as (y * w).to(out dtype), w the route's router
 // weight — `expert_output * weights[:, None]` (:201) with unweighted rows.
 // The same kernel with weights off and OUT = fp32 is the backward of the row
 // gather flat[tokens] (:192): index_add of the rows' gradients.
 // ---------------------------------------------------------------------------
+// STATIC: the accumulation of the capacity-free static dispatch
+// (TopKMoE._static_output, src/quantweave_moe_model.py:235-245): the route
+// weight is cast to the output dtype before the product
+// (`dense_weights[:, e].to(flat_hidden.dtype)`), and `output = output + term`
+// rounds after every add, expert by expert in ascending order (the experts
+// with weight zero add exact zeros and are skipped).
 // KMAX >= K bounds the routes per token; the token's kept routes are put in
 // ascending expert order in registers (a static ranking network, no indexed
 // private memory).
-template <int ACT, int OUT, int VEC, int KMAX, bool WEIGHTED>
+template <int ACT, int OUT, int VEC, int KMAX, bool WEIGHTED, bool STATIC = false>
 __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y, const int32_t* __restrict__ route_slot,
                                                       const int32_t* __restrict__ top_idx,
                                                       const float* __restrict__ top_w, int K, int D,
                                                       void* __restrict__ out) {
   // products and sums rounded one by one (no fused multiply-add): the weighted
-  // term is the reference's y * w, rounded before its index_add
+  // term is the reference's y * w, rounded to the output dtype before its
+  // index_add; the sum is rounded when it is stored
 #pragma clang fp contract(off)
   const int t = blockIdx.x;
   int sl[KMAX], ex[KMAX];
@@ -69,6 +78,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
     sl[j] = j < K ? route_slot[static_cast<int64_t>(t) * K + j] : -1;
     ex[j] = j < K ? top_idx[static_cast<int64_t>(t) * K + j] : 0;
     wt[j] = (WEIGHTED && j < K) ? top_w[static_cast<int64_t>(t) * K + j] : 1.0f;
+    if (STATIC) wt[j] = round_act<OUT>(wt[j]);
   }
   // rank of each kept route among the kept routes by expert id (experts of a token are distinct)
   int rk[KMAX];
@@ -108,7 +118,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
 #pragma unroll
         for (int v = 0; v < VEC; ++v) {
           const float term = WEIGHTED ? round_act<OUT>(yv[v] * wsl[j]) : yv[v];
-          acc[v] = round_act<OUT>(acc[v] + term);
+          acc[v] = STATIC ? round_act<OUT>(acc[v] + term) : acc[v] + term;
         }
       }
     }
@@ -116,54 +126,74 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
   }
 }
 
-template <int ACT, int OUT, int KMAX, bool WEIGHTED>
+template <int ACT, int OUT, int KMAX, bool WEIGHTED, bool STATIC>
 void launch_combine_vec(const void* y, const int32_t* route_slot, const int32_t* top_idx, const float* top_w,
                         unsigned g, int k, int d, void* out, hipStream_t stream) {
   constexpr int V = (ACT == QW_BF16 || OUT == QW_BF16) ? 8 : 4;
   if (d % V == 0)
-    combine_kernel<ACT, OUT, V, KMAX, WEIGHTED><<<g, 256, 0, stream>>>(y, route_slot, top_idx, top_w, k, d, out);
+    combine_kernel<ACT, OUT, V, KMAX, WEIGHTED, STATIC>
+        <<<g, 256, 0, stream>>>(y, route_slot, top_idx, top_w, k, d, out);
   else
-    combine_kernel<ACT, OUT, 1, KMAX, WEIGHTED><<<g, 256, 0, stream>>>(y, route_slot, top_idx, top_w, k, d, out);
+    combine_kernel<ACT, OUT, 1, KMAX, WEIGHTED, STATIC>
+        <<<g, 256, 0, stream>>>(y, route_slot, top_idx, top_w, k, d, out);
 }
 
-template <int KMAX, bool WEIGHTED>
+template <int KMAX, bool WEIGHTED, bool STATIC>
 int launch_combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, const float* top_w,
                    unsigned g, int k, int d, void* out, int out_dtype, hipStream_t stream) {
   if (dtype == QW_F32 && out_dtype == QW_F32)
-    launch_combine_vec<QW_F32, QW_F32, KMAX, WEIGHTED>(y, route_slot, top_idx, top_w, g, k, d, out, stream);
+    launch_combine_vec<QW_F32, QW_F32, KMAX, WEIGHTED, STATIC>(y, route_slot, top_idx, top_w, g, k, d, out, stream);
   else if (dtype == QW_F32)
-    launch_combine_vec<QW_F32, QW_BF16, KMAX, WEIGHTED>(y, route_slot, top_idx, top_w, g, k, d, out, stream);
+    launch_combine_vec<QW_F32, QW_BF16, KMAX, WEIGHTED, STATIC>(y, route_slot, top_idx, top_w, g, k, d, out, stream);
   else if (out_dtype == QW_F32)
-    launch_combine_vec<QW_BF16, QW_F32, KMAX, WEIGHTED>(y, route_slot, top_idx, top_w, g, k, d, out, stream);
+    launch_combine_vec<QW_BF16, QW_F32, KMAX, WEIGHTED, STATIC>(y, route_slot, top_idx, top_w, g, k, d, out, stream);
   else
-    launch_combine_vec<QW_BF16, QW_BF16, KMAX, WEIGHTED>(y, route_slot, top_idx, top_w, g, k, d, out, stream);
+    launch_combine_vec<QW_BF16, QW_BF16, KMAX, WEIGHTED, STATIC>(y, route_slot, top_idx, top_w, g, k, d, out,
+                                                                 stream);
   QW_LAUNCH_CHECK("combine_kernel");
   return QW_OK;
 }
 
-template <bool WEIGHTED>
+template <bool WEIGHTED, bool STATIC = false>
 int combine_k(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, const float* top_w,
               int64_t T, int64_t K, int64_t D, void* out, int out_dtype, hipStream_t stream) {
   const unsigned g = static_cast<unsigned>(T);
   const int k = static_cast<int>(K), d = static_cast<int>(D);
-  if (K <= 2) return launch_combine<2, WEIGHTED>(y, dtype, route_slot, top_idx, top_w, g, k, d, out, out_dtype, stream);
-  if (K <= 4) return launch_combine<4, WEIGHTED>(y, dtype, route_slot, top_idx, top_w, g, k, d, out, out_dtype, stream);
-  if (K <= 8) return launch_combine<8, WEIGHTED>(y, dtype, route_slot, top_idx, top_w, g, k, d, out, out_dtype, stream);
-  if (K <= 16)
-    return launch_combine<16, WEIGHTED>(y, dtype, route_slot, top_idx, top_w, g, k, d, out, out_dtype, stream);
-  return launch_combine<64, WEIGHTED>(y, dtype, route_slot, top_idx, top_w, g, k, d, out, out_dtype, stream);
+#define QW_CK(N)                                                                                                 \
+  if (K <= N)                                                                                                    \
+    return launch_combine<N, WEIGHTED, STATIC>(y, dtype, route_slot, top_idx, top_w, g, k, d, out, out_dtype, stream);
+  QW_CK(2)
+  QW_CK(4)
+  QW_CK(8)
+  QW_CK(16)
+#undef QW_CK
+  return launch_combine<64, WEIGHTED, STATIC>(y, dtype, route_slot, top_idx, top_w, g, k, d, out, out_dtype, stream);
 }
 
-int combine_weighted(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, const float* top_w,
-                     int64_t T, int64_t K, int64_t D, void* out, int out_dtype, hipStream_t stream) {
+static int combine_check(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, int64_t T,
+                         int64_t K, int64_t D, void* out, int out_dtype) {
   QW_REQUIRE((dtype == QW_F32 || dtype == QW_BF16) && (out_dtype == QW_F32 || out_dtype == QW_BF16),
              "combine dtypes must be f32 or bf16");
   QW_REQUIRE(K >= 1 && K <= 64, "combine supports top_k in [1, 64], got %lld", (long long)K);
   QW_REQUIRE(T >= 0 && T <= INT32_MAX && D >= 1 && D <= INT32_MAX, "bad combine sizes");
+  QW_REQUIRE(T == 0 || (y && route_slot && top_idx && out), "combine pointers are required");
+  return QW_OK;
+}
+
+int combine_weighted(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, const float* top_w,
+                     int64_t T, int64_t K, int64_t D, void* out, int out_dtype, hipStream_t stream) {
+  if (const int st = combine_check(y, dtype, route_slot, top_idx, T, K, D, out, out_dtype)) return st;
   if (T == 0) return QW_OK;
-  QW_REQUIRE(y && route_slot && top_idx && out, "combine pointers are required");
   if (top_w) return combine_k<true>(y, dtype, route_slot, top_idx, top_w, T, K, D, out, out_dtype, stream);
   return combine_k<false>(y, dtype, route_slot, top_idx, nullptr, T, K, D, out, out_dtype, stream);
+}
+
+int combine_static(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, const float* top_w,
+                   int64_t T, int64_t K, int64_t D, void* out, int out_dtype, hipStream_t stream) {
+  if (const int st = combine_check(y, dtype, route_slot, top_idx, T, K, D, out, out_dtype)) return st;
+  QW_REQUIRE(T == 0 || top_w, "the static combine needs the route weights");
+  if (T == 0) return QW_OK;
+  return combine_k<true, true>(y, dtype, route_slot, top_idx, top_w, T, K, D, out, out_dtype, stream);
 }
 
 int combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, int64_t T, int64_t K,

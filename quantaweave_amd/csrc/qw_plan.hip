@@ -16,8 +16,9 @@
 // network for large experts) and writes kept slots and dropped routes at
 // their plan positions.  Keys are unique, so the order inside the gather does
 // not matter and the result does not depend on scheduling.  An expert with
-// more routes than the LDS holds ranks its keys against each other through
-// global memory instead (same result, slower).
+// more routes than the LDS holds gathers its keys into its own slice of the
+// workspace and sorts them there with the same kind of network (same result,
+// slower: one global-memory pass per network stage).
 #include "qw_common.h"
 
 namespace qw {
@@ -56,11 +57,14 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   __shared__ int hist[kWaves][kMaxExperts];
   __shared__ int warp_tot[kWaves];
   __shared__ int s_tot_kept, s_tot_drop, s_tot_routes;
-  __shared__ int s_kept_off, s_drop_off, s_route_off, s_fill;
+  __shared__ int s_kept_off, s_drop_off, s_route_off, s_fill, s_fill_big;
   const int e = blockIdx.x;
   const int tid = threadIdx.x, wave = tid / kWave;
   for (int i = tid; i < kWaves * E; i += kPlanThreads) hist[i / E][i % E] = 0;
-  if (tid == 0) s_fill = 0;
+  if (tid == 0) {
+    s_fill = 0;
+    s_fill_big = 0;
+  }
   __syncthreads();
 
   // ---- one pass over the routes: histogram of all experts, keys of expert e ----
@@ -183,26 +187,53 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     }
     for (int i = tid; i < n; i += blockDim.x) place(keys[i], i);
   } else {
-    // ---- large expert: keys in global scratch, rank by counting ----
+    // ---- large expert: its n keys in its own slice of the workspace (n routes
+    //      of expert e start at s_route_off), sorted there ----
     uint64_t* mine = spill + s_route_off;
-    if (tid == 0) s_fill = 0;
-    __syncthreads();
     for (int r = tid; r < R; r += blockDim.x) {
       if (top_idx[r] == e) {
-        const int p = atomicAdd(&s_fill, 1);
+        const int p = atomicAdd(&s_fill_big, 1);  // its own counter: s_fill is still read above
         mine[p] = route_key(top_w, r);
       }
     }
     __threadfence();
     __syncthreads();
-    // coherent (L1-bypassing) loads: the keys were just written by other waves
-    for (int i = tid; i < n; i += blockDim.x) {
-      const uint64_t k = __hip_atomic_load(&mine[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      int rank = 0;
-      for (int j = 0; j < n; ++j)
-        rank += (__hip_atomic_load(&mine[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < k) ? 1 : 0;
-      place(k, rank);
+    // Bitonic network in the form whose compare-exchanges all put the smaller
+    // key first: the first stage of each merge pairs i with the mirror index
+    // (size - 1 - i within the block), the later ones i with i + stride.
+    // Positions n .. p2-1 stand for +infinity keys: such a key never moves, so
+    // a pair whose upper index is past n is skipped and nothing is padded.
+    // Loads bypass the L1 (the keys were just written by other waves).
+    auto cmpx = [&](int lo, int hi) {
+      if (hi >= n) return;
+      const uint64_t a = __hip_atomic_load(&mine[lo], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint64_t b = __hip_atomic_load(&mine[hi], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (a > b) {
+        mine[lo] = b;
+        mine[hi] = a;
+      }
+    };
+    int p2 = 1;
+    while (p2 < n) p2 <<= 1;
+    for (int size = 2; size <= p2; size <<= 1) {
+      const int half = size >> 1;
+      for (int i = tid; i < p2 / 2; i += blockDim.x) {
+        const int blk = i / half, j = i % half;
+        cmpx(blk * size + j, blk * size + size - 1 - j);
+      }
+      __threadfence();
+      __syncthreads();
+      for (int stride = half >> 1; stride > 0; stride >>= 1) {
+        for (int i = tid; i < p2 / 2; i += blockDim.x) {
+          const int lo = 2 * i - (i & (stride - 1));
+          cmpx(lo, lo + stride);
+        }
+        __threadfence();
+        __syncthreads();
+      }
     }
+    for (int i = tid; i < n; i += blockDim.x)
+      place(__hip_atomic_load(&mine[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), i);
   }
 }
 

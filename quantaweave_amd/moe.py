@@ -289,12 +289,17 @@ class TopKMoE(nn.Module):
         if self.expert_bias is not None:
             bias = self.expert_bias.detach().to(dev, torch.float32).contiguous()
         pack = packed_experts(self, self.experts)
-        # static dispatch is the capacity-free evaluation (src/quantweave_moe_model.py:235-245)
-        cap = T * K if self.static_dispatch else self.capacity(T)
+        # static dispatch is the capacity-free evaluation (src/quantweave_moe_model.py:235-245),
+        # with its own accumulation (route weights cast to the hidden dtype, a rounding per add)
+        static = bool(self.static_dispatch)
+        cap = T * K if static else self.capacity(T)
         cdt = _compute_dtype(flat)
         # per-expert timing (profile_experts) runs the experts one call at a time and
         # records no autograd graph; an input that requires grad keeps the graph instead
         profiling = self.profile_experts and not (hidden.requires_grad and torch.is_grad_enabled())
+        # the loop executor (use_triton_kernels False, set_moe_kernel("loop")) launches
+        # the experts one at a time, as the reference's loop does (:203-209)
+        loop = not self.use_triton_kernels
         if not profiling and self._wants_grad(hidden):
             if pack.fmt not in (_lib.QW_F32, _lib.QW_BF16, _lib.QW_BF16T):
                 if hidden.requires_grad:
@@ -302,17 +307,18 @@ class TopKMoE(nn.Module):
             else:
                 weights = [getattr(e, n).weight for e in self.experts for n in ("gate", "up", "down")]
                 out, probs, balance, top_idx, top_w, counts, kept_counts, totals, dropped_token, dropped_expert = \
-                    _MoELayer.apply(flat, self.router.weight, self, pack, cap, bias, cdt, *weights)
+                    _MoELayer.apply(flat, self.router.weight, self, pack, cap, bias, cdt, loop, static, *weights)
                 return self._finish(out, probs, balance, top_idx, top_w, counts, kept_counts, totals, dropped_token,
                                     dropped_expert, token_domains, num_domains, (batch, sequence, width))
         with torch.no_grad():
             flat = flat.detach().contiguous()
             if profiling:
-                res = _layer_chain(flat, cdt, self.router.weight, self, pack, cap, bias, profile=self.expert_seconds)
-            elif cdt == flat.dtype:
+                res = _layer_chain(flat, cdt, self.router.weight, self, pack, cap, bias, loop=True, static=static,
+                                   profile=self.expert_seconds)
+            elif cdt == flat.dtype and not loop and not static:
                 res = _forward_call(flat, act, self.router.weight, self, pack, cap, bias)
             else:
-                res = _layer_chain(flat, cdt, self.router.weight, self, pack, cap, bias)
+                res = _layer_chain(flat, cdt, self.router.weight, self, pack, cap, bias, loop=loop, static=static)
         return self._finish(res["out"], res["probs"], res["balance"], res["top_idx"], res["top_w"], res["counts"],
                             res["kept_counts"], res["totals"], res["dropped_token"], res["dropped_expert"],
                             token_domains, num_domains, (batch, sequence, width))
@@ -415,23 +421,25 @@ def _compute_dtype(flat: Tensor) -> torch.dtype:
 
 
 def _layer_chain(flat: Tensor, cdt: torch.dtype, router_w: Tensor, moe: TopKMoE, pack: ExpertPack, cap: int,
-                 bias: Optional[Tensor], save: bool = False, profile: Optional[list] = None) -> dict:
+                 bias: Optional[Tensor], save: bool = False, loop: bool = False, static: bool = False,
+                 profile: Optional[list] = None) -> dict:
     """The layer forward as one C call per stage: qw_moe_route (on the input
     dtype, src/quantweave_moe_model.py:126-127), qw_moe_plan, qw_moe_experts
-    on the rows cast to `cdt` and qw_moe_combine, then qw_moe_balance.
-
-    With cdt == flat.dtype the experts scale their rows by the route weights
-    and the combine adds them in that dtype — the stages and arguments of
-    qw_moe_forward, so the output is identical.  With cdt != flat.dtype (bf16
-    autocast on an fp32 stream) the expert rows stay unweighted in bf16 and
-    qw_moe_combine_weighted adds (y * w) in the input dtype, as
-    `(expert_output * weights[:, None]).to(output.dtype)` does (:201).
+    on the rows cast to `cdt` (unweighted rows) and qw_moe_combine_weighted,
+    which forms `(expert_output * weights[:, None]).to(output.dtype)` and adds
+    it in the input dtype (:201), then qw_moe_balance.  With cdt == flat.dtype
+    these are the stages and arguments of qw_moe_forward, so the output is
+    identical; with cdt != flat.dtype (bf16 autocast on an fp32 stream) the
+    rows are bf16 and the weighted sum fp32, as under the reference's autocast.
     save: keep the activations a backward pass reads (qw_moe_experts_save):
-    gate, up, hidden [R, d_ff] and the unweighted expert rows [R, d_model].
-    profile: a list of per-expert seconds; the experts then run one call per
-    expert with rows, each bracketed by synchronisations and its wall time
-    added to the list (the reference's profile_experts,
-    src/quantweave_moe_model.py:220-233)."""
+    gate, up, hidden [R, d_ff]; the unweighted expert rows are `y` itself.
+    loop: the experts run one call per expert with rows (the reference's loop
+    executor, :203-209), after reading the kept counts back to the host as the
+    reference does.  profile: a list of per-expert seconds; each expert call is
+    then bracketed by synchronisations and its wall time added to the list
+    (the reference's profile_experts, src/quantweave_moe_model.py:220-233).
+    static: the combine of the static dispatch, qw_moe_combine_static
+    (`_static_output`, :235-245; the caller passes a capacity-free plan)."""
     dev = flat.device
     T, D = flat.shape
     E, K = moe.num_experts, moe.top_k
@@ -468,11 +476,15 @@ def _layer_chain(flat: Tensor, cdt: torch.dtype, router_w: Tensor, moe: TopKMoE,
     xc = flat.to(cdt) if mixed else flat
     max_rows = min(R, cap * E)
     y = torch.empty(R, D, dtype=cdt, device=dev)
-    nb = lib.qw_moe_experts_workspace_bytes(R if profile is not None else max_rows, E, D, F_, act)
+    if save:
+        for name in ("gate", "up", "hidden"):
+            r[name] = torch.empty(R, F_, dtype=cdt, device=dev)
+        r["y_unweighted"] = y  # the rows carry no route weight: the combine applies it
+    nb = lib.qw_moe_experts_workspace_bytes(R if loop else max_rows, E, D, F_, act)
     ws = _hip.workspace(nb, dev)
-    args = [_hip.ptr(xc), act, p["slot_token"], p["kept_offsets"], E, D, F_, max_rows, min(cap, R),
-            *pack.args_for(act), None if mixed else p["slot_weight"], _hip.ptr(y)]
-    if profile is not None:
+    saved = [_hip.ptr(r[n]) for n in ("gate", "up", "hidden")] + [_hip.ptr(y)] if save else []
+    fn = "qw_moe_experts_save" if save else "qw_moe_experts"
+    if loop:
         import time
 
         kept = r["kept_counts"].tolist()  # host sync, as the reference's loop makes
@@ -481,24 +493,19 @@ def _layer_chain(flat: Tensor, cdt: torch.dtype, router_w: Tensor, moe: TopKMoE,
             if not kept[e]:
                 continue
             offs = ctypes.c_void_p(r["kept_offsets"].data_ptr() + 4 * e)
-            torch.cuda.synchronize(dev)
-            started = time.perf_counter()
-            _lib.call("qw_moe_experts", _hip.ptr(xc), act, p["slot_token"], offs, 1, D, F_, R, min(cap, R),
-                      *weights.expert_args(e), None if mixed else p["slot_weight"], _hip.ptr(y), _hip.ptr(ws), nb, s)
-            torch.cuda.synchronize(dev)
-            profile[e] += time.perf_counter() - started
-    elif save:
-        for name, width in (("gate", F_), ("up", F_), ("hidden", F_), ("y_unweighted", D)):
-            r[name] = torch.empty(R, width, dtype=cdt, device=dev)
-        _lib.call("qw_moe_experts_save", *args, *(_hip.ptr(r[n]) for n in ("gate", "up", "hidden", "y_unweighted")),
-                  _hip.ptr(ws), nb, s)
+            if profile is not None:
+                torch.cuda.synchronize(dev)
+                started = time.perf_counter()
+            _lib.call(fn, _hip.ptr(xc), act, p["slot_token"], offs, 1, D, F_, R, min(cap, R),
+                      *weights.expert_args(e), None, _hip.ptr(y), *saved, _hip.ptr(ws), nb, s)
+            if profile is not None:
+                torch.cuda.synchronize(dev)
+                profile[e] += time.perf_counter() - started
     else:
-        _lib.call("qw_moe_experts", *args, _hip.ptr(ws), nb, s)
-    if mixed:
-        _lib.call("qw_moe_combine_weighted", _hip.ptr(y), act, p["route_slot"], p["top_idx"], p["top_w"], T, K, D,
-                  p["out"], act_in, s)
-    else:
-        _lib.call("qw_moe_combine", _hip.ptr(y), act, p["route_slot"], p["top_idx"], T, K, D, p["out"], s)
+        _lib.call(fn, _hip.ptr(xc), act, p["slot_token"], p["kept_offsets"], E, D, F_, max_rows, min(cap, R),
+                  *pack.args_for(act), None, _hip.ptr(y), *saved, _hip.ptr(ws), nb, s)
+    _lib.call("qw_moe_combine_static" if static else "qw_moe_combine_weighted", _hip.ptr(y), act, p["route_slot"],
+              p["top_idx"], p["top_w"], T, K, D, p["out"], act_in, s)
     importance = torch.empty(E, dtype=torch.float32, device=dev)
     _lib.call("qw_moe_balance", p["probs"], p["counts"], T, K, E, _hip.ptr(importance), p["balance"], s)
     return r
@@ -518,10 +525,11 @@ class _MoELayer(torch.autograd.Function):
     and the router's two plain products (library GEMMs)."""
 
     @staticmethod
-    def forward(ctx, flat, router_w, moe, pack, cap, bias, cdt, *weights):
+    def forward(ctx, flat, router_w, moe, pack, cap, bias, cdt, loop, static, *weights):
         ctx.set_materialize_grads(False)
         flat = flat.detach().contiguous()
-        r = _layer_chain(flat, cdt, router_w.detach(), moe, pack, cap, bias, save=flat.size(0) > 0)
+        r = _layer_chain(flat, cdt, router_w.detach(), moe, pack, cap, bias, save=flat.size(0) > 0, loop=loop,
+                         static=static)
         saved = [r.get(n) for n in ("gate", "up", "hidden", "y_unweighted")]
         ctx.save_for_backward(flat, _router_operand(router_w), r["probs"], r["top_idx"], r["top_w"], r["counts"],
                               r["kept_offsets"], r["slot_token"], r["route_slot"], r["totals"], *saved)
@@ -538,7 +546,7 @@ class _MoELayer(torch.autograd.Function):
         moe, cdt = ctx.moe, ctx.cdt
         n_w = 3 * len(moe.experts)
         need_x, need_router = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        need_experts = any(ctx.needs_input_grad[7:7 + n_w])
+        need_experts = any(ctx.needs_input_grad[9:9 + n_w])
         T, D = flat.shape
         E, K = moe.num_experts, moe.top_k
         R = T * K
@@ -593,7 +601,7 @@ class _MoELayer(torch.autograd.Function):
             if need_x:
                 dx_router = (d_scores @ rw.float()).to(flat.dtype)
                 d_flat = dx_router if d_flat is None else d_flat + dx_router
-        return (d_flat, d_router, None, None, None, None, None, *expert_grads)
+        return (d_flat, d_router, None, None, None, None, None, None, None, *expert_grads)
 
 
 class _RowPlan:
@@ -607,21 +615,26 @@ class _RowPlan:
 
 
 def set_moe_kernel(model: nn.Module, kernel: str) -> str:
-    """Expert-compute selection (src/quantweave_moe_model.py:381-393).
+    """Expert executor of every TopKMoE in `model`: "loop", "triton" (the
+    grouped kernels; "hip" is an alias) or "auto".  Returns the active one,
+    with the reference's names and errors (src/quantweave_moe_model.py:381-393):
+    "auto" gives "triton" where the grouped kernels can run and "loop"
+    elsewhere; asking for "triton" (or "hip") where they cannot raises.
 
-    "hip" is the grouped HIP path; "triton" and "auto" select it too (the
-    grouped executor of this build).  "loop" — the reference's per-expert
-    PyTorch loop — has no counterpart here and raises."""
+    Both executors run the same HIP kernels: "triton" launches all experts at
+    once, "loop" one launch per expert with rows after reading the kept counts
+    back to the host (the reference's per-expert loop, :203-209)."""
     if kernel not in {"loop", "triton", "auto", "hip"}:
-        raise ValueError("kernel must be loop, triton, hip or auto")
+        raise ValueError("kernel must be loop, triton or auto")
     from .moe_kernels import kernels_available
 
-    device = next(model.parameters()).device
-    if kernel == "loop":
-        raise RuntimeError("the per-expert loop executor is not part of the HIP build; use 'hip' or 'auto'")
-    if not kernels_available(device):
-        raise RuntimeError("the HIP MoE kernels need a ROCm device and the built libqwmoe.so")
+    available = kernels_available(next(model.parameters()).device)
+    if kernel in ("triton", "hip") and not available:
+        raise RuntimeError("the grouped MoE kernels need a CUDA (ROCm) device and the built libqwmoe.so")
+    grouped = kernel in ("triton", "hip") or (kernel == "auto" and available)
     for m in model.modules():
         if isinstance(m, TopKMoE):
-            m.use_triton_kernels = True
-    return "hip"
+            m.use_triton_kernels = grouped
+    if not grouped:
+        return "loop"
+    return "hip" if kernel == "hip" else "triton"

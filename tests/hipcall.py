@@ -67,8 +67,12 @@ def plan(top_idx: torch.Tensor, top_w: torch.Tensor, E: int, cap: int):
     return res
 
 
+PATHS = {"auto": _lib.QW_PATH_AUTO, "generic": _lib.QW_PATH_GENERAL, "mfma": _lib.QW_PATH_MFMA,
+         "stream": _lib.QW_PATH_STREAM}
+
+
 def experts(x, offsets, fmt, gate, up, down, gate_s=None, up_s=None, down_s=None, group_in=0, group_ff=0,
-            row_index=None, row_weight=None, max_rows=None, rows_per_expert=0):
+            row_index=None, row_weight=None, max_rows=None, rows_per_expert=0, path="auto"):
     D = x.shape[1]
     E, F_ = gate.shape[0], gate.shape[1]
     rows = int(offsets[-1].item()) if max_rows is None else max_rows
@@ -76,8 +80,8 @@ def experts(x, offsets, fmt, gate, up, down, gate_s=None, up_s=None, down_s=None
     y = torch.full((max(rows, 1), D), float("nan"), dtype=x.dtype, device="cuda")
     nb = _lib.load().qw_moe_experts_workspace_bytes(rows, E, D, F_, act)
     ws = _hip.workspace(nb, torch.device("cuda"))
-    _lib.call("qw_moe_experts", P(x), act, P(row_index), P(offsets), E, D, F_, rows, rows_per_expert, fmt, group_in,
-              group_ff, P(gate),
-              P(gate_s), P(up), P(up_s), P(down), P(down_s), P(row_weight), P(y), P(ws), nb, s())
+    _lib.call("qw_moe_experts_on_path", PATHS[path], P(x), act, P(row_index), P(offsets), E, D, F_, rows,
+              rows_per_expert, fmt, group_in, group_ff, P(gate), P(gate_s), P(up), P(up_s), P(down), P(down_s),
+              P(row_weight), P(y), P(ws), nb, s())
     torch.cuda.synchronize()
     return y[:rows]

@@ -4,8 +4,6 @@ Tolerances (normwise, max|got-ref| / max|ref|): 1e-4 for fp32, 2e-2 for
 bf16 / int8 / int4 weights with fp32 accumulation.
 """
 
-import os
-
 import numpy as np
 import pytest
 import torch
@@ -64,7 +62,7 @@ def device_weights(w):
     return out
 
 
-def run_experts(x_np, counts, w, act, row_weight=None, row_index=None, x_rows=None):
+def run_experts(x_np, counts, w, act, row_weight=None, row_index=None, x_rows=None, path="auto"):
     dw = device_weights(w)
     tdt = torch.float32 if act == "f32" else torch.bfloat16
     x = H.dev(x_np, tdt)
@@ -73,7 +71,7 @@ def run_experts(x_np, counts, w, act, row_weight=None, row_index=None, x_rows=No
                   dw.get("down_s"), dw.get("group_in", 0), dw.get("group_ff", 0),
                   row_index=None if row_index is None else H.dev(row_index.astype(np.int32)),
                   row_weight=None if row_weight is None else H.dev(row_weight.astype(np.float32)),
-                  max_rows=int(sum(counts)), rows_per_expert=int(max(counts)))
+                  max_rows=int(sum(counts)), rows_per_expert=int(max(counts)), path=path)
     return y.float().cpu().numpy()
 
 
@@ -86,10 +84,8 @@ CASES = [
 
 @pytest.mark.parametrize("path", ["auto", "generic"])
 @pytest.mark.parametrize("act,fmt,D,F_,group", CASES)
-def test_grouped_swiglu_matches_oracle(act, fmt, D, F_, group, path, monkeypatch):
+def test_grouped_swiglu_matches_oracle(act, fmt, D, F_, group, path):
     print(f"case act={act} fmt={fmt} D={D} F={F_} group={group} path={path}", flush=True)
-    if path == "generic" and os.environ.get("QW_FFN_PATH") != "generic":
-        pytest.skip("the general kernel is exercised in a process started with QW_FFN_PATH=generic")
     rng = np.random.RandomState(D + F_)
     rows = sum(COUNTS)
     x = rng.randn(rows, D).astype(np.float32)
@@ -97,10 +93,36 @@ def test_grouped_swiglu_matches_oracle(act, fmt, D, F_, group, path, monkeypatch
         x = oracle.round_bf16(x)
     w = make_weights(len(COUNTS), D, F_, fmt, D * F_, group)
     rw = rng.rand(rows).astype(np.float32)
-    got = run_experts(x, COUNTS, w, act, row_weight=rw)
+    got = run_experts(x, COUNTS, w, act, row_weight=rw, path=path)
     ref = oracle.round_act(oracle.experts_forward(x, np.array(COUNTS), w, act) * rw[:, None], act)
     assert np.isfinite(got).all()
     assert normwise(got, ref) <= TOL[act]
+
+
+@pytest.mark.parametrize("act,fmt,group,path", [
+    ("bf16", "bf16", None, "mfma"), ("bf16", "bf16", None, "stream"), ("bf16", "bf16", None, "generic"),
+    ("bf16", "i8", None, "stream"), ("bf16", "i8", None, "generic"), ("bf16", "u4", 32, "stream"),
+    ("bf16", "u4", 32, "generic"), ("f32", "f32", None, "generic")])
+def test_each_kernel_family_matches_oracle(act, fmt, group, path):
+    """The same inputs through every kernel family that takes them
+    (qw_moe_experts_on_path), each against the oracle."""
+    print(f"case family act={act} fmt={fmt} path={path}", flush=True)
+    D, F_ = 256, 512
+    rng = np.random.RandomState(17)
+    rows = sum(COUNTS)
+    x = oracle.round_act(rng.randn(rows, D).astype(np.float32), act)
+    w = make_weights(len(COUNTS), D, F_, fmt, 23, group)
+    rw = rng.rand(rows).astype(np.float32)
+    got = run_experts(x, COUNTS, w, act, row_weight=rw, path=path)
+    ref = oracle.round_act(oracle.experts_forward(x, np.array(COUNTS), w, act) * rw[:, None], act)
+    assert normwise(got, ref) <= TOL[act]
+
+
+def test_kernel_family_that_does_not_take_the_format_refuses():
+    w = make_weights(len(COUNTS), 256, 512, "i8", 3)
+    x = oracle.round_bf16(np.random.RandomState(0).randn(sum(COUNTS), 256).astype(np.float32))
+    with pytest.raises(RuntimeError, match="matrix-core"):
+        run_experts(x, COUNTS, w, "bf16", path="mfma")
 
 
 def test_gathered_rows_through_row_index():

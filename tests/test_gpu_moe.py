@@ -52,10 +52,13 @@ def host_weights(layer):
     return out
 
 
-def check_layer(workload, tol_scale=1.0):
-    print(f"case {workload.name} T={workload.tokens} d={workload.d_model} E={workload.experts} f={workload.d_ff}",
-          flush=True)
+def check_layer(workload, tol_scale=1.0, tiles=False):
+    print(f"case {workload.name} T={workload.tokens} d={workload.d_model} E={workload.experts} f={workload.d_ff}"
+          f"{' tiled' if tiles else ''}", flush=True)
     layer = W.build_layer(workload)
+    if tiles:
+        layer.add_tiles()
+        assert "tiles" in layer.extra
     run = W.LayerRunner(layer)
     run()
     torch.cuda.synchronize()
@@ -111,6 +114,13 @@ def test_layer_matches_oracle_small(workload):
 @pytest.mark.parametrize("name", [n for n in W.WORKLOADS if not n.startswith("fp32")])
 def test_layer_matches_oracle_full_size(name):
     check_layer(W.WORKLOADS[name])
+
+
+@pytest.mark.parametrize("name", ["bf16-prefill-T8192-d2048-E64-f1024-k2", "skewed-T4096-d2048-E64-f1024-k2"])
+def test_layer_matches_oracle_full_size_tiled(name):
+    """The weights in the QW_BF16T tiles the module (and the benchmark) uses:
+    the exact kernel instantiations behind the benchmark figures."""
+    check_layer(W.WORKLOADS[name], tiles=True)
 
 
 def test_layer_is_deterministic_across_calls():
@@ -306,3 +316,96 @@ def test_expert_profiling_accumulates_time_per_expert():
     used = moe.last_plan["kept_counts"].cpu()
     assert all((s > 0) == (c > 0) for s, c in zip(moe.expert_seconds, used.tolist()))
     assert normwise(out.detach().cpu().numpy(), plain.cpu().numpy()) <= 1e-4
+
+
+def bf16_module(E=8, D=256, F_=512, k=2, cf=1.25, seed=5):
+    cfg = small_config(hidden_size=D, ffn_size=F_, num_experts=E, top_k=k, attention_heads=1, capacity_factor=cf)
+    torch.manual_seed(seed)
+    return qa.TopKMoE(cfg).cuda().to(torch.bfloat16)
+
+
+def bf16_module_weights(moe):
+    w = dict(format="bf16", d_model=moe.router.in_features, d_ff=moe.experts[0].gate.out_features)
+    for n in ("gate", "up", "down"):
+        w[n] = np.stack([getattr(e, n).weight.detach().float().cpu().numpy() for e in moe.experts])
+    return w
+
+
+def test_loop_executor_selected_by_set_moe_kernel():
+    """set_moe_kernel (src/quantweave_moe_model.py:381-393): "loop" launches one
+    expert at a time, "triton"/"auto" all at once; both match the oracle, and
+    the loop equals the grouped call to accumulation order."""
+    moe = bf16_module()
+    hidden = torch.randn(2, 160, 256, device="cuda").bfloat16()
+    assert qa.set_moe_kernel(moe, "auto") == "triton" and moe.use_triton_kernels
+    with torch.no_grad():
+        grouped = moe(hidden)[0]
+    assert qa.set_moe_kernel(moe, "loop") == "loop" and not moe.use_triton_kernels
+    with torch.no_grad():
+        looped, _, dropped, overflow, _ = moe(hidden)
+    assert qa.set_moe_kernel(moe, "triton") == "triton" and qa.set_moe_kernel(moe, "hip") == "hip"
+    flat = hidden.reshape(-1, 256).float().cpu().numpy()
+    ref = oracle.moe_forward(flat, moe.router.weight.detach().float().cpu().numpy(), bf16_module_weights(moe), top_k=2,
+                             cap=moe.capacity(320), dtype="bf16")
+    for out in (grouped, looped):
+        assert normwise(out.reshape(-1, 256).float().cpu().numpy(), ref["out"]) <= TOL["bf16"]
+    assert int(overflow) == int(ref["plan"]["totals"][1])
+    assert normwise(looped.float().cpu().numpy(), grouped.float().cpu().numpy()) <= 1e-2
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_static_dispatch_matches_the_reference_static_output(dtype):
+    """TopKMoE._static_output (src/quantweave_moe_model.py:235-245): capacity
+    off, route weights cast to the hidden dtype before the product, a rounding
+    per add; in fp32 it equals the dynamic path with capacity off
+    (tests/test_model_features.py:49-56)."""
+    moe = bf16_module(cf=0.5) if dtype == "bf16" else bf16_module(cf=0.5).float()
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    hidden = torch.randn(2, 96, 256, device="cuda").to(tdt)
+    moe.static_dispatch = True
+    with torch.no_grad():
+        out, _, dropped, overflow, _ = moe(hidden)
+    assert int(overflow) == 0 and int(dropped) == 0
+    flat = hidden.reshape(-1, 256).float().cpu().numpy()
+    w = bf16_module_weights(moe)
+    w["format"] = dtype
+    rw = moe.router.weight.detach().float().cpu().numpy()
+    ref = oracle.moe_forward(flat, rw, w, top_k=2, cap=192 * 2, dtype=dtype)
+    p = ref["plan"]
+    static_ref = oracle.combine_static(ref["y"], p["slot_token"], p["slot_weight"], 192, dtype)
+    got = out.reshape(-1, 256).float().cpu().numpy()
+    assert normwise(got, static_ref) <= TOL[dtype]
+    moe.static_dispatch = False
+    moe.capacity_factor = 0.0
+    with torch.no_grad():
+        dynamic = moe(hidden)[0]
+    if dtype == "f32":
+        assert torch.equal(out, dynamic)
+    else:  # only the bf16 cast of the route weights separates the two
+        assert normwise(got, dynamic.reshape(-1, 256).float().cpu().numpy()) <= 1e-2
+
+
+@pytest.mark.parametrize("k", [2, 3, 4])
+def test_combine_is_bit_exact_against_the_oracle(k):
+    """qw_moe_combine_weighted from bf16 expert rows: torch's index_add_ rule
+    (fp32 sum in plan order, one rounding) bit for bit, also at k >= 3 where a
+    rounding per add would differ; and the static-dispatch combine."""
+    from quantaweave_amd import _hip, _lib
+
+    T, D, E = 700, 512, 16
+    g = torch.Generator().manual_seed(40 + k)
+    _, idx, w = oracle.route_from_logits((torch.randn(T, E, generator=g) * 2).numpy(), k)
+    p = oracle.plan(idx, w, E, oracle.capacity(T, k, E, 1.0))
+    n = len(p["slot_token"])
+    y = oracle.round_bf16((torch.randn(n, D, generator=g) * torch.logspace(-3, 3, D)[None]).numpy())
+    yd = torch.from_numpy(y).cuda().bfloat16()
+    slot = torch.from_numpy(p["route_slot"]).cuda()
+    tidx = torch.from_numpy(idx).cuda()
+    tw = torch.from_numpy(w).cuda()
+    for fn, ref in (("qw_moe_combine_weighted", oracle.combine(y, p["slot_token"], p["slot_weight"], T, "bf16")),
+                    ("qw_moe_combine_static", oracle.combine_static(y, p["slot_token"], p["slot_weight"], T, "bf16"))):
+        out = torch.empty(T, D, dtype=torch.bfloat16, device="cuda")
+        _lib.call(fn, _hip.ptr(yd), _lib.QW_BF16, _hip.ptr(slot), _hip.ptr(tidx), _hip.ptr(tw), T, k, D, _hip.ptr(out),
+                  _lib.QW_BF16, _hip.stream(out.device))
+        torch.cuda.synchronize()
+        assert np.array_equal(out.float().cpu().numpy(), ref), fn

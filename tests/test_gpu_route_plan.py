@@ -103,6 +103,8 @@ def _check_plan(idx, w, E, cap):
     (512, 8, 2, 1.25, 0.0, 0), (8192, 64, 2, 1.25, 0.0, 1), (64, 64, 2, 0.0, 0.0, 2), (16, 64, 2, 0.0, 0.0, 3),
     (4096, 64, 2, 1.0, 3.0, 4), (300, 16, 3, 0.5, 2.0, 5), (1000, 4, 1, 0.3, 0.0, 6), (9000, 1, 1, 0.5, 0.0, 7),
     (3000, 2, 2, 0.1, 0.0, 8), (5, 64, 2, 1.0, 0.0, 9), (8191, 64, 2, 1.25, 0.0, 10), (4097, 64, 2, 1.0, 3.0, 11),
+    # experts past the 8192 keys the LDS sorts: the sorting network in the workspace
+    (12000, 1, 1, 0.5, 0.0, 12), (20000, 8, 2, 0.3, 8.0, 13), (40000, 4, 2, 1.0, 8.0, 14),
 ])
 def test_plan_is_bit_exact(T, E, k, cf, hot, seed):
     print(f"case T={T} E={E} k={k} cf={cf}", flush=True)
@@ -111,6 +113,8 @@ def test_plan_is_bit_exact(T, E, k, cf, hot, seed):
     got = _check_plan(idx, w, E, cap)
     if cf and hot:
         assert got["totals"][1] > 0
+    if T >= 12000:
+        assert got["counts"].max() > 8192
 
 
 def test_plan_with_equal_weights_and_tiny_capacity():

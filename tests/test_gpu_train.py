@@ -218,6 +218,24 @@ def test_layer_output_is_the_inference_output():
     assert torch.equal(train_out.detach(), infer_out)
 
 
+@pytest.mark.parametrize("E,D,F_,tokens,cf", [(16, 256, 512, 512, 1.25), (64, 256, 512, 16, 0.0)],
+                         ids=["matrix-core", "weight-streaming"])
+def test_bf16_layer_output_is_the_inference_output(E, D, F_, tokens, cf):
+    """bf16 experts: the forward with autograd on (qw_moe_experts_save, which
+    also keeps the activations) gives the inference call's output bit for bit,
+    at a shape the matrix-core kernels take (64 rows per expert) and at one
+    the weight-streaming kernels take (half a row per expert)."""
+    print(f"case layer train/inference bf16 E={E} D={D} F={F_} T={tokens}", flush=True)
+    moe = make_moe(E, D, F_, 2, cf, seed=12).to(torch.bfloat16)
+    x = torch.randn(1, tokens, D, device="cuda").to(torch.bfloat16)
+    train_out = moe(x.clone().requires_grad_())[0]
+    with torch.no_grad():
+        infer_out = moe(x)[0]
+    assert torch.equal(train_out.detach(), infer_out)
+    train_out.float().square().sum().backward()
+    assert all(torch.isfinite(p.grad).all() for p in moe.parameters() if p.grad is not None)
+
+
 def test_training_steps_reduce_the_loss():
     print("case layer sgd", flush=True)
     moe = make_moe(8, 64, 128, 2, 1.25, seed=9)

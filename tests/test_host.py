@@ -72,16 +72,19 @@ def test_cpu_tensors_are_refused_not_computed():
         mk.grouped_swiglu(torch.randn(3, 16), moe.experts, [3, 0, 0, 0, 0, 0])
 
 
-def test_kernel_selection_errors():
+def test_kernel_selection_without_a_device():
+    """tests/test_moe_kernels.py:137-143 of the reference: a CPU model falls
+    back to the loop for "auto", keeps "loop", and refuses "triton"."""
     moe = qa.TopKMoE(small_config())
     with pytest.raises(ValueError):
         qa.set_moe_kernel(moe, "bogus")
-    with pytest.raises(RuntimeError):
-        qa.set_moe_kernel(moe, "loop")
     assert not mk.kernels_available(torch.device("cpu"))
-    if not torch.cuda.is_available():
-        with pytest.raises(RuntimeError):
-            qa.set_moe_kernel(moe, "auto")
+    assert qa.set_moe_kernel(moe, "auto") == "loop" and qa.set_moe_kernel(moe, "loop") == "loop"
+    assert moe.use_triton_kernels is False
+    with pytest.raises(RuntimeError, match="CUDA"):
+        qa.set_moe_kernel(moe, "triton")
+    with pytest.raises(RuntimeError, match="CUDA"):
+        qa.set_moe_kernel(moe, "hip")
 
 
 def test_compute_dtype_rule():

@@ -491,3 +491,133 @@ def test_tile_layout_matches_the_element_formula():
     assert np.array_equal(oracle.untile_bf16(oracle.tile_bf16(w)), w)
     with pytest.raises(ValueError):
         oracle.tile_bf16(np.zeros((1, 8, 32), np.float32))
+
+
+# ---------------------------------------------------------------- the oracle's routing vs torch's own composition
+def torch_route(logits: torch.Tensor, k: int, bias: torch.Tensor | None):
+    """src/quantweave_moe_model.py:129-136 with torch's own softmax, topk,
+    gather and renormalisation on the given fp32 logits."""
+    probs = logits.softmax(dim=-1)
+    if bias is None:
+        top_w, top_idx = probs.topk(k, dim=-1)
+    else:
+        top_idx = (logits + bias.to(logits)).topk(k, dim=-1).indices
+        top_w = probs.gather(1, top_idx)
+    top_w = top_w / top_w.sum(dim=-1, keepdim=True)
+    return probs, top_idx, top_w
+
+
+# (tokens, d_model, experts, top_k, capacity factor, dtype, Zipf bias): the five
+# workload shapes of the benchmark, plus many experts with top-3
+ROUTING_SHAPES = {
+    "fp32-T512-E8": (512, 256, 8, 2, 1.25, torch.float32, False),
+    "bf16-T8192-E64": (8192, 2048, 64, 2, 1.25, torch.bfloat16, False),
+    "int8-decode-T64-E64": (64, 2048, 64, 2, 0.0, torch.bfloat16, False),
+    "int4-decode-T16-E64": (16, 4096, 64, 2, 0.0, torch.bfloat16, False),
+    "skewed-T4096-E64": (4096, 2048, 64, 2, 1.0, torch.bfloat16, True),
+    "T2048-E184-k3": (2048, 256, 184, 3, 1.25, torch.float32, False),
+}
+
+
+@pytest.mark.parametrize("name", list(ROUTING_SHAPES))
+def test_routing_and_plan_equal_torchs_composition_on_the_same_logits(name):
+    """From identical logits, the oracle's top-k indices, capacity slots, drop
+    lists and overflow equal the reference's composition of torch calls
+    (softmax -> topk or biased topk + gather -> renormalise -> double stable
+    argsort).  The oracle's probabilities use its own exp and summation order
+    and differ from torch's by a few ulp (reported); the indices must not."""
+    from quantaweave_amd.workloads import zipf_bias
+
+    T, D, E, k, cf, dt, skew = ROUTING_SHAPES[name]
+    g = torch.Generator().manual_seed(1000 + len(name))
+    x = torch.randn(T, D, generator=g).to(dt)
+    router = (torch.randn(E, D, generator=g) * 0.02).to(dt)
+    logits = F.linear(x.float(), router.float())  # src/quantweave_moe_model.py:128
+    bias = zipf_bias(E) if skew else None
+    cap = oracle.capacity(T, k, E, cf)
+    probs_t, idx_t, w_t = torch_route(logits, k, bias)
+    probs_o, idx_o, w_o = oracle.route_from_logits(logits.numpy(), k, None if bias is None else bias.numpy())
+    assert np.array_equal(idx_o, idx_t.numpy().astype(np.int32)), "top-k indices differ from torch's"
+    ours = oracle.plan(idx_o, w_o, E, cap)
+    ref = torch_plan(idx_t.numpy().astype(np.int32), w_t.numpy(), E, cap)
+    assert np.array_equal(ours["slot_token"], ref["tokens"].numpy())
+    assert np.array_equal(ours["kept_counts"], ref["kept_counts"].numpy())
+    assert int(ours["totals"][1]) == ref["overflow"]
+    assert np.array_equal(ours["dropped_token"], ref["dropped_tokens"].numpy())
+    assert np.array_equal(ours["dropped_expert"], ref["dropped_experts"].numpy())
+    if skew:
+        assert ref["overflow"] > 0  # the hot experts overflow
+    up = ulp_diff(probs_o, probs_t.numpy())
+    uw = ulp_diff(w_o, w_t.numpy())
+    hist = {int(u): int(c) for u, c in zip(*np.unique(np.minimum(up, 8), return_counts=True))}
+    print(f"{name}: probability ulp histogram (8 = 8 or more) {hist}; top_w max ulp {int(uw.max())}; "
+          f"drops {ref['overflow']}")
+    assert up.max() <= 16 and uw.max() <= 16
+
+
+# ---------------------------------------------------------------- combine vs torch's index_add_
+@pytest.mark.parametrize("k", [2, 3, 4])
+def test_bf16_combine_equals_torch_index_add(k):
+    """oracle.combine against the reference's last two lines
+    (src/quantweave_moe_model.py:200-201) run by torch: bf16 expert rows times
+    fp32 route weights, cast to bf16, index_add_ into bf16 zeros in plan order.
+    Bit-exact for every k; a rounding after each add (the other plausible rule)
+    is checked to differ at k >= 3, so the test tells the two apart."""
+    T, D, E = 512, 256, 16
+    g = torch.Generator().manual_seed(70 + k)
+    logits = torch.randn(T, E, generator=g) * 2
+    _, idx, w = oracle.route_from_logits(logits.numpy(), k)
+    p = oracle.plan(idx, w, E, T * k)
+    n = len(p["slot_token"])
+    y = (torch.randn(n, D, generator=g) * torch.logspace(-3, 3, D)[None]).to(torch.bfloat16)
+    tokens = torch.from_numpy(p["slot_token"].astype(np.int64))
+    weights = torch.from_numpy(p["slot_weight"])
+    ref = torch.zeros(T, D, dtype=torch.bfloat16).index_add_(0, tokens, (y * weights[:, None]).to(torch.bfloat16))
+    got = oracle.combine(y.float().numpy(), p["slot_token"], p["slot_weight"], T, "bf16")
+    assert np.array_equal(got, ref.float().numpy())
+    # the per-add rule, for contrast
+    contrib = oracle.round_bf16(y.float().numpy() * p["slot_weight"][:, None])
+    per_add = np.zeros((T, D), np.float32)
+    for s, t in enumerate(p["slot_token"].tolist()):
+        per_add[t] = oracle.round_bf16(per_add[t] + contrib[s])
+    if k == 2:
+        assert np.array_equal(per_add, got)
+    else:
+        assert not np.array_equal(per_add, got)
+
+
+def test_fp32_combine_equals_torch_index_add():
+    T, D, E, k = 256, 64, 8, 3
+    g = torch.Generator().manual_seed(9)
+    _, idx, w = oracle.route_from_logits((torch.randn(T, E, generator=g) * 2).numpy(), k)
+    p = oracle.plan(idx, w, E, T * k)
+    y = torch.randn(len(p["slot_token"]), D, generator=g) * torch.logspace(-4, 4, D)[None]
+    tokens = torch.from_numpy(p["slot_token"].astype(np.int64))
+    ref = torch.zeros(T, D).index_add_(0, tokens, y * torch.from_numpy(p["slot_weight"])[:, None])
+    got = oracle.combine(y.numpy(), p["slot_token"], p["slot_weight"], T, "f32")
+    assert np.array_equal(got, ref.numpy())
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_static_combine_equals_torchs_static_output(dt):
+    """oracle.combine_static against the loop of TopKMoE._static_output
+    (src/quantweave_moe_model.py:240-245) run by torch: every expert's output
+    for every token, times the dense weights cast to the hidden dtype, added
+    expert by expert.  The experts a token does not use see random rows
+    multiplied by an exact zero."""
+    T, D, E, k = 300, 64, 8, 2
+    g = torch.Generator().manual_seed(31)
+    logits = torch.randn(T, E, generator=g) * 2
+    probs_o, idx, w = oracle.route_from_logits(logits.numpy(), k)
+    dense_y = (torch.randn(E, T, D, generator=g) * 3).to(dt)     # expert(flat_hidden) of every expert
+    dense_w = torch.zeros(T, E).scatter(1, torch.from_numpy(idx.astype(np.int64)), torch.from_numpy(w))
+    ref = torch.zeros(T, D, dtype=dt)
+    for e in range(E):
+        ref = ref + dense_y[e] * dense_w[:, e:e + 1].to(dt)
+    p = oracle.plan(idx, w, E, T * k)
+    rows = np.stack([dense_y[e, t].float().numpy() for e in range(E) for t in p["slot_token"][
+        p["kept_offsets"][e]:p["kept_offsets"][e + 1]]])
+    got = oracle.combine_static(rows, p["slot_token"], p["slot_weight"], T, "bf16" if dt == torch.bfloat16 else "f32")
+    assert np.array_equal(got, ref.float().numpy())
+    if dt == torch.float32:  # in fp32 the static and dynamic accumulations agree (src: tests/test_model_features.py:49-56)
+        assert np.array_equal(got, oracle.combine(rows, p["slot_token"], p["slot_weight"], T, "f32"))
