@@ -10,9 +10,11 @@
  * Ownership: every pointer is caller-owned device memory.  The library never
  * allocates device memory; entry points that need scratch take an explicit
  * `workspace` whose size the caller obtains from the matching
- * qw_*_workspace_bytes() function.  The library keeps no mutable global state,
- * so calls on different streams do not interfere (calls that share a workspace
- * must be ordered on one stream).
+ * qw_*_workspace_bytes() function.  Apart from the one allocation-free entry
+ * point (qw_moe_decode_step_noalloc, whose scratch is a static per-device
+ * array), the library keeps no mutable global state, so calls on different
+ * streams do not interfere (calls that share a workspace must be ordered on
+ * one stream).
  *
  * Reference citations are paths inside the QuantaWeave source tree.
  */
@@ -219,6 +221,28 @@ int qw_moe_decode_step(const float* x, const float* residual, int64_t tokens, in
                        const float* up_scales, const void* down_w, const float* down_scales, float* out,
                        float* probs, int32_t* top_idx, float* top_w, void* workspace, size_t workspace_bytes,
                        void* stream);
+
+/* qw_moe_decode_step without a workspace argument: its scratch is a
+ * library-owned array of qw_moe_decode_step_noalloc_scratch_bytes() (32 MiB)
+ * on each device, so the call performs no allocation of any kind (it calls no
+ * hipMalloc, and torch allocates nothing for it).  No counterpart in the
+ * reference: it is for callers that cannot allocate — code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation.  The caller
+ * still passes inputs and outputs, exactly as for qw_moe_decode_step, whose
+ * results it reproduces bit for bit.  A step whose workspace would exceed the
+ * array (qw_moe_decode_step_workspace_bytes) is refused with QW_ERR_INVALID
+ * before any device work.  The stream must belong to the current device.
+ * Every call on one device shares that device's array and leaves its last
+ * contents there (every value a step reads it first writes, so nothing needs
+ * clearing); calls that overlap on one device — on different streams or
+ * threads without ordering — race. */
+size_t qw_moe_decode_step_noalloc_scratch_bytes(void);
+int qw_moe_decode_step_noalloc(const float* x, const float* residual, int64_t tokens, int64_t d_model,
+                               const float* router_w, float temperature, const float* expert_bias, int64_t experts,
+                               int64_t top_k, int64_t d_ff, int compute_dtype, int w_format, int64_t group_in,
+                               int64_t group_ff, const void* gate_w, const float* gate_scales, const void* up_w,
+                               const float* up_scales, const void* down_w, const float* down_scales, float* out,
+                               float* probs, int32_t* top_idx, float* top_w, void* stream);
 
 /* Weight-only quantisation, QuantizedLinear.from_linear
  * (src/quantization.py:43-59): w [out, in] fp32 or bf16 is zero-padded to

@@ -43,6 +43,9 @@ SIGNATURES = {
     "qw_moe_decode_step_workspace_bytes": (SZ, [I64, I64, I64, I64, I64, I32]),
     "qw_moe_decode_step": (I32, [P, P, I64, I64, P, F32, P, I64, I64, I64, I32, I32, I64, I64,
                                  P, P, P, P, P, P, P, P, P, P, P, SZ, P]),
+    "qw_moe_decode_step_noalloc_scratch_bytes": (SZ, []),
+    "qw_moe_decode_step_noalloc": (I32, [P, P, I64, I64, P, F32, P, I64, I64, I64, I32, I32, I64, I64,
+                                         P, P, P, P, P, P, P, P, P, P, P]),
     "qw_quantize": (I32, [P, I32, I64, I64, I32, I64, P, P, P]),
     "qw_dequantize": (I32, [P, P, I32, I64, I64, I64, P, P]),
     "qw_pack_bf16_tiles": (I32, [P, I64, I64, I64, P, P]),

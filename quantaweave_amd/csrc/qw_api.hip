@@ -222,6 +222,35 @@ static DecodeWs carve_decode(void* base, int64_t T, int64_t D, int64_t E, int64_
   return w;
 }
 
+// ---------------------------------------------------------------------------
+// Library-owned scratch of the allocation-free decode step
+// (qw_moe_decode_step_noalloc): one array per device, kept until the process
+// ends.  In host code `scratch` names a host-side stand-in, not device
+// memory: its device address on each GPU comes from hipGetSymbolAddress,
+// made once per device with that device current, and only that address is
+// ever handed to kernels.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;  // 32 MiB per device
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the current device (looked up once per device).
+static int scratch_on_current_device(void** out) {
+  int dev = 0;
+  QW_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return set_error(QW_ERR_UNSUPPORTED, "device %d is beyond the library's table", dev);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    QW_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return set_error(QW_ERR_HIP, "hipGetSymbolAddress returned no address for the scratch array");
+    g_scratch_ptr[dev].store(p, std::memory_order_release);  // the same address whoever stores it first
+  }
+  *out = p;
+  return QW_OK;
+}
+
 }  // namespace qw
 
 using namespace qw;
@@ -469,6 +498,38 @@ int qw_moe_decode_step(const float* x, const float* residual, int64_t tokens, in
                    w.exp_bytes, s, avg, std::min<int64_t>(tokens, R));
   if (st) return st;
   return decode_combine(w.y, compute_dtype, w.route_slot, top_w, residual, tokens, top_k, d_model, out, s);
+}
+
+size_t qw_moe_decode_step_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+int qw_moe_decode_step_noalloc(const float* x, const float* residual, int64_t tokens, int64_t d_model,
+                               const float* router_w, float temperature, const float* expert_bias, int64_t experts,
+                               int64_t top_k, int64_t d_ff, int compute_dtype, int w_format, int64_t group_in,
+                               int64_t group_ff, const void* gate_w, const float* gate_scales, const void* up_w,
+                               const float* up_scales, const void* down_w, const float* down_scales, float* out,
+                               float* probs, int32_t* top_idx, float* top_w, void* stream) {
+  clear_error();
+  QW_REQUIRE(compute_dtype == QW_F32 || compute_dtype == QW_BF16, "compute dtype must be f32 or bf16");
+  QW_REQUIRE(tokens >= 0 && top_k >= 1 && experts >= 1 && d_model >= 1 && d_ff >= 1, "bad decode step sizes");
+  // sizes first: an oversized call is refused before any device work
+  const size_t need = carve_decode(nullptr, tokens, d_model, experts, top_k, d_ff, compute_dtype).used;
+  QW_REQUIRE(need <= kNoAllocScratchBytes,
+             "this decode step needs %zu bytes of scratch; the allocation-free entry point has %zu per device "
+             "(use qw_moe_decode_step with a workspace)",
+             need, kNoAllocScratchBytes);
+  if (tokens == 0) return QW_OK;
+  hipStream_t s = as_stream(stream);
+  if (s != nullptr) {  // the scratch address is per device: the stream must be on the current device
+    int cur = 0, sdev = 0;
+    QW_HIP_CHECK(hipGetDevice(&cur));
+    QW_HIP_CHECK(hipStreamGetDevice(s, &sdev));
+    QW_REQUIRE(sdev == cur, "the stream belongs to device %d but device %d is current", sdev, cur);
+  }
+  void* ws = nullptr;
+  if (const int st = scratch_on_current_device(&ws)) return st;
+  return qw_moe_decode_step(x, residual, tokens, d_model, router_w, temperature, expert_bias, experts, top_k, d_ff,
+                            compute_dtype, w_format, group_in, group_ff, gate_w, gate_scales, up_w, up_scales, down_w,
+                            down_scales, out, probs, top_idx, top_w, ws, kNoAllocScratchBytes, stream);
 }
 
 int qw_quantize(const void* w, int w_dtype, int64_t out_features, int64_t in_features, int bits, int64_t group_size,
