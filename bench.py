@@ -7,8 +7,10 @@ grouped SwiGLU experts -> weighted combine) over one batch of synthetic input
 already resident in HBM.  Prints ONE JSON line: throughput of the headline
 workload (bf16 prefill, T=8192, d=2048, 64 experts, d_ff=1024, top-2,
 capacity factor 1.25) with a roofline entry for the expert-FFN stage, the
-CPU baseline (the oracle on the host cores, bounded sample), and per-workload
-numbers for the other workloads, and the batch-1 decode step
+CPU baseline (the reference's forward restated with torch CPU ops, whole
+workload, on the host cores), per-workload numbers for the other workloads
+(each with its own CPU baseline), the same layer timed through the TopKMoE
+module, and the batch-1 decode step
 (qw_moe_decode_step: the routed experts of one token, fp32 routing, no
 capacity) at three of the workloads' layer shapes, eager and replayed from a
 HIP graph.
@@ -221,42 +223,86 @@ def measure_decode(name, steps, warmup):
     )
 
 
-def cpu_baseline(name, budget_s=20.0):
-    """The oracle's whole-layer forward on the host cores over a bounded token sample."""
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(name, budget_s=8.0):
+    """The reference's layer forward (loop executor, dequantise-then-matmul for
+    int8/int4 experts) restated with torch CPU operators (oracle.torch_ref), on
+    the whole workload, timed on the host cores: one warm-up, then the median
+    of up to five runs within `budget_s`."""
     import torch
-    import oracle
+    from oracle import torch_ref
     from quantaweave_amd import workloads as W
 
     w = W.WORKLOADS[name]
     layer = W.build_layer(w)
-    sample = 512 if w.tokens >= 512 else w.tokens
-    x = layer.x[:sample].float().cpu().numpy()
-    rw = layer.router.float().cpu().numpy()
-    wts = dict(format=w.weights, d_model=w.d_model, d_ff=w.d_ff, group_in=layer.group_in, group_ff=layer.group_ff)
-    for n in ("gate", "up", "down"):
-        t = getattr(layer, n)
-        wts[n] = t.float().cpu().numpy() if w.weights in ("f32", "bf16") else t.cpu().numpy()
-        sc = getattr(layer, n + "_s")
-        if sc is not None:
-            wts[n + "_scales"] = sc.cpu().numpy()
-    bias = None if layer.bias is None else layer.bias.cpu().numpy()
-    cap = W.Workload(w.name, sample, w.d_model, w.experts, w.d_ff, w.top_k, w.capacity_factor, w.act, w.weights,
-                     w.seed).capacity()
+    cpu = lambda t: None if t is None else t.cpu()  # noqa: E731
+    x, router = layer.x.cpu(), layer.router.cpu()
+    experts = torch_ref.Experts(w.weights, cpu(layer.gate), cpu(layer.up), cpu(layer.down), cpu(layer.gate_s),
+                                cpu(layer.up_s), cpu(layer.down_s))
+    bias = cpu(layer.bias)
     del layer
     torch.cuda.empty_cache()
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while True:
+    cap = w.capacity()
+    threads = torch.get_num_threads()
+    with torch.no_grad():
         t0 = time.perf_counter()
-        oracle.moe_forward(x, rw, wts, top_k=w.top_k, cap=cap, dtype=w.act, expert_bias=bias, accum="f32")
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 5 or time.perf_counter() > t_end:
-            break
+        torch_ref.moe_forward(x, router, experts, w.top_k, cap, expert_bias=bias)  # warm-up
+        times = []
+        t_end = t0 + budget_s
+        while len(times) < 5 and (not times or time.perf_counter() < t_end):
+            t1 = time.perf_counter()
+            torch_ref.moe_forward(x, router, experts, w.top_k, cap, expert_bias=bias)
+            times.append(time.perf_counter() - t1)
     med = float(np.median(times))
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return dict(value=sample / med, unit="tokens/s", cores=threads, kind="port",
-                sample=f"{sample} of {w.tokens} tokens of {w.name}, all {w.experts} experts, capacity {cap}, "
-                       f"oracle (numpy fp32 BLAS + C routing), median of {len(times)} runs")
+    return dict(value=round(w.tokens / med, 1), unit="tokens/s", cores=threads, kind="port",
+                sample=f"the whole workload ({w.tokens} tokens, {w.experts} experts, capacity {cap}) through the "
+                       f"reference's loop-executor forward restated with torch CPU ops (oracle/torch_ref.py), "
+                       f"{w.act} activations, {w.weights} experts; median of {len(times)} runs after one warm-up; "
+                       f"{threads} torch threads on {cpu_model()}")
+
+
+def committed_traffic(name):
+    """HBM bytes per call of the expert stage from the committed counter summary
+    (profiles/moe_layer_all_workloads_hbm_bytes.md, its json block), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "moe_layer_all_workloads_hbm_bytes.md")
+    try:
+        text = open(path).read()
+        block = text.split("```json", 1)[1].split("```", 1)[0]
+        return json.loads(block)["expert_stage_bytes"].get(name)
+    except (OSError, IndexError, KeyError, ValueError):
+        return None
+
+
+def measure_module(name, steps, warmup):
+    """The drop-in surface: TopKMoE.forward (no grad) on the workload's layer,
+    wall ms per call, with the module's own per-call work (workspace,
+    balance loss, Python)."""
+    import torch
+    from quantaweave_amd import workloads as W
+
+    w = W.WORKLOADS[name]
+    layer = W.build_layer(w)
+    moe = W.module_from_layer(layer)
+    hidden = layer.x.reshape(w.batch, w.seq, w.d_model)
+    with torch.no_grad():
+        for _ in range(warmup):
+            moe(hidden)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            moe(hidden)
+        torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1000 / steps
 
 
 def main():
@@ -282,11 +328,14 @@ def main():
         print(json.dumps({"copy_probe_bytes": n, "launches": 3}), flush=True)
         return
     head = args.workload or W.HEADLINE
-    results = {head: measure(head, args.steps, args.warmup)}
+    results = {}
     if not args.only_headline:
         for name in W.WORKLOADS:
-            if name not in results:
+            if name != head:
                 results[name] = measure(name, args.steps, args.warmup)
+    # the headline last, on a GPU already at its steady clocks
+    results[head] = measure(head, args.steps, args.warmup)
+    module_ms = measure_module(head, args.steps, args.warmup)
     h = results[head]
     w = h["workload"]
     t_exp = h["stages"]["experts"]
@@ -294,11 +343,11 @@ def main():
     if mfma:
         achieved = h["flops"] / (t_exp / 1000) / 1e12
         roof = dict(bound="mfma", achieved=round(achieved, 2), peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
-                    frac=round(achieved / BF16_PEAK_TFLOPS, 4), traffic=None)
+                    frac=round(achieved / BF16_PEAK_TFLOPS, 4), traffic=committed_traffic(head))
     else:
         achieved = h["stage_bytes"] / (t_exp / 1000) / 1e9
         roof = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None)
+                    frac=round(achieved / HBM_PEAK_GBS, 4), traffic=committed_traffic(head))
     roof["kernel"] = "qw_moe_experts (grouped SwiGLU: gate/up+SiLU*mul, down+weight)"
     roof["algorithmic"] = dict(flops=h["flops"], bytes=h["stage_bytes"], launch_ms=round(t_exp, 4))
     per = {}
@@ -317,6 +366,8 @@ def main():
             experts_cold_ms={k: round(v, 4) for k, v in r["experts_cold"].items()},
             hbm_frac_cold=round(r["stage_bytes"] / (tc / 1000) / 1e9 / HBM_PEAK_GBS, 4),
         )
+    per[head]["module_ms_per_step"] = round(module_ms, 4)
+    per[head]["module_tokens_per_s"] = round(w.tokens / (module_ms / 1000.0), 1)
     decode = {}
     if not args.only_headline:
         for name in DECODE_SHAPES:
@@ -325,6 +376,11 @@ def main():
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(head)
+        per[head]["cpu_tokens_per_s"] = cpu["value"]
+        if not args.only_headline:
+            for name in results:
+                if name != head:
+                    per[name]["cpu_tokens_per_s"] = cpu_baseline(name)["value"]
     line = {
         "metric": "MoE FFN tokens/s + % roofline (HBM GB/s decode, MFMA util prefill)",
         "value": round(h["tokens_per_s"], 1),

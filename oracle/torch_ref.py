@@ -1,0 +1,97 @@
+"""The reference's MoE layer forward restated with torch CPU operators — TEST
+INFRASTRUCTURE AND CPU BASELINE ONLY.
+
+The same library calls, in the same composition, as the reference's
+per-expert loop path (``TopKMoE.forward`` with ``use_triton_kernels`` off,
+src/quantweave_moe_model.py:113-164, :166-188, :190-211) and
+``QuantizedLinear.forward`` (src/quantization.py:61-72: dequantise to fp32,
+cast to the activation dtype, ``F.linear``).  ``bench.py`` times it on the
+host cores as the CPU baseline of every workload; the tests use it as a
+second, independent restatement next to the numpy/C oracle.  The product
+library never imports it.
+
+Weights are stacks ``[E, out, in]`` (float) or the stored int8/int4 buffers
+with their fp32 scales, as ``Layer`` of quantaweave_amd.workloads holds them.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+
+def dequantize(qweight: torch.Tensor, scales: torch.Tensor, bits: int, in_features: int) -> torch.Tensor:
+    """QuantizedLinear.dequantize (src/quantization.py:61-69): fp32 [out, in]."""
+    out_features = qweight.shape[0]
+    if bits == 8:
+        values = qweight.float()
+    else:
+        pairs = torch.stack([(qweight & 0xF).float() - 8, (qweight >> 4).float() - 8], dim=-1)
+        values = pairs.reshape(out_features, -1)
+    group = values.shape[1] // scales.shape[1]
+    values = values.reshape(out_features, -1, group) * scales[..., None]
+    return values.reshape(out_features, -1)[:, :in_features]
+
+
+class Experts:
+    """The experts of one layer, evaluated one at a time as nn.Linear /
+    QuantizedLinear modules would be (src/quantweave_moe_model.py:59-60)."""
+
+    def __init__(self, fmt: str, gate, up, down, gate_s=None, up_s=None, down_s=None) -> None:
+        self.fmt = fmt
+        self.w = (gate, up, down)
+        self.s = (gate_s, up_s, down_s)
+
+    def _linear(self, x: torch.Tensor, which: int, e: int, in_features: int) -> torch.Tensor:
+        w = self.w[which][e]
+        if self.fmt in ("f32", "bf16"):
+            return F.linear(x, w)
+        bits = 8 if self.fmt == "i8" else 4
+        return F.linear(x, dequantize(w, self.s[which][e], bits, in_features).to(x.dtype))
+
+    def __call__(self, e: int, x: torch.Tensor) -> torch.Tensor:
+        d_model = x.shape[1]
+        d_ff = (self.w[0].shape[1])
+        gate = self._linear(x, 0, e, d_model)
+        up = self._linear(x, 1, e, d_model)
+        return self._linear(F.silu(gate) * up, 2, e, d_ff)
+
+
+def moe_forward(hidden: torch.Tensor, router_w: torch.Tensor, experts: Experts, top_k: int, capacity: int,
+                temperature: float = 1.0, expert_bias: torch.Tensor | None = None):
+    """TopKMoE.forward, dynamic dispatch with the loop executor.  hidden
+    [T, d] in the layer dtype.  Returns (output [T, d], balance, overflow,
+    top_idx, kept_counts)."""
+    E = router_w.shape[0]
+    logits = F.linear(hidden.float(), router_w.float()) / temperature               # :128
+    probs = logits.softmax(dim=-1)                                                  # :129
+    if expert_bias is None:
+        top_w, top_idx = probs.topk(top_k, dim=-1)                                  # :131
+    else:
+        top_idx = (logits + expert_bias.to(logits)).topk(top_k, dim=-1).indices     # :134
+        top_w = probs.gather(1, top_idx)
+    top_w = top_w / top_w.sum(dim=-1, keepdim=True)                                 # :136
+    # the capacity plan: expert ascending, weight descending, route ascending (:172-188)
+    route_e, route_w = top_idx.reshape(-1), top_w.reshape(-1)
+    by_weight = torch.argsort(route_w, descending=True, stable=True)
+    order = by_weight[torch.argsort(route_e[by_weight], stable=True)]
+    counts = torch.bincount(route_e, minlength=E)
+    starts = torch.cumsum(counts, 0) - counts
+    keep = torch.arange(order.numel()) - starts[route_e[order]] < capacity
+    kept = order[keep]
+    tokens, weights = kept // top_k, route_w[kept]
+    kept_counts = counts.clamp(max=capacity)
+    # the loop executor over expert-contiguous rows (:190-211)
+    output = torch.zeros_like(hidden)
+    if tokens.numel():
+        inputs = hidden[tokens]
+        rows, first = [], 0
+        for e, n in enumerate(kept_counts.tolist()):
+            if n:
+                rows.append(experts(e, inputs[first:first + n]))
+                first += n
+        output.index_add_(0, tokens, (torch.cat(rows) * weights[:, None]).to(output.dtype))
+    importance = probs.mean(dim=0)                                                  # :152-154
+    assignments = F.one_hot(top_idx, E).float().mean(dim=(0, 1))
+    balance = E * (importance * assignments).sum()
+    return output, balance, int((~keep).sum()), top_idx, kept_counts

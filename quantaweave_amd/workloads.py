@@ -269,3 +269,34 @@ class DecodeRunner:
         st = self._fn(*self._head, _hip.stream(self.x.device))
         if st:
             _lib.check(st, "qw_moe_decode_step")
+
+
+def module_from_layer(layer: Layer):
+    """A TopKMoE module holding this layer's router and experts (the drop-in
+    surface the reference's callers use), on the layer's device."""
+    from .moe import QuantaWeaveConfig, TopKMoE
+    from .quantization import QuantizedLinear
+
+    w = layer.w
+    cfg = QuantaWeaveConfig(vocab_size=2, hidden_size=w.d_model, layers=1, ffn_size=w.d_ff, num_experts=w.experts,
+                            top_k=w.top_k, attention_heads=1, capacity_factor=w.capacity_factor)
+    dev = layer.x.device
+    moe = TopKMoE(cfg).to(device=dev, dtype=layer.x.dtype)
+    with torch.no_grad():
+        moe.router.weight.copy_(layer.router)
+        for e, expert in enumerate(moe.experts):
+            for name in ("gate", "up", "down"):
+                stored = getattr(layer, name)[e]
+                if layer.fmt in (_lib.QW_F32, _lib.QW_BF16):
+                    getattr(expert, name).weight.copy_(stored)
+                    continue
+                lin = getattr(expert, name)
+                bits = 8 if layer.fmt == _lib.QW_I8 else 4
+                group = layer.group_ff if name == "down" else layer.group_in
+                q = QuantizedLinear(lin.in_features, lin.out_features, bits, group).to(dev)
+                q.qweight.copy_(stored)
+                q.scales.copy_(getattr(layer, name + "_s")[e])
+                setattr(expert, name, q)
+    moe.expert_bias = layer.bias
+    moe.requires_grad_(False)
+    return moe
