@@ -147,7 +147,7 @@ int qw_moe_experts(const void* x, int act_dtype, const int32_t* row_index, const
 enum qw_ffn_path {
   QW_PATH_AUTO = 0,    /* what qw_moe_experts picks for the shape */
   QW_PATH_GENERAL = 1, /* the general kernel: every format and shape */
-  QW_PATH_MFMA = 2,    /* the matrix-core prefill kernels */
+  QW_PATH_MFMA = 2,    /* the matrix-core kernels (bf16 prefill; fp32) */
   QW_PATH_STREAM = 3   /* the weight-streaming decode kernels */
 };
 

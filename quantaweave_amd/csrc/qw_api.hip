@@ -153,11 +153,15 @@ int experts(const void* x, int act, const int32_t* row_index, const int32_t* off
       a.avg_rows = std::max<int64_t>(a.avg_rows, 16);
       st = launch_ffn_mfma(a, stream, &handled);
       if (st || handled) return st;
+      st = launch_ffn_f32(a, stream, &handled);
+      if (st || handled) return st;
       return set_error(QW_ERR_UNSUPPORTED, "the matrix-core kernels do not take this shape or format");
     default:
       st = launch_ffn_gemv(a, stream, &handled);
       if (st || handled) return st;
       st = launch_ffn_mfma(a, stream, &handled);
+      if (st || handled) return st;
+      st = launch_ffn_f32(a, stream, &handled);
       if (st || handled) return st;
       return launch_ffn_generic(a, stream);
   }
@@ -572,6 +576,12 @@ int qw_grouped_matmul(const void* x, int act_dtype, const void* w, int w_format,
   if (act_dtype == QW_BF16 && w_format == QW_BF16 && gemm_rows_fits(in_features, rows, experts) &&
       ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out)) & 15) == 0)
     return gemm_grouped_forward(x, w, experts, out_features, in_features, offsets, rows, per, out, as_stream(stream));
+  if (act_dtype == QW_F32 && w_format == QW_F32) {
+    bool handled = false;
+    const int st = grouped_matmul_f32(static_cast<const float*>(x), static_cast<const float*>(w), experts, out_features,
+                                      in_features, offsets, rows, static_cast<float*>(out), as_stream(stream), &handled);
+    if (st || handled) return st;
+  }
   const WView v = make_wview(w_format, w, scales, out_features, in_features, group);
   return grouped_matmul_generic(x, act_dtype, v, w_format, experts, offsets, rows, out, as_stream(stream));
 }

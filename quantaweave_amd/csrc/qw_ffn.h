@@ -29,6 +29,9 @@ struct FfnArgs {
 
 int launch_ffn_generic(const FfnArgs& a, hipStream_t stream);
 int launch_ffn_mfma(const FfnArgs& a, hipStream_t stream, bool* handled);
+int launch_ffn_f32(const FfnArgs& a, hipStream_t stream, bool* handled);
+int grouped_matmul_f32(const float* x, const float* w, int64_t E, int64_t N, int64_t K, const int32_t* offsets,
+                       int64_t rows, float* out, hipStream_t stream, bool* handled);
 int launch_ffn_gemv(const FfnArgs& a, hipStream_t stream, bool* handled);
 
 }  // namespace qw

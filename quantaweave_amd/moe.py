@@ -130,13 +130,15 @@ class ExpertPack:
     """Experts' weights stacked once into [E, out, in] device buffers.
 
     Replaces the per-call ``torch.stack`` of src/moe_kernels.py:191-193; the pack
-    is rebuilt only when a parameter or buffer changes (tracked by its storage
-    pointer and version counter).  bf16 weights whose shapes allow it are kept
+    is rebuilt only when a projection module, parameter or buffer changes
+    (tracked by identity, storage pointer and version counter).  bf16 weights whose shapes allow it are kept
     in the QW_BF16T tiles the prefill kernels stream contiguously."""
 
     def __init__(self, experts: nn.ModuleList) -> None:
         self.fmt, self.group_in, self.group_ff = _expert_format(experts)
-        self.key = ExpertPack.signature(experts)
+        self.mods, self.tensors = ExpertPack.sources(experts)
+        self.versions = [t._version for t in self.tensors]
+        self.ptrs = [t.data_ptr() for t in self.tensors]
         if self.fmt in (_lib.QW_F32, _lib.QW_BF16):
             self.gate = torch.stack([e.gate.weight.detach() for e in experts]).contiguous()
             self.up = torch.stack([e.up.weight.detach() for e in experts]).contiguous()
@@ -160,14 +162,26 @@ class ExpertPack:
             self.fmt = _lib.QW_BF16T
 
     @staticmethod
-    def signature(experts: nn.ModuleList) -> tuple:
-        sig = []
-        for e in experts:
-            for name in ("gate", "up", "down"):
-                p = getattr(e, name)
-                tensors = (p.qweight, p.scales) if isinstance(p, QuantizedLinear) else (p.weight,)
-                sig.extend((t.data_ptr(), t._version, t.dtype, tuple(t.shape)) for t in tensors)
-        return tuple(sig)
+    def sources(experts: nn.ModuleList) -> tuple[list, list]:
+        """The projection modules and the tensors the pack was made from."""
+        mods = [m for e in experts._modules.values() for m in (e._modules["gate"], e._modules["up"], e._modules["down"])]
+        tensors = []
+        for m in mods:
+            if isinstance(m, QuantizedLinear):
+                tensors += (m._buffers["qweight"], m._buffers["scales"])
+            else:
+                tensors.append(m._parameters["weight"])
+        return mods, tensors
+
+    def current(self, experts: nn.ModuleList) -> bool:
+        """True while the experts hold the same modules and tensors, unmodified
+        (same storage, same version counter): the per-call check."""
+        mods, tensors = ExpertPack.sources(experts)
+        if len(mods) != len(self.mods) or any(a is not b for a, b in zip(mods, self.mods)):
+            return False
+        if any(a is not b for a, b in zip(tensors, self.tensors)):
+            return False
+        return [t._version for t in tensors] == self.versions and [t.data_ptr() for t in tensors] == self.ptrs
 
     def args(self) -> list:
         return [self.fmt, self.group_in, self.group_ff, _hip.ptr(self.gate), _hip.ptr(self.gate_s),
@@ -197,7 +211,7 @@ class ExpertPack:
             return self
         if getattr(self, "_bf16", None) is None:
             cast = ExpertPack.__new__(ExpertPack)
-            cast.fmt, cast.group_in, cast.group_ff, cast.key = _lib.QW_BF16, 0, 0, self.key
+            cast.fmt, cast.group_in, cast.group_ff = _lib.QW_BF16, 0, 0
             cast.gate, cast.up, cast.down = (t.to(torch.bfloat16).contiguous() for t in (self.gate, self.up, self.down))
             cast.gate_s = cast.up_s = cast.down_s = None
             cast.maybe_tile()
@@ -215,7 +229,7 @@ class ExpertPack:
 
 def packed_experts(owner: nn.Module, experts: nn.ModuleList) -> ExpertPack:
     pack = getattr(owner, "_qw_pack", None)
-    if pack is None or pack.key != ExpertPack.signature(experts):
+    if pack is None or not pack.current(experts):
         pack = ExpertPack(experts)
         owner._qw_pack = pack
     return pack
@@ -384,30 +398,46 @@ def _forward_call(flat: Tensor, act: int, router_w: Tensor, moe: TopKMoE, pack: 
     T, width = flat.shape
     E, K = moe.num_experts, moe.top_k
     R = T * K
+    Rm = max(R, 1)
     rw = _router_operand(router_w)
-    r = dict(out=torch.empty_like(flat), probs=torch.empty(T, E, dtype=torch.float32, device=dev),
-             top_idx=torch.empty(T, K, dtype=torch.int32, device=dev),
-             top_w=torch.empty(T, K, dtype=torch.float32, device=dev),
-             counts=torch.empty(E, dtype=torch.int32, device=dev),
-             kept_counts=torch.empty(E, dtype=torch.int32, device=dev),
-             totals=torch.zeros(2, dtype=torch.int32, device=dev),
-             dropped_token=torch.empty(max(R, 1), dtype=torch.int32, device=dev),
-             dropped_expert=torch.empty(max(R, 1), dtype=torch.int32, device=dev),
-             balance=torch.zeros((), dtype=torch.float32, device=dev))
-    if T:
-        s = _hip.stream(dev)
-        d_ff = moe.experts[0].gate.out_features
-        nbytes = _lib.load().qw_moe_forward_workspace_bytes(T, width, E, K, d_ff, act)
-        ws = _hip.workspace(nbytes, dev)
-        _lib.call("qw_moe_forward", _hip.ptr(flat), act, T, width, _hip.ptr(rw), _hip.act_code(rw, "router"),
-                  float(moe.router_temperature), _hip.ptr(bias), E, K, cap, d_ff, *pack.args(), _hip.ptr(r["out"]),
-                  _hip.ptr(r["probs"]), _hip.ptr(r["top_idx"]), _hip.ptr(r["top_w"]), _hip.ptr(r["counts"]),
-                  _hip.ptr(r["kept_counts"]), _hip.ptr(r["totals"]), _hip.ptr(r["dropped_token"]),
-                  _hip.ptr(r["dropped_expert"]), _hip.ptr(ws), nbytes, s)
-        importance = torch.empty(E, dtype=torch.float32, device=dev)
-        _lib.call("qw_moe_balance", _hip.ptr(r["probs"]), _hip.ptr(r["counts"]), T, K, E, _hip.ptr(importance),
-                  _hip.ptr(r["balance"]), s)
+    # the per-call outputs in two slabs (int32 and fp32), handed out as views
+    ints = torch.empty(T * K + 2 * E + 2 + 2 * Rm, dtype=torch.int32, device=dev)
+    flts = torch.empty(T * E + T * K + 1 + E, dtype=torch.float32, device=dev)
+    r = dict(out=torch.empty_like(flat), probs=flts[:T * E].view(T, E), top_w=flts[T * E:T * E + T * K].view(T, K),
+             balance=flts[T * E + T * K:T * E + T * K + 1].view(()),
+             top_idx=ints[:T * K].view(T, K), counts=ints[T * K:T * K + E], kept_counts=ints[T * K + E:T * K + 2 * E],
+             totals=ints[T * K + 2 * E:T * K + 2 * E + 2], dropped_token=ints[T * K + 2 * E + 2:T * K + 2 * E + 2 + Rm],
+             dropped_expert=ints[T * K + 2 * E + 2 + Rm:])
+    importance = flts[T * E + T * K + 1:]
+    if not T:
+        r["totals"].zero_()
+        r["balance"].zero_()
+        return r
+    s = _hip.stream(dev)
+    d_ff = moe.experts[0].gate.out_features
+    nbytes = _lib.load().qw_moe_forward_workspace_bytes(T, width, E, K, d_ff, act)
+    ws = _stream_workspace(moe, nbytes, dev)
+    _lib.call("qw_moe_forward", _hip.ptr(flat), act, T, width, _hip.ptr(rw), _hip.act_code(rw, "router"),
+              float(moe.router_temperature), _hip.ptr(bias), E, K, cap, d_ff, *pack.args(), _hip.ptr(r["out"]),
+              _hip.ptr(r["probs"]), _hip.ptr(r["top_idx"]), _hip.ptr(r["top_w"]), _hip.ptr(r["counts"]),
+              _hip.ptr(r["kept_counts"]), _hip.ptr(r["totals"]), _hip.ptr(r["dropped_token"]),
+              _hip.ptr(r["dropped_expert"]), _hip.ptr(ws), nbytes, s)
+    _lib.call("qw_moe_balance", _hip.ptr(r["probs"]), _hip.ptr(r["counts"]), T, K, E, _hip.ptr(importance),
+              _hip.ptr(r["balance"]), s)
     return r
+
+
+def _stream_workspace(moe: nn.Module, nbytes: int, dev: torch.device) -> Tensor:
+    """The module's forward workspace for the current stream, kept between
+    calls (calls on one stream are ordered, so one buffer serves them all;
+    a call on another stream gets its own).  Grown when a call needs more."""
+    cache = moe.__dict__.setdefault("_qw_workspaces", {})
+    key = (dev, torch.cuda.current_stream(dev).cuda_stream)
+    ws = cache.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = _hip.workspace(nbytes, dev)
+        cache[key] = ws
+    return ws
 
 
 def _compute_dtype(flat: Tensor) -> torch.dtype:

@@ -102,7 +102,7 @@ def test_grouped_swiglu_matches_oracle(act, fmt, D, F_, group, path):
 @pytest.mark.parametrize("act,fmt,group,path", [
     ("bf16", "bf16", None, "mfma"), ("bf16", "bf16", None, "stream"), ("bf16", "bf16", None, "generic"),
     ("bf16", "i8", None, "stream"), ("bf16", "i8", None, "generic"), ("bf16", "u4", 32, "stream"),
-    ("bf16", "u4", 32, "generic"), ("f32", "f32", None, "generic")])
+    ("bf16", "u4", 32, "generic"), ("f32", "f32", None, "generic"), ("f32", "f32", None, "mfma")])
 def test_each_kernel_family_matches_oracle(act, fmt, group, path):
     """The same inputs through every kernel family that takes them
     (qw_moe_experts_on_path), each against the oracle."""
