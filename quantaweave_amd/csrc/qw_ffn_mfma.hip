@@ -38,6 +38,17 @@
 // lane ends up holding 4 consecutive output columns of one row and stores them
 // with one 8-byte write.
 //
+// Quantised weights (QW_I8, QW_U4; src/quantization.py:61-72) take the same
+// path: the slice's stored bytes (64 or 32 per weight row) and its two scales
+// per row (one per MFMA K step; the group size is a multiple of 32) stream into
+// LDS the same way, and each wave turns its weight fragments into bf16 as it
+// reads them: w = bf16(q * scale), the fp32 product rounded once, which is
+// exactly the reference's `dequantize().to(bfloat16)`.  The stored value
+// u = q + bias (bias 128 after flipping the int8 sign bit, 8 for int4 nibbles)
+// is converted to fp32 and fma(u, s, -bias*s) gives q*s with one rounding
+// (bias*s is a power-of-two multiple of s, so exact).  No bf16 copy of the
+// weights is made.
+//
 // Workgroup -> tile order is XCD-aware: workgroups are dispatched round-robin
 // over the 8 XCDs, so block b runs on XCD b%8; all tiles of one expert are
 // given to one XCD and enumerated column-fastest, which keeps the expert's
@@ -63,10 +74,34 @@ constexpr int MF_WAVES = 8;
 constexpr int MF_NT = 4;        // 16-column MFMA tiles per wave
 constexpr int MF_LDS = 160 * 1024;  // LDS per workgroup
 
+// Weight stage of one K slice per weight format: 256 rows of ROWB bytes (64
+// columns), rows XOR-swizzled by 16-byte piece, then (quantised formats) two
+// fp32 scales per row.  A 1 KiB load group covers GROWS whole rows.
+template <int WF>
+struct MfB {
+  static constexpr bool Q = WF == QW_I8 || WF == QW_U4;
+  static constexpr int ROWB = WF == QW_I8 ? 64 : WF == QW_U4 ? 32 : MF_ROWB;
+  static constexpr int W_STAGE = MF_NB * ROWB;
+  static constexpr int S_STAGE = Q ? MF_NB * 2 * 4 : 0;
+  static constexpr int STAGE = W_STAGE + S_STAGE;
+  static constexpr int LPR = ROWB / 16;     // lanes (16-byte pieces) per row
+  static constexpr int GROWS = 64 / LPR;    // rows per load group
+  static constexpr int BL = W_STAGE / 1024 / MF_WAVES;  // weight load groups per wave
+  static constexpr int SL = Q ? 1 : 0;      // scale loads per wave (256 bytes each)
+  // physical piece of logical piece p in row r: the 16 rows of a fragment read
+  // spread over distinct banks
+  static __device__ __forceinline__ int swz(int r, int p) {
+    if constexpr (WF == QW_I8) return p ^ ((r >> 2) & 3);
+    else if constexpr (WF == QW_U4) return p ^ ((r >> 3) & 1);
+    else return p ^ ((r >> 1) & 7);
+  }
+};
+
 // Ring stages (activation and weight slices together) that fit the LDS, at most
 // three; the slices requested ahead are one fewer.
+template <int WF>
 constexpr int mf_stages(int subt) {
-  const int stage = 32 * subt * MF_ROWB + MF_NB * MF_ROWB;
+  const int stage = 32 * subt * MF_ROWB + MfB<WF>::STAGE;
   return MF_LDS / stage >= 3 ? 3 : 2;
 }
 constexpr int kXcds = 8;
@@ -93,20 +128,59 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <bool GATEUP, int SUBT, bool TILED>
+// Weights of one projection for the kernel: bytes per expert and per stored
+// row; scales (quantised formats) per expert, per row, and the group size.
+struct MfW {
+  const char* w;
+  const float* scales;
+  int64_t expert_bytes, row_bytes, expert_scales;
+  int groups, group;
+};
+
+// Eight int8 weights (bytes 0..7 = columns c..c+7) -> bf16(q * s).  The sign
+// bit flip stores u = q + 128; fma(u, s, -128 s) = q s rounded once.
+__device__ __forceinline__ bf16x8 dequant_i8(uint2 raw, float s) {
+  const uint32_t u0 = raw.x ^ 0x80808080u, u1 = raw.y ^ 0x80808080u;
+  const float c = -128.0f * s;
+  bf16x8 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    r[i] = static_cast<__bf16>(__builtin_fmaf(static_cast<float>((u0 >> (8 * i)) & 0xffu), s, c));
+    r[4 + i] = static_cast<__bf16>(__builtin_fmaf(static_cast<float>((u1 >> (8 * i)) & 0xffu), s, c));
+  }
+  return r;
+}
+
+// Eight int4 weights (byte b: column c+2b in the low nibble, c+2b+1 in the
+// high one, each stored as q + 8) -> bf16(q * s).
+__device__ __forceinline__ bf16x8 dequant_u4(uint32_t raw, float s) {
+  const uint32_t lo = raw & 0x0f0f0f0fu, hi = (raw >> 4) & 0x0f0f0f0fu;
+  const float c = -8.0f * s;
+  bf16x8 r;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    r[2 * b] = static_cast<__bf16>(__builtin_fmaf(static_cast<float>((lo >> (8 * b)) & 0xffu), s, c));
+    r[2 * b + 1] = static_cast<__bf16>(__builtin_fmaf(static_cast<float>((hi >> (8 * b)) & 0xffu), s, c));
+  }
+  return r;
+}
+
+template <bool GATEUP, int SUBT, int WF>
 __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
-    int max_rows, const uint16_t* __restrict__ wa, const uint16_t* __restrict__ wb, int64_t w_expert_stride,
-    int n_w, int K, const float* __restrict__ row_weight, uint16_t* __restrict__ out, int n_out, int n_tiles,
-    int m_chunks, int experts, uint16_t* __restrict__ save_a, uint16_t* __restrict__ save_b) {
+    int max_rows, const MfW wa, const MfW wb, int n_w, int K, const float* __restrict__ row_weight,
+    uint16_t* __restrict__ out, int n_out, int n_tiles, int m_chunks, int experts, uint16_t* __restrict__ save_a,
+    uint16_t* __restrict__ save_b) {
+  using B = MfB<WF>;
+  constexpr bool TILED = WF == QW_BF16T;
   constexpr int MCH = 32 * SUBT;                 // rows per chunk
   constexpr int AG = MCH / MF_GROWS;             // 8-row load groups of the A slice
-  constexpr int BG = MF_NB / MF_GROWS;           // ... of the B slice
-  constexpr int A_STAGE = MCH * MF_ROWB, B_STAGE = MF_NB * MF_ROWB;
+  constexpr int A_STAGE = MCH * MF_ROWB, B_STAGE = B::STAGE;
   constexpr int AL = AG / MF_WAVES;              // A groups per wave
-  constexpr int BL = BG / MF_WAVES;
-  constexpr int ST = mf_stages(SUBT), AHEAD = ST - 1;
-  static_assert(AG % MF_WAVES == 0 && BG % MF_WAVES == 0, "load groups per wave");
+  constexpr int BL = B::BL, SL = B::SL;          // weight groups and scale loads per wave
+  constexpr int BLQ = BL + SL;
+  constexpr int ST = mf_stages<WF>(SUBT), AHEAD = ST - 1;
+  static_assert(AG % MF_WAVES == 0 && B::W_STAGE % (1024 * MF_WAVES) == 0, "load groups per wave");
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   char* const a_ring = smem;
   char* const b_ring = smem + ST * A_STAGE;
@@ -137,8 +211,8 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
   const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
   const int wm = wave / 4, wn = wave % 4;
   const int n0 = nt * (GATEUP ? MF_NB / 2 : MF_NB);
-  const uint16_t* wa_e = wa + static_cast<int64_t>(e) * w_expert_stride;
-  const uint16_t* wb_e = wb + static_cast<int64_t>(e) * w_expert_stride;
+  const char* wa_e = wa.w + static_cast<int64_t>(e) * wa.expert_bytes;
+  const char* wb_e = wb.w + static_cast<int64_t>(e) * wb.expert_bytes;
 
   // ---- per-lane global sources of this wave's load groups (constant over K) ----
   // lane i of a group writes LDS row (8g + i/8), physical piece i%8, which holds
@@ -154,26 +228,45 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
     const int64_t src = row_index ? row_index[r0 + rr] : (r0 + rr);
     a_src[q] = x + src * K + swz(row, lpiece) * 8;
   }
-  const uint16_t* b_src[BL];
+  // weight row (of the projection) behind LDS weight row `row`
+  auto weight_row = [&](int row, bool* second) {
+    int wrow;
+    if (GATEUP) {
+      wrow = n0 + (row % (MF_NB / 2));
+      *second = row >= MF_NB / 2;
+    } else {
+      wrow = n0 + row;
+      *second = false;
+    }
+    return min(wrow, n_w - 1);
+  };
+  const char* b_src[BL];
 #pragma unroll
   for (int q = 0; q < BL; ++q) {
     const int g = wave + q * MF_WAVES;
-    const int row = MF_GROWS * g + lrow;
-    int wrow;
-    const uint16_t* base;
-    if (GATEUP) {
-      wrow = n0 + (row % (MF_NB / 2));
-      base = row < MF_NB / 2 ? wa_e : wb_e;
-    } else {
-      wrow = n0 + row;
-      base = wa_e;
-    }
-    wrow = min(wrow, n_w - 1);
+    const int row = B::GROWS * g + lane / B::LPR;
+    bool second;
+    const int wrow = weight_row(row, &second);
+    const char* base = second ? wb_e : wa_e;
+    const int64_t row_bytes = second ? wb.row_bytes : wa.row_bytes;
     // the LDS row's swizzle, (row >> 1) & 7, equals (wrow >> 1) & 7: n0 is a multiple of 128
     if (TILED)  // the group's tile column: tiles [wrow/8][kt], one contiguous KiB each
-      b_src[q] = base + static_cast<int64_t>(wrow & ~7) * K + lane * 8;
+      b_src[q] = base + static_cast<int64_t>(wrow & ~7) * row_bytes + lane * 16;
     else
-      b_src[q] = base + static_cast<int64_t>(wrow) * K + swz(row, lpiece) * 8;
+      b_src[q] = base + static_cast<int64_t>(wrow) * row_bytes + B::swz(row, lane % B::LPR) * 16;
+  }
+  // scales: lane i of wave w loads the scale of LDS row (64w + i) / 2 for MFMA
+  // K step i % 2 (dword 64w + i of the scale stage)
+  const float* s_src = nullptr;
+  int s_ks = 0, s_group = 1;
+  if constexpr (B::Q) {
+    const int idx = wave * 64 + lane;
+    bool second;
+    const int wrow = weight_row(idx / 2, &second);
+    const MfW& v = second ? wb : wa;
+    s_src = v.scales + static_cast<int64_t>(e) * v.expert_scales + static_cast<int64_t>(wrow) * v.groups;
+    s_ks = idx % 2;
+    s_group = v.group;
   }
   auto issue_a = [&](int kt) {
     char* st = a_ring + (kt % ST) * A_STAGE;
@@ -187,13 +280,15 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
   };
   auto issue_b = [&](int kt) {
     char* st = b_ring + (kt % ST) * B_STAGE;
-    const int k0 = kt * MF_BK;
 #pragma unroll
     for (int q = 0; q < BL; ++q) {
       const int g = wave + q * MF_WAVES;
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(b_src[q] + (TILED ? kt * 512 : k0)),
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(b_src[q] + kt * (TILED ? 1024 : B::ROWB)),
                                        (lds_void*)(st + g * 1024), 16, 0, 0);
     }
+    if constexpr (B::Q)
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(s_src + (kt * MF_BK + 32 * s_ks) / s_group),
+                                       (lds_void*)(st + B::W_STAGE + wave * 256), 4, 0, 0);
   };
 
   f32x4 acc[SUBT][MF_NT];
@@ -223,7 +318,7 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
     issue_b(j);
   }
   static_assert(SUBT % 2 == 0, "sub-tiles come in pairs");
-  static_assert(AHEAD >= 1 && AHEAD <= 2 && 2 * (AL + BL) < 64, "ring depth");
+  static_assert(AHEAD >= 1 && AHEAD <= 2 && 2 * (AL + BLQ) < 64, "ring depth");
   constexpr int NP = SUBT / 2;  // pairs of sub-tiles per K step
   // The K loop, for a wave whose first NPA sub-tile pairs hold rows: pairs
   // wholly past the expert's rows are not multiplied (their rows are loaded
@@ -232,7 +327,7 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
   auto k_loop = [&](auto npa) {
     constexpr int NPA = decltype(npa)::value;
     for (int kt = 0; kt < KT; ++kt) {
-      if (AHEAD == 2 && kt + 1 < KT) wait_vmcnt<AL + BL>();
+      if (AHEAD == 2 && kt + 1 < KT) wait_vmcnt<AL + BLQ>();
       else wait_vmcnt<0>();
       ring_barrier();
       const char* st_a = a_ring + (kt % ST) * A_STAGE;
@@ -241,9 +336,18 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
         const int row = (wm + 2 * i) * 16 + l16;
         return *reinterpret_cast<const bf16x8*>(st_a + row * MF_ROWB + swz(row, lq + 4 * ks) * 16);
       };
-      auto read_b = [&](int t, int ks) {
+      auto read_b = [&](int t, int ks) -> bf16x8 {
         const int row = brow[t] + l16;
-        return *reinterpret_cast<const bf16x8*>(st_b + row * MF_ROWB + swz(row, lq + 4 * ks) * 16);
+        if constexpr (WF == QW_I8) {  // 8 bytes: columns 32ks + 8lq ..
+          const uint2 raw = *reinterpret_cast<const uint2*>(st_b + row * B::ROWB +
+                                                            B::swz(row, 2 * ks + lq / 2) * 16 + (lq % 2) * 8);
+          return dequant_i8(raw, *reinterpret_cast<const float*>(st_b + B::W_STAGE + (row * 2 + ks) * 4));
+        } else if constexpr (WF == QW_U4) {  // 4 bytes: columns 32ks + 8lq ..
+          const uint32_t raw = *reinterpret_cast<const uint32_t*>(st_b + row * B::ROWB + B::swz(row, ks) * 16 + lq * 4);
+          return dequant_u4(raw, *reinterpret_cast<const float*>(st_b + B::W_STAGE + (row * 2 + ks) * 4));
+        } else {
+          return *reinterpret_cast<const bf16x8*>(st_b + row * MF_ROWB + swz(row, lq + 4 * ks) * 16);
+        }
       };
       // Units u = 0 .. 2*NP-1 are (K step ks = u / NP, sub-tile pair p = u % NP),
       // with activation fragments in two pair buffers (u & 1) and weight fragments
@@ -256,7 +360,7 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
       for (int t = 0; t < MF_NT; ++t) wfr[0][t] = read_b(t, 0);
       xb[0][0] = read_a(0, 0);
       xb[0][1] = read_a(1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, MF_NT + 2, 0);  // first fragments, then the requests
+      __builtin_amdgcn_sched_group_barrier(0x100, (B::Q ? 2 : 1) * MF_NT + 2, 0);  // first fragments, then the requests
       if (kt + AHEAD < KT) {
         issue_a(kt + AHEAD);
         issue_b(kt + AHEAD);
@@ -274,7 +378,7 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
             for (int t = 0; t < MF_NT; ++t) wfr[1][t] = read_b(t, 1);
             xb[(u + 1) & 1][0] = read_a(2 * p1, 1);
             xb[(u + 1) & 1][1] = read_a(2 * p1 + 1, 1);
-            __builtin_amdgcn_sched_group_barrier(0x100, MF_NT + 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, (B::Q ? 2 : 1) * MF_NT + 2, 0);
           } else {
             xb[(u + 1) & 1][0] = read_a(2 * p1, ks1);
             xb[(u + 1) & 1][1] = read_a(2 * p1 + 1, ks1);
@@ -376,10 +480,24 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
   }
 }
 
-template <bool GATEUP, int SUBT, bool TILED>
-int launch_t(const void* x, const int32_t* row_index, const int32_t* offsets, int max_rows, const void* wa,
-             const void* wb, int64_t w_stride, int n_w, int K, const float* row_weight, void* out, int n_out,
-             int experts, int64_t rows_cap, void* save_a, void* save_b, hipStream_t stream) {
+// Kernel view of one stacked projection.
+MfW mf_view(int wf, const WView& v) {
+  const int64_t esize = wf == QW_BF16 || wf == QW_BF16T ? 2 : 1;  // QW_U4 strides are in bytes already
+  MfW m;
+  m.w = static_cast<const char*>(v.w);
+  m.scales = v.scales;
+  m.expert_bytes = v.expert_elems * esize;
+  m.row_bytes = v.row_stride * esize;
+  m.expert_scales = v.expert_scales;
+  m.groups = static_cast<int>(v.groups);
+  m.group = static_cast<int>(v.group > 0 ? v.group : 1);
+  return m;
+}
+
+template <bool GATEUP, int SUBT, int WF>
+int launch_t(const void* x, const int32_t* row_index, const int32_t* offsets, int max_rows, const MfW& wa,
+             const MfW& wb, int n_w, int K, const float* row_weight, void* out, int n_out, int experts,
+             int64_t rows_cap, void* save_a, void* save_b, hipStream_t stream) {
   const int n_tiles = static_cast<int>(ceil_div(GATEUP ? n_w : n_out, GATEUP ? MF_NB / 2 : MF_NB));
   // chunks one XCD can own: its experts' chunks at the capacity bound, and at
   // most all rows in chunks plus one partial chunk per expert
@@ -390,27 +508,27 @@ int launch_t(const void* x, const int32_t* row_index, const int32_t* offsets, in
   const int m_chunks = slots <= found ? static_cast<int>(ceil_div(rows_cap, 32 * SUBT)) : 0;
   const int64_t grid = static_cast<int64_t>(kXcds) * chunks * n_tiles;
   if (grid > INT32_MAX) return set_error(QW_ERR_UNSUPPORTED, "MFMA grid too large");
-  const size_t lds = static_cast<size_t>(mf_stages(SUBT)) * (32 * SUBT * MF_ROWB + MF_NB * MF_ROWB);
-  const hipError_t attr = reserve_lds<ffn_mfma_kernel<GATEUP, SUBT, TILED>>(static_cast<int>(lds));
+  const size_t lds = static_cast<size_t>(mf_stages<WF>(SUBT)) * (32 * SUBT * MF_ROWB + MfB<WF>::STAGE);
+  const hipError_t attr = reserve_lds<ffn_mfma_kernel<GATEUP, SUBT, WF>>(static_cast<int>(lds));
   if (attr != hipSuccess)
     return set_error(QW_ERR_HIP, "cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(attr));
-  ffn_mfma_kernel<GATEUP, SUBT, TILED><<<static_cast<unsigned>(grid), MF_THREADS, lds, stream>>>(
-      static_cast<const uint16_t*>(x), row_index, offsets, max_rows, static_cast<const uint16_t*>(wa),
-      static_cast<const uint16_t*>(wb), w_stride, n_w, K, row_weight, static_cast<uint16_t*>(out), n_out, n_tiles,
-      m_chunks, experts, static_cast<uint16_t*>(save_a), static_cast<uint16_t*>(save_b));
+  ffn_mfma_kernel<GATEUP, SUBT, WF><<<static_cast<unsigned>(grid), MF_THREADS, lds, stream>>>(
+      static_cast<const uint16_t*>(x), row_index, offsets, max_rows, wa, wb, n_w, K, row_weight,
+      static_cast<uint16_t*>(out), n_out, n_tiles, m_chunks, experts, static_cast<uint16_t*>(save_a),
+      static_cast<uint16_t*>(save_b));
   QW_LAUNCH_CHECK(GATEUP ? "ffn_mfma_kernel<gateup>" : "ffn_mfma_kernel<down>");
   return QW_OK;
 }
 
 // rows_cap: most rows any expert can hold (the capacity bound).
-template <bool GATEUP, bool TILED>
+template <bool GATEUP, int WF>
 int launch_sel(int subt, const void* x, const int32_t* row_index, const int32_t* offsets, int max_rows,
-               const void* wa, const void* wb, int64_t w_stride, int n_w, int K, const float* row_weight, void* out,
-               int n_out, int experts, int64_t rows_cap, void* save_a, void* save_b, hipStream_t stream) {
+               const MfW& wa, const MfW& wb, int n_w, int K, const float* row_weight, void* out, int n_out,
+               int experts, int64_t rows_cap, void* save_a, void* save_b, hipStream_t stream) {
 #define QW_MF(S)                                                                                                \
   if (subt == S)                                                                                               \
-    return launch_t<GATEUP, S, TILED>(x, row_index, offsets, max_rows, wa, wb, w_stride, n_w, K, row_weight, out,   \
-                                      n_out, experts, rows_cap, save_a, save_b, stream);
+    return launch_t<GATEUP, S, WF>(x, row_index, offsets, max_rows, wa, wb, n_w, K, row_weight, out, n_out,     \
+                                   experts, rows_cap, save_a, save_b, stream);
   QW_MF(2)
   QW_MF(4)
   QW_MF(6)
@@ -427,26 +545,44 @@ int pick_subt(int64_t rows_cap) {
   return 10;
 }
 
+// The quantised projection suits the LDS stage: groups of whole MFMA K steps,
+// 16-byte aligned rows and base.
+bool quant_fits(const WView& v, int wf) {
+  const int64_t row_bytes = v.row_stride;  // int8: one byte per element; int4: bytes
+  return v.group > 0 && v.group % 32 == 0 && row_bytes % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(v.w) % 16 == 0 && reinterpret_cast<uintptr_t>(v.scales) % 4 == 0 &&
+         (wf == QW_I8 || wf == QW_U4);
+}
+
 }  // namespace
 
 int launch_ffn_mfma(const FfnArgs& a, hipStream_t stream, bool* handled) {
   *handled = false;
-  if (a.act != QW_BF16 || (a.wfmt != QW_BF16 && a.wfmt != QW_BF16T)) return QW_OK;
+  const bool quant = a.wfmt == QW_I8 || a.wfmt == QW_U4;
+  if (a.act != QW_BF16 || (a.wfmt != QW_BF16 && a.wfmt != QW_BF16T && !quant)) return QW_OK;
   if (a.d_model % 64 || a.d_ff % 64) return QW_OK;
+  if (quant && !(quant_fits(a.gate, a.wfmt) && quant_fits(a.up, a.wfmt) && quant_fits(a.down, a.wfmt))) return QW_OK;
   if (a.avg_rows < 16) return QW_OK;  // decode-sized: weight streaming kernels
   const int64_t rows_cap = a.row_cap > 0 ? a.row_cap : a.max_rows;
   const int subt = pick_subt(rows_cap);
   const int D = static_cast<int>(a.d_model), F = static_cast<int>(a.d_ff), E = static_cast<int>(a.experts);
   const int mr = static_cast<int>(a.max_rows);
-  auto both = [&](auto tiled) -> int {
-    constexpr bool T = decltype(tiled)::value;
-    int st = launch_sel<true, T>(subt, a.x, a.row_index, a.offsets, mr, a.gate.w, a.up.w, a.gate.expert_elems, F, D,
-                                 nullptr, a.hidden, F, E, rows_cap, a.save_gate, a.save_up, stream);
+  const MfW g = mf_view(a.wfmt, a.gate), u = mf_view(a.wfmt, a.up), dn = mf_view(a.wfmt, a.down);
+  auto both = [&](auto wf) -> int {
+    constexpr int WF = decltype(wf)::value;
+    int st = launch_sel<true, WF>(subt, a.x, a.row_index, a.offsets, mr, g, u, F, D, nullptr, a.hidden, F, E,
+                                  rows_cap, a.save_gate, a.save_up, stream);
     if (st) return st;
-    return launch_sel<false, T>(subt, a.hidden, nullptr, a.offsets, mr, a.down.w, a.down.w, a.down.expert_elems, D,
-                                F, a.row_weight, a.y, D, E, rows_cap, a.save_y, nullptr, stream);
+    return launch_sel<false, WF>(subt, a.hidden, nullptr, a.offsets, mr, dn, dn, D, F, a.row_weight, a.y, D, E,
+                                 rows_cap, a.save_y, nullptr, stream);
   };
-  const int st = a.wfmt == QW_BF16T ? both(std::true_type{}) : both(std::false_type{});
+  int st;
+  switch (a.wfmt) {
+    case QW_BF16T: st = both(std::integral_constant<int, QW_BF16T>{}); break;
+    case QW_I8: st = both(std::integral_constant<int, QW_I8>{}); break;
+    case QW_U4: st = both(std::integral_constant<int, QW_U4>{}); break;
+    default: st = both(std::integral_constant<int, QW_BF16>{}); break;
+  }
   if (st) return st;
   *handled = true;
   return QW_OK;

@@ -53,6 +53,11 @@ WORKLOADS = {
         Workload("int4-decode-T16-d4096-E64-f1408-k2", 16, 4096, 64, 1408, 2, 0.0, "bf16", "u4", 1004, group_size=32,
                  batch=16),
         Workload("skewed-T4096-d2048-E64-f1024-k2", 4096, 2048, 64, 1024, 2, 1.0, "bf16", "bf16", 1005, zipf=1.2),
+        # the prefill layer with weight-only quantised experts (int8 per output
+        # row, int4 in groups of 32): the matrix-core path with in-register dequant
+        Workload("int8-prefill-T8192-d2048-E64-f1024-k2", 8192, 2048, 64, 1024, 2, 1.25, "bf16", "i8", 1006, batch=8),
+        Workload("int4-prefill-T8192-d2048-E64-f1024-k2", 8192, 2048, 64, 1024, 2, 1.25, "bf16", "u4", 1007,
+                 group_size=32, batch=8),
     ]
 }
 

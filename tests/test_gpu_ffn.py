@@ -102,7 +102,8 @@ def test_grouped_swiglu_matches_oracle(act, fmt, D, F_, group, path):
 @pytest.mark.parametrize("act,fmt,group,path", [
     ("bf16", "bf16", None, "mfma"), ("bf16", "bf16", None, "stream"), ("bf16", "bf16", None, "generic"),
     ("bf16", "i8", None, "stream"), ("bf16", "i8", None, "generic"), ("bf16", "u4", 32, "stream"),
-    ("bf16", "u4", 32, "generic"), ("f32", "f32", None, "generic"), ("f32", "f32", None, "mfma")])
+    ("bf16", "u4", 32, "generic"), ("f32", "f32", None, "generic"), ("f32", "f32", None, "mfma"),
+    ("bf16", "i8", None, "mfma"), ("bf16", "i8", 64, "mfma"), ("bf16", "u4", 32, "mfma"), ("bf16", "u4", 128, "mfma")])
 def test_each_kernel_family_matches_oracle(act, fmt, group, path):
     """The same inputs through every kernel family that takes them
     (qw_moe_experts_on_path), each against the oracle."""
@@ -119,10 +120,37 @@ def test_each_kernel_family_matches_oracle(act, fmt, group, path):
 
 
 def test_kernel_family_that_does_not_take_the_format_refuses():
-    w = make_weights(len(COUNTS), 256, 512, "i8", 3)
+    # the matrix-core kernels take quantisation groups of whole 32-column K steps
+    w = make_weights(len(COUNTS), 256, 512, "i8", 3, group=16)
     x = oracle.round_bf16(np.random.RandomState(0).randn(sum(COUNTS), 256).astype(np.float32))
     with pytest.raises(RuntimeError, match="matrix-core"):
         run_experts(x, COUNTS, w, "bf16", path="mfma")
+
+
+@pytest.mark.parametrize("fmt,group,D,F_,counts", [
+    ("i8", None, 512, 256, [300, 0, 17, 64, 320, 1]), ("i8", 64, 512, 256, [300, 0, 17, 64, 320, 1]),
+    ("u4", 32, 512, 256, [300, 0, 17, 64, 320, 1]), ("u4", 128, 256, 512, [40, 200, 3]),
+    ("i8", None, 2048, 1024, [256, 250, 262, 241]), ("u4", 32, 2048, 1024, [256, 250, 262, 241])])
+def test_quantised_mfma_equals_bf16_mfma_of_dequantised_weights(fmt, group, D, F_, counts):
+    """The matrix-core path dequantises each weight to bf16(q * scale), the
+    reference's dequantize().to(bfloat16) (src/quantization.py:61-72), and then
+    runs the bf16 kernel's MFMA sequence: its outputs equal, bit for bit, those
+    of the bf16 path given the dequantised weights."""
+    print(f"case quantised mfma fmt={fmt} group={group} D={D} F={F_} counts={counts}", flush=True)
+    rng = np.random.RandomState(D + len(counts))
+    rows = sum(counts)
+    x = oracle.round_bf16(rng.randn(rows, D).astype(np.float32))
+    w = make_weights(len(counts), D, F_, fmt, 5, group)
+    deq = dict(format="bf16", d_model=D, d_ff=F_)
+    for name, gname in (("gate", "group_in"), ("up", "group_in"), ("down", "group_ff")):
+        cols = F_ if name == "down" else D
+        deq[name] = oracle.round_bf16(np.stack([
+            oracle.dequantize(w[name][e], w[name + "_scales"][e], 8 if fmt == "i8" else 4, cols, w[gname])
+            for e in range(len(counts))]))
+    rw = rng.rand(rows).astype(np.float32)
+    got = run_experts(x, counts, w, "bf16", row_weight=rw, path="mfma")
+    ref = run_experts(x, counts, deq, "bf16", row_weight=rw, path="mfma")
+    assert np.array_equal(got.view(np.int32), ref.view(np.int32))
 
 
 def test_gathered_rows_through_row_index():

@@ -101,6 +101,8 @@ SMALL = [
     W.scaled(W.WORKLOADS["int8-decode-T64-d2048-E64-f1024-k2"], d_model=512, d_ff=256),
     W.scaled(W.WORKLOADS["int4-decode-T16-d4096-E64-f1408-k2"], d_model=1024, d_ff=352),
     W.scaled(W.WORKLOADS["skewed-T4096-d2048-E64-f1024-k2"], tokens=1024, d_model=512, d_ff=256),
+    W.scaled(W.WORKLOADS["int8-prefill-T8192-d2048-E64-f1024-k2"], tokens=2048, d_model=512, d_ff=256, experts=8),
+    W.scaled(W.WORKLOADS["int4-prefill-T8192-d2048-E64-f1024-k2"], tokens=2048, d_model=512, d_ff=256, experts=8),
 ]
 
 
