@@ -28,7 +28,9 @@
 extern "C" {
 #endif
 
-/* Element formats.  QW_F32/QW_BF16 describe activations and plain weights.
+/* Element formats.  QW_F32/QW_BF16/QW_F16 describe activations and plain
+ * weights (QW_F16: IEEE binary16, the reference's fp16 autocast and
+ * precision="fp16" decode, src/moe_kernels.py:179-183, src/fast_decode.py:77-80).
  * QW_I8: int8 weights [out, padded] with fp32 scales [out, padded/group].
  * QW_U4: int4 weights packed two per byte [out, padded/2] — even input column
  * in the low nibble, odd column in the high nibble, each stored as q + 8 — with
@@ -40,8 +42,9 @@ extern "C" {
  * p = (i % 8) ^ ((r / 2) % 8).  One tile is what an 8-row, 64-column operand
  * slice of the MFMA kernels holds in LDS, so it streams as one contiguous KiB.
  * No reference counterpart: it is a cache of QW_BF16 weights made by
- * qw_pack_bf16_tiles. */
-enum qw_dtype { QW_F32 = 0, QW_BF16 = 1, QW_I8 = 2, QW_U4 = 3, QW_BF16T = 4 };
+ * qw_pack_bf16_tiles.  QW_F16T: QW_F16 weights in the same tiles (the packing
+ * moves 16-bit elements, so qw_pack_bf16_tiles makes them too). */
+enum qw_dtype { QW_F32 = 0, QW_BF16 = 1, QW_I8 = 2, QW_U4 = 3, QW_BF16T = 4, QW_F16 = 5, QW_F16T = 6 };
 
 /* Status codes.  INVALID maps to ValueError, the others to RuntimeError. */
 enum qw_status {
@@ -73,8 +76,9 @@ int64_t qw_moe_capacity(int64_t tokens, int64_t top_k, int64_t experts, double c
  *   top_idx, w = topk(probs, k)            (expert_bias == NULL)
  *   top_idx = topk(logits + expert_bias, k).indices; w = probs.gather(top_idx)
  *   top_w  = w / w.sum(-1)                                       [T, k] fp32
- * x: [tokens, d_model] (QW_F32 or QW_BF16) with row stride x_row_stride
- * elements; router_w: [experts, d_model] contiguous (QW_F32 or QW_BF16).
+ * x: [tokens, d_model] (QW_F32, QW_BF16 or QW_F16) with row stride x_row_stride
+ * elements; router_w: [experts, d_model] contiguous (QW_F32, QW_BF16 or
+ * QW_F16).  Both are widened to fp32 (the reference's `.float()`).
  * Top-k order is descending, ties resolved towards the lower expert index.
  * 1 <= top_k <= experts <= 1024.  The router GEMM is split over d_model; its
  * fp32 partial sums go to `workspace` and are added in a fixed order. */
@@ -126,10 +130,14 @@ int qw_moe_permute(const void* x, int dtype, int64_t d_model, const int32_t* slo
  * x[row_index[s]] (row_index == NULL: x[s]).  row_weight may be NULL (factor 1).
  * Weights per expert, nn.Linear [out, in] layout, stacked over experts:
  *   QW_F32 / QW_BF16 : gate_w, up_w [E, d_ff, d_model]; down_w [E, d_model, d_ff]
- *   QW_BF16T         : the same matrices in tiles (d_model and d_ff multiples of 64)
+ *   QW_F16           : the same layout in fp16
+ *   QW_BF16T/QW_F16T : the same matrices in tiles (d_model and d_ff multiples of 64)
  *   QW_I8 / QW_U4    : qweight and fp32 scales stacked the same way, group sizes
  *                      group_in (gate/up, over d_model) and group_ff (down)
- * act_dtype: QW_F32 or QW_BF16 (x and y).  Quantised weights are dequantised
+ * act_dtype: QW_F32, QW_BF16 or QW_F16 (x and y).  Weights of another float
+ * type are rounded to act_dtype (the reference's `.to(dtype)` of the stacked
+ * weights); the matrix-core and weight-streaming kernels take 16-bit weights of
+ * act_dtype itself or quantised ones.  Quantised weights are dequantised
  * to fp32, rounded to act_dtype, and multiplied with fp32 accumulation.
  * max_rows bounds kept_offsets[E] (rows of y and of the hidden workspace);
  * max_rows_per_expert bounds every expert's row count (the capacity; 0 when
@@ -147,7 +155,7 @@ int qw_moe_experts(const void* x, int act_dtype, const int32_t* row_index, const
 enum qw_ffn_path {
   QW_PATH_AUTO = 0,    /* what qw_moe_experts picks for the shape */
   QW_PATH_GENERAL = 1, /* the general kernel: every format and shape */
-  QW_PATH_MFMA = 2,    /* the matrix-core kernels (bf16 prefill; fp32) */
+  QW_PATH_MFMA = 2,    /* the matrix-core kernels (bf16/fp16 prefill; fp32) */
   QW_PATH_STREAM = 3   /* the weight-streaming decode kernels */
 };
 
@@ -259,8 +267,9 @@ int qw_quantize(const void* w, int w_dtype, int64_t out_features, int64_t in_fea
 int qw_dequantize(const void* qweight, const float* scales, int bits, int64_t out_features, int64_t in_features,
                   int64_t group_size, float* out, void* stream);
 
-/* Rearranges bf16 weights w [experts, out_features, in_features] (nn.Linear
- * layout, stacked) into the QW_BF16T tiles of the same size.  No reference
+/* Rearranges bf16 (or fp16) weights w [experts, out_features, in_features]
+ * (nn.Linear layout, stacked) into the QW_BF16T (QW_F16T) tiles of the same
+ * size; the packing moves 16-bit elements and ignores their type.  No reference
  * counterpart (the reference's Triton kernels read nn.Linear weights as
  * stored); callers pack once per weight update and pass QW_BF16T. */
 int qw_pack_bf16_tiles(const void* w, int64_t experts, int64_t out_features, int64_t in_features, void* tiled,
@@ -271,9 +280,9 @@ int qw_pack_bf16_tiles(const void* w, int64_t experts, int64_t out_features, int
  * [offsets[e], offsets[e+1]); w [E, out_features, in_features] in w_format
  * (QW_I8 / QW_U4 with fp32 scales and group size `group`, as
  * QuantizedLinear.forward, src/quantization.py:71-72); x and out have
- * act_dtype (QW_F32 or QW_BF16); fp32 accumulation, quantised weights rounded
+ * act_dtype (QW_F32, QW_BF16 or QW_F16); fp32 accumulation, quantised weights rounded
  * to act_dtype before the multiply.  max_rows_per_expert bounds every
- * expert's row count (0: rows); bf16 with plain bf16 weights and
+ * expert's row count (0: rows); bf16 (fp16) with plain bf16 (fp16) weights and
  * in_features % 64 == 0 runs on the matrix cores. */
 int qw_grouped_matmul(const void* x, int act_dtype, const void* w, int w_format, const float* scales, int64_t group,
                       int64_t experts, int64_t out_features, int64_t in_features, const int32_t* offsets,
@@ -293,7 +302,7 @@ int qw_moe_combine_static(const void* y, int y_dtype, const int32_t* route_slot,
 /* ------------------------------------------------------------------------
  * Training: the backward pass of the grouped expert matmuls and of the MoE
  * layer's routing and combine.  All gradients are fp32-accumulated; bf16
- * tensors are rounded where torch's bf16 ops round.
+ * and fp16 tensors are rounded where torch's ops round them.
  * ------------------------------------------------------------------------ */
 
 /* Backward of qw_grouped_matmul with plain weights, _GroupedMatmul.backward
@@ -301,12 +310,12 @@ int qw_moe_combine_static(const void* y, int y_dtype, const int32_t* route_slot,
  *   grad_x[r]   = grad_out[r] @ w[e]            (r in [offsets[e], offsets[e+1]))
  *   grad_w[e]   = grad_out[rows of e]^T @ x[rows of e]   (exactly 0 without rows)
  * grad_out [rows, out_features], x [rows, in_features], w [E, out, in], all of
- * `dtype` (QW_F32 or QW_BF16).  grad_x or grad_w may be NULL (not computed).
+ * `dtype` (QW_F32, QW_BF16 or QW_F16).  grad_x or grad_w may be NULL (not computed).
  * grad_w has grad_w_dtype: `dtype`, or QW_F32 for fp32 parameters multiplied
  * in bf16 (the gradient is then not rounded to bf16).
  * accumulate_grad_x != 0 adds to grad_x instead of overwriting it.
  * max_rows_per_expert bounds every expert's row count (0: `rows`).
- * bf16 with a workspace of qw_grouped_matmul_backward_workspace_bytes runs on
+ * bf16 or fp16 with a workspace of qw_grouped_matmul_backward_workspace_bytes runs on
  * the matrix cores (grad_x when out_features % 64 == 0; grad_w always): the
  * weights and the row blocks are transposed into the workspace first.  fp32,
  * or no workspace, runs the vector-ALU kernels. */

@@ -80,9 +80,21 @@ def round_bf16(a: np.ndarray) -> np.ndarray:
     return out
 
 
+def round_f16(a: np.ndarray) -> np.ndarray:
+    """float32 array rounded to the nearest IEEE binary16 value (returned as
+    float32): numpy's conversion rounds to nearest even and overflows to
+    infinity, as torch's .to(torch.float16) does."""
+    with np.errstate(over="ignore"):
+        return np.asarray(a, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
 def round_act(a: np.ndarray, dtype: str) -> np.ndarray:
     a = np.asarray(a, dtype=np.float32)
-    return round_bf16(a) if dtype == "bf16" else a
+    if dtype == "bf16":
+        return round_bf16(a)
+    if dtype == "f16":
+        return round_f16(a)
+    return a
 
 
 def bf16_bits(a: np.ndarray) -> np.ndarray:
@@ -271,8 +283,9 @@ def expert_weights(w: dict, e: int, dtype: str) -> tuple[np.ndarray, np.ndarray,
     """Effective (gate, up, down) of expert e as the reference multiplies them:
     float weights as stored; quantised ones dequantised (fp32) and cast to the
     activation dtype (src/quantization.py:72)."""
-    if w["format"] in ("f32", "bf16"):
-        return w["gate"][e], w["up"][e], w["down"][e]
+    if w["format"] in ("f32", "bf16", "f16"):
+        # float weights are cast to the activation dtype (src/moe_kernels.py:191-193)
+        return tuple(round_act(w[n][e], dtype) for n in ("gate", "up", "down"))
     bits = 8 if w["format"] == "i8" else 4
     d, f = w["d_model"], w["d_ff"]
     g = dequantize(w["gate"][e], w["gate_scales"][e], bits, d, w["group_in"])

@@ -8,7 +8,10 @@ import torch
 
 from . import _lib
 
-_ACT = {torch.float32: _lib.QW_F32, torch.bfloat16: _lib.QW_BF16}
+_ACT = {torch.float32: _lib.QW_F32, torch.bfloat16: _lib.QW_BF16, torch.float16: _lib.QW_F16}
+# 16-bit float types and the codes of their plain and tiled weight formats
+HALF = {torch.bfloat16: (_lib.QW_BF16, _lib.QW_BF16T), torch.float16: (_lib.QW_F16, _lib.QW_F16T)}
+FLOAT_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
 
 def require_device(t: torch.Tensor, what: str) -> None:
@@ -20,7 +23,7 @@ def act_code(t: torch.Tensor, what: str) -> int:
     try:
         return _ACT[t.dtype]
     except KeyError:
-        raise ValueError(f"{what}: dtype {t.dtype} is not supported (float32 or bfloat16)") from None
+        raise ValueError(f"{what}: dtype {t.dtype} is not supported (float32, bfloat16 or float16)") from None
 
 
 def ptr(t: torch.Tensor | None):

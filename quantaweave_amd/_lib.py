@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libqwmoe.so"
 
-QW_F32, QW_BF16, QW_I8, QW_U4, QW_BF16T = 0, 1, 2, 3, 4
+QW_F32, QW_BF16, QW_I8, QW_U4, QW_BF16T, QW_F16, QW_F16T = 0, 1, 2, 3, 4, 5, 6
 QW_OK, QW_ERR_INVALID, QW_ERR_UNSUPPORTED, QW_ERR_HIP, QW_ERR_WORKSPACE = 0, -1, -2, -3, -4
 QW_PATH_AUTO, QW_PATH_GENERAL, QW_PATH_MFMA, QW_PATH_STREAM = 0, 1, 2, 3
 

@@ -37,8 +37,8 @@ int route_plan_small(const void* x, int xdt, int64_t x_stride, const void* w, in
                      float* probs, int32_t* top_idx, float* top_w, int64_t capacity, int32_t* counts,
                      int32_t* kept_counts, int32_t* kept_offsets, int32_t* totals, int32_t* slot_token,
                      float* slot_weight, int32_t* route_slot, int32_t* dropped_token, int32_t* dropped_expert,
-                     const float* cast_x, uint16_t* cast_out, float* partial, size_t partial_bytes,
-                     hipStream_t stream);
+                     const float* cast_x, uint16_t* cast_out, int cast_dtype, float* partial,
+                     size_t partial_bytes, hipStream_t stream);
 int plan(const int32_t* top_idx, const float* top_w, int64_t T, int64_t K, int64_t E, int64_t capacity,
          int32_t* counts, int32_t* kept_counts, int32_t* kept_offsets, int32_t* slot_token, float* slot_weight,
          int32_t* route_slot, int32_t* dropped_token, int32_t* dropped_expert, int32_t* totals, void* ws,
@@ -49,7 +49,7 @@ int combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* 
             int64_t D, void* out, hipStream_t stream);
 int decode_combine(const void* y, int dtype, const int32_t* route_slot, const float* top_w, const float* residual,
                    int64_t T, int64_t K, int64_t D, float* out, hipStream_t stream);
-int cast_bf16(const float* x, int64_t n, uint16_t* out, hipStream_t stream);
+int cast_half(const float* x, int64_t n, uint16_t* out, int dtype, hipStream_t stream);
 int pack_bf16_tiles(const void* w, int64_t E, int64_t rows, int64_t cols, void* out, hipStream_t stream);
 int balance(const float* probs, const int32_t* counts, int64_t T, int64_t K, int64_t E, float* importance,
             float* bal, hipStream_t stream, float* scratch_importance);
@@ -68,8 +68,8 @@ int grouped_matmul_backward(const void* gy, const void* x, const void* w, int dt
                             void* gw, int gw_dtype, void* ws, size_t ws_bytes, hipStream_t stream);
 size_t grouped_backward_workspace_bytes(int64_t E, int64_t N, int64_t K, int64_t rows, int dtype);
 bool gemm_rows_fits(int64_t K, int64_t rows, int64_t E);
-int gemm_grouped_forward(const void* x, const void* w, int64_t E, int64_t N, int64_t K, const int32_t* offsets,
-                         int64_t rows, int64_t rows_per_expert, void* out, hipStream_t stream);
+int gemm_grouped_forward(const void* x, const void* w, int dtype, int64_t E, int64_t N, int64_t K,
+                         const int32_t* offsets, int64_t rows, int64_t rows_per_expert, void* out, hipStream_t stream);
 int swiglu(const void* g, const void* u, int dtype, int64_t n, void* h, hipStream_t stream);
 int swiglu_backward(const void* dh, const void* g, const void* u, int dtype, int64_t n, void* dg, void* du,
                     hipStream_t stream);
@@ -97,11 +97,11 @@ int experts(const void* x, int act, const int32_t* row_index, const int32_t* off
             void* save_gate = nullptr, void* save_up = nullptr, void* save_y = nullptr,
             void* hidden_out = nullptr, int path = QW_PATH_AUTO) {
   QW_REQUIRE(path >= QW_PATH_AUTO && path <= QW_PATH_STREAM, "unknown kernel path %d", path);
-  QW_REQUIRE(act == QW_F32 || act == QW_BF16, "activation dtype must be f32 or bf16");
-  QW_REQUIRE(wfmt >= QW_F32 && wfmt <= QW_BF16T, "unknown weight format %d", wfmt);
+  QW_REQUIRE(act == QW_F32 || act == QW_BF16 || act == QW_F16, "activation dtype must be f32, bf16 or f16");
+  QW_REQUIRE(wfmt >= QW_F32 && wfmt <= QW_F16T, "unknown weight format %d", wfmt);
   QW_REQUIRE(E >= 1 && E <= 65535, "experts out of range");
-  QW_REQUIRE(wfmt != QW_BF16T || (D % 64 == 0 && F % 64 == 0),
-             "tiled bf16 weights need d_model and d_ff multiples of 64 (got %lld, %lld)", (long long)D, (long long)F);
+  QW_REQUIRE((wfmt != QW_BF16T && wfmt != QW_F16T) || (D % 64 == 0 && F % 64 == 0),
+             "tiled weights need d_model and d_ff multiples of 64 (got %lld, %lld)", (long long)D, (long long)F);
   QW_REQUIRE(D >= 1 && D <= INT32_MAX / 2 && F >= 1 && F <= INT32_MAX / 2, "d_model/d_ff out of range");
   QW_REQUIRE(max_rows >= 0 && max_rows <= INT32_MAX, "max_rows out of range");
   if (wfmt == QW_I8 || wfmt == QW_U4) {
@@ -214,7 +214,7 @@ static DecodeWs carve_decode(void* base, int64_t T, int64_t D, int64_t E, int64_
   w.dropped_token = c.take<int32_t>(R);
   w.dropped_expert = c.take<int32_t>(R);
   w.slot_weight = c.take<float>(R);
-  w.xc = act == QW_BF16 ? c.take<uint16_t>(static_cast<size_t>(T) * D) : nullptr;
+  w.xc = is_half(act) ? c.take<uint16_t>(static_cast<size_t>(T) * D) : nullptr;
   w.y = c.take<char>(static_cast<size_t>(R) * D * act_size(act));
   w.plan_bytes = plan_workspace_bytes(T, K, E);
   w.plan_ws = c.take<char>(w.plan_bytes);
@@ -393,7 +393,8 @@ int qw_moe_forward(const void* x, int act_dtype, int64_t tokens, int64_t d_model
                    float* top_w, int32_t* counts, int32_t* kept_counts, int32_t* totals, int32_t* dropped_token,
                    int32_t* dropped_expert, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
-  QW_REQUIRE(act_dtype == QW_F32 || act_dtype == QW_BF16, "activation dtype must be f32 or bf16");
+  QW_REQUIRE(act_dtype == QW_F32 || act_dtype == QW_BF16 || act_dtype == QW_F16,
+             "activation dtype must be f32, bf16 or f16");
   QW_REQUIRE(tokens >= 0 && top_k >= 1 && experts >= 1 && d_model >= 1 && d_ff >= 1, "bad forward sizes");
   QW_REQUIRE(capacity >= 0, "capacity must be >= 0");
   QW_REQUIRE(probs && top_idx && top_w && counts && kept_counts && totals, "forward outputs are required");
@@ -423,7 +424,7 @@ int qw_moe_forward(const void* x, int act_dtype, int64_t tokens, int64_t d_model
     st = route_plan_small(x, act_dtype, d_model, router_w, router_dtype, tokens, d_model, experts, top_k, temperature,
                           expert_bias, false, logits, probs, top_idx, top_w, capacity, counts, kept_counts,
                           kept_offsets, totals, slot_token, slot_weight, route_slot, dropped_token, dropped_expert,
-                          nullptr, nullptr, rws, route_ws, s);
+                          nullptr, nullptr, act_dtype, rws, route_ws, s);
     if (st) return st;
   } else {
     st = route(x, act_dtype, d_model, router_w, router_dtype, tokens, d_model, experts, top_k, temperature,
@@ -450,7 +451,7 @@ int qw_moe_forward(const void* x, int act_dtype, int64_t tokens, int64_t d_model
 size_t qw_moe_decode_step_workspace_bytes(int64_t tokens, int64_t d_model, int64_t experts, int64_t top_k,
                                           int64_t d_ff, int compute_dtype) {
   if (tokens < 0 || d_model < 1 || experts < 1 || top_k < 1 || d_ff < 1) return 0;
-  if (compute_dtype != QW_F32 && compute_dtype != QW_BF16) return 0;
+  if (compute_dtype != QW_F32 && compute_dtype != QW_BF16 && compute_dtype != QW_F16) return 0;
   return carve_decode(nullptr, tokens, d_model, experts, top_k, d_ff, compute_dtype).used;
 }
 
@@ -462,7 +463,8 @@ int qw_moe_decode_step(const float* x, const float* residual, int64_t tokens, in
                        float* probs, int32_t* top_idx, float* top_w, void* workspace, size_t workspace_bytes,
                        void* stream) {
   clear_error();
-  QW_REQUIRE(compute_dtype == QW_F32 || compute_dtype == QW_BF16, "compute dtype must be f32 or bf16");
+  QW_REQUIRE(compute_dtype == QW_F32 || compute_dtype == QW_BF16 || compute_dtype == QW_F16,
+             "compute dtype must be f32, bf16 or f16");
   QW_REQUIRE(tokens >= 0 && top_k >= 1 && experts >= 1 && d_model >= 1 && d_ff >= 1, "bad decode step sizes");
   QW_REQUIRE(top_k <= experts, "top_k must be between 1 and num_experts (got %lld, %lld)", (long long)top_k,
              (long long)experts);
@@ -475,14 +477,14 @@ int qw_moe_decode_step(const float* x, const float* residual, int64_t tokens, in
   const int64_t R = tokens * top_k;
   const DecodeWs w = carve_decode(workspace, tokens, d_model, experts, top_k, d_ff, compute_dtype);
   // capacity R: every route keeps its slot
-  const void* xc = compute_dtype == QW_BF16 ? static_cast<const void*>(w.xc) : static_cast<const void*>(x);
+  const void* xc = is_half(compute_dtype) ? static_cast<const void*>(w.xc) : static_cast<const void*>(x);
   int st;
   if (route_plan_small_fits(tokens, experts, top_k)) {
     st = route_plan_small(x, QW_F32, d_model, router_w, QW_F32, tokens, d_model, experts, top_k, temperature,
                           expert_bias, /*select_logits=*/true, w.logits, probs, top_idx, top_w, R, w.counts,
                           w.kept_counts, w.kept_offsets, w.totals, w.slot_token, w.slot_weight, w.route_slot,
-                          w.dropped_token, w.dropped_expert, x, compute_dtype == QW_BF16 ? w.xc : nullptr,
-                          w.route_ws, w.route_bytes, s);
+                          w.dropped_token, w.dropped_expert, x, is_half(compute_dtype) ? w.xc : nullptr,
+                          compute_dtype, w.route_ws, w.route_bytes, s);
     if (st) return st;
   } else {
     st = route(x, QW_F32, d_model, router_w, QW_F32, tokens, d_model, experts, top_k, temperature, expert_bias,
@@ -491,8 +493,8 @@ int qw_moe_decode_step(const float* x, const float* residual, int64_t tokens, in
     st = plan(top_idx, top_w, tokens, top_k, experts, R, w.counts, w.kept_counts, w.kept_offsets, w.slot_token,
               w.slot_weight, w.route_slot, w.dropped_token, w.dropped_expert, w.totals, w.plan_ws, w.plan_bytes, s);
     if (st) return st;
-    if (compute_dtype == QW_BF16) {
-      st = cast_bf16(x, tokens * d_model, w.xc, s);
+    if (is_half(compute_dtype)) {
+      st = cast_half(x, tokens * d_model, w.xc, compute_dtype, s);
       if (st) return st;
     }
   }
@@ -513,7 +515,8 @@ int qw_moe_decode_step_noalloc(const float* x, const float* residual, int64_t to
                                const float* up_scales, const void* down_w, const float* down_scales, float* out,
                                float* probs, int32_t* top_idx, float* top_w, void* stream) {
   clear_error();
-  QW_REQUIRE(compute_dtype == QW_F32 || compute_dtype == QW_BF16, "compute dtype must be f32 or bf16");
+  QW_REQUIRE(compute_dtype == QW_F32 || compute_dtype == QW_BF16 || compute_dtype == QW_F16,
+             "compute dtype must be f32, bf16 or f16");
   QW_REQUIRE(tokens >= 0 && top_k >= 1 && experts >= 1 && d_model >= 1 && d_ff >= 1, "bad decode step sizes");
   // sizes first: an oversized call is refused before any device work
   const size_t need = carve_decode(nullptr, tokens, d_model, experts, top_k, d_ff, compute_dtype).used;
@@ -558,10 +561,11 @@ int qw_grouped_matmul(const void* x, int act_dtype, const void* w, int w_format,
                       int64_t experts, int64_t out_features, int64_t in_features, const int32_t* offsets,
                       int64_t rows, int64_t max_rows_per_expert, void* out, void* stream) {
   clear_error();
-  QW_REQUIRE(act_dtype == QW_F32 || act_dtype == QW_BF16, "grouped_matmul dtype must be f32 or bf16");
-  QW_REQUIRE(w_format >= QW_F32 && w_format <= QW_BF16T, "unknown weight format %d", w_format);
-  QW_REQUIRE(w_format != QW_BF16T || (out_features % 8 == 0 && in_features % 64 == 0),
-             "tiled bf16 weights need out_features %% 8 == 0 and in_features %% 64 == 0");
+  QW_REQUIRE(act_dtype == QW_F32 || act_dtype == QW_BF16 || act_dtype == QW_F16,
+             "grouped_matmul dtype must be f32, bf16 or f16");
+  QW_REQUIRE(w_format >= QW_F32 && w_format <= QW_F16T, "unknown weight format %d", w_format);
+  QW_REQUIRE((w_format != QW_BF16T && w_format != QW_F16T) || (out_features % 8 == 0 && in_features % 64 == 0),
+             "tiled weights need out_features %% 8 == 0 and in_features %% 64 == 0");
   QW_REQUIRE(experts >= 1 && experts <= 65535 && out_features >= 1 && in_features >= 1 && rows >= 0 &&
                  out_features <= INT32_MAX / 2 && in_features <= INT32_MAX / 2 && rows <= INT32_MAX,
              "bad grouped_matmul sizes");
@@ -573,9 +577,9 @@ int qw_grouped_matmul(const void* x, int act_dtype, const void* w, int w_format,
   if (rows == 0) return QW_OK;
   QW_REQUIRE(x && w && offsets && out, "grouped_matmul pointers are required");
   const int64_t per = max_rows_per_expert > 0 && max_rows_per_expert < rows ? max_rows_per_expert : rows;
-  if (act_dtype == QW_BF16 && w_format == QW_BF16 && gemm_rows_fits(in_features, rows, experts) &&
+  if (is_half(act_dtype) && w_format == act_dtype && gemm_rows_fits(in_features, rows, experts) &&
       ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out)) & 15) == 0)
-    return gemm_grouped_forward(x, w, experts, out_features, in_features, offsets, rows, per, out, as_stream(stream));
+    return gemm_grouped_forward(x, w, act_dtype, experts, out_features, in_features, offsets, rows, per, out, as_stream(stream));
   if (act_dtype == QW_F32 && w_format == QW_F32) {
     bool handled = false;
     const int st = grouped_matmul_f32(static_cast<const float*>(x), static_cast<const float*>(w), experts, out_features,

@@ -90,22 +90,53 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_
 
 __device__ __forceinline__ float round_to_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// IEEE binary16: the conversion rounds to nearest even (v_cvt_f16_f32), as
+// torch's `.to(torch.float16)` does; values past 65504 become infinities.
+// The fp32 value is pinned first (an empty asm operand): otherwise the
+// compiler folds an fp32 fma or multiply feeding the conversion into one
+// mixed-precision instruction (v_fma_mix*) that rounds once to fp16, where
+// the reference forms the fp32 result and then rounds it to fp16.
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
+__device__ __forceinline__ float pin_f32(float f) {
+  asm("" : "+v"(f));
+  return f;
+}
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(pin_f32(f)));
+}
+__device__ __forceinline__ float round_to_f16(float f) { return f16_to_f32(f32_to_f16(f)); }
+
+// 16-bit activation types (QW_BF16, QW_F16) and their weight formats.
+__host__ __device__ constexpr bool is_half(int dt) { return dt == QW_BF16 || dt == QW_F16; }
+
+template <int DT>
+__device__ __forceinline__ float half_to_f32(uint16_t h) {
+  if constexpr (DT == QW_F16) return f16_to_f32(h);
+  else return bf16_to_f32(h);
+}
+template <int DT>
+__device__ __forceinline__ uint16_t f32_to_half(float f) {
+  if constexpr (DT == QW_F16) return f32_to_f16(f);
+  else return f32_to_bf16(f);
+}
+
 template <int DT>
 __device__ __forceinline__ float load_act(const void* p, int64_t i) {
   if constexpr (DT == QW_F32) return static_cast<const float*>(p)[i];
-  else return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  else return half_to_f32<DT>(static_cast<const uint16_t*>(p)[i]);
 }
 
 template <int DT>
 __device__ __forceinline__ void store_act(void* p, int64_t i, float v) {
   if constexpr (DT == QW_F32) static_cast<float*>(p)[i] = v;
-  else static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+  else static_cast<uint16_t*>(p)[i] = f32_to_half<DT>(v);
 }
 
 // Rounds an fp32 value to what storing it in activation dtype DT keeps.
 template <int DT>
 __device__ __forceinline__ float round_act(float v) {
   if constexpr (DT == QW_F32) return v;
+  else if constexpr (DT == QW_F16) return round_to_f16(v);
   else return round_to_bf16(v);
 }
 
@@ -130,7 +161,16 @@ __device__ __forceinline__ void load_vec(const void* p, int64_t i, float (&v)[VE
       v[u + 2] = q.z;
       v[u + 3] = q.w;
     }
-  } else if constexpr (VEC == 4) {
+  } else if constexpr (VEC % 4 == 0 && DT == QW_F16) {
+#pragma unroll
+    for (int u = 0; u < VEC; u += 4) {
+      const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i + u);
+      v[u] = f16_to_f32(q.x & 0xffffu);
+      v[u + 1] = f16_to_f32(q.x >> 16);
+      v[u + 2] = f16_to_f32(q.y & 0xffffu);
+      v[u + 3] = f16_to_f32(q.y >> 16);
+    }
+  } else if constexpr (VEC == 4 && DT == QW_BF16) {
     const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
     v[0] = __uint_as_float(q.x << 16);
     v[1] = __uint_as_float(q.x & 0xffff0000u);
@@ -156,7 +196,14 @@ __device__ __forceinline__ void store_vec(void* p, int64_t i, const float (&v)[V
 #pragma unroll
     for (int u = 0; u < VEC; u += 4)
       *reinterpret_cast<float4*>(static_cast<float*>(p) + i + u) = make_float4(v[u], v[u + 1], v[u + 2], v[u + 3]);
-  } else if constexpr (VEC == 4) {
+  } else if constexpr (VEC % 4 == 0 && DT == QW_F16) {
+#pragma unroll
+    for (int u = 0; u < VEC; u += 4) {
+      const uint32_t lo = f32_to_f16(v[u]) | (static_cast<uint32_t>(f32_to_f16(v[u + 1])) << 16);
+      const uint32_t hi = f32_to_f16(v[u + 2]) | (static_cast<uint32_t>(f32_to_f16(v[u + 3])) << 16);
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p) + i + u) = make_uint2(lo, hi);
+    }
+  } else if constexpr (VEC == 4 && DT == QW_BF16) {
     const uint32_t lo = f32_to_bf16(v[0]) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
     const uint32_t hi = f32_to_bf16(v[2]) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
     *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p) + i) = make_uint2(lo, hi);

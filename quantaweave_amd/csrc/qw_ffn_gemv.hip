@@ -21,6 +21,10 @@
 //  QW_BF16: a chunk is 8 bf16 weights, used directly by v_dot2_f32_bf16 (also
 //           from QW_BF16T tiles, which only changes where a chunk is read).
 //
+// fp16 activations (QW_F16) take QW_F16/QW_F16T weights with v_dot2_f32_f16;
+// int4 nibbles then become the fp16 pairs 0x64nn = 1024 + n (bias 1032), and
+// int8 codes meet the fp16 activations as they are (no rescaling).
+//
 // The activation pieces matching a lane's chunks come straight from L2 (every
 // wave of the expert reads the same few rows), are put in the pair order of
 // the conversion once per chunk and reused for every row of the wave.  There
@@ -42,12 +46,14 @@ struct Fmt;
 template <>
 struct Fmt<QW_U4> {
   static constexpr int CW = 32;     // weights per 16-byte chunk
-  static constexpr float BIAS = 136.0f;
+  static constexpr float BIAS = 136.0f;       // bf16 activations: nibble pairs 128 + n
+  static constexpr float BIAS_F16 = 1032.0f;  // fp16 activations: 1024 + n
 };
 template <>
 struct Fmt<QW_I8> {
   static constexpr int CW = 16;
   static constexpr float BIAS = 1152.0f;
+  static constexpr float BIAS_F16 = 1152.0f;
 };
 template <>
 struct Fmt<QW_BF16> {
@@ -55,9 +61,13 @@ struct Fmt<QW_BF16> {
 };
 template <>
 struct Fmt<QW_BF16T> : Fmt<QW_BF16> {};  // the same weights in 1 KiB tiles
+template <>
+struct Fmt<QW_F16> : Fmt<QW_BF16> {};
+template <>
+struct Fmt<QW_F16T> : Fmt<QW_BF16> {};
 
-// Format of the arithmetic: tiled bf16 weights are bf16 weights once loaded.
-constexpr int math_fmt(int wf) { return wf == QW_BF16T ? QW_BF16 : wf; }
+// Format of the arithmetic: tiled weights are plain weights once loaded.
+constexpr int math_fmt(int wf) { return wf == QW_BF16T ? QW_BF16 : wf == QW_F16T ? QW_F16 : wf; }
 constexpr bool quantized(int wf) { return wf == QW_I8 || wf == QW_U4; }
 
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
@@ -67,20 +77,23 @@ __device__ __forceinline__ float dot2_f16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(gf16x2, a), __builtin_bit_cast(gf16x2, b), c, false);
 }
 
-// Converts one 16-byte weight chunk into the operand pairs of the dot products.
-template <int WF>
+// Converts one 16-byte weight chunk into the operand pairs of the dot products
+// with activations of type ACT.
+template <int ACT, int WF>
 __device__ __forceinline__ void chunk_pairs(const uint4 w, uint32_t* cw) {
   const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
   if constexpr (WF == QW_U4) {
+    // high bytes 0x43 (bf16 128 + n) or 0x64 (fp16 1024 + n)
+    constexpr uint32_t HB = ACT == QW_F16 ? 0x64646464u : 0x43434343u;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t lo = wd[i] & 0x0F0F0F0Fu;
       const uint32_t hi = (wd[i] >> 4) & 0x0F0F0F0Fu;
-      // bytes [n, 0x43, n', 0x43]: selector picks from {0x43434343 (bytes 4-7), src (bytes 0-3)}
-      cw[4 * i + 0] = __builtin_amdgcn_perm(0x43434343u, lo, 0x04010400u);
-      cw[4 * i + 1] = __builtin_amdgcn_perm(0x43434343u, lo, 0x04030402u);
-      cw[4 * i + 2] = __builtin_amdgcn_perm(0x43434343u, hi, 0x04010400u);
-      cw[4 * i + 3] = __builtin_amdgcn_perm(0x43434343u, hi, 0x04030402u);
+      // bytes [n, HB, n', HB]: selector picks from {HB (bytes 4-7), src (bytes 0-3)}
+      cw[4 * i + 0] = __builtin_amdgcn_perm(HB, lo, 0x04010400u);
+      cw[4 * i + 1] = __builtin_amdgcn_perm(HB, lo, 0x04030402u);
+      cw[4 * i + 2] = __builtin_amdgcn_perm(HB, hi, 0x04010400u);
+      cw[4 * i + 3] = __builtin_amdgcn_perm(HB, hi, 0x04030402u);
     }
   } else if constexpr (WF == QW_I8) {
 #pragma unroll
@@ -99,8 +112,9 @@ __device__ __forceinline__ void chunk_pairs(const uint4 w, uint32_t* cw) {
 // U4: bf16 pairs in the order the nibble conversion emits them, plus the sum
 //     of the chunk's 32 values (the bias correction);
 // I8: fp16 pairs of x * 2^s (s per route, brings max|x| into [2^14, 2^15));
-// BF16: the bf16 pairs as stored.
-template <int WF>
+// BF16 / F16: the pairs as stored.
+// fp16 activations (ACT == QW_F16) are used as they are (scale 1).
+template <int ACT, int WF>
 __device__ __forceinline__ void prep_chunk(const uint4* raw, float scale, uint32_t* xq, float* xsum) {
   if constexpr (WF == QW_U4) {
     float sm = 0.0f;
@@ -112,7 +126,8 @@ __device__ __forceinline__ void prep_chunk(const uint4* raw, float scale, uint32
       xq[4 * q + 2] = __builtin_amdgcn_perm(v[1], v[0], 0x07060302u);  // (1, 3)
       xq[4 * q + 3] = __builtin_amdgcn_perm(v[3], v[2], 0x07060302u);  // (5, 7)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) sm = dot2_bf16(v[t], 0x3f803f80u, sm);  // + x[2t] + x[2t+1]
+      for (int t = 0; t < 4; ++t)  // + x[2t] + x[2t+1]
+        sm = ACT == QW_F16 ? dot2_f16(v[t], 0x3c003c00u, sm) : dot2_bf16(v[t], 0x3f803f80u, sm);
     }
     *xsum = sm;
   } else if constexpr (WF == QW_I8) {
@@ -121,6 +136,10 @@ __device__ __forceinline__ void prep_chunk(const uint4* raw, float scale, uint32
       const uint32_t v[4] = {raw[q].x, raw[q].y, raw[q].z, raw[q].w};
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
+        if constexpr (ACT == QW_F16) {
+          xq[4 * q + t] = v[t];
+          continue;
+        }
         const _Float16 a = static_cast<_Float16>(__uint_as_float(v[t] << 16) * scale);
         const _Float16 b = static_cast<_Float16>(__uint_as_float(v[t] & 0xffff0000u) * scale);
         xq[4 * q + t] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
@@ -299,14 +318,14 @@ __device__ __forceinline__ int nth_active_expert(const int32_t* __restrict__ off
 // the pass is done (a store between the ring loads would break the counts).
 // SAVE (training): gate/up also stores the gate and up projections (save_a,
 // save_b); down also stores the rows before their row weight (save_a).
-template <int WF, bool GATEUP, int UNITS, int CPL, int MAXM, bool SAVE>
+template <int ACT, int WF, bool GATEUP, int UNITS, int CPL, int MAXM, bool SAVE>
 __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
     int n_experts, int max_rows, WView wa, WView wb, int K, int n_out, int gpw,
     const float* __restrict__ row_weight, uint16_t* __restrict__ out, uint16_t* __restrict__ save_a,
     uint16_t* __restrict__ save_b) {
   constexpr int MW = math_fmt(WF);
-  constexpr bool TILED = WF == QW_BF16T;
+  constexpr bool TILED = WF == QW_BF16T || WF == QW_F16T;
   constexpr int CW = Fmt<WF>::CW;
   constexpr int DW = CW / 2;   // activation pairs per chunk
   constexpr int XP = CW / 8;   // 16-byte activation pieces per chunk
@@ -330,7 +349,7 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
   float* const staged = reinterpret_cast<float*>(ring + LD::STAGES * LD::STAGE);
   const int KC = K / CW;
   const int cpg = wa.group / CW;  // chunks per quantisation group
-  const int64_t esz = MW == QW_BF16 ? 2 : 1;
+  const int64_t esz = quantized(MW) ? 1 : 2;
   const uint8_t* wbase[ROWS];
   const float* sbase[ROWS];
 #pragma unroll
@@ -402,7 +421,7 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
     float scale[MAXM], inv[MAXM];
 #pragma unroll
     for (int m = 0; m < MAXM; ++m) scale[m] = inv[m] = 1.0f;
-    if constexpr (WF == QW_I8) {
+    if constexpr (WF == QW_I8 && ACT == QW_BF16) {
       // per-route power of two bringing max|x| into [2^14, 2^15): fp16 then holds the bf16 values exactly
 #pragma unroll
       for (int m = 0; m < MAXM; ++m) {
@@ -433,7 +452,7 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
       const bool valid = lane + 64 * j < KC;
 #pragma unroll
       for (int m = 0; m < MAXM; ++m) {
-        prep_chunk<MW>(raw[j][m], scale[m], xq[j][m], &xs[j][m]);
+        prep_chunk<ACT, MW>(raw[j][m], scale[m], xq[j][m], &xs[j][m]);
 #pragma unroll
         for (int p = 0; p < DW; ++p) xq[j][m][p] = valid ? xq[j][m][p] : 0u;
         xs[j][m] = valid ? xs[j][m] : 0.0f;
@@ -469,21 +488,21 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
             const uint4 wv = wq[q];
             const float sv = sq[q];
             uint32_t cw[DW];
-            chunk_pairs<MW>(wv, cw);
+            chunk_pairs<ACT, MW>(wv, cw);
 #pragma unroll
             for (int m = 0; m < MAXM; ++m) {
               if (m >= M) break;
               float d = 0.0f;
 #pragma unroll
               for (int p = 0; p < DW; ++p)
-                d = WF == QW_I8 ? dot2_f16(cw[p], xq[j][m][p], d) : dot2_bf16(cw[p], xq[j][m][p], d);
+                d = (WF == QW_I8 || ACT == QW_F16) ? dot2_f16(cw[p], xq[j][m][p], d) : dot2_bf16(cw[p], xq[j][m][p], d);
               float& acc = part[((u * MAXM + m) << (ROWS - 1)) | rr];
-              if constexpr (MW == QW_BF16) acc += d;
-              else acc = __builtin_fmaf(sv, d - Fmt<MW>::BIAS * xs[j][m], acc);
+              if constexpr (!quantized(MW)) acc += d;
+              else acc = __builtin_fmaf(sv, d - (ACT == QW_F16 ? Fmt<MW>::BIAS_F16 : Fmt<MW>::BIAS) * xs[j][m], acc);
             }
           }
       }
-      if constexpr (WF == QW_I8) {  // undo the power-of-two activation scaling (exact)
+      if constexpr (WF == QW_I8 && ACT == QW_BF16) {  // undo the power-of-two activation scaling (exact)
 #pragma unroll
         for (int u = 0; u < UNITS; ++u)
 #pragma unroll
@@ -498,7 +517,7 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
       if constexpr (GATEUP) {
         const float up = __shfl_xor(r, 1 << (6 - L), kWave);  // the up row of the same unit and route
         if ((lane & ((2 << (6 - L)) - 1)) == 0) {
-          *slot = swiglu_bf16(r, up);
+          *slot = swiglu_act<ACT>(r, up);
           if constexpr (SAVE) {
             slot[SLOTS] = r;
             slot[2 * SLOTS] = up;
@@ -520,15 +539,15 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
       const float val = staged[v];
       const int64_t o = static_cast<int64_t>(srow) * n_out + n;
       if constexpr (GATEUP) {
-        out[o] = f32_to_bf16(val);
+        out[o] = f32_to_half<ACT>(val);
         if constexpr (SAVE) {
-          save_a[o] = f32_to_bf16(staged[SLOTS + v]);
-          save_b[o] = f32_to_bf16(staged[2 * SLOTS + v]);
+          save_a[o] = f32_to_half<ACT>(staged[SLOTS + v]);
+          save_b[o] = f32_to_half<ACT>(staged[2 * SLOTS + v]);
         }
       } else {
         const float wgt = row_weight ? row_weight[srow] : 1.0f;
-        out[o] = f32_to_bf16(round_to_bf16(val) * wgt);
-        if constexpr (SAVE) save_a[o] = f32_to_bf16(val);
+        out[o] = f32_to_half<ACT>(round_act<ACT>(val) * wgt);
+        if constexpr (SAVE) save_a[o] = f32_to_half<ACT>(val);
       }
     }
   }
@@ -545,15 +564,16 @@ static int groups_per_wave(int64_t touched, int64_t n_groups) {
   return 1;
 }
 
-template <int WF, bool GATEUP, int UNITS, int CPL, bool SAVE>
+template <int ACT, int WF, bool GATEUP, int UNITS, int CPL, bool SAVE>
 int launch_save(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
                 int n_out, const float* row_weight, void* out, void* save_a, void* save_b, hipStream_t stream) {
   // routes per pass: int4 activation pieces are 4x larger per chunk than bf16 ones
   constexpr int MAXM = WF == QW_U4 ? 2 : 4;
   using LD = GvLds<WF, UNITS, GATEUP ? 2 : 1, CPL, MAXM, SAVE>;
   constexpr size_t lds = static_cast<size_t>(GV_WAVES) * LD::WAVE;
-  auto kernel = ffn_gemv_kernel<WF, GATEUP, UNITS, CPL, MAXM, SAVE>;
-  const hipError_t attr = reserve_lds<ffn_gemv_kernel<WF, GATEUP, UNITS, CPL, MAXM, SAVE>>(static_cast<int>(lds));
+  auto kernel = ffn_gemv_kernel<ACT, WF, GATEUP, UNITS, CPL, MAXM, SAVE>;
+  const hipError_t attr =
+      reserve_lds<ffn_gemv_kernel<ACT, WF, GATEUP, UNITS, CPL, MAXM, SAVE>>(static_cast<int>(lds));
   if (attr != hipSuccess)
     return set_error(QW_ERR_HIP, "cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(attr));
   const int64_t n_groups = ceil_div(n_out, UNITS);
@@ -569,44 +589,44 @@ int launch_save(const FfnArgs& a, const WView& wa, const WView& wb, const void* 
   return QW_OK;
 }
 
-// The saving variants exist for bf16 weights only (quantised experts do not train).
-template <int WF, bool GATEUP, int UNITS, int CPL>
+// The saving variants exist for 16-bit weights only (quantised experts do not train).
+template <int ACT, int WF, bool GATEUP, int UNITS, int CPL>
 int launch_one(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
                int n_out, const float* row_weight, void* out, void* save_a, void* save_b, hipStream_t stream) {
   if constexpr (!quantized(WF)) {
     if (save_a)
-      return launch_save<WF, GATEUP, UNITS, CPL, true>(a, wa, wb, x, row_index, K, n_out, row_weight, out, save_a,
+      return launch_save<ACT, WF, GATEUP, UNITS, CPL, true>(a, wa, wb, x, row_index, K, n_out, row_weight, out, save_a,
                                                        save_b, stream);
   }
-  return launch_save<WF, GATEUP, UNITS, CPL, false>(a, wa, wb, x, row_index, K, n_out, row_weight, out, nullptr,
+  return launch_save<ACT, WF, GATEUP, UNITS, CPL, false>(a, wa, wb, x, row_index, K, n_out, row_weight, out, nullptr,
                                                     nullptr, stream);
 }
 
 // Units per group for a row of CPL chunks per lane: 4 weight chunks (16-byte
 // loads) per lane and group (8 for gate/up rows of more than 128 chunks).
-template <int WF, bool GATEUP>
+template <int ACT, int WF, bool GATEUP>
 int launch_cpl(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
                int n_out, const float* row_weight, void* out, void* save_a, void* save_b, hipStream_t stream) {
   const int KC = K / Fmt<WF>::CW;
   const int cpl = static_cast<int>(ceil_div(KC, 64));
   constexpr int U1 = GATEUP ? 2 : 4;
   if (cpl <= 1)
-    return launch_one<WF, GATEUP, U1, 1>(a, wa, wb, x, row_index, K, n_out, row_weight, out, save_a, save_b, stream);
+    return launch_one<ACT, WF, GATEUP, U1, 1>(a, wa, wb, x, row_index, K, n_out, row_weight, out, save_a, save_b, stream);
   if (cpl <= 2)
-    return launch_one<WF, GATEUP, U1 / 2, 2>(a, wa, wb, x, row_index, K, n_out, row_weight, out, save_a, save_b,
+    return launch_one<ACT, WF, GATEUP, U1 / 2, 2>(a, wa, wb, x, row_index, K, n_out, row_weight, out, save_a, save_b,
                                              stream);
   if (cpl <= 4)
-    return launch_one<WF, GATEUP, 1, 4>(a, wa, wb, x, row_index, K, n_out, row_weight, out, save_a, save_b, stream);
+    return launch_one<ACT, WF, GATEUP, 1, 4>(a, wa, wb, x, row_index, K, n_out, row_weight, out, save_a, save_b, stream);
   return set_error(QW_ERR_UNSUPPORTED, "row of %d chunks is too long for the decode kernel", KC);
 }
 
-template <int WF>
+template <int ACT, int WF>
 int launch_fmt(const FfnArgs& a, hipStream_t stream) {
   const int D = static_cast<int>(a.d_model), F = static_cast<int>(a.d_ff);
-  int st = launch_cpl<WF, true>(a, a.gate, a.up, a.x, a.row_index, D, F, nullptr, a.hidden, a.save_gate, a.save_up,
+  int st = launch_cpl<ACT, WF, true>(a, a.gate, a.up, a.x, a.row_index, D, F, nullptr, a.hidden, a.save_gate, a.save_up,
                                 stream);
   if (st) return st;
-  return launch_cpl<WF, false>(a, a.down, a.down, a.hidden, nullptr, F, D, a.row_weight, a.y, a.save_y, nullptr,
+  return launch_cpl<ACT, WF, false>(a, a.down, a.down, a.hidden, nullptr, F, D, a.row_weight, a.y, a.save_y, nullptr,
                                stream);
 }
 
@@ -614,7 +634,8 @@ int launch_fmt(const FfnArgs& a, hipStream_t stream) {
 
 int launch_ffn_gemv(const FfnArgs& a, hipStream_t stream, bool* handled) {
   *handled = false;
-  if (a.act != QW_BF16 || a.avg_rows >= 16) return QW_OK;
+  if (!is_half(a.act) || a.avg_rows >= 16) return QW_OK;
+  const bool f16 = a.act == QW_F16;
   if ((a.save_gate || a.save_y) && quantized(a.wfmt)) return QW_OK;  // quantised experts do not train
   int cw = 0;
   if (a.wfmt == QW_U4) {
@@ -623,7 +644,7 @@ int launch_ffn_gemv(const FfnArgs& a, hipStream_t stream, bool* handled) {
   } else if (a.wfmt == QW_I8) {
     if (a.gate.group % 16 || a.down.group % 16) return QW_OK;
     cw = 16;
-  } else if (a.wfmt == QW_BF16 || a.wfmt == QW_BF16T) {
+  } else if ((!f16 && (a.wfmt == QW_BF16 || a.wfmt == QW_BF16T)) || (f16 && (a.wfmt == QW_F16 || a.wfmt == QW_F16T))) {
     cw = 8;
   } else {
     return QW_OK;
@@ -635,10 +656,17 @@ int launch_ffn_gemv(const FfnArgs& a, hipStream_t stream, bool* handled) {
                             a.down.row_stride * (a.wfmt == QW_U4 ? 2 : 1) != a.d_ff))
     return QW_OK;
   int st;
-  if (a.wfmt == QW_U4) st = launch_fmt<QW_U4>(a, stream);
-  else if (a.wfmt == QW_I8) st = launch_fmt<QW_I8>(a, stream);
-  else if (a.wfmt == QW_BF16T) st = launch_fmt<QW_BF16T>(a, stream);
-  else st = launch_fmt<QW_BF16>(a, stream);
+  if (f16) {
+    if (a.wfmt == QW_U4) st = launch_fmt<QW_F16, QW_U4>(a, stream);
+    else if (a.wfmt == QW_I8) st = launch_fmt<QW_F16, QW_I8>(a, stream);
+    else if (a.wfmt == QW_F16T) st = launch_fmt<QW_F16, QW_F16T>(a, stream);
+    else st = launch_fmt<QW_F16, QW_F16>(a, stream);
+  } else {
+    if (a.wfmt == QW_U4) st = launch_fmt<QW_BF16, QW_U4>(a, stream);
+    else if (a.wfmt == QW_I8) st = launch_fmt<QW_BF16, QW_I8>(a, stream);
+    else if (a.wfmt == QW_BF16T) st = launch_fmt<QW_BF16, QW_BF16T>(a, stream);
+    else st = launch_fmt<QW_BF16, QW_BF16>(a, stream);
+  }
   if (st) return st;
   *handled = true;
   return QW_OK;

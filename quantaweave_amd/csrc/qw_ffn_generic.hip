@@ -159,6 +159,15 @@ int launch_ffn_generic(const FfnArgs& a, hipStream_t stream) {
   QW_GEN(QW_BF16, QW_U4)
   QW_GEN(QW_F32, QW_BF16T)
   QW_GEN(QW_BF16, QW_BF16T)
+  QW_GEN(QW_F16, QW_F16)
+  QW_GEN(QW_F16, QW_F16T)
+  QW_GEN(QW_F16, QW_F32)
+  QW_GEN(QW_F16, QW_BF16)
+  QW_GEN(QW_F16, QW_I8)
+  QW_GEN(QW_F16, QW_U4)
+  QW_GEN(QW_F32, QW_F16)
+  QW_GEN(QW_F32, QW_F16T)
+  QW_GEN(QW_BF16, QW_F16)
 #undef QW_GEN
   return set_error(QW_ERR_INVALID, "unsupported activation/weight format pair (%d, %d)", a.act, a.wfmt);
 }
@@ -184,6 +193,15 @@ int grouped_matmul_generic(const void* x, int act, const WView& w, int wfmt, int
   QW_GM(QW_BF16, QW_U4)
   QW_GM(QW_F32, QW_BF16T)
   QW_GM(QW_BF16, QW_BF16T)
+  QW_GM(QW_F16, QW_F16)
+  QW_GM(QW_F16, QW_F16T)
+  QW_GM(QW_F16, QW_F32)
+  QW_GM(QW_F16, QW_BF16)
+  QW_GM(QW_F16, QW_I8)
+  QW_GM(QW_F16, QW_U4)
+  QW_GM(QW_F32, QW_F16)
+  QW_GM(QW_F32, QW_F16T)
+  QW_GM(QW_BF16, QW_F16)
 #undef QW_GM
   return set_error(QW_ERR_INVALID, "unsupported activation/weight format pair (%d, %d)", act, wfmt);
 }

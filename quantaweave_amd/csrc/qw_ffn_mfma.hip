@@ -1,5 +1,6 @@
-// Grouped SwiGLU expert FFN on bf16 MFMA (v_mfma_f32_16x16x32_bf16, gfx950)
-// for prefill-sized rows per expert.
+// Grouped SwiGLU expert FFN on 16-bit MFMA (v_mfma_f32_16x16x32_bf16, or
+// v_mfma_f32_16x16x32_f16 for fp16 activations; gfx950) for prefill-sized rows
+// per expert.
 //
 // Reference: src/moe_kernels.py:41-64, :186-195 (grouped GEMM over
 // expert-sorted rows, fp32 accumulation) and src/quantweave_moe_model.py:59-60.
@@ -61,7 +62,8 @@ namespace qw {
 
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));  // 16-bit operands (bf16 or fp16 bits)
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -137,42 +139,71 @@ struct MfW {
   int groups, group;
 };
 
-// Eight int8 weights (bytes 0..7 = columns c..c+7) -> bf16(q * s).  The sign
+// One 16x16x32 MFMA step in the activation type: bf16, or fp16 bits carried
+// in the same 16-byte operand registers.
+template <int ACT>
+__device__ __forceinline__ f32x4 mfma_step(bf16x8 a, bf16x8 b, f32x4 c) {
+  if constexpr (ACT == QW_F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                   0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Eight fp32 values rounded to the activation type, as 16-bit operand bits.
+template <int ACT>
+__device__ __forceinline__ bf16x8 pack_act8(const float (&f)[8]) {
+  if constexpr (ACT == QW_F16) {
+    f16x8 r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = static_cast<_Float16>(pin_f32(f[i]));  // fp32 first, then RNE to fp16
+    return __builtin_bit_cast(bf16x8, r);
+  } else {
+    bf16x8 r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = static_cast<__bf16>(f[i]);
+    return r;
+  }
+}
+
+// Eight int8 weights (bytes 0..7 = columns c..c+7) -> act(q * s).  The sign
 // bit flip stores u = q + 128; fma(u, s, -128 s) = q s rounded once.
+template <int ACT>
 __device__ __forceinline__ bf16x8 dequant_i8(uint2 raw, float s) {
   const uint32_t u0 = raw.x ^ 0x80808080u, u1 = raw.y ^ 0x80808080u;
   const float c = -128.0f * s;
-  bf16x8 r;
+  float f[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    r[i] = static_cast<__bf16>(__builtin_fmaf(static_cast<float>((u0 >> (8 * i)) & 0xffu), s, c));
-    r[4 + i] = static_cast<__bf16>(__builtin_fmaf(static_cast<float>((u1 >> (8 * i)) & 0xffu), s, c));
+    f[i] = __builtin_fmaf(static_cast<float>((u0 >> (8 * i)) & 0xffu), s, c);
+    f[4 + i] = __builtin_fmaf(static_cast<float>((u1 >> (8 * i)) & 0xffu), s, c);
   }
-  return r;
+  return pack_act8<ACT>(f);
 }
 
 // Eight int4 weights (byte b: column c+2b in the low nibble, c+2b+1 in the
-// high one, each stored as q + 8) -> bf16(q * s).
+// high one, each stored as q + 8) -> act(q * s).
+template <int ACT>
 __device__ __forceinline__ bf16x8 dequant_u4(uint32_t raw, float s) {
   const uint32_t lo = raw & 0x0f0f0f0fu, hi = (raw >> 4) & 0x0f0f0f0fu;
   const float c = -8.0f * s;
-  bf16x8 r;
+  float f[8];
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
-    r[2 * b] = static_cast<__bf16>(__builtin_fmaf(static_cast<float>((lo >> (8 * b)) & 0xffu), s, c));
-    r[2 * b + 1] = static_cast<__bf16>(__builtin_fmaf(static_cast<float>((hi >> (8 * b)) & 0xffu), s, c));
+    f[2 * b] = __builtin_fmaf(static_cast<float>((lo >> (8 * b)) & 0xffu), s, c);
+    f[2 * b + 1] = __builtin_fmaf(static_cast<float>((hi >> (8 * b)) & 0xffu), s, c);
   }
-  return r;
+  return pack_act8<ACT>(f);
 }
 
-template <bool GATEUP, int SUBT, int WF>
+template <int ACT, bool GATEUP, int SUBT, int WF>
 __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
     int max_rows, const MfW wa, const MfW wb, int n_w, int K, const float* __restrict__ row_weight,
     uint16_t* __restrict__ out, int n_out, int n_tiles, int m_chunks, int experts, uint16_t* __restrict__ save_a,
     uint16_t* __restrict__ save_b) {
   using B = MfB<WF>;
-  constexpr bool TILED = WF == QW_BF16T;
+  constexpr bool TILED = WF == QW_BF16T || WF == QW_F16T;
   constexpr int MCH = 32 * SUBT;                 // rows per chunk
   constexpr int AG = MCH / MF_GROWS;             // 8-row load groups of the A slice
   constexpr int A_STAGE = MCH * MF_ROWB, B_STAGE = B::STAGE;
@@ -341,10 +372,10 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
         if constexpr (WF == QW_I8) {  // 8 bytes: columns 32ks + 8lq ..
           const uint2 raw = *reinterpret_cast<const uint2*>(st_b + row * B::ROWB +
                                                             B::swz(row, 2 * ks + lq / 2) * 16 + (lq % 2) * 8);
-          return dequant_i8(raw, *reinterpret_cast<const float*>(st_b + B::W_STAGE + (row * 2 + ks) * 4));
+          return dequant_i8<ACT>(raw, *reinterpret_cast<const float*>(st_b + B::W_STAGE + (row * 2 + ks) * 4));
         } else if constexpr (WF == QW_U4) {  // 4 bytes: columns 32ks + 8lq ..
           const uint32_t raw = *reinterpret_cast<const uint32_t*>(st_b + row * B::ROWB + B::swz(row, ks) * 16 + lq * 4);
-          return dequant_u4(raw, *reinterpret_cast<const float*>(st_b + B::W_STAGE + (row * 2 + ks) * 4));
+          return dequant_u4<ACT>(raw, *reinterpret_cast<const float*>(st_b + B::W_STAGE + (row * 2 + ks) * 4));
         } else {
           return *reinterpret_cast<const bf16x8*>(st_b + row * MF_ROWB + swz(row, lq + 4 * ks) * 16);
         }
@@ -369,7 +400,7 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
       for (int u = 0; u < 2 * NPA; ++u) {
         const int ks = u / NPA, p = u % NPA;
         const bf16x8 x0 = xb[u & 1][0], x1 = xb[u & 1][1];
-        acc[2 * p][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[ks][0], x0, acc[2 * p][0], 0, 0, 0);
+        acc[2 * p][0] = mfma_step<ACT>(wfr[ks][0], x0, acc[2 * p][0]);
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         if (u + 1 < 2 * NPA) {
           const int ks1 = (u + 1) / NPA, p1 = (u + 1) % NPA;
@@ -387,10 +418,10 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
         }
   #pragma unroll
         for (int t = 1; t < MF_NT; ++t)
-          acc[2 * p][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[ks][t], x0, acc[2 * p][t], 0, 0, 0);
+          acc[2 * p][t] = mfma_step<ACT>(wfr[ks][t], x0, acc[2 * p][t]);
   #pragma unroll
         for (int t = 0; t < MF_NT; ++t)
-          acc[2 * p + 1][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wfr[ks][t], x1, acc[2 * p + 1][t], 0, 0, 0);
+          acc[2 * p + 1][t] = mfma_step<ACT>(wfr[ks][t], x1, acc[2 * p + 1][t]);
         __builtin_amdgcn_sched_group_barrier(0x008, 2 * MF_NT - 1, 0);
       }
     }
@@ -434,20 +465,21 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
         uint32_t pk[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          // the reference's bf16 tensors: gate, up and silu(gate) are each
-          // rounded to bf16 before the product (src/moe_kernels.py:194)
-          const float a = swiglu_bf16(acc[i][t][2 * h], acc[i][t + MF_NT / 2][2 * h]);
-          const float c = swiglu_bf16(acc[i][t][2 * h + 1], acc[i][t + MF_NT / 2][2 * h + 1]);
-          pk[h] = f32_to_bf16(a) | (static_cast<uint32_t>(f32_to_bf16(c)) << 16);
+          // the reference's 16-bit tensors: gate, up and silu(gate) are each
+          // rounded to the activation type before the product (src/moe_kernels.py:194)
+          const float a = swiglu_act<ACT>(acc[i][t][2 * h], acc[i][t + MF_NT / 2][2 * h]);
+          const float c = swiglu_act<ACT>(acc[i][t][2 * h + 1], acc[i][t + MF_NT / 2][2 * h + 1]);
+          pk[h] = f32_to_half<ACT>(a) | (static_cast<uint32_t>(f32_to_half<ACT>(c)) << 16);
         }
         *reinterpret_cast<uint2*>(out + orow + col) = make_uint2(pk[0], pk[1]);
         if (save_a) {  // gate and up projections, for the backward pass
           uint32_t g2[2], u2[2];
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            g2[h] = f32_to_bf16(acc[i][t][2 * h]) | (static_cast<uint32_t>(f32_to_bf16(acc[i][t][2 * h + 1])) << 16);
-            u2[h] = f32_to_bf16(acc[i][t + MF_NT / 2][2 * h]) |
-                    (static_cast<uint32_t>(f32_to_bf16(acc[i][t + MF_NT / 2][2 * h + 1])) << 16);
+            g2[h] = f32_to_half<ACT>(acc[i][t][2 * h]) |
+                    (static_cast<uint32_t>(f32_to_half<ACT>(acc[i][t][2 * h + 1])) << 16);
+            u2[h] = f32_to_half<ACT>(acc[i][t + MF_NT / 2][2 * h]) |
+                    (static_cast<uint32_t>(f32_to_half<ACT>(acc[i][t + MF_NT / 2][2 * h + 1])) << 16);
           }
           *reinterpret_cast<uint2*>(save_a + orow + col) = make_uint2(g2[0], g2[1]);
           *reinterpret_cast<uint2*>(save_b + orow + col) = make_uint2(u2[0], u2[1]);
@@ -462,17 +494,18 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
         uint32_t pk[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          // without weights bf16(bf16(v) * 1) is bf16(v): one rounding
-          const float a = row_weight ? round_to_bf16(acc[i][t][2 * h]) * wgt : acc[i][t][2 * h];
-          const float c = row_weight ? round_to_bf16(acc[i][t][2 * h + 1]) * wgt : acc[i][t][2 * h + 1];
-          pk[h] = f32_to_bf16(a) | (static_cast<uint32_t>(f32_to_bf16(c)) << 16);
+          // without weights act(act(v) * 1) is act(v): one rounding
+          const float a = row_weight ? round_act<ACT>(acc[i][t][2 * h]) * wgt : acc[i][t][2 * h];
+          const float c = row_weight ? round_act<ACT>(acc[i][t][2 * h + 1]) * wgt : acc[i][t][2 * h + 1];
+          pk[h] = f32_to_half<ACT>(a) | (static_cast<uint32_t>(f32_to_half<ACT>(c)) << 16);
         }
         *reinterpret_cast<uint2*>(out + orow + col) = make_uint2(pk[0], pk[1]);
         if (save_a) {  // the rows before their weight, for the backward pass
           uint32_t un[2];
 #pragma unroll
           for (int h = 0; h < 2; ++h)
-            un[h] = f32_to_bf16(acc[i][t][2 * h]) | (static_cast<uint32_t>(f32_to_bf16(acc[i][t][2 * h + 1])) << 16);
+            un[h] = f32_to_half<ACT>(acc[i][t][2 * h]) |
+                    (static_cast<uint32_t>(f32_to_half<ACT>(acc[i][t][2 * h + 1])) << 16);
           *reinterpret_cast<uint2*>(save_a + orow + col) = make_uint2(un[0], un[1]);
         }
       }
@@ -482,7 +515,7 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
 
 // Kernel view of one stacked projection.
 MfW mf_view(int wf, const WView& v) {
-  const int64_t esize = wf == QW_BF16 || wf == QW_BF16T ? 2 : 1;  // QW_U4 strides are in bytes already
+  const int64_t esize = wf == QW_I8 || wf == QW_U4 ? 1 : 2;  // QW_U4 strides are in bytes already
   MfW m;
   m.w = static_cast<const char*>(v.w);
   m.scales = v.scales;
@@ -494,7 +527,7 @@ MfW mf_view(int wf, const WView& v) {
   return m;
 }
 
-template <bool GATEUP, int SUBT, int WF>
+template <int ACT, bool GATEUP, int SUBT, int WF>
 int launch_t(const void* x, const int32_t* row_index, const int32_t* offsets, int max_rows, const MfW& wa,
              const MfW& wb, int n_w, int K, const float* row_weight, void* out, int n_out, int experts,
              int64_t rows_cap, void* save_a, void* save_b, hipStream_t stream) {
@@ -509,10 +542,10 @@ int launch_t(const void* x, const int32_t* row_index, const int32_t* offsets, in
   const int64_t grid = static_cast<int64_t>(kXcds) * chunks * n_tiles;
   if (grid > INT32_MAX) return set_error(QW_ERR_UNSUPPORTED, "MFMA grid too large");
   const size_t lds = static_cast<size_t>(mf_stages<WF>(SUBT)) * (32 * SUBT * MF_ROWB + MfB<WF>::STAGE);
-  const hipError_t attr = reserve_lds<ffn_mfma_kernel<GATEUP, SUBT, WF>>(static_cast<int>(lds));
+  const hipError_t attr = reserve_lds<ffn_mfma_kernel<ACT, GATEUP, SUBT, WF>>(static_cast<int>(lds));
   if (attr != hipSuccess)
     return set_error(QW_ERR_HIP, "cannot reserve %zu bytes of LDS: %s", lds, hipGetErrorString(attr));
-  ffn_mfma_kernel<GATEUP, SUBT, WF><<<static_cast<unsigned>(grid), MF_THREADS, lds, stream>>>(
+  ffn_mfma_kernel<ACT, GATEUP, SUBT, WF><<<static_cast<unsigned>(grid), MF_THREADS, lds, stream>>>(
       static_cast<const uint16_t*>(x), row_index, offsets, max_rows, wa, wb, n_w, K, row_weight,
       static_cast<uint16_t*>(out), n_out, n_tiles, m_chunks, experts, static_cast<uint16_t*>(save_a),
       static_cast<uint16_t*>(save_b));
@@ -521,13 +554,13 @@ int launch_t(const void* x, const int32_t* row_index, const int32_t* offsets, in
 }
 
 // rows_cap: most rows any expert can hold (the capacity bound).
-template <bool GATEUP, int WF>
+template <int ACT, bool GATEUP, int WF>
 int launch_sel(int subt, const void* x, const int32_t* row_index, const int32_t* offsets, int max_rows,
                const MfW& wa, const MfW& wb, int n_w, int K, const float* row_weight, void* out, int n_out,
                int experts, int64_t rows_cap, void* save_a, void* save_b, hipStream_t stream) {
 #define QW_MF(S)                                                                                                \
   if (subt == S)                                                                                               \
-    return launch_t<GATEUP, S, WF>(x, row_index, offsets, max_rows, wa, wb, n_w, K, row_weight, out, n_out,     \
+    return launch_t<ACT, GATEUP, S, WF>(x, row_index, offsets, max_rows, wa, wb, n_w, K, row_weight, out, n_out,     \
                                    experts, rows_cap, save_a, save_b, stream);
   QW_MF(2)
   QW_MF(4)
@@ -559,7 +592,10 @@ bool quant_fits(const WView& v, int wf) {
 int launch_ffn_mfma(const FfnArgs& a, hipStream_t stream, bool* handled) {
   *handled = false;
   const bool quant = a.wfmt == QW_I8 || a.wfmt == QW_U4;
-  if (a.act != QW_BF16 || (a.wfmt != QW_BF16 && a.wfmt != QW_BF16T && !quant)) return QW_OK;
+  const bool f16 = a.act == QW_F16;
+  if (!is_half(a.act)) return QW_OK;
+  if (!quant && (f16 ? (a.wfmt != QW_F16 && a.wfmt != QW_F16T) : (a.wfmt != QW_BF16 && a.wfmt != QW_BF16T)))
+    return QW_OK;
   if (a.d_model % 64 || a.d_ff % 64) return QW_OK;
   if (quant && !(quant_fits(a.gate, a.wfmt) && quant_fits(a.up, a.wfmt) && quant_fits(a.down, a.wfmt))) return QW_OK;
   if (a.avg_rows < 16) return QW_OK;  // decode-sized: weight streaming kernels
@@ -568,20 +604,28 @@ int launch_ffn_mfma(const FfnArgs& a, hipStream_t stream, bool* handled) {
   const int D = static_cast<int>(a.d_model), F = static_cast<int>(a.d_ff), E = static_cast<int>(a.experts);
   const int mr = static_cast<int>(a.max_rows);
   const MfW g = mf_view(a.wfmt, a.gate), u = mf_view(a.wfmt, a.up), dn = mf_view(a.wfmt, a.down);
-  auto both = [&](auto wf) -> int {
-    constexpr int WF = decltype(wf)::value;
-    int st = launch_sel<true, WF>(subt, a.x, a.row_index, a.offsets, mr, g, u, F, D, nullptr, a.hidden, F, E,
+  auto both = [&](auto act, auto wf) -> int {
+    constexpr int ACT = decltype(act)::value, WF = decltype(wf)::value;
+    int st = launch_sel<ACT, true, WF>(subt, a.x, a.row_index, a.offsets, mr, g, u, F, D, nullptr, a.hidden, F, E,
                                   rows_cap, a.save_gate, a.save_up, stream);
     if (st) return st;
-    return launch_sel<false, WF>(subt, a.hidden, nullptr, a.offsets, mr, dn, dn, D, F, a.row_weight, a.y, D, E,
+    return launch_sel<ACT, false, WF>(subt, a.hidden, nullptr, a.offsets, mr, dn, dn, D, F, a.row_weight, a.y, D, E,
                                  rows_cap, a.save_y, nullptr, stream);
   };
+  using BF = std::integral_constant<int, QW_BF16>;
+  using HF = std::integral_constant<int, QW_F16>;
   int st;
   switch (a.wfmt) {
-    case QW_BF16T: st = both(std::integral_constant<int, QW_BF16T>{}); break;
-    case QW_I8: st = both(std::integral_constant<int, QW_I8>{}); break;
-    case QW_U4: st = both(std::integral_constant<int, QW_U4>{}); break;
-    default: st = both(std::integral_constant<int, QW_BF16>{}); break;
+    case QW_BF16T: st = both(BF{}, std::integral_constant<int, QW_BF16T>{}); break;
+    case QW_F16T: st = both(HF{}, std::integral_constant<int, QW_F16T>{}); break;
+    case QW_F16: st = both(HF{}, HF{}); break;
+    case QW_I8:
+      st = f16 ? both(HF{}, std::integral_constant<int, QW_I8>{}) : both(BF{}, std::integral_constant<int, QW_I8>{});
+      break;
+    case QW_U4:
+      st = f16 ? both(HF{}, std::integral_constant<int, QW_U4>{}) : both(BF{}, std::integral_constant<int, QW_U4>{});
+      break;
+    default: st = both(BF{}, BF{}); break;
   }
   if (st) return st;
   *handled = true;

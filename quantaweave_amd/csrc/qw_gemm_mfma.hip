@@ -26,7 +26,8 @@ namespace qw {
 
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));  // 16-bit operands (bf16 or fp16 bits)
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int MODE_ROWS = 0, MODE_RED = 1;
@@ -42,7 +43,7 @@ constexpr int G_XCDS = 8;                    // XCDs of the MI355X, workgroups d
 // quarter-wave reads at one logical piece land on 16 different bank groups.
 __device__ __forceinline__ int gswz(int row, int piece) { return piece ^ ((row >> 1) & 7); }
 
-template <int MODE, bool ACCUM, bool BRED, bool C32>
+template <int DT, int MODE, bool ACCUM, bool BRED, bool C32>
 __global__ __launch_bounds__(256) void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda,
                                                       const uint16_t* __restrict__ B, int64_t ldb,
                                                       int64_t b_expert_stride, void* __restrict__ C, int64_t ldc,
@@ -205,7 +206,13 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(const uint16_t* __restrict
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[j], af[i], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 4; ++j) {
+          if constexpr (DT == QW_F16)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, bf[j]),
+                                                               __builtin_bit_cast(f16x8, af[i]), acc[i][j], 0, 0, 0);
+          else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[j], af[i], acc[i][j], 0, 0, 0);
+        }
     }
     if (more) QW_G_STORE((kt + 1) & 1);
     __syncthreads();
@@ -216,7 +223,7 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(const uint16_t* __restrict
 #undef QW_HI2
 
   // lane holds C[m = 16 i + l16][n = 16 j + 4 lq + v] of its wave's quarter;
-  // C32: fp32 output, else bf16
+  // C32: fp32 output, else the operands' 16-bit type
   const bool vec = (ldc & 3) == 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -249,19 +256,18 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(const uint16_t* __restrict
       if (vec && n + 3 < ncount) {
         if (ACCUM) {
           const uint2 old = *reinterpret_cast<const uint2*>(crow + n);
-          v[0] += __uint_as_float(old.x << 16);
-          v[1] += __uint_as_float(old.x & 0xffff0000u);
-          v[2] += __uint_as_float(old.y << 16);
-          v[3] += __uint_as_float(old.y & 0xffff0000u);
+          v[0] += half_to_f32<DT>(old.x & 0xffffu);
+          v[1] += half_to_f32<DT>(old.x >> 16);
+          v[2] += half_to_f32<DT>(old.y & 0xffffu);
+          v[3] += half_to_f32<DT>(old.y >> 16);
         }
-        const uint32_t lo = f32_to_bf16(v[0]) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
-        const uint32_t hi = f32_to_bf16(v[2]) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+        const uint32_t lo = f32_to_half<DT>(v[0]) | (static_cast<uint32_t>(f32_to_half<DT>(v[1])) << 16);
+        const uint32_t hi = f32_to_half<DT>(v[2]) | (static_cast<uint32_t>(f32_to_half<DT>(v[3])) << 16);
         *reinterpret_cast<uint2*>(crow + n) = make_uint2(lo, hi);
       } else {
-        if (n < ncount) crow[n] = f32_to_bf16(v[0] + (ACCUM ? bf16_to_f32(crow[n]) : 0.0f));
-        if (n + 1 < ncount) crow[n + 1] = f32_to_bf16(v[1] + (ACCUM ? bf16_to_f32(crow[n + 1]) : 0.0f));
-        if (n + 2 < ncount) crow[n + 2] = f32_to_bf16(v[2] + (ACCUM ? bf16_to_f32(crow[n + 2]) : 0.0f));
-        if (n + 3 < ncount) crow[n + 3] = f32_to_bf16(v[3] + (ACCUM ? bf16_to_f32(crow[n + 3]) : 0.0f));
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (n + u < ncount) crow[n + u] = f32_to_half<DT>(v[u] + (ACCUM ? half_to_f32<DT>(crow[n + u]) : 0.0f));
       }
     }
   }
@@ -320,11 +326,11 @@ __global__ __launch_bounds__(256) void transpose_pad_kernel(const uint16_t* __re
   }
 }
 
-template <int MODE, bool ACCUM, bool BRED = false, bool C32 = false>
+template <int DT, int MODE, bool ACCUM, bool BRED = false, bool C32 = false>
 int launch_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t b_stride, void* C, int64_t ldc,
                 int64_t c_stride, const int32_t* offsets, int rows, int M, int N, int K, int E, int64_t m_extent,
                 hipStream_t stream) {
-  const hipError_t attr = reserve_lds<gemm_nt_kernel<MODE, ACCUM, BRED, C32>>(G_LDS);
+  const hipError_t attr = reserve_lds<gemm_nt_kernel<DT, MODE, ACCUM, BRED, C32>>(G_LDS);
   if (attr != hipSuccess) return set_error(QW_ERR_HIP, "cannot reserve LDS: %s", hipGetErrorString(attr));
   // one grid dimension: MODE_ROWS, the row tiles of all experts (at most
   // rows/128 + E) times the column tiles; MODE_RED, experts times output tiles;
@@ -333,7 +339,7 @@ int launch_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t 
   const int64_t blocks = MODE == MODE_ROWS ? G_XCDS * n_nt * ceil_div(ceil_div(m_extent, GT) + E, G_XCDS)
                                            : G_XCDS * n_nt * ceil_div(m_extent, GT) * ceil_div(E, G_XCDS);
   if (blocks > INT32_MAX) return set_error(QW_ERR_UNSUPPORTED, "grouped GEMM grid too large");
-  gemm_nt_kernel<MODE, ACCUM, BRED, C32><<<static_cast<unsigned>(blocks), 256, G_LDS, stream>>>(
+  gemm_nt_kernel<DT, MODE, ACCUM, BRED, C32><<<static_cast<unsigned>(blocks), 256, G_LDS, stream>>>(
       static_cast<const uint16_t*>(A), lda, static_cast<const uint16_t*>(B), ldb, b_stride, C, ldc, c_stride, offsets,
       rows, M, N, K, E);
   QW_LAUNCH_CHECK("gemm_nt_kernel");
@@ -361,19 +367,25 @@ bool gemm_rows_fits(int64_t K, int64_t rows, int64_t E) {
 
 bool gemm_backward_fits(int64_t rows, int64_t E) { return ceil_div(rows, 64) + E <= 65535; }
 
-// out[r] = x[r] . w[e]^T over the rows of each expert (bf16, w [E, N, K]).
-int gemm_grouped_forward(const void* x, const void* w, int64_t E, int64_t N, int64_t K, const int32_t* offsets,
-                         int64_t rows, int64_t rows_per_expert, void* out, hipStream_t stream) {
+// out[r] = x[r] . w[e]^T over the rows of each expert (bf16 or fp16, w [E, N, K]).
+int gemm_grouped_forward(const void* x, const void* w, int dtype, int64_t E, int64_t N, int64_t K,
+                         const int32_t* offsets, int64_t rows, int64_t rows_per_expert, void* out, hipStream_t stream) {
   (void)rows_per_expert;
-  return launch_gemm<MODE_ROWS, false>(x, K, w, K, N * K, out, N, 0, offsets, static_cast<int>(rows), 0,
-                                       static_cast<int>(N), static_cast<int>(K), static_cast<int>(E), rows, stream);
+  if (dtype == QW_F16)
+    return launch_gemm<QW_F16, MODE_ROWS, false>(x, K, w, K, N * K, out, N, 0, offsets, static_cast<int>(rows), 0,
+                                                 static_cast<int>(N), static_cast<int>(K), static_cast<int>(E), rows,
+                                                 stream);
+  return launch_gemm<QW_BF16, MODE_ROWS, false>(x, K, w, K, N * K, out, N, 0, offsets, static_cast<int>(rows), 0,
+                                                static_cast<int>(N), static_cast<int>(K), static_cast<int>(E), rows,
+                                                stream);
 }
 
-// Backward of gemm_grouped_forward on the matrix cores (bf16):
+// Backward of gemm_grouped_forward on the matrix cores (bf16 or fp16, DT):
 //   gx = gy . w[e] (+ gx when accumulate), gw[e] = gy_e^T . x_e (fp32 when gw_f32).
-int gemm_grouped_backward(const void* gy, const void* x, const void* w, int64_t E, int64_t N, int64_t K,
-                          const int32_t* offsets, int64_t rows, int64_t rows_per_expert, void* gx, int accumulate,
-                          void* gw, int gw_f32, void* ws, size_t ws_bytes, hipStream_t stream) {
+template <int DT>
+int gemm_backward_t(const void* gy, const void* x, const void* w, int64_t E, int64_t N, int64_t K,
+                    const int32_t* offsets, int64_t rows, void* gx, int accumulate, void* gw, int gw_f32, void* ws,
+                    size_t ws_bytes, hipStream_t stream) {
   const size_t need = gemm_backward_workspace_bytes(E, N, K, rows);
   if (!ws || ws_bytes < need)
     return set_error(QW_ERR_WORKSPACE, "grouped backward workspace needs %zu bytes, got %zu", need, ws_bytes);
@@ -385,10 +397,10 @@ int gemm_grouped_backward(const void* gy, const void* x, const void* w, int64_t 
   const int e = static_cast<int>(E), n = static_cast<int>(N), k = static_cast<int>(K), r = static_cast<int>(rows);
   if (gx != nullptr && rows > 0) {  // B = w read reduction-major: no transposed copy
     const int st = accumulate
-                       ? launch_gemm<MODE_ROWS, true, true>(gy, N, w, K, N * K, gx, K, 0, offsets, r, 0, k, n, e, rows,
-                                                            stream)
-                       : launch_gemm<MODE_ROWS, false, true>(gy, N, w, K, N * K, gx, K, 0, offsets, r, 0, k, n, e,
-                                                             rows, stream);
+                       ? launch_gemm<DT, MODE_ROWS, true, true>(gy, N, w, K, N * K, gx, K, 0, offsets, r, 0, k, n, e,
+                                                                rows, stream)
+                       : launch_gemm<DT, MODE_ROWS, false, true>(gy, N, w, K, N * K, gx, K, 0, offsets, r, 0, k, n, e,
+                                                                 rows, stream);
     if (st) return st;
   }
   if (gw != nullptr) {
@@ -403,11 +415,21 @@ int gemm_grouped_backward(const void* gy, const void* x, const void* w, int64_t 
       transpose_pad_kernel<<<g2, 256, 0, stream>>>(static_cast<const uint16_t*>(x), k, offsets, poff, e, r, rp, xt);
       QW_LAUNCH_CHECK("transpose_pad_kernel");
     }
-    return gw_f32 ? launch_gemm<MODE_RED, false, false, true>(gyt, rp, xt, rp, 0, gw, K, N * K, poff, r, n, k, 0, e,
-                                                              N, stream)
-                  : launch_gemm<MODE_RED, false>(gyt, rp, xt, rp, 0, gw, K, N * K, poff, r, n, k, 0, e, N, stream);
+    return gw_f32 ? launch_gemm<DT, MODE_RED, false, false, true>(gyt, rp, xt, rp, 0, gw, K, N * K, poff, r, n, k,
+                                                                  0, e, N, stream)
+                  : launch_gemm<DT, MODE_RED, false>(gyt, rp, xt, rp, 0, gw, K, N * K, poff, r, n, k, 0, e, N, stream);
   }
   return QW_OK;
+}
+
+int gemm_grouped_backward(const void* gy, const void* x, const void* w, int dtype, int64_t E, int64_t N, int64_t K,
+                          const int32_t* offsets, int64_t rows, int64_t rows_per_expert, void* gx, int accumulate,
+                          void* gw, int gw_f32, void* ws, size_t ws_bytes, hipStream_t stream) {
+  (void)rows_per_expert;
+  if (dtype == QW_F16)
+    return gemm_backward_t<QW_F16>(gy, x, w, E, N, K, offsets, rows, gx, accumulate, gw, gw_f32, ws, ws_bytes,
+                                   stream);
+  return gemm_backward_t<QW_BF16>(gy, x, w, E, N, K, offsets, rows, gx, accumulate, gw, gw_f32, ws, ws_bytes, stream);
 }
 
 }  // namespace qw

@@ -130,12 +130,12 @@ __global__ __launch_bounds__(256) void grouped_dw_kernel(const void* __restrict_
 
 size_t gemm_backward_workspace_bytes(int64_t E, int64_t N, int64_t K, int64_t rows);
 bool gemm_backward_fits(int64_t rows, int64_t E);
-int gemm_grouped_backward(const void* gy, const void* x, const void* w, int64_t E, int64_t N, int64_t K,
+int gemm_grouped_backward(const void* gy, const void* x, const void* w, int dtype, int64_t E, int64_t N, int64_t K,
                           const int32_t* offsets, int64_t rows, int64_t rows_per_expert, void* gx, int accumulate,
                           void* gw, int gw_f32, void* ws, size_t ws_bytes, hipStream_t stream);
 
 size_t grouped_backward_workspace_bytes(int64_t E, int64_t N, int64_t K, int64_t rows, int dtype) {
-  return dtype == QW_BF16 ? gemm_backward_workspace_bytes(E, N, K, rows) : 256;
+  return is_half(dtype) ? gemm_backward_workspace_bytes(E, N, K, rows) : 256;
 }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -143,7 +143,7 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 int grouped_matmul_backward(const void* gy, const void* x, const void* w, int dtype, int64_t E, int64_t N, int64_t K,
                             const int32_t* offsets, int64_t rows, int64_t max_rows_per_expert, void* gx, int accumulate,
                             void* gw, int gw_dtype, void* ws, size_t ws_bytes, hipStream_t stream) {
-  QW_REQUIRE(dtype == QW_F32 || dtype == QW_BF16, "grouped backward dtype must be f32 or bf16");
+  QW_REQUIRE(dtype == QW_F32 || dtype == QW_BF16 || dtype == QW_F16, "grouped backward dtype must be f32, bf16 or f16");
   QW_REQUIRE(gw_dtype == dtype || gw_dtype == QW_F32, "grad_w dtype must be the operands' dtype or f32");
   QW_REQUIRE(E >= 1 && E <= 65535 && N >= 1 && K >= 1 && N <= INT32_MAX && K <= INT32_MAX && rows >= 0 &&
                  rows <= INT32_MAX && max_rows_per_expert >= 0,
@@ -153,13 +153,13 @@ int grouped_matmul_backward(const void* gy, const void* x, const void* w, int dt
   if (gw != nullptr) QW_REQUIRE(rows == 0 || (gy && x), "grad_w needs grad_out and x");
   const int64_t per = max_rows_per_expert > 0 && max_rows_per_expert < rows ? max_rows_per_expert : rows;
   QW_REQUIRE(ceil_div(per, BT) <= 65535 && ceil_div(N, BT) <= 65535, "grouped backward sizes out of range");
-  // matrix-core path (bf16 with a workspace): dX needs out_features % 64 == 0, dW any shape
-  const bool core = dtype == QW_BF16 && ws != nullptr && ws_bytes >= gemm_backward_workspace_bytes(E, N, K, rows) &&
+  // matrix-core path (bf16/fp16 with a workspace): dX needs out_features % 64 == 0, dW any shape
+  const bool core = is_half(dtype) && ws != nullptr && ws_bytes >= gemm_backward_workspace_bytes(E, N, K, rows) &&
                     aligned16(gy) && aligned16(x) && aligned16(w) && gemm_backward_fits(rows, E);
   const bool core_dx = core && gx != nullptr && aligned16(gx) && N % 64 == 0 && K % 4 == 0;
   const bool core_dw = core && gw != nullptr && aligned16(gw);
   if (core_dx || core_dw) {
-    const int st = gemm_grouped_backward(gy, x, w, E, N, K, offsets, rows, per, core_dx ? gx : nullptr, accumulate,
+    const int st = gemm_grouped_backward(gy, x, w, dtype, E, N, K, offsets, rows, per, core_dx ? gx : nullptr, accumulate,
                                          core_dw ? gw : nullptr, gw_dtype == QW_F32, ws, ws_bytes, stream);
     if (st) return st;
     if (core_dx) gx = nullptr;
@@ -170,6 +170,7 @@ int grouped_matmul_backward(const void* gy, const void* x, const void* w, int dt
     const dim3 g(static_cast<unsigned>(ceil_div(K, BT)), static_cast<unsigned>(ceil_div(per, BT)),
                  static_cast<unsigned>(E));
     if (dtype == QW_F32) grouped_dx_kernel<QW_F32><<<g, 256, 0, stream>>>(gy, w, offsets, n, k, r, accumulate, gx);
+    else if (dtype == QW_F16) grouped_dx_kernel<QW_F16><<<g, 256, 0, stream>>>(gy, w, offsets, n, k, r, accumulate, gx);
     else grouped_dx_kernel<QW_BF16><<<g, 256, 0, stream>>>(gy, w, offsets, n, k, r, accumulate, gx);
     QW_LAUNCH_CHECK("grouped_dx_kernel");
   }
@@ -177,6 +178,9 @@ int grouped_matmul_backward(const void* gy, const void* x, const void* w, int dt
     const dim3 g(static_cast<unsigned>(ceil_div(K, BT)), static_cast<unsigned>(ceil_div(N, BT)),
                  static_cast<unsigned>(E));
     if (dtype == QW_F32) grouped_dw_kernel<QW_F32, QW_F32><<<g, 256, 0, stream>>>(gy, x, offsets, n, k, r, gw);
+    else if (dtype == QW_F16 && gw_dtype == QW_F32)
+      grouped_dw_kernel<QW_F16, QW_F32><<<g, 256, 0, stream>>>(gy, x, offsets, n, k, r, gw);
+    else if (dtype == QW_F16) grouped_dw_kernel<QW_F16, QW_F16><<<g, 256, 0, stream>>>(gy, x, offsets, n, k, r, gw);
     else if (gw_dtype == QW_F32) grouped_dw_kernel<QW_BF16, QW_F32><<<g, 256, 0, stream>>>(gy, x, offsets, n, k, r, gw);
     else grouped_dw_kernel<QW_BF16, QW_BF16><<<g, 256, 0, stream>>>(gy, x, offsets, n, k, r, gw);
     QW_LAUNCH_CHECK("grouped_dw_kernel");

@@ -29,7 +29,7 @@ __global__ __launch_bounds__(256) void permute_kernel(const char* __restrict__ x
 
 int permute(const void* x, int dtype, int64_t D, const int32_t* slot_token, const int32_t* totals, int64_t max_rows,
             void* out, hipStream_t stream) {
-  QW_REQUIRE(dtype == QW_F32 || dtype == QW_BF16, "permute dtype must be f32 or bf16");
+  QW_REQUIRE(dtype == QW_F32 || dtype == QW_BF16 || dtype == QW_F16, "permute dtype must be f32, bf16 or f16");
   QW_REQUIRE(D >= 1 && max_rows >= 0 && max_rows <= INT32_MAX, "bad permute sizes");
   if (max_rows == 0) return QW_OK;
   QW_REQUIRE(x && slot_token && totals && out, "permute pointers are required");
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
 template <int ACT, int OUT, int KMAX, bool WEIGHTED, bool STATIC>
 void launch_combine_vec(const void* y, const int32_t* route_slot, const int32_t* top_idx, const float* top_w,
                         unsigned g, int k, int d, void* out, hipStream_t stream) {
-  constexpr int V = (ACT == QW_BF16 || OUT == QW_BF16) ? 8 : 4;
+  constexpr int V = (ACT != QW_F32 || OUT != QW_F32) ? 8 : 4;
   if (d % V == 0)
     combine_kernel<ACT, OUT, V, KMAX, WEIGHTED, STATIC>
         <<<g, 256, 0, stream>>>(y, route_slot, top_idx, top_w, k, d, out);
@@ -141,15 +141,20 @@ void launch_combine_vec(const void* y, const int32_t* route_slot, const int32_t*
 template <int KMAX, bool WEIGHTED, bool STATIC>
 int launch_combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, const float* top_w,
                    unsigned g, int k, int d, void* out, int out_dtype, hipStream_t stream) {
-  if (dtype == QW_F32 && out_dtype == QW_F32)
-    launch_combine_vec<QW_F32, QW_F32, KMAX, WEIGHTED, STATIC>(y, route_slot, top_idx, top_w, g, k, d, out, stream);
-  else if (dtype == QW_F32)
-    launch_combine_vec<QW_F32, QW_BF16, KMAX, WEIGHTED, STATIC>(y, route_slot, top_idx, top_w, g, k, d, out, stream);
-  else if (out_dtype == QW_F32)
-    launch_combine_vec<QW_BF16, QW_F32, KMAX, WEIGHTED, STATIC>(y, route_slot, top_idx, top_w, g, k, d, out, stream);
+#define QW_CB(A, O)                                                                                             \
+  if (dtype == A && out_dtype == O)                                                                             \
+    launch_combine_vec<A, O, KMAX, WEIGHTED, STATIC>(y, route_slot, top_idx, top_w, g, k, d, out, stream);   \
   else
-    launch_combine_vec<QW_BF16, QW_BF16, KMAX, WEIGHTED, STATIC>(y, route_slot, top_idx, top_w, g, k, d, out,
-                                                                 stream);
+  QW_CB(QW_F32, QW_F32)
+  QW_CB(QW_F32, QW_BF16)
+  QW_CB(QW_BF16, QW_F32)
+  QW_CB(QW_BF16, QW_BF16)
+  QW_CB(QW_F16, QW_F16)
+  QW_CB(QW_F16, QW_F32)
+  QW_CB(QW_F32, QW_F16)
+  return set_error(QW_ERR_INVALID, "combine does not take rows of dtype %d into an output of dtype %d", dtype,
+                   out_dtype);
+#undef QW_CB
   QW_LAUNCH_CHECK("combine_kernel");
   return QW_OK;
 }
@@ -172,8 +177,11 @@ int combine_k(const void* y, int dtype, const int32_t* route_slot, const int32_t
 
 static int combine_check(const void* y, int dtype, const int32_t* route_slot, const int32_t* top_idx, int64_t T,
                          int64_t K, int64_t D, void* out, int out_dtype) {
-  QW_REQUIRE((dtype == QW_F32 || dtype == QW_BF16) && (out_dtype == QW_F32 || out_dtype == QW_BF16),
-             "combine dtypes must be f32 or bf16");
+  QW_REQUIRE((dtype == QW_F32 || dtype == QW_BF16 || dtype == QW_F16) &&
+                 (out_dtype == QW_F32 || out_dtype == QW_BF16 || out_dtype == QW_F16),
+             "combine dtypes must be f32, bf16 or f16");
+  QW_REQUIRE(!(is_half(dtype) && is_half(out_dtype) && dtype != out_dtype),
+             "combine does not mix bf16 and f16 (rows %d, output %d)", dtype, out_dtype);
   QW_REQUIRE(K >= 1 && K <= 64, "combine supports top_k in [1, 64], got %lld", (long long)K);
   QW_REQUIRE(T >= 0 && T <= INT32_MAX && D >= 1 && D <= INT32_MAX, "bad combine sizes");
   QW_REQUIRE(T == 0 || (y && route_slot && top_idx && out), "combine pointers are required");
@@ -242,6 +250,8 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const void* __restr
         yv[1] = q.y;
         yv[2] = q.z;
         yv[3] = q.w;
+      } else if constexpr (VEC == 8 && ACT == QW_F16) {
+        load_vec<QW_F16, 8>(y, src, yv);
       } else {
 #pragma unroll
         for (int v = 0; v < VEC; ++v) yv[v] = load_act<ACT>(y, src + v);
@@ -260,13 +270,17 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const void* __restr
 
 int decode_combine(const void* y, int dtype, const int32_t* route_slot, const float* top_w, const float* residual,
                    int64_t T, int64_t K, int64_t D, float* out, hipStream_t stream) {
-  QW_REQUIRE(dtype == QW_F32 || dtype == QW_BF16, "decode combine dtype must be f32 or bf16");
+  QW_REQUIRE(dtype == QW_F32 || dtype == QW_BF16 || dtype == QW_F16, "decode combine dtype must be f32, bf16 or f16");
   QW_REQUIRE(T >= 0 && T <= INT32_MAX && K >= 1 && D >= 1 && D <= INT32_MAX, "bad decode combine sizes");
   if (T == 0) return QW_OK;
   QW_REQUIRE(y && route_slot && top_w && out, "decode combine pointers are required");
   const unsigned g = static_cast<unsigned>(T);
   const int k = static_cast<int>(K), d = static_cast<int>(D);
-  if (dtype == QW_BF16 && d % 8 == 0)
+  if (dtype == QW_F16 && d % 8 == 0)
+    decode_combine_kernel<QW_F16, 8><<<g, 256, 0, stream>>>(y, route_slot, top_w, residual, k, d, out);
+  else if (dtype == QW_F16)
+    decode_combine_kernel<QW_F16, 1><<<g, 256, 0, stream>>>(y, route_slot, top_w, residual, k, d, out);
+  else if (dtype == QW_BF16 && d % 8 == 0)
     decode_combine_kernel<QW_BF16, 8><<<g, 256, 0, stream>>>(y, route_slot, top_w, residual, k, d, out);
   else if (dtype == QW_BF16)
     decode_combine_kernel<QW_BF16, 1><<<g, 256, 0, stream>>>(y, route_slot, top_w, residual, k, d, out);
@@ -278,29 +292,33 @@ int decode_combine(const void* y, int dtype, const int32_t* route_slot, const fl
   return QW_OK;
 }
 
-// fp32 -> bf16, round to nearest even (`normed.to(torch.bfloat16)`,
+// fp32 -> bf16 or fp16, round to nearest even (`normed.to(dtype)`,
 // src/fast_decode.py:174).  Four elements per thread when n % 4 == 0.
-__global__ __launch_bounds__(256) void cast_bf16_kernel(const float* __restrict__ x, int64_t n,
+template <int DT>
+__global__ __launch_bounds__(256) void cast_half_kernel(const float* __restrict__ x, int64_t n,
                                                         uint16_t* __restrict__ out) {
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
   if (i >= n) return;
   if ((n & 3) == 0) {
     const float4 v = *reinterpret_cast<const float4*>(x + i);
     uint2 o;
-    o.x = f32_to_bf16(v.x) | (static_cast<uint32_t>(f32_to_bf16(v.y)) << 16);
-    o.y = f32_to_bf16(v.z) | (static_cast<uint32_t>(f32_to_bf16(v.w)) << 16);
+    o.x = f32_to_half<DT>(v.x) | (static_cast<uint32_t>(f32_to_half<DT>(v.y)) << 16);
+    o.y = f32_to_half<DT>(v.z) | (static_cast<uint32_t>(f32_to_half<DT>(v.w)) << 16);
     *reinterpret_cast<uint2*>(out + i) = o;
   } else {
-    for (int64_t j = i; j < i + 4 && j < n; ++j) out[j] = f32_to_bf16(x[j]);
+    for (int64_t j = i; j < i + 4 && j < n; ++j) out[j] = f32_to_half<DT>(x[j]);
   }
 }
 
-int cast_bf16(const float* x, int64_t n, uint16_t* out, hipStream_t stream) {
+int cast_half(const float* x, int64_t n, uint16_t* out, int dtype, hipStream_t stream) {
   QW_REQUIRE(n >= 0, "bad cast size");
+  QW_REQUIRE(is_half(dtype), "the cast is to bf16 or f16");
   if (n == 0) return QW_OK;
   QW_REQUIRE(x && out, "cast pointers are required");
-  cast_bf16_kernel<<<static_cast<unsigned>(ceil_div(ceil_div(n, 4), 256)), 256, 0, stream>>>(x, n, out);
-  QW_LAUNCH_CHECK("cast_bf16_kernel");
+  const unsigned g = static_cast<unsigned>(ceil_div(ceil_div(n, 4), 256));
+  if (dtype == QW_F16) cast_half_kernel<QW_F16><<<g, 256, 0, stream>>>(x, n, out);
+  else cast_half_kernel<QW_BF16><<<g, 256, 0, stream>>>(x, n, out);
+  QW_LAUNCH_CHECK("cast_half_kernel");
   return QW_OK;
 }
 
@@ -422,7 +440,7 @@ __global__ void quantize_kernel(const void* __restrict__ w, int64_t rows, int64_
 int quantize(const void* w, int wdt, int64_t rows, int64_t cols, int bits, int64_t group, void* qweight, float* scales,
              hipStream_t stream) {
   QW_REQUIRE(bits == 4 || bits == 8, "bits must be 4 or 8");
-  QW_REQUIRE(wdt == QW_F32 || wdt == QW_BF16, "weight dtype must be f32 or bf16");
+  QW_REQUIRE(wdt == QW_F32 || wdt == QW_BF16 || wdt == QW_F16, "weight dtype must be f32, bf16 or f16");
   QW_REQUIRE(group >= 1, "group_size must be positive");
   QW_REQUIRE(!(bits == 4 && (group % 2)), "group_size must be even for 4-bit weights");
   QW_REQUIRE(rows >= 0 && cols >= 1, "bad quantize sizes");
@@ -433,6 +451,8 @@ int quantize(const void* w, int wdt, int64_t rows, int64_t cols, int bits, int64
   const unsigned g = static_cast<unsigned>(ceil_div(n, 256));
   if (wdt == QW_F32 && bits == 8) quantize_kernel<QW_F32, 8><<<g, 256, 0, stream>>>(w, rows, cols, group, groups, qweight, scales);
   else if (wdt == QW_F32) quantize_kernel<QW_F32, 4><<<g, 256, 0, stream>>>(w, rows, cols, group, groups, qweight, scales);
+  else if (wdt == QW_F16 && bits == 8) quantize_kernel<QW_F16, 8><<<g, 256, 0, stream>>>(w, rows, cols, group, groups, qweight, scales);
+  else if (wdt == QW_F16) quantize_kernel<QW_F16, 4><<<g, 256, 0, stream>>>(w, rows, cols, group, groups, qweight, scales);
   else if (bits == 8) quantize_kernel<QW_BF16, 8><<<g, 256, 0, stream>>>(w, rows, cols, group, groups, qweight, scales);
   else quantize_kernel<QW_BF16, 4><<<g, 256, 0, stream>>>(w, rows, cols, group, groups, qweight, scales);
   QW_LAUNCH_CHECK("quantize_kernel");

@@ -6,6 +6,8 @@
 // div, rint) in a fixed order, so the same sequence evaluated on any IEEE
 // machine gives the same bits.  That is what makes the routing decisions
 // (indices, capacity slots, drops) reproducible bit-for-bit from the logits.
+#include <type_traits>
+
 #include "qw_common.h"
 
 namespace qw {
@@ -600,8 +602,8 @@ static int launch_topk(const float* partial, int splits, float temperature, floa
 //   3. thread r ranks route r among the routes of its expert by the plan key
 //      (weight descending, then route id: src/quantweave_moe_model.py:174-175)
 //      and writes its slot, or its dropped entry.
-// Optionally the same workgroup writes cast_out = bf16(cast_x) (n values),
-// the decode step's expert input.
+// Optionally the same workgroup writes cast_out = bf16(cast_x) (or fp16 with
+// cast_f16; n values), the decode step's expert input.
 // ---------------------------------------------------------------------------
 constexpr int kSmallThreads = 1024;
 constexpr int kSmallTokens = 64;       // tokens of the one-workgroup plan
@@ -617,7 +619,7 @@ __global__ __launch_bounds__(kSmallThreads) void route_plan_small_kernel(
     int32_t* __restrict__ counts, int32_t* __restrict__ kept_counts, int32_t* __restrict__ kept_offsets,
     int32_t* __restrict__ totals, int32_t* __restrict__ slot_token, float* __restrict__ slot_weight,
     int32_t* __restrict__ route_slot, int32_t* __restrict__ dropped_token, int32_t* __restrict__ dropped_expert,
-    const float* __restrict__ cast_x, int cast_n, uint16_t* __restrict__ cast_out) {
+    const float* __restrict__ cast_x, int cast_n, uint16_t* __restrict__ cast_out, int cast_f16) {
   constexpr int kWaves = kSmallThreads / kWave;
   __shared__ float s_logit[kSmallLogits];
   __shared__ int s_e[kSmallRoutes];
@@ -634,11 +636,17 @@ __global__ __launch_bounds__(kSmallThreads) void route_plan_small_kernel(
       if (i + 4 <= cast_n && (cast_n & 3) == 0) {
         const float4 v = *reinterpret_cast<const float4*>(cast_x + i);
         uint2 o;
-        o.x = f32_to_bf16(v.x) | (static_cast<uint32_t>(f32_to_bf16(v.y)) << 16);
-        o.y = f32_to_bf16(v.z) | (static_cast<uint32_t>(f32_to_bf16(v.w)) << 16);
+        if (cast_f16) {
+          o.x = f32_to_f16(v.x) | (static_cast<uint32_t>(f32_to_f16(v.y)) << 16);
+          o.y = f32_to_f16(v.z) | (static_cast<uint32_t>(f32_to_f16(v.w)) << 16);
+        } else {
+          o.x = f32_to_bf16(v.x) | (static_cast<uint32_t>(f32_to_bf16(v.y)) << 16);
+          o.y = f32_to_bf16(v.z) | (static_cast<uint32_t>(f32_to_bf16(v.w)) << 16);
+        }
         *reinterpret_cast<uint2*>(cast_out + i) = o;
       } else {
-        for (int j = i; j < i + 4 && j < cast_n; ++j) cast_out[j] = f32_to_bf16(cast_x[j]);
+        for (int j = i; j < i + 4 && j < cast_n; ++j)
+          cast_out[j] = cast_f16 ? f32_to_f16(cast_x[j]) : f32_to_bf16(cast_x[j]);
       }
     }
   }
@@ -748,14 +756,28 @@ static void launch_router_gemv_vec(bool vec, const void* x, int64_t x_stride, co
   else launch_router_gemv_tt<XD, WD, 1>(x, x_stride, w, t, d, e, temperature, logits, stream);
 }
 
+// Calls f(XD, WD) with the dtype codes of the router input and weights as
+// compile-time constants (fp32, bf16 or fp16 each).
+template <typename Fn>
+static void with_router_dtypes(int xdt, int wdt, Fn&& f) {
+  auto inner = [&](auto xd) {
+    if (wdt == QW_F32) f(xd, std::integral_constant<int, QW_F32>{});
+    else if (wdt == QW_F16) f(xd, std::integral_constant<int, QW_F16>{});
+    else f(xd, std::integral_constant<int, QW_BF16>{});
+  };
+  if (xdt == QW_F32) inner(std::integral_constant<int, QW_F32>{});
+  else if (xdt == QW_F16) inner(std::integral_constant<int, QW_F16>{});
+  else inner(std::integral_constant<int, QW_BF16>{});
+}
+
 static int launch_router_gemv(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int t, int d,
                               int e, float temperature, float* logits, hipStream_t stream) {
   const bool vec = d % 4 == 0 && x_stride % 4 == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0 &&
                    (reinterpret_cast<uintptr_t>(w) % 16) == 0;
-  if (xdt == QW_F32 && wdt == QW_F32) launch_router_gemv_vec<QW_F32, QW_F32>(vec, x, x_stride, w, t, d, e, temperature, logits, stream);
-  else if (xdt == QW_F32) launch_router_gemv_vec<QW_F32, QW_BF16>(vec, x, x_stride, w, t, d, e, temperature, logits, stream);
-  else if (wdt == QW_F32) launch_router_gemv_vec<QW_BF16, QW_F32>(vec, x, x_stride, w, t, d, e, temperature, logits, stream);
-  else launch_router_gemv_vec<QW_BF16, QW_BF16>(vec, x, x_stride, w, t, d, e, temperature, logits, stream);
+  with_router_dtypes(xdt, wdt, [&](auto xd, auto wd) {
+    launch_router_gemv_vec<decltype(xd)::value, decltype(wd)::value>(vec, x, x_stride, w, t, d, e, temperature,
+                                                                       logits, stream);
+  });
   QW_LAUNCH_CHECK("router_gemv_kernel");
   return QW_OK;
 }
@@ -817,13 +839,10 @@ static int launch_router(const void* x, int xdt, int64_t x_stride, const void* w
                                                  static_cast<const uint16_t*>(w), t, d, e, kl, partial);
     QW_LAUNCH_CHECK("router_mfma_kernel");
   } else {
-#define QW_RL(XD, WD) \
-  router_logits_kernel<XD, WD><<<grid, 256, 0, stream>>>(x, x_stride, w, t, d, e, kl, partial)
-    if (xdt == QW_F32 && wdt == QW_F32) QW_RL(QW_F32, QW_F32);
-    else if (xdt == QW_F32) QW_RL(QW_F32, QW_BF16);
-    else if (wdt == QW_F32) QW_RL(QW_BF16, QW_F32);
-    else QW_RL(QW_BF16, QW_BF16);
-#undef QW_RL
+    with_router_dtypes(xdt, wdt, [&](auto xd, auto wd) {
+      router_logits_kernel<decltype(xd)::value, decltype(wd)::value>
+          <<<grid, 256, 0, stream>>>(x, x_stride, w, t, d, e, kl, partial);
+    });
     QW_LAUNCH_CHECK("router_logits_kernel");
   }
   return QW_OK;
@@ -834,8 +853,8 @@ int route(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int6
           float* top_w, float* partial, size_t partial_bytes, hipStream_t stream, bool select_logits) {
   int st = route_validate(T, E, K);
   if (st) return st;
-  QW_REQUIRE(xdt == QW_F32 || xdt == QW_BF16, "router input dtype must be f32 or bf16");
-  QW_REQUIRE(wdt == QW_F32 || wdt == QW_BF16, "router weight dtype must be f32 or bf16");
+  QW_REQUIRE(xdt == QW_F32 || xdt == QW_BF16 || xdt == QW_F16, "router input dtype must be f32, bf16 or f16");
+  QW_REQUIRE(wdt == QW_F32 || wdt == QW_BF16 || wdt == QW_F16, "router weight dtype must be f32, bf16 or f16");
   QW_REQUIRE(D >= 1 && D <= INT32_MAX, "d_model out of range");
   QW_REQUIRE(x_stride >= D, "x row stride %lld smaller than d_model %lld", (long long)x_stride, (long long)D);
   QW_REQUIRE(temperature > 0.0f, "router_temperature must be positive");
@@ -868,13 +887,13 @@ int route_plan_small(const void* x, int xdt, int64_t x_stride, const void* w, in
                      float* probs, int32_t* top_idx, float* top_w, int64_t capacity, int32_t* counts,
                      int32_t* kept_counts, int32_t* kept_offsets, int32_t* totals, int32_t* slot_token,
                      float* slot_weight, int32_t* route_slot, int32_t* dropped_token, int32_t* dropped_expert,
-                     const float* cast_x, uint16_t* cast_out, float* partial, size_t partial_bytes,
-                     hipStream_t stream) {
+                     const float* cast_x, uint16_t* cast_out, int cast_dtype, float* partial,
+                     size_t partial_bytes, hipStream_t stream) {
   int st = route_validate(T, E, K);
   if (st) return st;
   QW_REQUIRE(route_plan_small_fits(T, E, K), "batch too large for the one-workgroup plan");
-  QW_REQUIRE(xdt == QW_F32 || xdt == QW_BF16, "router input dtype must be f32 or bf16");
-  QW_REQUIRE(wdt == QW_F32 || wdt == QW_BF16, "router weight dtype must be f32 or bf16");
+  QW_REQUIRE(xdt == QW_F32 || xdt == QW_BF16 || xdt == QW_F16, "router input dtype must be f32, bf16 or f16");
+  QW_REQUIRE(wdt == QW_F32 || wdt == QW_BF16 || wdt == QW_F16, "router weight dtype must be f32, bf16 or f16");
   QW_REQUIRE(D >= 1 && D <= INT32_MAX / kSmallTokens && x_stride >= D, "bad router sizes");
   QW_REQUIRE(temperature > 0.0f, "router_temperature must be positive");
   QW_REQUIRE(capacity >= 0, "capacity must be >= 0");
@@ -882,6 +901,7 @@ int route_plan_small(const void* x, int xdt, int64_t x_stride, const void* w, in
                  slot_weight && route_slot && dropped_token && dropped_expert,
              "routing and plan arrays are required");
   QW_REQUIRE(cast_out == nullptr || (cast_x != nullptr && x_stride == D), "cast needs contiguous fp32 rows");
+  QW_REQUIRE(cast_out == nullptr || is_half(cast_dtype), "the cast is to bf16 or f16");
   const int t = static_cast<int>(T), d = static_cast<int>(D), e = static_cast<int>(E), k = static_cast<int>(K);
   int splits = 0;
   const int routed = T > kSmallRouteTokens ? 1 : 0;
@@ -903,7 +923,8 @@ int route_plan_small(const void* x, int xdt, int64_t x_stride, const void* w, in
                                                               select_logits ? 1 : 0, probs,                           \
                                                               top_idx, top_w, cap, counts, kept_counts, kept_offsets, \
                                                               totals, slot_token, slot_weight, route_slot,          \
-                                                              dropped_token, dropped_expert, cast_x, n, cast_out)
+                                                              dropped_token, dropped_expert, cast_x, n, cast_out,  \
+                                                              cast_dtype == QW_F16 ? 1 : 0)
   if (epl <= 1) QW_RP(1);
   else if (epl <= 2) QW_RP(2);
   else if (epl <= 4) QW_RP(4);

@@ -187,12 +187,13 @@ void launch_combine_backward(const void* grad_out, const void* y, const int32_t*
 }  // namespace
 
 int swiglu(const void* g, const void* u, int dtype, int64_t n, void* h, hipStream_t stream) {
-  QW_REQUIRE(dtype == QW_F32 || dtype == QW_BF16, "swiglu dtype must be f32 or bf16");
+  QW_REQUIRE(dtype == QW_F32 || dtype == QW_BF16 || dtype == QW_F16, "swiglu dtype must be f32, bf16 or f16");
   QW_REQUIRE(n >= 0, "bad swiglu size");
   if (n == 0) return QW_OK;
   QW_REQUIRE(g && u && h, "swiglu pointers are required");
   QW_REQUIRE(ceil_div(n, 256) <= INT32_MAX, "swiglu size out of range");
   if (dtype == QW_F32) launch_swiglu<QW_F32>(g, u, n, h, nullptr, nullptr, nullptr, false, stream);
+  else if (dtype == QW_F16) launch_swiglu<QW_F16>(g, u, n, h, nullptr, nullptr, nullptr, false, stream);
   else launch_swiglu<QW_BF16>(g, u, n, h, nullptr, nullptr, nullptr, false, stream);
   QW_LAUNCH_CHECK("swiglu_kernel");
   return QW_OK;
@@ -200,12 +201,13 @@ int swiglu(const void* g, const void* u, int dtype, int64_t n, void* h, hipStrea
 
 int swiglu_backward(const void* dh, const void* g, const void* u, int dtype, int64_t n, void* dg, void* du,
                     hipStream_t stream) {
-  QW_REQUIRE(dtype == QW_F32 || dtype == QW_BF16, "swiglu dtype must be f32 or bf16");
+  QW_REQUIRE(dtype == QW_F32 || dtype == QW_BF16 || dtype == QW_F16, "swiglu dtype must be f32, bf16 or f16");
   QW_REQUIRE(n >= 0, "bad swiglu size");
   if (n == 0) return QW_OK;
   QW_REQUIRE(dh && g && u && dg && du, "swiglu backward pointers are required");
   QW_REQUIRE(ceil_div(n, 256) <= INT32_MAX, "swiglu size out of range");
   if (dtype == QW_F32) launch_swiglu<QW_F32>(g, u, n, nullptr, const_cast<void*>(dh), dg, du, true, stream);
+  else if (dtype == QW_F16) launch_swiglu<QW_F16>(g, u, n, nullptr, const_cast<void*>(dh), dg, du, true, stream);
   else launch_swiglu<QW_BF16>(g, u, n, nullptr, const_cast<void*>(dh), dg, du, true, stream);
   QW_LAUNCH_CHECK("swiglu_backward_kernel");
   return QW_OK;
@@ -214,14 +216,22 @@ int swiglu_backward(const void* dh, const void* g, const void* u, int dtype, int
 int combine_backward(const void* grad_out, int out_dtype, const void* y, int y_dtype, const int32_t* route_slot,
                      const float* top_w, int64_t T, int64_t K, int64_t D, void* grad_y, float* grad_top_w,
                      hipStream_t stream) {
-  QW_REQUIRE((out_dtype == QW_F32 || out_dtype == QW_BF16) && (y_dtype == QW_F32 || y_dtype == QW_BF16),
-             "combine backward dtypes must be f32 or bf16");
+  QW_REQUIRE((out_dtype == QW_F32 || out_dtype == QW_BF16 || out_dtype == QW_F16) &&
+                 (y_dtype == QW_F32 || y_dtype == QW_BF16 || y_dtype == QW_F16) &&
+                 !(is_half(out_dtype) && is_half(y_dtype) && out_dtype != y_dtype),
+             "combine backward dtypes must be f32, bf16 or f16 (bf16 and f16 not mixed)");
   QW_REQUIRE(T >= 0 && T <= INT32_MAX && K >= 1 && K <= 64 && D >= 1 && D <= INT32_MAX,
              "bad combine backward sizes");
   if (T == 0) return QW_OK;
   QW_REQUIRE(grad_out && y && route_slot && top_w && grad_y && grad_top_w, "combine backward pointers are required");
   const int t = static_cast<int>(T), k = static_cast<int>(K), d = static_cast<int>(D);
-  if (out_dtype == QW_F32 && y_dtype == QW_F32)
+  if (out_dtype == QW_F16 && y_dtype == QW_F16)
+    launch_combine_backward<QW_F16, QW_F16>(grad_out, y, route_slot, top_w, t, k, d, grad_y, grad_top_w, stream);
+  else if (out_dtype == QW_F32 && y_dtype == QW_F16)
+    launch_combine_backward<QW_F32, QW_F16>(grad_out, y, route_slot, top_w, t, k, d, grad_y, grad_top_w, stream);
+  else if (out_dtype == QW_F16 && y_dtype == QW_F32)
+    launch_combine_backward<QW_F16, QW_F32>(grad_out, y, route_slot, top_w, t, k, d, grad_y, grad_top_w, stream);
+  else if (out_dtype == QW_F32 && y_dtype == QW_F32)
     launch_combine_backward<QW_F32, QW_F32>(grad_out, y, route_slot, top_w, t, k, d, grad_y, grad_top_w, stream);
   else if (out_dtype == QW_F32)
     launch_combine_backward<QW_F32, QW_BF16>(grad_out, y, route_slot, top_w, t, k, d, grad_y, grad_top_w, stream);

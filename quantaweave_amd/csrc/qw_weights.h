@@ -33,7 +33,7 @@ inline WView make_wview(int fmt, const void* w, const float* scales, int64_t row
   v.rows = rows;
   v.cols = cols;
   v.group = group;
-  if (fmt == QW_F32 || fmt == QW_BF16 || fmt == QW_BF16T) {
+  if (fmt == QW_F32 || fmt == QW_BF16 || fmt == QW_BF16T || fmt == QW_F16 || fmt == QW_F16T) {
     v.row_stride = cols;
     v.groups = 0;
   } else {
@@ -65,6 +65,10 @@ __device__ __forceinline__ float load_weight(const WView& v, int64_t e, int64_t 
     return bf16_to_f32(static_cast<const uint16_t*>(v.w)[e * v.expert_elems + row * v.row_stride + col]);
   } else if constexpr (WF == QW_BF16T) {
     return bf16_to_f32(static_cast<const uint16_t*>(v.w)[e * v.expert_elems + bf16t_index(row, col, v.cols)]);
+  } else if constexpr (WF == QW_F16) {
+    return f16_to_f32(static_cast<const uint16_t*>(v.w)[e * v.expert_elems + row * v.row_stride + col]);
+  } else if constexpr (WF == QW_F16T) {
+    return f16_to_f32(static_cast<const uint16_t*>(v.w)[e * v.expert_elems + bf16t_index(row, col, v.cols)]);
   } else if constexpr (WF == QW_I8) {
     const int8_t q = static_cast<const int8_t*>(v.w)[e * v.expert_elems + row * v.row_stride + col];
     const float s = v.scales[e * v.expert_scales + row * v.groups + col / v.group];

@@ -25,14 +25,11 @@ from .moe import ExpertPack
 
 
 def precision_dtype(device: torch.device, precision: str) -> torch.dtype:
-    """src/fast_decode.py:75-78: "auto" is bf16 on a GPU.  fp16 is not a
-    compute dtype of the HIP expert kernels and is refused."""
+    """src/fast_decode.py:75-78: "auto" is bf16 on a GPU; "bf16", "fp16" and
+    "fp32" name their dtypes."""
     if precision == "auto":
         precision = "bf16" if device.type == "cuda" else "fp32"
-    table = {"bf16": torch.bfloat16, "fp32": torch.float32}
-    if precision not in table:
-        raise ValueError(f"precision {precision!r} is not supported by the HIP decode step (bf16 or fp32)")
-    return table[precision]
+    return {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[precision]
 
 
 class MoEDecodeStep:
@@ -72,16 +69,14 @@ class MoEDecodeStep:
         bias = getattr(moe, "expert_bias", None)
         self.bias = None if bias is None else bias.detach().to(device, torch.float32).contiguous()
         experts = moe.experts
-        self.pack = ExpertPack(experts)
-        cast = self.pack.fmt == _lib.QW_F32 and self.dtype == torch.bfloat16
+        pack = ExpertPack(experts)
         for name in ("gate", "up", "down", "gate_s", "up_s", "down_s"):
-            t = getattr(self.pack, name)
+            t = getattr(pack, name)
             if t is not None:
-                t = t.to(device, torch.bfloat16 if cast and not name.endswith("_s") else t.dtype)
-                setattr(self.pack, name, t.contiguous())
-        if cast:
-            self.pack.fmt = _lib.QW_BF16
-            self.pack.maybe_tile()
+                setattr(pack, name, t.to(device).contiguous())
+        pack.maybe_tile()
+        # float experts in another 16-bit compute type: one cast copy (tiled where the shapes allow)
+        self.pack = pack.for_act(self.compute)
         self.ffn = int(experts[0].gate.out_features)
         T, E, K = self.tokens, self.experts_count, self.top_k
         lib = _lib.load()

@@ -104,18 +104,18 @@ def _expert_format(experts: nn.ModuleList) -> tuple[int, int, int]:
             p = getattr(e, name)
             if not isinstance(p, nn.Linear) or p.bias is not None or p.weight.dtype != dt:
                 raise ValueError("experts must be bias-free nn.Linear (one dtype) or QuantizedLinear projections")
-    if dt not in (torch.float32, torch.bfloat16):
-        raise ValueError(f"expert weight dtype {dt} is not supported (float32 or bfloat16)")
-    return (_lib.QW_F32 if dt == torch.float32 else _lib.QW_BF16), 0, 0
+    if dt not in _hip.FLOAT_DTYPES:
+        raise ValueError(f"expert weight dtype {dt} is not supported (float32, bfloat16 or float16)")
+    return _hip.act_code(first.weight, "experts"), 0, 0
 
 
 def tile_bf16(stack: Tensor) -> Tensor:
-    """bf16 weights [E, out, in] (nn.Linear layout) rearranged into the 1 KiB
-    tiles of QW_BF16T (qw_pack_bf16_tiles); same shape and size."""
+    """bf16 (or fp16) weights [E, out, in] (nn.Linear layout) rearranged into
+    the 1 KiB tiles of QW_BF16T (QW_F16T) (qw_pack_bf16_tiles); same shape and size."""
     stack = stack.contiguous()
     _hip.require_device(stack, "tile_bf16")
-    if stack.dtype != torch.bfloat16 or stack.dim() != 3:
-        raise ValueError("tile_bf16 takes a bf16 [experts, out, in] tensor")
+    if stack.dtype not in _hip.HALF or stack.dim() != 3:
+        raise ValueError("tile_bf16 takes a bf16 or fp16 [experts, out, in] tensor")
     out = torch.empty_like(stack)
     E, rows, cols = stack.shape
     _lib.call("qw_pack_bf16_tiles", _hip.ptr(stack), E, rows, cols, _hip.ptr(out), _hip.stream(stack.device))
@@ -123,7 +123,7 @@ def tile_bf16(stack: Tensor) -> Tensor:
 
 
 def can_tile(stack: Tensor) -> bool:
-    return stack.dtype == torch.bfloat16 and stack.size(1) % 64 == 0 and stack.size(2) % 64 == 0
+    return stack.dtype in _hip.HALF and stack.size(1) % 64 == 0 and stack.size(2) % 64 == 0
 
 
 class ExpertPack:
@@ -131,15 +131,15 @@ class ExpertPack:
 
     Replaces the per-call ``torch.stack`` of src/moe_kernels.py:191-193; the pack
     is rebuilt only when a projection module, parameter or buffer changes
-    (tracked by identity, storage pointer and version counter).  bf16 weights whose shapes allow it are kept
-    in the QW_BF16T tiles the prefill kernels stream contiguously."""
+    (tracked by identity, storage pointer and version counter).  bf16 and fp16 weights whose shapes allow it
+    are kept in the QW_BF16T / QW_F16T tiles the prefill kernels stream contiguously."""
 
     def __init__(self, experts: nn.ModuleList) -> None:
         self.fmt, self.group_in, self.group_ff = _expert_format(experts)
         self.mods, self.tensors = ExpertPack.sources(experts)
         self.versions = [t._version for t in self.tensors]
         self.ptrs = [t.data_ptr() for t in self.tensors]
-        if self.fmt in (_lib.QW_F32, _lib.QW_BF16):
+        if self.fmt in (_lib.QW_F32, _lib.QW_BF16, _lib.QW_F16):
             self.gate = torch.stack([e.gate.weight.detach() for e in experts]).contiguous()
             self.up = torch.stack([e.up.weight.detach() for e in experts]).contiguous()
             self.down = torch.stack([e.down.weight.detach() for e in experts]).contiguous()
@@ -154,12 +154,12 @@ class ExpertPack:
             self.down_s = torch.stack([e.down.scales.float() for e in experts]).contiguous()
 
     def maybe_tile(self) -> None:
-        """bf16 stacks on a ROCm device -> QW_BF16T tiles (in place of the plain stacks)."""
-        if self.fmt != _lib.QW_BF16 or self.gate.device.type != "cuda":
+        """bf16 / fp16 stacks on a ROCm device -> QW_BF16T / QW_F16T tiles (in place of the plain stacks)."""
+        if self.fmt not in (_lib.QW_BF16, _lib.QW_F16) or self.gate.device.type != "cuda":
             return
         if all(can_tile(t) for t in (self.gate, self.up, self.down)):
             self.gate, self.up, self.down = tile_bf16(self.gate), tile_bf16(self.up), tile_bf16(self.down)
-            self.fmt = _lib.QW_BF16T
+            self.fmt = _lib.QW_BF16T if self.fmt == _lib.QW_BF16 else _lib.QW_F16T
 
     @staticmethod
     def sources(experts: nn.ModuleList) -> tuple[list, list]:
@@ -199,24 +199,35 @@ class ExpertPack:
         return cache[1]
 
     def args_for(self, act: int) -> list:
-        """Weight arguments for activations of dtype code `act`: fp32 experts
-        multiplied in bf16 use bf16 copies (tiled where the shapes allow),
-        made once per weight version — the reference's per-call
-        ``stack(...).to(dtype)`` (src/moe_kernels.py:191-193)."""
+        """Weight arguments for activations of dtype code `act`: float experts
+        multiplied in another 16-bit type (fp32 experts under bf16 or fp16
+        autocast, bf16 experts under fp16 autocast and the reverse) use copies
+        in that type (tiled where the shapes allow), made once per weight
+        version — the reference's per-call ``stack(...).to(dtype)``
+        (src/moe_kernels.py:191-193)."""
         return self.for_act(act).args()
 
     def for_act(self, act: int) -> "ExpertPack":
-        """This pack, or its bf16 copy for fp32 experts multiplied in bf16."""
-        if not (self.fmt == _lib.QW_F32 and act == _lib.QW_BF16):
+        """This pack, or its copy in the 16-bit activation type `act`."""
+        plain_of = {_lib.QW_BF16T: _lib.QW_BF16, _lib.QW_F16T: _lib.QW_F16}
+        src = plain_of.get(self.fmt, self.fmt)
+        if act not in (_lib.QW_BF16, _lib.QW_F16) or src not in (_lib.QW_F32, _lib.QW_BF16, _lib.QW_F16) or src == act:
             return self
-        if getattr(self, "_bf16", None) is None:
+        copies = self.__dict__.setdefault("_copies", {})
+        if act not in copies:
+            dt = torch.bfloat16 if act == _lib.QW_BF16 else torch.float16
             cast = ExpertPack.__new__(ExpertPack)
-            cast.fmt, cast.group_in, cast.group_ff = _lib.QW_BF16, 0, 0
-            cast.gate, cast.up, cast.down = (t.to(torch.bfloat16).contiguous() for t in (self.gate, self.up, self.down))
+            cast.group_in, cast.group_ff = 0, 0
+            # tiles are a permutation of the elements: a cast keeps them tiles
+            cast.gate, cast.up, cast.down = (t.to(dt).contiguous() for t in (self.gate, self.up, self.down))
             cast.gate_s = cast.up_s = cast.down_s = None
-            cast.maybe_tile()
-            self._bf16 = cast
-        return self._bf16
+            if self.fmt in plain_of:
+                cast.fmt = _lib.QW_BF16T if act == _lib.QW_BF16 else _lib.QW_F16T
+            else:
+                cast.fmt = act
+                cast.maybe_tile()
+            copies[act] = cast
+        return copies[act]
 
     def expert_args(self, e: int) -> list:
         """Weight arguments of expert e alone (views into the stacks)."""
@@ -315,7 +326,7 @@ class TopKMoE(nn.Module):
         # the experts one at a time, as the reference's loop does (:203-209)
         loop = not self.use_triton_kernels
         if not profiling and self._wants_grad(hidden):
-            if pack.fmt not in (_lib.QW_F32, _lib.QW_BF16, _lib.QW_BF16T):
+            if pack.fmt not in (_lib.QW_F32, _lib.QW_BF16, _lib.QW_BF16T, _lib.QW_F16, _lib.QW_F16T):
                 if hidden.requires_grad:
                     raise NotImplementedError("gradients through quantised experts are not supported")
             else:
@@ -386,7 +397,7 @@ class TopKMoE(nn.Module):
 
 def _router_operand(router_w: Tensor) -> Tensor:
     w = router_w.detach()
-    if w.dtype not in (torch.float32, torch.bfloat16):
+    if w.dtype not in _hip.FLOAT_DTYPES:
         w = w.float()
     return w.contiguous()
 
@@ -442,12 +453,13 @@ def _stream_workspace(moe: nn.Module, nbytes: int, dev: torch.device) -> Tensor:
 
 def _compute_dtype(flat: Tensor) -> torch.dtype:
     """The experts' arithmetic dtype: the autocast dtype when autocast is on,
-    else the input dtype (src/moe_kernels.py:179-183).  An autocast dtype the
-    kernels do not take (fp16) leaves the input dtype in place."""
+    else the input dtype (src/moe_kernels.py:179-183): fp32, bf16 or fp16."""
     dt = flat.dtype
     if torch.is_autocast_enabled(flat.device.type):
         dt = torch.get_autocast_dtype(flat.device.type)
-    return dt if dt in (torch.float32, torch.bfloat16) else flat.dtype
+    if dt not in _hip.FLOAT_DTYPES:
+        raise ValueError(f"TopKMoE.forward: compute dtype {dt} is not supported (float32, bfloat16 or float16)")
+    return dt
 
 
 def _layer_chain(flat: Tensor, cdt: torch.dtype, router_w: Tensor, moe: TopKMoE, pack: ExpertPack, cap: int,

@@ -57,7 +57,7 @@ class QuantizedLinear(nn.Module):
             raise ValueError("bias is not supported")
         layer = cls(linear.in_features, linear.out_features, bits, group_size).to(linear.weight.device)
         weight = linear.weight.detach()
-        if weight.dtype not in (torch.float32, torch.bfloat16):
+        if weight.dtype not in _hip.FLOAT_DTYPES:
             weight = weight.float()
         dev = weight.device if weight.device.type == "cuda" else _gpu()
         w = weight.to(dev).contiguous()

@@ -28,8 +28,8 @@ class Workload:
     d_ff: int
     top_k: int
     capacity_factor: float   # 0 = no capacity drop
-    act: str                 # "f32" | "bf16"
-    weights: str             # "f32" | "bf16" | "i8" | "u4"
+    act: str                 # "f32" | "bf16" | "f16"
+    weights: str             # "f32" | "bf16" | "f16" | "i8" | "u4"
     seed: int
     group_size: int | None = None
     zipf: float = 0.0        # Zipf exponent of the selection bias (0 = none)
@@ -64,7 +64,8 @@ WORKLOADS = {
 HEADLINE = "bf16-prefill-T8192-d2048-E64-f1024-k2"
 ZIPF_BETA = 0.4
 
-_TORCH = {"f32": torch.float32, "bf16": torch.bfloat16}
+_TORCH = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+_CODE = {"f32": _lib.QW_F32, "bf16": _lib.QW_BF16, "f16": _lib.QW_F16}
 
 
 def scaled(w: Workload, tokens: int | None = None, d_model: int | None = None, experts: int | None = None,
@@ -94,17 +95,18 @@ class Layer:
     extra: dict = field(default_factory=dict)
 
     def weight_args(self) -> list:
-        """Weight arguments of the C ABI; bf16 layers pass their QW_BF16T tiles when they have them."""
+        """Weight arguments of the C ABI; 16-bit layers pass their QW_BF16T / QW_F16T tiles when they have them."""
         if "tiles" in self.extra:
             g, u, d = self.extra["tiles"]
-            return [_lib.QW_BF16T, 0, 0, _hip.ptr(g), None, _hip.ptr(u), None, _hip.ptr(d), None]
+            code = _lib.QW_BF16T if self.fmt == _lib.QW_BF16 else _lib.QW_F16T
+            return [code, 0, 0, _hip.ptr(g), None, _hip.ptr(u), None, _hip.ptr(d), None]
         return [self.fmt, self.group_in, self.group_ff, _hip.ptr(self.gate), _hip.ptr(self.gate_s),
                 _hip.ptr(self.up), _hip.ptr(self.up_s), _hip.ptr(self.down), _hip.ptr(self.down_s)]
 
     def add_tiles(self) -> "Layer":
-        """Pack bf16 weights into QW_BF16T tiles (as the TopKMoE module does) and use them."""
+        """Pack 16-bit weights into QW_BF16T / QW_F16T tiles (as the TopKMoE module does) and use them."""
         from .moe import can_tile, tile_bf16
-        if self.fmt == _lib.QW_BF16 and all(can_tile(t) for t in (self.gate, self.up, self.down)):
+        if self.fmt in (_lib.QW_BF16, _lib.QW_F16) and all(can_tile(t) for t in (self.gate, self.up, self.down)):
             self.extra["tiles"] = (tile_bf16(self.gate), tile_bf16(self.up), tile_bf16(self.down))
         return self
 
@@ -150,10 +152,10 @@ def build_layer(w: Workload, device: torch.device | str = "cuda") -> Layer:
     up32 = normal(w.experts, w.d_ff, w.d_model)
     down32 = normal(w.experts, w.d_model, w.d_ff)
     layer: Layer
-    if w.weights in ("f32", "bf16"):
+    if w.weights in _TORCH:
         wt = _TORCH[w.weights]
-        layer = Layer(w, x, router, _lib.QW_F32 if wt == torch.float32 else _lib.QW_BF16,
-                      gate32.to(wt).contiguous(), up32.to(wt).contiguous(), down32.to(wt).contiguous())
+        layer = Layer(w, x, router, _CODE[w.weights], gate32.to(wt).contiguous(), up32.to(wt).contiguous(),
+                      down32.to(wt).contiguous())
     else:
         bits = 8 if w.weights == "i8" else 4
         g_in = w.group_size or (w.d_model if bits == 8 else 32)
@@ -178,7 +180,7 @@ class LayerRunner:
         self.capacity = w.capacity() if capacity is None else capacity
         T, E, K = w.tokens, w.experts, w.top_k
         R = T * K
-        self.act = _lib.QW_F32 if w.act == "f32" else _lib.QW_BF16
+        self.act = _CODE[w.act]
         self.out = torch.empty_like(layer.x)
         self.probs = torch.empty(T, E, dtype=torch.float32, device=dev)
         self.top_idx = torch.empty(T, K, dtype=torch.int32, device=dev)
@@ -232,7 +234,7 @@ class LayerRunner:
             "slot_weight": (slot_weight, torch.float32, (R,)),
             "route_slot": (route_slot, torch.int32, (R,)),
             "kept_offsets": (kept_offsets, torch.int32, (E + 1,)),
-            "y": (y, torch.float32 if self.act == _lib.QW_F32 else torch.bfloat16, (R, D)),
+            "y": (y, _TORCH[w.act], (R, D)),
         }
         start, dt, shape = views[name]
         n = 1
@@ -245,7 +247,8 @@ class LayerRunner:
 class DecodeRunner:
     """Preallocated buffers for repeated qw_moe_decode_step calls on one layer:
     `tokens` rows of fp32 normed input, the fp32 router (the layer's router
-    widened), the layer's experts in their stored format, bf16 compute."""
+    widened), the layer's experts in their stored format, compute in the
+    layer's activation dtype (bf16 or fp16)."""
 
     def __init__(self, layer: Layer, tokens: int = 1, seed: int = 0) -> None:
         w = layer.w
@@ -262,11 +265,12 @@ class DecodeRunner:
         self.probs = torch.empty(T, E, dtype=torch.float32, device=dev)
         self.top_idx = torch.empty(T, K, dtype=torch.int32, device=dev)
         self.top_w = torch.empty(T, K, dtype=torch.float32, device=dev)
-        self.ws_bytes = _lib.load().qw_moe_decode_step_workspace_bytes(T, w.d_model, E, K, w.d_ff, _lib.QW_BF16)
+        self.compute = _CODE[w.act] if w.act in ("bf16", "f16") else _lib.QW_BF16
+        self.ws_bytes = _lib.load().qw_moe_decode_step_workspace_bytes(T, w.d_model, E, K, w.d_ff, self.compute)
         self.ws = _hip.workspace(self.ws_bytes, dev)
         self._fn = _lib.load().qw_moe_decode_step
         self._head = [_hip.ptr(self.x), _hip.ptr(self.residual), T, w.d_model, _hip.ptr(self.router), 1.0,
-                      _hip.ptr(layer.bias), E, K, w.d_ff, _lib.QW_BF16, *layer.weight_args(), _hip.ptr(self.out),
+                      _hip.ptr(layer.bias), E, K, w.d_ff, self.compute, *layer.weight_args(), _hip.ptr(self.out),
                       _hip.ptr(self.probs), _hip.ptr(self.top_idx), _hip.ptr(self.top_w), _hip.ptr(self.ws),
                       self.ws_bytes]
 
@@ -292,7 +296,7 @@ def module_from_layer(layer: Layer):
         for e, expert in enumerate(moe.experts):
             for name in ("gate", "up", "down"):
                 stored = getattr(layer, name)[e]
-                if layer.fmt in (_lib.QW_F32, _lib.QW_BF16):
+                if layer.fmt in (_lib.QW_F32, _lib.QW_BF16, _lib.QW_F16):
                     getattr(expert, name).weight.copy_(stored)
                     continue
                 lin = getattr(expert, name)

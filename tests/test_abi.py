@@ -75,8 +75,8 @@ def test_workspace_sizes_are_positive_and_monotone():
 
 def test_decode_step_validation_and_workspace():
     lib = _lib.load()
-    # fp16 is not a compute dtype; top_k > experts; missing workspace
-    st = lib.qw_moe_decode_step(None, None, 1, 64, None, 1.0, None, 8, 2, 32, 5, _lib.QW_BF16, 0, 0,
+    # an unknown compute dtype (7); top_k > experts; missing workspace
+    st = lib.qw_moe_decode_step(None, None, 1, 64, None, 1.0, None, 8, 2, 32, 7, _lib.QW_BF16, 0, 0,
                                 None, None, None, None, None, None, None, None, None, None, None, 0, None)
     assert st == _lib.QW_ERR_INVALID and b"compute dtype" in lib.qw_last_error()
     st = lib.qw_moe_decode_step(None, None, 1, 64, None, 1.0, None, 8, 9, 32, _lib.QW_BF16, _lib.QW_BF16, 0, 0,

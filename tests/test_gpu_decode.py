@@ -18,7 +18,7 @@ from quantaweave_amd import _lib
 
 pytestmark = pytest.mark.gpu
 
-TOL = {"fp32": 1e-4, "bf16": 2e-2}
+TOL = {"fp32": 1e-4, "bf16": 2e-2, "fp16": 5e-3}
 
 
 def normwise(got, ref):
@@ -41,6 +41,8 @@ def make_moe(E, D, F_, k, fmt, seed, temperature=1.0, bias=False, group=None):
     moe = moe.cuda()
     if fmt == "bf16":
         moe.to(torch.bfloat16)
+    elif fmt == "f16":
+        moe.half()
     elif fmt in ("i8", "u4"):
         qa.quantize_model(moe, 8 if fmt == "i8" else 4, group)
     if bias:
@@ -51,13 +53,13 @@ def make_moe(E, D, F_, k, fmt, seed, temperature=1.0, bias=False, group=None):
 def oracle_weights(step):
     """The expert weights the step multiplies, as the oracle's weight dict."""
     p = step.pack
-    fmt = {_lib.QW_F32: "f32", _lib.QW_BF16: "bf16", _lib.QW_BF16T: "bf16", _lib.QW_I8: "i8",
-           _lib.QW_U4: "u4"}[p.fmt]
+    fmt = {_lib.QW_F32: "f32", _lib.QW_BF16: "bf16", _lib.QW_BF16T: "bf16", _lib.QW_F16: "f16",
+           _lib.QW_F16T: "f16", _lib.QW_I8: "i8", _lib.QW_U4: "u4"}[p.fmt]
     w = dict(format=fmt, d_model=step.hidden, d_ff=step.ffn, group_in=p.group_in, group_ff=p.group_ff)
     for name in ("gate", "up", "down"):
         t = getattr(p, name)
-        w[name] = t.float().cpu().numpy() if fmt in ("f32", "bf16") else t.cpu().numpy()
-        if p.fmt == _lib.QW_BF16T:
+        w[name] = t.float().cpu().numpy() if fmt in ("f32", "bf16", "f16") else t.cpu().numpy()
+        if p.fmt in (_lib.QW_BF16T, _lib.QW_F16T):
             w[name] = oracle.untile_bf16(w[name])
         s = getattr(p, name + "_s")
         if s is not None:
@@ -82,7 +84,7 @@ def check_step(moe, T, precision, seed=7):
     ref_scores = oracle.router_logits(xs, rw, step.temperature)
     assert np.abs(scores - ref_scores).max() <= 1e-5 * max(1.0, np.abs(ref_scores).max())
     bias = None if step.bias is None else step.bias.cpu().numpy()
-    dtype = "f32" if precision == "fp32" else "bf16"
+    dtype = {"fp32": "f32", "bf16": "bf16", "fp16": "f16"}[precision]
     res = oracle.decode_step(xs, rw, oracle_weights(step), top_k=step.top_k, dtype=dtype,
                              temperature=step.temperature, expert_bias=bias, logits=scores)
     # bit-exact routing given the scores
@@ -108,6 +110,12 @@ CASES = [
     (16, 1024, 352, 2, "u4", 32, 1, "bf16"),
     (16, 1024, 352, 3, "u4", 32, 4, "bf16"),
     (8, 96, 40, 2, "u4", 8, 1, "bf16"),
+    (16, 512, 256, 2, "f16", None, 1, "fp16"),
+    (16, 512, 256, 4, "f16", None, 5, "fp16"),
+    (8, 256, 384, 2, "f32", None, 3, "fp16"),
+    (16, 512, 256, 2, "bf16", None, 2, "fp16"),
+    (16, 512, 256, 2, "i8", None, 1, "fp16"),
+    (16, 1024, 352, 3, "u4", 32, 4, "fp16"),
 ]
 
 
@@ -116,11 +124,12 @@ def test_decode_step_matches_oracle(E, D, F_, k, fmt, group, T, precision):
     check_step(make_moe(E, D, F_, k, fmt, seed=E + D + T, group=group), T, precision)
 
 
+@pytest.mark.parametrize("precision", ["bf16", "fp16"])
 @pytest.mark.parametrize("fmt,D,F_,group", [("u4", 4096, 1408, 32), ("i8", 2048, 1024, None),
                                             ("bf16", 2048, 1024, None)])
-def test_decode_step_full_size(fmt, D, F_, group):
+def test_decode_step_full_size(fmt, D, F_, group, precision):
     """Batch-1 decode at the decode workloads' layer shapes (64 experts, top-2)."""
-    check_step(make_moe(64, D, F_, 2, fmt, seed=3, group=group), 1, "bf16")
+    check_step(make_moe(64, D, F_, 2, fmt, seed=3, group=group), 1, precision)
 
 
 @pytest.mark.parametrize("top_k,temperature,bias", [(1, 1.0, False), (2, 1.0, False), (2, 0.7, True), (3, 2.0, False)])

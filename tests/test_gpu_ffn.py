@@ -17,7 +17,8 @@ from tests import hipcall as H
 pytestmark = pytest.mark.gpu
 
 COUNTS = [0, 5, 37, 1, 0, 64, 33, 2]          # empty experts, partial tiles, exact multiples (tests/test_moe_kernels.py:24)
-TOL = {"f32": 1e-4, "bf16": 2e-2}
+TOL = {"f32": 1e-4, "bf16": 2e-2, "f16": 5e-3}
+TORCH_DT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
 
 
 def normwise(got, ref):
@@ -32,9 +33,8 @@ def make_weights(E, D, F_, fmt, seed, group=None, scale=0.05):
     u32 = (rng.randn(E, F_, D) * scale).astype(np.float32)
     d32 = (rng.randn(E, D, F_) * scale).astype(np.float32)
     w = dict(format=fmt, d_model=D, d_ff=F_)
-    if fmt in ("f32", "bf16"):
-        cast = oracle.round_bf16 if fmt == "bf16" else (lambda a: a)
-        w.update(gate=cast(g32), up=cast(u32), down=cast(d32))
+    if fmt in ("f32", "bf16", "f16"):
+        w.update(gate=oracle.round_act(g32, fmt), up=oracle.round_act(u32, fmt), down=oracle.round_act(d32, fmt))
         return w
     bits = 8 if fmt == "i8" else 4
     for name, arr in (("gate", g32), ("up", u32), ("down", d32)):
@@ -47,12 +47,12 @@ def make_weights(E, D, F_, fmt, seed, group=None, scale=0.05):
 
 def device_weights(w):
     fmt = w["format"]
-    code = {"f32": _lib.QW_F32, "bf16": _lib.QW_BF16, "i8": _lib.QW_I8, "u4": _lib.QW_U4}[fmt]
+    code = {"f32": _lib.QW_F32, "bf16": _lib.QW_BF16, "f16": _lib.QW_F16, "i8": _lib.QW_I8, "u4": _lib.QW_U4}[fmt]
     out = dict(fmt=code)
     for name in ("gate", "up", "down"):
         a = w[name]
-        if fmt == "bf16":
-            out[name] = H.dev(a, torch.bfloat16)
+        if fmt in ("bf16", "f16"):
+            out[name] = H.dev(a, TORCH_DT[fmt])
         else:
             out[name] = H.dev(a)
         if fmt in ("i8", "u4"):
@@ -64,8 +64,7 @@ def device_weights(w):
 
 def run_experts(x_np, counts, w, act, row_weight=None, row_index=None, x_rows=None, path="auto"):
     dw = device_weights(w)
-    tdt = torch.float32 if act == "f32" else torch.bfloat16
-    x = H.dev(x_np, tdt)
+    x = H.dev(x_np, TORCH_DT[act])
     offsets = H.dev(np.concatenate([[0], np.cumsum(counts)]).astype(np.int32))
     y = H.experts(x, offsets, dw["fmt"], dw["gate"], dw["up"], dw["down"], dw.get("gate_s"), dw.get("up_s"),
                   dw.get("down_s"), dw.get("group_in", 0), dw.get("group_ff", 0),
@@ -79,6 +78,9 @@ CASES = [
     ("f32", "f32", 48, 80, None), ("f32", "f32", 33, 17, None), ("bf16", "bf16", 64, 96, None),
     ("bf16", "bf16", 256, 512, None), ("bf16", "i8", 64, 96, None), ("bf16", "i8", 40, 24, 16),
     ("bf16", "u4", 64, 96, None), ("bf16", "u4", 40, 24, 16), ("f32", "i8", 64, 64, None), ("f32", "u4", 64, 64, 32),
+    ("f16", "f16", 64, 96, None), ("f16", "f16", 256, 512, None), ("f16", "i8", 64, 96, None),
+    ("f16", "u4", 40, 24, 16), ("f16", "f32", 48, 80, None), ("f16", "bf16", 64, 96, None),
+    ("bf16", "f16", 64, 96, None), ("f32", "f16", 48, 80, None),
 ]
 
 
@@ -89,8 +91,7 @@ def test_grouped_swiglu_matches_oracle(act, fmt, D, F_, group, path):
     rng = np.random.RandomState(D + F_)
     rows = sum(COUNTS)
     x = rng.randn(rows, D).astype(np.float32)
-    if act == "bf16":
-        x = oracle.round_bf16(x)
+    x = oracle.round_act(x, act)
     w = make_weights(len(COUNTS), D, F_, fmt, D * F_, group)
     rw = rng.rand(rows).astype(np.float32)
     got = run_experts(x, COUNTS, w, act, row_weight=rw, path=path)
@@ -103,7 +104,9 @@ def test_grouped_swiglu_matches_oracle(act, fmt, D, F_, group, path):
     ("bf16", "bf16", None, "mfma"), ("bf16", "bf16", None, "stream"), ("bf16", "bf16", None, "generic"),
     ("bf16", "i8", None, "stream"), ("bf16", "i8", None, "generic"), ("bf16", "u4", 32, "stream"),
     ("bf16", "u4", 32, "generic"), ("f32", "f32", None, "generic"), ("f32", "f32", None, "mfma"),
-    ("bf16", "i8", None, "mfma"), ("bf16", "i8", 64, "mfma"), ("bf16", "u4", 32, "mfma"), ("bf16", "u4", 128, "mfma")])
+    ("bf16", "i8", None, "mfma"), ("bf16", "i8", 64, "mfma"), ("bf16", "u4", 32, "mfma"), ("bf16", "u4", 128, "mfma"),
+    ("f16", "f16", None, "mfma"), ("f16", "f16", None, "stream"), ("f16", "f16", None, "generic"),
+    ("f16", "i8", None, "mfma"), ("f16", "u4", 32, "mfma"), ("f16", "i8", None, "stream"), ("f16", "u4", 32, "stream")])
 def test_each_kernel_family_matches_oracle(act, fmt, group, path):
     """The same inputs through every kernel family that takes them
     (qw_moe_experts_on_path), each against the oracle."""
@@ -127,29 +130,30 @@ def test_kernel_family_that_does_not_take_the_format_refuses():
         run_experts(x, COUNTS, w, "bf16", path="mfma")
 
 
-@pytest.mark.parametrize("fmt,group,D,F_,counts", [
-    ("i8", None, 512, 256, [300, 0, 17, 64, 320, 1]), ("i8", 64, 512, 256, [300, 0, 17, 64, 320, 1]),
-    ("u4", 32, 512, 256, [300, 0, 17, 64, 320, 1]), ("u4", 128, 256, 512, [40, 200, 3]),
-    ("i8", None, 2048, 1024, [256, 250, 262, 241]), ("u4", 32, 2048, 1024, [256, 250, 262, 241])])
-def test_quantised_mfma_equals_bf16_mfma_of_dequantised_weights(fmt, group, D, F_, counts):
+@pytest.mark.parametrize("act,fmt,group,D,F_,counts", [
+    ("bf16", "i8", None, 512, 256, [300, 0, 17, 64, 320, 1]), ("bf16", "i8", 64, 512, 256, [300, 0, 17, 64, 320, 1]),
+    ("bf16", "u4", 32, 512, 256, [300, 0, 17, 64, 320, 1]), ("bf16", "u4", 128, 256, 512, [40, 200, 3]),
+    ("bf16", "i8", None, 2048, 1024, [256, 250, 262, 241]), ("bf16", "u4", 32, 2048, 1024, [256, 250, 262, 241]),
+    ("f16", "i8", None, 512, 256, [300, 0, 17, 64, 320, 1]), ("f16", "u4", 32, 2048, 1024, [256, 250, 262, 241])])
+def test_quantised_mfma_equals_bf16_mfma_of_dequantised_weights(act, fmt, group, D, F_, counts):
     """The matrix-core path dequantises each weight to bf16(q * scale), the
     reference's dequantize().to(bfloat16) (src/quantization.py:61-72), and then
     runs the bf16 kernel's MFMA sequence: its outputs equal, bit for bit, those
-    of the bf16 path given the dequantised weights."""
-    print(f"case quantised mfma fmt={fmt} group={group} D={D} F={F_} counts={counts}", flush=True)
+    of the bf16 path given the dequantised weights.  The same for fp16."""
+    print(f"case quantised mfma act={act} fmt={fmt} group={group} D={D} F={F_} counts={counts}", flush=True)
     rng = np.random.RandomState(D + len(counts))
     rows = sum(counts)
-    x = oracle.round_bf16(rng.randn(rows, D).astype(np.float32))
+    x = oracle.round_act(rng.randn(rows, D).astype(np.float32), act)
     w = make_weights(len(counts), D, F_, fmt, 5, group)
-    deq = dict(format="bf16", d_model=D, d_ff=F_)
+    deq = dict(format=act, d_model=D, d_ff=F_)
     for name, gname in (("gate", "group_in"), ("up", "group_in"), ("down", "group_ff")):
         cols = F_ if name == "down" else D
-        deq[name] = oracle.round_bf16(np.stack([
+        deq[name] = oracle.round_act(np.stack([
             oracle.dequantize(w[name][e], w[name + "_scales"][e], 8 if fmt == "i8" else 4, cols, w[gname])
-            for e in range(len(counts))]))
+            for e in range(len(counts))]), act)
     rw = rng.rand(rows).astype(np.float32)
-    got = run_experts(x, counts, w, "bf16", row_weight=rw, path="mfma")
-    ref = run_experts(x, counts, deq, "bf16", row_weight=rw, path="mfma")
+    got = run_experts(x, counts, w, act, row_weight=rw, path="mfma")
+    ref = run_experts(x, counts, deq, act, row_weight=rw, path="mfma")
     assert np.array_equal(got.view(np.int32), ref.view(np.int32))
 
 
@@ -195,6 +199,23 @@ def test_grouped_matmul_bf16_is_close_and_all_empty_plan_is_safe():
     assert (y.double() - expected).abs().max() < 0.25 and y.dtype == torch.bfloat16
     empty = mk.grouped_matmul(torch.empty(0, 64, device="cuda"), weight.float(), mk.GroupedPlan([0] * len(COUNTS), x.device))
     assert empty.shape == (0, 96)
+
+
+@pytest.mark.parametrize("in_features", [128, 40])
+def test_grouped_matmul_f16_matches_per_expert_matmuls(in_features):
+    """fp16 operands: the matrix-core GEMM (in_features % 64 == 0) or the
+    general kernel, fp32 accumulation, one rounding to fp16."""
+    torch.manual_seed(3)
+    x = torch.randn(sum(COUNTS), in_features, device="cuda").half()
+    weight = (torch.randn(len(COUNTS), 96, in_features, device="cuda") * 0.1).half()
+    y = mk.grouped_matmul(x, weight, mk.GroupedPlan(COUNTS, x.device))
+    assert y.dtype == torch.float16
+    parts, start = [], 0
+    for e, c in enumerate(COUNTS):
+        parts.append(x[start:start + c].double() @ weight[e].double().t())
+        start += c
+    expected = torch.cat(parts)
+    assert normwise(y.double().cpu().numpy(), expected.cpu().numpy()) <= 2e-3
 
 
 def test_grouped_swiglu_api_matches_oracle_over_real_experts():
@@ -246,14 +267,16 @@ def test_quantized_linear_forward(bits, group, max_rel):
     torch.manual_seed(0)
     lin = torch.nn.Linear(40, 24, bias=False).cuda()
     q = qa.QuantizedLinear.from_linear(lin, bits, group)
-    for dtype, tol in ((torch.float32, 1e-5), (torch.bfloat16, 2e-2)):
+    for dtype, tol in ((torch.float32, 1e-5), (torch.bfloat16, 2e-2), (torch.float16, 5e-3)):
+        name = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}[dtype]
         x = torch.randn(5, 40, device="cuda").to(dtype)
         got = q(x).float().cpu().numpy()
-        deq = oracle.round_act(q.dequantize().cpu().numpy(), "bf16" if dtype == torch.bfloat16 else "f32")
-        ref = oracle.linear(x.float().cpu().numpy(), deq, "bf16" if dtype == torch.bfloat16 else "f32")
+        assert q(x).dtype == dtype
+        deq = oracle.round_act(q.dequantize().cpu().numpy(), name)
+        ref = oracle.linear(x.float().cpu().numpy(), deq, name)
         assert normwise(got, ref) <= tol
         err = np.linalg.norm(got - (x.float() @ lin.weight.T).detach().cpu().numpy()) / np.linalg.norm(ref)
-        assert err < max_rel + (0.02 if dtype == torch.bfloat16 else 0)
+        assert err < max_rel + (0.02 if dtype != torch.float32 else 0)
     assert q.stored_bytes() < lin.weight.numel() * 4 / (3.5 if bits == 8 else 4)
 
 

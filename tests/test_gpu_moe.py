@@ -16,7 +16,7 @@ from quantaweave_amd import workloads as W
 
 pytestmark = pytest.mark.gpu
 
-TOL = {"f32": 1e-4, "bf16": 2e-2}
+TOL = {"f32": 1e-4, "bf16": 2e-2, "f16": 5e-3}
 
 
 def normwise(got, ref):
@@ -29,7 +29,7 @@ def normwise(got, ref):
 # of the normwise tolerance times the output's largest magnitude (below it, a
 # sum whose terms cancel has no relative accuracy to speak of in bf16): a
 # second view of the same outputs next to the normwise bound.
-P999 = {"f32": 1e-3, "bf16": 0.5}
+P999 = {"f32": 1e-3, "bf16": 0.5, "f16": 0.1}
 
 
 def elementwise_p999(got, ref, dtype):
@@ -45,7 +45,7 @@ def host_weights(layer):
     out = dict(format=fmt, d_model=w.d_model, d_ff=w.d_ff, group_in=layer.group_in, group_ff=layer.group_ff)
     for name in ("gate", "up", "down"):
         t = getattr(layer, name)
-        out[name] = t.float().cpu().numpy() if fmt in ("f32", "bf16") else t.cpu().numpy()
+        out[name] = t.float().cpu().numpy() if fmt in ("f32", "bf16", "f16") else t.cpu().numpy()
         s = getattr(layer, name + "_s")
         if s is not None:
             out[name + "_scales"] = s.cpu().numpy()
@@ -123,6 +123,34 @@ def test_layer_matches_oracle_full_size_tiled(name):
     """The weights in the QW_BF16T tiles the module (and the benchmark) uses:
     the exact kernel instantiations behind the benchmark figures."""
     check_layer(W.WORKLOADS[name], tiles=True)
+
+
+def f16_workload(name: str, **sizes) -> W.Workload:
+    """A workload with fp16 activations (and fp16 weights where it has 16-bit ones)."""
+    base = W.WORKLOADS[name]
+    small = W.scaled(base, **sizes) if sizes else base
+    return W.Workload(small.name.replace("bf16", "f16") + "-f16", small.tokens, small.d_model, small.experts,
+                      small.d_ff, small.top_k, small.capacity_factor, "f16",
+                      "f16" if small.weights == "bf16" else small.weights, small.seed, small.group_size, small.zipf)
+
+
+F16_CASES = [
+    (f16_workload("bf16-prefill-T8192-d2048-E64-f1024-k2", tokens=1024, d_model=512, d_ff=256), False),
+    (f16_workload("bf16-prefill-T8192-d2048-E64-f1024-k2"), False),
+    (f16_workload("bf16-prefill-T8192-d2048-E64-f1024-k2"), True),
+    (f16_workload("int8-decode-T64-d2048-E64-f1024-k2"), False),
+    (f16_workload("int4-decode-T16-d4096-E64-f1408-k2"), False),
+    (f16_workload("int4-prefill-T8192-d2048-E64-f1024-k2", tokens=2048, d_model=512, d_ff=256, experts=8), False),
+    (f16_workload("skewed-T4096-d2048-E64-f1024-k2", tokens=1024, d_model=512, d_ff=256), True),
+]
+
+
+@pytest.mark.parametrize("workload,tiles", F16_CASES, ids=lambda v: v.name if hasattr(v, "name") else str(v))
+def test_layer_matches_oracle_f16(workload, tiles):
+    """fp16 activations and weights (the reference's fp16 precision): the
+    matrix-core, weight-streaming and quantised paths in fp16 against the
+    oracle with fp16 rounding points."""
+    check_layer(workload, tiles=tiles)
 
 
 def test_layer_is_deterministic_across_calls():
@@ -355,6 +383,26 @@ def test_loop_executor_selected_by_set_moe_kernel():
     assert normwise(looped.float().cpu().numpy(), grouped.float().cpu().numpy()) <= 1e-2
 
 
+def test_half_module_matches_oracle():
+    """A TopKMoE in fp16 (`model.half()`): router, experts and hidden states in
+    fp16; the experts packed into QW_F16T tiles; routing in fp32."""
+    moe = bf16_module().half()
+    hidden = torch.randn(2, 160, 256, device="cuda").half()
+    with torch.no_grad():
+        out, _, dropped, overflow, _ = moe(hidden)
+    assert out.dtype == torch.float16
+    from quantaweave_amd import _lib
+    assert moe._qw_pack.fmt == _lib.QW_F16T
+    flat = hidden.reshape(-1, 256).float().cpu().numpy()
+    w = bf16_module_weights(moe)
+    w["format"] = "f16"
+    ref = oracle.moe_forward(flat, moe.router.weight.detach().float().cpu().numpy(), w, top_k=2,
+                             cap=moe.capacity(320), dtype="f16")
+    assert np.array_equal(moe.last_top_indices.cpu().numpy(), ref["top_idx"])
+    assert int(overflow) == int(ref["plan"]["totals"][1])
+    assert normwise(out.reshape(-1, 256).float().cpu().numpy(), ref["out"]) <= TOL["f16"]
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
 def test_static_dispatch_matches_the_reference_static_output(dtype):
     """TopKMoE._static_output (src/quantweave_moe_model.py:235-245): capacity
@@ -387,8 +435,9 @@ def test_static_dispatch_matches_the_reference_static_output(dtype):
         assert normwise(got, dynamic.reshape(-1, 256).float().cpu().numpy()) <= 1e-2
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("k", [2, 3, 4])
-def test_combine_is_bit_exact_against_the_oracle(k):
+def test_combine_is_bit_exact_against_the_oracle(k, dt):
     """qw_moe_combine_weighted from bf16 expert rows: torch's index_add_ rule
     (fp32 sum in plan order, one rounding) bit for bit, also at k >= 3 where a
     rounding per add would differ; and the static-dispatch combine."""
@@ -399,15 +448,16 @@ def test_combine_is_bit_exact_against_the_oracle(k):
     _, idx, w = oracle.route_from_logits((torch.randn(T, E, generator=g) * 2).numpy(), k)
     p = oracle.plan(idx, w, E, oracle.capacity(T, k, E, 1.0))
     n = len(p["slot_token"])
-    y = oracle.round_bf16((torch.randn(n, D, generator=g) * torch.logspace(-3, 3, D)[None]).numpy())
-    yd = torch.from_numpy(y).cuda().bfloat16()
+    tdt, code = (torch.bfloat16, _lib.QW_BF16) if dt == "bf16" else (torch.float16, _lib.QW_F16)
+    y = oracle.round_act((torch.randn(n, D, generator=g) * torch.logspace(-3, 3, D)[None]).numpy(), dt)
+    yd = torch.from_numpy(y).cuda().to(tdt)
     slot = torch.from_numpy(p["route_slot"]).cuda()
     tidx = torch.from_numpy(idx).cuda()
     tw = torch.from_numpy(w).cuda()
-    for fn, ref in (("qw_moe_combine_weighted", oracle.combine(y, p["slot_token"], p["slot_weight"], T, "bf16")),
-                    ("qw_moe_combine_static", oracle.combine_static(y, p["slot_token"], p["slot_weight"], T, "bf16"))):
-        out = torch.empty(T, D, dtype=torch.bfloat16, device="cuda")
-        _lib.call(fn, _hip.ptr(yd), _lib.QW_BF16, _hip.ptr(slot), _hip.ptr(tidx), _hip.ptr(tw), T, k, D, _hip.ptr(out),
-                  _lib.QW_BF16, _hip.stream(out.device))
+    for fn, ref in (("qw_moe_combine_weighted", oracle.combine(y, p["slot_token"], p["slot_weight"], T, dt)),
+                    ("qw_moe_combine_static", oracle.combine_static(y, p["slot_token"], p["slot_weight"], T, dt))):
+        out = torch.empty(T, D, dtype=tdt, device="cuda")
+        _lib.call(fn, _hip.ptr(yd), code, _hip.ptr(slot), _hip.ptr(tidx), _hip.ptr(tw), T, k, D, _hip.ptr(out),
+                  code, _hip.stream(out.device))
         torch.cuda.synchronize()
         assert np.array_equal(out.float().cpu().numpy(), ref), fn

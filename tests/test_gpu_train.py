@@ -278,6 +278,46 @@ def test_layer_under_bf16_autocast():
         assert normwise(got, want) <= 3e-2
 
 
+def test_layer_under_f16_autocast():
+    """The same under fp16 autocast (the reference's --precision fp16 training,
+    src/train_quantweave_moe.py:598-600): expert rows and weights in fp16,
+    routing and the weighted sum in fp32."""
+    print("case layer f16 autocast", flush=True)
+    moe = make_moe(16, 128, 256, 2, 1.25, seed=13)
+    x = torch.randn(2, 64, 128, device="cuda", requires_grad=True)
+    with torch.autocast("cuda", dtype=torch.float16):
+        out, balance, *_ = moe(x)
+    assert out.dtype == torch.float32
+    (out.square().sum() + balance).backward()
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.float16):
+        infer = moe(x)[0]
+    assert torch.equal(infer, out.detach())
+    ref, probs, bal, xr, rw, ws, _ = layer_reference(moe, x)
+    (ref.square().sum() + bal).backward()
+    assert normwise(out, ref) <= 5e-3
+    assert x.grad.dtype == torch.float32
+    for got, want in ((x.grad, xr.grad), (moe.router.weight.grad, rw.grad),
+                      (torch.stack([e.down.weight.grad for e in moe.experts]), ws[2].grad)):
+        assert normwise(got, want) <= 1e-2
+
+
+def test_grouped_swiglu_under_f16_autocast():
+    print("case grouped_swiglu f16 autocast", flush=True)
+    moe = make_moe(len(COUNTS), 64, 128, 1, seed=6)
+    x = torch.randn(sum(COUNTS), 64, device="cuda", requires_grad=True)
+    with torch.autocast("cuda", dtype=torch.float16):
+        out = mk.grouped_swiglu(x, moe.experts, COUNTS)
+    assert out.dtype == torch.float16
+    out.float().square().sum().backward()
+    xr = cpu64(x).requires_grad_()
+    ws = [w.requires_grad_() for w in stacks(moe)]
+    ref = tr.grouped_swiglu(xr, *ws, COUNTS)
+    ref.square().sum().backward()
+    assert (cpu64(out) - ref.detach()).abs().max() / ref.detach().abs().max() < 5e-3
+    err = (cpu64(x.grad) - xr.grad).abs().max() / xr.grad.abs().max()
+    assert err < 1e-2
+
+
 def test_kernel_benchmark_reports_forward_and_backward():
     # tests/test_moe_kernels.py:113-116
     result = mk.benchmark(experts=16, tokens=2048, hidden=64, ffn=128, repeats=3)
@@ -286,19 +326,21 @@ def test_kernel_benchmark_reports_forward_and_backward():
     assert result["hip_ms"] > 0 and result["bf16"]
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("counts,in_features,out_features", [
     ([0, 5, 300, 1, 0, 129, 64, 2], 128, 192),     # matrix cores for dX (192 % 64 == 0) and dW
     ([7, 0, 200, 33], 320, 96),                    # dX on the vector ALUs (96 % 64 != 0), dW on the matrix cores
     ([1000, 24], 64, 2048),                        # many row tiles, many column tiles
 ])
-def test_grouped_matmul_bf16_matrix_core_paths(counts, in_features, out_features):
-    print(f"case grouped_matmul bf16 {counts} {in_features}x{out_features}", flush=True)
+def test_grouped_matmul_half_matrix_core_paths(counts, in_features, out_features, dtype):
+    print(f"case grouped_matmul {dtype} {counts} {in_features}x{out_features}", flush=True)
     g = torch.Generator(device="cuda").manual_seed(sum(counts))
-    x = torch.randn(sum(counts), in_features, device="cuda", generator=g).bfloat16().requires_grad_()
-    weight = (torch.randn(len(counts), out_features, in_features, device="cuda", generator=g) * 0.1).bfloat16()
+    x = torch.randn(sum(counts), in_features, device="cuda", generator=g).to(dtype).requires_grad_()
+    weight = (torch.randn(len(counts), out_features, in_features, device="cuda", generator=g) * 0.1).to(dtype)
     weight.requires_grad_()
     y = mk.grouped_matmul(x, weight, mk.GroupedPlan(counts, x.device))
-    upstream = torch.randn(y.shape, device="cuda", generator=g).bfloat16()
+    assert y.dtype == dtype
+    upstream = torch.randn(y.shape, device="cuda", generator=g).to(dtype)
     y.backward(upstream)
     xr, wr = cpu64(x).requires_grad_(), cpu64(weight).requires_grad_()
     ref = tr.grouped_matmul(xr, wr, counts)

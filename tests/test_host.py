@@ -94,12 +94,15 @@ def test_compute_dtype_rule():
         assert mk.compute_dtype(x) == torch.bfloat16
 
 
-def test_decode_step_refuses_cpu_and_fp16():
+def test_decode_step_refuses_cpu_and_names_precisions():
     moe = qa.TopKMoE(small_config())
     with pytest.raises(RuntimeError, match="ROCm"):
         qa.MoEDecodeStep(moe, device=torch.device("cpu"))
     from quantaweave_amd.decode import precision_dtype
+    # src/fast_decode.py:75-78
     assert precision_dtype(torch.device("cuda"), "auto") == torch.bfloat16
     assert precision_dtype(torch.device("cpu"), "auto") == torch.float32
-    with pytest.raises(ValueError, match="fp16"):
-        precision_dtype(torch.device("cuda"), "fp16")
+    assert precision_dtype(torch.device("cuda"), "fp16") == torch.float16
+    assert precision_dtype(torch.device("cuda"), "fp32") == torch.float32
+    with pytest.raises(KeyError):
+        precision_dtype(torch.device("cuda"), "fp8")

@@ -305,6 +305,32 @@ def test_round_bf16_matches_torch():
     assert np.array_equal(oracle.round_bf16(v), torch.from_numpy(v).bfloat16().float().numpy())
 
 
+def test_round_f16_matches_torch_on_ties_overflow_and_subnormals():
+    rng = np.random.RandomState(3)
+    v = (rng.randn(20000) * np.exp(rng.uniform(-20, 12, 20000))).astype(np.float32)
+    ties = (np.arange(1, 2049, dtype=np.float32) + 0.5) * np.float32(2.0 ** -10)   # halfway between fp16 neighbours
+    edge = np.array([65504.0, 65519.99, 65520.0, 1e6, -1e6, 6e-8, 3e-8, 2.98e-8, 6.1e-5, 0.0, -0.0, np.inf, -np.inf],
+                    np.float32)
+    v = np.concatenate([v, ties, -ties, edge])
+    ref = torch.from_numpy(v).half().float().numpy()
+    got = oracle.round_f16(v)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    assert np.isnan(oracle.round_f16(np.array([np.nan], np.float32))).all()
+    # the ties go to the even neighbour: 1 + 0.5*2^-10 -> 1, 1 + 1.5*2^-10 -> 1 + 2*2^-10
+    assert oracle.round_f16(np.float32(1 + 2.0 ** -11)) == 1.0
+    assert oracle.round_f16(np.float32(1 + 3 * 2.0 ** -11)) == np.float32(1 + 2.0 ** -9)
+
+
+def test_swiglu_f16_matches_torch_f16_module():
+    """The reference's rounding points in fp16 (src/moe_kernels.py:194, torch's CPU fp16 ops)."""
+    torch.manual_seed(16)
+    x = torch.randn(9, 64).half()
+    g, u, d = (torch.randn(48, 64) * 0.1).half(), (torch.randn(48, 64) * 0.1).half(), (torch.randn(64, 48) * 0.1).half()
+    ref = F.linear(F.silu(F.linear(x, g)) * F.linear(x, u), d).float()
+    got = oracle.swiglu(x.float().numpy(), g.float().numpy(), u.float().numpy(), d.float().numpy(), "f16")
+    assert np.abs(got - ref.numpy()).max() <= 2e-3 * np.abs(ref.numpy()).max()
+
+
 def reference_moe(x, router_w, w, top_k, capacity):
     """Straightforward per-expert loop (tests/test_model_features.py:21-35), fp32 torch."""
     flat = torch.from_numpy(x)
@@ -556,8 +582,9 @@ def test_routing_and_plan_equal_torchs_composition_on_the_same_logits(name):
 
 
 # ---------------------------------------------------------------- combine vs torch's index_add_
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("k", [2, 3, 4])
-def test_bf16_combine_equals_torch_index_add(k):
+def test_half_combine_equals_torch_index_add(k, dt):
     """oracle.combine against the reference's last two lines
     (src/quantweave_moe_model.py:200-201) run by torch: bf16 expert rows times
     fp32 route weights, cast to bf16, index_add_ into bf16 zeros in plan order.
@@ -569,17 +596,18 @@ def test_bf16_combine_equals_torch_index_add(k):
     _, idx, w = oracle.route_from_logits(logits.numpy(), k)
     p = oracle.plan(idx, w, E, T * k)
     n = len(p["slot_token"])
-    y = (torch.randn(n, D, generator=g) * torch.logspace(-3, 3, D)[None]).to(torch.bfloat16)
+    name = "bf16" if dt == torch.bfloat16 else "f16"
+    y = (torch.randn(n, D, generator=g) * torch.logspace(-3, 3, D)[None]).to(dt)
     tokens = torch.from_numpy(p["slot_token"].astype(np.int64))
     weights = torch.from_numpy(p["slot_weight"])
-    ref = torch.zeros(T, D, dtype=torch.bfloat16).index_add_(0, tokens, (y * weights[:, None]).to(torch.bfloat16))
-    got = oracle.combine(y.float().numpy(), p["slot_token"], p["slot_weight"], T, "bf16")
+    ref = torch.zeros(T, D, dtype=dt).index_add_(0, tokens, (y * weights[:, None]).to(dt))
+    got = oracle.combine(y.float().numpy(), p["slot_token"], p["slot_weight"], T, name)
     assert np.array_equal(got, ref.float().numpy())
     # the per-add rule, for contrast
-    contrib = oracle.round_bf16(y.float().numpy() * p["slot_weight"][:, None])
+    contrib = oracle.round_act(y.float().numpy() * p["slot_weight"][:, None], name)
     per_add = np.zeros((T, D), np.float32)
     for s, t in enumerate(p["slot_token"].tolist()):
-        per_add[t] = oracle.round_bf16(per_add[t] + contrib[s])
+        per_add[t] = oracle.round_act(per_add[t] + contrib[s], name)
     if k == 2:
         assert np.array_equal(per_add, got)
     else:
@@ -598,7 +626,7 @@ def test_fp32_combine_equals_torch_index_add():
     assert np.array_equal(got, ref.numpy())
 
 
-@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
 def test_static_combine_equals_torchs_static_output(dt):
     """oracle.combine_static against the loop of TopKMoE._static_output
     (src/quantweave_moe_model.py:240-245) run by torch: every expert's output
@@ -617,7 +645,8 @@ def test_static_combine_equals_torchs_static_output(dt):
     p = oracle.plan(idx, w, E, T * k)
     rows = np.stack([dense_y[e, t].float().numpy() for e in range(E) for t in p["slot_token"][
         p["kept_offsets"][e]:p["kept_offsets"][e + 1]]])
-    got = oracle.combine_static(rows, p["slot_token"], p["slot_weight"], T, "bf16" if dt == torch.bfloat16 else "f32")
+    got = oracle.combine_static(rows, p["slot_token"], p["slot_weight"], T,
+                                {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}[dt])
     assert np.array_equal(got, ref.float().numpy())
     if dt == torch.float32:  # in fp32 the static and dynamic accumulations agree (src: tests/test_model_features.py:49-56)
         assert np.array_equal(got, oracle.combine(rows, p["slot_token"], p["slot_weight"], T, "f32"))
