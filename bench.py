@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--workload", default=None)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only-headline", action="store_true")
+    ap.add_argument("--decode-steps-only", action="store_true",
+                    help="only time the batch-1 decode steps (one JSON line with their figures)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (calibrates HBM byte counters)")
     return ap.parse_args()
@@ -326,6 +328,13 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": n, "launches": 3}), flush=True)
+        return
+    if args.decode_steps_only:
+        decode = {}
+        for name in DECODE_SHAPES:
+            r = measure_decode(name, args.steps, args.warmup)
+            decode[r.pop("shape")] = r
+        print(json.dumps({"decode_step": decode}), flush=True)
         return
     head = args.workload or W.HEADLINE
     results = {}
