@@ -371,7 +371,7 @@ def main():
             expert_stage_tflops=round(r["flops"] / (te / 1000) / 1e12, 2),
             expert_stage_gbs=round(r["stage_bytes"] / (te / 1000) / 1e9, 1),
             hbm_frac=round(r["stage_bytes"] / (te / 1000) / 1e9 / HBM_PEAK_GBS, 4),
-            mfma_frac=round(r["flops"] / (te / 1000) / 1e12 / BF16_PEAK_TFLOPS, 4) if ww.act == "bf16" else None,
+            mfma_frac=round(r["flops"] / (te / 1000) / 1e12 / BF16_PEAK_TFLOPS, 4) if ww.act in ("bf16", "f16") else None,
             experts_cold_ms={k: round(v, 4) for k, v in r["experts_cold"].items()},
             hbm_frac_cold=round(r["stage_bytes"] / (tc / 1000) / 1e9 / HBM_PEAK_GBS, 4),
         )
@@ -401,7 +401,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if w.act == "bf16" else "f32",
+        "dtype": w.act,
         "data": "synthetic (N(0,1) activations, N(0,0.02) weights, fixed seed)",
         "config": {"workload": head, "tokens": w.tokens, "d_model": w.d_model, "experts": w.experts, "d_ff": w.d_ff,
                    "top_k": w.top_k, "capacity_factor": w.capacity_factor, "weights": w.weights, "seed": w.seed},

@@ -44,7 +44,7 @@ class Experts:
 
     def _linear(self, x: torch.Tensor, which: int, e: int, in_features: int) -> torch.Tensor:
         w = self.w[which][e]
-        if self.fmt in ("f32", "bf16"):
+        if self.fmt in ("f32", "bf16", "f16"):
             return F.linear(x, w)
         bits = 8 if self.fmt == "i8" else 4
         return F.linear(x, dequantize(w, self.s[which][e], bits, in_features).to(x.dtype))

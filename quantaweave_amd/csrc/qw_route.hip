@@ -147,12 +147,25 @@ __global__ __launch_bounds__(256) void router_gemv_kernel(const void* __restrict
   }
 }
 
-// bf16 x bf16 router GEMM on MFMA (products of bf16 values are exact in fp32,
-// so this is the same fp32 dot product up to accumulation order).  Tile: 64
-// tokens x 64 experts per 256-thread block; wave w owns tokens w*16..w*16+15.
-typedef __bf16 rbf16x8 __attribute__((ext_vector_type(8)));
+// bf16 x bf16 (or fp16 x fp16) router GEMM on MFMA (products of bf16 or fp16
+// values are exact in fp32, so this is the same fp32 dot product up to
+// accumulation order).  Tile: 64 tokens x 64 experts per 256-thread block;
+// wave w owns tokens w*16..w*16+15.
+typedef __bf16 rbf16x8 __attribute__((ext_vector_type(8)));  // 16-bit operands (bf16 or fp16 bits)
+typedef _Float16 rf16x8 __attribute__((ext_vector_type(8)));
 typedef float rf32x4 __attribute__((ext_vector_type(4)));
 
+// One 16x16x32 MFMA step on operands of the 16-bit type DT.
+template <int DT>
+__device__ __forceinline__ rf32x4 rmfma(rbf16x8 a, rbf16x8 b, rf32x4 c) {
+  if constexpr (DT == QW_F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(rf16x8, a), __builtin_bit_cast(rf16x8, b), c, 0,
+                                                   0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+template <int DT>
 __global__ __launch_bounds__(256) void router_mfma_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
                                                           const uint16_t* __restrict__ w, int T, int D, int E,
                                                           int k_len, float* __restrict__ partial) {
@@ -207,7 +220,7 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const uint16_t* __rest
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const rbf16x8 bfr = *reinterpret_cast<const rbf16x8*>(&Bs[(t * 16 + l16) * LROW + ks * 32 + kq]);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr, bfr, acc[t], 0, 0, 0);
+        acc[t] = rmfma<DT>(afr, bfr, acc[t]);
       }
     }
     __syncthreads();
@@ -445,10 +458,10 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
 }
 
 // ---------------------------------------------------------------------------
-// Router logits and routing in one kernel (bf16 x and weights, E <= 64,
+// Router logits and routing in one kernel (bf16, or fp16, x and weights, E <= 64,
 // D % 64 == 0): 32 tokens per 512-thread block.  Wave w multiplies the
 // block's token rows by the E router rows over the 64-wide k chunks
-// w, w + 8, w + 16, ... with bf16 MFMA (fp32 accumulation; operands go from
+// w, w + 8, w + 16, ... with bf16 (fp16) MFMA (fp32 accumulation; operands go from
 // global memory straight into registers, one chunk in flight while the
 // previous is multiplied), the eight partial sums meet in LDS and are added in
 // wave order, L = (((p_0 + p_1) + ...) + p_7) / temperature, and wave w then
@@ -458,6 +471,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
 constexpr int kFuseTokens = 32, kFuseWaves = 8, kFuseChunk = 64, kFuseSteps = kFuseChunk / 32;
 constexpr int kFusePitch = 68;  // LDS row pitch in floats: the partial stores of a wave hit 64 distinct banks
 
+template <int DT>
 __global__ __launch_bounds__(kFuseWaves * kWave) void router_topk_kernel(
     const uint16_t* __restrict__ x, int64_t x_stride, const uint16_t* __restrict__ w, int T, int D, int E, int K,
     float temperature, const float* __restrict__ bias, int select_logits, float* __restrict__ logits,
@@ -497,8 +511,7 @@ __global__ __launch_bounds__(kFuseWaves * kWave) void router_topk_kernel(
       _Pragma("unroll") for (int m = 0; m < 2; ++m) {                                        \
         const rbf16x8 af = __builtin_bit_cast(rbf16x8, A[m][s]);                             \
         _Pragma("unroll") for (int n = 0; n < 4; ++n) acc[m][n] =                            \
-            __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, __builtin_bit_cast(rbf16x8, B[n][s]), \
-                                                    acc[m][n], 0, 0, 0);                     \
+            rmfma<DT>(af, __builtin_bit_cast(rbf16x8, B[n][s]), acc[m][n]);                  \
       }                                                                                      \
     }                                                                                        \
   }
@@ -565,7 +578,7 @@ __global__ __launch_bounds__(kFuseWaves * kWave) void router_topk_kernel(
 
 static bool router_topk_fits(int xdt, int wdt, const void* x, int64_t x_stride, const void* w, int64_t T,
                              int64_t D, int64_t E) {
-  return xdt == QW_BF16 && wdt == QW_BF16 && T > kGemvMaxTokens && E <= kWave && D % kFuseChunk == 0 &&
+  return is_half(xdt) && wdt == xdt && T > kGemvMaxTokens && E <= kWave && D % kFuseChunk == 0 &&
          x_stride % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
 }
 
@@ -834,9 +847,13 @@ static int launch_router(const void* x, int xdt, int64_t x_stride, const void* w
   const dim3 grid(static_cast<unsigned>(ceil_div(T, 64)), static_cast<unsigned>(splits),
                   static_cast<unsigned>(ceil_div(E, 64)));
   const int kl = static_cast<int>(k_len);
-  if (xdt == QW_BF16 && wdt == QW_BF16 && D % 64 == 0) {
-    router_mfma_kernel<<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(x), x_stride,
-                                                 static_cast<const uint16_t*>(w), t, d, e, kl, partial);
+  if (is_half(xdt) && wdt == xdt && D % 64 == 0) {
+    if (xdt == QW_F16)
+      router_mfma_kernel<QW_F16><<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(x), x_stride,
+                                                           static_cast<const uint16_t*>(w), t, d, e, kl, partial);
+    else
+      router_mfma_kernel<QW_BF16><<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(x), x_stride,
+                                                            static_cast<const uint16_t*>(w), t, d, e, kl, partial);
     QW_LAUNCH_CHECK("router_mfma_kernel");
   } else {
     with_router_dtypes(xdt, wdt, [&](auto xd, auto wd) {
@@ -862,9 +879,15 @@ int route(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int6
   QW_REQUIRE(x && w && logits && top_idx && top_w, "x, router_w, logits, top_idx and top_w are required");
   const int t = static_cast<int>(T), e = static_cast<int>(E), k = static_cast<int>(K);
   if (router_topk_fits(xdt, wdt, x, x_stride, w, T, D, E)) {
-    router_topk_kernel<<<static_cast<unsigned>(ceil_div(T, kFuseTokens)), kFuseWaves * kWave, 0, stream>>>(
-        static_cast<const uint16_t*>(x), x_stride, static_cast<const uint16_t*>(w), t, static_cast<int>(D), e, k,
-        temperature, bias, select_logits ? 1 : 0, logits, probs, top_idx, top_w);
+    const unsigned g = static_cast<unsigned>(ceil_div(T, kFuseTokens));
+    if (xdt == QW_F16)
+      router_topk_kernel<QW_F16><<<g, kFuseWaves * kWave, 0, stream>>>(
+          static_cast<const uint16_t*>(x), x_stride, static_cast<const uint16_t*>(w), t, static_cast<int>(D), e, k,
+          temperature, bias, select_logits ? 1 : 0, logits, probs, top_idx, top_w);
+    else
+      router_topk_kernel<QW_BF16><<<g, kFuseWaves * kWave, 0, stream>>>(
+          static_cast<const uint16_t*>(x), x_stride, static_cast<const uint16_t*>(w), t, static_cast<int>(D), e, k,
+          temperature, bias, select_logits ? 1 : 0, logits, probs, top_idx, top_w);
     QW_LAUNCH_CHECK("router_topk_kernel");
     return QW_OK;
   }

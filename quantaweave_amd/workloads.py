@@ -58,6 +58,8 @@ WORKLOADS = {
         Workload("int8-prefill-T8192-d2048-E64-f1024-k2", 8192, 2048, 64, 1024, 2, 1.25, "bf16", "i8", 1006, batch=8),
         Workload("int4-prefill-T8192-d2048-E64-f1024-k2", 8192, 2048, 64, 1024, 2, 1.25, "bf16", "u4", 1007,
                  group_size=32, batch=8),
+        # the prefill layer in fp16 (the reference's fp16 precision): fp16 matrix cores
+        Workload("f16-prefill-T8192-d2048-E64-f1024-k2", 8192, 2048, 64, 1024, 2, 1.25, "f16", "f16", 1008, batch=8),
     ]
 }
 

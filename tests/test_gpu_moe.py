@@ -136,7 +136,6 @@ def f16_workload(name: str, **sizes) -> W.Workload:
 
 F16_CASES = [
     (f16_workload("bf16-prefill-T8192-d2048-E64-f1024-k2", tokens=1024, d_model=512, d_ff=256), False),
-    (f16_workload("bf16-prefill-T8192-d2048-E64-f1024-k2"), False),
     (f16_workload("bf16-prefill-T8192-d2048-E64-f1024-k2"), True),
     (f16_workload("int8-decode-T64-d2048-E64-f1024-k2"), False),
     (f16_workload("int4-decode-T16-d4096-E64-f1408-k2"), False),
