@@ -188,6 +188,14 @@ int qw_moe_combine(const void* y, int dtype, const int32_t* route_slot, const in
 int qw_moe_balance(const float* probs, const int32_t* counts, int64_t tokens, int64_t top_k, int64_t experts,
                    float* importance, float* balance, void* stream);
 
+/* qw_moe_balance with a caller workspace of qw_moe_balance_workspace_bytes:
+ * the same quantities, the importance summed from per-64-token partial sums
+ * in a fixed order (deterministic; the probs rows are read coalesced by many
+ * workgroups).  No reference counterpart beyond qw_moe_balance (:152-154). */
+size_t qw_moe_balance_workspace_bytes(int64_t tokens, int64_t experts);
+int qw_moe_balance_ws(const float* probs, const int32_t* counts, int64_t tokens, int64_t top_k, int64_t experts,
+                      float* importance, float* balance, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Whole MoE layer forward (TopKMoE.forward, src/quantweave_moe_model.py:113-164,
  * dynamic-dispatch branch): route -> plan -> grouped SwiGLU -> combine, no host
  * synchronisation.  `out` [tokens, d_model] has act_dtype.  Outputs as for the

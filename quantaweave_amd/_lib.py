@@ -37,6 +37,8 @@ SIGNATURES = {
                                      P, P, P, SZ, P]),
     "qw_moe_combine": (I32, [P, I32, P, P, I64, I64, I64, P, P]),
     "qw_moe_balance": (I32, [P, P, I64, I64, I64, P, P, P]),
+    "qw_moe_balance_workspace_bytes": (SZ, [I64, I64]),
+    "qw_moe_balance_ws": (I32, [P, P, I64, I64, I64, P, P, P, SZ, P]),
     "qw_moe_forward_workspace_bytes": (SZ, [I64, I64, I64, I64, I64, I32]),
     "qw_moe_forward": (I32, [P, I32, I64, I64, P, I32, F32, P, I64, I64, I64, I64, I32, I64, I64,
                              P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, SZ, P]),

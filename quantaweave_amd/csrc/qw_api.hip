@@ -51,6 +51,9 @@ int decode_combine(const void* y, int dtype, const int32_t* route_slot, const fl
                    int64_t T, int64_t K, int64_t D, float* out, hipStream_t stream);
 int cast_half(const float* x, int64_t n, uint16_t* out, int dtype, hipStream_t stream);
 int pack_bf16_tiles(const void* w, int64_t E, int64_t rows, int64_t cols, void* out, hipStream_t stream);
+size_t balance_workspace_bytes(int64_t T, int64_t E);
+int balance_ws(const float* probs, const int32_t* counts, int64_t T, int64_t K, int64_t E, float* importance,
+               float* bal, void* ws, size_t ws_bytes, hipStream_t stream);
 int balance(const float* probs, const int32_t* counts, int64_t T, int64_t K, int64_t E, float* importance,
             float* bal, hipStream_t stream, float* scratch_importance);
 int quantize(const void* w, int wdt, int64_t rows, int64_t cols, int bits, int64_t group, void* qweight, float* scales,
@@ -377,6 +380,18 @@ int qw_moe_balance(const float* probs, const int32_t* counts, int64_t tokens, in
   clear_error();
   QW_REQUIRE(importance != nullptr, "importance buffer [experts] is required");
   return balance(probs, counts, tokens, top_k, experts, importance, balance_out, as_stream(stream), nullptr);
+}
+
+size_t qw_moe_balance_workspace_bytes(int64_t tokens, int64_t experts) {
+  if (tokens < 1 || experts < 1) return 0;
+  return balance_workspace_bytes(tokens, experts);
+}
+
+int qw_moe_balance_ws(const float* probs, const int32_t* counts, int64_t tokens, int64_t top_k, int64_t experts,
+                      float* importance, float* balance_out, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  return balance_ws(probs, counts, tokens, top_k, experts, importance, balance_out, workspace, workspace_bytes,
+                    as_stream(stream));
 }
 
 size_t qw_moe_forward_workspace_bytes(int64_t tokens, int64_t d_model, int64_t experts, int64_t top_k, int64_t d_ff,

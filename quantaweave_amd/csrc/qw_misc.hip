@@ -385,6 +385,71 @@ __global__ void balance_kernel(const float* __restrict__ importance, const int32
   *balance = static_cast<float>(E) * s;
 }
 
+// The same with per-workgroup partial sums (coalesced row reads over token
+// chunks) summed afterwards in a fixed order: deterministic, and the probs
+// matrix is read by many CUs instead of one workgroup per strided column.
+constexpr int kImpRows = 64;  // tokens per partial-sum workgroup
+
+__global__ __launch_bounds__(256) void importance_partial_kernel(const float* __restrict__ probs, int T, int E,
+                                                                 float* __restrict__ partial) {
+  __shared__ float red[4][64];
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  const int e = blockIdx.y * 64 + lane;
+  const int t0 = blockIdx.x * kImpRows, t1 = min(T, t0 + kImpRows);
+  float s = 0.0f;
+  if (e < E)
+    for (int t = t0 + wave; t < t1; t += 4) s += probs[static_cast<int64_t>(t) * E + e];
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && e < E)
+    partial[static_cast<int64_t>(blockIdx.x) * E + e] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+}
+
+// One workgroup: importance[e] = (sum over partials in order) / T, then the
+// balance term summed over experts in ascending order by one thread.
+__global__ __launch_bounds__(1024) void importance_final_kernel(const float* __restrict__ partial, int nb, int T,
+                                                                int K, int E, const int32_t* __restrict__ counts,
+                                                                float* __restrict__ importance,
+                                                                float* __restrict__ balance) {
+  __shared__ float term[1024];
+  const float routes = static_cast<float>(static_cast<int64_t>(T) * K);
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    float s = 0.0f;
+    for (int b = 0; b < nb; ++b) s += partial[static_cast<int64_t>(b) * E + e];
+    const float imp = s / static_cast<float>(T);
+    importance[e] = imp;
+    term[e] = imp * (static_cast<float>(counts[e]) / routes);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = 0.0f;
+    for (int e = 0; e < E; ++e) s += term[e];
+    *balance = static_cast<float>(E) * s;
+  }
+}
+
+size_t balance_workspace_bytes(int64_t T, int64_t E) {
+  return static_cast<size_t>(ceil_div(T, kImpRows)) * static_cast<size_t>(E) * sizeof(float) + 256;
+}
+
+int balance_ws(const float* probs, const int32_t* counts, int64_t T, int64_t K, int64_t E, float* importance,
+               float* bal, void* ws, size_t ws_bytes, hipStream_t stream) {
+  QW_REQUIRE(T >= 1 && T <= INT32_MAX && E >= 1 && E <= 1024 && K >= 1, "bad balance sizes");
+  QW_REQUIRE(probs && counts && bal && importance, "balance pointers are required");
+  const size_t need = balance_workspace_bytes(T, E);
+  if (!ws || ws_bytes < need)
+    return set_error(QW_ERR_WORKSPACE, "balance workspace needs %zu bytes, got %zu", need, ws_bytes);
+  const int nb = static_cast<int>(ceil_div(T, kImpRows));
+  float* partial = static_cast<float*>(ws);
+  const dim3 g(static_cast<unsigned>(nb), static_cast<unsigned>(ceil_div(E, 64)));
+  importance_partial_kernel<<<g, 256, 0, stream>>>(probs, static_cast<int>(T), static_cast<int>(E), partial);
+  QW_LAUNCH_CHECK("importance_partial_kernel");
+  importance_final_kernel<<<1, 1024, 0, stream>>>(partial, nb, static_cast<int>(T), static_cast<int>(K),
+                                                   static_cast<int>(E), counts, importance, bal);
+  QW_LAUNCH_CHECK("importance_final_kernel");
+  return QW_OK;
+}
+
 int balance(const float* probs, const int32_t* counts, int64_t T, int64_t K, int64_t E, float* importance,
             float* bal, hipStream_t stream, float* scratch_importance) {
   QW_REQUIRE(T >= 1 && T <= INT32_MAX && E >= 1 && E <= 1024 && K >= 1, "bad balance sizes");

@@ -16,6 +16,8 @@ from __future__ import annotations
 import ctypes
 import math
 from dataclasses import dataclass
+from itertools import chain
+from operator import attrgetter, itemgetter, methodcaller
 from typing import Optional
 
 import torch
@@ -126,6 +128,16 @@ def can_tile(stack: Tensor) -> bool:
     return stack.dtype in _hip.HALF and stack.size(1) % 64 == 0 and stack.size(2) % 64 == 0
 
 
+_SUBMODULES = attrgetter("_modules")
+_GATE_UP_DOWN = itemgetter("gate", "up", "down")
+_PARAMETERS = attrgetter("_parameters")
+_BUFFERS = attrgetter("_buffers")
+_WEIGHT = itemgetter("weight")
+_QBUFFERS = itemgetter("qweight", "scales")
+_VERSION = attrgetter("_version")
+_DATA_PTR = methodcaller("data_ptr")
+
+
 class ExpertPack:
     """Experts' weights stacked once into [E, out, in] device buffers.
 
@@ -137,8 +149,15 @@ class ExpertPack:
     def __init__(self, experts: nn.ModuleList) -> None:
         self.fmt, self.group_in, self.group_ff = _expert_format(experts)
         self.mods, self.tensors = ExpertPack.sources(experts)
-        self.versions = [t._version for t in self.tensors]
-        self.ptrs = [t.data_ptr() for t in self.tensors]
+        # what current() compares, as tuples built by C-level iteration (the
+        # pack holds the objects, so their ids cannot be reused meanwhile)
+        self._exps = tuple(experts._modules.values())
+        self._exp_ids = tuple(map(id, self._exps))
+        self._mod_ids = tuple(map(id, self.mods))
+        self._tensor_ids = tuple(map(id, self.tensors))
+        self._quant = isinstance(self.mods[0], QuantizedLinear)
+        self.versions = tuple(map(_VERSION, self.tensors))
+        self.ptrs = tuple(map(_DATA_PTR, self.tensors))
         if self.fmt in (_lib.QW_F32, _lib.QW_BF16, _lib.QW_F16):
             self.gate = torch.stack([e.gate.weight.detach() for e in experts]).contiguous()
             self.up = torch.stack([e.up.weight.detach() for e in experts]).contiguous()
@@ -176,12 +195,19 @@ class ExpertPack:
     def current(self, experts: nn.ModuleList) -> bool:
         """True while the experts hold the same modules and tensors, unmodified
         (same storage, same version counter): the per-call check."""
-        mods, tensors = ExpertPack.sources(experts)
-        if len(mods) != len(self.mods) or any(a is not b for a, b in zip(mods, self.mods)):
+        if tuple(map(id, experts._modules.values())) != self._exp_ids:
             return False
-        if any(a is not b for a, b in zip(tensors, self.tensors)):
+        mods = tuple(chain.from_iterable(map(_GATE_UP_DOWN, map(_SUBMODULES, self._exps))))
+        if tuple(map(id, mods)) != self._mod_ids:
             return False
-        return [t._version for t in tensors] == self.versions and [t.data_ptr() for t in tensors] == self.ptrs
+        if self._quant:
+            tensors = chain.from_iterable(map(_QBUFFERS, map(_BUFFERS, mods)))
+        else:
+            tensors = map(_WEIGHT, map(_PARAMETERS, mods))
+        if tuple(map(id, tensors)) != self._tensor_ids:
+            return False
+        return (tuple(map(_VERSION, self.tensors)) == self.versions
+                and tuple(map(_DATA_PTR, self.tensors)) == self.ptrs)
 
     def args(self) -> list:
         return [self.fmt, self.group_in, self.group_ff, _hip.ptr(self.gate), _hip.ptr(self.gate_s),
@@ -426,15 +452,18 @@ def _forward_call(flat: Tensor, act: int, router_w: Tensor, moe: TopKMoE, pack: 
         return r
     s = _hip.stream(dev)
     d_ff = moe.experts[0].gate.out_features
-    nbytes = _lib.load().qw_moe_forward_workspace_bytes(T, width, E, K, d_ff, act)
-    ws = _stream_workspace(moe, nbytes, dev)
+    lib = _lib.load()
+    nbytes = lib.qw_moe_forward_workspace_bytes(T, width, E, K, d_ff, act)
+    fwd_bytes = (nbytes + 255) // 256 * 256
+    bal_bytes = lib.qw_moe_balance_workspace_bytes(T, E)
+    ws = _stream_workspace(moe, fwd_bytes + bal_bytes, dev)
     _lib.call("qw_moe_forward", _hip.ptr(flat), act, T, width, _hip.ptr(rw), _hip.act_code(rw, "router"),
               float(moe.router_temperature), _hip.ptr(bias), E, K, cap, d_ff, *pack.args(), _hip.ptr(r["out"]),
               _hip.ptr(r["probs"]), _hip.ptr(r["top_idx"]), _hip.ptr(r["top_w"]), _hip.ptr(r["counts"]),
               _hip.ptr(r["kept_counts"]), _hip.ptr(r["totals"]), _hip.ptr(r["dropped_token"]),
               _hip.ptr(r["dropped_expert"]), _hip.ptr(ws), nbytes, s)
-    _lib.call("qw_moe_balance", _hip.ptr(r["probs"]), _hip.ptr(r["counts"]), T, K, E, _hip.ptr(importance),
-              _hip.ptr(r["balance"]), s)
+    _lib.call("qw_moe_balance_ws", _hip.ptr(r["probs"]), _hip.ptr(r["counts"]), T, K, E, _hip.ptr(importance),
+              _hip.ptr(r["balance"]), _hip.ptr(ws[fwd_bytes:]), bal_bytes, s)
     return r
 
 
@@ -549,7 +578,10 @@ def _layer_chain(flat: Tensor, cdt: torch.dtype, router_w: Tensor, moe: TopKMoE,
     _lib.call("qw_moe_combine_static" if static else "qw_moe_combine_weighted", _hip.ptr(y), act, p["route_slot"],
               p["top_idx"], p["top_w"], T, K, D, p["out"], act_in, s)
     importance = torch.empty(E, dtype=torch.float32, device=dev)
-    _lib.call("qw_moe_balance", p["probs"], p["counts"], T, K, E, _hip.ptr(importance), p["balance"], s)
+    nb = lib.qw_moe_balance_workspace_bytes(T, E)
+    ws = _hip.workspace(nb, dev)
+    _lib.call("qw_moe_balance_ws", p["probs"], p["counts"], T, K, E, _hip.ptr(importance), p["balance"], _hip.ptr(ws),
+              nb, s)
     return r
 
 

@@ -460,3 +460,37 @@ def test_combine_is_bit_exact_against_the_oracle(k, dt):
                   code, _hip.stream(out.device))
         torch.cuda.synchronize()
         assert np.array_equal(out.float().cpu().numpy(), ref), fn
+
+
+@pytest.mark.parametrize("T,E,K", [(8192, 64, 2), (100, 184, 3), (1, 8, 1), (4097, 1024, 4)])
+def test_balance_with_workspace_matches_float64_and_is_deterministic(T, E, K):
+    """qw_moe_balance_ws (per-64-token partial sums, fixed order) and
+    qw_moe_balance: importance = probs.mean(0) and the balance term
+    E * sum(importance * counts / (T*K)) (src/quantweave_moe_model.py:152-154)."""
+    from quantaweave_amd import _hip, _lib
+
+    g = torch.Generator().manual_seed(T + E)
+    probs = torch.softmax(torch.randn(T, E, generator=g) * 3, dim=-1)
+    counts = torch.randint(0, 2 * T * K // E + 2, (E,), generator=g, dtype=torch.int32)
+    imp64 = probs.double().mean(0)
+    bal64 = float(E * (imp64 * counts.double() / (T * K)).sum())
+    pd, cd = probs.cuda(), counts.cuda()
+    lib = _lib.load()
+    nb = lib.qw_moe_balance_workspace_bytes(T, E)
+    ws = _hip.workspace(nb, pd.device)
+    outs = []
+    for _ in range(2):
+        imp = torch.empty(E, device="cuda")
+        bal = torch.empty((), device="cuda")
+        _lib.call("qw_moe_balance_ws", _hip.ptr(pd), _hip.ptr(cd), T, K, E, _hip.ptr(imp), _hip.ptr(bal),
+                  _hip.ptr(ws), nb, _hip.stream(pd.device))
+        outs.append((imp.cpu(), bal.cpu()))
+    imp0 = torch.empty(E, device="cuda")
+    bal0 = torch.empty((), device="cuda")
+    _lib.call("qw_moe_balance", _hip.ptr(pd), _hip.ptr(cd), T, K, E, _hip.ptr(imp0), _hip.ptr(bal0),
+              _hip.stream(pd.device))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    for imp, bal in (outs[0], (imp0.cpu(), bal0.cpu())):
+        assert (imp.double() - imp64).abs().max() <= 1e-6 * max(imp64.abs().max().item(), 1e-30)
+        assert abs(float(bal) - bal64) <= 1e-5 * max(abs(bal64), 1e-30)
