@@ -10,9 +10,10 @@
 // receives grad_x + result (one rounding), which sums the gate and up
 // projections' input gradients of a SwiGLU expert in place.
 //
-// bf16 with a workspace runs on the matrix cores (gemm_grouped_backward,
-// qw_gemm_mfma.hip).  Otherwise (fp32, or shapes the matrix-core path does not
-// take) two vector-ALU kernels compute a 64x64 output tile per 256-thread
+// bf16 and fp16 with a workspace run on the matrix cores (gemm_grouped_backward,
+// qw_gemm_mfma.hip); fp32 runs on the fp32 matrix cores (v_mfma_f32_16x16x4_f32,
+// the two kernels below) when rows are 16-byte aligned.  Otherwise two
+// vector-ALU kernels compute a 64x64 output tile per 256-thread
 // block (4x4 per thread) from 16-deep slices of the reduction staged in LDS;
 // the reduction runs in ascending order, so results do not depend on
 // scheduling.
@@ -126,6 +127,191 @@ __global__ __launch_bounds__(256) void grouped_dw_kernel(const void* __restrict_
   }
 }
 
+// ---------------------------------------------------------------------------
+// fp32 on the matrix cores.  A 256-thread workgroup (2 x 2 waves) computes a
+// 64 x 64 output tile from 64-deep reduction slices staged in LDS (two
+// buffers; the next slice is loaded into registers while the current one is
+// multiplied).  Each LDS tile is [64 tile rows][64 reduction indices] with
+// the reduction contiguous, so a lane reads the 4 reduction values of a
+// 16-wide step with one 16-byte read; lane group q of the four 16x16x4
+// instructions of a step takes reduction index 4q + j (any assignment works
+// when both operands agree).  Operands whose reduction index is not the
+// contiguous one in memory are transposed on their way into LDS.  The
+// reduction runs in ascending order.
+// ---------------------------------------------------------------------------
+typedef float bf32x4 __attribute__((ext_vector_type(4)));
+constexpr int FB_T = 64, FB_R = 64, FB_LD = FB_R + 4;
+
+// Products of one slice: acc[i][t] += A rows (wn*32 + 16t) x B rows (wm*32 + 16i)
+__device__ __forceinline__ void fb_compute(const float* As, const float* Bs, int wm, int wn, int l16, int lq,
+                                           bf32x4 (&acc)[2][2]) {
+#pragma unroll
+  for (int kk = 0; kk < FB_R; kk += 16) {
+    bf32x4 a[2], b[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) a[t] = *reinterpret_cast<const bf32x4*>(As + (wn * 32 + 16 * t + l16) * FB_LD + kk + 4 * lq);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) b[i] = *reinterpret_cast<const bf32x4*>(Bs + (wm * 32 + 16 * i + l16) * FB_LD + kk + 4 * lq);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][j], b[i][j], acc[i][t], 0, 0, 0);
+  }
+}
+
+// grad_x[r, k] (+)= sum_n gy[r, n] W_e[n, k]; block (k tile, row tile, expert).
+// A = W_e transposed into LDS ([k][n]), B = gy rows ([r][n]).
+__global__ __launch_bounds__(256) void grouped_dx_f32_kernel(const float* __restrict__ gy, const float* __restrict__ w,
+                                                             const int32_t* __restrict__ offsets, int N, int K,
+                                                             int rows, int accumulate, float* __restrict__ gx) {
+  __shared__ __attribute__((aligned(16))) float As[2][FB_T * FB_LD];
+  __shared__ __attribute__((aligned(16))) float Bs[2][FB_T * FB_LD];
+  const int e = blockIdx.z;
+  const int lo = min(max(offsets[e], 0), rows), hi = min(offsets[e + 1], rows);
+  const int r0 = lo + blockIdx.y * FB_T;
+  if (r0 >= hi) return;
+  const int k0 = blockIdx.x * FB_T;
+  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const int wm = wave / 2, wn = wave % 2, l16 = lane % 16, lq = lane / 16;
+  const float* we = w + static_cast<int64_t>(e) * N * K;
+  // this thread's 16-byte pieces: tile rows tid/16 + 16h, columns 4*(tid%16)
+  const int pr = tid / 16, pc = 4 * (tid % 16);
+  bf32x4 ra[4], rb[4];
+  auto load = [&](int n0) {
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int n = n0 + pr + 16 * h, k = k0 + pc;  // W row n, columns k..k+3
+      ra[h] = (n < N && k < K) ? *reinterpret_cast<const bf32x4*>(we + static_cast<int64_t>(n) * K + k)
+                               : bf32x4{0.f, 0.f, 0.f, 0.f};
+      const int r = r0 + pr + 16 * h, nn = n0 + pc;  // gy row r, columns nn..nn+3
+      rb[h] = (r < hi && nn < N) ? *reinterpret_cast<const bf32x4*>(gy + static_cast<int64_t>(r) * N + nn)
+                                 : bf32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) As[buf][(pc + j) * FB_LD + pr + 16 * h] = ra[h][j];  // [k][n]
+      *reinterpret_cast<bf32x4*>(&Bs[buf][(pr + 16 * h) * FB_LD + pc]) = rb[h];      // [r][n]
+    }
+  };
+  bf32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) acc[i][t] = bf32x4{0.f, 0.f, 0.f, 0.f};
+  const int S = (N + FB_R - 1) / FB_R;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int sl = 0; sl < S; ++sl) {
+    if (sl + 1 < S) load((sl + 1) * FB_R);
+    fb_compute(As[sl & 1], Bs[sl & 1], wm, wn, l16, lq, acc);
+    if (sl + 1 < S) store((sl + 1) & 1);
+    __syncthreads();
+  }
+  // lane holds grad_x[row wm*32 + 16i + l16][k wn*32 + 16t + 4lq .. +3]
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = r0 + wm * 32 + 16 * i + l16;
+    if (r >= hi) continue;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int k = k0 + wn * 32 + 16 * t + 4 * lq;
+      float* o = gx + static_cast<int64_t>(r) * K + k;
+      if (k + 3 < K) {
+        bf32x4 v = acc[i][t];
+        if (accumulate) {
+          const bf32x4 old = *reinterpret_cast<const bf32x4*>(o);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v[j] = old[j] + v[j];
+        }
+        *reinterpret_cast<bf32x4*>(o) = v;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (k + j < K) o[j] = accumulate ? o[j] + acc[i][t][j] : acc[i][t][j];
+      }
+    }
+  }
+}
+
+// grad_W_e[n, k] = sum over the rows r of expert e of gy[r, n] x[r, k] (exactly
+// zero without rows); block (k tile, n tile, expert).  A = x transposed
+// ([k][r]), B = gy transposed ([n][r]).
+__global__ __launch_bounds__(256) void grouped_dw_f32_kernel(const float* __restrict__ gy, const float* __restrict__ x,
+                                                             const int32_t* __restrict__ offsets, int N, int K,
+                                                             int rows, float* __restrict__ gw) {
+  __shared__ __attribute__((aligned(16))) float As[2][FB_T * FB_LD];
+  __shared__ __attribute__((aligned(16))) float Bs[2][FB_T * FB_LD];
+  const int e = blockIdx.z;
+  const int lo = min(max(offsets[e], 0), rows), hi = min(offsets[e + 1], rows);
+  const int n0 = blockIdx.y * FB_T, k0 = blockIdx.x * FB_T;
+  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const int wm = wave / 2, wn = wave % 2, l16 = lane % 16, lq = lane / 16;
+  const int pr = tid / 16, pc = 4 * (tid % 16);
+  bf32x4 ra[4], rb[4];
+  auto load = [&](int m0) {
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int r = m0 + pr + 16 * h;
+      const bool ok = r < hi;
+      ra[h] = (ok && k0 + pc < K) ? *reinterpret_cast<const bf32x4*>(x + static_cast<int64_t>(r) * K + k0 + pc)
+                                  : bf32x4{0.f, 0.f, 0.f, 0.f};
+      rb[h] = (ok && n0 + pc < N) ? *reinterpret_cast<const bf32x4*>(gy + static_cast<int64_t>(r) * N + n0 + pc)
+                                  : bf32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        As[buf][(pc + j) * FB_LD + pr + 16 * h] = ra[h][j];  // [k][r]
+        Bs[buf][(pc + j) * FB_LD + pr + 16 * h] = rb[h][j];  // [n][r]
+      }
+  };
+  bf32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) acc[i][t] = bf32x4{0.f, 0.f, 0.f, 0.f};
+  const int S = (hi - lo + FB_R - 1) / FB_R;  // 0 for an expert without rows
+  if (S > 0) {
+    load(lo);
+    store(0);
+  }
+  __syncthreads();
+  for (int sl = 0; sl < S; ++sl) {
+    if (sl + 1 < S) load(lo + (sl + 1) * FB_R);
+    fb_compute(As[sl & 1], Bs[sl & 1], wm, wn, l16, lq, acc);
+    if (sl + 1 < S) store((sl + 1) & 1);
+    __syncthreads();
+  }
+  // lane holds grad_W[n wm*32 + 16i + l16][k wn*32 + 16t + 4lq .. +3]
+  float* ge = gw + static_cast<int64_t>(e) * N * K;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int n = n0 + wm * 32 + 16 * i + l16;
+    if (n >= N) continue;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int k = k0 + wn * 32 + 16 * t + 4 * lq;
+      float* o = ge + static_cast<int64_t>(n) * K + k;
+      if (k + 3 < K) {
+        *reinterpret_cast<bf32x4*>(o) = acc[i][t];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (k + j < K) o[j] = acc[i][t][j];
+      }
+    }
+  }
+}
+
 }  // namespace
 
 size_t gemm_backward_workspace_bytes(int64_t E, int64_t N, int64_t K, int64_t rows);
@@ -166,6 +352,25 @@ int grouped_matmul_backward(const void* gy, const void* x, const void* w, int dt
     if (core_dw) gw = nullptr;
   }
   const int n = static_cast<int>(N), k = static_cast<int>(K), r = static_cast<int>(rows);
+  // fp32 matrix-core path: 16-byte rows and bases
+  const bool f32_core = dtype == QW_F32 && N % 4 == 0 && K % 4 == 0 && aligned16(gy) && aligned16(x) &&
+                        aligned16(w) && (gx == nullptr || aligned16(gx)) && (gw == nullptr || aligned16(gw));
+  if (f32_core && gx != nullptr && rows > 0) {
+    const dim3 g(static_cast<unsigned>(ceil_div(K, FB_T)), static_cast<unsigned>(ceil_div(per, FB_T)),
+                 static_cast<unsigned>(E));
+    grouped_dx_f32_kernel<<<g, 256, 0, stream>>>(static_cast<const float*>(gy), static_cast<const float*>(w), offsets,
+                                                 n, k, r, accumulate, static_cast<float*>(gx));
+    QW_LAUNCH_CHECK("grouped_dx_f32_kernel");
+    gx = nullptr;
+  }
+  if (f32_core && gw != nullptr && gw_dtype == QW_F32) {
+    const dim3 g(static_cast<unsigned>(ceil_div(K, FB_T)), static_cast<unsigned>(ceil_div(N, FB_T)),
+                 static_cast<unsigned>(E));
+    grouped_dw_f32_kernel<<<g, 256, 0, stream>>>(static_cast<const float*>(gy), static_cast<const float*>(x), offsets,
+                                                 n, k, r, static_cast<float*>(gw));
+    QW_LAUNCH_CHECK("grouped_dw_f32_kernel");
+    gw = nullptr;
+  }
   if (gx != nullptr && rows > 0) {
     const dim3 g(static_cast<unsigned>(ceil_div(K, BT)), static_cast<unsigned>(ceil_div(per, BT)),
                  static_cast<unsigned>(E));

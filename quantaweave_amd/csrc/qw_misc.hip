@@ -405,20 +405,27 @@ __global__ __launch_bounds__(256) void importance_partial_kernel(const float* __
     partial[static_cast<int64_t>(blockIdx.x) * E + e] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
 }
 
-// One workgroup: importance[e] = (sum over partials in order) / T, then the
-// balance term summed over experts in ascending order by one thread.
+// One workgroup: wave w takes experts w, w + 16, ...; for expert e lane l adds
+// the partials l, l + 64, ... in order and the 64 lane sums meet in a fixed
+// xor butterfly, so importance[e] = sum / T does not depend on scheduling.
+// The balance term is then summed over experts in ascending order by one thread.
 __global__ __launch_bounds__(1024) void importance_final_kernel(const float* __restrict__ partial, int nb, int T,
                                                                 int K, int E, const int32_t* __restrict__ counts,
                                                                 float* __restrict__ importance,
                                                                 float* __restrict__ balance) {
   __shared__ float term[1024];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
   const float routes = static_cast<float>(static_cast<int64_t>(T) * K);
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+  for (int e = wave; e < E; e += waves) {
     float s = 0.0f;
-    for (int b = 0; b < nb; ++b) s += partial[static_cast<int64_t>(b) * E + e];
-    const float imp = s / static_cast<float>(T);
-    importance[e] = imp;
-    term[e] = imp * (static_cast<float>(counts[e]) / routes);
+    for (int b = lane; b < nb; b += kWave) s += partial[static_cast<int64_t>(b) * E + e];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, kWave);
+    if (lane == 0) {
+      const float imp = s / static_cast<float>(T);
+      importance[e] = imp;
+      term[e] = imp * (static_cast<float>(counts[e]) / routes);
+    }
   }
   __syncthreads();
   if (threadIdx.x == 0) {
