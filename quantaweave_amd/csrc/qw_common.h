@@ -307,31 +307,32 @@ __device__ __forceinline__ float reduce_scatter(float (&v)[V], int lane) {
   return r;
 }
 
-// Block-wide exclusive scan of one int per thread; *total gets the sum.
-__device__ int block_exclusive_scan(int v, int* warp_tot, int* total) {
+// Block-wide exclusive scan of one integer per thread; *total gets the sum.
+template <typename T>
+__device__ T block_exclusive_scan(T v, T* warp_tot, T* total) {
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  int incl = v;
+  T incl = v;
 #pragma unroll
   for (int o = 1; o < kWave; o <<= 1) {
-    const int n = __shfl_up(incl, o, kWave);
+    const T n = __shfl_up(incl, o, kWave);
     if (lane >= o) incl += n;
   }
   if (lane == kWave - 1) warp_tot[wave] = incl;
   __syncthreads();
   if (wave == 0) {
     const int nw = blockDim.x / kWave;
-    const int w = lane < nw ? warp_tot[lane] : 0;
-    int wi = w;
+    const T w = lane < nw ? warp_tot[lane] : T(0);
+    T wi = w;
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
-      const int n = __shfl_up(wi, o, kWave);
+      const T n = __shfl_up(wi, o, kWave);
       if (lane >= o) wi += n;
     }
     if (lane < nw) warp_tot[lane] = wi - w;
     if (lane == nw - 1) *total = wi;
   }
   __syncthreads();
-  const int r = warp_tot[wave] + incl - v;
+  const T r = warp_tot[wave] + incl - v;
   __syncthreads();
   return r;
 }

@@ -12,20 +12,26 @@
 //   key = (~order(weight)) << 32 | route id        (unique per route)
 // into LDS (a wave finds its matches with one ballot per route column and
 // claims their positions with a single LDS atomic).  From the histogram it
-// derives every offset itself, ranks its keys (by counting, or with a bitonic
-// network for large experts) and writes kept slots and dropped routes at
-// their plan positions.  Keys are unique, so the order inside the gather does
-// not matter and the result does not depend on scheduling.  An expert with
-// more routes than the LDS holds gathers its keys into its own slice of the
-// workspace and sorts them there with the same kind of network (same result,
-// slower: one global-memory pass per network stage).
+// derives every offset itself (one scan of the packed kept and dropped
+// counts), sorts its keys and writes kept slots and dropped routes at their
+// plan positions.  The sort ranks each 64-key chunk by counting (one wave per
+// chunk), then merges sorted runs pairwise: a key's place in the merged run is
+// its index in its own run plus the number of smaller keys in the partner
+// run (a binary search).  Keys are unique, so these places form a
+// permutation, the order inside the gather does not matter and the result
+// does not depend on scheduling.  An expert with more routes than the LDS
+// holds gathers its keys into its own slice of the workspace and sorts them
+// there with a bitonic network (same result, slower: one global-memory pass
+// per network stage).
 #include "qw_common.h"
 
 namespace qw {
 
 constexpr int kPlanThreads = 1024;
-constexpr int kSortCap = 8192;  // keys an expert sorts in LDS (64 KiB)
-constexpr int kRankCap = 1024;  // keys an expert ranks by counting (n^2 compares) instead of sorting
+constexpr int kSortCap = 8192;  // keys an expert sorts in LDS (two buffers of 64 KiB)
+constexpr int kChunkLog = 6;
+constexpr int kChunk = 1 << kChunkLog;  // keys one wave ranks by counting before the merges
+constexpr int kKeysPerThread = kSortCap / kPlanThreads;
 constexpr int kMaxExperts = 1024;
 constexpr int kRoutesPerThread = 16;
 
@@ -45,6 +51,59 @@ __device__ __forceinline__ uint64_t route_key(const float* top_w, int r) {
   return (static_cast<uint64_t>(~weight_key(top_w[r])) << 32) | static_cast<uint32_t>(r);
 }
 
+// One merge round over n keys in LDS: run r (keys [r*run, (r+1)*run)) pairs
+// with run r ^ 1, and a key moves to (start of the pair) + (its index in its
+// run) + (keys of the partner run below it), found by binary lifting over the
+// powers of two <= run.  Thread t holds keys t + u*kPlanThreads, u < NU; their
+// searches step together, so their LDS reads are in flight together.  A wave
+// with no key skips the search.
+template <int NU>
+__device__ __forceinline__ void merge_round(const uint64_t* __restrict__ src, uint64_t* __restrict__ dst, int n,
+                                            int lg, int tid) {
+  const int run = 1 << lg;
+  if ((tid & ~(kWave - 1)) >= n) return;  // the wave's first key is past n (and so are its later ones)
+  uint64_t k[NU];
+  int pb[NU], len[NU], cnt[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    const int i = tid + u * kPlanThreads;
+    pb[u] = ((i >> lg) ^ 1) << lg;
+    const int pe = pb[u] + run < n ? pb[u] + run : n;
+    len[u] = i < n && pb[u] < n ? pe - pb[u] : 0;
+    k[u] = src[i < n ? i : 0];
+    cnt[u] = 0;
+  }
+  for (int step = run; step >= 1; step >>= 1) {
+    uint64_t v[NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int j = cnt[u] + step - 1;
+      v[u] = src[j < len[u] ? pb[u] + j : 0];  // past the partner's length: element 0, ignored
+    }
+#pragma unroll
+    for (int u = 0; u < NU; ++u)
+      if (cnt[u] + step <= len[u] && v[u] < k[u]) cnt[u] += step;
+  }
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    const int i = tid + u * kPlanThreads;
+    if (i < n) dst[((i >> lg) & ~1) * run + (i & (run - 1)) + cnt[u]] = k[u];
+  }
+}
+
+// Merge rounds from sorted runs of kChunk keys in buf[1] up to one run of n keys;
+// returns the buffer that holds the result.
+template <int NU>
+__device__ __forceinline__ int merge_all(uint64_t (*buf)[kSortCap], int n, int tid) {
+  int cur = 1;
+  for (int lg = kChunkLog; (1 << lg) < n; ++lg) {
+    merge_round<NU>(buf[cur], buf[cur ^ 1], n, lg, tid);
+    __syncthreads();
+    cur ^= 1;
+  }
+  return cur;
+}
+
 // Offsets, per-expert ranking and placement.
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const int32_t* __restrict__ top_idx, const float* __restrict__ top_w, int R, int E, int K, int capacity,
@@ -53,13 +112,17 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     int32_t* __restrict__ route_slot, int32_t* __restrict__ dropped_token, int32_t* __restrict__ dropped_expert,
     uint64_t* __restrict__ spill) {
   constexpr int kWaves = kPlanThreads / kWave;
-  __shared__ uint64_t keys[kSortCap];
-  __shared__ int hist[kWaves][kMaxExperts];
-  __shared__ int warp_tot[kWaves];
-  __shared__ int s_tot_kept, s_tot_drop, s_tot_routes;
+  // Two key buffers; the second holds the per-wave histograms until the
+  // offsets are known.
+  __shared__ uint64_t buf[2][kSortCap];
+  static_assert(sizeof(int) * kWaves * kMaxExperts <= sizeof(buf[1]), "histograms must fit a key buffer");
+  uint64_t* const keys = buf[0];
+  int (*const hist)[kMaxExperts] = reinterpret_cast<int (*)[kMaxExperts]>(&buf[1][0]);
+  __shared__ uint64_t warp_tot[kWaves];
+  __shared__ uint64_t s_tot;
   __shared__ int s_kept_off, s_drop_off, s_route_off, s_fill, s_fill_big;
   const int e = blockIdx.x;
-  const int tid = threadIdx.x, wave = tid / kWave;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   for (int i = tid; i < kWaves * E; i += kPlanThreads) hist[i / E][i % E] = 0;
   if (tid == 0) {
     s_fill = 0;
@@ -92,7 +155,6 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     }
     if (wave_n != 0) {
       // this expert's routes of the wave: one LDS atomic, then consecutive positions
-      const int lane = tid % kWave;
       int first = 0;
       if (lane == 0) first = atomicAdd(&s_fill, wave_n);
       first = __shfl(first, 0, kWave);
@@ -117,26 +179,44 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     for (int w = 0; w < kWaves; ++w) c += hist[w][tid];
   }
   const int kc = c < capacity ? c : capacity;
-  const int ko = block_exclusive_scan(kc, warp_tot, &s_tot_kept);
-  const int dof = block_exclusive_scan(c - kc, warp_tot, &s_tot_drop);
-  const int ro = block_exclusive_scan(c, warp_tot, &s_tot_routes);
-  if (tid == e) {
-    s_kept_off = ko;
-    s_drop_off = dof;
-    s_route_off = ro;
-  }
-  if (e == 0 && tid < E) {
-    counts[tid] = c;
-    kept_counts[tid] = kc;
-    kept_offsets[tid] = ko;
-  }
-  if (e == 0 && tid == 0) {
-    kept_offsets[E] = s_tot_kept;
-    totals[0] = s_tot_kept;
-    totals[1] = s_tot_drop;
+  // kept count in the low word, dropped count in the high word: every prefix
+  // sum of either is at most R < 2^31, so the words never carry into each other
+  const uint64_t packed = (static_cast<uint64_t>(c - kc) << 32) | static_cast<uint32_t>(kc);
+  auto publish = [&](uint64_t excl, uint64_t tot) {
+    const int ko = static_cast<int>(excl & 0xffffffffu), dof = static_cast<int>(excl >> 32);
+    if (tid == e) {
+      s_kept_off = ko;
+      s_drop_off = dof;
+      s_route_off = ko + dof;
+    }
+    if (e == 0 && tid < E) {
+      counts[tid] = c;
+      kept_counts[tid] = kc;
+      kept_offsets[tid] = ko;
+    }
+    if (e == 0 && tid == 0) {
+      kept_offsets[E] = static_cast<int>(tot & 0xffffffffu);
+      totals[0] = static_cast<int>(tot & 0xffffffffu);
+      totals[1] = static_cast<int>(tot >> 32);
+    }
+  };
+  if (E <= kWave) {
+    // every expert in wave 0: a wave scan, no workgroup barrier
+    if (wave == 0) {
+      uint64_t incl = packed;
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) {
+        const uint64_t v = __shfl_up(incl, o, kWave);
+        if (lane >= o) incl += v;
+      }
+      publish(incl - packed, __shfl(incl, kWave - 1, kWave));
+    }
+  } else {
+    const uint64_t excl = block_exclusive_scan(packed, warp_tot, &s_tot);
+    publish(excl, s_tot);
   }
   __syncthreads();
-  const int n = s_fill;
+  const int n = __builtin_amdgcn_readfirstlane(s_fill);  // the same in every lane
   if (n == 0) return;
   const int kept_off = s_kept_off, drop_off = s_drop_off;
 
@@ -155,37 +235,27 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     }
   };
 
-  if (n <= kRankCap) {
-    // ---- rank by counting: every key against every key (all lanes read the same key: broadcast) ----
-    for (int i = tid; i < n; i += kPlanThreads) {
-      const uint64_t k = keys[i];
+  if (n <= kSortCap) {
+    // ---- sort in LDS: rank each 64-key chunk by counting (all lanes of the
+    //      wave read the same key: broadcast), sorted chunks to buf[1] ----
+    for (int q = wave; q * kChunk < n; q += kWaves) {
+      const int base = q * kChunk, m = n - base < kChunk ? n - base : kChunk;
+      const int i = base + lane;
+      const uint64_t k = i < n ? keys[i] : 0ull;
       int rank = 0;
 #pragma unroll 16
-      for (int j = 0; j < n; ++j) rank += keys[j] < k ? 1 : 0;  // reads in flight together
-      place(k, rank);
+      for (int j = 0; j < m; ++j) rank += keys[base + j] < k ? 1 : 0;
+      if (i < n) buf[1][base + rank] = k;
     }
-  } else if (n <= kSortCap) {
-    int p2 = 1;
-    while (p2 < n) p2 <<= 1;
-    for (int i = n + tid; i < p2; i += blockDim.x) keys[i] = ~0ull;  // padding sorts last
     __syncthreads();
-    // ---- bitonic sort, ascending ----
-    for (int size = 2; size <= p2; size <<= 1) {
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        for (int i = tid; i < p2 / 2; i += blockDim.x) {
-          const int lo = 2 * i - (i & (stride - 1));
-          const int hi = lo + stride;
-          const bool up = ((lo & size) == 0);
-          const uint64_t a = keys[lo], b = keys[hi];
-          if ((a > b) == up) {
-            keys[lo] = b;
-            keys[hi] = a;
-          }
-        }
-        __syncthreads();
-      }
-    }
-    for (int i = tid; i < n; i += blockDim.x) place(keys[i], i);
+    // ---- merge sorted runs pairwise up to one sorted run ----
+    const int nu = (n + kPlanThreads - 1) / kPlanThreads;  // keys per thread
+    const int cur = nu == 1   ? merge_all<1>(buf, n, tid)
+                    : nu == 2 ? merge_all<2>(buf, n, tid)
+                    : nu <= 4 ? merge_all<4>(buf, n, tid)
+                              : merge_all<kKeysPerThread>(buf, n, tid);
+    const uint64_t* src = buf[cur];
+    for (int i = tid; i < n; i += kPlanThreads) place(src[i], i);
   } else {
     // ---- large expert: its n keys in its own slice of the workspace (n routes
     //      of expert e start at s_route_off), sorted there ----

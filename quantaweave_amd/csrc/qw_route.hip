@@ -639,8 +639,8 @@ __global__ __launch_bounds__(kSmallThreads) void route_plan_small_kernel(
   __shared__ float s_w[kSmallRoutes];
   __shared__ uint64_t s_key[kSmallRoutes];
   __shared__ int hist[1024], s_ko[1024], s_do[1024];
-  __shared__ int warp_tot[kWaves];
-  __shared__ int s_tot_kept, s_tot_drop;
+  __shared__ uint64_t warp_tot[kWaves];
+  __shared__ uint64_t s_tot;
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const int R = T * K;
   for (int i = tid; i < E; i += kSmallThreads) hist[i] = 0;
@@ -718,8 +718,11 @@ __global__ __launch_bounds__(kSmallThreads) void route_plan_small_kernel(
   __syncthreads();
   const int c = tid < E ? hist[tid] : 0;
   const int kc = c < capacity ? c : capacity;
-  const int ko = block_exclusive_scan(kc, warp_tot, &s_tot_kept);
-  const int dof = block_exclusive_scan(c - kc, warp_tot, &s_tot_drop);
+  // kept count in the low word, dropped count in the high word (every prefix
+  // sum is at most R, so the words never carry into each other): one scan
+  const uint64_t excl =
+      block_exclusive_scan((static_cast<uint64_t>(c - kc) << 32) | static_cast<uint32_t>(kc), warp_tot, &s_tot);
+  const int ko = static_cast<int>(excl & 0xffffffffu), dof = static_cast<int>(excl >> 32);
   if (tid < E) {
     s_ko[tid] = ko;
     s_do[tid] = dof;
@@ -728,9 +731,9 @@ __global__ __launch_bounds__(kSmallThreads) void route_plan_small_kernel(
     kept_offsets[tid] = ko;
   }
   if (tid == 0) {
-    kept_offsets[E] = s_tot_kept;
-    totals[0] = s_tot_kept;
-    totals[1] = s_tot_drop;
+    kept_offsets[E] = static_cast<int>(s_tot & 0xffffffffu);
+    totals[0] = static_cast<int>(s_tot & 0xffffffffu);
+    totals[1] = static_cast<int>(s_tot >> 32);
   }
   __syncthreads();
   // ---- 3. rank within the expert and place ----

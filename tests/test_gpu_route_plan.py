@@ -105,6 +105,9 @@ def _check_plan(idx, w, E, cap):
     (3000, 2, 2, 0.1, 0.0, 8), (5, 64, 2, 1.0, 0.0, 9), (8191, 64, 2, 1.25, 0.0, 10), (4097, 64, 2, 1.0, 3.0, 11),
     # experts past the 8192 keys the LDS sorts: the sorting network in the workspace
     (12000, 1, 1, 0.5, 0.0, 12), (20000, 8, 2, 0.3, 8.0, 13), (40000, 4, 2, 1.0, 8.0, 14),
+    # more than 64 experts: the histogram from LDS atomics instead of bit-plane ballots
+    (4096, 65, 2, 1.0, 3.0, 15), (3000, 100, 4, 1.25, 0.0, 16), (8192, 256, 8, 1.0, 3.0, 17),
+    (2048, 1024, 2, 2.0, 0.0, 18),
 ])
 def test_plan_is_bit_exact(T, E, k, cf, hot, seed):
     print(f"case T={T} E={E} k={k} cf={cf}", flush=True)
