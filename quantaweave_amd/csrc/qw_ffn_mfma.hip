@@ -439,6 +439,67 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
     k_loop(std::integral_constant<int, NP>{});
   }
 
+  // ---- epilogue without route weights or saved copies: the tile goes through
+  //      LDS (the ring is free once every wave is past its last slice) and
+  //      leaves in whole row segments, 16 bytes per lane (gate/up: 128 columns,
+  //      256-byte segments, all rows at once; down: 256 columns, 512-byte
+  //      segments, half the rows per pass).  A lane's 8-byte pieces (row l16,
+  //      columns 4lq..4lq+3 of each 16-column MFMA tile) land in 16-byte chunk
+  //      (col / 8) ^ ((row & 15) << 1) of the row (mod the chunks per row),
+  //      so neither the writes nor the row reads repeat a bank more than the
+  //      access width requires.  Same values as the direct stores below. ----
+  if (row_weight == nullptr && save_a == nullptr && n_out % 8 == 0 &&
+      (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+    constexpr int OC = GATEUP ? MF_NB / 2 : MF_NB;  // output columns of the tile
+    constexpr int CPR = OC / 8;                     // 16-byte chunks per row
+    constexpr int PASSES = GATEUP ? 1 : 2;
+    constexpr int PR = MCH / PASSES;                // rows per pass
+    static_assert(PR * OC * 2 <= ST * (A_STAGE + B_STAGE), "the staged tile fits the ring");
+    static_assert(MCH % (16 * PASSES * 2) == 0, "a pass holds whole sub-tile pairs");
+    char* const ot = smem;
+    auto chunk_of = [](int row, int col) { return (col / 8) ^ (((row & 15) << 1) & (CPR - 1)); };
+#pragma unroll
+    for (int pass = 0; pass < PASSES; ++pass) {
+      __syncthreads();  // pass 0: every wave is done with the ring; pass 1: the stores of pass 0 read LDS
+#pragma unroll
+      for (int i = 0; i < SUBT; ++i) {
+        const int sub = wm + 2 * i;
+        if (sub * 16 < pass * PR || sub * 16 >= (pass + 1) * PR) continue;  // not this pass's rows
+        if (sub >= active_sub) continue;
+        const int row = sub * 16 + l16, rl = row - pass * PR;
+#pragma unroll
+        for (int t = 0; t < (GATEUP ? MF_NT / 2 : MF_NT); ++t) {
+          const int col = GATEUP ? wn * 32 + t * 16 + 4 * lq : wn * 64 + t * 16 + 4 * lq;
+          uint32_t pk[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            float a, c;
+            if (GATEUP) {
+              a = swiglu_act<ACT>(acc[i][t][2 * h], acc[i][t + MF_NT / 2][2 * h]);
+              c = swiglu_act<ACT>(acc[i][t][2 * h + 1], acc[i][t + MF_NT / 2][2 * h + 1]);
+            } else {
+              a = acc[i][t][2 * h];
+              c = acc[i][t][2 * h + 1];
+            }
+            pk[h] = f32_to_half<ACT>(a) | (static_cast<uint32_t>(f32_to_half<ACT>(c)) << 16);
+          }
+          *reinterpret_cast<uint2*>(ot + rl * (OC * 2) + chunk_of(row, col) * 16 + (col % 8) * 2) =
+              make_uint2(pk[0], pk[1]);
+        }
+      }
+      __syncthreads();
+      const int rows = min(count - pass * PR, PR);
+      for (int c = tid; c < rows * CPR; c += MF_THREADS) {
+        const int rl = c / CPR, q = c % CPR, row = pass * PR + rl;
+        const int col = n0 + q * 8;
+        if (col < n_out)
+          *reinterpret_cast<uint4*>(out + static_cast<int64_t>(r0 + row) * n_out + col) =
+              *reinterpret_cast<const uint4*>(ot + rl * (OC * 2) + chunk_of(row, q * 8) * 16);
+      }
+    }
+    return;
+  }
+
   // ---- epilogue: lane holds row l16 of the sub-tile, columns 4*lq .. 4*lq+3 of each tile ----
   // DOWN: the route weights of all of this lane's rows are requested together
   // (one memory round trip, not one per sub-tile).
