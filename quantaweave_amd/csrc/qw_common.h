@@ -250,10 +250,57 @@ __device__ __forceinline__ int find_tile(const int32_t* __restrict__ offsets, in
   return -1;
 }
 
+// Value of another lane of the same 16-lane row (DPP; gfx9 controls), or the
+// lane's own value where the control writes nothing.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), CTRL, 0xf, 0xf, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i of 8 <- lane 7 - i
+constexpr int kDppMirror = 0x140;      // lane i of 16 <- lane 15 - i
+
+// Maximum over the wave, in every lane.  A maximum is exact in any order, so
+// the lanes of each 16-lane row are combined with DPP moves (quad xor 1 and 2,
+// half-row mirror, row mirror: no LDS round trips) and the four row maxima
+// are read from lanes 15, 31, 47 and 63.
 __device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, __uint_as_float(dpp_u32<kDppXor1>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp_u32<kDppXor2>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp_u32<kDppHalfMirror>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp_u32<kDppMirror>(__float_as_uint(v))));
+  const int b = __float_as_int(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 15));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(b, 31));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 47));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(b, 63));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_max_u64(uint64_t v) {
+  const uint64_t o = (static_cast<uint64_t>(dpp_u32<CTRL>(static_cast<uint32_t>(v >> 32))) << 32) |
+                     dpp_u32<CTRL>(static_cast<uint32_t>(v));
+  return o > v ? o : v;
+}
+
+// Maximum of a 64-bit key over the wave, in every lane (as wave_max).
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  v = dpp_max_u64<kDppXor1>(v);
+  v = dpp_max_u64<kDppXor2>(v);
+  v = dpp_max_u64<kDppHalfMirror>(v);
+  v = dpp_max_u64<kDppMirror>(v);
+  const int hi = static_cast<int>(v >> 32), lo = static_cast<int>(v);
+  uint64_t r = 0;
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
+  for (int row = 0; row < 4; ++row) {
+    const uint64_t x = (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(hi, 16 * row + 15))) << 32) |
+                       static_cast<uint32_t>(__builtin_amdgcn_readlane(lo, 16 * row + 15));
+    r = x > r ? x : r;
+  }
+  return r;
 }
 
 __device__ __forceinline__ float wave_sum_f(float v) {

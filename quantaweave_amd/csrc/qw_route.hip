@@ -313,18 +313,15 @@ __device__ __forceinline__ void select_token(float (&l)[EPL], int t, int E, int 
         best = cand > best ? cand : best;
       }
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const uint64_t other = __shfl_xor(best, o, kWave);
-      best = other > best ? other : best;
-    }
-    const int e_sel = static_cast<int>(0xffffffffu - static_cast<uint32_t>(best & 0xffffffffu));
+    best = wave_max_u64(best);
+    const int e_sel = __builtin_amdgcn_readfirstlane(
+        static_cast<int>(0xffffffffu - static_cast<uint32_t>(best & 0xffffffffu)));  // the same in every lane
     const int owner = e_sel % kWave, slot = e_sel / kWave;
     float p_sel = 0.0f;
 #pragma unroll
     for (int c = 0; c < EPL; ++c)
       if (c == slot) p_sel = p[c];
-    p_sel = __shfl(p_sel, owner, kWave);
+    p_sel = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p_sel), owner));
     if (lane == owner) taken |= 1u << slot;
     sel_sum = (j == 0) ? p_sel : sel_sum + p_sel;
     if (lane == j) {
@@ -362,11 +359,7 @@ __device__ __forceinline__ void select_tokens(float (&l)[TT], const int (&t)[TT]
   const bool live = lane < E;
   float m[TT], p[TT], s[TT];
 #pragma unroll
-  for (int i = 0; i < TT; ++i) m[i] = l[i];
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1)
-#pragma unroll
-    for (int i = 0; i < TT; ++i) m[i] = fmaxf(m[i], __shfl_xor(m[i], o, kWave));
+  for (int i = 0; i < TT; ++i) m[i] = wave_max(l[i]);
 #pragma unroll
   for (int i = 0; i < TT; ++i) {
     if (__any(l[i] != l[i])) m[i] = __builtin_nanf("");  // fmaxf drops NaN; torch's softmax does not
@@ -392,18 +385,12 @@ __device__ __forceinline__ void select_tokens(float (&l)[TT], const int (&t)[TT]
   for (int j = 0; j < K; ++j) {
     uint64_t best[TT];
 #pragma unroll
-    for (int i = 0; i < TT; ++i) best[i] = key[i];
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1)
-#pragma unroll
-      for (int i = 0; i < TT; ++i) {
-        const uint64_t other = __shfl_xor(best[i], o, kWave);
-        best[i] = other > best[i] ? other : best[i];
-      }
+    for (int i = 0; i < TT; ++i) best[i] = wave_max_u64(key[i]);
 #pragma unroll
     for (int i = 0; i < TT; ++i) {
-      const int e_sel = static_cast<int>(0xffffffffu - static_cast<uint32_t>(best[i] & 0xffffffffu));
-      const float p_sel = __shfl(p[i], e_sel, kWave);
+      const int e_sel = __builtin_amdgcn_readfirstlane(
+          static_cast<int>(0xffffffffu - static_cast<uint32_t>(best[i] & 0xffffffffu)));  // the same in every lane
+      const float p_sel = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[i]), e_sel));
       if (lane == e_sel) key[i] = 0;  // taken
       sel_sum[i] = (j == 0) ? p_sel : sel_sum[i] + p_sel;
       if (lane == j) {
@@ -462,8 +449,8 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
 // D % 64 == 0): 32 tokens per 512-thread block.  Wave w multiplies the
 // block's token rows by the E router rows over the 64-wide k chunks
 // w, w + 8, w + 16, ... with bf16 (fp16) MFMA (fp32 accumulation; operands go from
-// global memory straight into registers, one chunk in flight while the
-// previous is multiplied), the eight partial sums meet in LDS and are added in
+// global memory straight into registers, up to four chunks requested together
+// before their multiplies), the eight partial sums meet in LDS and are added in
 // wave order, L = (((p_0 + p_1) + ...) + p_7) / temperature, and wave w then
 // routes tokens 4w..4w+3 together (select_tokens), writing logits, probs and
 // choices exactly as route_topk_kernel does from the same logits.
@@ -494,7 +481,6 @@ __global__ __launch_bounds__(kFuseWaves * kWave) void router_topk_kernel(
 #pragma unroll
     for (int n = 0; n < 4; ++n) acc[m][n] = rf32x4{0.f, 0.f, 0.f, 0.f};
   // one chunk: k-steps of 32, lane (l16, kq) holding elements k0 + 32s + kq .. +7 of its rows
-  uint4 a0[2][kFuseSteps], b0[4][kFuseSteps], a1[2][kFuseSteps], b1[4][kFuseSteps];
 #define QW_RT_LOAD(A, B, C)                                                                  \
   {                                                                                          \
     const int k0_ = (C) * kFuseChunk;                                                        \
@@ -515,25 +501,26 @@ __global__ __launch_bounds__(kFuseWaves * kWave) void router_topk_kernel(
       }                                                                                      \
     }                                                                                        \
   }
-  // The next chunk's loads are issued unconditionally (past the wave's last
-  // chunk they re-read it), so each multiply waits for exactly its own loads.
+  // The wave's chunks go in batches of up to four: all loads of a batch are
+  // issued before its first multiply (one memory round trip per batch).
   const int nc = D / kFuseChunk;
   const int mine = wave < nc ? (nc - 1 - wave) / kFuseWaves + 1 : 0;  // chunks of this wave
-  int c = wave;
-  if (mine > 0) {
-    QW_RT_LOAD(a0, b0, c);
-    for (int i = 0;; i += 2) {
-      QW_RT_LOAD(a1, b1, i + 1 < mine ? c + kFuseWaves : c);
-      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the multiplies
-      QW_RT_MUL(a0, b0);
-      if (i + 1 >= mine) break;
-      c += kFuseWaves;
-      QW_RT_LOAD(a0, b0, i + 2 < mine ? c + kFuseWaves : c);
-      __builtin_amdgcn_sched_barrier(0);
-      QW_RT_MUL(a1, b1);
-      if (i + 2 >= mine) break;
-      c += kFuseWaves;
-    }
+  auto batch = [&](auto n_c, int c0) {
+    constexpr int N = decltype(n_c)::value;
+    uint4 a[N][2][kFuseSteps], b[N][4][kFuseSteps];
+#pragma unroll
+    for (int i = 0; i < N; ++i) QW_RT_LOAD(a[i], b[i], c0 + i * kFuseWaves);
+    __builtin_amdgcn_sched_barrier(0);  // every load of the batch before the first multiply
+#pragma unroll
+    for (int i = 0; i < N; ++i) QW_RT_MUL(a[i], b[i]);
+  };
+  for (int i0 = 0; i0 < mine; i0 += 4) {
+    const int c0 = wave + i0 * kFuseWaves;
+    const int n = mine - i0;
+    if (n >= 4) batch(std::integral_constant<int, 4>{}, c0);
+    else if (n == 3) batch(std::integral_constant<int, 3>{}, c0);
+    else if (n == 2) batch(std::integral_constant<int, 2>{}, c0);
+    else batch(std::integral_constant<int, 1>{}, c0);
   }
 #undef QW_RT_LOAD
 #undef QW_RT_MUL

@@ -59,7 +59,9 @@ def test_expert_bias_steers_selection_only():
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("T,D,E", [(512, 256, 8), (100, 2048, 64), (16, 4096, 64), (7, 33, 5),
-                                   (8192, 2048, 64), (301, 192, 40), (65, 64, 1)])
+                                   (8192, 2048, 64), (301, 192, 40), (65, 64, 1),
+                                   # 16-bit router kernel: 2, 3, 5 and 8 k-chunks per wave
+                                   (100, 1024, 64), (100, 1536, 48), (40, 2560, 64), (64, 4096, 64)])
 def test_router_logits_match_oracle_and_routing_follows(dtype, T, D, E):
     print(f"case T={T} D={D} E={E} {dtype}", flush=True)
     g = torch.Generator().manual_seed(T + D)
