@@ -211,6 +211,159 @@ __global__ __launch_bounds__(F32_THREADS) void ffn_f32_mfma_kernel(
   }
 }
 
+// Small problems (too few 64 x 64 tiles to fill the GPU): a workgroup of 4
+// waves owns a 32-row by 32-weight-row tile (GATEUP: 16 gate rows and the
+// matching 16 up rows) and its waves split K: wave w takes the 32-wide K
+// slices w, w + 4, ...  Each wave reads its MFMA operands straight from
+// global memory into registers (lane (l16, q) of a 16-wide K step loads the 4
+// consecutive values 4q .. 4q+3 of its row, the same index order as the LDS
+// kernel above), with the next slice's loads in flight during the current
+// slice's MFMAs; there is no LDS ring and no barrier in the K loop.  The four
+// partial tiles meet in LDS and are added in wave order ((w0 + w1) + w2) + w3,
+// then the epilogue is the one above.
+constexpr int F32S_M = 32, F32S_N = 32, F32S_BK = 32, F32S_ST = F32S_BK / 16;
+
+template <bool GATEUP>
+__global__ __launch_bounds__(F32_THREADS) void ffn_f32_small_kernel(
+    const float* __restrict__ x, const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
+    const float* __restrict__ wa, const float* __restrict__ wb, int64_t w_expert_stride, int n_w, int K, int n_out,
+    int max_rows, const float* __restrict__ row_weight, float* __restrict__ out, float* __restrict__ save_a,
+    float* __restrict__ save_b) {
+  __shared__ __attribute__((aligned(16))) f32x4 red[4][4][64];  // [wave][tile (i, t)][lane]
+  const int e = blockIdx.y;
+  const int r0 = max(offsets[e], 0), r1 = min(offsets[e + 1], max_rows);
+  if (r1 <= r0) return;
+  constexpr int COLS = GATEUP ? F32S_N / 2 : F32S_N;  // output columns per tile
+  const int c0 = blockIdx.x * COLS;
+  if (c0 >= n_out) return;
+  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const int l16 = lane % 16, lq = lane / 16;
+  // weight rows of the two 16-row A tiles: GATEUP t = 0 gate, t = 1 up; DOWN t = 0, 1 consecutive
+  const float* wsrc[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int row = GATEUP ? c0 + l16 : c0 + 16 * t + l16;
+    const float* base = (GATEUP && t == 1 ? wb : wa) + static_cast<int64_t>(e) * w_expert_stride;
+    wsrc[t] = base + static_cast<int64_t>(min(row, n_w - 1)) * K + 4 * lq;  // rows past the end: loaded, not stored
+  }
+  const int KS = (K + F32S_BK - 1) / F32S_BK;
+  for (int m0 = r0 + static_cast<int>(blockIdx.z) * F32S_M; m0 < r1; m0 += static_cast<int>(gridDim.z) * F32S_M) {
+    const float* xsrc[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int s = min(m0 + 16 * i + l16, r1 - 1);  // rows past the end: a valid row, not stored
+      const int64_t src = row_index ? row_index[s] : s;
+      xsrc[i] = x + src * K + 4 * lq;
+    }
+    // one slice: K steps of 16, per step the lane's 4 values of each operand tile
+    struct Slice {
+      f32x4 a[F32S_ST][2], b[F32S_ST][2];
+    };
+    auto load = [&](int ks, Slice& r) {
+#pragma unroll
+      for (int st = 0; st < F32S_ST; ++st) {
+        const int k = ks * F32S_BK + 16 * st;  // + 4 * lq inside the sources
+        const bool in_k = k + 4 * lq + 3 < K;  // K % 4 == 0: a piece is wholly inside K or wholly past it
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          r.a[st][t] = in_k ? *reinterpret_cast<const f32x4*>(wsrc[t] + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          r.b[st][i] = in_k ? *reinterpret_cast<const f32x4*>(xsrc[i] + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    };
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) acc[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](const Slice& r) {
+#pragma unroll
+      for (int st = 0; st < F32S_ST; ++st)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+              acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(r.a[st][t][j], r.b[st][i][j], acc[i][t], 0, 0, 0);
+    };
+    // this wave's slices: wave, wave + 4, ... (the next one loaded during the current one's MFMAs)
+    Slice ra, rb;
+    int ks = wave;
+    if (ks < KS) load(ks, ra);
+    while (ks < KS) {
+      if (ks + 4 < KS) load(ks + 4, rb);
+      compute(ra);
+      ks += 4;
+      if (ks >= KS) break;
+      if (ks + 4 < KS) load(ks + 4, ra);
+      compute(rb);
+      ks += 4;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) red[wave][2 * i + t][lane] = acc[i][t];
+    __syncthreads();
+    // tile (i, t) summed in wave order; GATEUP: wave i < 2 takes row block i (gate and up), DOWN: wave w tile w
+    auto total = [&](int tile) {
+      return ((red[0][tile][lane] + red[1][tile][lane]) + red[2][tile][lane]) + red[3][tile][lane];
+    };
+    if (GATEUP ? wave < 2 : true) {
+      const int i = GATEUP ? wave : wave / 2;
+      const int s = m0 + 16 * i + l16;
+      if (s < r1) {
+        const int64_t orow = static_cast<int64_t>(s) * n_out;
+        if constexpr (GATEUP) {
+          const f32x4 g = total(2 * i), u = total(2 * i + 1);
+          const int col = c0 + 4 * lq;
+          f32x4 h;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) h[v] = swiglu_act<QW_F32>(g[v], u[v]);
+          if (col + 3 < n_out) {
+            *reinterpret_cast<f32x4*>(out + orow + col) = h;
+            if (save_a) {
+              *reinterpret_cast<f32x4*>(save_a + orow + col) = g;
+              *reinterpret_cast<f32x4*>(save_b + orow + col) = u;
+            }
+          } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              if (col + v >= n_out) continue;
+              out[orow + col + v] = h[v];
+              if (save_a) {
+                save_a[orow + col + v] = g[v];
+                save_b[orow + col + v] = u[v];
+              }
+            }
+          }
+        } else {
+          const int t = wave % 2;
+          const f32x4 a = total(2 * i + t);
+          const float wgt = row_weight ? row_weight[s] : 1.0f;
+          const int col = c0 + 16 * t + 4 * lq;
+          f32x4 y;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) y[v] = a[v] * wgt;
+          if (col + 3 < n_out) {
+            *reinterpret_cast<f32x4*>(out + orow + col) = y;
+            if (save_a) *reinterpret_cast<f32x4*>(save_a + orow + col) = a;
+          } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              if (col + v >= n_out) continue;
+              out[orow + col + v] = y[v];
+              if (save_a) save_a[orow + col + v] = a[v];
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();  // red is reused by the next row chunk
+  }
+}
+
 // Workgroups per (column tile, expert) over the grid's z extent: one per
 // 64-row chunk of an expert of the expected size, at most 16 (each then loops
 // over its share of the chunks).
@@ -230,7 +383,26 @@ int launch_ffn_f32(const FfnArgs& a, hipStream_t stream, bool* handled) {
        reinterpret_cast<uintptr_t>(a.down.w)) % 16)
     return QW_OK;
   const int D = static_cast<int>(a.d_model), F = static_cast<int>(a.d_ff), mr = static_cast<int>(a.max_rows);
-  const unsigned z = f32_row_splits(a.avg_rows > 0 ? a.avg_rows : ceil_div(a.max_rows, a.experts));
+  const int64_t avg = a.avg_rows > 0 ? a.avg_rows : ceil_div(a.max_rows, a.experts);
+  const unsigned z = f32_row_splits(avg);
+  if (static_cast<int64_t>(ceil_div(D, F32_N)) * a.experts * z < 512) {
+    // too few 64 x 64 down tiles to fill the GPU: 32 x 32 tiles with K split over the waves
+    const unsigned zs = static_cast<unsigned>(std::min<int64_t>(std::max<int64_t>(ceil_div(avg, F32S_M), 1), 32));
+    const dim3 s1(static_cast<unsigned>(ceil_div(F, F32S_N / 2)), static_cast<unsigned>(a.experts), zs);
+    ffn_f32_small_kernel<true><<<s1, F32_THREADS, 0, stream>>>(
+        static_cast<const float*>(a.x), a.row_index, a.offsets, static_cast<const float*>(a.gate.w),
+        static_cast<const float*>(a.up.w), a.gate.expert_elems, F, D, F, mr, nullptr, static_cast<float*>(a.hidden),
+        static_cast<float*>(a.save_gate), static_cast<float*>(a.save_up));
+    QW_LAUNCH_CHECK("ffn_f32_small_kernel<gateup>");
+    const dim3 s2(static_cast<unsigned>(ceil_div(D, F32S_N)), static_cast<unsigned>(a.experts), zs);
+    ffn_f32_small_kernel<false><<<s2, F32_THREADS, 0, stream>>>(
+        static_cast<const float*>(a.hidden), nullptr, a.offsets, static_cast<const float*>(a.down.w),
+        static_cast<const float*>(a.down.w), a.down.expert_elems, D, F, D, mr, a.row_weight, static_cast<float*>(a.y),
+        static_cast<float*>(a.save_y), nullptr);
+    QW_LAUNCH_CHECK("ffn_f32_small_kernel<down>");
+    *handled = true;
+    return QW_OK;
+  }
   const dim3 g1(static_cast<unsigned>(ceil_div(F, F32_N / 2)), static_cast<unsigned>(a.experts), z);
   ffn_f32_mfma_kernel<true><<<g1, F32_THREADS, 0, stream>>>(
       static_cast<const float*>(a.x), a.row_index, a.offsets, static_cast<const float*>(a.gate.w),

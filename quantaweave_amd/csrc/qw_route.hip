@@ -50,7 +50,8 @@ __device__ __forceinline__ uint32_t sortable_key(float f) {
 // in ascending s, so the logits do not depend on scheduling.
 //
 // General kernel (any dtype pair, any d): 64x64 output tile per 256-thread
-// block, K staged through LDS in slices of 16, fp32 FMA.
+// block, K staged through LDS in slices of 16 (the next slice loaded into
+// registers during the current one's multiplies), fp32 FMA.
 // ---------------------------------------------------------------------------
 template <int XDT, int WDT>
 __global__ __launch_bounds__(256) void router_logits_kernel(const void* __restrict__ x, int64_t x_stride,
@@ -65,15 +66,30 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const void* __restri
   float* out = partial + static_cast<int64_t>(blockIdx.y) * T * E;
   const int ty = tid / 16, tx = tid % 16;
   float acc[4][4] = {};
-  for (int k0 = k_begin; k0 < k_end; k0 += TK) {
-    for (int i = tid; i < TM * TK; i += 256) {
+  // the next slice's values are loaded into registers while this one is
+  // multiplied, so only the first slice waits for memory
+  constexpr int PER = TM * TK / 256;
+  float xr[PER], wr[PER];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int i = tid + q * 256;
       const int m = i / TK, kk = i % TK;
-      const int t = t0 + m, k = k0 + kk;
-      xs[kk][m] = (t < T && k < k_end) ? load_act<XDT>(x, static_cast<int64_t>(t) * x_stride + k) : 0.0f;
-      const int e = e0 + m;
-      ws[kk][m] = (e < E && k < k_end) ? load_act<WDT>(w, static_cast<int64_t>(e) * D + k) : 0.0f;
+      const int t = t0 + m, k = k0 + kk, e = e0 + m;
+      xr[q] = (t < T && k < k_end) ? load_act<XDT>(x, static_cast<int64_t>(t) * x_stride + k) : 0.0f;
+      wr[q] = (e < E && k < k_end) ? load_act<WDT>(w, static_cast<int64_t>(e) * D + k) : 0.0f;
+    }
+  };
+  if (k_begin < k_end) fetch(k_begin);
+  for (int k0 = k_begin; k0 < k_end; k0 += TK) {
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int i = tid + q * 256;
+      xs[i % TK][i / TK] = xr[q];
+      ws[i % TK][i / TK] = wr[q];
     }
     __syncthreads();
+    if (k0 + TK < k_end) fetch(k0 + TK);
 #pragma unroll
     for (int kk = 0; kk < TK; ++kk) {
       float a[4], b[4];
@@ -817,14 +833,18 @@ size_t route_workspace_bytes(int64_t T, int64_t D, int64_t E) {
   return static_cast<size_t>(router_splits(T, D, E)) * T * E * sizeof(float);
 }
 
-// Router logits: up to kGemvMaxTokens tokens by the GEMV kernel straight into
-// `logits` (*splits = 0); more by the tiled GEMM into split-K partials
-// (*splits > 0) that the next kernel sums and divides by the temperature.
+// Router logits: up to kGemvMaxTokens tokens (or a small layer) by the GEMV
+// kernel straight into `logits` (*splits = 0); more by the tiled GEMM into
+// split-K partials (*splits > 0) that the next kernel sums and divides by the
+// temperature.
 static int launch_router(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int64_t T, int64_t D,
                          int64_t E, float temperature, float* logits, float* partial, size_t partial_bytes,
                          int* splits_out, hipStream_t stream) {
   const int t = static_cast<int>(T), d = static_cast<int>(D), e = static_cast<int>(E);
-  if (T <= kGemvMaxTokens) {
+  // The GEMV kernel issues all its loads at once but reads x once per expert:
+  // it serves a few tokens, and any batch whose x re-reads stay within 16 MiB
+  // (small layers, where the tiled kernel's K loop would wait on every slice).
+  if (T <= kGemvMaxTokens || T * E * D * (xdt == QW_F32 ? 4 : 2) <= (int64_t{16} << 20)) {
     *splits_out = 0;
     return launch_router_gemv(x, xdt, x_stride, w, wdt, t, d, e, temperature, logits, stream);
   }

@@ -100,6 +100,24 @@ def test_grouped_swiglu_matches_oracle(act, fmt, D, F_, group, path):
     assert normwise(got, ref) <= TOL[act]
 
 
+@pytest.mark.parametrize("E,D,F_,rows", [(16, 1024, 256, 100), (8, 256, 512, 128)])
+def test_fp32_tile_sizes_match_oracle(E, D, F_, rows):
+    """fp32 experts on the matrix cores: enough 64 x 64 down tiles to fill the GPU
+    (the 64 x 64 kernel) and a small layer (32 x 32 tiles, K split over the waves)."""
+    print(f"case f32 E={E} D={D} F={F_} rows~{rows}", flush=True)
+    rng = np.random.RandomState(E + D)
+    counts = [int(c) for c in rng.randint(rows - 40, rows + 40, size=E)]
+    counts[1] = 0
+    n = sum(counts)
+    x = rng.randn(n, D).astype(np.float32)
+    w = make_weights(E, D, F_, "f32", D + F_)
+    rw = rng.rand(n).astype(np.float32)
+    got = run_experts(x, counts, w, "f32", row_weight=rw)
+    ref = oracle.experts_forward(x, np.array(counts), w, "f32") * rw[:, None]
+    assert np.isfinite(got).all()
+    assert normwise(got, ref) <= TOL["f32"]
+
+
 @pytest.mark.parametrize("act,fmt,group,path", [
     ("bf16", "bf16", None, "mfma"), ("bf16", "bf16", None, "stream"), ("bf16", "bf16", None, "generic"),
     ("bf16", "i8", None, "stream"), ("bf16", "i8", None, "generic"), ("bf16", "u4", 32, "stream"),
