@@ -386,8 +386,11 @@ int launch_ffn_f32(const FfnArgs& a, hipStream_t stream, bool* handled) {
   const int64_t avg = a.avg_rows > 0 ? a.avg_rows : ceil_div(a.max_rows, a.experts);
   const unsigned z = f32_row_splits(avg);
   if (static_cast<int64_t>(ceil_div(D, F32_N)) * a.experts * z < 512) {
-    // too few 64 x 64 down tiles to fill the GPU: 32 x 32 tiles with K split over the waves
-    const unsigned zs = static_cast<unsigned>(std::min<int64_t>(std::max<int64_t>(ceil_div(avg, F32S_M), 1), 32));
+    // too few 64 x 64 down tiles to fill the GPU: 32 x 32 tiles with K split over the
+    // waves, one workgroup per 32-row chunk up to the capacity bound (so no
+    // workgroup takes two chunks of a full expert one after the other)
+    const int64_t cap_rows = a.row_cap > 0 ? std::min<int64_t>(a.row_cap, a.max_rows) : 2 * avg;
+    const unsigned zs = static_cast<unsigned>(std::min<int64_t>(std::max<int64_t>(ceil_div(cap_rows, F32S_M), 1), 64));
     const dim3 s1(static_cast<unsigned>(ceil_div(F, F32S_N / 2)), static_cast<unsigned>(a.experts), zs);
     ffn_f32_small_kernel<true><<<s1, F32_THREADS, 0, stream>>>(
         static_cast<const float*>(a.x), a.row_index, a.offsets, static_cast<const float*>(a.gate.w),
