@@ -123,13 +123,16 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const void* __restri
 // the TT per-thread sums are reduced across
 // the wave (reduce_scatter) and then across the 4 waves in wave order, and
 //   logits[t, e] = sum / temperature
-// is written directly (no split-K partials).
+// is written directly (no split-K partials).  With cast_out (fp32 x only) the
+// expert-0 blocks also write x rounded to bf16 or fp16 (the decode step's
+// expert input), so no other kernel reads x again for it.
 constexpr int kGemvMaxTokens = 64;  // the GEMV router serves up to this many tokens
 
 template <int XDT, int WDT, int VEC, int TT>
 __global__ __launch_bounds__(256) void router_gemv_kernel(const void* __restrict__ x, int64_t x_stride,
                                                           const void* __restrict__ w, int T, int D, int E,
-                                                          float temperature, float* __restrict__ logits) {
+                                                          float temperature, float* __restrict__ logits,
+                                                          uint16_t* __restrict__ cast_out, int cast_f16) {
   constexpr int L = log2i<TT>();
   __shared__ float red[4][TT];
   const int e = blockIdx.x;
@@ -148,6 +151,15 @@ __global__ __launch_bounds__(256) void router_gemv_kernel(const void* __restrict
 #pragma unroll
       for (int i = 0; i < TT; ++i)
         load_vec<XDT, VEC>(x, static_cast<int64_t>(t0 + min(i, nt - 1)) * x_stride + d, xv[i]);
+      if (XDT == QW_F32 && cast_out != nullptr && e == 0) {
+        // the expert-0 blocks also write the rows rounded to bf16 (fp16): contiguous x, x_stride == D
+#pragma unroll
+        for (int i = 0; i < TT; ++i)
+          if (i < nt)
+#pragma unroll
+            for (int u = 0; u < VEC; ++u)
+              cast_out[static_cast<int64_t>(t0 + i) * D + d + u] = cast_f16 ? f32_to_f16(xv[i][u]) : f32_to_bf16(xv[i][u]);
+      }
 #pragma unroll
       for (int i = 0; i < TT; ++i)
 #pragma unroll
@@ -619,7 +631,9 @@ static int launch_topk(const float* partial, int splits, float temperature, floa
 //      (weight descending, then route id: src/quantweave_moe_model.py:174-175)
 //      and writes its slot, or its dropped entry.
 // Optionally the same workgroup writes cast_out = bf16(cast_x) (or fp16 with
-// cast_f16; n values), the decode step's expert input.
+// cast_f16; n values), the decode step's expert input.  THREADS is 1024, or 64
+// (one wave: its barriers cost next to nothing) for one or two tokens with
+// at most 64 routes and 64 experts, whose cast the router GEMV writes instead.
 // ---------------------------------------------------------------------------
 constexpr int kSmallThreads = 1024;
 constexpr int kSmallTokens = 64;       // tokens of the one-workgroup plan
@@ -627,8 +641,8 @@ constexpr int kSmallRouteTokens = 16;  // tokens it also routes (one per wave)
 constexpr int kSmallRoutes = 256;
 constexpr int kSmallLogits = 8192;  // T*E logits staged in LDS
 
-template <int EPL>
-__global__ __launch_bounds__(kSmallThreads) void route_plan_small_kernel(
+template <int EPL, int THREADS>
+__global__ __launch_bounds__(THREADS) void route_plan_small_kernel(
     int routed, const float* __restrict__ partial, int splits, float temperature, float* __restrict__ logits, int T,
     int E, int K, const float* __restrict__ bias, int select_logits,
     float* __restrict__ probs, int32_t* __restrict__ top_idx, float* __restrict__ top_w, int capacity,
@@ -636,7 +650,7 @@ __global__ __launch_bounds__(kSmallThreads) void route_plan_small_kernel(
     int32_t* __restrict__ totals, int32_t* __restrict__ slot_token, float* __restrict__ slot_weight,
     int32_t* __restrict__ route_slot, int32_t* __restrict__ dropped_token, int32_t* __restrict__ dropped_expert,
     const float* __restrict__ cast_x, int cast_n, uint16_t* __restrict__ cast_out, int cast_f16) {
-  constexpr int kWaves = kSmallThreads / kWave;
+  constexpr int kWaves = THREADS / kWave;
   __shared__ float s_logit[kSmallLogits];
   __shared__ int s_e[kSmallRoutes];
   __shared__ float s_w[kSmallRoutes];
@@ -646,9 +660,9 @@ __global__ __launch_bounds__(kSmallThreads) void route_plan_small_kernel(
   __shared__ uint64_t s_tot;
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const int R = T * K;
-  for (int i = tid; i < E; i += kSmallThreads) hist[i] = 0;
+  for (int i = tid; i < E; i += THREADS) hist[i] = 0;
   if (cast_out != nullptr) {
-    for (int i = tid * 4; i < cast_n; i += kSmallThreads * 4) {
+    for (int i = tid * 4; i < cast_n; i += THREADS * 4) {
       if (i + 4 <= cast_n && (cast_n & 3) == 0) {
         const float4 v = *reinterpret_cast<const float4*>(cast_x + i);
         uint2 o;
@@ -668,7 +682,7 @@ __global__ __launch_bounds__(kSmallThreads) void route_plan_small_kernel(
   }
   if (routed) {
     // ---- the routing was done by route_topk_kernel: its choices into LDS ----
-    for (int r = tid; r < R; r += kSmallThreads) {
+    for (int r = tid; r < R; r += THREADS) {
       const int me = top_idx[r];
       const float mw = top_w[r];
       s_e[r] = me;
@@ -677,7 +691,7 @@ __global__ __launch_bounds__(kSmallThreads) void route_plan_small_kernel(
     }
   }
   // ---- 0. all logits into LDS at once (summing split-K partials if given) ----
-  for (int i = tid; i < (routed ? 0 : T * E); i += kSmallThreads) {
+  for (int i = tid; i < (routed ? 0 : T * E); i += THREADS) {
     float v;
     if (partial != nullptr) {
       v = partial[i];
@@ -761,18 +775,26 @@ __global__ __launch_bounds__(kSmallThreads) void route_plan_small_kernel(
 
 template <int XD, int WD, int VEC>
 static void launch_router_gemv_tt(const void* x, int64_t x_stride, const void* w, int t, int d, int e,
-                                  float temperature, float* logits, hipStream_t stream) {
+                                  float temperature, float* logits, uint16_t* cast_out, int cast_f16,
+                                  hipStream_t stream) {
   const dim3 g16(e, static_cast<unsigned>(ceil_div(t, 16)));
-  if (t <= 1) router_gemv_kernel<XD, WD, VEC, 1><<<e, 256, 0, stream>>>(x, x_stride, w, t, d, e, temperature, logits);
-  else if (t <= 4) router_gemv_kernel<XD, WD, VEC, 4><<<e, 256, 0, stream>>>(x, x_stride, w, t, d, e, temperature, logits);
-  else router_gemv_kernel<XD, WD, VEC, 16><<<g16, 256, 0, stream>>>(x, x_stride, w, t, d, e, temperature, logits);
+  if (t <= 1)
+    router_gemv_kernel<XD, WD, VEC, 1><<<e, 256, 0, stream>>>(x, x_stride, w, t, d, e, temperature, logits, cast_out,
+                                                              cast_f16);
+  else if (t <= 4)
+    router_gemv_kernel<XD, WD, VEC, 4><<<e, 256, 0, stream>>>(x, x_stride, w, t, d, e, temperature, logits, cast_out,
+                                                              cast_f16);
+  else
+    router_gemv_kernel<XD, WD, VEC, 16><<<g16, 256, 0, stream>>>(x, x_stride, w, t, d, e, temperature, logits,
+                                                                 cast_out, cast_f16);
 }
 
 template <int XD, int WD>
 static void launch_router_gemv_vec(bool vec, const void* x, int64_t x_stride, const void* w, int t, int d, int e,
-                                   float temperature, float* logits, hipStream_t stream) {
-  if (vec) launch_router_gemv_tt<XD, WD, 4>(x, x_stride, w, t, d, e, temperature, logits, stream);
-  else launch_router_gemv_tt<XD, WD, 1>(x, x_stride, w, t, d, e, temperature, logits, stream);
+                                   float temperature, float* logits, uint16_t* cast_out, int cast_f16,
+                                   hipStream_t stream) {
+  if (vec) launch_router_gemv_tt<XD, WD, 4>(x, x_stride, w, t, d, e, temperature, logits, cast_out, cast_f16, stream);
+  else launch_router_gemv_tt<XD, WD, 1>(x, x_stride, w, t, d, e, temperature, logits, cast_out, cast_f16, stream);
 }
 
 // Calls f(XD, WD) with the dtype codes of the router input and weights as
@@ -790,12 +812,13 @@ static void with_router_dtypes(int xdt, int wdt, Fn&& f) {
 }
 
 static int launch_router_gemv(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int t, int d,
-                              int e, float temperature, float* logits, hipStream_t stream) {
+                              int e, float temperature, float* logits, hipStream_t stream,
+                              uint16_t* cast_out = nullptr, int cast_f16 = 0) {
   const bool vec = d % 4 == 0 && x_stride % 4 == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0 &&
                    (reinterpret_cast<uintptr_t>(w) % 16) == 0;
   with_router_dtypes(xdt, wdt, [&](auto xd, auto wd) {
     launch_router_gemv_vec<decltype(xd)::value, decltype(wd)::value>(vec, x, x_stride, w, t, d, e, temperature,
-                                                                       logits, stream);
+                                                                       logits, cast_out, cast_f16, stream);
   });
   QW_LAUNCH_CHECK("router_gemv_kernel");
   return QW_OK;
@@ -837,17 +860,19 @@ size_t route_workspace_bytes(int64_t T, int64_t D, int64_t E) {
 // kernel straight into `logits` (*splits = 0); more by the tiled GEMM into
 // split-K partials (*splits > 0) that the next kernel sums and divides by the
 // temperature.
-static int launch_router(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int64_t T, int64_t D,
-                         int64_t E, float temperature, float* logits, float* partial, size_t partial_bytes,
-                         int* splits_out, hipStream_t stream) {
+static int launch_router_cast(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int64_t T,
+                              int64_t D, int64_t E, float temperature, float* logits, float* partial,
+                              size_t partial_bytes, int* splits_out, hipStream_t stream, uint16_t* cast_out,
+                              int cast_f16) {
   const int t = static_cast<int>(T), d = static_cast<int>(D), e = static_cast<int>(E);
   // The GEMV kernel issues all its loads at once but reads x once per expert:
   // it serves a few tokens, and any batch whose x re-reads stay within 16 MiB
   // (small layers, where the tiled kernel's K loop would wait on every slice).
   if (T <= kGemvMaxTokens || T * E * D * (xdt == QW_F32 ? 4 : 2) <= (int64_t{16} << 20)) {
     *splits_out = 0;
-    return launch_router_gemv(x, xdt, x_stride, w, wdt, t, d, e, temperature, logits, stream);
+    return launch_router_gemv(x, xdt, x_stride, w, wdt, t, d, e, temperature, logits, stream, cast_out, cast_f16);
   }
+  QW_REQUIRE(cast_out == nullptr, "the cast rides on the GEMV router only");
   const int splits = router_splits(T, D, E);
   if (partial_bytes < static_cast<size_t>(splits) * T * E * sizeof(float) || !partial)
     return set_error(QW_ERR_WORKSPACE, "router needs %zu bytes of partial sums", route_workspace_bytes(T, D, E));
@@ -873,6 +898,13 @@ static int launch_router(const void* x, int xdt, int64_t x_stride, const void* w
     QW_LAUNCH_CHECK("router_logits_kernel");
   }
   return QW_OK;
+}
+
+static int launch_router(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int64_t T, int64_t D,
+                         int64_t E, float temperature, float* logits, float* partial, size_t partial_bytes,
+                         int* splits_out, hipStream_t stream) {
+  return launch_router_cast(x, xdt, x_stride, w, wdt, T, D, E, temperature, logits, partial, partial_bytes,
+                            splits_out, stream, nullptr, 0);
 }
 
 int route(const void* x, int xdt, int64_t x_stride, const void* w, int wdt, int64_t T, int64_t D, int64_t E,
@@ -941,28 +973,31 @@ int route_plan_small(const void* x, int xdt, int64_t x_stride, const void* w, in
   if (routed) {
     st = route(x, xdt, x_stride, w, wdt, T, D, E, K, temperature, bias, logits, probs, top_idx, top_w, partial,
                partial_bytes, stream, select_logits);
-  } else {
-    st = launch_router(x, xdt, x_stride, w, wdt, T, D, E, temperature, logits, partial, partial_bytes, &splits,
-                       stream);
+  }
+  // one or two tokens: the GEMV router writes the cast and one wave plans
+  const bool tiny = !routed && T <= 2 && T * K <= kWave && E <= kWave && T <= kGemvMaxTokens &&
+                    (cast_out == nullptr || (cast_x == x && xdt == QW_F32));
+  if (!routed) {
+    st = launch_router_cast(x, xdt, x_stride, w, wdt, T, D, E, temperature, logits, partial, partial_bytes, &splits,
+                            stream, tiny ? cast_out : nullptr, cast_dtype == QW_F16 ? 1 : 0);
   }
   if (st) return st;
   const float* part = splits ? partial : nullptr;
   const int cap = capacity > INT32_MAX ? INT32_MAX : static_cast<int>(capacity);
-  const int n = cast_out ? t * d : 0;
+  const int n = cast_out && !tiny ? t * d : 0;
   const int epl = static_cast<int>(ceil_div(E, kWave));
-#define QW_RP(N)                                                                                                  \
-  route_plan_small_kernel<N><<<1, kSmallThreads, 0, stream>>>(routed, part, splits, temperature, logits, t, e, k, \
-                                                              bias,                                                   \
-                                                              select_logits ? 1 : 0, probs,                           \
-                                                              top_idx, top_w, cap, counts, kept_counts, kept_offsets, \
-                                                              totals, slot_token, slot_weight, route_slot,          \
-                                                              dropped_token, dropped_expert, cast_x, n, cast_out,  \
-                                                              cast_dtype == QW_F16 ? 1 : 0)
-  if (epl <= 1) QW_RP(1);
-  else if (epl <= 2) QW_RP(2);
-  else if (epl <= 4) QW_RP(4);
-  else if (epl <= 8) QW_RP(8);
-  else QW_RP(16);
+#define QW_RP(N, TH)                                                                                          \
+  route_plan_small_kernel<N, TH><<<1, TH, 0, stream>>>(routed, part, splits, temperature, logits, t, e, k, bias, \
+                                                       select_logits ? 1 : 0, probs, top_idx, top_w, cap, counts, \
+                                                       kept_counts, kept_offsets, totals, slot_token, slot_weight, \
+                                                       route_slot, dropped_token, dropped_expert, cast_x, n,       \
+                                                       n ? cast_out : nullptr, cast_dtype == QW_F16 ? 1 : 0)
+  if (tiny) QW_RP(1, kWave);
+  else if (epl <= 1) QW_RP(1, kSmallThreads);
+  else if (epl <= 2) QW_RP(2, kSmallThreads);
+  else if (epl <= 4) QW_RP(4, kSmallThreads);
+  else if (epl <= 8) QW_RP(8, kSmallThreads);
+  else QW_RP(16, kSmallThreads);
 #undef QW_RP
   QW_LAUNCH_CHECK("route_plan_small_kernel");
   return QW_OK;
