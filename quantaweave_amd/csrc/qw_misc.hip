@@ -396,41 +396,74 @@ __global__ __launch_bounds__(256) void importance_partial_kernel(const float* __
   const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
   const int e = blockIdx.y * 64 + lane;
   const int t0 = blockIdx.x * kImpRows, t1 = min(T, t0 + kImpRows);
+  // all of the thread's loads in flight at once, then added in token order
+  // (a token past the end adds +0, which leaves the non-negative sum as it is)
+  float v[kImpRows / 4];
+#pragma unroll
+  for (int i = 0; i < kImpRows / 4; ++i) {
+    const int t = t0 + wave + 4 * i;
+    v[i] = (e < E && t < t1) ? probs[static_cast<int64_t>(t) * E + e] : 0.0f;
+  }
   float s = 0.0f;
-  if (e < E)
-    for (int t = t0 + wave; t < t1; t += 4) s += probs[static_cast<int64_t>(t) * E + e];
+#pragma unroll
+  for (int i = 0; i < kImpRows / 4; ++i) s += v[i];
   red[wave][lane] = s;
   __syncthreads();
   if (wave == 0 && e < E)
     partial[static_cast<int64_t>(blockIdx.x) * E + e] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
 }
 
-// One workgroup: wave w takes experts w, w + 16, ...; for expert e lane l adds
-// the partials l, l + 64, ... in order and the 64 lane sums meet in a fixed
-// xor butterfly, so importance[e] = sum / T does not depend on scheduling.
-// The balance term is then summed over experts in ascending order by one thread.
+// One workgroup of 16 waves; lane l holds expert e0 + l of each 64-expert
+// block.  Wave w adds the partial rows w, w + 16, ... in order (whole rows:
+// coalesced loads, all of a wave's rows in flight together), the 16 wave sums
+// are added in wave order, so importance[e] = sum / T does not depend on
+// scheduling.  The balance term is then summed over experts in ascending order
+// by one thread.
 __global__ __launch_bounds__(1024) void importance_final_kernel(const float* __restrict__ partial, int nb, int T,
                                                                 int K, int E, const int32_t* __restrict__ counts,
                                                                 float* __restrict__ importance,
                                                                 float* __restrict__ balance) {
+  constexpr int kW = 16, kRowsPerLoad = 8;
   __shared__ float term[1024];
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
+  __shared__ float red[kW][kWave];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const float routes = static_cast<float>(static_cast<int64_t>(T) * K);
-  for (int e = wave; e < E; e += waves) {
+  for (int e0 = 0; e0 < E; e0 += kWave) {
+    const int e = e0 + lane;
     float s = 0.0f;
-    for (int b = lane; b < nb; b += kWave) s += partial[static_cast<int64_t>(b) * E + e];
+    for (int b0 = wave; b0 < nb; b0 += kW * kRowsPerLoad) {
+      float v[kRowsPerLoad];
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, kWave);
-    if (lane == 0) {
-      const float imp = s / static_cast<float>(T);
+      for (int i = 0; i < kRowsPerLoad; ++i) {
+        const int b = b0 + kW * i;
+        v[i] = (b < nb && e < E) ? partial[static_cast<int64_t>(b) * E + e] : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < kRowsPerLoad; ++i) s += v[i];  // rows in order; +0 past the end (sums are >= 0)
+    }
+    red[wave][lane] = s;
+    __syncthreads();
+    if (wave == 0 && e < E) {
+      float t = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kW; ++w) t += red[w][lane];
+      const float imp = t / static_cast<float>(T);
       importance[e] = imp;
       term[e] = imp * (static_cast<float>(counts[e]) / routes);
     }
+    __syncthreads();
   }
-  __syncthreads();
   if (threadIdx.x == 0) {
+    // ascending order; 16 reads in flight at a time (the terms are >= 0, so
+    // the +0 past E changes nothing)
     float s = 0.0f;
-    for (int e = 0; e < E; ++e) s += term[e];
+    for (int e0 = 0; e0 < E; e0 += 16) {
+      float v[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = e0 + i < E ? term[e0 + i] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s += v[i];
+    }
     *balance = static_cast<float>(E) * s;
   }
 }
