@@ -313,6 +313,23 @@ class TopKMoE(nn.Module):
         self.last_stats: dict[str, Tensor] = {}
         self.last_plan: dict[str, Tensor] = {}
 
+    @property
+    def last_top_indices(self) -> Optional[Tensor]:
+        """The last forward's expert choices [tokens, top_k], int64 as the
+        reference stores them (src/quantweave_moe_model.py:137).  The forward
+        keeps the kernel's int32 choices (a fresh tensor per call) and widens
+        them on first read, so a forward whose choices nobody reads launches
+        no conversion."""
+        v = self.__dict__.get("_last_top_idx")
+        if v is not None and v.dtype != torch.long:
+            v = v.long()
+            self.__dict__["_last_top_idx"] = v
+        return v
+
+    @last_top_indices.setter
+    def last_top_indices(self, value: Optional[Tensor]) -> None:
+        self.__dict__["_last_top_idx"] = value
+
     def capacity(self, num_tokens: int) -> int:
         """Route slots per expert (src/quantweave_moe_model.py:100-111)."""
         if self.capacity_factor > 0 and self.drop_overflow_tokens:
@@ -377,12 +394,14 @@ class TopKMoE(nn.Module):
     def _finish(self, out, probs, balance, top_idx, top_w, counts, kept_counts, totals, dropped_token, dropped_expert,
                 token_domains, num_domains, shape):
         dev = out.device
-        self.last_top_indices = top_idx.long()
+        self.last_top_indices = top_idx  # widened to int64 when read
         self.last_plan = dict(counts=counts, kept_counts=kept_counts, totals=totals, top_w=top_w,
                               dropped_token=dropped_token, dropped_expert=dropped_expert)
         overflow_routes = totals[1].long()
-        zero = torch.zeros((), device=dev, dtype=torch.long)
-        dropped_routes = overflow_routes if self.overflow_policy == "drop" else zero
+        if self.overflow_policy == "drop":
+            dropped_routes = overflow_routes
+        else:
+            dropped_routes = torch.zeros((), device=dev, dtype=torch.long)
         if self.collect_stats:
             self._record_stats(probs.detach(), top_idx, kept_counts, totals, dropped_token, dropped_expert)
         domain_loss = probs.new_zeros(())
