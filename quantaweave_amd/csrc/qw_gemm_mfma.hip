@@ -326,6 +326,49 @@ __global__ __launch_bounds__(256) void transpose_pad_kernel(const uint16_t* __re
   }
 }
 
+// The same transpose 16 bytes per access (C % 8 == 0, 16-byte aligned rows):
+// a thread loads 8 consecutive columns of a row and stores 8 consecutive rows
+// of a column.  The 16-byte chunk j of tile row i sits at chunk j ^ ((i / 8) % 8),
+// so the column reads (rows 8j .. 8j+7 for the 8 chunks j of a wave) spread
+// over 32 banks.
+__global__ __launch_bounds__(256) void transpose_pad_vec_kernel(const uint16_t* __restrict__ src, int C,
+                                                                const int32_t* __restrict__ offsets,
+                                                                const int32_t* __restrict__ poff, int E, int rows,
+                                                                int64_t ld, uint16_t* __restrict__ dst) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[64][72];  // 144-byte rows
+  int local = 0;
+  const int e = find_tile(offsets, E, rows, 64, blockIdx.y, &local);
+  if (e < 0) return;
+  const int lo = min(max(offsets[e], 0), rows), hi = min(offsets[e + 1], rows);
+  const int len = max(hi - lo, 0);
+  const int r0 = local * 64;
+  const int c0 = blockIdx.x * 64;
+  const int t = threadIdx.x, j = t % 8;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int i = t / 8 + 32 * h;  // tile row
+    const int r = r0 + i, c = c0 + 8 * j;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (r < len && c < C) v = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(lo + r) * C + c);
+    *reinterpret_cast<uint4*>(&tile[i][8 * (j ^ ((i / 8) % 8))]) = v;
+  }
+  __syncthreads();
+  const int64_t col0 = poff[e] + r0;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int cc = t / 8 + 32 * h;  // tile column = output row
+    const int c = c0 + cc;
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t a = tile[8 * j + 2 * q][8 * ((cc / 8) ^ j) + cc % 8];
+      const uint32_t b = tile[8 * j + 2 * q + 1][8 * ((cc / 8) ^ j) + cc % 8];
+      w[q] = a | (b << 16);
+    }
+    if (c < C) *reinterpret_cast<uint4*>(dst + static_cast<int64_t>(c) * ld + col0 + 8 * j) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 template <int DT, int MODE, bool ACCUM, bool BRED = false, bool C32 = false>
 int launch_gemm(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t b_stride, void* C, int64_t ldc,
                 int64_t c_stride, const int32_t* offsets, int rows, int M, int N, int K, int E, int64_t m_extent,
@@ -410,9 +453,18 @@ int gemm_backward_t(const void* gy, const void* x, const void* w, int64_t E, int
       const int64_t rt = ceil_div(rows, 64) + E;  // 64-row tiles of all experts, at most
       if (rt > 65535) return set_error(QW_ERR_UNSUPPORTED, "too many row tiles for the transpose grid");
       const dim3 g1(static_cast<unsigned>(ceil_div(N, 64)), static_cast<unsigned>(rt));
-      transpose_pad_kernel<<<g1, 256, 0, stream>>>(static_cast<const uint16_t*>(gy), n, offsets, poff, e, r, rp, gyt);
       const dim3 g2(static_cast<unsigned>(ceil_div(K, 64)), static_cast<unsigned>(rt));
-      transpose_pad_kernel<<<g2, 256, 0, stream>>>(static_cast<const uint16_t*>(x), k, offsets, poff, e, r, rp, xt);
+      auto vec_ok = [](const void* p, int64_t cols) { return cols % 8 == 0 && reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+      if (vec_ok(gy, N))
+        transpose_pad_vec_kernel<<<g1, 256, 0, stream>>>(static_cast<const uint16_t*>(gy), n, offsets, poff, e, r, rp,
+                                                         gyt);
+      else
+        transpose_pad_kernel<<<g1, 256, 0, stream>>>(static_cast<const uint16_t*>(gy), n, offsets, poff, e, r, rp, gyt);
+      if (vec_ok(x, K))
+        transpose_pad_vec_kernel<<<g2, 256, 0, stream>>>(static_cast<const uint16_t*>(x), k, offsets, poff, e, r, rp,
+                                                         xt);
+      else
+        transpose_pad_kernel<<<g2, 256, 0, stream>>>(static_cast<const uint16_t*>(x), k, offsets, poff, e, r, rp, xt);
       QW_LAUNCH_CHECK("transpose_pad_kernel");
     }
     return gw_f32 ? launch_gemm<DT, MODE_RED, false, false, true>(gyt, rp, xt, rp, 0, gw, K, N * K, poff, r, n, k,
