@@ -222,6 +222,81 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(const uint16_t* __restrict
 #undef QW_LO2
 #undef QW_HI2
 
+  // ---- epilogue through LDS when the output rows are 16-byte aligned: the fp32
+  //      tile (the stages are free after the loop's last barrier) leaves in
+  //      whole row segments, 16 bytes per lane.  Chunk c (4 fp32) of tile row m
+  //      sits at chunk c ^ (m & 15), so the 16 rows of an MFMA tile write 16
+  //      different bank groups.  Same sums and roundings as the direct stores
+  //      below (the accumulate path adds the old value before rounding). ----
+  {
+    constexpr int ES = C32 ? 4 : 2;  // output bytes per element
+    constexpr int OV = 16 / ES;      // output elements per 16-byte store
+    static_assert(GT * GT * 4 <= G_LDS, "the fp32 tile fits the stages");
+    const bool aligned = (reinterpret_cast<uintptr_t>(static_cast<char*>(C) + (c_off + n0) * ES) % 16) == 0 &&
+                         ((ldc * ES) % 16) == 0;
+    if (aligned) {
+      float* const t = reinterpret_cast<float*>(smem);  // [GT][GT]
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int m = wm * 64 + 16 * i + l16, n = wn * 64 + 16 * j + 4 * lq;
+          *reinterpret_cast<f32x4*>(t + m * GT + 4 * ((n / 4) ^ (m & 15))) = acc[i][j];
+        }
+      __syncthreads();
+      constexpr int CPR = GT / OV;  // 16-byte output chunks per tile row
+      for (int c = tid; c < mcount * CPR; c += 256) {
+        const int r = c / CPR, n = (c % CPR) * OV;
+        if (n >= ncount) continue;
+        float v[OV];
+#pragma unroll
+        for (int h = 0; h < OV / 4; ++h) {
+          const f32x4 x = *reinterpret_cast<const f32x4*>(t + r * GT + 4 * ((n / 4 + h) ^ (r & 15)));
+#pragma unroll
+          for (int u = 0; u < 4; ++u) v[4 * h + u] = x[u];
+        }
+        const int64_t o = c_off + static_cast<int64_t>(r) * ldc + n0 + n;
+        if constexpr (C32) {
+          float* co = static_cast<float*>(C) + o;
+          if (n + OV <= ncount) {
+            if (ACCUM) {
+              const float4 old = *reinterpret_cast<const float4*>(co);
+              v[0] += old.x;
+              v[1] += old.y;
+              v[2] += old.z;
+              v[3] += old.w;
+            }
+            *reinterpret_cast<float4*>(co) = make_float4(v[0], v[1], v[2], v[3]);
+          } else {
+            for (int u = 0; u < OV && n + u < ncount; ++u) co[u] = v[u] + (ACCUM ? co[u] : 0.0f);
+          }
+        } else {
+          uint16_t* co = static_cast<uint16_t*>(C) + o;
+          if (n + OV <= ncount) {
+            uint32_t w[OV / 2];
+            if (ACCUM) {
+              const uint4 old = *reinterpret_cast<const uint4*>(co);
+              const uint32_t ow[4] = {old.x, old.y, old.z, old.w};
+#pragma unroll
+              for (int u = 0; u < 4; ++u) {
+                v[2 * u] += half_to_f32<DT>(ow[u] & 0xffffu);
+                v[2 * u + 1] += half_to_f32<DT>(ow[u] >> 16);
+              }
+            }
+#pragma unroll
+            for (int u = 0; u < OV / 2; ++u)
+              w[u] = f32_to_half<DT>(v[2 * u]) | (static_cast<uint32_t>(f32_to_half<DT>(v[2 * u + 1])) << 16);
+            *reinterpret_cast<uint4*>(co) = make_uint4(w[0], w[1], w[2], w[3]);
+          } else {
+            for (int u = 0; u < OV && n + u < ncount; ++u)
+              co[u] = f32_to_half<DT>(v[u] + (ACCUM ? half_to_f32<DT>(co[u]) : 0.0f));
+          }
+        }
+      }
+      return;
+    }
+  }
+
   // lane holds C[m = 16 i + l16][n = 16 j + 4 lq + v] of its wave's quarter;
   // C32: fp32 output, else the operands' 16-bit type
   const bool vec = (ldc & 3) == 0;
