@@ -25,6 +25,9 @@ ARCH = "gfx950"
 
 # Files whose arithmetic must be the plain IEEE sequence written in the source.
 NO_CONTRACT = {"qw_route.hip"}
+# Files whose matrix-core results feed VALU work right away: keep them in
+# VGPRs (the AGPR form costs a copy per result register).
+MFMA_VGPR = {"qw_ffn_gemv.hip"}
 
 
 def hipcc() -> str:
@@ -44,6 +47,8 @@ def compile_flags(name: str) -> list[str]:
     ]
     if name in NO_CONTRACT:
         flags.append("-ffp-contract=off")
+    if name in MFMA_VGPR:
+        flags += ["-mllvm", "-amdgpu-mfma-vgpr-form"]
     return flags
 
 

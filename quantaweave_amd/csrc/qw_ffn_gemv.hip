@@ -273,6 +273,28 @@ __device__ __forceinline__ void ring_read4(uint32_t w_addr, uint32_t s_addr, uin
   }
 }
 
+// Six chunks and their scales (the int4 matrix-core kernel's groups of 6).
+__device__ __forceinline__ void ring_read6(uint32_t w_addr, uint32_t s_addr, uint4 (&w)[8], float (&sv)[8]) {
+  asm volatile(
+      "ds_read_b128 %0, %12\n"
+      "ds_read_b128 %1, %12 offset:1024\n"
+      "ds_read_b128 %2, %12 offset:2048\n"
+      "ds_read_b128 %3, %12 offset:3072\n"
+      "ds_read_b128 %4, %12 offset:4096\n"
+      "ds_read_b128 %5, %12 offset:5120\n"
+      "ds_read_b32 %6, %13\n"
+      "ds_read_b32 %7, %13 offset:256\n"
+      "ds_read_b32 %8, %13 offset:512\n"
+      "ds_read_b32 %9, %13 offset:768\n"
+      "ds_read_b32 %10, %13 offset:1024\n"
+      "ds_read_b32 %11, %13 offset:1280\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]), "=&v"(sv[0]), "=&v"(sv[1]),
+        "=&v"(sv[2]), "=&v"(sv[3]), "=&v"(sv[4]), "=&v"(sv[5])
+      : "v"(w_addr), "v"(s_addr)
+      : "memory");
+}
+
 // LDS byte address of a pointer into the kernel's dynamic LDS.
 __device__ __forceinline__ uint32_t lds_addr(const char* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
@@ -557,6 +579,285 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// int4 experts with the dot products on the matrix cores (decode rows).
+//
+// v_mfma_f32_4x4x4_16b (bf16 or f16 operands) forms 16 independent 4x4
+// products over 4 k values: in block b = lane / 4, lane 4b + i supplies row i
+// of A, lane 4b + j column j of B, and lane 4b + j receives D[i][j] in its
+// result register i.  Here lane 4b + t supplies route t's activations (A row t)
+// and weight row t of the current row set (B column t), and the 16 blocks work
+// on 16 different chunks of the rows; one instruction therefore forms the
+// products of 4 routes with 4 weight rows over 4 codes of 16 chunks.  Unlike
+// the dot-product kernel above, the VALU work per weight (the code conversion
+// and one scale per chunk) does not grow with the number of routes.
+//
+// A dword of 8 codes (byte j holds codes 2j and 2j + 1, low nibble first)
+// becomes the operand pairs (0, 2), (4, 6), (1, 3), (5, 7) as in the kernel
+// above: the low and the high nibbles are masked into bytes (an AND, a shift and
+// an AND) and v_perm puts each pair under the high byte 0x43 (bf16 128 + u) or
+// 0x64 (fp16 1024 + u).  The activations are put in the same order once per
+// pass by v_perm.  A chunk's chain of 8 instructions yields
+// sum x * (magic value + u); its result times the chunk's group scale is
+// accumulated, and one fp32 4x4x1 product per chunk adds
+// -(magic value + 8) * (the chunk's sum of x) * scale for the 4 routes and 4
+// rows, which removes both the magic offset and the +8 storage bias of the
+// codes u = q + 8 without VALU work.
+//
+// Lane (b, t) holds chunks c = 16 s + b (s < S) of every row it streams, so one
+// row set of 4 rows takes S chunk loads per lane and a group of R row sets
+// S * R loads, through the same two-stage ring of global_load_lds as above.
+// GATEUP row sets are (gate u, up u, gate u + 1, up u + 1); DOWN row sets are 4
+// consecutive output rows.  The partial sums of the 16 blocks are added with a
+// reduce-scatter over lane bits 5..2 (ds_bpermute for 32, ds_swizzle below).
+
+typedef _Float16 gf16x4 __attribute__((ext_vector_type(4)));
+typedef short gs16x4 __attribute__((ext_vector_type(4)));
+typedef float gf32x4 __attribute__((ext_vector_type(4)));
+
+// One 4x4x4 product of 16 blocks on two packed pairs of A and of B.
+template <int ACT>
+__device__ __forceinline__ gf32x4 mfma4(uint2 a, uint2 b, gf32x4 c) {
+  if constexpr (ACT == QW_F16)
+    return __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(gf16x4, a), __builtin_bit_cast(gf16x4, b), c, 0, 0,
+                                              0);
+  else
+    return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(gs16x4, a), __builtin_bit_cast(gs16x4, b), c, 0,
+                                                  0, 0);
+}
+
+template <int NCH, int UPG, int NST>
+struct Q4Lds {
+  static constexpr int STAGE = NCH * 1024 + NCH * 256;  // chunks, then their scales
+  static constexpr int STAGES = NST;
+  static constexpr int NDMA = 2 * NCH;
+  static constexpr int OUT = GV_GPW_MAX * UPG * 4 * 4;  // fp32, 4 routes per unit
+  static constexpr int BYTES = STAGES * STAGE + OUT;
+};
+
+// Value of lane (lane ^ O) for O in 4, 8, 16 (ds_swizzle, bit mode) or 32
+// (ds_bpermute with the byte address of lane ^ 32 in addr32).
+template <int O>
+__device__ __forceinline__ float xor_lane(float v, int addr32) {
+  if constexpr (O == 32) return __int_as_float(__builtin_amdgcn_ds_bpermute(addr32, __float_as_int(v)));
+  else return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (O << 10) | 0x1F));
+}
+
+// Sum over lane bits O..4 of V values per lane: the first log2(V) steps halve
+// the values a lane holds (bit O set keeps the upper half), the rest add.  A
+// lane ends with value (lane >> (6 - log2 V)) & (V - 1), summed over the 16
+// lanes that share lane bits 0 and 1.
+template <int V, int N, int O>
+__device__ __forceinline__ void rs_blocks(float (&v)[V], int lane, int addr32) {
+  if constexpr (O >= 4) {
+    if constexpr (N > 1) {
+      constexpr int half = N / 2;
+      const bool upper = lane & O;
+#pragma unroll
+      for (int i = 0; i < half; ++i) {
+        const float give = upper ? v[i] : v[i + half];
+        const float keep = upper ? v[i + half] : v[i];
+        v[i] = keep + xor_lane<O>(give, addr32);
+      }
+      rs_blocks<V, half, O / 2>(v, lane, addr32);
+    } else {
+      v[0] += xor_lane<O>(v[0], addr32);
+      rs_blocks<V, 1, O / 2>(v, lane, addr32);
+    }
+  }
+}
+
+// Broadcast of lane 4 * (lane / 4) + I's value to the 4 lanes of its quad.
+template <int I>
+__device__ __forceinline__ float quad_bcast(float v) {
+  return __uint_as_float(dpp_u32<I * 0x55>(__float_as_uint(v)));
+}
+
+// FULL: rows of exactly 16 S chunks with one scale per chunk (group 32), so a
+// slot's chunk and scale offsets are a lane constant plus an immediate.
+template <int ACT, bool GATEUP, int S, int R, bool FULL, int NST>
+__global__ __launch_bounds__(64) void ffn_q4mf_kernel(
+    const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
+    int n_experts, int max_rows, WView wa, WView wb, int K, int n_out, int gpw, const float* __restrict__ row_weight,
+    uint16_t* __restrict__ out) {
+  constexpr int NCH = S * R;                     // chunk loads per lane and group
+  constexpr int UPG = GATEUP ? 2 * R : 4 * R;    // units (hidden columns or output rows) per group
+  constexpr int V = 4 * R;                       // values per lane reduced per group: (row set, route)
+  constexpr int L = log2i<V>();
+  static_assert(NCH == 4 || NCH == 6 || NCH == 8, "the ring reads four, six or eight chunks per group");
+  static_assert(V <= 16, "at most four row sets per group");
+  static_assert(NST >= 2 && NST <= 4, "two to four ring stages");
+  using LD = Q4Lds<NCH, UPG, NST>;
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  int r_lo = 0, r_hi = 0;
+  const int e = nth_active_expert(offsets, n_experts, max_rows, blockIdx.y, &r_lo, &r_hi);
+  if (e < 0) return;
+  const int lane = threadIdx.x;
+  const int blk = lane >> 2, t = lane & 3;
+  const int n_groups = (n_out + UPG - 1) / UPG;
+  const int g_first = blockIdx.x * gpw;
+  if (g_first >= n_groups) return;
+  const int g_end = min(g_first + gpw, n_groups);
+  char* const ring = smem;
+  float* const staged = reinterpret_cast<float*>(smem + LD::STAGES * LD::STAGE);
+  const int KC = K / 32;
+  const int cpg = static_cast<int>(wa.group / 32);  // chunks per quantisation group
+  // Loads are coalesced: lane 16 t' + j fetches row t' of the row set, chunk
+  // 16 s + (j ^ 4 t'), so each quad of lanes reads 64 contiguous bytes; the
+  // chunk lands at ring slot 16 t' + j, and lane (b, t) reads row t, chunk b
+  // from slot 16 t + (b ^ 4 t) (16 lanes in a row cover all 16 slot offsets: no
+  // bank conflicts).
+  const int ld_row = lane >> 4, ld_blk = (lane & 15) ^ (4 * ld_row);
+  const int rd_slot = 16 * t + (blk ^ (4 * t));
+  // the loading lane's matrix: gate/up row sets alternate gate (even) and up (odd) rows
+  const bool up_row = GATEUP && (ld_row & 1);
+  const uint8_t* const wbase =
+      static_cast<const uint8_t*>(up_row ? wb.w : wa.w) + e * (up_row ? wb.expert_elems : wa.expert_elems);
+  const float* const sbase = (up_row ? wb.scales : wa.scales) + e * (up_row ? wb.expert_scales : wa.expert_scales);
+  const int64_t wstride = wa.row_stride;  // bytes per int4 row
+  const int sstride = static_cast<int>(wa.groups);
+  // chunk and scale index of slot s for the loading lane (chunks past the row end
+  // are loaded, never used)
+  auto chunk_of = [&](int s) { return FULL ? 16 * s + ld_blk : min(16 * s + ld_blk, KC - 1); };
+  auto scale_of = [&](int s) { return FULL ? 16 * s + ld_blk : chunk_of(s) / cpg; };
+  const int addr32 = (lane ^ 32) << 2;
+
+  // DMA of group g into its ring stage
+  auto issue = [&](int g) {
+    char* st = ring + ((g - g_first) % LD::STAGES) * LD::STAGE;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int n = min(GATEUP ? g * UPG + 2 * r + (ld_row >> 1) : g * UPG + 4 * r + ld_row, n_out - 1);
+      const uint8_t* wrow = wbase + static_cast<int64_t>(n) * wstride;
+      const float* srow = sbase + static_cast<int64_t>(n) * sstride;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const int q = r * S + s;
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(wrow + 16 * chunk_of(s)),
+                                         (lds_void*)(st + q * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(srow + scale_of(s)),
+                                         (lds_void*)(st + NCH * 1024 + q * 256), 4, 0, 0);
+      }
+    }
+  };
+
+  for (int m0 = r_lo; m0 < r_hi; m0 += 4) {
+    const int M = min(4, r_hi - m0);
+    const bool live = t < M;  // this lane's route exists
+    const int xr = live ? (row_index ? row_index[m0 + t] : m0 + t) : 0;
+#pragma unroll
+    for (int i = 0; i < LD::STAGES - 1; ++i)
+      if (g_first + i < g_end) issue(g_first + i);
+    // ---- activations of route t for this lane's chunks, in the operand order of the codes ----
+    uint2 xa[S][8];  // A operands: per chunk 8 instructions of 4 activations
+    float cz[S];     // this route's chain start per chunk
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const bool ok = live && 16 * s + blk < KC;
+      const int c = min(16 * s + blk, KC - 1);
+      const uint4* src = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(xr) * K + 32 * c);
+      float z = 0.0f;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const uint4 v = ok ? src[p] : make_uint4(0u, 0u, 0u, 0u);  // pairs (0,1) (2,3) (4,5) (6,7)
+        // (0, 2, 4, 6) and (1, 3, 5, 7): the order of the code pairs below
+        xa[s][2 * p] = make_uint2(__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x05040100u));
+        xa[s][2 * p + 1] =
+            make_uint2(__builtin_amdgcn_perm(v.y, v.x, 0x07060302u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u));
+        const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int h = 0; h < 4; ++h)  // + x[2h] + x[2h+1]
+          z = ACT == QW_F16 ? dot2_f16(vv[h], 0x3c003c00u, z) : dot2_bf16(vv[h], 0x3f803f80u, z);
+      }
+      cz[s] = -(ACT == QW_F16 ? 1032.0f : 136.0f) * z;
+    }
+    const int idx = (lane >> (6 - L)) & (V - 1);  // value this lane holds after the reduction
+    const int rset = idx >> 2, route = idx & 3;
+    const bool lead = ((lane >> 2) & ((1 << (4 - L)) - 1)) == 0;  // first of the lanes holding this value
+
+    // ---- the groups ----
+    for (int g = g_first; g < g_end; ++g) {
+      // keep STAGES - 1 groups in flight; wait until group g has landed (loads complete in order)
+      if (g + LD::STAGES - 1 < g_end) issue(g + LD::STAGES - 1);
+      const int after = min(LD::STAGES - 1, g_end - 1 - g);  // groups issued after g
+      if (after >= 3) wait_vmcnt<3 * LD::NDMA>();
+      else if (after == 2) wait_vmcnt<2 * LD::NDMA>();
+      else if (after == 1) wait_vmcnt<LD::NDMA>();
+      else wait_vmcnt<0>();
+      const char* st = ring + ((g - g_first) % LD::STAGES) * LD::STAGE;
+      uint4 wq[8];
+      float sq[8];
+      const uint32_t wa_l = lds_addr(st) + rd_slot * 16, sa_l = lds_addr(st + NCH * 1024) + rd_slot * 4;
+      if constexpr (NCH == 8) {
+        ring_read8<true>(wa_l, sa_l, wq, sq);
+      } else if constexpr (NCH == 6) {
+        ring_read6(wa_l, sa_l, wq, sq);
+      } else {
+        uint4 w4[4];
+        float s4[4];
+        ring_read4<true>(wa_l, sa_l, w4, s4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          wq[i] = w4[i];
+          sq[i] = s4[i];
+        }
+      }
+      float acc[V];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        gf32x4 a4 = gf32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          const int q = r * S + s;
+          const uint32_t wd[4] = {wq[q].x, wq[q].y, wq[q].z, wq[q].w};
+          gf32x4 d = gf32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            constexpr uint32_t HB = ACT == QW_F16 ? 0x64646464u : 0x43434343u;
+            const uint32_t lo = wd[p] & 0x0F0F0F0Fu, hi = (wd[p] >> 4) & 0x0F0F0F0Fu;
+            const uint2 b0 = make_uint2(__builtin_amdgcn_perm(HB, lo, 0x04010400u), __builtin_amdgcn_perm(HB, lo, 0x04030402u));
+            const uint2 b1 = make_uint2(__builtin_amdgcn_perm(HB, hi, 0x04010400u), __builtin_amdgcn_perm(HB, hi, 0x04030402u));
+            d = mfma4<ACT>(xa[s][2 * p], b0, d);
+            d = mfma4<ACT>(xa[s][2 * p + 1], b1, d);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) a4[i] = __builtin_fmaf(sq[q], d[i], a4[i]);
+          // bias: D[i][j] += (route i's chunk term) * (row j's scale), the 16 blocks at once
+          a4 = __builtin_amdgcn_mfma_f32_4x4x1f32(cz[s], sq[q], a4, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[4 * r + i] = a4[i];
+      }
+      rs_blocks<V, V, 32>(acc, lane, addr32);
+      const float val = acc[0];
+      float* slot = staged + (g - g_first) * (UPG * 4);
+      if constexpr (GATEUP) {
+        const float up = __uint_as_float(dpp_u32<kDppXor1>(__float_as_uint(val)));  // the up row of the same unit
+        if (lead && !(t & 1)) slot[(2 * rset + (t >> 1)) * 4 + route] = swiglu_act<ACT>(val, up);
+      } else {
+        if (lead) slot[(4 * rset + t) * 4 + route] = val;
+      }
+    }
+    // ---- outputs of the pass: value v = (group, unit, route) of the staging area ----
+    const int n_vals = (g_end - g_first) * UPG * 4;
+    for (int v = lane; v < n_vals; v += 64) {
+      const int gi = v / (UPG * 4), rem = v % (UPG * 4);
+      const int u = rem >> 2, m = rem & 3;
+      const int n = (g_first + gi) * UPG + u;
+      if (m >= M || n >= n_out) continue;
+      const int srow = m0 + m;
+      const float val = staged[v];
+      const int64_t o = static_cast<int64_t>(srow) * n_out + n;
+      if constexpr (GATEUP) {
+        out[o] = f32_to_half<ACT>(val);
+      } else {
+        const float wgt = row_weight ? row_weight[srow] : 1.0f;
+        out[o] = f32_to_half<ACT>(round_act<ACT>(val) * wgt);
+      }
+    }
+  }
+}
+
 // Groups per wave: with 6*4096 groups or more over the touched experts (at
 // most one per row), 6 for gate/up and 4 for down (the fastest of 3, 4, 6 and 8
 // on the int4 and int8 decode layers); below that fewer, so that about 2048
@@ -608,6 +909,56 @@ int launch_one(const FfnArgs& a, const WView& wa, const WView& wb, const void* x
                                                     nullptr, stream);
 }
 
+// The int4 matrix-core kernel for one projection: S chunk slots per lane cover
+// rows of up to 16 S chunks; R row sets per group keep 4 to 8 chunk loads per
+// lane and group.
+#ifndef Q4_STAGES
+#define Q4_STAGES 2
+#endif
+template <int ACT, bool GATEUP, int S, bool FULL, int NST = Q4_STAGES>
+int launch_q4mf_s(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
+                  int n_out, const float* row_weight, void* out, hipStream_t stream) {
+  constexpr int R = S <= 2 ? 4 : S <= 4 ? 2 : 1;
+  constexpr int UPG = GATEUP ? 2 * R : 4 * R;
+  using LD = Q4Lds<S * R, UPG, NST>;
+  auto kernel = ffn_q4mf_kernel<ACT, GATEUP, S, R, FULL, NST>;
+  const hipError_t attr = reserve_lds<ffn_q4mf_kernel<ACT, GATEUP, S, R, FULL, NST>>(LD::BYTES);
+  if (attr != hipSuccess)
+    return set_error(QW_ERR_HIP, "cannot reserve %d bytes of LDS: %s", LD::BYTES, hipGetErrorString(attr));
+  const int64_t n_groups = ceil_div(n_out, UPG);
+  const int64_t touched = a.max_rows < a.experts ? a.max_rows : a.experts;
+  // 6 groups per wave from 8192 groups over the touched experts (the fastest of
+  // 2, 3, 4, 6 and 8 on the int4 decode layer), fewer below
+  const int gpw = touched * n_groups >= 8192 ? 6 : groups_per_wave(touched, n_groups, GATEUP);
+  static_assert(GV_GPW_MAX >= 6, "staging holds the groups of one wave");
+  const dim3 grid(static_cast<unsigned>(ceil_div(n_groups, gpw)), static_cast<unsigned>(touched));
+  kernel<<<grid, 64, LD::BYTES, stream>>>(static_cast<const uint16_t*>(x), row_index, a.offsets,
+                                          static_cast<int>(a.experts), static_cast<int>(a.max_rows), wa, wb, K, n_out,
+                                          gpw, row_weight, static_cast<uint16_t*>(out));
+  QW_LAUNCH_CHECK(GATEUP ? "ffn_q4mf_kernel<gateup>" : "ffn_q4mf_kernel<down>");
+  return QW_OK;
+}
+
+template <int ACT, bool GATEUP, int S>
+int launch_q4mf_full(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
+                     int n_out, const float* row_weight, void* out, hipStream_t stream) {
+  if (K / 32 == 16 * S && wa.group == 32)
+    return launch_q4mf_s<ACT, GATEUP, S, true>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+  return launch_q4mf_s<ACT, GATEUP, S, false>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+}
+
+template <int ACT, bool GATEUP>
+int launch_q4mf(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
+                int n_out, const float* row_weight, void* out, hipStream_t stream) {
+  const int KC = K / 32;
+  if (KC <= 16) return launch_q4mf_full<ACT, GATEUP, 1>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+  if (KC <= 32) return launch_q4mf_full<ACT, GATEUP, 2>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+  if (KC <= 48) return launch_q4mf_full<ACT, GATEUP, 3>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+  if (KC <= 64) return launch_q4mf_full<ACT, GATEUP, 4>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+  if (KC <= 96) return launch_q4mf_full<ACT, GATEUP, 6>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+  return launch_q4mf_full<ACT, GATEUP, 8>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+}
+
 // Units per group for a row of CPL chunks per lane: 4 weight chunks (16-byte
 // loads) per lane and group (8 for gate/up rows of more than 128 chunks).
 template <int ACT, int WF, bool GATEUP>
@@ -629,11 +980,17 @@ int launch_cpl(const FfnArgs& a, const WView& wa, const WView& wb, const void* x
 template <int ACT, int WF>
 int launch_fmt(const FfnArgs& a, hipStream_t stream) {
   const int D = static_cast<int>(a.d_model), F = static_cast<int>(a.d_ff);
-  int st = launch_cpl<ACT, WF, true>(a, a.gate, a.up, a.x, a.row_index, D, F, nullptr, a.hidden, a.save_gate, a.save_up,
-                                stream);
+  // int4 rows of up to 128 chunks (4096 codes) take the matrix-core kernel
+  constexpr bool Q4 = WF == QW_U4;
+  int st = Q4 && D <= 4096
+               ? launch_q4mf<ACT, true>(a, a.gate, a.up, a.x, a.row_index, D, F, nullptr, a.hidden, stream)
+               : launch_cpl<ACT, WF, true>(a, a.gate, a.up, a.x, a.row_index, D, F, nullptr, a.hidden, a.save_gate,
+                                           a.save_up, stream);
   if (st) return st;
-  return launch_cpl<ACT, WF, false>(a, a.down, a.down, a.hidden, nullptr, F, D, a.row_weight, a.y, a.save_y, nullptr,
-                               stream);
+  return Q4 && F <= 4096
+             ? launch_q4mf<ACT, false>(a, a.down, a.down, a.hidden, nullptr, F, D, a.row_weight, a.y, stream)
+             : launch_cpl<ACT, WF, false>(a, a.down, a.down, a.hidden, nullptr, F, D, a.row_weight, a.y, a.save_y,
+                                          nullptr, stream);
 }
 
 }  // namespace
