@@ -675,11 +675,16 @@ __device__ __forceinline__ float quad_bcast(float v) {
 
 // FULL: rows of exactly 16 S chunks with one scale per chunk (group 32), so a
 // slot's chunk and scale offsets are a lane constant plus an immediate.
-template <int ACT, bool GATEUP, int S, int R, bool FULL, int NST>
-__global__ __launch_bounds__(64) void ffn_q4mf_kernel(
+template <int ACT, int WF, bool GATEUP, int S, int R, bool FULL, int NST>
+__global__ __launch_bounds__(64) void ffn_qmf_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
     int n_experts, int max_rows, WView wa, WView wb, int K, int n_out, int gpw, const float* __restrict__ row_weight,
     uint16_t* __restrict__ out) {
+  constexpr bool I8 = WF == QW_I8;
+  static_assert(WF == QW_U4 || WF == QW_I8, "int4 or int8 weights");
+  constexpr int CW = I8 ? 16 : 32;               // codes per 16-byte chunk
+  constexpr int NMF = CW / 4;                    // 4x4x4 products per chunk
+  constexpr int MT = (I8 || ACT == QW_F16) ? QW_F16 : QW_BF16;  // operand type of the products
   constexpr int NCH = S * R;                     // chunk loads per lane and group
   constexpr int UPG = GATEUP ? 2 * R : 4 * R;    // units (hidden columns or output rows) per group
   constexpr int V = 4 * R;                       // values per lane reduced per group: (row set, route)
@@ -700,8 +705,8 @@ __global__ __launch_bounds__(64) void ffn_q4mf_kernel(
   const int g_end = min(g_first + gpw, n_groups);
   char* const ring = smem;
   float* const staged = reinterpret_cast<float*>(smem + LD::STAGES * LD::STAGE);
-  const int KC = K / 32;
-  const int cpg = static_cast<int>(wa.group / 32);  // chunks per quantisation group
+  const int KC = K / CW;
+  const int cpg = static_cast<int>(wa.group / CW);  // chunks per quantisation group
   // Loads are coalesced: lane 16 t' + j fetches row t' of the row set, chunk
   // 16 s + (j ^ 4 t'), so each quad of lanes reads 64 contiguous bytes; the
   // chunk lands at ring slot 16 t' + j, and lane (b, t) reads row t, chunk b
@@ -714,12 +719,26 @@ __global__ __launch_bounds__(64) void ffn_q4mf_kernel(
   const uint8_t* const wbase =
       static_cast<const uint8_t*>(up_row ? wb.w : wa.w) + e * (up_row ? wb.expert_elems : wa.expert_elems);
   const float* const sbase = (up_row ? wb.scales : wa.scales) + e * (up_row ? wb.expert_scales : wa.expert_scales);
-  const int64_t wstride = wa.row_stride;  // bytes per int4 row
+  const int64_t wstride = wa.row_stride;  // bytes per stored row
   const int sstride = static_cast<int>(wa.groups);
   // chunk and scale index of slot s for the loading lane (chunks past the row end
-  // are loaded, never used)
-  auto chunk_of = [&](int s) { return FULL ? 16 * s + ld_blk : min(16 * s + ld_blk, KC - 1); };
-  auto scale_of = [&](int s) { return FULL ? 16 * s + ld_blk : chunk_of(s) / cpg; };
+  // are loaded, never used); FULL: one scale per chunk and no clamping
+  int cidx[FULL ? 1 : S], sidx[FULL ? 1 : S];
+  if constexpr (!FULL) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      cidx[s] = min(16 * s + ld_blk, KC - 1);
+      sidx[s] = cidx[s] / cpg;
+    }
+  }
+  auto chunk_of = [&](int s) {
+    if constexpr (FULL) return 16 * s + ld_blk;
+    else return cidx[s];
+  };
+  auto scale_of = [&](int s) {
+    if constexpr (FULL) return 16 * s + ld_blk;
+    else return sidx[s];
+  };
   const int addr32 = (lane ^ 32) << 2;
 
   // DMA of group g into its ring stage
@@ -749,31 +768,104 @@ __global__ __launch_bounds__(64) void ffn_q4mf_kernel(
     for (int i = 0; i < LD::STAGES - 1; ++i)
       if (g_first + i < g_end) issue(g_first + i);
     // ---- activations of route t for this lane's chunks, in the operand order of the codes ----
-    uint2 xa[S][8];  // A operands: per chunk 8 instructions of 4 activations
-    float cz[S];     // this route's chain start per chunk
+    uint2 xa[S][NMF];  // A operands: per chunk NMF instructions of 4 activations
+    float cz[S];       // this route's bias term per chunk
+    float inv_own = 1.0f;  // int8: 1 / sigma of this lane's route
+    if constexpr (!I8) {
 #pragma unroll
-    for (int s = 0; s < S; ++s) {
-      const bool ok = live && 16 * s + blk < KC;
-      const int c = min(16 * s + blk, KC - 1);
-      const uint4* src = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(xr) * K + 32 * c);
-      float z = 0.0f;
+      for (int s = 0; s < S; ++s) {
+        const bool ok = live && 16 * s + blk < KC;
+        const int c = min(16 * s + blk, KC - 1);
+        const uint4* src = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(xr) * K + 32 * c);
+        float z = 0.0f;
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const uint4 v = ok ? src[p] : make_uint4(0u, 0u, 0u, 0u);  // pairs (0,1) (2,3) (4,5) (6,7)
-        // (0, 2, 4, 6) and (1, 3, 5, 7): the order of the code pairs below
-        xa[s][2 * p] = make_uint2(__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x05040100u));
-        xa[s][2 * p + 1] =
-            make_uint2(__builtin_amdgcn_perm(v.y, v.x, 0x07060302u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u));
-        const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+        for (int p = 0; p < 4; ++p) {
+          const uint4 v = ok ? src[p] : make_uint4(0u, 0u, 0u, 0u);  // pairs (0,1) (2,3) (4,5) (6,7)
+          // (0, 2, 4, 6) and (1, 3, 5, 7): the order of the code pairs below
+          xa[s][2 * p] =
+              make_uint2(__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x05040100u));
+          xa[s][2 * p + 1] =
+              make_uint2(__builtin_amdgcn_perm(v.y, v.x, 0x07060302u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u));
+          const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int h = 0; h < 4; ++h)  // + x[2h] + x[2h+1]
-          z = ACT == QW_F16 ? dot2_f16(vv[h], 0x3c003c00u, z) : dot2_bf16(vv[h], 0x3f803f80u, z);
+          for (int h = 0; h < 4; ++h)  // + x[2h] + x[2h+1]
+            z = ACT == QW_F16 ? dot2_f16(vv[h], 0x3c003c00u, z) : dot2_bf16(vv[h], 0x3f803f80u, z);
+        }
+        cz[s] = -(ACT == QW_F16 ? 1032.0f : 136.0f) * z;
       }
-      cz[s] = -(ACT == QW_F16 ? 1032.0f : 136.0f) * z;
+    } else {
+      // int8: fp16 operands; bf16 activations are scaled by sigma, the power of two
+      // per route bringing its largest |x| into [2^14, 2^15), where they are exact
+      // in fp16 (fp16 activations are used as they are)
+      uint4 raw[S][2];
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const bool ok = live && 16 * s + blk < KC;
+        const int c = min(16 * s + blk, KC - 1);
+        const uint4* src = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(xr) * K + 16 * c);
+#pragma unroll
+        for (int p = 0; p < 2; ++p) raw[s][p] = ok ? src[p] : make_uint4(0u, 0u, 0u, 0u);
+      }
+      float sigma = 1.0f;
+      if constexpr (ACT == QW_BF16) {
+        float amax = 0.0f;
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+          for (int p = 0; p < 2; ++p) {
+            const uint32_t v[4] = {raw[s][p].x, raw[s][p].y, raw[s][p].z, raw[s][p].w};
+#pragma unroll
+            for (int h = 0; h < 4; ++h)
+              amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(v[h] << 16)), fabsf(__uint_as_float(v[h] & 0xffff0000u))));
+          }
+        // the route's largest |x|: the lanes with the same t hold the same route
+        amax = fmaxf(amax, xor_lane<4>(amax, addr32));
+        amax = fmaxf(amax, xor_lane<8>(amax, addr32));
+        amax = fmaxf(amax, xor_lane<16>(amax, addr32));
+        amax = fmaxf(amax, xor_lane<32>(amax, addr32));
+        int ex = 0;
+        frexpf(amax, &ex);  // amax in [2^(ex-1), 2^ex)
+        sigma = amax > 0.0f ? ldexpf(1.0f, 15 - ex) : 1.0f;
+        inv_own = 1.0f / sigma;
+      }
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        uint32_t h2[8];  // fp16 pairs (0,1) .. (14,15)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const uint32_t v[4] = {raw[s][p].x, raw[s][p].y, raw[s][p].z, raw[s][p].w};
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+            if constexpr (ACT == QW_F16) {
+              h2[4 * p + h] = v[h];
+            } else {
+              const _Float16 lo = static_cast<_Float16>(__uint_as_float(v[h] << 16) * sigma);
+              const _Float16 hi = static_cast<_Float16>(__uint_as_float(v[h] & 0xffff0000u) * sigma);
+              h2[4 * p + h] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo)) |
+                              (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
+            }
+          }
+        }
+        float z = 0.0f;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          xa[s][p] = make_uint2(h2[2 * p], h2[2 * p + 1]);
+          z = dot2_f16(h2[2 * p], 0x3c003c00u, z);
+          z = dot2_f16(h2[2 * p + 1], 0x3c003c00u, z);
+        }
+        cz[s] = -1152.0f * z;  // fp16 codes 1024 + u, u = q + 128
+      }
     }
     const int idx = (lane >> (6 - L)) & (V - 1);  // value this lane holds after the reduction
     const int rset = idx >> 2, route = idx & 3;
     const bool lead = ((lane >> 2) & ((1 << (4 - L)) - 1)) == 0;  // first of the lanes holding this value
+    // 1 / sigma of the route this lane's value belongs to (1 for int4)
+    float inv_mine = 1.0f;
+    if constexpr (I8 && ACT == QW_BF16) {
+      const float q0 = quad_bcast<0>(inv_own), q1 = quad_bcast<1>(inv_own), q2 = quad_bcast<2>(inv_own),
+                  q3 = quad_bcast<3>(inv_own);
+      inv_mine = route == 0 ? q0 : route == 1 ? q1 : route == 2 ? q2 : q3;
+    }
 
     // ---- the groups ----
     for (int g = g_first; g < g_end; ++g) {
@@ -813,12 +905,20 @@ __global__ __launch_bounds__(64) void ffn_q4mf_kernel(
           gf32x4 d = gf32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
           for (int p = 0; p < 4; ++p) {
-            constexpr uint32_t HB = ACT == QW_F16 ? 0x64646464u : 0x43434343u;
-            const uint32_t lo = wd[p] & 0x0F0F0F0Fu, hi = (wd[p] >> 4) & 0x0F0F0F0Fu;
-            const uint2 b0 = make_uint2(__builtin_amdgcn_perm(HB, lo, 0x04010400u), __builtin_amdgcn_perm(HB, lo, 0x04030402u));
-            const uint2 b1 = make_uint2(__builtin_amdgcn_perm(HB, hi, 0x04010400u), __builtin_amdgcn_perm(HB, hi, 0x04030402u));
-            d = mfma4<ACT>(xa[s][2 * p], b0, d);
-            d = mfma4<ACT>(xa[s][2 * p + 1], b1, d);
+            constexpr uint32_t HB = MT == QW_F16 ? 0x64646464u : 0x43434343u;
+            if constexpr (I8) {  // codes 4p..4p+3 as fp16 1024 + u, u = q ^ 0x80
+              const uint32_t u = wd[p] ^ 0x80808080u;
+              const uint2 b = make_uint2(__builtin_amdgcn_perm(HB, u, 0x04010400u), __builtin_amdgcn_perm(HB, u, 0x04030402u));
+              d = mfma4<MT>(xa[s][p], b, d);
+            } else {
+              const uint32_t lo = wd[p] & 0x0F0F0F0Fu, hi = (wd[p] >> 4) & 0x0F0F0F0Fu;
+              const uint2 b0 =
+                  make_uint2(__builtin_amdgcn_perm(HB, lo, 0x04010400u), __builtin_amdgcn_perm(HB, lo, 0x04030402u));
+              const uint2 b1 =
+                  make_uint2(__builtin_amdgcn_perm(HB, hi, 0x04010400u), __builtin_amdgcn_perm(HB, hi, 0x04030402u));
+              d = mfma4<MT>(xa[s][2 * p], b0, d);
+              d = mfma4<MT>(xa[s][2 * p + 1], b1, d);
+            }
           }
 #pragma unroll
           for (int i = 0; i < 4; ++i) a4[i] = __builtin_fmaf(sq[q], d[i], a4[i]);
@@ -829,7 +929,7 @@ __global__ __launch_bounds__(64) void ffn_q4mf_kernel(
         for (int i = 0; i < 4; ++i) acc[4 * r + i] = a4[i];
       }
       rs_blocks<V, V, 32>(acc, lane, addr32);
-      const float val = acc[0];
+      const float val = acc[0] * inv_mine;
       float* slot = staged + (g - g_first) * (UPG * 4);
       if constexpr (GATEUP) {
         const float up = __uint_as_float(dpp_u32<kDppXor1>(__float_as_uint(val)));  // the up row of the same unit
@@ -915,14 +1015,14 @@ int launch_one(const FfnArgs& a, const WView& wa, const WView& wb, const void* x
 #ifndef Q4_STAGES
 #define Q4_STAGES 2
 #endif
-template <int ACT, bool GATEUP, int S, bool FULL, int NST = Q4_STAGES>
-int launch_q4mf_s(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
+template <int ACT, int WF, bool GATEUP, int S, bool FULL, int NST = Q4_STAGES>
+int launch_qmf_s(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
                   int n_out, const float* row_weight, void* out, hipStream_t stream) {
   constexpr int R = S <= 2 ? 4 : S <= 4 ? 2 : 1;
   constexpr int UPG = GATEUP ? 2 * R : 4 * R;
   using LD = Q4Lds<S * R, UPG, NST>;
-  auto kernel = ffn_q4mf_kernel<ACT, GATEUP, S, R, FULL, NST>;
-  const hipError_t attr = reserve_lds<ffn_q4mf_kernel<ACT, GATEUP, S, R, FULL, NST>>(LD::BYTES);
+  auto kernel = ffn_qmf_kernel<ACT, WF, GATEUP, S, R, FULL, NST>;
+  const hipError_t attr = reserve_lds<ffn_qmf_kernel<ACT, WF, GATEUP, S, R, FULL, NST>>(LD::BYTES);
   if (attr != hipSuccess)
     return set_error(QW_ERR_HIP, "cannot reserve %d bytes of LDS: %s", LD::BYTES, hipGetErrorString(attr));
   const int64_t n_groups = ceil_div(n_out, UPG);
@@ -935,28 +1035,33 @@ int launch_q4mf_s(const FfnArgs& a, const WView& wa, const WView& wb, const void
   kernel<<<grid, 64, LD::BYTES, stream>>>(static_cast<const uint16_t*>(x), row_index, a.offsets,
                                           static_cast<int>(a.experts), static_cast<int>(a.max_rows), wa, wb, K, n_out,
                                           gpw, row_weight, static_cast<uint16_t*>(out));
-  QW_LAUNCH_CHECK(GATEUP ? "ffn_q4mf_kernel<gateup>" : "ffn_q4mf_kernel<down>");
+  QW_LAUNCH_CHECK(GATEUP ? "ffn_qmf_kernel<gateup>" : "ffn_qmf_kernel<down>");
   return QW_OK;
 }
 
-template <int ACT, bool GATEUP, int S>
-int launch_q4mf_full(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
-                     int n_out, const float* row_weight, void* out, hipStream_t stream) {
-  if (K / 32 == 16 * S && wa.group == 32)
-    return launch_q4mf_s<ACT, GATEUP, S, true>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
-  return launch_q4mf_s<ACT, GATEUP, S, false>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+template <int ACT, int WF, bool GATEUP, int S>
+int launch_qmf_full(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
+                    int n_out, const float* row_weight, void* out, hipStream_t stream) {
+  constexpr int CW = WF == QW_I8 ? 16 : 32;
+  if (K / CW == 16 * S && wa.group == CW)
+    return launch_qmf_s<ACT, WF, GATEUP, S, true>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+  return launch_qmf_s<ACT, WF, GATEUP, S, false>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
 }
 
-template <int ACT, bool GATEUP>
-int launch_q4mf(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
-                int n_out, const float* row_weight, void* out, hipStream_t stream) {
-  const int KC = K / 32;
-  if (KC <= 16) return launch_q4mf_full<ACT, GATEUP, 1>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
-  if (KC <= 32) return launch_q4mf_full<ACT, GATEUP, 2>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
-  if (KC <= 48) return launch_q4mf_full<ACT, GATEUP, 3>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
-  if (KC <= 64) return launch_q4mf_full<ACT, GATEUP, 4>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
-  if (KC <= 96) return launch_q4mf_full<ACT, GATEUP, 6>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
-  return launch_q4mf_full<ACT, GATEUP, 8>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+// Quantised rows of up to 128 chunks (4096 int4 or 2048 int8 codes) on the
+// matrix cores.
+template <int ACT, int WF, bool GATEUP>
+int launch_qmf(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
+               int n_out, const float* row_weight, void* out, hipStream_t stream) {
+  const int KC = K / (WF == QW_I8 ? 16 : 32);
+#define QW_QMF(S_) launch_qmf_full<ACT, WF, GATEUP, S_>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream)
+  if (KC <= 16) return QW_QMF(1);
+  if (KC <= 32) return QW_QMF(2);
+  if (KC <= 48) return QW_QMF(3);
+  if (KC <= 64) return QW_QMF(4);
+  if (KC <= 96) return QW_QMF(6);
+  return QW_QMF(8);
+#undef QW_QMF
 }
 
 // Units per group for a row of CPL chunks per lane: 4 weight chunks (16-byte
@@ -980,17 +1085,24 @@ int launch_cpl(const FfnArgs& a, const WView& wa, const WView& wb, const void* x
 template <int ACT, int WF>
 int launch_fmt(const FfnArgs& a, hipStream_t stream) {
   const int D = static_cast<int>(a.d_model), F = static_cast<int>(a.d_ff);
-  // int4 rows of up to 128 chunks (4096 codes) take the matrix-core kernel
-  constexpr bool Q4 = WF == QW_U4;
-  int st = Q4 && D <= 4096
-               ? launch_q4mf<ACT, true>(a, a.gate, a.up, a.x, a.row_index, D, F, nullptr, a.hidden, stream)
-               : launch_cpl<ACT, WF, true>(a, a.gate, a.up, a.x, a.row_index, D, F, nullptr, a.hidden, a.save_gate,
-                                           a.save_up, stream);
-  if (st) return st;
-  return Q4 && F <= 4096
-             ? launch_q4mf<ACT, false>(a, a.down, a.down, a.hidden, nullptr, F, D, a.row_weight, a.y, stream)
-             : launch_cpl<ACT, WF, false>(a, a.down, a.down, a.hidden, nullptr, F, D, a.row_weight, a.y, a.save_y,
-                                          nullptr, stream);
+  // quantised rows of up to 128 chunks (4096 int4 or 2048 int8 codes) take the matrix-core kernel
+  constexpr int KMAX = WF == QW_I8 ? 2048 : WF == QW_U4 ? 4096 : 0;
+  int st;
+  if constexpr (KMAX > 0) {
+    st = D <= KMAX ? launch_qmf<ACT, WF, true>(a, a.gate, a.up, a.x, a.row_index, D, F, nullptr, a.hidden, stream)
+                   : launch_cpl<ACT, WF, true>(a, a.gate, a.up, a.x, a.row_index, D, F, nullptr, a.hidden, nullptr,
+                                               nullptr, stream);
+    if (st) return st;
+    return F <= KMAX ? launch_qmf<ACT, WF, false>(a, a.down, a.down, a.hidden, nullptr, F, D, a.row_weight, a.y, stream)
+                     : launch_cpl<ACT, WF, false>(a, a.down, a.down, a.hidden, nullptr, F, D, a.row_weight, a.y, nullptr,
+                                                  nullptr, stream);
+  } else {
+    st = launch_cpl<ACT, WF, true>(a, a.gate, a.up, a.x, a.row_index, D, F, nullptr, a.hidden, a.save_gate, a.save_up,
+                                   stream);
+    if (st) return st;
+    return launch_cpl<ACT, WF, false>(a, a.down, a.down, a.hidden, nullptr, F, D, a.row_weight, a.y, a.save_y, nullptr,
+                                      stream);
+  }
 }
 
 }  // namespace

@@ -140,26 +140,31 @@ def test_each_kernel_family_matches_oracle(act, fmt, group, path):
     assert normwise(got, ref) <= TOL[act]
 
 
-@pytest.mark.parametrize("act,group,D,F_", [
-    ("bf16", 32, 512, 1408),    # gate/up 16 chunks per row (1 slot, whole), down 44 (3 slots, clamped)
-    ("bf16", 32, 1024, 3072),   # 2 slots whole; down 96 chunks (6 slots, whole)
-    ("bf16", 32, 2048, 4096),   # 4 slots whole; down 128 chunks (8 slots, whole)
-    ("bf16", 32, 1536, 2560),   # 3 slots whole; down 80 chunks (6 slots, clamped)
-    ("bf16", 64, 1024, 1408),   # two chunks per scale (not whole)
-    ("bf16", 128, 4096, 1024),  # 8 slots, four chunks per scale
-    ("f16", 32, 4096, 1408),    # the int4 decode layer's rows with fp16 activations
-    ("bf16", 32, 6144, 512),    # gate/up rows of 192 chunks take the dot-product kernel
+@pytest.mark.parametrize("act,fmt,group,D,F_", [
+    ("bf16", "u4", 32, 512, 1408),    # gate/up 16 chunks per row (1 slot, whole), down 44 (3 slots, clamped)
+    ("bf16", "u4", 32, 1024, 3072),   # 2 slots whole; down 96 chunks (6 slots, whole)
+    ("bf16", "u4", 32, 2048, 4096),   # 4 slots whole; down 128 chunks (8 slots, whole)
+    ("bf16", "u4", 32, 1536, 2560),   # 3 slots whole; down 80 chunks (6 slots, clamped)
+    ("bf16", "u4", 64, 1024, 1408),   # two chunks per scale (not whole)
+    ("bf16", "u4", 128, 4096, 1024),  # 8 slots, four chunks per scale
+    ("f16", "u4", 32, 4096, 1408),    # the int4 decode layer's rows with fp16 activations
+    ("bf16", "u4", 32, 6144, 512),    # gate/up rows of 192 chunks take the dot-product kernel
+    ("bf16", "i8", None, 2048, 1024),  # the int8 decode layer: one scale per row, 8 and 4 slots
+    ("bf16", "i8", 16, 256, 512),     # one scale per chunk, whole rows (1 and 2 slots)
+    ("bf16", "i8", 64, 1536, 768),    # 6 slots, four chunks per scale; down 3 slots
+    ("f16", "i8", None, 2048, 1024),  # fp16 activations (used unscaled)
+    ("bf16", "i8", None, 4096, 1024),  # gate/up rows of 256 chunks take the dot-product kernel
 ])
-def test_int4_decode_rows_match_oracle(act, group, D, F_):
-    """int4 experts at decode row counts (1 to 9 rows, so one to three passes of
-    4 routes) through the weight-streaming family, whose int4 rows of up to 128
-    chunks run on the 4x4x4 matrix-core kernel, against the oracle."""
-    print(f"case int4 decode act={act} group={group} D={D} F={F_}", flush=True)
+def test_quantized_decode_rows_match_oracle(act, fmt, group, D, F_):
+    """int4 / int8 experts at decode row counts (1 to 9 rows, so one to three
+    passes of 4 routes) through the weight-streaming family, whose quantised rows
+    of up to 128 chunks run on the 4x4x4 matrix-core kernel, against the oracle."""
+    print(f"case quantised decode act={act} fmt={fmt} group={group} D={D} F={F_}", flush=True)
     counts = [1, 0, 3, 9, 2]
-    rng = np.random.RandomState(D + F_ + group)
+    rng = np.random.RandomState(D + F_ + (group or 0))
     rows = sum(counts)
     x = oracle.round_act(rng.randn(rows, D).astype(np.float32), act)
-    w = make_weights(len(counts), D, F_, "u4", D * 7 + F_, group)
+    w = make_weights(len(counts), D, F_, fmt, D * 7 + F_, group)
     rw = rng.rand(rows).astype(np.float32)
     got = run_experts(x, counts, w, act, row_weight=rw, path="stream")
     ref = oracle.round_act(oracle.experts_forward(x, np.array(counts), w, act) * rw[:, None], act)
