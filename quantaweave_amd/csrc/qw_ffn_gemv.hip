@@ -30,6 +30,8 @@
 // the conversion once per chunk and reused for every row of the wave.  There
 // is no LDS and no barrier, so the waves of a CU overlap freely.  Per-row
 // partial sums are reduced across the wave with butterflies.
+#include <cmath>
+
 #include "qw_ffn.h"
 
 namespace qw {
@@ -292,6 +294,35 @@ __device__ __forceinline__ void ring_read6(uint32_t w_addr, uint32_t s_addr, uin
       : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]), "=&v"(sv[0]), "=&v"(sv[1]),
         "=&v"(sv[2]), "=&v"(sv[3]), "=&v"(sv[4]), "=&v"(sv[5])
       : "v"(w_addr), "v"(s_addr)
+      : "memory");
+}
+
+// Eight chunks and their eight scales, the scales at sa[q & 3] + 1024 * (q >> 2)
+// (the matrix-core kernel's scales loaded 16 bytes per lane).
+__device__ __forceinline__ void ring_read8_sv(uint32_t w_addr, const uint32_t (&sa)[4], uint4 (&w)[8],
+                                              float (&sv)[8]) {
+  asm volatile(
+      "ds_read_b128 %0, %16\n"
+      "ds_read_b128 %1, %16 offset:1024\n"
+      "ds_read_b128 %2, %16 offset:2048\n"
+      "ds_read_b128 %3, %16 offset:3072\n"
+      "ds_read_b128 %4, %16 offset:4096\n"
+      "ds_read_b128 %5, %16 offset:5120\n"
+      "ds_read_b128 %6, %16 offset:6144\n"
+      "ds_read_b128 %7, %16 offset:7168\n"
+      "ds_read_b32 %8, %17\n"
+      "ds_read_b32 %9, %18\n"
+      "ds_read_b32 %10, %19\n"
+      "ds_read_b32 %11, %20\n"
+      "ds_read_b32 %12, %17 offset:1024\n"
+      "ds_read_b32 %13, %18 offset:1024\n"
+      "ds_read_b32 %14, %19 offset:1024\n"
+      "ds_read_b32 %15, %20 offset:1024\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]), "=&v"(w[6]), "=&v"(w[7]),
+        "=&v"(sv[0]), "=&v"(sv[1]), "=&v"(sv[2]), "=&v"(sv[3]), "=&v"(sv[4]), "=&v"(sv[5]), "=&v"(sv[6]),
+        "=&v"(sv[7])
+      : "v"(w_addr), "v"(sa[0]), "v"(sa[1]), "v"(sa[2]), "v"(sa[3])
       : "memory");
 }
 
@@ -631,7 +662,8 @@ struct Q4Lds {
   static constexpr int STAGE = NCH * 1024 + NCH * 256;  // chunks, then their scales
   static constexpr int STAGES = NST;
   static constexpr int NDMA = 2 * NCH;
-  static constexpr int OUT = GV_GPW_MAX * UPG * 4 * 4;  // fp32, 4 routes per unit
+  static constexpr int GPW_MAX = 16;                    // groups per wave, at most
+  static constexpr int OUT = GPW_MAX * UPG * 4 * 4;     // fp32, 4 routes per unit
   static constexpr int BYTES = STAGES * STAGE + OUT;
 };
 
@@ -693,6 +725,11 @@ __global__ __launch_bounds__(64) void ffn_qmf_kernel(
   static_assert(V <= 16, "at most four row sets per group");
   static_assert(NST >= 2 && NST <= 4, "two to four ring stages");
   using LD = Q4Lds<NCH, UPG, NST>;
+  // SV: one scale per chunk and 4 or 8 slots, so a row set's scales are blocks of
+  // 64 floats per row, loaded 16 bytes per lane (S / 4 loads per row set instead
+  // of S); lane 16 t' + j fetches row t', floats 4 (j ^ 4 t') .. + 3 of a block
+  constexpr bool SV = FULL && S % 4 == 0 && NCH == 8;
+  constexpr int NDMA = NCH + (SV ? NCH / 4 : NCH);  // DMA instructions per group
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   int r_lo = 0, r_hi = 0;
   const int e = nth_active_expert(offsets, n_experts, max_rows, blockIdx.y, &r_lo, &r_hi);
@@ -713,6 +750,7 @@ __global__ __launch_bounds__(64) void ffn_qmf_kernel(
   // from slot 16 t + (b ^ 4 t) (16 lanes in a row cover all 16 slot offsets: no
   // bank conflicts).
   const int ld_row = lane >> 4, ld_blk = (lane & 15) ^ (4 * ld_row);
+  const int sv_grp = (lane & 15) ^ (4 * ld_row);  // SV: the loading lane's group of 4 scales in a block
   const int rd_slot = 16 * t + (blk ^ (4 * t));
   // the loading lane's matrix: gate/up row sets alternate gate (even) and up (odd) rows
   const bool up_row = GATEUP && (ld_row & 1);
@@ -754,8 +792,15 @@ __global__ __launch_bounds__(64) void ffn_qmf_kernel(
         const int q = r * S + s;
         __builtin_amdgcn_global_load_lds(static_cast<const void*>(wrow + 16 * chunk_of(s)),
                                          (lds_void*)(st + q * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(srow + scale_of(s)),
-                                         (lds_void*)(st + NCH * 1024 + q * 256), 4, 0, 0);
+        if constexpr (!SV)
+          __builtin_amdgcn_global_load_lds(static_cast<const void*>(srow + scale_of(s)),
+                                           (lds_void*)(st + NCH * 1024 + q * 256), 4, 0, 0);
+      }
+      if constexpr (SV) {
+#pragma unroll
+        for (int ib = 0; ib < S / 4; ++ib)
+          __builtin_amdgcn_global_load_lds(static_cast<const void*>(srow + 64 * ib + 4 * sv_grp),
+                                           (lds_void*)(st + NCH * 1024 + (r * (S / 4) + ib) * 1024), 16, 0, 0);
       }
     }
   };
@@ -872,15 +917,21 @@ __global__ __launch_bounds__(64) void ffn_qmf_kernel(
       // keep STAGES - 1 groups in flight; wait until group g has landed (loads complete in order)
       if (g + LD::STAGES - 1 < g_end) issue(g + LD::STAGES - 1);
       const int after = min(LD::STAGES - 1, g_end - 1 - g);  // groups issued after g
-      if (after >= 3) wait_vmcnt<3 * LD::NDMA>();
-      else if (after == 2) wait_vmcnt<2 * LD::NDMA>();
-      else if (after == 1) wait_vmcnt<LD::NDMA>();
+      if (after >= 3) wait_vmcnt<3 * NDMA>();
+      else if (after == 2) wait_vmcnt<2 * NDMA>();
+      else if (after == 1) wait_vmcnt<NDMA>();
       else wait_vmcnt<0>();
       const char* st = ring + ((g - g_first) % LD::STAGES) * LD::STAGE;
       uint4 wq[8];
       float sq[8];
       const uint32_t wa_l = lds_addr(st) + rd_slot * 16, sa_l = lds_addr(st + NCH * 1024) + rd_slot * 4;
-      if constexpr (NCH == 8) {
+      if constexpr (SV) {
+        // scale of chunk 16 s + b of row t: block q >> 2, float group 4 (s & 3) + b / 4, read by
+        // lane 16 t + (group ^ 4 t), i.e. at 256 t + 64 ((q & 3) ^ t) + 4 b (no bank conflicts)
+        const uint32_t sb = lds_addr(st + NCH * 1024) + 256 * t + 4 * blk;
+        const uint32_t sa[4] = {sb + 64 * (0 ^ t), sb + 64 * (1 ^ t), sb + 64 * (2 ^ t), sb + 64 * (3 ^ t)};
+        ring_read8_sv(wa_l, sa, wq, sq);
+      } else if constexpr (NCH == 8) {
         ring_read8<true>(wa_l, sa_l, wq, sq);
       } else if constexpr (NCH == 6) {
         ring_read6(wa_l, sa_l, wq, sq);
@@ -1027,10 +1078,34 @@ int launch_qmf_s(const FfnArgs& a, const WView& wa, const WView& wb, const void*
     return set_error(QW_ERR_HIP, "cannot reserve %d bytes of LDS: %s", LD::BYTES, hipGetErrorString(attr));
   const int64_t n_groups = ceil_div(n_out, UPG);
   const int64_t touched = a.max_rows < a.experts ? a.max_rows : a.experts;
-  // 6 groups per wave from 8192 groups over the touched experts (the fastest of
-  // 2, 3, 4, 6 and 8 on the int4 decode layer), fewer below
-  const int gpw = touched * n_groups >= 8192 ? 6 : groups_per_wave(touched, n_groups, GATEUP);
-  static_assert(GV_GPW_MAX >= 6, "staging holds the groups of one wave");
+  // Groups per wave.  int4: about one round of waves over the device's slots
+  // for this kernel (waves per CU as its LDS and registers allow), for the number
+  // of experts that uniform routing of max_rows rows touches on average; a grid
+  // of 1.6 rounds left the second round two-thirds full (int4 decode layer:
+  // expert stage 53.9 us against 56.2 us with 6 groups per wave).  int8: 6 (its
+  // decode layer has experts with two passes of 4 routes, and one round measured
+  // 89.4 us against 87.9 us).  Small layers keep the fewer, shorter waves of
+  // groups_per_wave.
+  int gpw = groups_per_wave(touched, n_groups, GATEUP);
+  if (touched * n_groups >= 8192 && WF == QW_I8) {
+    gpw = 6;
+  } else if (touched * n_groups >= 8192) {
+    static int slots = 0;  // per instantiation: waves of this kernel the device holds at once
+    if (slots == 0) {
+      int dev = 0, cus = 0, per_cu = 0;
+      if (hipGetDevice(&dev) != hipSuccess ||
+          hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+          hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 64, LD::BYTES) != hipSuccess || cus <= 0 ||
+          per_cu <= 0)
+        return set_error(QW_ERR_HIP, "cannot query the occupancy of ffn_qmf_kernel");
+      slots = cus * per_cu;
+    }
+    const double E = static_cast<double>(a.experts);
+    const double active = E * (1.0 - std::pow(1.0 - 1.0 / E, static_cast<double>(a.max_rows)));
+    const int64_t want = static_cast<int64_t>(std::ceil(active * static_cast<double>(n_groups) / slots));
+    gpw = static_cast<int>(want < 2 ? 2 : want > LD::GPW_MAX ? LD::GPW_MAX : want);
+  }
+  static_assert(LD::GPW_MAX >= 6, "staging holds the groups of one wave");
   const dim3 grid(static_cast<unsigned>(ceil_div(n_groups, gpw)), static_cast<unsigned>(touched));
   kernel<<<grid, 64, LD::BYTES, stream>>>(static_cast<const uint16_t*>(x), row_index, a.offsets,
                                           static_cast<int>(a.experts), static_cast<int>(a.max_rows), wa, wb, K, n_out,
