@@ -28,8 +28,13 @@
 // The activation pieces matching a lane's chunks come straight from L2 (every
 // wave of the expert reads the same few rows), are put in the pair order of
 // the conversion once per chunk and reused for every row of the wave.  There
-// is no LDS and no barrier, so the waves of a CU overlap freely.  Per-row
-// partial sums are reduced across the wave with butterflies.
+// is no barrier, so the waves of a CU overlap freely.  Per-row partial sums
+// are reduced across the wave with butterflies.
+//
+// int4 rows of up to 4096 codes and int8 rows of up to 2048 take the second
+// kernel of this file (ffn_qmf_kernel), which keeps the same streaming scheme
+// but forms the dot products on the 4x4x4 matrix cores; the kernel above serves
+// bf16 / fp16 weights and longer quantised rows.
 #include <cmath>
 
 #include "qw_ffn.h"
@@ -611,7 +616,8 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// int4 experts with the dot products on the matrix cores (decode rows).
+// Quantised (int4 / int8) experts with the dot products on the matrix cores
+// (decode rows).
 //
 // v_mfma_f32_4x4x4_16b (bf16 or f16 operands) forms 16 independent 4x4
 // products over 4 k values: in block b = lane / 4, lane 4b + i supplies row i
@@ -623,17 +629,19 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
 // the dot-product kernel above, the VALU work per weight (the code conversion
 // and one scale per chunk) does not grow with the number of routes.
 //
-// A dword of 8 codes (byte j holds codes 2j and 2j + 1, low nibble first)
-// becomes the operand pairs (0, 2), (4, 6), (1, 3), (5, 7) as in the kernel
-// above: the low and the high nibbles are masked into bytes (an AND, a shift and
-// an AND) and v_perm puts each pair under the high byte 0x43 (bf16 128 + u) or
-// 0x64 (fp16 1024 + u).  The activations are put in the same order once per
-// pass by v_perm.  A chunk's chain of 8 instructions yields
-// sum x * (magic value + u); its result times the chunk's group scale is
-// accumulated, and one fp32 4x4x1 product per chunk adds
-// -(magic value + 8) * (the chunk's sum of x) * scale for the 4 routes and 4
-// rows, which removes both the magic offset and the +8 storage bias of the
-// codes u = q + 8 without VALU work.
+// int4: a dword of 8 codes (byte j holds codes 2j and 2j + 1, low nibble
+// first) becomes the operand pairs (0, 2), (4, 6), (1, 3), (5, 7) as in the
+// kernel above: the low and the high nibbles are masked into bytes (an AND, a
+// shift and an AND) and v_perm puts each pair under the high byte 0x43 (bf16
+// 128 + u) or 0x64 (fp16 1024 + u), u = q + 8.  int8: a dword of 4 codes, u =
+// q ^ 0x80 = q + 128, becomes two fp16 pairs 1024 + u by v_perm, against fp16
+// activations scaled by a power of two per route as in the kernel above.  The
+// activations are put in the operand order once per pass.  A chunk's chain of
+// 8 (int4) or 4 (int8) instructions yields sum x * (magic value + u); its
+// result times the chunk's group scale is accumulated, and one fp32 4x4x1
+// product per chunk adds -(magic value + storage bias) * (the chunk's sum of x)
+// * scale for the 4 routes and 4 rows, which removes both offsets without VALU
+// work.
 //
 // Lane (b, t) holds chunks c = 16 s + b (s < S) of every row it streams, so one
 // row set of 4 rows takes S chunk loads per lane and a group of R row sets
@@ -658,10 +666,9 @@ __device__ __forceinline__ gf32x4 mfma4(uint2 a, uint2 b, gf32x4 c) {
 }
 
 template <int NCH, int UPG, int NST>
-struct Q4Lds {
+struct QmfLds {
   static constexpr int STAGE = NCH * 1024 + NCH * 256;  // chunks, then their scales
   static constexpr int STAGES = NST;
-  static constexpr int NDMA = 2 * NCH;
   static constexpr int GPW_MAX = 16;                    // groups per wave, at most
   static constexpr int OUT = GPW_MAX * UPG * 4 * 4;     // fp32, 4 routes per unit
   static constexpr int BYTES = STAGES * STAGE + OUT;
@@ -724,7 +731,7 @@ __global__ __launch_bounds__(64) void ffn_qmf_kernel(
   static_assert(NCH == 4 || NCH == 6 || NCH == 8, "the ring reads four, six or eight chunks per group");
   static_assert(V <= 16, "at most four row sets per group");
   static_assert(NST >= 2 && NST <= 4, "two to four ring stages");
-  using LD = Q4Lds<NCH, UPG, NST>;
+  using LD = QmfLds<NCH, UPG, NST>;
   // SV: one scale per chunk and 4 or 8 slots, so a row set's scales are blocks of
   // 64 floats per row, loaded 16 bytes per lane (S / 4 loads per row set instead
   // of S); lane 16 t' + j fetches row t', floats 4 (j ^ 4 t') .. + 3 of a block
@@ -749,8 +756,8 @@ __global__ __launch_bounds__(64) void ffn_qmf_kernel(
   // chunk lands at ring slot 16 t' + j, and lane (b, t) reads row t, chunk b
   // from slot 16 t + (b ^ 4 t) (16 lanes in a row cover all 16 slot offsets: no
   // bank conflicts).
+  // (with SV, ld_blk is also the loading lane's group of 4 scales in a block)
   const int ld_row = lane >> 4, ld_blk = (lane & 15) ^ (4 * ld_row);
-  const int sv_grp = (lane & 15) ^ (4 * ld_row);  // SV: the loading lane's group of 4 scales in a block
   const int rd_slot = 16 * t + (blk ^ (4 * t));
   // the loading lane's matrix: gate/up row sets alternate gate (even) and up (odd) rows
   const bool up_row = GATEUP && (ld_row & 1);
@@ -799,7 +806,7 @@ __global__ __launch_bounds__(64) void ffn_qmf_kernel(
       if constexpr (SV) {
 #pragma unroll
         for (int ib = 0; ib < S / 4; ++ib)
-          __builtin_amdgcn_global_load_lds(static_cast<const void*>(srow + 64 * ib + 4 * sv_grp),
+          __builtin_amdgcn_global_load_lds(static_cast<const void*>(srow + 64 * ib + 4 * ld_blk),
                                            (lds_void*)(st + NCH * 1024 + (r * (S / 4) + ib) * 1024), 16, 0, 0);
       }
     }
@@ -1063,15 +1070,15 @@ int launch_one(const FfnArgs& a, const WView& wa, const WView& wb, const void* x
 // The int4 matrix-core kernel for one projection: S chunk slots per lane cover
 // rows of up to 16 S chunks; R row sets per group keep 4 to 8 chunk loads per
 // lane and group.
-#ifndef Q4_STAGES
-#define Q4_STAGES 2
-#endif
-template <int ACT, int WF, bool GATEUP, int S, bool FULL, int NST = Q4_STAGES>
+// Two ring stages: 3 and 4 stages cost waves per CU and measured slower.
+constexpr int kQmfStages = 2;
+
+template <int ACT, int WF, bool GATEUP, int S, bool FULL, int NST = kQmfStages>
 int launch_qmf_s(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
                   int n_out, const float* row_weight, void* out, hipStream_t stream) {
   constexpr int R = S <= 2 ? 4 : S <= 4 ? 2 : 1;
   constexpr int UPG = GATEUP ? 2 * R : 4 * R;
-  using LD = Q4Lds<S * R, UPG, NST>;
+  using LD = QmfLds<S * R, UPG, NST>;
   auto kernel = ffn_qmf_kernel<ACT, WF, GATEUP, S, R, FULL, NST>;
   const hipError_t attr = reserve_lds<ffn_qmf_kernel<ACT, WF, GATEUP, S, R, FULL, NST>>(LD::BYTES);
   if (attr != hipSuccess)
