@@ -1085,16 +1085,17 @@ int launch_qmf_s(const FfnArgs& a, const WView& wa, const WView& wb, const void*
     return set_error(QW_ERR_HIP, "cannot reserve %d bytes of LDS: %s", LD::BYTES, hipGetErrorString(attr));
   const int64_t n_groups = ceil_div(n_out, UPG);
   const int64_t touched = a.max_rows < a.experts ? a.max_rows : a.experts;
-  // Groups per wave.  int4: about one round of waves over the device's slots
-  // for this kernel (waves per CU as its LDS and registers allow), for the number
-  // of experts that uniform routing of max_rows rows touches on average; a grid
-  // of 1.6 rounds left the second round two-thirds full (int4 decode layer:
-  // expert stage 53.9 us against 56.2 us with 6 groups per wave).  int8: 6 (its
+  // Groups per wave: about one round of waves over the device's slots for this
+  // kernel (waves per CU as its LDS and registers allow), for the number of
+  // experts that uniform routing of max_rows rows touches on average; a grid of
+  // 1.3 to 1.6 rounds left the last round partly empty (int4 decode layer:
+  // expert stage 53.9 us against 56.2 us with 6 groups per wave; int8 decode
+  // layer, down projection: 84.4 us against 88.1 us).  int8 gate/up keeps 6 (its
   // decode layer has experts with two passes of 4 routes, and one round measured
-  // 89.4 us against 87.9 us).  Small layers keep the fewer, shorter waves of
+  // slower there).  Small layers keep the fewer, shorter waves of
   // groups_per_wave.
   int gpw = groups_per_wave(touched, n_groups, GATEUP);
-  if (touched * n_groups >= 8192 && WF == QW_I8) {
+  if (touched * n_groups >= 8192 && WF == QW_I8 && GATEUP) {
     gpw = 6;
   } else if (touched * n_groups >= 8192) {
     static int slots = 0;  // per instantiation: waves of this kernel the device holds at once
