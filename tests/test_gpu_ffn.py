@@ -151,6 +151,7 @@ def test_each_kernel_family_matches_oracle(act, fmt, group, path):
     ("bf16", "u4", 32, 6144, 512),    # gate/up rows of 192 chunks take the dot-product kernel
     ("bf16", "i8", None, 2048, 1024),  # the int8 decode layer: one scale per row, 8 and 4 slots
     ("bf16", "i8", 16, 256, 512),     # one scale per chunk, whole rows (1 and 2 slots)
+    ("bf16", "i8", 16, 2048, 1024),   # one scale per chunk, whole rows of 8 and 4 slots: scale blocks
     ("bf16", "i8", 64, 1536, 768),    # 6 slots, four chunks per scale; down 3 slots
     ("f16", "i8", None, 2048, 1024),  # fp16 activations (used unscaled)
     ("bf16", "i8", None, 4096, 1024),  # gate/up rows of 256 chunks take the dot-product kernel
