@@ -52,6 +52,8 @@ def lib() -> ctypes.CDLL:
         L.orc_softmax_row.argtypes = [P, i32, P]
         L.orc_route_from_logits.argtypes = [P, i32, i32, i32, P, P, P, P]
         L.orc_route_select.argtypes = [P, i32, i32, i32, P, i32, P, P, P]
+        L.orc_route_select_probs.argtypes = [P, P, i32, i32, i32, P, i32, P, P]
+        L.orc_topk_weight_sum.argtypes, L.orc_topk_weight_sum.restype = [P, i32], f32
         L.orc_router_logits.argtypes = [P, P, i32, i32, i32, f32, P]
         L.orc_capacity.argtypes, L.orc_capacity.restype = [i64, i64, i64, f64, f64, i64, i32], i64
         L.orc_plan.argtypes = [P, P, i32, i32, i32, i64, P, P, P, P, P, P, P, P, P]
@@ -152,6 +154,31 @@ def route_from_logits(logits: np.ndarray, top_k: int, expert_bias: np.ndarray | 
     lib().orc_route_select(_ptr(logits), T, E, top_k, _ptr(bias), int(select == "logits"), _ptr(probs), _ptr(idx),
                            _ptr(w))
     return probs, idx, w
+
+
+def route_from_probs(logits: np.ndarray, probs: np.ndarray, top_k: int, expert_bias: np.ndarray | None = None,
+                     select: str = "probs"):
+    """The selection and renormalisation of route_from_logits from given
+    probabilities (e.g. torch's softmax on the device).  Returns (top_idx
+    int32, top_w)."""
+    if select not in ("probs", "logits"):
+        raise ValueError("select must be 'probs' or 'logits'")
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    probs = np.ascontiguousarray(probs, dtype=np.float32)
+    T, E = logits.shape
+    assert probs.shape == (T, E)
+    idx = np.empty((T, top_k), dtype=np.int32)
+    w = np.empty((T, top_k), dtype=np.float32)
+    bias = None if expert_bias is None else np.ascontiguousarray(expert_bias, dtype=np.float32)
+    lib().orc_route_select_probs(_ptr(logits), _ptr(probs), T, E, top_k, _ptr(bias), int(select == "logits"),
+                                 _ptr(idx), _ptr(w))
+    return idx, w
+
+
+def topk_weight_sum(w: np.ndarray) -> np.ndarray:
+    """Per-row sum of a [T, k] array in torch-ROCm's reduction order (k < 128)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    return np.array([lib().orc_topk_weight_sum(_ptr(row), w.shape[1]) for row in w], dtype=np.float32)
 
 
 def capacity(tokens: int, top_k: int, experts: int, capacity_factor: float, capacity_scale: float = 1.0,
@@ -337,7 +364,7 @@ def combine_static(y_rows: np.ndarray, slot_token: np.ndarray, slot_weight: np.n
 
 def decode_step(x: np.ndarray, router_w: np.ndarray, w: dict, *, top_k: int, dtype: str, temperature: float = 1.0,
                 expert_bias: np.ndarray | None = None, residual: np.ndarray | None = None,
-                logits: np.ndarray | None = None, accum: str = "f64"):
+                logits: np.ndarray | None = None, accum: str = "f64", probs: np.ndarray | None = None):
     """The routed-expert lines of FastDecoder._step, src/fast_decode.py:170-177.
 
     x [T, d] fp32 (the normed hidden state), router_w fp32 [E, d].  Routing in
@@ -345,12 +372,17 @@ def decode_step(x: np.ndarray, router_w: np.ndarray, w: dict, *, top_k: int, dty
     capacity); expert inputs are x rounded to `dtype` (:174); each expert's
     SwiGLU in `dtype` (:175-177, the weights as `expert_weights` gives them);
     then out = residual + sum_j float(y_j) * w_j in fp32, in top-k order.
+    `probs`, when given, is the softmax of `logits` as computed elsewhere (torch
+    on the device); the selection then starts from it.
     Returns a dict with logits, probs, top_idx, top_w, y [T, k, d] and out."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     T, d = x.shape
     if logits is None:
         logits = router_logits(x, router_w, temperature)
-    probs, idx, tw = route_from_logits(logits, top_k, expert_bias, select="logits")
+    if probs is None:
+        probs, idx, tw = route_from_logits(logits, top_k, expert_bias, select="logits")
+    else:
+        idx, tw = route_from_probs(logits, probs, top_k, expert_bias, select="logits")
     xc = round_act(x, dtype)
     y = np.zeros((T, top_k, d), dtype=np.float32)
     for e in np.unique(idx).tolist():
@@ -366,7 +398,7 @@ def decode_step(x: np.ndarray, router_w: np.ndarray, w: dict, *, top_k: int, dty
 
 def moe_forward(x: np.ndarray, router_w: np.ndarray, w: dict, *, top_k: int, cap: int, dtype: str,
                 temperature: float = 1.0, expert_bias: np.ndarray | None = None, logits: np.ndarray | None = None,
-                accum: str = "f64"):
+                accum: str = "f64", probs: np.ndarray | None = None):
     """TopKMoE.forward, src/quantweave_moe_model.py:113-164 (dynamic dispatch).
 
     x [T, d] holds activation values (already rounded to `dtype`).  Returns a
@@ -377,7 +409,10 @@ def moe_forward(x: np.ndarray, router_w: np.ndarray, w: dict, *, top_k: int, cap
     E = router_w.shape[0]
     if logits is None:
         logits = router_logits(x, router_w, temperature)
-    probs, idx, tw = route_from_logits(logits, top_k, expert_bias)
+    if probs is None:
+        probs, idx, tw = route_from_logits(logits, top_k, expert_bias)
+    else:
+        idx, tw = route_from_probs(logits, probs, top_k, expert_bias)
     p = plan(idx, tw, E, cap)
     rows = x[p["slot_token"]]
     y = experts_forward(rows, p["kept_counts"], w, dtype, accum)

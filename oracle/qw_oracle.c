@@ -11,7 +11,10 @@
  * Functions and the reference lines they restate:
  *   orc_expf, orc_softmax_row  softmax of src/quantweave_moe_model.py:129 with
  *                              an exactly specified exp and summation order
- *   orc_route_from_logits      :129-137 (softmax, topk / biased topk, renorm)
+ *   orc_route_from_logits      :129-137 (softmax, topk / biased topk, renorm;
+ *                              topk's tie order and the renormalising sum
+ *                              are torch-ROCm's, which the reference runs)
+ *   orc_route_select_probs     the same selection from given probabilities
  *   orc_route_select           the same with the decode step's selection,
  *                              src/fast_decode.py:170-174 (topk of the
  *                              scores, biased or not)
@@ -99,38 +102,162 @@ static uint32_t sort_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-/* probs = softmax(logits); indices = topk(key, k) in descending order, equal
- * keys by ascending expert index, with key = logits + bias when a bias is
- * given, else logits when select_logits, else probs; w = probs[idx];
- * top_w = w / (((w0 + w1) + w2) + ...). */
+/* torch.topk's comparison (GTOp with NaN handling): NaN above numbers. */
+static int topk_greater(float a, float b) { return (a != a && b == b) || a > b; }
+
+/* torch.topk's order (torch-ROCm, measured on the device and pinned by
+ * tests/golden/torch_rocm_routing.npz): the chosen values above the k-th
+ * value in index order, then the k-th value's ties in index order, sorted for
+ * k <= 32 by the 32-wide bitonic network of
+ * aten/src/ATen/native/cuda/SortUtils.cuh (bitonicSort / bitonicSwap, GTOp,
+ * invalid entries last), for larger k stably.  kv, idx, pv hold the k choices
+ * (any order) and are rewritten in torch's order. */
+static void topk_torch_order(int k, float* kv, int32_t* idx, float* pv) {
+  float K[1024], P[1024];
+  int32_t V[1024];
+  int valid[1024];
+  /* the split compares radix-select keys (sort_key: -0 below +0); the
+   * network compares floats (-0 equal to +0) */
+  uint32_t kth = sort_key(kv[0]);
+  for (int j = 0; j < k; ++j)
+    if (sort_key(kv[j]) < kth) kth = sort_key(kv[j]); /* the smallest chosen value */
+  int n = 0;
+  for (int pass = 0; pass < 2; ++pass) {
+    for (int e = -1;;) { /* next chosen expert above e in index order */
+      int best = -1;
+      for (int j = 0; j < k; ++j) {
+        const int grp = sort_key(kv[j]) > kth ? 0 : 1;
+        if (grp != pass || idx[j] <= e) continue;
+        if (best < 0 || idx[j] < idx[best]) best = j;
+      }
+      if (best < 0) break;
+      K[n] = kv[best];
+      V[n] = idx[best];
+      P[n] = pv[best];
+      valid[n] = 1;
+      ++n;
+      e = idx[best];
+    }
+  }
+  if (k > 32) { /* torch sorts longer selections stably */
+    for (int i = 1; i < n; ++i)
+      for (int j = i; j > 0 && topk_greater(K[j], K[j - 1]); --j) {
+        float tk = K[j]; K[j] = K[j - 1]; K[j - 1] = tk;
+        int32_t tv = V[j]; V[j] = V[j - 1]; V[j - 1] = tv;
+        float tp = P[j]; P[j] = P[j - 1]; P[j - 1] = tp;
+      }
+    for (int j = 0; j < k; ++j) {
+      kv[j] = K[j];
+      idx[j] = V[j];
+      pv[j] = P[j];
+    }
+    return;
+  }
+  for (int i = n; i < 32; ++i) {
+    K[i] = 0.0f;
+    V[i] = 0;
+    P[i] = 0.0f;
+    valid[i] = 0;
+  }
+  for (unsigned size = 2; size <= 32; size *= 2) {
+    for (unsigned stride = size / 2; stride > 0; stride /= 2) {
+      for (unsigned t = 0; t < 16; ++t) {
+        const unsigned a = 2 * t - (t & (stride - 1)), b = a + stride;
+        const int dir = size < 32 && (t & (size / 2)) != 0;
+        const int swap = (topk_greater(K[a], K[b]) && valid[a]) || !valid[b];
+        if (swap == dir) {
+          float tk = K[a]; K[a] = K[b]; K[b] = tk;
+          int32_t tv = V[a]; V[a] = V[b]; V[b] = tv;
+          float tp = P[a]; P[a] = P[b]; P[b] = tp;
+          int tvl = valid[a]; valid[a] = valid[b]; valid[b] = tvl;
+        }
+      }
+    }
+  }
+  for (int j = 0; j < k; ++j) {
+    kv[j] = K[j];
+    idx[j] = V[j];
+    pv[j] = P[j];
+  }
+}
+
+/* w.sum(-1) of k < 128 values as torch-ROCm reduces a contiguous last
+ * dimension (aten/src/ATen/native/cuda/Reduce.cuh): B = 2^floor(log2 k)
+ * threads (at most 64), thread i holding w_i + w_{i+B} (w_i alone when
+ * i + B >= k), then adjacent pairs in a tree. */
+float orc_topk_weight_sum(const float* w, int k) {
+  int B = 1;
+  while (B * 2 <= k && B < 64) B *= 2;
+  float v[64];
+  for (int i = 0; i < B; ++i) v[i] = (i + B < k) ? w[i] + w[i + B] : w[i];
+  for (int n = B; n > 1; n /= 2)
+    for (int i = 0; i < n / 2; ++i) v[i] = v[2 * i] + v[2 * i + 1];
+  return v[0];
+}
+
+/* One token's selection from its probabilities p (and logits l): indices =
+ * topk(key, k) with key = l + bias when a bias is given, else l when
+ * select_logits, else p; chosen by (key descending, index ascending), which
+ * is the set torch.topk chooses, then put in torch.topk's order; w = p[idx] /
+ * torch's sum of the chosen p (orc_topk_weight_sum; the plain sum in choice
+ * order beyond 128 choices). */
+static void select_row(const float* l, const float* p, int E, int K, const float* bias, int select_logits,
+                       uint32_t* key, char* taken, float* kv, int32_t* top_idx, float* top_w) {
+  for (int e = 0; e < E; ++e) {
+    key[e] = sort_key(bias ? l[e] + bias[e] : (select_logits ? l[e] : p[e]));
+    taken[e] = 0;
+  }
+  for (int j = 0; j < K; ++j) {
+    int best = -1;
+    for (int e = 0; e < E; ++e) {
+      if (taken[e]) continue;
+      if (best < 0 || key[e] > key[best]) best = e;
+    }
+    taken[best] = 1;
+    top_idx[j] = best;
+    top_w[j] = p[best];
+    kv[j] = bias ? l[best] + bias[best] : (select_logits ? l[best] : p[best]);
+  }
+  if (K >= 2 && K <= 1024) topk_torch_order(K, kv, top_idx, top_w);
+  float sum;
+  if (K < 128) {
+    sum = orc_topk_weight_sum(top_w, K);
+  } else {
+    sum = top_w[0];
+    for (int j = 1; j < K; ++j) sum = sum + top_w[j];
+  }
+  for (int j = 0; j < K; ++j) top_w[j] = top_w[j] / sum;
+}
+
+/* probs = softmax(logits), then select_row per token. */
 void orc_route_select(const float* logits, int T, int E, int K, const float* bias, int select_logits,
                       float* probs, int32_t* top_idx, float* top_w) {
   uint32_t* key = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)E);
   char* taken = (char*)malloc((size_t)E);
+  float* kv = (float*)malloc(sizeof(float) * (size_t)K);
   for (int t = 0; t < T; ++t) {
-    const float* l = logits + (size_t)t * E;
-    float* p = probs + (size_t)t * E;
-    orc_softmax_row(l, E, p);
-    for (int e = 0; e < E; ++e) {
-      key[e] = sort_key(bias ? l[e] + bias[e] : (select_logits ? l[e] : p[e]));
-      taken[e] = 0;
-    }
-    float sum = 0.0f;
-    for (int j = 0; j < K; ++j) {
-      int best = -1;
-      for (int e = 0; e < E; ++e) {
-        if (taken[e]) continue;
-        if (best < 0 || key[e] > key[best]) best = e;
-      }
-      taken[best] = 1;
-      top_idx[(size_t)t * K + j] = best;
-      top_w[(size_t)t * K + j] = p[best];
-      sum = (j == 0) ? p[best] : sum + p[best];
-    }
-    for (int j = 0; j < K; ++j) top_w[(size_t)t * K + j] = top_w[(size_t)t * K + j] / sum;
+    orc_softmax_row(logits + (size_t)t * E, E, probs + (size_t)t * E);
+    select_row(logits + (size_t)t * E, probs + (size_t)t * E, E, K, bias, select_logits, key, taken, kv,
+               top_idx + (size_t)t * K, top_w + (size_t)t * K);
   }
   free(key);
   free(taken);
+  free(kv);
+}
+
+/* The same selection from given probabilities (softmax computed elsewhere,
+ * e.g. by torch on the device). */
+void orc_route_select_probs(const float* logits, const float* probs, int T, int E, int K, const float* bias,
+                            int select_logits, int32_t* top_idx, float* top_w) {
+  uint32_t* key = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)E);
+  char* taken = (char*)malloc((size_t)E);
+  float* kv = (float*)malloc(sizeof(float) * (size_t)K);
+  for (int t = 0; t < T; ++t)
+    select_row(logits + (size_t)t * E, probs + (size_t)t * E, E, K, bias, select_logits, key, taken, kv,
+               top_idx + (size_t)t * K, top_w + (size_t)t * K);
+  free(key);
+  free(taken);
+  free(kv);
 }
 
 void orc_route_from_logits(const float* logits, int T, int E, int K, const float* bias, float* probs,

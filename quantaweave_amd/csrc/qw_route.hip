@@ -1,47 +1,113 @@
 // Router logits, softmax, top-k and renormalisation on gfx950.
 //
 // Reference: src/quantweave_moe_model.py:124-137 (TopKMoE.forward, fp32 routing
-// with autocast disabled).  This file is compiled with -ffp-contract=off: the
-// softmax below uses only IEEE-754 single-precision operations (add, mul, fma,
-// div, rint) in a fixed order, so the same sequence evaluated on any IEEE
-// machine gives the same bits.  That is what makes the routing decisions
-// (indices, capacity slots, drops) reproducible bit-for-bit from the logits.
+// with autocast disabled).  The reference routes with torch's own kernels, so
+// the routing here is torch's arithmetic step for step: the softmax is the
+// one-wave softmax PyTorch runs for rows of up to 1024 fp32 values
+// (softmax_warp_forward in aten/src/ATen/native/cuda/PersistentSoftmax.cuh:
+// the maximum, e = exp(l - max) with the device library's expf, per-lane sums
+// over the lane's values in index order, an xor butterfly over lane offsets
+// 32, 16, ..., 1, then e / sum), the selection is torch.topk's order and the
+// renormalisation is w / w.sum(-1).  This file is compiled with
+// -ffp-contract=off so each of those operations stays the single IEEE-754
+// operation written.
 #include <type_traits>
 
 #include "qw_common.h"
 
 namespace qw {
 
-// ---------------------------------------------------------------------------
-// Deterministic exp for the softmax argument x = logit - max <= 0.
-// Cody-Waite reduction x = n*ln2 + r with ln2 split into a 16-bit head
-// (0x3f317200, so n*head is exact) and a tail, |r| <= ln2/2; e^r by its
-// degree-7 Taylor polynomial (truncation < 0.1 ulp) in Horner form with fma;
-// scaling by 2^n through the exponent field, in two steps below 2^-126 so the
-// only rounding of a subnormal result is the last multiply.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ float det_expf(float x) {
-  if (!(x >= -104.0f)) return (x != x) ? x : 0.0f;  // NaN passes through; e^-104 < 2^-150
-  const float n = __builtin_rintf(x * 1.4426950216293335f);
-  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
-  r = __builtin_fmaf(-n, 1.428606765330187e-06f, r);
-  float p = 0.00019841270113829523f;
-  p = __builtin_fmaf(p, r, 0.0013888889225199819f);
-  p = __builtin_fmaf(p, r, 0.008333333767950535f);
-  p = __builtin_fmaf(p, r, 0.0416666679084301f);
-  p = __builtin_fmaf(p, r, 0.1666666716337204f);
-  p = __builtin_fmaf(p, r, 0.5f);
-  p = __builtin_fmaf(p, r, 1.0f);
-  p = __builtin_fmaf(p, r, 1.0f);
-  const int ni = static_cast<int>(n);
-  if (ni >= -126) return p * __int_as_float((ni + 127) << 23);
-  return (p * __int_as_float((ni + 127 + 64) << 23)) * 5.421010862427522e-20f;  // * 2^-64
-}
+// e^x as torch's softmax computes it: the device math library's expf (what
+// the float overload of ::exp calls in device code).
+__device__ __forceinline__ float softmax_expf(float x) { return expf(x); }
 
 // Total order on floats as unsigned keys: -inf < ... < -0 < +0 < ... < +inf < NaN.
 __device__ __forceinline__ uint32_t sortable_key(float f) {
   uint32_t u = __float_as_uint(f);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// torch.topk's comparison: NaN above every number, otherwise a > b.
+__device__ __forceinline__ bool topk_greater(float a, float b) { return (a != a && b == b) || a > b; }
+
+// torch.topk's order of the K <= 64 chosen values (lane j < K holds choice j
+// as (key value kv, expert e, probability p); the choices arrive sorted by
+// sortable_key(kv) descending, equal keys by ascending expert, which is the set
+// torch.topk chooses).  torch's selection writes the chosen values above the
+// k-th value in expert order, then those equal to the k-th value in expert
+// order (compared as its radix-select keys: sortable_key's order, -0 below
+// +0), and then sorts them by their float value (-0 equal to +0):
+//   K <= 32: a 32-wide bitonic network that is not stable (bitonicSort and
+//            bitonicSwap in aten/src/ATen/native/cuda/SortUtils.cuh with GTOp,
+//            invalid entries last); lane i of the first 32 plays element i,
+//            exchanging with lane i ^ stride;
+//   K > 32:  a stable sort, which differs from the arrival order only where
+//            -0 and +0 are both chosen next to each other.
+// Without equal float values among the choices both give the arrival order, so
+// the common case returns after one wave vote.
+__device__ __forceinline__ void topk_tie_order(int K, float& kv, int& e, float& p) {
+  const int lane = threadIdx.x % kWave;
+  const float prev = __shfl_up(kv, 1, kWave);
+  const bool tie = lane >= 1 && lane < K && prev == kv;
+  if (K > 32 ? !__any(tie && sortable_key(prev) != sortable_key(kv)) : !__any(tie)) return;
+  const uint32_t kth = sortable_key(__shfl(kv, K - 1, kWave));
+  const int grp = (lane < K && sortable_key(kv) > kth) ? 0 : 1;
+  int pos = 0;  // place in the order torch's selection writes
+  for (int i = 0; i < K; ++i) {
+    const int gi = __builtin_amdgcn_readlane(grp, i), ei = __builtin_amdgcn_readlane(e, i);
+    pos += (gi < grp || (gi == grp && ei < e)) ? 1 : 0;
+  }
+  if (K > 32) {
+    int rank = 0;  // stable descending sort of that order
+    for (int i = 0; i < K; ++i) {
+      const float ki = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kv), i));
+      const int pi = __builtin_amdgcn_readlane(pos, i);
+      rank += (topk_greater(ki, kv) || (!topk_greater(kv, ki) && pi < pos)) ? 1 : 0;
+    }
+    pos = rank;
+  }
+  const int dst = (lane < K ? pos : lane) * 4;  // a permutation of the lanes: choice j moves to lane pos
+  kv = __int_as_float(__builtin_amdgcn_ds_permute(dst, __float_as_int(kv)));
+  e = __builtin_amdgcn_ds_permute(dst, e);
+  p = __int_as_float(__builtin_amdgcn_ds_permute(dst, __float_as_int(p)));
+  if (K > 32) return;
+  int valid = lane < K ? 1 : 0;
+#pragma unroll
+  for (int size = 2; size <= 32; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const float okv = __shfl_xor(kv, stride, kWave);
+      const int oe = __shfl_xor(e, stride, kWave);
+      const float op = __shfl_xor(p, stride, kWave);
+      const int ovalid = __shfl_xor(valid, stride, kWave);
+      const bool lower = (lane & stride) == 0;
+      const float ka = lower ? kv : okv, kb = lower ? okv : kv;
+      const int va = lower ? valid : ovalid, vb = lower ? ovalid : valid;
+      const bool swap = (topk_greater(ka, kb) && va) || !vb;
+      const bool dir = size < 32 && (lane & size) != 0;  // the last merge runs in one direction
+      if (swap == dir) {
+        kv = okv;
+        e = oe;
+        p = op;
+        valid = ovalid;
+      }
+    }
+  }
+}
+
+// w.sum(-1) of a row of K < 128 chosen weights as torch reduces it (the
+// thread reduction of aten/src/ATen/native/cuda/Reduce.cuh for a contiguous
+// last dimension of K values): with B = 2^floor(log2 K) (at most 64) threads,
+// thread i adds w_i + w_{i+B} (just w_i when i + B >= K), then the B partial
+// sums meet in a shuffle-down tree (offsets 1, 2, 4, ...).  Lane j holds w_j in
+// lo and, for K > 64, w_{j+64} in hi.  Every lane gets the sum.
+__device__ __forceinline__ float topk_weight_sum(float lo, float hi, int K) {
+  const int lane = threadIdx.x % kWave;
+  const int B = K >= kWave ? kWave : (1 << (31 - __builtin_clz(static_cast<unsigned>(K))));
+  const float up = K > kWave ? hi : __shfl_down(lo, B < kWave ? B : 0, kWave);
+  float v = lane < B ? (lane + B < K ? lo + up : lo) : 0.0f;
+  for (int o = 1; o < B; o <<= 1) v = v + __shfl_down(v, o, kWave);
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
 }
 
 // ---------------------------------------------------------------------------
@@ -272,22 +338,23 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const uint16_t* __rest
 
 // ---------------------------------------------------------------------------
 // One wavefront per token.  Lane l owns experts l, l+64, ..., l+64*(EPL-1).
-//   m = max_e L_e;  q_e = det_expf(L_e - m)
+//   m = max_e L_e;  q_e = softmax_expf(L_e - m)
 //   S = (per-lane sequential sum over its experts in index order) reduced by
 //       the xor butterfly with lane offsets 32, 16, 8, 4, 2, 1
 //   p_e = q_e / S
 //   top-k: k rounds of a wave argmax on (key desc, expert asc), key = p_e,
 //          or L_e + bias_e when a bias is given, or L_e when `select_logits`
-//          is set and there is no bias (the decode step's selection)
-//   w_j = p_{idx_j} / (((p_{idx_0} + p_{idx_1}) + p_{idx_2}) + ...)
+//          is set and there is no bias (the decode step's selection); equal
+//          keys then take torch.topk's order (topk_tie_order)
+//   w_j = p_{idx_j} / S_w, S_w = torch's sum of the k weights (topk_weight_sum)
 // ---------------------------------------------------------------------------
 //
 // The per-token part: softmax and top-k of one token's logits l (lane l owns
 // experts l + 64*c) by one wave.  probs are stored here.  With K <= 64 the
-// choices are returned, lane j holding round j's expert and renormalised weight
-// in *out_e / *out_w (lanes >= K: unspecified), and the caller stores them; with
-// more rounds lane 0 stores each choice to top_idx/top_w and renormalises them
-// in memory.
+// choices are returned, lane j holding choice j's expert and renormalised
+// weight in *out_e / *out_w (lanes >= K: unspecified), and the caller stores
+// them; with more choices lane 0 stores each expert to top_idx and every lane
+// stores its renormalised weights.
 template <int EPL>
 __device__ __forceinline__ void select_token(float (&l)[EPL], int t, int E, int K, const float* __restrict__ bias,
                                              int select_logits, float* __restrict__ probs,
@@ -308,7 +375,7 @@ __device__ __forceinline__ void select_token(float (&l)[EPL], int t, int E, int 
 #pragma unroll
   for (int c = 0; c < EPL; ++c) {
     const int e = lane + c * kWave;
-    p[c] = (e < E) ? det_expf(l[c] - m) : 0.0f;
+    p[c] = (e < E) ? softmax_expf(l[c] - m) : 0.0f;
     s += p[c];
   }
 #pragma unroll
@@ -321,16 +388,16 @@ __device__ __forceinline__ void select_token(float (&l)[EPL], int t, int E, int 
   }
   // selection keys
   uint32_t key[EPL];
+  float kval[EPL];
 #pragma unroll
   for (int c = 0; c < EPL; ++c) {
     const int e = lane + c * kWave;
-    const float v = (bias != nullptr && e < E) ? l[c] + bias[e] : (select_logits ? l[c] : p[c]);
-    key[c] = (e < E) ? sortable_key(v) : 0u;
+    kval[c] = (bias != nullptr && e < E) ? l[c] + bias[e] : (select_logits ? l[c] : p[c]);
+    key[c] = (e < E) ? sortable_key(kval[c]) : 0u;
   }
   uint32_t taken = 0;
-  float sel_sum = 0.0f;
   int my_e = 0;
-  float my_p = 0.0f;
+  float my_p = 0.0f, my_p_hi = 0.0f, my_k = 0.0f, seq_sum = 0.0f;
   for (int j = 0; j < K; ++j) {
     uint64_t best = 0;
 #pragma unroll
@@ -345,30 +412,44 @@ __device__ __forceinline__ void select_token(float (&l)[EPL], int t, int E, int 
     const int e_sel = __builtin_amdgcn_readfirstlane(
         static_cast<int>(0xffffffffu - static_cast<uint32_t>(best & 0xffffffffu)));  // the same in every lane
     const int owner = e_sel % kWave, slot = e_sel / kWave;
-    float p_sel = 0.0f;
+    float p_sel = 0.0f, k_sel = 0.0f;
 #pragma unroll
     for (int c = 0; c < EPL; ++c)
-      if (c == slot) p_sel = p[c];
+      if (c == slot) {
+        p_sel = p[c];
+        k_sel = kval[c];
+      }
     p_sel = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p_sel), owner));
+    k_sel = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(k_sel), owner));
     if (lane == owner) taken |= 1u << slot;
-    sel_sum = (j == 0) ? p_sel : sel_sum + p_sel;
     if (lane == j) {
       my_e = e_sel;
       my_p = p_sel;
+      my_k = k_sel;
     }
+    if (lane == j - kWave) my_p_hi = p_sel;
     if (K > kWave && lane == 0) {
       top_idx[static_cast<int64_t>(t) * K + j] = e_sel;
-      top_w[static_cast<int64_t>(t) * K + j] = p_sel;  // renormalised below
+      if (K > 2 * kWave) top_w[static_cast<int64_t>(t) * K + j] = p_sel;
     }
+    seq_sum = (j == 0) ? p_sel : seq_sum + p_sel;
   }
+  if (K > 2 * kWave) {
+    // more than 128 choices: renormalised by the plain sum in choice order
+    // (torch reduces rows this long in vectors; not restated here)
+    if (lane == 0)
+      for (int j = 0; j < K; ++j) top_w[static_cast<int64_t>(t) * K + j] /= seq_sum;
+    return;
+  }
+  if (K <= kWave) topk_tie_order(K, my_k, my_e, my_p);
+  const float sum = topk_weight_sum(my_p, my_p_hi, K);
   if (K <= kWave) {
     *out_e = my_e;
-    *out_w = my_p / sel_sum;
-  } else if (lane == 0) {
-    for (int j = 0; j < K; ++j) {
-      float* w = top_w + static_cast<int64_t>(t) * K + j;
-      *w = *w / sel_sum;
-    }
+    *out_w = my_p / sum;
+  } else {
+    float* w = top_w + static_cast<int64_t>(t) * K;
+    w[lane] = my_p / sum;
+    if (lane + kWave < K) w[lane + kWave] = my_p_hi / sum;
   }
 }
 
@@ -391,7 +472,7 @@ __device__ __forceinline__ void select_tokens(float (&l)[TT], const int (&t)[TT]
 #pragma unroll
   for (int i = 0; i < TT; ++i) {
     if (__any(l[i] != l[i])) m[i] = __builtin_nanf("");  // fmaxf drops NaN; torch's softmax does not
-    p[i] = live ? det_expf(l[i] - m[i]) : 0.0f;
+    p[i] = live ? softmax_expf(l[i] - m[i]) : 0.0f;
     s[i] = 0.0f + p[i];  // select_token's per-lane sum starts at 0 (0 + -0 is +0)
     out_e[i] = 0;
     out_w[i] = 0.0f;
@@ -401,15 +482,17 @@ __device__ __forceinline__ void select_tokens(float (&l)[TT], const int (&t)[TT]
 #pragma unroll
     for (int i = 0; i < TT; ++i) s[i] += __shfl_xor(s[i], o, kWave);
   uint64_t key[TT];
+  float kval[TT], out_k[TT];
   const float b = (bias != nullptr && live) ? bias[lane] : 0.0f;
 #pragma unroll
   for (int i = 0; i < TT; ++i) {
     p[i] = p[i] / s[i];
     if (probs != nullptr && live && valid[i]) probs[static_cast<int64_t>(t[i]) * E + lane] = p[i];
-    const float v = (bias != nullptr && live) ? l[i] + b : (select_logits ? l[i] : p[i]);
-    key[i] = live ? (static_cast<uint64_t>(sortable_key(v)) << 32) | (0xffffffffu - static_cast<uint32_t>(lane)) : 0;
+    kval[i] = (bias != nullptr && live) ? l[i] + b : (select_logits ? l[i] : p[i]);
+    key[i] = live ? (static_cast<uint64_t>(sortable_key(kval[i])) << 32) | (0xffffffffu - static_cast<uint32_t>(lane))
+                  : 0;
+    out_k[i] = 0.0f;
   }
-  float sel_sum[TT];
   for (int j = 0; j < K; ++j) {
     uint64_t best[TT];
 #pragma unroll
@@ -419,16 +502,20 @@ __device__ __forceinline__ void select_tokens(float (&l)[TT], const int (&t)[TT]
       const int e_sel = __builtin_amdgcn_readfirstlane(
           static_cast<int>(0xffffffffu - static_cast<uint32_t>(best[i] & 0xffffffffu)));  // the same in every lane
       const float p_sel = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[i]), e_sel));
+      const float k_sel = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kval[i]), e_sel));
       if (lane == e_sel) key[i] = 0;  // taken
-      sel_sum[i] = (j == 0) ? p_sel : sel_sum[i] + p_sel;
       if (lane == j) {
         out_e[i] = e_sel;
         out_w[i] = p_sel;
+        out_k[i] = k_sel;
       }
     }
   }
 #pragma unroll
-  for (int i = 0; i < TT; ++i) out_w[i] = out_w[i] / sel_sum[i];
+  for (int i = 0; i < TT; ++i) {
+    topk_tie_order(K, out_k[i], out_e[i], out_w[i]);
+    out_w[i] = out_w[i] / topk_weight_sum(out_w[i], 0.0f, K);
+  }
 }
 
 // With `partial` != NULL the logits are first assembled from the router GEMM's

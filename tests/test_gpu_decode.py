@@ -85,8 +85,11 @@ def check_step(moe, T, precision, seed=7):
     assert np.abs(scores - ref_scores).max() <= 1e-5 * max(1.0, np.abs(ref_scores).max())
     bias = None if step.bias is None else step.bias.cpu().numpy()
     dtype = {"fp32": "f32", "bf16": "bf16", "fp16": "f16"}[precision]
+    probs_t = torch.softmax(step.scores(), dim=-1)             # torch's softmax on this device
+    assert torch.equal(step.probs, probs_t)
     res = oracle.decode_step(xs, rw, oracle_weights(step), top_k=step.top_k, dtype=dtype,
-                             temperature=step.temperature, expert_bias=bias, logits=scores)
+                             temperature=step.temperature, expert_bias=bias, logits=scores,
+                             probs=probs_t.cpu().numpy())
     # bit-exact routing given the scores
     assert np.array_equal(step.probs.cpu().numpy().view(np.int32), res["probs"].view(np.int32))
     assert np.array_equal(step.last_top_indices.cpu().numpy(), res["top_idx"])

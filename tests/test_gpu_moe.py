@@ -1,7 +1,8 @@
 """Whole MoE layer forward on the GPU (qw_moe_forward / TopKMoE) against the oracle.
 
-Routing (indices, weights, capacity slots, drops, overflow) is compared bit
-for bit given the kernel's logits; outputs normwise within 1e-4 (fp32) or
+Routing (probabilities against torch's softmax on the device; indices,
+weights, capacity slots, drops, overflow against the oracle fed those
+probabilities) is compared bit for bit given the kernel's logits; outputs normwise within 1e-4 (fp32) or
 2e-2 (bf16 / int8 / int4).  Each workload runs at an oracle-friendly scale and
 at its full size.
 """
@@ -69,8 +70,11 @@ def check_layer(workload, tol_scale=1.0, tiles=False):
     ref_logits = oracle.router_logits(x, rw)
     assert np.abs(logits - ref_logits).max() <= 1e-5 * max(1.0, np.abs(ref_logits).max())
     bias = None if layer.bias is None else layer.bias.cpu().numpy()
+    # the probabilities are torch's softmax on this device, bit for bit
+    probs_t = torch.softmax(run.workspace_view("logits"), dim=-1)
+    assert torch.equal(run.probs, probs_t)
     res = oracle.moe_forward(x, rw, host_weights(layer), top_k=workload.top_k, cap=run.capacity, dtype=workload.act,
-                             expert_bias=bias, logits=logits)
+                             expert_bias=bias, logits=logits, probs=probs_t.cpu().numpy())
     # bit-exact routing and plan
     assert np.array_equal(run.probs.cpu().numpy().view(np.int32), res["probs"].view(np.int32))
     assert np.array_equal(run.top_idx.cpu().numpy(), res["top_idx"])
@@ -296,8 +300,10 @@ def test_small_batch_routing_and_plan_with_duplicate_tokens(T, E, k, cap):
     run()
     torch.cuda.synchronize()
     logits = run.workspace_view("logits").cpu().numpy()
+    probs_t = torch.softmax(run.workspace_view("logits"), dim=-1)
+    assert torch.equal(run.probs, probs_t)
     res = oracle.moe_forward(layer.x.float().cpu().numpy(), layer.router.float().cpu().numpy(), host_weights(layer),
-                             top_k=k, cap=cap, dtype="bf16", logits=logits)
+                             top_k=k, cap=cap, dtype="bf16", logits=logits, probs=probs_t.cpu().numpy())
     assert np.array_equal(run.top_idx.cpu().numpy(), res["top_idx"])
     assert np.array_equal(run.top_w.cpu().numpy().view(np.int32), res["top_w"].view(np.int32))
     assert np.array_equal(run.probs.cpu().numpy().view(np.int32), res["probs"].view(np.int32))

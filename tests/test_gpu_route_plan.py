@@ -1,7 +1,11 @@
-"""Routing and capacity plan on the GPU against the oracle — bit-exact.
+"""Routing and capacity plan on the GPU — bit-exact.
 
-Given identical fp32 logits, probabilities, top-k indices, renormalised
-weights, capacity slots, dropped lists and overflow must be identical bits.
+The reference routes with torch's own kernels (src/quantweave_moe_model.py:
+127-136, :172-188), so on this device its bits are torch-ROCm's: given
+identical fp32 logits the library's probabilities, top-k indices (in
+torch.topk's order, ties included), renormalised weights, capacity slots,
+dropped lists and overflow must equal what torch computes here, bit for bit.
+The oracle's selection and plan, fed the same probabilities, must agree too.
 """
 
 import numpy as np
@@ -9,7 +13,9 @@ import pytest
 import torch
 
 import oracle
+from quantaweave_amd import workloads as W
 from tests import hipcall as H
+from tests.torch_routing import assert_plan_equal, torch_plan, torch_route
 
 pytestmark = pytest.mark.gpu
 
@@ -22,29 +28,57 @@ def _logits(T, E, seed, scale=2.0, hot=0.0):
     return L
 
 
+def _check_route(L: torch.Tensor, k: int, bias: torch.Tensor | None = None):
+    """qw_moe_route_from_logits against torch on the device and the oracle's selection from torch's probabilities."""
+    p_g, i_g, w_g = H.route_from_logits(L, k, bias)
+    p_t, i_t, w_t = torch_route(L, k, bias)
+    assert torch.equal(p_g, p_t), "probabilities differ from torch's softmax"
+    assert torch.equal(i_g.long(), i_t), "top-k indices differ from torch.topk"
+    assert torch.equal(w_g, w_t), "renormalised weights differ from torch's"
+    i_o, w_o = oracle.route_from_probs(L.cpu().numpy(), p_t.cpu().numpy(), k,
+                                       None if bias is None else bias.cpu().numpy())
+    assert np.array_equal(i_o, i_g.cpu().numpy()) and np.array_equal(w_o.view(np.int32),
+                                                                       w_g.cpu().numpy().view(np.int32))
+    return p_g, i_g, w_g
+
+
 @pytest.mark.parametrize("T,E,k", [(512, 8, 2), (8192, 64, 2), (16, 64, 2), (300, 100, 3), (257, 184, 1),
-                                   (64, 1024, 8), (1, 64, 64), (33, 1, 1), (130, 65, 2)])
-def test_route_from_logits_is_bit_exact(T, E, k):
+                                   (2048, 184, 3), (64, 1024, 8), (1, 64, 64), (33, 1, 1), (130, 65, 2),
+                                   (4096, 64, 4), (1000, 16, 5), (500, 128, 7), (200, 256, 33), (100, 200, 100)])
+def test_route_from_logits_equals_torch_on_device(T, E, k):
     print(f"case T={T} E={E} k={k}", flush=True)
-    L = _logits(T, E, T + E + k)
-    p_o, i_o, w_o = oracle.route_from_logits(L, k)
-    p_g, i_g, w_g = (t.cpu().numpy() for t in H.route_from_logits(H.dev(L), k))
-    assert np.array_equal(p_g.view(np.int32), p_o.view(np.int32))
-    assert np.array_equal(i_g, i_o)
-    assert np.array_equal(w_g.view(np.int32), w_o.view(np.int32))
+    for seed in range(3):
+        _check_route(H.dev(_logits(T, E, T + E + k + 1000 * seed)), k)
 
 
-def test_route_with_bias_and_extreme_logits_is_bit_exact():
+@pytest.mark.parametrize("k", [1, 2, 3, 4, 5, 8, 16, 32, 33])
+def test_route_ties_take_torch_topk_order(k):
+    """Logits on a coarse grid, so many probabilities tie exactly: the chosen set
+    and its order must be torch.topk's (its 32-wide bitonic sort is not stable)."""
+    print(f"case ties k={k}", flush=True)
+    for E in (64, 184):
+        if k > E:
+            continue
+        rng = np.random.RandomState(E + k)
+        L = (np.rint(rng.randn(600, E) * 2) / 2).astype(np.float32)
+        L[0, :] = 0.0                                             # one all-equal row
+        L[1, :] = -3.0
+        L[1, [5, 40, E - 1]] = 2.0                                # a three-way tie at the top
+        _check_route(H.dev(L), k)
+        bias = H.dev((np.rint(rng.randn(E) * 2) / 4).astype(np.float32))
+        _check_route(H.dev(L), k, bias)                          # biased scores tie as well
+
+
+def test_route_with_bias_and_extreme_logits():
     L = _logits(400, 64, 5, scale=30.0)                       # probabilities down to subnormals and zero
     L[3, :] = 0.0                                             # an all-tie row
     L[4, 10:20] = 5.0                                         # ties at the top
-    bias = np.linspace(-2, 2, 64).astype(np.float32)
-    for b in (None, bias):
-        p_o, i_o, w_o = oracle.route_from_logits(L, 4, b)
-        p_g, i_g, w_g = (t.cpu().numpy() for t in H.route_from_logits(H.dev(L), 4, None if b is None else H.dev(b)))
-        assert np.array_equal(p_g.view(np.int32), p_o.view(np.int32))
-        assert np.array_equal(i_g, i_o) and np.array_equal(w_g.view(np.int32), w_o.view(np.int32))
-    assert (p_o < 2 ** -126).any() and (p_o == 0).any()
+    bias = H.dev(np.linspace(-2, 2, 64).astype(np.float32))
+    for k in (1, 2, 4, 8):
+        for b in (None, bias):
+            p, _, _ = _check_route(H.dev(L), k, b)
+    p = p.cpu().numpy()
+    assert (p < 2 ** -126).any() and (p == 0).any()
 
 
 def test_expert_bias_steers_selection_only():
@@ -72,24 +106,59 @@ def test_router_logits_match_oracle_and_routing_follows(dtype, T, D, E):
     ref = oracle.router_logits(x.float().numpy(), w.float().numpy(), 1.5)
     got = logits.cpu().numpy()
     assert np.abs(got - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
-    # the rest of the routing is bit-exact given the kernel's own logits
-    p_o, i_o, w_o = oracle.route_from_logits(got, k)
-    assert np.array_equal(probs.cpu().numpy().view(np.int32), p_o.view(np.int32))
-    assert np.array_equal(idx.cpu().numpy(), i_o) and np.array_equal(tw.cpu().numpy(), w_o)
+    # the rest of the routing is torch's, bit for bit, given the kernel's own logits
+    p_t, i_t, w_t = torch_route(logits, k)
+    assert torch.equal(probs, p_t) and torch.equal(idx.long(), i_t) and torch.equal(tw, w_t)
 
 
+# the benchmark's workload shapes (routing part), a many-expert top-3 layer, and
+# a batch of near-duplicate tokens whose routes tie on weight across tokens
+SWEEP = {
+    "fp32-T512-E8": (W.WORKLOADS["fp32-plumbing-T512-d256-E8-f512-k2"], None),
+    "bf16-T8192-E64": (W.WORKLOADS["bf16-prefill-T8192-d2048-E64-f1024-k2"], None),
+    "int8-decode-T64-E64": (W.WORKLOADS["int8-decode-T64-d2048-E64-f1024-k2"], None),
+    "int4-decode-T16-E64": (W.WORKLOADS["int4-decode-T16-d4096-E64-f1408-k2"], None),
+    "skewed-T4096-E64": (W.WORKLOADS["skewed-T4096-d2048-E64-f1024-k2"], None),
+    "T2048-E184-k3": (W.Workload("e184", 2048, 256, 184, 64, 3, 1.25, "f32", "f32", 0), None),
+    "near-duplicate-T4096-E64": (W.Workload("dup", 4096, 256, 64, 64, 2, 1.0, "bf16", "bf16", 0), "dup"),
+}
 
-@pytest.mark.parametrize("T,D,E", [(300, 256, 64), (40, 512, 16)])
-def test_router_reads_strided_rows(T, D, E):
-    """x given as a view with a row stride larger than d_model gives the same bits as contiguous rows."""
-    print(f"case T={T} D={D} E={E} strided", flush=True)
-    g = torch.Generator().manual_seed(T * D)
-    wide = torch.randn(T, D + 64, generator=g).to(torch.bfloat16).cuda()
-    w = (torch.randn(E, D, generator=g) * 0.02).to(torch.bfloat16).cuda()
-    got = H.route(wide[:, :D], w, 2)
-    ref = H.route(wide[:, :D].contiguous(), w, 2)
-    for a, b in zip(got, ref):
-        assert torch.equal(a, b)
+
+def _sweep_inputs(w, kind, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    act = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[w.act]
+    if kind == "dup":
+        base = torch.randn(8, w.d_model, generator=g, device="cuda")
+        x = base.repeat(w.tokens // 8, 1) + 1e-6 * torch.randn(w.tokens, w.d_model, generator=g, device="cuda")
+    else:
+        x = torch.randn(w.tokens, w.d_model, generator=g, device="cuda")
+    router = torch.randn(w.experts, w.d_model, generator=g, device="cuda") * 0.02
+    bias = W.zipf_bias(w.experts, w.zipf).cuda() if w.zipf else None
+    return x.to(act).contiguous(), router.to(act).contiguous(), bias
+
+
+@pytest.mark.parametrize("name", list(SWEEP))
+def test_routing_and_plan_equal_torch_on_device_over_seeds(name):
+    """20 seeds per shape: the product's routing (router kernel, then the plan)
+    against the reference's composition run by torch on this GPU from the
+    router kernel's own logits — probabilities, indices, weights, slots,
+    dropped lists and overflow identical."""
+    w, kind = SWEEP[name]
+    cap = w.capacity()
+    drops = 0
+    for seed in range(20):
+        print(f"case {name} seed={seed}", flush=True)
+        x, router, bias = _sweep_inputs(w, kind, seed)
+        logits, probs, idx, tw = H.route(x, router, w.top_k, bias=bias)
+        p_t, i_t, w_t = torch_route(logits, w.top_k, bias)
+        assert torch.equal(probs, p_t) and torch.equal(idx.long(), i_t) and torch.equal(tw, w_t)
+        got = H.plan(idx, tw, w.experts, cap)
+        ref = torch_plan(i_t, w_t, w.experts, cap)
+        assert_plan_equal(got, ref)
+        drops += ref["overflow"]
+    if w.zipf or kind == "dup":
+        assert drops > 0  # hot experts overflow
+
 
 def _check_plan(idx, w, E, cap):
     ref = oracle.plan(idx, w, E, cap)
@@ -135,21 +204,12 @@ def test_plan_with_equal_weights_and_tiny_capacity():
 def test_plan_matches_torch_double_argsort_on_device():
     """The reference's own ops (src/quantweave_moe_model.py:172-188) run by torch on the GPU."""
     T, E, k = 4096, 64, 2
-    _, idx, w = oracle.route_from_logits(_logits(T, E, 11, hot=3.0), k)
+    _, idx, w = torch_route(H.dev(_logits(T, E, 11, hot=3.0)), k)
     cap = oracle.capacity(T, k, E, 1.0)
-    re = torch.from_numpy(idx.astype(np.int64)).cuda().reshape(-1)
-    rw = torch.from_numpy(w).cuda().reshape(-1)
-    by_weight = torch.argsort(rw, descending=True, stable=True)
-    order = by_weight[torch.argsort(re[by_weight], stable=True)]
-    counts = torch.bincount(re, minlength=E)
-    offsets = torch.cumsum(counts, 0) - counts
-    position = torch.arange(order.numel(), device="cuda") - offsets[re[order]]
-    keep = position < cap
-    got = H.plan(H.dev(idx), H.dev(w), E, cap)
-    assert np.array_equal(got["slot_token"], (order[keep] // k).cpu().numpy())
-    assert np.array_equal(got["dropped_token"], (order[~keep] // k).cpu().numpy())
-    assert np.array_equal(got["dropped_expert"], re[order[~keep]].cpu().numpy())
-    assert int(got["totals"][1]) == int((~keep).sum())
+    got = H.plan(idx.int().contiguous(), w, E, cap)
+    ref = torch_plan(idx, w, E, cap)
+    assert ref["overflow"] > 0
+    assert_plan_equal(got, ref)
 
 
 def test_empty_token_batch_is_a_no_op():
