@@ -12,9 +12,11 @@
  * `workspace` whose size the caller obtains from the matching
  * qw_*_workspace_bytes() function.  Apart from the one allocation-free entry
  * point (qw_moe_decode_step_noalloc, whose scratch is a static per-device
- * array), the library keeps no mutable global state, so calls on different
- * streams do not interfere (calls that share a workspace must be ordered on
- * one stream).
+ * array) and two read-only per-device caches filled on first use (that
+ * array's address, and the occupancy figure the int4/int8 decode kernels size
+ * their grid by), the library keeps no mutable global state, so calls on
+ * different streams do not interfere (calls that share a workspace must be
+ * ordered on one stream).
  *
  * Reference citations are paths inside the QuantaWeave source tree.
  */
@@ -238,6 +240,14 @@ int qw_moe_decode_step(const float* x, const float* residual, int64_t tokens, in
                        float* probs, int32_t* top_idx, float* top_w, void* workspace, size_t workspace_bytes,
                        void* stream);
 
+/* Library set-up for the current device: looks up the device address of the
+ * allocation-free entry point's static scratch array (which may load the
+ * library's code object on that device and so allocate its global memory).
+ * Call it once per device, outside graph capture, before a graph captures
+ * qw_moe_decode_step_noalloc; calling it again is cheap.  No counterpart in
+ * the reference (no other entry point needs it). */
+int qw_init(void);
+
 /* qw_moe_decode_step without a workspace argument: its scratch is a
  * library-owned array of qw_moe_decode_step_noalloc_scratch_bytes() (32 MiB)
  * on each device, so the call performs no allocation of any kind (it calls no
@@ -251,7 +261,10 @@ int qw_moe_decode_step(const float* x, const float* residual, int64_t tokens, in
  * Every call on one device shares that device's array and leaves its last
  * contents there (every value a step reads it first writes, so nothing needs
  * clearing); calls that overlap on one device — on different streams or
- * threads without ordering — race. */
+ * threads without ordering — race.  The array's address is looked up by
+ * qw_init(); a call on a device where that has not happened does it first,
+ * unless the stream is being captured, in which case the call is refused
+ * (QW_ERR_INVALID) so that nothing is loaded or allocated under capture. */
 size_t qw_moe_decode_step_noalloc_scratch_bytes(void);
 int qw_moe_decode_step_noalloc(const float* x, const float* residual, int64_t tokens, int64_t d_model,
                                const float* router_w, float temperature, const float* expert_bias, int64_t experts,

@@ -306,29 +306,53 @@ def swiglu(x: np.ndarray, gate: np.ndarray, up: np.ndarray, down: np.ndarray, dt
     return linear(h, down, dtype, accum)
 
 
-def expert_weights(w: dict, e: int, dtype: str) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+def _codes_times_scales(q: np.ndarray, scales: np.ndarray, bits: int, in_features: int, group: int) -> np.ndarray:
+    """q * scale per group in float64 (exact: a code has at most 8 bits, a
+    scale 24), from the stored bytes (the layout of src/quantization.py:43-59)."""
+    q = np.asarray(q)
+    if bits == 4:
+        u = q.astype(np.int16)
+        codes = np.empty((q.shape[0], q.shape[1] * 2), np.int16)
+        codes[:, 0::2] = (u & 0xF) - 8
+        codes[:, 1::2] = (u >> 4) - 8
+    else:
+        codes = q.astype(np.int16)
+    s = np.repeat(np.asarray(scales, np.float64), group, axis=1)
+    return (codes.astype(np.float64) * s)[:, :in_features]
+
+
+def expert_weights(w: dict, e: int, dtype: str, quantised: str = "reference") -> tuple[np.ndarray, np.ndarray, np.ndarray]:
     """Effective (gate, up, down) of expert e as the reference multiplies them:
     float weights as stored; quantised ones dequantised (fp32) and cast to the
-    activation dtype (src/quantization.py:72)."""
+    activation dtype (src/quantization.py:72).  quantised="exact" instead keeps
+    q * scale unrounded (float64): the arithmetic of the weight-streaming
+    decode kernels, which multiply the exact codes and apply each group's fp32
+    scale to the group's partial sum."""
     if w["format"] in ("f32", "bf16", "f16"):
         # float weights are cast to the activation dtype (src/moe_kernels.py:191-193)
         return tuple(round_act(w[n][e], dtype) for n in ("gate", "up", "down"))
     bits = 8 if w["format"] == "i8" else 4
     d, f = w["d_model"], w["d_ff"]
+    if quantised == "exact":
+        return (_codes_times_scales(w["gate"][e], w["gate_scales"][e], bits, d, w["group_in"]),
+                _codes_times_scales(w["up"][e], w["up_scales"][e], bits, d, w["group_in"]),
+                _codes_times_scales(w["down"][e], w["down_scales"][e], bits, f, w["group_ff"]))
     g = dequantize(w["gate"][e], w["gate_scales"][e], bits, d, w["group_in"])
     u = dequantize(w["up"][e], w["up_scales"][e], bits, d, w["group_in"])
     dn = dequantize(w["down"][e], w["down_scales"][e], bits, f, w["group_ff"])
     return round_act(g, dtype), round_act(u, dtype), round_act(dn, dtype)
 
 
-def experts_forward(x_rows: np.ndarray, kept_counts: np.ndarray, w: dict, dtype: str, accum: str = "f64") -> np.ndarray:
+def experts_forward(x_rows: np.ndarray, kept_counts: np.ndarray, w: dict, dtype: str, accum: str = "f64",
+                    quantised: str = "reference") -> np.ndarray:
     """The per-expert loop, src/quantweave_moe_model.py:203-209: expert e runs on
-    its contiguous block of plan-ordered rows."""
+    its contiguous block of plan-ordered rows (quantised weights as
+    expert_weights gives them)."""
     out = np.zeros((x_rows.shape[0], w["d_model"]), dtype=np.float32)
     start = 0
     for e, c in enumerate(kept_counts.tolist()):
         if c:
-            g, u, dn = expert_weights(w, e, dtype)
+            g, u, dn = expert_weights(w, e, dtype, quantised)
             out[start:start + c] = swiglu(x_rows[start:start + c], g, u, dn, dtype, accum)
         start += c
     return out

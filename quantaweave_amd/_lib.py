@@ -45,6 +45,7 @@ SIGNATURES = {
     "qw_moe_decode_step_workspace_bytes": (SZ, [I64, I64, I64, I64, I64, I32]),
     "qw_moe_decode_step": (I32, [P, P, I64, I64, P, F32, P, I64, I64, I64, I32, I32, I64, I64,
                                  P, P, P, P, P, P, P, P, P, P, P, SZ, P]),
+    "qw_init": (I32, []),
     "qw_moe_decode_step_noalloc_scratch_bytes": (SZ, []),
     "qw_moe_decode_step_noalloc": (I32, [P, P, I64, I64, P, F32, P, I64, I64, I64, I32, I32, I64, I64,
                                          P, P, P, P, P, P, P, P, P, P, P]),

@@ -240,14 +240,13 @@ static DecodeWs carve_decode(void* base, int64_t T, int64_t D, int64_t E, int64_
 constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;  // 32 MiB per device
 static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
 
-constexpr int kMaxDevices = 64;
 static std::atomic<void*> g_scratch_ptr[kMaxDevices];
 
-// Device address of `scratch` on the current device (looked up once per device).
-static int scratch_on_current_device(void** out) {
-  int dev = 0;
-  QW_HIP_CHECK(hipGetDevice(&dev));
-  if (dev < 0 || dev >= kMaxDevices) return set_error(QW_ERR_UNSUPPORTED, "device %d is beyond the library's table", dev);
+// Looks up the device address of `scratch` on the current device (once per
+// device; qw_init).  The lookup can load the library's code object on that
+// device, which allocates its global memory, so it must not happen inside a
+// graph capture: the allocation-free entry point does it only outside one.
+static int scratch_lookup(int dev, void** out) {
   void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
   if (!p) {
     QW_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
@@ -255,6 +254,13 @@ static int scratch_on_current_device(void** out) {
     g_scratch_ptr[dev].store(p, std::memory_order_release);  // the same address whoever stores it first
   }
   *out = p;
+  return QW_OK;
+}
+
+static int current_device(int* dev) {
+  QW_HIP_CHECK(hipGetDevice(dev));
+  if (*dev < 0 || *dev >= kMaxDevices)
+    return set_error(QW_ERR_UNSUPPORTED, "device %d is beyond the library's table", *dev);
   return QW_OK;
 }
 
@@ -521,6 +527,14 @@ int qw_moe_decode_step(const float* x, const float* residual, int64_t tokens, in
   return decode_combine(w.y, compute_dtype, w.route_slot, top_w, residual, tokens, top_k, d_model, out, s);
 }
 
+int qw_init(void) {
+  clear_error();
+  int dev = 0;
+  if (const int st = current_device(&dev)) return st;
+  void* p = nullptr;
+  return scratch_lookup(dev, &p);
+}
+
 size_t qw_moe_decode_step_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
 
 int qw_moe_decode_step_noalloc(const float* x, const float* residual, int64_t tokens, int64_t d_model,
@@ -547,8 +561,19 @@ int qw_moe_decode_step_noalloc(const float* x, const float* residual, int64_t to
     QW_HIP_CHECK(hipStreamGetDevice(s, &sdev));
     QW_REQUIRE(sdev == cur, "the stream belongs to device %d but device %d is current", sdev, cur);
   }
-  void* ws = nullptr;
-  if (const int st = scratch_on_current_device(&ws)) return st;
+  int dev = 0;
+  if (const int st = current_device(&dev)) return st;
+  void* ws = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!ws) {
+    // not set up on this device: look the array up now unless the stream is
+    // being captured (the lookup may load the code object and allocate)
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    QW_HIP_CHECK(hipStreamIsCapturing(s, &cap));
+    QW_REQUIRE(cap == hipStreamCaptureStatusNone,
+               "qw_moe_decode_step_noalloc: call qw_init() on device %d outside graph capture before capturing it",
+               dev);
+    if (const int st = scratch_lookup(dev, &ws)) return st;
+  }
   return qw_moe_decode_step(x, residual, tokens, d_model, router_w, temperature, expert_bias, experts, top_k, d_ff,
                             compute_dtype, w_format, group_in, group_ff, gate_w, gate_scales, up_w, up_scales, down_w,
                             down_scales, out, probs, top_idx, top_w, ws, kNoAllocScratchBytes, stream);

@@ -76,6 +76,7 @@ inline hipError_t reserve_lds(int bytes) {
 // Device helpers
 // ---------------------------------------------------------------------------
 constexpr int kWave = 64;
+constexpr int kMaxDevices = 64;  // per-device tables of the library (scratch addresses, occupancy caches)
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
 

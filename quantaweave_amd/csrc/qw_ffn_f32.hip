@@ -379,8 +379,12 @@ int launch_ffn_f32(const FfnArgs& a, hipStream_t stream, bool* handled) {
   *handled = false;
   if (a.act != QW_F32 || a.wfmt != QW_F32) return QW_OK;
   if (a.d_model % 4 || a.d_ff % 4) return QW_OK;
+  // every operand the kernels read or write in 16-byte vectors (rows of d_model
+  // or d_ff floats, so each row start is aligned when the base is)
   if ((reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.gate.w) | reinterpret_cast<uintptr_t>(a.up.w) |
-       reinterpret_cast<uintptr_t>(a.down.w)) % 16)
+       reinterpret_cast<uintptr_t>(a.down.w) | reinterpret_cast<uintptr_t>(a.y) | reinterpret_cast<uintptr_t>(a.hidden) |
+       reinterpret_cast<uintptr_t>(a.save_gate) | reinterpret_cast<uintptr_t>(a.save_up) |
+       reinterpret_cast<uintptr_t>(a.save_y)) % 16)
     return QW_OK;
   const int D = static_cast<int>(a.d_model), F = static_cast<int>(a.d_ff), mr = static_cast<int>(a.max_rows);
   const int64_t avg = a.avg_rows > 0 ? a.avg_rows : ceil_div(a.max_rows, a.experts);
@@ -427,7 +431,10 @@ int launch_ffn_f32(const FfnArgs& a, hipStream_t stream, bool* handled) {
 int grouped_matmul_f32(const float* x, const float* w, int64_t E, int64_t N, int64_t K, const int32_t* offsets,
                        int64_t rows, float* out, hipStream_t stream, bool* handled) {
   *handled = false;
-  if (K % 4 || (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) % 16) return QW_OK;
+  // 16-byte vectors: x and w rows of K floats, out rows of N floats
+  if (K % 4 || N % 4 ||
+      (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out)) % 16)
+    return QW_OK;
   const unsigned z = f32_row_splits(ceil_div(rows, E));
   const dim3 g(static_cast<unsigned>(ceil_div(N, F32_N)), static_cast<unsigned>(E), z);
   ffn_f32_mfma_kernel<false><<<g, F32_THREADS, 0, stream>>>(x, nullptr, offsets, w, w, N * K, static_cast<int>(N),

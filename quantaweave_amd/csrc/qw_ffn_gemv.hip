@@ -502,7 +502,9 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
         a = wave_max(a);
         int ex = 0;
         frexpf(a, &ex);  // a in [2^(ex-1), 2^ex)
-        scale[m] = a > 0.0f ? ldexpf(1.0f, 15 - ex) : 1.0f;
+        // 2^(15 - ex), at most 2^126 (routes of tiny activations: the scale and
+        // its inverse stay finite and normal; such rows are then below 2^14)
+        scale[m] = a > 0.0f ? ldexpf(1.0f, min(15 - ex, 126)) : 1.0f;
         inv[m] = 1.0f / scale[m];
       }
     }
@@ -877,7 +879,7 @@ __global__ __launch_bounds__(64) void ffn_qmf_kernel(
         amax = fmaxf(amax, xor_lane<32>(amax, addr32));
         int ex = 0;
         frexpf(amax, &ex);  // amax in [2^(ex-1), 2^ex)
-        sigma = amax > 0.0f ? ldexpf(1.0f, 15 - ex) : 1.0f;
+        sigma = amax > 0.0f ? ldexpf(1.0f, min(15 - ex, 126)) : 1.0f;  // at most 2^126, as above
         inv_own = 1.0f / sigma;
       }
 #pragma unroll
@@ -1098,15 +1100,22 @@ int launch_qmf_s(const FfnArgs& a, const WView& wa, const WView& wb, const void*
   if (touched * n_groups >= 8192 && WF == QW_I8 && GATEUP) {
     gpw = 6;
   } else if (touched * n_groups >= 8192) {
-    static int slots = 0;  // per instantiation: waves of this kernel the device holds at once
+    // per instantiation and device: waves of this kernel the device holds at
+    // once.  A read-only cache filled on first use; threads that race to fill
+    // it compute and store the same value (atomics: no torn or unordered access).
+    static std::atomic<int> slot_cache[kMaxDevices];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+      return set_error(QW_ERR_HIP, "cannot query the current device");
+    int slots = slot_cache[dev].load(std::memory_order_relaxed);
     if (slots == 0) {
-      int dev = 0, cus = 0, per_cu = 0;
-      if (hipGetDevice(&dev) != hipSuccess ||
-          hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      int cus = 0, per_cu = 0;
+      if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
           hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 64, LD::BYTES) != hipSuccess || cus <= 0 ||
           per_cu <= 0)
         return set_error(QW_ERR_HIP, "cannot query the occupancy of ffn_qmf_kernel");
       slots = cus * per_cu;
+      slot_cache[dev].store(slots, std::memory_order_relaxed);
     }
     const double E = static_cast<double>(a.experts);
     const double active = E * (1.0 - std::pow(1.0 - 1.0 / E, static_cast<double>(a.max_rows)));

@@ -69,7 +69,7 @@ class MoEDecodeStep:
         bias = getattr(moe, "expert_bias", None)
         self.bias = None if bias is None else bias.detach().to(device, torch.float32).contiguous()
         experts = moe.experts
-        pack = ExpertPack(experts)
+        pack = ExpertPack(experts, rehome=False)
         for name in ("gate", "up", "down", "gate_s", "up_s", "down_s"):
             t = getattr(pack, name)
             if t is not None:

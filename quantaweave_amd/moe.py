@@ -128,6 +128,23 @@ def can_tile(stack: Tensor) -> bool:
     return stack.dtype in _hip.HALF and stack.size(1) % 64 == 0 and stack.size(2) % 64 == 0
 
 
+# Every registration of a module, parameter or buffer anywhere in the process
+# (nn.Module.__setattr__, add_module, register_parameter / register_buffer)
+# bumps this generation.  An expert pack that recorded the current generation
+# knows that no expert module, weight or buffer object was swapped since.
+_GENERATION = [0]
+
+
+def _registered(*_args) -> None:
+    _GENERATION[0] += 1
+
+
+_REGISTRATION_HOOKS = (
+    torch.nn.modules.module.register_module_module_registration_hook(_registered),
+    torch.nn.modules.module.register_module_parameter_registration_hook(_registered),
+    torch.nn.modules.module.register_module_buffer_registration_hook(_registered),
+)
+
 _SUBMODULES = attrgetter("_modules")
 _GATE_UP_DOWN = itemgetter("gate", "up", "down")
 _PARAMETERS = attrgetter("_parameters")
@@ -142,22 +159,30 @@ class ExpertPack:
     """Experts' weights stacked once into [E, out, in] device buffers.
 
     Replaces the per-call ``torch.stack`` of src/moe_kernels.py:191-193; the pack
-    is rebuilt only when a projection module, parameter or buffer changes
-    (tracked by identity, storage pointer and version counter).  bf16 and fp16 weights whose shapes allow it
-    are kept in the QW_BF16T / QW_F16T tiles the prefill kernels stream contiguously."""
+    is rebuilt only when a projection module, parameter or buffer changes.
+    bf16 and fp16 weights whose shapes allow it are kept in the QW_BF16T /
+    QW_F16T tiles the prefill kernels stream contiguously.
 
-    def __init__(self, experts: nn.ModuleList) -> None:
+    Quantised experts' ``qweight`` / ``scales`` buffers are re-registered as
+    views of the pack's stacks (``rehome``): the module and the kernels then
+    read one copy of the bytes.
+
+    Currency, per call: ``fast_current`` when the pack is armed, else
+    ``current``.  ``current`` compares every module, tensor, version counter
+    and storage pointer (O(experts)).  ``arm`` makes an O(1) token when the
+    experts' tensors share a few version counters (float weights created by
+    TopKMoE as views of one buffer, quantised buffers re-homed into the
+    stacks): the registration generation, those counters' versions and the
+    first and last tensor's identity and storage.  What the token cannot see:
+    replacing one expert tensor's storage without registering anything (an
+    ``_apply`` on a single expert, ``.data =`` on one weight); call
+    ``TopKMoE.refresh_experts()`` after such a change."""
+
+    def __init__(self, experts: nn.ModuleList, rehome: bool = True) -> None:
         self.fmt, self.group_in, self.group_ff = _expert_format(experts)
-        self.mods, self.tensors = ExpertPack.sources(experts)
-        # what current() compares, as tuples built by C-level iteration (the
-        # pack holds the objects, so their ids cannot be reused meanwhile)
         self._exps = tuple(experts._modules.values())
-        self._exp_ids = tuple(map(id, self._exps))
-        self._mod_ids = tuple(map(id, self.mods))
-        self._tensor_ids = tuple(map(id, self.tensors))
-        self._quant = isinstance(self.mods[0], QuantizedLinear)
-        self.versions = tuple(map(_VERSION, self.tensors))
-        self.ptrs = tuple(map(_DATA_PTR, self.tensors))
+        self._quant = isinstance(self._exps[0]._modules["gate"], QuantizedLinear)
+        self._token = None
         if self.fmt in (_lib.QW_F32, _lib.QW_BF16, _lib.QW_F16):
             self.gate = torch.stack([e.gate.weight.detach() for e in experts]).contiguous()
             self.up = torch.stack([e.up.weight.detach() for e in experts]).contiguous()
@@ -171,6 +196,61 @@ class ExpertPack:
             self.gate_s = torch.stack([e.gate.scales.float() for e in experts]).contiguous()
             self.up_s = torch.stack([e.up.scales.float() for e in experts]).contiguous()
             self.down_s = torch.stack([e.down.scales.float() for e in experts]).contiguous()
+            if rehome and self.gate.device.type == "cuda":
+                for i, e in enumerate(self._exps):
+                    for name, q, sc in (("gate", self.gate, self.gate_s), ("up", self.up, self.up_s),
+                                        ("down", self.down, self.down_s)):
+                        m = e._modules[name]
+                        m.qweight, m.scales = q[i], sc[i]
+        self._record(experts)
+
+    def _record(self, experts: nn.ModuleList) -> None:
+        """What ``current`` compares, as tuples built by C-level iteration (the
+        pack holds the objects, so their ids cannot be reused meanwhile)."""
+        self.mods, self.tensors = ExpertPack.sources(experts)
+        self._exp_ids = tuple(map(id, self._exps))
+        self._mod_ids = tuple(map(id, self.mods))
+        self._tensor_ids = tuple(map(id, self.tensors))
+        self.versions = tuple(map(_VERSION, self.tensors))
+        self.ptrs = tuple(map(_DATA_PTR, self.tensors))
+
+    def __getstate__(self) -> dict:
+        state = dict(self.__dict__)
+        state["_token"] = None  # a copy's tensors may not share counters: re-armed on first use
+        return state
+
+    def arm(self) -> None:
+        """Make the O(1) token if the pack's tensors share at most 8 version
+        counters.  Sharing is found by bumping each candidate counter once
+        (torch.autograd.graph.increment_version: no data is touched) and
+        seeing which tensors' versions move with it."""
+        self._token = None
+        reps, rest = [], list(self.tensors)
+        while rest and len(reps) < 8:
+            before = tuple(map(_VERSION, rest))
+            torch.autograd.graph.increment_version(rest[0])
+            after = tuple(map(_VERSION, rest))
+            reps.append(rest[0])
+            rest = [t for t, b, a in zip(rest, before, after) if a == b]
+        self.versions = tuple(map(_VERSION, self.tensors))
+        if rest:
+            return
+        self._reps = tuple(reps)
+        first, last = self.tensors[0], self.tensors[-1]
+        self._token = (_GENERATION[0], tuple(map(_VERSION, self._reps)), first.data_ptr(), last.data_ptr())
+
+    def fast_current(self) -> bool:
+        """The O(1) check of an armed pack (see the class docstring)."""
+        tok = self._token
+        if tok is None or tok[0] != _GENERATION[0] or tuple(map(_VERSION, self._reps)) != tok[1]:
+            return False
+        e0, e1 = self._exps[0]._modules, self._exps[-1]._modules
+        if self._quant:
+            first, last = e0["gate"]._buffers["qweight"], e1["down"]._buffers["scales"]
+        else:
+            first, last = e0["gate"]._parameters["weight"], e1["down"]._parameters["weight"]
+        return (first is self.tensors[0] and last is self.tensors[-1] and first.data_ptr() == tok[2]
+                and last.data_ptr() == tok[3])
 
     def maybe_tile(self) -> None:
         """bf16 / fp16 stacks on a ROCm device -> QW_BF16T / QW_F16T tiles (in place of the plain stacks)."""
@@ -265,10 +345,16 @@ class ExpertPack:
 
 
 def packed_experts(owner: nn.Module, experts: nn.ModuleList) -> ExpertPack:
-    pack = getattr(owner, "_qw_pack", None)
+    """The owner's expert pack, rebuilt when the experts changed: an armed
+    pack is checked in O(1), otherwise every expert tensor is compared and the
+    pack re-armed."""
+    pack = owner.__dict__.get("_qw_pack")
+    if pack is not None and pack.fast_current():
+        return pack
     if pack is None or not pack.current(experts):
         pack = ExpertPack(experts)
         owner._qw_pack = pack
+    pack.arm()
     return pack
 
 
@@ -301,6 +387,7 @@ class TopKMoE(nn.Module):
         if self.num_local_experts != self.num_experts:
             raise ValueError("expert-parallel sharding is not supported by the single-GPU HIP path")
         self.experts = nn.ModuleList(SparseSwiGLU(config, config.ffn_size) for _ in range(self.num_local_experts))
+        self._share_expert_storage()
         # runtime switches (not parameters or saved state), as in the reference
         self.collect_stats = False
         self.static_dispatch = False
@@ -329,6 +416,30 @@ class TopKMoE(nn.Module):
     @last_top_indices.setter
     def last_top_indices(self, value: Optional[Tensor]) -> None:
         self.__dict__["_last_top_idx"] = value
+
+    @torch.no_grad()
+    def _share_expert_storage(self) -> None:
+        """Re-create the experts' weights (same values, shapes and
+        requires_grad) as views of one buffer.  Views of one tensor share its
+        version counter, and keep sharing it through .to() / .cuda() / .half()
+        (which swap each parameter's data in place), so the expert pack's
+        per-call check reads one version instead of one per weight."""
+        lins = [e._modules[n] for e in self.experts for n in ("gate", "up", "down")]
+        ws = [lin._parameters["weight"] for lin in lins]
+        base = torch.empty(sum(w.numel() for w in ws), dtype=ws[0].dtype, device=ws[0].device)
+        off = 0
+        for lin, w in zip(lins, ws):
+            view = base[off:off + w.numel()].view_as(w)
+            view.copy_(w)
+            lin.weight = nn.Parameter(view, requires_grad=w.requires_grad)
+            off += w.numel()
+
+    def refresh_experts(self) -> None:
+        """Drop the expert pack, so the next forward re-stacks the experts'
+        weights.  Needed only after a change the pack's checks cannot see:
+        ``.data =`` on one expert weight, or ``.to()`` applied to a single
+        expert."""
+        self.__dict__.pop("_qw_pack", None)
 
     def capacity(self, num_tokens: int) -> int:
         """Route slots per expert (src/quantweave_moe_model.py:100-111)."""
@@ -402,7 +513,7 @@ class TopKMoE(nn.Module):
             dropped_routes = overflow_routes
         else:
             dropped_routes = torch.zeros((), device=dev, dtype=torch.long)
-        if self.collect_stats:
+        if self.collect_stats and not self.static_dispatch:  # the dynamic path only (:141-149)
             self._record_stats(probs.detach(), top_idx, kept_counts, totals, dropped_token, dropped_expert)
         domain_loss = probs.new_zeros(())
         if token_domains is not None and num_domains > 1:

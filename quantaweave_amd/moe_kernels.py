@@ -229,13 +229,12 @@ def grouped_swiglu(inputs: Tensor, experts: nn.ModuleList, counts: Sequence[int]
 
 def benchmark(experts: int = 32, tokens: int = 8192, hidden: int = 256, ffn: int = 512, top_k: int = 2, repeats: int = 20,
               bf16: bool = False) -> dict:
-    """Wall-clock forward + backward of the HIP MoE layer on the current GPU,
-    optionally under bf16 autocast (src/moe_kernels.py:198-227).
-
-    The reference times its per-expert loop and its Triton executor; this
-    build has one executor, reported as ``hip_ms`` (forward + backward, the
-    reference's measurement), with ``forward_ms`` the forward alone under
-    no_grad."""
+    """Wall-clock the loop and grouped expert paths on the current GPU
+    (forward + backward), optionally under bf16 autocast (src/moe_kernels.py:
+    198-227): ``loop_ms`` is the per-expert executor (``use_triton_kernels =
+    False``), ``triton_ms`` the grouped one, ``speedup`` their ratio; both run
+    the HIP kernels.  ``forward_ms`` (not in the reference) is the grouped
+    forward alone under no_grad."""
     from .moe import QuantaWeaveConfig, TopKMoE
 
     if not kernels_available(torch.device("cuda")):
@@ -258,7 +257,8 @@ def benchmark(experts: int = 32, tokens: int = 8192, hidden: int = 256, ffn: int
             moe(x)
 
     result = {}
-    for name, fn in (("hip", train_step), ("forward", forward)):
+    for name, fn, grouped in (("loop", train_step, False), ("triton", train_step, True), ("forward", forward, True)):
+        moe.use_triton_kernels = grouped
         for _ in range(3):
             fn()
         torch.cuda.synchronize()
@@ -267,6 +267,7 @@ def benchmark(experts: int = 32, tokens: int = 8192, hidden: int = 256, ffn: int
             fn()
         torch.cuda.synchronize()
         result[name + "_ms"] = (time.perf_counter() - started) / repeats * 1000
+    result["speedup"] = result["loop_ms"] / result["triton_ms"]
     result.update(experts=experts, tokens=tokens, hidden=hidden, ffn=ffn, top_k=top_k, bf16=bf16)
     return result
 
@@ -276,7 +277,7 @@ if __name__ == "__main__":
     import argparse
     import json
 
-    ap = argparse.ArgumentParser(description="forward + backward wall clock of the HIP MoE layer")
+    ap = argparse.ArgumentParser(description="forward + backward wall clock of the loop and grouped executors")
     ap.add_argument("--experts", type=int, default=32)
     ap.add_argument("--tokens", type=int, default=8192)
     ap.add_argument("--hidden", type=int, default=256)

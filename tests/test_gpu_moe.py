@@ -282,8 +282,11 @@ def test_stats_and_static_dispatch():
     assert st["dropped_tokens"].numel() == overflow.item() == st["dropped_experts"].numel()
     assert st["expert_assigned"].sum().item() == 32
     moe.static_dispatch = True
+    before = st
     _, _, dropped, overflow, _ = moe(hidden)
     assert overflow.item() == 0
+    # the reference records stats on the dynamic path only (src/quantweave_moe_model.py:141-149)
+    assert moe.last_stats is before
 
 
 @pytest.mark.parametrize("T,E,k,cap", [(1, 64, 2, 2), (7, 8, 2, 3), (16, 64, 2, 32), (24, 6, 3, 5), (40, 16, 4, 4),
@@ -500,3 +503,43 @@ def test_balance_with_workspace_matches_float64_and_is_deterministic(T, E, K):
     for imp, bal in (outs[0], (imp0.cpu(), bal0.cpu())):
         assert (imp.double() - imp64).abs().max() <= 1e-6 * max(imp64.abs().max().item(), 1e-30)
         assert abs(float(bal) - bal64) <= 1e-5 * max(abs(bal64), 1e-30)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_fast_decoder_prefill_composition(dt):
+    """The call FastDecoder._prefill makes (src/fast_decode.py:219-235): fp32
+    hidden states under bf16 (fp16) autocast, drop_overflow_tokens=False, and
+    static_dispatch on (dense: E*n <= 4096) or off.  Each output is checked
+    against the oracle on the run's routing (rows and weights rounded to the
+    autocast type, expert arithmetic in that type, route terms added in fp32:
+    index_add_ in plan order for the sorted path, the per-expert loop of
+    _static_output for the dense one), and the two paths agree as in
+    tests/test_fast_decode.py:70-79 (atol 1e-5)."""
+    print(f"case prefill composition {dt}", flush=True)
+    torch.manual_seed(21)
+    moe = qa.TopKMoE(small_config(hidden_size=64, ffn_size=128, num_experts=8, capacity_factor=1.0)).cuda()
+    n = 40
+    x = torch.randn(n, 64, device="cuda")
+    hidden = torch.nn.functional.layer_norm(x, (64,)).unsqueeze(0)           # [1, n, d] fp32
+    name = "bf16" if dt == torch.bfloat16 else "f16"
+    outs = {}
+    for dense in (True, False):
+        moe.drop_overflow_tokens, moe.static_dispatch = False, dense
+        with torch.no_grad(), torch.autocast("cuda", dtype=dt):
+            res = moe(hidden)
+        out = res[0][0].float()
+        assert res[0].dtype == torch.float32 and int(res[3]) == 0             # no capacity: nothing overflows
+        plan = moe.last_plan
+        top_idx = moe.last_top_indices.cpu().numpy().astype(np.int32)
+        top_w = plan["top_w"].cpu().numpy()
+        p = oracle.plan(top_idx, top_w, 8, n * 2)
+        rows = oracle.round_act(hidden[0].cpu().numpy()[p["slot_token"]], name)
+        y = oracle.experts_forward(rows, p["kept_counts"], module_weights(moe), name)
+        combine = oracle.combine_static if dense else oracle.combine
+        ref = combine(y, p["slot_token"], p["slot_weight"], n, "f32")
+        err = normwise(out.cpu().numpy(), ref)
+        print(f"  dense={dense} normwise {err:.3e}", flush=True)
+        assert err <= TOL[name]
+        outs[dense] = out
+    moe.drop_overflow_tokens, moe.static_dispatch = True, False
+    assert torch.allclose(outs[True], outs[False], atol=1e-5)

@@ -106,3 +106,64 @@ def test_decode_step_refuses_cpu_and_names_precisions():
     assert precision_dtype(torch.device("cuda"), "fp32") == torch.float32
     with pytest.raises(KeyError):
         precision_dtype(torch.device("cuda"), "fp8")
+
+
+def test_expert_pack_currency_check_is_o1_and_sees_every_change():
+    """The pack is re-stacked when the experts change; an armed pack checks
+    one shared version counter, the registration generation and the first and
+    last weight instead of every tensor."""
+    import copy
+
+    from quantaweave_amd.moe import packed_experts
+
+    moe = qa.TopKMoE(small_config())
+    ws = [getattr(e, n).weight for e in moe.experts for n in ("gate", "up", "down")]
+    pack = packed_experts(moe, moe.experts)
+    assert pack._token is not None and len(pack._reps) == 1         # one counter covers all 18 weights
+    assert packed_experts(moe, moe.experts) is pack and pack.fast_current()
+    # an optimizer step on one expert (in place): the shared counter moves
+    opt = torch.optim.SGD([ws[7]], lr=0.1)
+    ws[7].grad = torch.ones_like(ws[7])
+    opt.step()
+    assert not pack.fast_current()
+    new = packed_experts(moe, moe.experts)
+    assert new is not pack and torch.equal(new.up[2], ws[7].detach())
+    # load_state_dict copies in place
+    sd = {k: v.clone() + 1 for k, v in moe.state_dict().items()}
+    moe.load_state_dict(sd)
+    assert not new.fast_current()
+    p2 = packed_experts(moe, moe.experts)
+    assert torch.equal(p2.down[5], moe.experts[5].down.weight.detach())
+    # replacing a projection module or a weight registers it: the generation moves
+    moe.experts[3].up = torch.nn.Linear(16, 32, bias=False)
+    assert not p2.fast_current()
+    p3 = packed_experts(moe, moe.experts)
+    assert torch.equal(p3.up[3], moe.experts[3].up.weight.detach())
+    assert p3._token is not None and len(p3._reps) == 2            # the new weight has its own counter
+    moe.experts[1].gate.weight = torch.nn.Parameter(torch.zeros(32, 16))
+    assert not p3.fast_current()
+    p4 = packed_experts(moe, moe.experts)
+    assert p4.gate[1].abs().sum() == 0
+    # a conversion of the whole module swaps every weight's data: the first and last storage move
+    moe.half()
+    assert not p4.fast_current()
+    p5 = packed_experts(moe, moe.experts)
+    assert p5.gate.dtype == torch.float16 and p5._token is not None
+    # a copy re-checks everything on first use
+    dup = copy.deepcopy(moe)
+    assert dup._qw_pack._token is None
+    moe.refresh_experts()
+    assert "_qw_pack" not in moe.__dict__
+
+
+def test_expert_weights_share_one_buffer_and_keep_their_values():
+    torch.manual_seed(0)
+    moe = qa.TopKMoE(small_config())
+    ws = [getattr(e, n).weight for e in moe.experts for n in ("gate", "up", "down")]
+    assert all(w.requires_grad and w.is_leaf for w in ws)
+    base = ws[0].untyped_storage().data_ptr()
+    assert all(w.untyped_storage().data_ptr() == base for w in ws)
+    assert len({w.data_ptr() for w in ws}) == len(ws)
+    # nn.Linear's init scale survives the move: |w| <= 1/sqrt(fan_in)
+    assert max(float(w.detach().abs().max()) for w in ws[:2]) <= 16 ** -0.5
+    assert set(dict(moe.named_parameters())) >= {"experts.0.gate.weight", "experts.5.down.weight"}

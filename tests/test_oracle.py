@@ -729,3 +729,25 @@ def test_static_combine_equals_torchs_static_output(dt):
     assert np.array_equal(got, ref.float().numpy())
     if dt == torch.float32:  # in fp32 the static and dynamic accumulations agree (src: tests/test_model_features.py:49-56)
         assert np.array_equal(got, oracle.combine(rows, p["slot_token"], p["slot_weight"], T, "f32"))
+
+
+@pytest.mark.parametrize("bits,group,shape", [(8, None, (16, 64)), (4, 32, (16, 64)), (4, 16, (8, 40)), (8, 16, (8, 40))])
+def test_exact_dequantisation_is_the_unrounded_product(bits, group, shape):
+    """quantised="exact" (the streaming decode kernels' weights) is q * scale
+    in float64: within fp32 rounding of dequantize(), equal to the codes times
+    the scales computed independently, and not the weights rounded to bf16."""
+    rng = np.random.RandomState(bits + shape[1])
+    w = (rng.randn(*shape) * 0.05).astype(np.float32)
+    q, s, g = oracle.quantize(w, bits, group)
+    exact = oracle._codes_times_scales(q, s, bits, shape[1], g)
+    deq = oracle.dequantize(q, s, bits, shape[1], g).astype(np.float64)
+    assert np.all(np.abs(exact - deq) <= np.abs(deq) * 2.0 ** -24)
+    if bits == 8:
+        codes = q.astype(np.float64)
+    else:
+        codes = np.empty((shape[0], q.shape[1] * 2))
+        codes[:, 0::2] = (q & 0xF).astype(np.float64) - 8
+        codes[:, 1::2] = (q >> 4).astype(np.float64) - 8
+    per_col = np.repeat(s.astype(np.float64), g, axis=1)
+    assert np.array_equal(exact, (codes * per_col)[:, :shape[1]])
+    assert not np.array_equal(exact, oracle.round_bf16(exact.astype(np.float32)).astype(np.float64))

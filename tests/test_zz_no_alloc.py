@@ -79,3 +79,70 @@ def test_noalloc_refuses_a_step_beyond_its_scratch():
     with pytest.raises(ValueError, match="scratch"):
         _lib.call("qw_moe_decode_step_noalloc", None, None, 4096, 4096, None, 1.0, None, 64, 2, 1408, _lib.QW_BF16,
                   _lib.QW_U4, 32, 32, None, None, None, None, None, None, None, None, None, None, None)
+
+
+CAPTURE_SCRIPT = r"""
+import sys
+import torch
+from quantaweave_amd import _hip, _lib
+from quantaweave_amd import workloads as W
+from tests.test_zz_no_alloc import decode_args, step_workspace
+
+P = _hip.ptr
+layer = W.build_layer(W.WORKLOADS["int4-decode-T16-d4096-E64-f1408-k2"])
+router = layer.router.float().contiguous()
+D = layer.w.d_model
+g = torch.Generator(device="cuda").manual_seed(5)
+x = torch.randn(3, D, generator=g, device="cuda")
+r = torch.randn(3, D, generator=g, device="cuda")
+head, outs = decode_args(layer, x, r, router)
+stream = torch.cuda.Stream()
+torch.cuda.synchronize()
+if sys.argv[1] == "refused":
+    # no set-up on this device: a call under capture must be refused, not allocate
+    graph = torch.cuda.CUDAGraph()
+    err = None
+    with torch.cuda.graph(graph, stream=stream):
+        try:
+            _lib.call("qw_moe_decode_step_noalloc", *head, _hip.stream(x.device))
+        except ValueError as e:
+            err = str(e)
+    assert err is not None and "qw_init" in err, err
+    print("refused ok", flush=True)
+    sys.exit(0)
+_lib.call("qw_init")                               # set-up, outside capture
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph, stream=stream):       # the process's first allocation-free call
+    _lib.call("qw_moe_decode_step_noalloc", *head, _hip.stream(x.device))
+want = step_workspace(layer, x, r, router)
+for rep in range(3):
+    for t in outs:
+        t.zero_()
+    x.add_(0.25 * rep)                              # eager work between the replays
+    want = step_workspace(layer, x, r, router)
+    graph.replay()
+    torch.cuda.synchronize()
+    for u, v in zip(outs, want):
+        assert torch.equal(u, v), rep
+print("capture ok", flush=True)
+"""
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["captured", "refused"])
+def test_noalloc_first_call_under_graph_capture(mode):
+    """A fresh process: with qw_init() made outside capture, the first
+    allocation-free call is recorded in a HIP graph, and every replay (eager
+    work in between) equals the workspace step bit for bit; without it, the
+    call under capture is refused with an error naming qw_init."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    print(f"case noalloc capture {mode}", flush=True)
+    root = Path(__file__).resolve().parent.parent
+    proc = subprocess.run([sys.executable, "-c", CAPTURE_SCRIPT, mode], cwd=root, capture_output=True, text=True,
+                          timeout=240)
+    print(proc.stdout[-2000:], proc.stderr[-2000:], flush=True)
+    assert proc.returncode == 0
+    assert ("capture ok" if mode == "captured" else "refused ok") in proc.stdout
