@@ -454,3 +454,24 @@ def test_grouped_matmul_f32_output_offset_by_one_float(N, K):
                      for e, (s, c) in enumerate(zip(np.cumsum([0] + counts[:-1]), counts))])
     assert torch.allclose(aligned.double(), ref, atol=1e-4, rtol=1e-4)
     assert torch.allclose(shifted.double(), ref, atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("D", [2048, 4096])
+def test_int8_decode_route_of_tiny_activations(D):
+    """int8 rows with bf16 activations scale each route by a power of two so
+    its values are exact in fp16; a route whose largest |x| is below 2^-112
+    must not overflow that scale (its output is ~0, not NaN).  D=2048 runs the
+    matrix-core kernel, D=4096 the dot-product one."""
+    print(f"case int8 decode tiny route D={D}", flush=True)
+    counts = [2, 3]
+    rng = np.random.RandomState(D)
+    x = rng.randn(sum(counts), D).astype(np.float32)
+    x[1] *= 2.0 ** -120
+    x[3] *= 2.0 ** -126
+    x = oracle.round_bf16(x)
+    w = make_weights(len(counts), D, 1024, "i8", 11)
+    got = run_experts(x, counts, w, "bf16", path="stream")
+    assert np.isfinite(got).all()
+    ref = oracle.experts_forward(x, np.array(counts), w, "bf16")
+    assert np.abs(got[[1, 3]]).max() <= 1e-30
+    assert normwise(got, ref) <= DECODE_DEV["bf16"]
