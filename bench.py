@@ -45,6 +45,9 @@ def parse():
                     help="only time the batch-1 decode steps (one JSON line with their figures)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (calibrates HBM byte counters)")
+    ap.add_argument("--stream-probe", action="store_true",
+                    help="only measure the HBM rates the chip sustains for a plain read (a 2 GiB sum) and a "
+                         "plain copy (1 GiB to 1 GiB): the practical ceiling next to the 8 TB/s peak")
     return ap.parse_args()
 
 
@@ -255,7 +258,13 @@ def cpu_baseline(name, budget_s=8.0):
     del layer
     torch.cuda.empty_cache()
     cap = w.capacity()
-    threads = torch.get_num_threads()
+    # the host's cores (BASELINE's plan: torch.set_num_threads(os.cpu_count())), but
+    # never more threads than this process may run on (a cpuset or affinity mask)
+    host_cores = os.cpu_count() or 1
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else host_cores
+    threads = min(host_cores, usable)
+    prev_threads = torch.get_num_threads()
+    torch.set_num_threads(threads)
     with torch.no_grad():
         t0 = time.perf_counter()
         torch_ref.moe_forward(x, router, experts, w.top_k, cap, expert_bias=bias)  # warm-up
@@ -265,12 +274,14 @@ def cpu_baseline(name, budget_s=8.0):
             t1 = time.perf_counter()
             torch_ref.moe_forward(x, router, experts, w.top_k, cap, expert_bias=bias)
             times.append(time.perf_counter() - t1)
+    torch.set_num_threads(prev_threads)
     med = float(np.median(times))
     return dict(value=round(w.tokens / med, 1), unit="tokens/s", cores=threads, kind="port",
                 sample=f"the whole workload ({w.tokens} tokens, {w.experts} experts, capacity {cap}) through the "
                        f"reference's loop-executor forward restated with torch CPU ops (oracle/torch_ref.py), "
                        f"{w.act} activations, {w.weights} experts; median of {len(times)} runs after one warm-up; "
-                       f"{threads} torch threads on {cpu_model()}")
+                       f"{threads} torch threads (host: {host_cores} logical CPUs, {usable} usable by this "
+                       f"process) on {cpu_model()}")
 
 
 def committed_traffic(name):
@@ -328,6 +339,17 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": n, "launches": 3}), flush=True)
+        return
+    if args.stream_probe:
+        n = 1 << 31
+        src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty(n // 8, dtype=torch.float32, device="cuda")
+        stream = torch.cuda.current_stream()
+        read_ms = min(event_time(lambda: src.sum(), 5, stream) for _ in range(3))
+        copy_ms = min(event_time(lambda: dst.copy_(src[: n // 8]), 5, stream) for _ in range(3))
+        print(json.dumps({"read_gbs": round(n / (read_ms / 1000) / 1e9, 1),
+                          "copy_gbs": round(n / (copy_ms / 1000) / 1e9, 1),
+                          "read_bytes": n, "copy_bytes_read_plus_written": n}), flush=True)
         return
     if args.decode_steps_only:
         decode = {}
@@ -407,6 +429,11 @@ def main():
                    "top_k": w.top_k, "capacity_factor": w.capacity_factor, "weights": w.weights, "seed": w.seed},
         "roofline": roof,
         "cpu_baseline": cpu,
+        # the same layer through the drop-in module (TopKMoE.forward, no grad): the
+        # value above plus the balance loss the reference computes on every call
+        # (src/quantweave_moe_model.py:152-154), the int64 counts and the Python call
+        "module": {"ms_per_step": round(module_ms, 4), "tokens_per_s": round(w.tokens / (module_ms / 1000.0), 1),
+                   "includes": "route, plan, experts, combine, balance loss, Python"},
         "workloads": per,
         "decode_step": decode,
     }
