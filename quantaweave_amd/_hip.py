@@ -2,8 +2,6 @@
 
 from __future__ import annotations
 
-import ctypes
-
 import torch
 
 from . import _lib
@@ -26,12 +24,15 @@ def act_code(t: torch.Tensor, what: str) -> int:
         raise ValueError(f"{what}: dtype {t.dtype} is not supported (float32, bfloat16 or float16)") from None
 
 
-def ptr(t: torch.Tensor | None):
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+def ptr(t: torch.Tensor | None) -> int | None:
+    """Device address of a tensor for a `void*` argument (ctypes converts the
+    int; None is NULL)."""
+    return None if t is None else t.data_ptr()
 
 
-def stream(device: torch.device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+def stream(device: torch.device) -> int:
+    """The current HIP stream of `device`, for a `void* stream` argument."""
+    return torch.cuda.current_stream(device).cuda_stream
 
 
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:

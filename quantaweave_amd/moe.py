@@ -153,6 +153,7 @@ _WEIGHT = itemgetter("weight")
 _QBUFFERS = itemgetter("qweight", "scales")
 _VERSION = attrgetter("_version")
 _DATA_PTR = methodcaller("data_ptr")
+_REQUIRES_GRAD = attrgetter("requires_grad")
 
 
 class ExpertPack:
@@ -289,9 +290,16 @@ class ExpertPack:
         return (tuple(map(_VERSION, self.tensors)) == self.versions
                 and tuple(map(_DATA_PTR, self.tensors)) == self.ptrs)
 
-    def args(self) -> list:
-        return [self.fmt, self.group_in, self.group_ff, _hip.ptr(self.gate), _hip.ptr(self.gate_s),
-                _hip.ptr(self.up), _hip.ptr(self.up_s), _hip.ptr(self.down), _hip.ptr(self.down_s)]
+    def args(self) -> tuple:
+        """Weight arguments of the C ABI (format, groups, weight and scale
+        pointers), kept while the pack holds the same tensors."""
+        key = (self.fmt, id(self.gate), id(self.up), id(self.down), id(self.gate_s), id(self.up_s), id(self.down_s))
+        cached = self.__dict__.get("_args")
+        if cached is None or cached[0] != key:
+            cached = (key, (self.fmt, self.group_in, self.group_ff, _hip.ptr(self.gate), _hip.ptr(self.gate_s),
+                            _hip.ptr(self.up), _hip.ptr(self.up_s), _hip.ptr(self.down), _hip.ptr(self.down_s)))
+            self._args = cached
+        return cached[1]
 
     def plain(self, experts: nn.ModuleList, dtype: torch.dtype) -> list:
         """[gate, up, down] stacks [E, out, in] in `dtype`, untiled, for the
@@ -450,10 +458,14 @@ class TopKMoE(nn.Module):
             )
         return num_tokens * self.top_k
 
-    def _wants_grad(self, hidden: Tensor) -> bool:
+    def _wants_grad(self, hidden: Tensor, pack: "ExpertPack") -> bool:
         if not torch.is_grad_enabled():
             return False
-        return hidden.requires_grad or any(p.requires_grad for p in self.parameters())
+        if hidden.requires_grad or self.router.weight.requires_grad:
+            return True
+        if pack._quant:
+            return False
+        return any(map(_REQUIRES_GRAD, pack.tensors))
 
     def forward(self, hidden: Tensor, token_domains: Optional[Tensor] = None,
                 num_domains: int = 0) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
@@ -479,7 +491,7 @@ class TopKMoE(nn.Module):
         # the loop executor (use_triton_kernels False, set_moe_kernel("loop")) launches
         # the experts one at a time, as the reference's loop does (:203-209)
         loop = not self.use_triton_kernels
-        if not profiling and self._wants_grad(hidden):
+        if not profiling and self._wants_grad(hidden, pack):
             if pack.fmt not in (_lib.QW_F32, _lib.QW_BF16, _lib.QW_BF16T, _lib.QW_F16, _lib.QW_F16T):
                 if hidden.requires_grad:
                     raise NotImplementedError("gradients through quantised experts are not supported")
@@ -568,41 +580,47 @@ def _forward_call(flat: Tensor, act: int, router_w: Tensor, moe: TopKMoE, pack: 
     Rm = max(R, 1)
     rw = _router_operand(router_w)
     # the per-call outputs in two slabs (int32 and fp32), handed out as views
-    ints = torch.empty(T * K + 2 * E + 2 + 2 * Rm, dtype=torch.int32, device=dev)
-    flts = torch.empty(T * E + T * K + 1 + E, dtype=torch.float32, device=dev)
-    r = dict(out=torch.empty_like(flat), probs=flts[:T * E].view(T, E), top_w=flts[T * E:T * E + T * K].view(T, K),
-             balance=flts[T * E + T * K:T * E + T * K + 1].view(()),
-             top_idx=ints[:T * K].view(T, K), counts=ints[T * K:T * K + E], kept_counts=ints[T * K + E:T * K + 2 * E],
-             totals=ints[T * K + 2 * E:T * K + 2 * E + 2], dropped_token=ints[T * K + 2 * E + 2:T * K + 2 * E + 2 + Rm],
-             dropped_expert=ints[T * K + 2 * E + 2 + Rm:])
-    importance = flts[T * E + T * K + 1:]
+    ints = torch.empty(R + 2 * E + 2 + 2 * Rm, dtype=torch.int32, device=dev)
+    flts = torch.empty(T * E + R + 1 + E, dtype=torch.float32, device=dev)
+    top_idx, counts, kept_counts, totals, dropped_token, dropped_expert = ints.split([R, E, E, 2, Rm, Rm])
+    probs, top_w, balance, importance = flts.split([T * E, R, 1, E])
+    r = dict(out=torch.empty_like(flat), probs=probs.view(T, E), top_w=top_w.view(T, K), balance=balance.view(()),
+             top_idx=top_idx.view(T, K), counts=counts, kept_counts=kept_counts, totals=totals,
+             dropped_token=dropped_token, dropped_expert=dropped_expert)
     if not T:
-        r["totals"].zero_()
-        r["balance"].zero_()
+        totals.zero_()
+        balance.zero_()
         return r
-    s = _hip.stream(dev)
-    d_ff = moe.experts[0].gate.out_features
+    key = (T, width, E, K, act)
+    sizes = moe.__dict__.setdefault("_qw_sizes", {}).get(key)
     lib = _lib.load()
-    nbytes = lib.qw_moe_forward_workspace_bytes(T, width, E, K, d_ff, act)
-    fwd_bytes = (nbytes + 255) // 256 * 256
-    bal_bytes = lib.qw_moe_balance_workspace_bytes(T, E)
-    ws = _stream_workspace(moe, fwd_bytes + bal_bytes, dev)
-    _lib.call("qw_moe_forward", _hip.ptr(flat), act, T, width, _hip.ptr(rw), _hip.act_code(rw, "router"),
-              float(moe.router_temperature), _hip.ptr(bias), E, K, cap, d_ff, *pack.args(), _hip.ptr(r["out"]),
-              _hip.ptr(r["probs"]), _hip.ptr(r["top_idx"]), _hip.ptr(r["top_w"]), _hip.ptr(r["counts"]),
-              _hip.ptr(r["kept_counts"]), _hip.ptr(r["totals"]), _hip.ptr(r["dropped_token"]),
-              _hip.ptr(r["dropped_expert"]), _hip.ptr(ws), nbytes, s)
-    _lib.call("qw_moe_balance_ws", _hip.ptr(r["probs"]), _hip.ptr(r["counts"]), T, K, E, _hip.ptr(importance),
-              _hip.ptr(r["balance"]), _hip.ptr(ws[fwd_bytes:]), bal_bytes, s)
+    if sizes is None:
+        d_ff = moe.experts[0].gate.out_features
+        nbytes = lib.qw_moe_forward_workspace_bytes(T, width, E, K, d_ff, act)
+        fwd_bytes = (nbytes + 255) // 256 * 256
+        sizes = (d_ff, nbytes, fwd_bytes, lib.qw_moe_balance_workspace_bytes(T, E))
+        moe._qw_sizes[key] = sizes
+    d_ff, nbytes, fwd_bytes, bal_bytes = sizes
+    s = torch.cuda.current_stream(dev).cuda_stream
+    ws = _stream_workspace(moe, fwd_bytes + bal_bytes, dev, s)
+    wp, ip, fp = ws.data_ptr(), ints.data_ptr(), flts.data_ptr()
+    p_probs, p_counts = fp, ip + 4 * (R + 0)
+    _lib.check(lib.qw_moe_forward(
+        flat.data_ptr(), act, T, width, rw.data_ptr(), _hip.act_code(rw, "router"), float(moe.router_temperature),
+        _hip.ptr(bias), E, K, cap, d_ff, *pack.args(), r["out"].data_ptr(), p_probs, ip, fp + 4 * T * E, p_counts,
+        ip + 4 * (R + E), ip + 4 * (R + 2 * E), ip + 4 * (R + 2 * E + 2), ip + 4 * (R + 2 * E + 2 + Rm), wp, nbytes,
+        s), "qw_moe_forward")
+    _lib.check(lib.qw_moe_balance_ws(p_probs, p_counts, T, K, E, fp + 4 * (T * E + R + 1), fp + 4 * (T * E + R), wp +
+                                     fwd_bytes, bal_bytes, s), "qw_moe_balance_ws")
     return r
 
 
-def _stream_workspace(moe: nn.Module, nbytes: int, dev: torch.device) -> Tensor:
-    """The module's forward workspace for the current stream, kept between
-    calls (calls on one stream are ordered, so one buffer serves them all;
-    a call on another stream gets its own).  Grown when a call needs more."""
+def _stream_workspace(moe: nn.Module, nbytes: int, dev: torch.device, stream: int) -> Tensor:
+    """The module's forward workspace for `stream` (the current one), kept
+    between calls (calls on one stream are ordered, so one buffer serves them
+    all; a call on another stream gets its own).  Grown when a call needs more."""
     cache = moe.__dict__.setdefault("_qw_workspaces", {})
-    key = (dev, torch.cuda.current_stream(dev).cuda_stream)
+    key = (dev, stream)
     ws = cache.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = _hip.workspace(nbytes, dev)
