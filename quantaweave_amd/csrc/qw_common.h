@@ -387,6 +387,14 @@ __device__ T block_exclusive_scan(T v, T* warp_tot, T* total) {
 
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
 
+// silu(g) = g * sigmoid(g) with the hardware reciprocal (v_rcp_f32, 1 ulp)
+// instead of an IEEE division: a few ulp of fp32 in all, below the bf16/fp16
+// rounding that follows, and about a third of the instructions (the prefill
+// gate/up epilogue forms 80 of these per lane per tile while its compute unit
+// streams nothing).  Limits as the quotient: g -> -inf gives -0 (NaN at -inf
+// itself), g -> +inf gives g.
+__device__ __forceinline__ float silu_fast(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
+
 // silu(gate) * up with the rounding points of tensors held in activation dtype
 // DT: gate and up are rounded (they are stored projections), silu(gate) is
 // rounded, and the caller rounds the product when it stores it.
@@ -396,6 +404,35 @@ __device__ __forceinline__ float swiglu_act(float g, float u) {
   return round_act<DT>(silu_f32(gr)) * round_act<DT>(u);
 }
 __device__ __forceinline__ float swiglu_bf16(float g, float u) { return swiglu_act<QW_BF16>(g, u); }
+
+// Two SwiGLU values with the rounding points of swiglu_act (and silu_fast),
+// returned as the packed 16-bit pair (element 0 in the low half) the caller
+// stores.  bf16: each rounding of a pair is one v_cvt_pk_bf16_f32, and a bf16
+// pair widens to fp32 with a shift and a mask.
+template <int DT>
+__device__ __forceinline__ uint32_t swiglu_pack2(float g0, float g1, float u0, float u1) {
+  static_assert(DT == QW_BF16 || DT == QW_F16, "16-bit activations");
+  if constexpr (DT == QW_BF16) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    auto round2 = [](float& a, float& b) {
+      const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+      const uint32_t w = __builtin_bit_cast(uint32_t, v);
+      a = __uint_as_float(w << 16);
+      b = __uint_as_float(w & 0xffff0000u);
+    };
+    round2(g0, g1);
+    round2(u0, u1);
+    float s0 = silu_fast(g0), s1 = silu_fast(g1);
+    round2(s0, s1);
+    const bf16x2_t h = {static_cast<__bf16>(s0 * u0), static_cast<__bf16>(s1 * u1)};
+    return __builtin_bit_cast(uint32_t, h);
+  } else {
+    auto one = [](float g, float u) {
+      return f32_to_f16(round_to_f16(silu_fast(round_to_f16(g))) * round_to_f16(u));
+    };
+    return one(g0, u0) | (static_cast<uint32_t>(one(g1, u1)) << 16);
+  }
+}
 
 // Workgroup barrier that orders LDS only.  __syncthreads() also waits for every
 // outstanding global load of the wave (vmcnt(0)); this one lets global loads

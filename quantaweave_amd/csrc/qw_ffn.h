@@ -27,6 +27,50 @@ struct FfnArgs {
   void* save_y = nullptr;
 };
 
+// Workgroup order of the grouped kernels whose work items are (column tile x,
+// expert e, row chunk z).  Workgroups are dispatched round-robin over the
+// chip's 8 XCDs (block b on XCD b % 8), each XCD with its own L2.  Every tile
+// of an expert reads the expert's rows or its weights, so all of an expert's
+// tiles go to one XCD (experts e, e + 8, ... on XCD e % 8) and each byte is
+// fetched from HBM by one L2 only.  With fewer than 8 experts an expert takes
+// xpe = 8 / E XCDs, which share its row chunks (z = sub, sub + xpe, ...), so
+// the whole chip still works.  The order is a performance choice only: every
+// (x, e, z) is visited by exactly one workgroup whatever the placement.
+constexpr int kXcds = 8;
+
+struct XcdGrid {
+  int gx, experts, zs, xpe;  // column tiles, experts, row chunks, XCDs per expert
+  unsigned blocks;  // 0 when the grid would not fit a launch
+};
+
+inline XcdGrid xcd_grid(int64_t gx, int64_t experts, int64_t zs) {
+  XcdGrid g;
+  g.gx = static_cast<int>(gx);
+  g.experts = static_cast<int>(experts);
+  g.zs = static_cast<int>(zs);
+  g.xpe = experts >= kXcds ? 1 : kXcds / static_cast<int>(experts);
+  const int64_t per_xcd = g.xpe == 1 ? (experts + kXcds - 1) / kXcds * gx * zs : gx * ((zs + g.xpe - 1) / g.xpe);
+  g.blocks = kXcds * per_xcd > INT32_MAX ? 0u : static_cast<unsigned>(kXcds * per_xcd);
+  return g;
+}
+
+// Work item of block b; false for the blocks past the work (an expert index
+// past E, or a row chunk past zs).
+__device__ __forceinline__ bool xcd_tile(const XcdGrid& g, int b, int* x, int* e, int* z) {
+  const int xcd = b % kXcds, j = b / kXcds;
+  if (g.xpe == 1) {
+    const int per = g.gx * g.zs;
+    *e = xcd + kXcds * (j / per);
+    *x = (j % per) % g.gx;
+    *z = (j % per) / g.gx;
+  } else {
+    *e = xcd / g.xpe;
+    *x = j % g.gx;
+    *z = xcd % g.xpe + g.xpe * (j / g.gx);
+  }
+  return *e < g.experts && *z < g.zs;
+}
+
 int launch_ffn_generic(const FfnArgs& a, hipStream_t stream);
 int launch_ffn_mfma(const FfnArgs& a, hipStream_t stream, bool* handled);
 int launch_ffn_f32(const FfnArgs& a, hipStream_t stream, bool* handled);

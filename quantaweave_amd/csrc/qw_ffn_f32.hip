@@ -42,14 +42,15 @@ __global__ __launch_bounds__(F32_THREADS) void ffn_f32_mfma_kernel(
     const float* __restrict__ x, const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
     const float* __restrict__ wa, const float* __restrict__ wb, int64_t w_expert_stride, int n_w, int K, int n_out,
     int max_rows, const float* __restrict__ row_weight, float* __restrict__ out, float* __restrict__ save_a,
-    float* __restrict__ save_b) {
+    float* __restrict__ save_b, const XcdGrid grid) {
   __shared__ __attribute__((aligned(16))) float xs[2][F32_M * F32_LD];
   __shared__ __attribute__((aligned(16))) float ws[2][F32_N * F32_LD];
-  const int e = blockIdx.y;
+  int tx, e, tz;
+  if (!xcd_tile(grid, blockIdx.x, &tx, &e, &tz)) return;
   const int r0 = max(offsets[e], 0), r1 = min(offsets[e + 1], max_rows);
   if (r1 <= r0) return;
   constexpr int COLS = GATEUP ? F32_N / 2 : F32_N;  // output columns per tile
-  const int c0 = blockIdx.x * COLS;
+  const int c0 = tx * COLS;
   if (c0 >= n_out) return;
   const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
   const int wm = wave / 2, wn = wave % 2;
@@ -74,7 +75,7 @@ __global__ __launch_bounds__(F32_THREADS) void ffn_f32_mfma_kernel(
   const int lr = tid / 8, lc = (tid % 8) * 4;
   const float* wsrc[2] = {w_row(lr), w_row(lr + 32)};
 
-  for (int m0 = r0 + static_cast<int>(blockIdx.z) * F32_M; m0 < r1; m0 += static_cast<int>(gridDim.z) * F32_M) {
+  for (int m0 = r0 + tz * F32_M; m0 < r1; m0 += grid.zs * F32_M) {
     const float* xsrc[2];
     bool xok[2];
 #pragma unroll
@@ -228,13 +229,14 @@ __global__ __launch_bounds__(F32_THREADS) void ffn_f32_small_kernel(
     const float* __restrict__ x, const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
     const float* __restrict__ wa, const float* __restrict__ wb, int64_t w_expert_stride, int n_w, int K, int n_out,
     int max_rows, const float* __restrict__ row_weight, float* __restrict__ out, float* __restrict__ save_a,
-    float* __restrict__ save_b) {
+    float* __restrict__ save_b, const XcdGrid grid) {
   __shared__ __attribute__((aligned(16))) f32x4 red[4][4][64];  // [wave][tile (i, t)][lane]
-  const int e = blockIdx.y;
+  int tx, e, tz;
+  if (!xcd_tile(grid, blockIdx.x, &tx, &e, &tz)) return;
   const int r0 = max(offsets[e], 0), r1 = min(offsets[e + 1], max_rows);
   if (r1 <= r0) return;
   constexpr int COLS = GATEUP ? F32S_N / 2 : F32S_N;  // output columns per tile
-  const int c0 = blockIdx.x * COLS;
+  const int c0 = tx * COLS;
   if (c0 >= n_out) return;
   const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
   const int l16 = lane % 16, lq = lane / 16;
@@ -247,7 +249,7 @@ __global__ __launch_bounds__(F32_THREADS) void ffn_f32_small_kernel(
     wsrc[t] = base + static_cast<int64_t>(min(row, n_w - 1)) * K + 4 * lq;  // rows past the end: loaded, not stored
   }
   const int KS = (K + F32S_BK - 1) / F32S_BK;
-  for (int m0 = r0 + static_cast<int>(blockIdx.z) * F32S_M; m0 < r1; m0 += static_cast<int>(gridDim.z) * F32S_M) {
+  for (int m0 = r0 + tz * F32S_M; m0 < r1; m0 += grid.zs * F32S_M) {
     const float* xsrc[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -395,32 +397,36 @@ int launch_ffn_f32(const FfnArgs& a, hipStream_t stream, bool* handled) {
     // workgroup takes two chunks of a full expert one after the other)
     const int64_t cap_rows = a.row_cap > 0 ? std::min<int64_t>(a.row_cap, a.max_rows) : 2 * avg;
     const unsigned zs = static_cast<unsigned>(std::min<int64_t>(std::max<int64_t>(ceil_div(cap_rows, F32S_M), 1), 64));
-    const dim3 s1(static_cast<unsigned>(ceil_div(F, F32S_N / 2)), static_cast<unsigned>(a.experts), zs);
-    ffn_f32_small_kernel<true><<<s1, F32_THREADS, 0, stream>>>(
+    const XcdGrid s1 = xcd_grid(ceil_div(F, F32S_N / 2), a.experts, zs);
+    if (s1.blocks == 0) return set_error(QW_ERR_UNSUPPORTED, "fp32 expert grid too large");
+    ffn_f32_small_kernel<true><<<s1.blocks, F32_THREADS, 0, stream>>>(
         static_cast<const float*>(a.x), a.row_index, a.offsets, static_cast<const float*>(a.gate.w),
         static_cast<const float*>(a.up.w), a.gate.expert_elems, F, D, F, mr, nullptr, static_cast<float*>(a.hidden),
-        static_cast<float*>(a.save_gate), static_cast<float*>(a.save_up));
+        static_cast<float*>(a.save_gate), static_cast<float*>(a.save_up), s1);
     QW_LAUNCH_CHECK("ffn_f32_small_kernel<gateup>");
-    const dim3 s2(static_cast<unsigned>(ceil_div(D, F32S_N)), static_cast<unsigned>(a.experts), zs);
-    ffn_f32_small_kernel<false><<<s2, F32_THREADS, 0, stream>>>(
+    const XcdGrid s2 = xcd_grid(ceil_div(D, F32S_N), a.experts, zs);
+    if (s2.blocks == 0) return set_error(QW_ERR_UNSUPPORTED, "fp32 expert grid too large");
+    ffn_f32_small_kernel<false><<<s2.blocks, F32_THREADS, 0, stream>>>(
         static_cast<const float*>(a.hidden), nullptr, a.offsets, static_cast<const float*>(a.down.w),
         static_cast<const float*>(a.down.w), a.down.expert_elems, D, F, D, mr, a.row_weight, static_cast<float*>(a.y),
-        static_cast<float*>(a.save_y), nullptr);
+        static_cast<float*>(a.save_y), nullptr, s2);
     QW_LAUNCH_CHECK("ffn_f32_small_kernel<down>");
     *handled = true;
     return QW_OK;
   }
-  const dim3 g1(static_cast<unsigned>(ceil_div(F, F32_N / 2)), static_cast<unsigned>(a.experts), z);
-  ffn_f32_mfma_kernel<true><<<g1, F32_THREADS, 0, stream>>>(
+  const XcdGrid g1 = xcd_grid(ceil_div(F, F32_N / 2), a.experts, z);
+  if (g1.blocks == 0) return set_error(QW_ERR_UNSUPPORTED, "fp32 expert grid too large");
+  ffn_f32_mfma_kernel<true><<<g1.blocks, F32_THREADS, 0, stream>>>(
       static_cast<const float*>(a.x), a.row_index, a.offsets, static_cast<const float*>(a.gate.w),
       static_cast<const float*>(a.up.w), a.gate.expert_elems, F, D, F, mr, nullptr, static_cast<float*>(a.hidden),
-      static_cast<float*>(a.save_gate), static_cast<float*>(a.save_up));
+      static_cast<float*>(a.save_gate), static_cast<float*>(a.save_up), g1);
   QW_LAUNCH_CHECK("ffn_f32_mfma_kernel<gateup>");
-  const dim3 g2(static_cast<unsigned>(ceil_div(D, F32_N)), static_cast<unsigned>(a.experts), z);
-  ffn_f32_mfma_kernel<false><<<g2, F32_THREADS, 0, stream>>>(
+  const XcdGrid g2 = xcd_grid(ceil_div(D, F32_N), a.experts, z);
+  if (g2.blocks == 0) return set_error(QW_ERR_UNSUPPORTED, "fp32 expert grid too large");
+  ffn_f32_mfma_kernel<false><<<g2.blocks, F32_THREADS, 0, stream>>>(
       static_cast<const float*>(a.hidden), nullptr, a.offsets, static_cast<const float*>(a.down.w),
       static_cast<const float*>(a.down.w), a.down.expert_elems, D, F, D, mr, a.row_weight, static_cast<float*>(a.y),
-      static_cast<float*>(a.save_y), nullptr);
+      static_cast<float*>(a.save_y), nullptr, g2);
   QW_LAUNCH_CHECK("ffn_f32_mfma_kernel<down>");
   *handled = true;
   return QW_OK;
@@ -436,10 +442,12 @@ int grouped_matmul_f32(const float* x, const float* w, int64_t E, int64_t N, int
       (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out)) % 16)
     return QW_OK;
   const unsigned z = f32_row_splits(ceil_div(rows, E));
-  const dim3 g(static_cast<unsigned>(ceil_div(N, F32_N)), static_cast<unsigned>(E), z);
-  ffn_f32_mfma_kernel<false><<<g, F32_THREADS, 0, stream>>>(x, nullptr, offsets, w, w, N * K, static_cast<int>(N),
-                                                          static_cast<int>(K), static_cast<int>(N),
-                                                          static_cast<int>(rows), nullptr, out, nullptr, nullptr);
+  const XcdGrid g = xcd_grid(ceil_div(N, F32_N), E, z);
+  if (g.blocks == 0) return set_error(QW_ERR_UNSUPPORTED, "fp32 expert grid too large");
+  ffn_f32_mfma_kernel<false><<<g.blocks, F32_THREADS, 0, stream>>>(x, nullptr, offsets, w, w, N * K,
+                                                                 static_cast<int>(N), static_cast<int>(K),
+                                                                 static_cast<int>(N), static_cast<int>(rows), nullptr,
+                                                                 out, nullptr, nullptr, g);
   QW_LAUNCH_CHECK("ffn_f32_mfma_kernel<matmul>");
   *handled = true;
   return QW_OK;

@@ -106,7 +106,6 @@ constexpr int mf_stages(int subt) {
   const int stage = 32 * subt * MF_ROWB + MfB<WF>::STAGE;
   return MF_LDS / stage >= 3 ? 3 : 2;
 }
-constexpr int kXcds = 8;
 
 // s_waitcnt immediate waiting for vmcnt <= n only (expcnt, lgkmcnt left at max).
 template <int N>
@@ -473,15 +472,12 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
           uint32_t pk[2];
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            float a, c;
-            if (GATEUP) {
-              a = swiglu_act<ACT>(acc[i][t][2 * h], acc[i][t + MF_NT / 2][2 * h]);
-              c = swiglu_act<ACT>(acc[i][t][2 * h + 1], acc[i][t + MF_NT / 2][2 * h + 1]);
-            } else {
-              a = acc[i][t][2 * h];
-              c = acc[i][t][2 * h + 1];
-            }
-            pk[h] = f32_to_half<ACT>(a) | (static_cast<uint32_t>(f32_to_half<ACT>(c)) << 16);
+            if (GATEUP)
+              pk[h] = swiglu_pack2<ACT>(acc[i][t][2 * h], acc[i][t][2 * h + 1], acc[i][t + MF_NT / 2][2 * h],
+                                        acc[i][t + MF_NT / 2][2 * h + 1]);
+            else
+              pk[h] = f32_to_half<ACT>(acc[i][t][2 * h]) |
+                      (static_cast<uint32_t>(f32_to_half<ACT>(acc[i][t][2 * h + 1])) << 16);
           }
           *reinterpret_cast<uint2*>(ot + rl * (OC * 2) + chunk_of(row, col) * 16 + (col % 8) * 2) =
               make_uint2(pk[0], pk[1]);
@@ -525,13 +521,11 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
         if (col >= n_out) continue;
         uint32_t pk[2];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < 2; ++h)
           // the reference's 16-bit tensors: gate, up and silu(gate) are each
           // rounded to the activation type before the product (src/moe_kernels.py:194)
-          const float a = swiglu_act<ACT>(acc[i][t][2 * h], acc[i][t + MF_NT / 2][2 * h]);
-          const float c = swiglu_act<ACT>(acc[i][t][2 * h + 1], acc[i][t + MF_NT / 2][2 * h + 1]);
-          pk[h] = f32_to_half<ACT>(a) | (static_cast<uint32_t>(f32_to_half<ACT>(c)) << 16);
-        }
+          pk[h] = swiglu_pack2<ACT>(acc[i][t][2 * h], acc[i][t][2 * h + 1], acc[i][t + MF_NT / 2][2 * h],
+                                    acc[i][t + MF_NT / 2][2 * h + 1]);
         *reinterpret_cast<uint2*>(out + orow + col) = make_uint2(pk[0], pk[1]);
         if (save_a) {  // gate and up projections, for the backward pass
           uint32_t g2[2], u2[2];
