@@ -76,6 +76,17 @@ inline hipError_t reserve_lds(int bytes) {
 // Device helpers
 // ---------------------------------------------------------------------------
 constexpr int kWave = 64;
+
+// Cache-policy operand of global_load_lds for a stream read once: the
+// non-temporal bit (nt), so the lines it brings in are the first to leave the
+// caches and the data that is read again (activation rows, hidden rows) stays.
+// Used where every line of the stream is consumed by one load instruction
+// (16-bit weight tiles and rows, int8 decode chunks); on partial-line streams
+// (int4 and int8 rows in the prefill kernel, read a quarter or half line per K
+// slice) it evicts lines that the next slice still needs, and is not used.
+// (An enumerator, used through a constexpr local: the builtin's operand must be
+// a constant that is not an l-value when the host pass parses the kernel.)
+enum : int { kLoadStream = 2 };
 constexpr int kMaxDevices = 64;  // per-device tables of the library (scratch addresses, occupancy caches)
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }

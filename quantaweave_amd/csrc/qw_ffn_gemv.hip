@@ -396,6 +396,7 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
   constexpr int L = log2i<V>();
   constexpr int OUTS = UNITS * MAXM;      // outputs per group
   using LD = GvLds<WF, UNITS, ROWS, CPL, MAXM, SAVE>;
+  constexpr int W_AUX = LD::QUANT ? 0 : kLoadStream;  // cache policy of the weight chunk loads
   constexpr int SLOTS = GV_GPW_MAX * OUTS;  // staged values of one kind per wave
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   int r_lo = 0, r_hi = 0;
@@ -449,7 +450,7 @@ __global__ __launch_bounds__(GV_WAVES * 64) void ffn_gemv_kernel(
                                           ((8 * (n & 7) + ((cidx[j] & 7) ^ ((n >> 1) & 7))) << 4)
                                     : 16 * static_cast<int64_t>(cidx[j]);
           __builtin_amdgcn_global_load_lds(static_cast<const void*>(wrow + off), (lds_void*)(st + q * 1024), 16, 0,
-                                           0);
+                                           W_AUX);
           if constexpr (LD::QUANT)
             __builtin_amdgcn_global_load_lds(static_cast<const void*>(sbase[rr] + n * sstride + sidx[j]),
                                              (lds_void*)(st + LD::NCH * 1024 + q * 256), 4, 0, 0);
@@ -734,6 +735,7 @@ __global__ __launch_bounds__(64) void ffn_qmf_kernel(
   static_assert(V <= 16, "at most four row sets per group");
   static_assert(NST >= 2 && NST <= 4, "two to four ring stages");
   using LD = QmfLds<NCH, UPG, NST>;
+  constexpr int W_AUX = I8 ? kLoadStream : 0;  // cache policy of the weight chunk loads
   // SV: one scale per chunk and 4 or 8 slots, so a row set's scales are blocks of
   // 64 floats per row, loaded 16 bytes per lane (S / 4 loads per row set instead
   // of S); lane 16 t' + j fetches row t', floats 4 (j ^ 4 t') .. + 3 of a block
@@ -800,7 +802,7 @@ __global__ __launch_bounds__(64) void ffn_qmf_kernel(
       for (int s = 0; s < S; ++s) {
         const int q = r * S + s;
         __builtin_amdgcn_global_load_lds(static_cast<const void*>(wrow + 16 * chunk_of(s)),
-                                         (lds_void*)(st + q * 1024), 16, 0, 0);
+                                         (lds_void*)(st + q * 1024), 16, 0, W_AUX);
         if constexpr (!SV)
           __builtin_amdgcn_global_load_lds(static_cast<const void*>(srow + scale_of(s)),
                                            (lds_void*)(st + NCH * 1024 + q * 256), 4, 0, 0);
