@@ -735,7 +735,11 @@ __global__ __launch_bounds__(64) void ffn_qmf_kernel(
   static_assert(V <= 16, "at most four row sets per group");
   static_assert(NST >= 2 && NST <= 4, "two to four ring stages");
   using LD = QmfLds<NCH, UPG, NST>;
-  constexpr int W_AUX = I8 ? kLoadStream : 0;  // cache policy of the weight chunk loads
+  // cache policies of the weight chunk and scale loads: the non-temporal policy
+  // where it measured faster (int8 chunks: int8 decode layer -3.7%; int4
+  // scales: int4 decode layer -1.5%); each measured slower or no faster on the
+  // other format
+  constexpr int W_AUX = I8 ? kLoadStream : 0, S_AUX = I8 ? 0 : kLoadStream;
   // SV: one scale per chunk and 4 or 8 slots, so a row set's scales are blocks of
   // 64 floats per row, loaded 16 bytes per lane (S / 4 loads per row set instead
   // of S); lane 16 t' + j fetches row t', floats 4 (j ^ 4 t') .. + 3 of a block
@@ -805,13 +809,13 @@ __global__ __launch_bounds__(64) void ffn_qmf_kernel(
                                          (lds_void*)(st + q * 1024), 16, 0, W_AUX);
         if constexpr (!SV)
           __builtin_amdgcn_global_load_lds(static_cast<const void*>(srow + scale_of(s)),
-                                           (lds_void*)(st + NCH * 1024 + q * 256), 4, 0, 0);
+                                           (lds_void*)(st + NCH * 1024 + q * 256), 4, 0, S_AUX);
       }
       if constexpr (SV) {
 #pragma unroll
         for (int ib = 0; ib < S / 4; ++ib)
           __builtin_amdgcn_global_load_lds(static_cast<const void*>(srow + 64 * ib + 4 * ld_blk),
-                                           (lds_void*)(st + NCH * 1024 + (r * (S / 4) + ib) * 1024), 16, 0, 0);
+                                           (lds_void*)(st + NCH * 1024 + (r * (S / 4) + ib) * 1024), 16, 0, S_AUX);
       }
     }
   };
