@@ -129,10 +129,14 @@ def test_grouped_swiglu_matches_oracle(act, fmt, D, F_, group, path):
     assert normwise(got, ref) <= TOL[act]
 
 
-@pytest.mark.parametrize("E,D,F_,rows", [(16, 1024, 256, 100), (8, 256, 512, 128)])
+@pytest.mark.parametrize("E,D,F_,rows", [(16, 1024, 256, 100), (8, 256, 512, 128), (2, 2048, 256, 1000),
+                                         (3, 256, 512, 128), (2, 64, 96, 60), (5, 256, 128, 100)])
 def test_fp32_tile_sizes_match_oracle(E, D, F_, rows):
     """fp32 experts on the matrix cores: enough 64 x 64 down tiles to fill the GPU
-    (the 64 x 64 kernel) and a small layer (32 x 32 tiles, K split over the waves)."""
+    (the 64 x 64 kernel) and a small layer (32 x 32 tiles, K split over the waves).
+    The kernels walk (column tile, expert, row chunk) in XCD order: with fewer
+    than 8 experts an expert spans 8 // E XCDs (2 and 3 experts), and with 5
+    experts three XCDs get no work; every tile must still be visited once."""
     print(f"case f32 E={E} D={D} F={F_} rows~{rows}", flush=True)
     rng = np.random.RandomState(E + D)
     counts = [int(c) for c in rng.randint(rows - 40, rows + 40, size=E)]
