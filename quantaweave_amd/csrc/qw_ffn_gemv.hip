@@ -280,6 +280,52 @@ __device__ __forceinline__ void ring_read4(uint32_t w_addr, uint32_t s_addr, uin
   }
 }
 
+// Eight chunks and the R scales of a group whose rows have one scale each (R
+// row sets of 8 / R slots): the scale of row set r sits at s_addr + 256 r and
+// serves every slot of that row set.
+template <int R>
+__device__ __forceinline__ void ring_read8_rs(uint32_t w_addr, uint32_t s_addr, uint4 (&w)[8], float (&sv)[8]) {
+  static_assert(R == 1 || R == 2, "one or two row sets of 8 or 4 slots");
+  float s0, s1;
+  if constexpr (R == 1) {
+    asm volatile(
+        "ds_read_b128 %0, %9\n"
+        "ds_read_b128 %1, %9 offset:1024\n"
+        "ds_read_b128 %2, %9 offset:2048\n"
+        "ds_read_b128 %3, %9 offset:3072\n"
+        "ds_read_b128 %4, %9 offset:4096\n"
+        "ds_read_b128 %5, %9 offset:5120\n"
+        "ds_read_b128 %6, %9 offset:6144\n"
+        "ds_read_b128 %7, %9 offset:7168\n"
+        "ds_read_b32 %8, %10\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]), "=&v"(w[6]), "=&v"(w[7]),
+          "=&v"(s0)
+        : "v"(w_addr), "v"(s_addr)
+        : "memory");
+    s1 = s0;
+  } else {
+    asm volatile(
+        "ds_read_b128 %0, %10\n"
+        "ds_read_b128 %1, %10 offset:1024\n"
+        "ds_read_b128 %2, %10 offset:2048\n"
+        "ds_read_b128 %3, %10 offset:3072\n"
+        "ds_read_b128 %4, %10 offset:4096\n"
+        "ds_read_b128 %5, %10 offset:5120\n"
+        "ds_read_b128 %6, %10 offset:6144\n"
+        "ds_read_b128 %7, %10 offset:7168\n"
+        "ds_read_b32 %8, %11\n"
+        "ds_read_b32 %9, %11 offset:256\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]), "=&v"(w[6]), "=&v"(w[7]),
+          "=&v"(s0), "=&v"(s1)
+        : "v"(w_addr), "v"(s_addr)
+        : "memory");
+  }
+#pragma unroll
+  for (int q = 0; q < 8; ++q) sv[q] = q < 8 / R ? s0 : s1;
+}
+
 // Six chunks and their scales (the int4 matrix-core kernel's groups of 6).
 __device__ __forceinline__ void ring_read6(uint32_t w_addr, uint32_t s_addr, uint4 (&w)[8], float (&sv)[8]) {
   asm volatile(
@@ -717,7 +763,9 @@ __device__ __forceinline__ float quad_bcast(float v) {
 
 // FULL: rows of exactly 16 S chunks with one scale per chunk (group 32), so a
 // slot's chunk and scale offsets are a lane constant plus an immediate.
-template <int ACT, int WF, bool GATEUP, int S, int R, bool FULL, int NST>
+// RS: one scale per row (a group as long as the row, as int8 rows quantised
+// without a group size are), loaded once per row set instead of once per slot.
+template <int ACT, int WF, bool GATEUP, int S, int R, bool FULL, int NST, bool RS = false>
 __global__ __launch_bounds__(64) void ffn_qmf_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
     int n_experts, int max_rows, WView wa, WView wb, int K, int n_out, int gpw, const float* __restrict__ row_weight,
@@ -744,7 +792,8 @@ __global__ __launch_bounds__(64) void ffn_qmf_kernel(
   // 64 floats per row, loaded 16 bytes per lane (S / 4 loads per row set instead
   // of S); lane 16 t' + j fetches row t', floats 4 (j ^ 4 t') .. + 3 of a block
   constexpr bool SV = FULL && S % 4 == 0 && NCH == 8;
-  constexpr int NDMA = NCH + (SV ? NCH / 4 : NCH);  // DMA instructions per group
+  static_assert(!RS || (!FULL && NCH == 8 && R <= 2), "row scales: eight slots in one or two row sets");
+  constexpr int NDMA = NCH + (SV ? NCH / 4 : RS ? R : NCH);  // DMA instructions per group
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   int r_lo = 0, r_hi = 0;
   const int e = nth_active_expert(offsets, n_experts, max_rows, blockIdx.y, &r_lo, &r_hi);
@@ -807,10 +856,13 @@ __global__ __launch_bounds__(64) void ffn_qmf_kernel(
         const int q = r * S + s;
         __builtin_amdgcn_global_load_lds(static_cast<const void*>(wrow + 16 * chunk_of(s)),
                                          (lds_void*)(st + q * 1024), 16, 0, W_AUX);
-        if constexpr (!SV)
+        if constexpr (!SV && !RS)
           __builtin_amdgcn_global_load_lds(static_cast<const void*>(srow + scale_of(s)),
                                            (lds_void*)(st + NCH * 1024 + q * 256), 4, 0, S_AUX);
       }
+      if constexpr (RS)  // the loading lane's row scale, once for the row set
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(srow), (lds_void*)(st + NCH * 1024 + r * 256), 4,
+                                         0, S_AUX);
       if constexpr (SV) {
 #pragma unroll
         for (int ib = 0; ib < S / 4; ++ib)
@@ -946,6 +998,8 @@ __global__ __launch_bounds__(64) void ffn_qmf_kernel(
         const uint32_t sb = lds_addr(st + NCH * 1024) + 256 * t + 4 * blk;
         const uint32_t sa[4] = {sb + 64 * (0 ^ t), sb + 64 * (1 ^ t), sb + 64 * (2 ^ t), sb + 64 * (3 ^ t)};
         ring_read8_sv(wa_l, sa, wq, sq);
+      } else if constexpr (RS) {
+        ring_read8_rs<R>(wa_l, sa_l, wq, sq);
       } else if constexpr (NCH == 8) {
         ring_read8<true>(wa_l, sa_l, wq, sq);
       } else if constexpr (NCH == 6) {
@@ -1081,14 +1135,14 @@ int launch_one(const FfnArgs& a, const WView& wa, const WView& wb, const void* x
 // Two ring stages: 3 and 4 stages cost waves per CU and measured slower.
 constexpr int kQmfStages = 2;
 
-template <int ACT, int WF, bool GATEUP, int S, bool FULL, int NST = kQmfStages>
+template <int ACT, int WF, bool GATEUP, int S, bool FULL, bool RS = false, int NST = kQmfStages>
 int launch_qmf_s(const FfnArgs& a, const WView& wa, const WView& wb, const void* x, const int32_t* row_index, int K,
                   int n_out, const float* row_weight, void* out, hipStream_t stream) {
   constexpr int R = S <= 2 ? 4 : S <= 4 ? 2 : 1;
   constexpr int UPG = GATEUP ? 2 * R : 4 * R;
   using LD = QmfLds<S * R, UPG, NST>;
-  auto kernel = ffn_qmf_kernel<ACT, WF, GATEUP, S, R, FULL, NST>;
-  const hipError_t attr = reserve_lds<ffn_qmf_kernel<ACT, WF, GATEUP, S, R, FULL, NST>>(LD::BYTES);
+  auto kernel = ffn_qmf_kernel<ACT, WF, GATEUP, S, R, FULL, NST, RS>;
+  const hipError_t attr = reserve_lds<ffn_qmf_kernel<ACT, WF, GATEUP, S, R, FULL, NST, RS>>(LD::BYTES);
   if (attr != hipSuccess)
     return set_error(QW_ERR_HIP, "cannot reserve %d bytes of LDS: %s", LD::BYTES, hipGetErrorString(attr));
   const int64_t n_groups = ceil_div(n_out, UPG);
@@ -1143,6 +1197,12 @@ int launch_qmf_full(const FfnArgs& a, const WView& wa, const WView& wb, const vo
   constexpr int CW = WF == QW_I8 ? 16 : 32;
   if (K / CW == 16 * S && wa.group == CW)
     return launch_qmf_s<ACT, WF, GATEUP, S, true>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
+  constexpr int R = S <= 2 ? 4 : S <= 4 ? 2 : 1;
+  if constexpr (S * R == 8 && R <= 2) {
+    if (wa.groups == 1 && wb.groups == 1)  // one scale per row
+      return launch_qmf_s<ACT, WF, GATEUP, S, false, true>(a, wa, wb, x, row_index, K, n_out, row_weight, out,
+                                                           stream);
+  }
   return launch_qmf_s<ACT, WF, GATEUP, S, false>(a, wa, wb, x, row_index, K, n_out, row_weight, out, stream);
 }
 
