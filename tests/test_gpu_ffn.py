@@ -182,6 +182,7 @@ def test_each_kernel_family_matches_oracle(act, fmt, group, path):
     ("bf16", "u4", 128, 4096, 1024),  # 8 slots, four chunks per scale
     ("f16", "u4", 32, 4096, 1408),    # the int4 decode layer's rows with fp16 activations
     ("bf16", "u4", 32, 6144, 512),    # gate/up rows of 192 chunks take the dot-product kernel
+    ("bf16", "u4", 2048, 2048, 2048),  # one scale per row: 4 slots in two row sets, loaded once per row set
     ("bf16", "i8", None, 2048, 1024),  # the int8 decode layer: one scale per row, 8 and 4 slots
     ("bf16", "i8", 16, 256, 512),     # one scale per chunk, whole rows (1 and 2 slots)
     ("bf16", "i8", 16, 2048, 1024),   # one scale per chunk, whole rows of 8 and 4 slots: scale blocks
