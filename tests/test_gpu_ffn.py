@@ -10,7 +10,7 @@ import torch
 
 import oracle
 import quantaweave_amd as qa
-from quantaweave_amd import _lib
+from quantaweave_amd import _hip, _lib
 from quantaweave_amd import moe_kernels as mk
 from tests import hipcall as H
 
@@ -480,3 +480,39 @@ def test_int8_decode_route_of_tiny_activations(D):
     ref = oracle.experts_forward(x, np.array(counts), w, "bf16")
     assert np.abs(got[[1, 3]]).max() <= 1e-30
     assert normwise(got, ref) <= DECODE_DEV["bf16"]
+
+
+def test_prefill_hidden_rows_follow_the_reference_rounding():
+    """The 16-bit prefill kernel forms silu with the hardware reciprocal
+    (silu_fast).  Given the kernel's own gate and up projections (saved,
+    already rounded to bf16), its hidden rows must equal the reference's
+    rounding chain bf16(bf16(silu(g)) * u), silu computed in float64 and
+    rounded to fp32 first as torch's fp32 opmath does: a value may differ only
+    where silu(g) lies within a few fp32 ulp of a bf16 rounding boundary, so
+    by at most one bf16 ulp and rarely (src/moe_kernels.py:194)."""
+    print("case prefill hidden rows: silu rounding", flush=True)
+    counts = [40, 64, 17, 100]
+    E, D, F_ = len(counts), 256, 384
+    rng = np.random.RandomState(7)
+    rows = sum(counts)
+    x = H.dev(rng.randn(rows, D).astype(np.float32), torch.bfloat16)
+    w = [H.dev((rng.randn(E, a, b) * 0.06).astype(np.float32), torch.bfloat16) for a, b in ((F_, D), (F_, D), (D, F_))]
+    offsets = H.dev(np.concatenate([[0], np.cumsum(counts)]).astype(np.int32))
+    outs = [torch.empty(rows, n, dtype=torch.bfloat16, device="cuda") for n in (D, F_, F_, F_, D)]
+    y, g_out, u_out, h_out, y_unw = outs
+    nb = _lib.load().qw_moe_experts_workspace_bytes(rows, E, D, F_, _lib.QW_BF16)
+    ws = _hip.workspace(nb, torch.device("cuda"))
+    P = _hip.ptr
+    _lib.call("qw_moe_experts_save", P(x), _lib.QW_BF16, None, P(offsets), E, D, F_, rows, max(counts), _lib.QW_BF16,
+              0, 0, P(w[0]), None, P(w[1]), None, P(w[2]), None, None, P(y), P(g_out), P(u_out), P(h_out), P(y_unw),
+              P(ws), nb, H.s())
+    torch.cuda.synchronize()
+    g = g_out.double().cpu()
+    u = u_out.double().cpu()
+    silu = (g / (1.0 + torch.exp(-g))).float().bfloat16().double()
+    want = (silu * u).float().bfloat16()
+    got = h_out.cpu()
+    ulps = (got.view(torch.int16).int() - want.view(torch.int16).int()).abs().numpy()
+    equal = float(np.mean(ulps == 0))
+    print(f"  {ulps.size} hidden values: {equal:.6f} equal, max {int(ulps.max())} ulp", flush=True)
+    assert int(ulps.max()) <= 1 and equal >= 0.999
