@@ -84,6 +84,29 @@ def event_samples(fn, iters, stream, flush=None):
     return dict(median=float(np.median(t)), p10=float(np.percentile(t, 10)), p90=float(np.percentile(t, 90)))
 
 
+def stage_times(calls, iters, stream):
+    """Average ms of each stage as it runs inside the layer: the stages called
+    in layer order, iters times, each bracketed by its own HIP event pair on
+    `stream` (the caches then hold what a layer call leaves in them, which
+    repeated calls of one stage alone do not reproduce)."""
+    import torch
+
+    names = list(calls)
+    pairs = []
+    for _ in range(iters):
+        row = []
+        for n in names:
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            calls[n]()
+            b.record(stream)
+            row.append((a, b))
+        pairs.append(row)
+    torch.cuda.synchronize()
+    return {n: sum(r[j][0].elapsed_time(r[j][1]) for r in pairs) / iters for j, n in enumerate(names)}
+
+
 def stage_calls(run):
     """The forward split into its entry points, with the same buffers as qw_moe_forward."""
     import torch
@@ -155,13 +178,11 @@ def measure(name, steps, warmup):
     kept = int(run.totals[0].item())
     dropped = int(run.totals[1].item())
     touched = int((counts > 0).sum())
-    stages = {}
     calls = stage_calls(run)
     for k_, fn in calls.items():
         fn()
     torch.cuda.synchronize()
-    for k_, fn in calls.items():
-        stages[k_] = event_time(fn, max(5, steps // 2), stream)
+    stages = stage_times(calls, max(5, steps // 2), stream)
     # the expert stage again with the 256 MB last-level cache (MALL) flushed before every call: reading
     # 512 MiB between calls evicts the weights (and leaves no dirty lines), so each call streams them from HBM
     scratch = torch.ones(64 << 20, dtype=torch.int64, device=layer.x.device)
