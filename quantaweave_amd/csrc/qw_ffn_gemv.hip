@@ -723,6 +723,42 @@ struct QmfLds {
   static constexpr int BYTES = STAGES * STAGE + OUT;
 };
 
+// The j-th (expert, pass) of the row ranges in ascending expert order, where a
+// pass is up to 4 consecutive rows of one expert (an expert with r rows has
+// ceil(r / 4) passes); -1 past the last one.  [*lo, *hi) are the pass's rows.
+// A block per pass spreads an expert with many routes over as many blocks as
+// it has passes.  Wave-uniform result.
+__device__ __forceinline__ int nth_active_pass(const int32_t* __restrict__ offsets, int E, int max_rows, int j,
+                                               int* lo, int* hi) {
+  const int lane = threadIdx.x % kWave;
+  for (int c = 0; c < E; c += kWave) {
+    const int e = c + lane;
+    int a = 0, b = 0;
+    if (e < E) {
+      a = min(max(offsets[e], 0), max_rows);
+      b = min(offsets[e + 1], max_rows);
+    }
+    const int np = b > a ? (b - a + 3) / 4 : 0;
+    int incl = np;  // inclusive prefix sum of the passes over the lanes
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int v = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += v;
+    }
+    const int total = __shfl(incl, kWave - 1, kWave);
+    if (j < total) {
+      const int src = __builtin_ctzll(__ballot(j < incl && j >= incl - np));
+      const int p = j - __shfl(incl - np, src, kWave);  // pass of expert c + src
+      const int a0 = __shfl(a, src, kWave), b0 = __shfl(b, src, kWave);
+      *lo = __builtin_amdgcn_readfirstlane(a0 + 4 * p);
+      *hi = __builtin_amdgcn_readfirstlane(min(a0 + 4 * p + 4, b0));
+      return c + src;
+    }
+    j -= total;
+  }
+  return -1;
+}
+
 // Value of lane (lane ^ O) for O in 4, 8, 16 (ds_swizzle, bit mode) or 32
 // (ds_bpermute with the byte address of lane ^ 32 in addr32).
 template <int O>
@@ -765,6 +801,10 @@ __device__ __forceinline__ float quad_bcast(float v) {
 // slot's chunk and scale offsets are a lane constant plus an immediate.
 // RS: one scale per row (a group as long as the row, as int8 rows quantised
 // without a group size are), loaded once per row set instead of once per slot.
+// Block (x, y) streams groups [x gpw, (x + 1) gpw) of the y-th pass (up to 4
+// rows of one expert, nth_active_pass), so an expert with more routes has more
+// blocks rather than longer ones (int8 decode layer: 102.4 -> 96.1 us against
+// a block per expert that walks its passes in turn).
 template <int ACT, int WF, bool GATEUP, int S, int R, bool FULL, int NST, bool RS = false>
 __global__ __launch_bounds__(64) void ffn_qmf_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
@@ -786,7 +826,8 @@ __global__ __launch_bounds__(64) void ffn_qmf_kernel(
   // cache policies of the weight chunk and scale loads: the non-temporal policy
   // where it measured faster (int8 chunks: int8 decode layer -3.7%; int4
   // scales: int4 decode layer -1.5%); each measured slower or no faster on the
-  // other format
+  // other format (int4 chunks: -0.5% to -2.8% with the last-level cache
+  // flushed before each layer, +1.2% to +2.5% without)
   constexpr int W_AUX = I8 ? kLoadStream : 0, S_AUX = I8 ? 0 : kLoadStream;
   // SV: one scale per chunk and 4 or 8 slots, so a row set's scales are blocks of
   // 64 floats per row, loaded 16 bytes per lane (S / 4 loads per row set instead
@@ -796,7 +837,7 @@ __global__ __launch_bounds__(64) void ffn_qmf_kernel(
   constexpr int NDMA = NCH + (SV ? NCH / 4 : RS ? R : NCH);  // DMA instructions per group
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   int r_lo = 0, r_hi = 0;
-  const int e = nth_active_expert(offsets, n_experts, max_rows, blockIdx.y, &r_lo, &r_hi);
+  const int e = nth_active_pass(offsets, n_experts, max_rows, blockIdx.y, &r_lo, &r_hi);  // at most 4 rows
   if (e < 0) return;
   const int lane = threadIdx.x;
   const int blk = lane >> 2, t = lane & 3;
@@ -1129,6 +1170,21 @@ int launch_one(const FfnArgs& a, const WView& wa, const WView& wb, const void* x
                                                     nullptr, stream);
 }
 
+// Passes that uniform routing of m rows over E experts makes on average:
+// E * sum_r P(r) ceil(r / 4), r ~ Binomial(m, 1 / E); at least 1.
+static double expected_passes(int64_t E, int64_t m) {
+  if (E <= 1) return std::max<double>(1.0, static_cast<double>((m + 3) / 4));
+  const double p = 1.0 / static_cast<double>(E);
+  double pr = std::pow(1.0 - p, static_cast<double>(m));  // P(r = 0)
+  double sum = 0.0;
+  for (int64_t r = 1; r <= m; ++r) {
+    pr *= static_cast<double>(m - r + 1) / static_cast<double>(r) * p / (1.0 - p);
+    sum += pr * static_cast<double>((r + 3) / 4);
+    if (static_cast<double>(r) > 4.0 * static_cast<double>(m) * p + 64.0 && pr < 1e-15) break;
+  }
+  return std::max(1.0, static_cast<double>(E) * sum);
+}
+
 // The int4 matrix-core kernel for one projection: S chunk slots per lane cover
 // rows of up to 16 S chunks; R row sets per group keep 4 to 8 chunk loads per
 // lane and group.
@@ -1147,15 +1203,18 @@ int launch_qmf_s(const FfnArgs& a, const WView& wa, const WView& wb, const void*
     return set_error(QW_ERR_HIP, "cannot reserve %d bytes of LDS: %s", LD::BYTES, hipGetErrorString(attr));
   const int64_t n_groups = ceil_div(n_out, UPG);
   const int64_t touched = a.max_rows < a.experts ? a.max_rows : a.experts;
+  // Blocks per pass (up to 4 rows of one expert): at most (max_rows + 3
+  // touched) / 4 passes, as an expert with r rows has ceil(r / 4) <= (r + 3) / 4.
+  const int64_t passes = (a.max_rows + 3 * touched) / 4;
   // Groups per wave: about one round of waves over the device's slots for this
-  // kernel (waves per CU as its LDS and registers allow), for the number of
-  // experts that uniform routing of max_rows rows touches on average; a grid of
-  // 1.3 to 1.6 rounds left the last round partly empty (int4 decode layer:
-  // expert stage 53.9 us against 56.2 us with 6 groups per wave; int8 decode
-  // layer, down projection: 84.4 us against 88.1 us).  int8 gate/up keeps 6 (its
-  // decode layer has experts with two passes of 4 routes, and one round measured
-  // slower there).  Small layers keep the fewer, shorter waves of
-  // groups_per_wave.
+  // kernel (waves per CU as its LDS and registers allow), for the passes that
+  // uniform routing of max_rows rows makes on average; a grid of 1.3 to 1.6
+  // rounds left the last round partly empty (int4 decode layer: expert stage
+  // 53.9 us against 56.2 us with 6 groups per wave; int8 decode layer, down
+  // projection: 84.4 us against 88.1 us).  int8 gate/up keeps 6 (several
+  // rounds of shorter waves measured faster on its decode layer: 96.1 us
+  // against 101.2 us with one round).  Small layers keep the fewer, shorter
+  // waves of groups_per_wave.
   int gpw = groups_per_wave(touched, n_groups, GATEUP);
   if (touched * n_groups >= 8192 && WF == QW_I8 && GATEUP) {
     gpw = 6;
@@ -1177,13 +1236,14 @@ int launch_qmf_s(const FfnArgs& a, const WView& wa, const WView& wb, const void*
       slots = cus * per_cu;
       slot_cache[dev].store(slots, std::memory_order_relaxed);
     }
-    const double E = static_cast<double>(a.experts);
-    const double active = E * (1.0 - std::pow(1.0 - 1.0 / E, static_cast<double>(a.max_rows)));
+    const double active = expected_passes(a.experts, a.max_rows);
     const int64_t want = static_cast<int64_t>(std::ceil(active * static_cast<double>(n_groups) / slots));
     gpw = static_cast<int>(want < 2 ? 2 : want > LD::GPW_MAX ? LD::GPW_MAX : want);
   }
   static_assert(LD::GPW_MAX >= 6, "staging holds the groups of one wave");
-  const dim3 grid(static_cast<unsigned>(ceil_div(n_groups, gpw)), static_cast<unsigned>(touched));
+  if (passes > 65535)
+    return set_error(QW_ERR_UNSUPPORTED, "too many rows for the decode kernel (%lld passes)", static_cast<long long>(passes));
+  const dim3 grid(static_cast<unsigned>(ceil_div(n_groups, gpw)), static_cast<unsigned>(passes));
   kernel<<<grid, 64, LD::BYTES, stream>>>(static_cast<const uint16_t*>(x), row_index, a.offsets,
                                           static_cast<int>(a.experts), static_cast<int>(a.max_rows), wa, wb, K, n_out,
                                           gpw, row_weight, static_cast<uint16_t*>(out));
