@@ -207,7 +207,22 @@ def test_quantized_decode_rows_match_oracle(act, fmt, group, D, F_):
     (only ~37% of outputs are then the same value), and the deviation measured
     over these cases, with a margin, bounds the comparison (DECODE_DEV)."""
     print(f"case quantised decode act={act} fmt={fmt} group={group} D={D} F={F_}", flush=True)
-    counts = [1, 0, 3, 9, 2]
+    _check_quantized_decode(act, fmt, group, D, F_, [1, 0, 3, 9, 2])
+
+
+@pytest.mark.parametrize("act,fmt,group,D,F_", [
+    ("bf16", "u4", 32, 4096, 1408),   # the int4 decode layer's shapes
+    ("bf16", "i8", None, 2048, 1024),  # the int8 decode layer's shapes
+])
+def test_quantized_decode_many_passes(act, fmt, group, D, F_):
+    """Experts with 5 to 17 routes at decode sizes: each pass of up to 4 routes
+    is its own column of blocks (14 passes over 6 experts here, an empty expert
+    among them), checked as test_quantized_decode_rows_match_oracle."""
+    print(f"case quantised decode passes act={act} fmt={fmt} D={D} F={F_}", flush=True)
+    _check_quantized_decode(act, fmt, group, D, F_, [17, 0, 5, 13, 1, 8])
+
+
+def _check_quantized_decode(act, fmt, group, D, F_, counts):
     rng = np.random.RandomState(D + F_ + (group or 0))
     rows = sum(counts)
     x = oracle.round_act(rng.randn(rows, D).astype(np.float32), act)
