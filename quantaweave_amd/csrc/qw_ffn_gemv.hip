@@ -1330,6 +1330,10 @@ int launch_ffn_gemv(const FfnArgs& a, hipStream_t stream, bool* handled) {
   if (!is_half(a.act) || a.avg_rows >= 16) return QW_OK;
   const bool f16 = a.act == QW_F16;
   if ((a.save_gate || a.save_y) && quantized(a.wfmt)) return QW_OK;  // quantised experts do not train
+  // the matrix-core decode kernel's grid has a row per pass of up to 4 routes:
+  // more than a grid dimension holds go to the other kernel families
+  const int64_t touched = a.max_rows < a.experts ? a.max_rows : a.experts;
+  if (quantized(a.wfmt) && (a.max_rows + 3 * touched) / 4 > 65535) return QW_OK;
   int cw = 0;
   if (a.wfmt == QW_U4) {
     if (a.gate.group % 32 || a.down.group % 32) return QW_OK;
