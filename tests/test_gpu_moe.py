@@ -503,6 +503,47 @@ def test_balance_with_workspace_matches_float64_and_is_deterministic(T, E, K):
     for imp, bal in (outs[0], (imp0.cpu(), bal0.cpu())):
         assert (imp.double() - imp64).abs().max() <= 1e-6 * max(imp64.abs().max().item(), 1e-30)
         assert abs(float(bal) - bal64) <= 1e-5 * max(abs(bal64), 1e-30)
+    # the workspace form's fixed fp32 order, restated: bit for bit
+    imp_ref, bal_ref = _balance_fixed_order(probs.numpy(), counts.numpy(), T, K, E)
+    assert np.array_equal(outs[0][0].numpy(), imp_ref)
+    assert outs[0][1].numpy().astype(np.float32) == bal_ref
+
+
+def _balance_fixed_order(probs, counts, T, K, E):
+    """qw_moe_balance_ws's additions in order, in float32: per 64-token chunk
+    four strided sums (tokens j, j + 4, ... of the chunk) added as ((s0 + s1) + s2)
+    + s3; 16 running sums over the chunk rows w, w + 16, ... (8 rows per step);
+    those added in order; / T; terms imp * (count / (T K)) added in ascending
+    expert order, times E."""
+    f32 = np.float32
+    nb = (T + 63) // 64
+    partial = np.zeros((nb, E), f32)
+    for b in range(nb):
+        q = []
+        for j in range(4):
+            acc = np.zeros(E, f32)
+            for i in range(16):
+                t = 64 * b + j + 4 * i
+                if t < min(T, 64 * b + 64):
+                    acc = (acc + probs[t]).astype(f32)
+            q.append(acc)
+        partial[b] = (((q[0] + q[1]).astype(f32) + q[2]).astype(f32) + q[3]).astype(f32)
+    tot = np.zeros(E, f32)
+    for w in range(16):
+        acc = np.zeros(E, f32)
+        b0 = w
+        while b0 < nb:
+            for i in range(8):
+                if b0 + 16 * i < nb:
+                    acc = (acc + partial[b0 + 16 * i]).astype(f32)
+            b0 += 128
+        tot = (tot + acc).astype(f32)
+    imp = (tot / f32(T)).astype(f32)
+    term = (imp * (counts.astype(f32) / f32(T * K))).astype(f32)
+    acc = f32(0)
+    for e in range(E):
+        acc = f32(acc + term[e])
+    return imp, f32(f32(E) * acc)
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
