@@ -132,6 +132,21 @@ __device__ __forceinline__ uint16_t f32_to_half(float f) {
   else return f32_to_bf16(f);
 }
 
+// Two values rounded to DT and packed, a in the low half: the bits of
+// f32_to_half(a) | f32_to_half(b) << 16.  For bf16 the pair is one
+// v_cvt_pk_bf16_f32; the scalar form compiles to one conversion per value
+// and a shift and an OR to merge them.
+template <int DT>
+__device__ __forceinline__ uint32_t pack_half2(float a, float b) {
+  if constexpr (DT == QW_F16) {
+    return f32_to_f16(a) | (static_cast<uint32_t>(f32_to_f16(b)) << 16);
+  } else {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+}
+
 template <int DT>
 __device__ __forceinline__ float load_act(const void* p, int64_t i) {
   if constexpr (DT == QW_F32) return static_cast<const float*>(p)[i];
@@ -202,7 +217,7 @@ __device__ __forceinline__ void store_vec(void* p, int64_t i, const float (&v)[V
     uint32_t w[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u)
-      w[u] = f32_to_bf16(v[2 * u]) | (static_cast<uint32_t>(f32_to_bf16(v[2 * u + 1])) << 16);
+      w[u] = pack_half2<QW_BF16>(v[2 * u], v[2 * u + 1]);
     *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p) + i) = make_uint4(w[0], w[1], w[2], w[3]);
   } else if constexpr (VEC % 4 == 0 && DT == QW_F32) {
 #pragma unroll
@@ -216,8 +231,8 @@ __device__ __forceinline__ void store_vec(void* p, int64_t i, const float (&v)[V
       *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p) + i + u) = make_uint2(lo, hi);
     }
   } else if constexpr (VEC == 4 && DT == QW_BF16) {
-    const uint32_t lo = f32_to_bf16(v[0]) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
-    const uint32_t hi = f32_to_bf16(v[2]) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+    const uint32_t lo = pack_half2<QW_BF16>(v[0], v[1]);
+    const uint32_t hi = pack_half2<QW_BF16>(v[2], v[3]);
     *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p) + i) = make_uint2(lo, hi);
   } else {
 #pragma unroll
@@ -426,8 +441,10 @@ __device__ __forceinline__ uint32_t swiglu_pack2(float g0, float g1, float u0, f
   if constexpr (DT == QW_BF16) {
     typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
     auto round2 = [](float& a, float& b) {
-      const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
-      const uint32_t w = __builtin_bit_cast(uint32_t, v);
+      uint32_t w = pack_half2<QW_BF16>(a, b);
+      // opaque to the optimiser: seeing that each half is used alone, it
+      // would split the pair conversion into one per value
+      asm("" : "+v"(w));
       a = __uint_as_float(w << 16);
       b = __uint_as_float(w & 0xffff0000u);
     };

@@ -480,21 +480,38 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
               pk[h] = swiglu_pack2<ACT>(acc[i][t][2 * h], acc[i][t][2 * h + 1], acc[i][t + MF_NT / 2][2 * h],
                                         acc[i][t + MF_NT / 2][2 * h + 1]);
             else
-              pk[h] = f32_to_half<ACT>(acc[i][t][2 * h]) |
-                      (static_cast<uint32_t>(f32_to_half<ACT>(acc[i][t][2 * h + 1])) << 16);
+              pk[h] = pack_half2<ACT>(acc[i][t][2 * h], acc[i][t][2 * h + 1]);
           }
           *reinterpret_cast<uint2*>(ot + rl * (OC * 2) + chunk_of(row, col) * 16 + (col % 8) * 2) =
               make_uint2(pk[0], pk[1]);
         }
       }
       __syncthreads();
+      // SUBT rounds of 16-byte pieces per thread: every LDS read is issued
+      // before the first global store, so the reads' latency is paid once.
+      // Pieces of rows past the expert's end are read (inside the staged
+      // tile) and not stored.
+      constexpr int ROUNDS = PR * CPR / MF_THREADS;
+      static_assert(PR * CPR % MF_THREADS == 0, "whole rounds of pieces");
       const int rows = min(count - pass * PR, PR);
-      for (int c = tid; c < rows * CPR; c += MF_THREADS) {
-        const int rl = c / CPR, q = c % CPR, row = pass * PR + rl;
+      uint4 piece[ROUNDS];
+#pragma unroll
+      for (int u = 0; u < ROUNDS; ++u) {
+        const int c = tid + u * MF_THREADS;
+        const int rl = c / CPR, q = c % CPR;
+        piece[u] = *reinterpret_cast<const uint4*>(ot + rl * (OC * 2) + chunk_of(pass * PR + rl, q * 8) * 16);
+      }
+      // the pieces as opaque values: otherwise each read sinks into its
+      // store's branch and waits there on its own
+#pragma unroll
+      for (int u = 0; u < ROUNDS; ++u) asm("" : "+v"(piece[u].x), "+v"(piece[u].y), "+v"(piece[u].z), "+v"(piece[u].w));
+#pragma unroll
+      for (int u = 0; u < ROUNDS; ++u) {
+        const int c = tid + u * MF_THREADS;
+        const int rl = c / CPR, q = c % CPR;
         const int col = n0 + q * 8;
-        if (col < n_out)
-          *reinterpret_cast<uint4*>(out + static_cast<int64_t>(r0 + row) * n_out + col) =
-              *reinterpret_cast<const uint4*>(ot + rl * (OC * 2) + chunk_of(row, q * 8) * 16);
+        if (rl < rows && col < n_out)
+          *reinterpret_cast<uint4*>(out + static_cast<int64_t>(r0 + pass * PR + rl) * n_out + col) = piece[u];
       }
     }
     return;
@@ -535,10 +552,8 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
           uint32_t g2[2], u2[2];
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            g2[h] = f32_to_half<ACT>(acc[i][t][2 * h]) |
-                    (static_cast<uint32_t>(f32_to_half<ACT>(acc[i][t][2 * h + 1])) << 16);
-            u2[h] = f32_to_half<ACT>(acc[i][t + MF_NT / 2][2 * h]) |
-                    (static_cast<uint32_t>(f32_to_half<ACT>(acc[i][t + MF_NT / 2][2 * h + 1])) << 16);
+            g2[h] = pack_half2<ACT>(acc[i][t][2 * h], acc[i][t][2 * h + 1]);
+            u2[h] = pack_half2<ACT>(acc[i][t + MF_NT / 2][2 * h], acc[i][t + MF_NT / 2][2 * h + 1]);
           }
           *reinterpret_cast<uint2*>(save_a + orow + col) = make_uint2(g2[0], g2[1]);
           *reinterpret_cast<uint2*>(save_b + orow + col) = make_uint2(u2[0], u2[1]);
@@ -556,15 +571,14 @@ __global__ __launch_bounds__(MF_THREADS) void ffn_mfma_kernel(
           // without weights act(act(v) * 1) is act(v): one rounding
           const float a = row_weight ? round_act<ACT>(acc[i][t][2 * h]) * wgt : acc[i][t][2 * h];
           const float c = row_weight ? round_act<ACT>(acc[i][t][2 * h + 1]) * wgt : acc[i][t][2 * h + 1];
-          pk[h] = f32_to_half<ACT>(a) | (static_cast<uint32_t>(f32_to_half<ACT>(c)) << 16);
+          pk[h] = pack_half2<ACT>(a, c);
         }
         *reinterpret_cast<uint2*>(out + orow + col) = make_uint2(pk[0], pk[1]);
         if (save_a) {  // the rows before their weight, for the backward pass
           uint32_t un[2];
 #pragma unroll
           for (int h = 0; h < 2; ++h)
-            un[h] = f32_to_half<ACT>(acc[i][t][2 * h]) |
-                    (static_cast<uint32_t>(f32_to_half<ACT>(acc[i][t][2 * h + 1])) << 16);
+            un[h] = pack_half2<ACT>(acc[i][t][2 * h], acc[i][t][2 * h + 1]);
           *reinterpret_cast<uint2*>(save_a + orow + col) = make_uint2(un[0], un[1]);
         }
       }

@@ -285,7 +285,7 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(const uint16_t* __restrict
             }
 #pragma unroll
             for (int u = 0; u < OV / 2; ++u)
-              w[u] = f32_to_half<DT>(v[2 * u]) | (static_cast<uint32_t>(f32_to_half<DT>(v[2 * u + 1])) << 16);
+              w[u] = pack_half2<DT>(v[2 * u], v[2 * u + 1]);
             *reinterpret_cast<uint4*>(co) = make_uint4(w[0], w[1], w[2], w[3]);
           } else {
             for (int u = 0; u < OV && n + u < ncount; ++u)
@@ -336,8 +336,8 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(const uint16_t* __restrict
           v[2] += half_to_f32<DT>(old.y & 0xffffu);
           v[3] += half_to_f32<DT>(old.y >> 16);
         }
-        const uint32_t lo = f32_to_half<DT>(v[0]) | (static_cast<uint32_t>(f32_to_half<DT>(v[1])) << 16);
-        const uint32_t hi = f32_to_half<DT>(v[2]) | (static_cast<uint32_t>(f32_to_half<DT>(v[3])) << 16);
+        const uint32_t lo = pack_half2<DT>(v[0], v[1]);
+        const uint32_t hi = pack_half2<DT>(v[2], v[3]);
         *reinterpret_cast<uint2*>(crow + n) = make_uint2(lo, hi);
       } else {
 #pragma unroll

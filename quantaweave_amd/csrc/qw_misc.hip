@@ -302,8 +302,8 @@ __global__ __launch_bounds__(256) void cast_half_kernel(const float* __restrict_
   if ((n & 3) == 0) {
     const float4 v = *reinterpret_cast<const float4*>(x + i);
     uint2 o;
-    o.x = f32_to_half<DT>(v.x) | (static_cast<uint32_t>(f32_to_half<DT>(v.y)) << 16);
-    o.y = f32_to_half<DT>(v.z) | (static_cast<uint32_t>(f32_to_half<DT>(v.w)) << 16);
+    o.x = pack_half2<DT>(v.x, v.y);
+    o.y = pack_half2<DT>(v.z, v.w);
     *reinterpret_cast<uint2*>(out + i) = o;
   } else {
     for (int64_t j = i; j < i + 4 && j < n; ++j) out[j] = f32_to_half<DT>(x[j]);

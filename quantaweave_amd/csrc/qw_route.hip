@@ -757,8 +757,8 @@ __global__ __launch_bounds__(THREADS) void route_plan_small_kernel(
           o.x = f32_to_f16(v.x) | (static_cast<uint32_t>(f32_to_f16(v.y)) << 16);
           o.y = f32_to_f16(v.z) | (static_cast<uint32_t>(f32_to_f16(v.w)) << 16);
         } else {
-          o.x = f32_to_bf16(v.x) | (static_cast<uint32_t>(f32_to_bf16(v.y)) << 16);
-          o.y = f32_to_bf16(v.z) | (static_cast<uint32_t>(f32_to_bf16(v.w)) << 16);
+          o.x = pack_half2<QW_BF16>(v.x, v.y);
+          o.y = pack_half2<QW_BF16>(v.z, v.w);
         }
         *reinterpret_cast<uint2*>(cast_out + i) = o;
       } else {
