@@ -106,19 +106,46 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
     wsl[p] = w;
   }
   const int64_t row = static_cast<int64_t>(t) * D;
+  // the rows of up to G routes are requested together, then added in order
+  // (a route past the kept ones reads the first kept route's row and adds
+  // nothing; the empty volatile asm keeps each load ahead of the additions
+  // instead of sunk into its route's branch)
+  constexpr int G = KMAX < 4 ? KMAX : 4;
+  static_assert(KMAX % G == 0, "whole groups of routes");
   for (int c = threadIdx.x * VEC; c < D; c += blockDim.x * VEC) {
     float acc[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
+    auto add = [&](const float (&yr)[VEC], float w) {
 #pragma unroll
-    for (int j = 0; j < KMAX; ++j) {
-      if (j < nk) {
-        float yv[VEC];
-        load_vec<ACT, VEC>(y, static_cast<int64_t>(slot[j]) * D + c, yv);
+      for (int v = 0; v < VEC; ++v) {
+        const float term = WEIGHTED ? round_act<OUT>(yr[v] * w) : yr[v];
+        acc[v] = STATIC ? round_act<OUT>(acc[v] + term) : acc[v] + term;
+      }
+    };
+    if constexpr (KMAX <= 16) {
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) {
-          const float term = WEIGHTED ? round_act<OUT>(yv[v] * wsl[j]) : yv[v];
-          acc[v] = STATIC ? round_act<OUT>(acc[v] + term) : acc[v] + term;
+      for (int j0 = 0; j0 < KMAX; j0 += G) {
+        if (j0 >= nk) break;
+        float yv[G][VEC];
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          load_vec<ACT, VEC>(y, static_cast<int64_t>(j0 + g < nk ? slot[j0 + g] : slot[0]) * D + c, yv[g]);
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) asm volatile("" : "+v"(yv[g][v]));
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          if (j0 + g < nk) add(yv[g], wsl[j0 + g]);
+      }
+    } else {  // one route at a time
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j) {
+        if (j < nk) {
+          float yv[VEC];
+          load_vec<ACT, VEC>(y, static_cast<int64_t>(slot[j]) * D + c, yv);
+          add(yv, wsl[j]);
         }
       }
     }
@@ -219,53 +246,101 @@ int combine(const void* y, int dtype, const int32_t* route_slot, const int32_t* 
 // Routes without a slot (route_slot < 0) add nothing.  One block per token;
 // `out` may be `residual` (each element is read, then written, by one thread).
 // ---------------------------------------------------------------------------
-template <int ACT, int VEC>
+template <int ACT, int VEC, int KMAX>
 __global__ __launch_bounds__(256) void decode_combine_kernel(const void* __restrict__ y,
                                                              const int32_t* __restrict__ route_slot,
                                                              const float* __restrict__ top_w, const float* residual,
                                                              int K, int D, float* out) {
   const int t = blockIdx.x;
   const int64_t row = static_cast<int64_t>(t) * D;
-  for (int c = threadIdx.x * VEC; c < D; c += blockDim.x * VEC) {
-    float acc[VEC];
+  const int64_t first = static_cast<int64_t>(t) * K;
+  if constexpr (KMAX > 0) {
+    // K <= KMAX: the token's slots and weights are read once, the rows of up
+    // to G routes and the residual are requested together, then added in
+    // top-k order (a route without a slot reads the row of the token's first
+    // slotted route and adds nothing; the empty volatile asm keeps each row's
+    // load ahead of the additions instead of sunk into its route's branch)
+    int sl[KMAX];
+    float wt[KMAX];
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
-    for (int j = 0; j < K; ++j) {
-      const int s = route_slot[static_cast<int64_t>(t) * K + j];
-      if (s < 0) continue;
-      const float w = top_w[static_cast<int64_t>(t) * K + j];
-      const int64_t src = static_cast<int64_t>(s) * D + c;
-      float yv[VEC];
-      if constexpr (VEC == 8 && ACT == QW_BF16) {
-        const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(y) + src);
-        const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+    for (int j = 0; j < KMAX; ++j) {
+      sl[j] = j < K ? route_slot[first + j] : -1;
+      wt[j] = j < K ? top_w[first + j] : 0.0f;
+    }
+    int any = -1;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          yv[2 * v] = __uint_as_float(w4[v] << 16);
-          yv[2 * v + 1] = __uint_as_float(w4[v] & 0xffff0000u);
+    for (int j = KMAX - 1; j >= 0; --j) any = sl[j] >= 0 ? sl[j] : any;
+    constexpr int G = KMAX < 4 ? KMAX : 4;
+    static_assert(KMAX % G == 0, "whole groups of routes");
+    for (int c = threadIdx.x * VEC; c < D; c += blockDim.x * VEC) {
+      float rv[VEC];
+      if (residual != nullptr) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) rv[v] = residual[row + c + v];
+      }
+      float acc[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
+#pragma unroll
+      for (int j0 = 0; j0 < KMAX; j0 += G) {
+        if (j0 >= K || any < 0) break;
+        float yv[G][VEC];
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          load_vec<ACT, VEC>(y, static_cast<int64_t>(sl[j0 + g] >= 0 ? sl[j0 + g] : any) * D + c, yv[g]);
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) asm volatile("" : "+v"(yv[g][v]));
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          if (sl[j0 + g] < 0) continue;
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) acc[v] = __fadd_rn(acc[v], __fmul_rn(yv[g][v], wt[j0 + g]));
         }
-      } else if constexpr (VEC == 4 && ACT == QW_F32) {
-        const float4 q = *reinterpret_cast<const float4*>(static_cast<const float*>(y) + src);
-        yv[0] = q.x;
-        yv[1] = q.y;
-        yv[2] = q.z;
-        yv[3] = q.w;
-      } else if constexpr (VEC == 8 && ACT == QW_F16) {
-        load_vec<QW_F16, 8>(y, src, yv);
-      } else {
+      }
+      if (residual != nullptr) {
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) yv[v] = load_act<ACT>(y, src + v);
+        for (int v = 0; v < VEC; ++v) acc[v] = __fadd_rn(rv[v], acc[v]);
       }
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) acc[v] = __fadd_rn(acc[v], __fmul_rn(yv[v], w));
+      for (int v = 0; v < VEC; ++v) out[row + c + v] = acc[v];
     }
-    if (residual != nullptr) {
+  } else {
+    for (int c = threadIdx.x * VEC; c < D; c += blockDim.x * VEC) {
+      float acc[VEC];
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) acc[v] = __fadd_rn(residual[row + c + v], acc[v]);
+      for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
+      for (int j = 0; j < K; ++j) {
+        const int s = route_slot[first + j];
+        if (s < 0) continue;
+        const float w = top_w[first + j];
+        float yv[VEC];
+        load_vec<ACT, VEC>(y, static_cast<int64_t>(s) * D + c, yv);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[v] = __fadd_rn(acc[v], __fmul_rn(yv[v], w));
+      }
+      if (residual != nullptr) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[v] = __fadd_rn(residual[row + c + v], acc[v]);
+      }
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) out[row + c + v] = acc[v];
     }
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) out[row + c + v] = acc[v];
   }
+}
+
+template <int ACT, int VEC>
+void launch_decode_combine(const void* y, const int32_t* route_slot, const float* top_w, const float* residual,
+                           unsigned g, int k, int d, float* out, hipStream_t stream) {
+  if (k <= 2)
+    decode_combine_kernel<ACT, VEC, 2><<<g, 256, 0, stream>>>(y, route_slot, top_w, residual, k, d, out);
+  else if (k <= 4)
+    decode_combine_kernel<ACT, VEC, 4><<<g, 256, 0, stream>>>(y, route_slot, top_w, residual, k, d, out);
+  else if (k <= 8)
+    decode_combine_kernel<ACT, VEC, 8><<<g, 256, 0, stream>>>(y, route_slot, top_w, residual, k, d, out);
+  else
+    decode_combine_kernel<ACT, VEC, 0><<<g, 256, 0, stream>>>(y, route_slot, top_w, residual, k, d, out);
 }
 
 int decode_combine(const void* y, int dtype, const int32_t* route_slot, const float* top_w, const float* residual,
@@ -277,17 +352,17 @@ int decode_combine(const void* y, int dtype, const int32_t* route_slot, const fl
   const unsigned g = static_cast<unsigned>(T);
   const int k = static_cast<int>(K), d = static_cast<int>(D);
   if (dtype == QW_F16 && d % 8 == 0)
-    decode_combine_kernel<QW_F16, 8><<<g, 256, 0, stream>>>(y, route_slot, top_w, residual, k, d, out);
+    launch_decode_combine<QW_F16, 8>(y, route_slot, top_w, residual, g, k, d, out, stream);
   else if (dtype == QW_F16)
-    decode_combine_kernel<QW_F16, 1><<<g, 256, 0, stream>>>(y, route_slot, top_w, residual, k, d, out);
+    launch_decode_combine<QW_F16, 1>(y, route_slot, top_w, residual, g, k, d, out, stream);
   else if (dtype == QW_BF16 && d % 8 == 0)
-    decode_combine_kernel<QW_BF16, 8><<<g, 256, 0, stream>>>(y, route_slot, top_w, residual, k, d, out);
+    launch_decode_combine<QW_BF16, 8>(y, route_slot, top_w, residual, g, k, d, out, stream);
   else if (dtype == QW_BF16)
-    decode_combine_kernel<QW_BF16, 1><<<g, 256, 0, stream>>>(y, route_slot, top_w, residual, k, d, out);
+    launch_decode_combine<QW_BF16, 1>(y, route_slot, top_w, residual, g, k, d, out, stream);
   else if (d % 4 == 0)
-    decode_combine_kernel<QW_F32, 4><<<g, 256, 0, stream>>>(y, route_slot, top_w, residual, k, d, out);
+    launch_decode_combine<QW_F32, 4>(y, route_slot, top_w, residual, g, k, d, out, stream);
   else
-    decode_combine_kernel<QW_F32, 1><<<g, 256, 0, stream>>>(y, route_slot, top_w, residual, k, d, out);
+    launch_decode_combine<QW_F32, 1>(y, route_slot, top_w, residual, g, k, d, out, stream);
   QW_LAUNCH_CHECK("decode_combine_kernel");
   return QW_OK;
 }
