@@ -344,7 +344,7 @@ def measure_module(name, steps, warmup):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU path is not part of this build",
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); runs over several GPUs are not implemented",
               file=sys.stderr)
         sys.exit(2)
     import torch

@@ -1,6 +1,6 @@
 """CPU oracle for the routed MoE expert-FFN forward — TEST INFRASTRUCTURE ONLY.
 
-This package is the checker.  Only ``tests/``, ``__graft_entry__.smoke()`` and
+The GPU parity tests compare against it.  Only ``tests/``, ``__graft_entry__.smoke()`` and
 the CPU-baseline leg of ``bench.py`` import it; the product library
 (``quantaweave_amd``) never does.
 

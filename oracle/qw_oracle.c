@@ -2,7 +2,8 @@
  * CPU oracle for the routed MoE expert-FFN forward path — TEST INFRASTRUCTURE.
  *
  * A plain-C restatement of the reference algorithm, used only by tests/,
- * __graft_entry__.smoke() and bench.py's CPU-baseline leg as the checker.  It
+ * __graft_entry__.smoke() and bench.py's CPU-baseline leg, as the reference
+ * the GPU results are compared with.  It
  * is never linked into or called by the product library.
  *
  * Built with -ffp-contract=off and no fast-math: every float operation below

@@ -24,7 +24,7 @@ TORCH_DT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
 # The streaming decode kernels against the reference's rounded-weight product
 # (normwise): measured at most 9.05e-3 (bf16) and 7.8e-4 (fp16) over
 # test_quantized_decode_rows_match_oracle's cases; bound with a margin, inside
-# the north-star 2e-2 (bf16) and the fp16 tolerance 5e-3.
+# the layer tolerances TOL above: 2e-2 (bf16) and 5e-3 (fp16).
 DECODE_DEV = {"bf16": 1.2e-2, "f16": 1.5e-3}
 # Fractions of outputs equal to / within one ulp of the restatement of the
 # kernels' own arithmetic: measured minima 0.959 / 0.987 (bf16) and

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/) before the GPU parity tests compare against it.
 
 Each oracle function is checked against something independent of its own
 formula: float64 mathematics, torch's library routines used the way the
