@@ -108,6 +108,8 @@ CASES = [
     (8, 256, 384, 2, "f32", None, 3, "bf16"),
     (16, 512, 256, 2, "bf16", None, 1, "bf16"),
     (16, 512, 256, 4, "bf16", None, 5, "bf16"),
+    (16, 512, 256, 6, "bf16", None, 2, "bf16"),   # the combine's bound of 8 routes
+    (16, 512, 256, 10, "i8", None, 1, "bf16"),    # above 8 routes: the combine's per-route loop
     (16, 512, 256, 2, "i8", None, 1, "bf16"),
     (16, 512, 256, 2, "i8", None, 2, "fp32"),
     (16, 1024, 352, 2, "u4", 32, 1, "bf16"),
