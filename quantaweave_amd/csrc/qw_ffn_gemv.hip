@@ -916,10 +916,31 @@ __global__ __launch_bounds__(64) void ffn_qmf_kernel(
   for (int m0 = r_lo; m0 < r_hi; m0 += 4) {
     const int M = min(4, r_hi - m0);
     const bool live = t < M;  // this lane's route exists
-    const int xr = live ? (row_index ? row_index[m0 + t] : m0 + t) : 0;
+    // The pass's row indices are read with uniform addresses through a
+    // read-only view (scalar loads, counted apart from the vector memory
+    // loads): the ring's first groups are requested while they are in
+    // flight, and the activation loads after them need not wait for those
+    // groups.  (Read as vector loads, the compiler's wait for the row index
+    // after the conditional ring requests was vmcnt(0), which also waited
+    // for the first weight groups.)
+    typedef __attribute__((address_space(4))) const int32_t* const_i32;
+    auto issue_first = [&]() {
 #pragma unroll
-    for (int i = 0; i < LD::STAGES - 1; ++i)
-      if (g_first + i < g_end) issue(g_first + i);
+      for (int i = 0; i < LD::STAGES - 1; ++i)
+        if (g_first + i < g_end) issue(g_first + i);
+    };
+    int xr;
+    if (row_index != nullptr) {
+      const const_i32 ri = (const_i32)row_index;
+      int xr4[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xr4[i] = ri[__builtin_amdgcn_readfirstlane(min(m0 + i, r_hi - 1))];
+      issue_first();
+      xr = live ? (t == 0 ? xr4[0] : t == 1 ? xr4[1] : t == 2 ? xr4[2] : xr4[3]) : 0;
+    } else {
+      issue_first();
+      xr = live ? m0 + t : 0;
+    }
     // ---- activations of route t for this lane's chunks, in the operand order of the codes ----
     uint2 xa[S][NMF];  // A operands: per chunk NMF instructions of 4 activations
     float cz[S];       // this route's bias term per chunk
