@@ -133,13 +133,15 @@ __device__ __forceinline__ uint16_t f32_to_half(float f) {
 }
 
 // Two values rounded to DT and packed, a in the low half: the bits of
-// f32_to_half(a) | f32_to_half(b) << 16.  For bf16 the pair is one
-// v_cvt_pk_bf16_f32; the scalar form compiles to one conversion per value
-// and a shift and an OR to merge them.
+// f32_to_half(a) | f32_to_half(b) << 16.  The pair is one v_cvt_pk_bf16_f32
+// or v_cvt_pk_f16_f32 (fp16 inputs pinned first, as in f32_to_f16); the
+// scalar form compiles to one conversion per value and an OR to merge them.
 template <int DT>
 __device__ __forceinline__ uint32_t pack_half2(float a, float b) {
   if constexpr (DT == QW_F16) {
-    return f32_to_f16(a) | (static_cast<uint32_t>(f32_to_f16(b)) << 16);
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    const f16x2_t v = {static_cast<_Float16>(pin_f32(a)), static_cast<_Float16>(pin_f32(b))};
+    return __builtin_bit_cast(uint32_t, v);
   } else {
     typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
     const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
@@ -226,8 +228,8 @@ __device__ __forceinline__ void store_vec(void* p, int64_t i, const float (&v)[V
   } else if constexpr (VEC % 4 == 0 && DT == QW_F16) {
 #pragma unroll
     for (int u = 0; u < VEC; u += 4) {
-      const uint32_t lo = f32_to_f16(v[u]) | (static_cast<uint32_t>(f32_to_f16(v[u + 1])) << 16);
-      const uint32_t hi = f32_to_f16(v[u + 2]) | (static_cast<uint32_t>(f32_to_f16(v[u + 3])) << 16);
+      const uint32_t lo = pack_half2<QW_F16>(v[u], v[u + 1]);
+      const uint32_t hi = pack_half2<QW_F16>(v[u + 2], v[u + 3]);
       *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p) + i + u) = make_uint2(lo, hi);
     }
   } else if constexpr (VEC == 4 && DT == QW_BF16) {

@@ -754,8 +754,8 @@ __global__ __launch_bounds__(THREADS) void route_plan_small_kernel(
         const float4 v = *reinterpret_cast<const float4*>(cast_x + i);
         uint2 o;
         if (cast_f16) {
-          o.x = f32_to_f16(v.x) | (static_cast<uint32_t>(f32_to_f16(v.y)) << 16);
-          o.y = f32_to_f16(v.z) | (static_cast<uint32_t>(f32_to_f16(v.w)) << 16);
+          o.x = pack_half2<QW_F16>(v.x, v.y);
+          o.y = pack_half2<QW_F16>(v.z, v.w);
         } else {
           o.x = pack_half2<QW_BF16>(v.x, v.y);
           o.y = pack_half2<QW_BF16>(v.z, v.w);
